@@ -1,0 +1,302 @@
+"""Benchmark of the MiniCPM-4 backbone's decode step on one MI355X.
+
+Workload (the headline): the full backbone shape — 24 layers, hidden 1024, 16 query / 2 KV heads,
+head_dim 64, SiLU-gated FFN 4096, bf16 weights drawn N(0, 0.02) from a seed — at batch 1, its
+cache filled to position 256 (a 256-position prompt), then `--steps` decode steps (500 by default),
+each at the next position, every input already in HBM. A step is one pass of the stack: 121
+kernels launched as one recorded HIP graph. `value` is decode steps per second.
+
+Beside it on the same JSON line:
+- "batches": decode at 16 and 64 requests, contexts drawn U[64, 1024] (seeded), 200 steps;
+- "roofline": the dominant kernel of the step, its algorithmic bytes per launch over its average
+  duration from per-dispatch HIP events (each recorded by the kernel's own dispatch);
+- "cpu_baseline": the fp32 CPU path (the oracle, OpenMP over the host's cores) on a bounded
+  sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "tgtts-v4_amd", ROOT / "oracle"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "LM decode steps/s at batch 1/16/64; % of 8 TB/s HBM roofline; prefill tok/s"
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+PROMPT = 256
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def spec_and_shape(capacity: int):
+    import tgx
+    from tgx.synth import StackSpec
+
+    spec = StackSpec(layers=24, dtype="bf16", seed=0)
+    shape = tgx.Shape(hidden=spec.hidden, inner=spec.inner, heads=spec.heads, kv_heads=spec.kv_heads,
+                      head_dim=spec.head_dim, layers=spec.layers, capacity=capacity, eps=spec.eps,
+                      rope_theta=spec.rope_theta)
+    return spec, shape
+
+
+def load(dec, weights):
+    from tgx.synth import bf16_bits
+
+    for name, v in weights.items():
+        dec.load(name, bf16_bits(v))
+
+
+def kernel_bytes(shape, label: str, rows: int, kv_positions: int) -> int:
+    """Algorithmic HBM bytes of one launch: weights once, activations in and out, and for the
+    attention the keys and values of every position read (kv_positions over the batch)."""
+    h, i, H, KV, d = shape.hidden, shape.inner, shape.heads, shape.kv_heads, shape.head_dim
+    qkv = (H + 2 * KV) * d
+    if label == "gemv_qkv_rope":
+        return qkv * h * 2 + rows * h * 4 + rows * qkv * 2
+    if label == "attention_split":
+        return kv_positions * KV * d * 2 * 2 + rows * H * d * 2 * 2
+    if label == "o_proj":
+        return h * H * d * 2 + rows * H * d * 2 + rows * h * 4 * 2
+    if label == "gemv_gate_up":
+        return 2 * i * h * 2 + rows * h * 4 + rows * i * 2
+    if label == "down_proj":
+        return h * i * 2 + rows * i * 2 + rows * h * 4 * 2
+    if label == "final_norm":
+        return rows * h * 4 * 2 + h * 4
+    return 0
+
+
+def step_bytes(shape, positions) -> int:
+    """A step's algorithmic bytes: every weight once, every cached key and value of each row read
+    (positions 0..p), the new ones written."""
+    kvpp = shape.kv_bytes_per_position()
+    return shape.weight_bytes() + sum(kvpp * (p + 1) for p in positions) + kvpp * len(positions)
+
+
+def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int, profile_steps: int = 4):
+    """Decode `steps` steps of `rows` requests, request r from position contexts[r]; returns the
+    timing record."""
+    import tgx
+
+    capacity = int(np.ceil((max(contexts) + steps + warmup + 1) / 256.0) * 256)
+    spec, shape = spec_and_shape(capacity)
+    dec = tgx.Decoder(ctx, shape, tgx.Batch(rows=rows, slots=rows))
+    load(dec, weights)
+    x = np.asarray(__import__("tgx.synth", fromlist=["embeddings"]).embeddings(7, "bench.x", rows, shape.hidden))
+    # Fill each request's cache up to its context: the rows walk their positions together, row r
+    # joining once the longest context has room for it.
+    longest = max(contexts)
+    for t in range(longest):
+        placed = [tgx.Row(t - (longest - c), r) if t >= longest - c else None for r, c in enumerate(contexts)]
+        if rows == 1:
+            break
+        dec.set_rows(placed, x)
+        dec.start()
+        dec.wait()
+    if rows == 1:
+        dec.set_rows([tgx.Row(0, 0)], x)
+        dec.launch(contexts[0], advance=True)
+        dec.wait()
+    for r, c in enumerate(contexts):
+        dec.reserve(r, c + steps + warmup + 1)
+    start_rows = [tgx.Row(c, r) for r, c in enumerate(contexts)]
+    if warmup:
+        dec.set_rows(start_rows, x)
+        dec.launch(warmup, advance=True)
+        dec.wait()
+    dec.set_rows(start_rows, x)
+    t0 = time.perf_counter()
+    dec.launch(steps, advance=True)
+    dec.wait()
+    wall = time.perf_counter() - t0
+    gpu_ms = dec.elapsed_ms()
+    # Per-dispatch times from a few steps in the middle of the run.
+    mid = [tgx.Row(c + steps // 2, r) for r, c in enumerate(contexts)]
+    dec.set_timed(True)
+    per = {}
+    for k in range(profile_steps):
+        dec.set_rows([tgx.Row(m.position + k, m.slot) for m in mid], x)
+        dec.start()
+        dec.wait()
+        for label, ms in dec.timings():
+            per.setdefault(label, []).append(ms)
+    dec.set_timed(False)
+    dec.close()
+    positions_mid = [c + steps // 2 for c in contexts]
+    bytes_mid = step_bytes(shape, positions_mid)
+    kernels = {}
+    kv_positions = sum(p + 1 for p in positions_mid)
+    for label, ms in per.items():
+        avg = float(np.mean(ms))
+        launches_per_step = len(ms) / profile_steps
+        b = kernel_bytes(shape, label, rows, kv_positions)
+        kernels[label] = {
+            "avg_us": avg * 1e3,
+            "per_step_us": avg * 1e3 * launches_per_step,
+            "bytes_per_launch": b,
+            "GB_s": b / (avg * 1e-3) / 1e9 if avg > 0 else None,
+        }
+    ms_per_step = wall * 1e3 / steps
+    return {
+        "rows": rows,
+        "steps": steps,
+        "steps_per_s": steps / wall,
+        "ms_per_step": ms_per_step,
+        "gpu_ms_per_step": gpu_ms / steps,
+        "step_bytes_mid": bytes_mid,
+        "hbm_fraction": bytes_mid / (ms_per_step * 1e-3) / HBM_PEAK,
+        "kernels": kernels,
+        "kernel_sum_us": sum(k["per_step_us"] for k in kernels.values()),
+        "shape": shape,
+    }
+
+
+def cpu_baseline(weights, seconds: float):
+    """The fp32 CPU path (the oracle in float32, OpenMP over the host's cores) on the same
+    24-layer stack at batch 1, decode steps from position 256 of a zero-filled cache."""
+    import oracle
+    from tgx.synth import StackSpec, embeddings
+
+    spec = StackSpec(layers=24, dtype="bf16", seed=0)
+    threads = os.cpu_count() or 1
+    oracle.set_threads(threads)
+    st = oracle.Stack(spec, weights, PROMPT + 512, "f32")
+    x = embeddings(7, "bench.cpu", 1, spec.hidden)[0]
+    t0 = time.perf_counter()
+    st.decode(PROMPT, x)
+    first = time.perf_counter() - t0
+    n = max(3, min(400, int(seconds / max(first, 1e-6))))
+    t0 = time.perf_counter()
+    for i in range(n):
+        st.decode(PROMPT + 1 + i, x)
+    dt = time.perf_counter() - t0
+    return {
+        "value": n / dt,
+        "unit": "steps/s",
+        "cores": oracle.threads(),
+        "kind": "port",
+        "sample": f"{n} fp32 decode steps of the 24-layer stack at batch 1, positions {PROMPT + 1}..{PROMPT + n} "
+                  f"(keys and values below {PROMPT} zero), {dt:.1f} s on {oracle.threads()} OpenMP threads",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=1, help="the batch the headline value is taken at")
+    ap.add_argument("--no-extra", action="store_true", help="skip the batch-16/64 runs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py runs on one GPU: this build has no multi-GPU path (requests would be routed to "
+              "GPUs at admission, with no collective); run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import tgx
+    from tgx.synth import StackSpec, stack_weights
+
+    t0 = time.perf_counter()
+    weights = stack_weights(StackSpec(layers=24, dtype="bf16", seed=0))
+    log(f"weights drawn in {time.perf_counter() - t0:.1f} s")
+    ctx = tgx.Context(0)
+    report = ctx.report()
+    log(f"device {report['name']} {report['arch']} {report['compute_units']} CUs {report['clock_khz']} kHz")
+
+    rng = np.random.default_rng(1234)
+    headline_contexts = [PROMPT] * args.batch if args.batch == 1 else list(rng.integers(64, 1025, args.batch))
+    head = run_decode(ctx, weights, args.batch, headline_contexts, args.steps, args.warmup)
+    shape = head.pop("shape")
+    log(f"batch {args.batch}: {head['steps_per_s']:.1f} steps/s, {head['ms_per_step']*1e3:.1f} us/step, "
+        f"kernels sum {head['kernel_sum_us']:.1f} us")
+    for label, k in sorted(head["kernels"].items(), key=lambda kv: -kv[1]["per_step_us"]):
+        log(f"  {label:16s} {k['avg_us']:8.2f} us/launch {k['per_step_us']:8.1f} us/step {k['GB_s'] or 0:8.1f} GB/s")
+
+    batches = {}
+    if not args.no_extra:
+        for rows in (16, 64):
+            if rows == args.batch:
+                continue
+            ctxs = [int(c) for c in np.random.default_rng(rows).integers(64, 1025, rows)]
+            r = run_decode(ctx, weights, rows, ctxs, 200, 10)
+            r.pop("shape")
+            batches[str(rows)] = {k: r[k] for k in ("steps_per_s", "ms_per_step", "hbm_fraction", "kernel_sum_us")}
+            batches[str(rows)]["tokens_per_s"] = r["steps_per_s"] * rows
+            batches[str(rows)]["contexts"] = "U[64,1024] seeded, 200 steps"
+            log(f"batch {rows}: {r['steps_per_s']:.1f} steps/s ({r['steps_per_s']*rows:.0f} tok/s), "
+                f"{r['hbm_fraction']*100:.1f}% of HBM peak on algorithmic bytes")
+
+    # The roofline of the step's dominant kernel: the one with the most time per step.
+    dom_label, dom = max(head["kernels"].items(), key=lambda kv: kv[1]["per_step_us"])
+    achieved = dom["bytes_per_launch"] / (dom["avg_us"] * 1e-6) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom_label,
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK / 1e9,
+        "unit": "GB/s",
+        "frac": round(achieved / (HBM_PEAK / 1e9), 4),
+        "traffic": None,
+        "bytes_per_launch": dom["bytes_per_launch"],
+        "avg_us": round(dom["avg_us"], 3),
+    }
+
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(weights, args.cpu_seconds)
+            log(f"cpu baseline: {cpu['value']:.2f} steps/s on {cpu['cores']} threads")
+        except Exception as e:  # the baseline is reported, never required
+            log(f"cpu baseline failed: {e}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["steps_per_s"], 2),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) bf16 weights, N(0,1) inputs)",
+        "config": {
+            "workload": f"MiniCPM-4 backbone decode: 24 layers, hidden 1024, 16/2 GQA heads, head_dim 64, "
+                        f"FFN 4096, bf16 weights; batch {args.batch}, from position {PROMPT} "
+                        f"({'256-position prompt' if args.batch == 1 else 'contexts U[64,1024]'}), "
+                        f"{args.steps} decode steps, paged KV cache (64-position blocks)",
+            "batch": args.batch,
+            "layers": 24,
+            "hidden": 1024,
+            "kernels_per_step": 121,
+        },
+        "hbm_fraction_step": round(head["hbm_fraction"], 4),
+        "gpu_ms_per_step": round(head["gpu_ms_per_step"], 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "batches": batches,
+        "kernels_us": {k: round(v["avg_us"], 3) for k, v in head["kernels"].items()},
+        "device": {"name": report["name"], "arch": report["arch"], "clock_khz": report["clock_khz"]},
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

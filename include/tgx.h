@@ -1,0 +1,204 @@
+/*
+ * tgx — the MI355X (gfx950) runtime for tgtts-v4's MiniCPM-4 hot path, as a C ABI.
+ *
+ * It replaces the reference's Vulkan runtime crate (crates/vulkan) and the graph crate's GPU
+ * programs for the decode step and the prefill (crates/graph/src/{decode,prefill,step}.rs) with
+ * hand-written HIP kernels for gfx950, recorded once into a HIP graph and launched every step.
+ * Every entry point takes plain pointers and sizes; the library owns all device memory, the
+ * caller owns the host arrays it passes in and out.
+ *
+ * Threading: a context and everything made from it belong to one thread at a time (as the
+ * reference's single GPU thread owns its Engine, crates/tgtts/src/rt.rs:1-7). Nothing here is
+ * safe to call from two threads at once on the same context.
+ *
+ * Errors: every function returns a tgx_status; on failure tgx_last_error() holds a message for
+ * the calling thread. Shapes and placements are checked on the host before anything is
+ * launched (decode.rs:440-449, :198-227).
+ */
+#ifndef TGX_H
+#define TGX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: the classes of vulkan::Error (crates/vulkan/src/error.rs:5-43) and graph::Error
+ * (crates/graph/src/lib.rs:41-59) a caller can act on. */
+typedef enum {
+    TGX_OK = 0,
+    TGX_E_SHAPE = 1,      /* graph::Error::Shape: shapes or placements the kernels cannot run */
+    TGX_E_HIP = 2,        /* vulkan::Error::Vk: a HIP call failed */
+    TGX_E_KERNELS = 3,    /* graph::Error::Kernels: the code object lacks a kernel or target */
+    TGX_E_WEIGHTS = 4,    /* graph::Error::Checkpoint: a weight of the wrong name or size */
+    TGX_E_NOT_FINITE = 5, /* graph::Error::NotFinite: an output came out NaN or infinite */
+    TGX_E_TIMEOUT = 6,    /* the fence wait's 60 s timeout (crates/vulkan/src/context.rs:24) */
+    TGX_E_BUSY = 7,       /* a run is under way: the host may not touch its buffers */
+    TGX_E_ARG = 8,        /* a null handle or pointer */
+    TGX_E_NO_DEVICE = 9   /* vulkan::Error::NoDevice */
+} tgx_status;
+
+/* The last error message of the calling thread ("" when none). */
+const char* tgx_last_error(void);
+
+/* Element types of host arrays handed to tgx_decoder_load. */
+typedef enum { TGX_F32 = 0, TGX_BF16 = 1, TGX_F16 = 2 } tgx_dtype;
+
+/* ---- context: replaces vulkan::Context (crates/vulkan/src/context.rs:237-540) ---- */
+
+typedef struct tgx_context tgx_context;
+
+typedef struct {
+    char name[64];         /* e.g. "AMD Instinct MI355X" */
+    char arch[32];         /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int compute_units;
+    int clock_khz;         /* peak engine clock */
+    int memory_clock_khz;
+    size_t memory_bytes;
+    int wavefront;         /* 64 */
+} tgx_device_report;
+
+/* Context::new: opens `device` and the stream every program of the context runs on. */
+tgx_status tgx_context_create(int device, tgx_context** out);
+void tgx_context_destroy(tgx_context* ctx);
+/* Context::report. */
+tgx_status tgx_context_report(const tgx_context* ctx, tgx_device_report* out);
+
+/* ---- the decode step: crates/graph/src/decode.rs ---- */
+
+/* decode::Shape (decode.rs:65-82). `capacity` is the most positions one request (slot) may
+ * reach. rope_factors: LongRoPE's short_factor (head_dim / 2 values), or NULL for all 1. */
+typedef struct {
+    int hidden, inner, heads, kv_heads, head_dim, layers, capacity;
+    float eps, rope_theta;
+    int rope;
+    const double* rope_factors;
+} tgx_shape;
+
+/* decode::Batch (decode.rs:171-178) and the paged cache that replaces the reference's
+ * [slots][kv_heads][capacity][head_dim] caches: `rows` run per step, `slots` requests are kept,
+ * the cache is a pool of `blocks` blocks of `block_tokens` positions (0: enough for every slot at
+ * full capacity) handed out to slots as their positions grow. */
+typedef struct {
+    int rows;
+    int slots;
+    int block_tokens; /* 64 is the only size the kernels take; 0 means 64 */
+    int blocks;
+} tgx_batch;
+
+/* decode::Row (decode.rs:230-235): a row's position in its slot. A row whose position is
+ * TGX_SPARE is spare: it writes no cache and attends to nothing (batch.glsl:9-14). */
+typedef struct {
+    uint32_t position;
+    uint32_t slot;
+} tgx_row;
+#define TGX_SPARE 0xFFFFFFFFu
+
+typedef struct tgx_decoder tgx_decoder;
+
+/* The shape checks tgx_decoder_create makes, on the host alone (Shape::new's refusals and
+ * decode_batch_graph's, decode.rs:87-126, :468-491): TGX_OK or TGX_E_SHAPE with the reason. */
+tgx_status tgx_shape_check(const tgx_shape* shape, const tgx_batch* batch);
+
+/* Batch::placement (decode.rs:198-227), on the host alone: writes 2 * nrows words, each row's
+ * position then each row's slot, TGX_SPARE for a spare row; refuses two rows in one slot, a slot
+ * past `slots` and a position past `capacity`. */
+tgx_status tgx_batch_placement(int slots, int capacity, const tgx_row* rows, int nrows,
+                               uint32_t* words);
+
+/* Decoder::with_batch (decode.rs:799-813): allocates weights (zero until loaded), the paged
+ * cache and the step's buffers, writes the RoPE tables and records the step as a HIP graph. */
+tgx_status tgx_decoder_create(tgx_context* ctx, const tgx_shape* shape, const tgx_batch* batch,
+                              tgx_decoder** out);
+void tgx_decoder_destroy(tgx_decoder* dec);
+
+/* load_stack's write of one tensor (decode.rs:740-776), under the names the step's graph gives
+ * them (decode.rs:632-650, 716): "layers.{l}.input_layernorm", "layers.{l}.qkv_proj" (q_proj;
+ * k_proj; v_proj joined along their outputs, [(heads + 2 kv_heads) head_dim][hidden]),
+ * "layers.{l}.o_proj" ([hidden][heads head_dim]), "layers.{l}.post_attention_layernorm",
+ * "layers.{l}.gate_up_proj" (gate_proj; up_proj, [2 inner][hidden]), "layers.{l}.down_proj"
+ * ([hidden][inner]) and "norm". `count` elements of `dtype`, row-major; converted to bf16
+ * (round to nearest even) and laid out in the kernels' tiles. */
+tgx_status tgx_decoder_load(tgx_decoder* dec, const char* name, const void* data, tgx_dtype dtype,
+                            size_t count);
+
+/* Decoder::set_rows (decode.rs:857-862): `x` is [rows][hidden] f32, `rows` one per row of the
+ * batch (nrows == batch.rows). Refuses two rows in one slot and positions past the capacity
+ * (Batch::placement, decode.rs:198-227). Hands out cache blocks to slots as needed. */
+tgx_status tgx_decoder_set_rows(tgx_decoder* dec, const tgx_row* rows, int nrows, const float* x);
+/* Decoder::start (decode.rs:865-867): launches the step over the input last written. */
+tgx_status tgx_decoder_start(tgx_decoder* dec);
+/* Submission::wait (crates/vulkan/src/recording.rs:747-753): waits for it, 60 s at most. */
+tgx_status tgx_decoder_wait(tgx_decoder* dec);
+/* Decoder::output (decode.rs:870-872): [rows][hidden] f32 after the final norm; a spare row's
+ * values are meaningless. */
+tgx_status tgx_decoder_output(tgx_decoder* dec, float* out);
+/* Decoder::step_rows (decode.rs:849-853): set_rows, start, wait, output. */
+tgx_status tgx_decoder_step_rows(tgx_decoder* dec, const tgx_row* rows, int nrows, const float* x,
+                                 float* out);
+/* Decoder::step (decode.rs:833-837): batch 1, slot 0. */
+tgx_status tgx_decoder_step(tgx_decoder* dec, uint32_t position, const float* x, float* out);
+
+/* Releases the cache blocks of `slot`, which a new request may then take (the paged cache's
+ * counterpart of starting a request over in a slot). */
+tgx_status tgx_decoder_release_slot(tgx_decoder* dec, uint32_t slot);
+/* Hands `slot` the blocks for positions 0..positions-1 now, so that steps running ahead on the
+ * device (tgx_decoder_launch with advance) find them. */
+tgx_status tgx_decoder_reserve(tgx_decoder* dec, uint32_t slot, uint32_t positions);
+/* The blocks free in the pool. */
+tgx_status tgx_decoder_free_blocks(const tgx_decoder* dec, int* out);
+
+/* Launches the recorded step `times` times back to back on the context's stream over the
+ * device-resident input, without copying anything in or out: what a caller whose inputs are
+ * already in HBM runs. With `advance`, each step moves every placed row on by one position
+ * after it (teacher-forced continuation); the slots must hold the blocks (tgx_decoder_reserve).
+ * Returns when launched; tgx_decoder_wait waits. */
+tgx_status tgx_decoder_launch(tgx_decoder* dec, int times, int advance);
+
+/* The GPU time of the last tgx_decoder_launch or step, in milliseconds, from HIP events on the
+ * context's stream around it (Step::elapsed, step.rs:381-384). */
+tgx_status tgx_decoder_elapsed_ms(const tgx_decoder* dec, float* out);
+
+/* Decoder::new's `timed` (decode.rs:788-796, recording.rs:15-17): when on, steps are launched
+ * dispatch by dispatch instead of as the recorded graph, each dispatch timed by events its own
+ * dispatch records, so that its time is the kernel's alone. */
+tgx_status tgx_decoder_set_timed(tgx_decoder* dec, int timed);
+
+/* Decoder::timings (decode.rs:891-893): each dispatch's label and GPU time in the last timed step,
+ * in order; *n is the number of dispatches (0 when not timed), of which `max` are written. */
+typedef struct {
+    char label[32];
+    float ms;
+} tgx_timing;
+tgx_status tgx_decoder_timings(tgx_decoder* dec, int max, tgx_timing* out, int* n);
+
+/* The step's dispatches and device bytes (Step::dispatches / arena_bytes, step.rs:398-411). */
+tgx_status tgx_decoder_dispatches(const tgx_decoder* dec, int* out);
+tgx_status tgx_decoder_device_bytes(const tgx_decoder* dec, size_t* out);
+
+/* Reads the cache of `slot` back, for tests: keys and values of positions 0..positions-1 as
+ * [layers][kv_heads][positions][head_dim] f32 each. */
+tgx_status tgx_decoder_read_cache(tgx_decoder* dec, uint32_t slot, uint32_t positions, float* k,
+                                  float* v);
+
+/* ---- the prefill: crates/graph/src/prefill.rs ---- */
+
+/* Prefill::run (prefill.rs:473-503): runs `len` positions from `start` of `slot` at once, their
+ * hidden states x [len][hidden] f32, writing their keys and values into the decoder's cache for
+ * its steps to go on from, each position attending over the slot up to itself. Returns the
+ * outputs after the final norm, [len][hidden] f32. The reference runs slot 0 only; any slot
+ * is taken here. */
+tgx_status tgx_prefill_run(tgx_decoder* dec, uint32_t slot, uint32_t start, uint32_t len,
+                           const float* x, float* out);
+
+/* Device-resident prefill for timing: `len` positions in each of `count` slots from position 0
+ * (slots 0..count-1), the hidden states already on the device (the last x given to
+ * tgx_prefill_run, repeated), launched `times` times. Returns when launched. */
+tgx_status tgx_prefill_launch(tgx_decoder* dec, uint32_t count, uint32_t len, int times);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,207 @@
+"""The decode step on the GPU through the C ABI against the oracle, as the reference's
+crates/graph/tests/decode.rs holds its decode step to goldens: per-step accuracy, each row of a
+batch bit for bit as it is alone, a defect that must fail, the KV cache itself, spare rows and
+the paged cache's refusals.
+
+Tolerance (bf16 weights and activations on the GPU, the fp64 oracle over the same bf16 weights):
+cosine >= 0.999 and max|got - ref| / max|ref| <= 1e-2 at every step.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import COSINE_MIN, REL_MAX, distance, within
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny_spec(layers=4, dtype="f32", seed=0):
+    from tgx.synth import StackSpec
+
+    return StackSpec(layers=layers, dtype=dtype, seed=seed)
+
+
+def make_decoder(ctx, spec, capacity, rows=1, slots=None, rope=True, blocks=0):
+    import tgx
+    from tgx.synth import stack_weights
+
+    shape = tgx.Shape(hidden=spec.hidden, inner=spec.inner, heads=spec.heads, kv_heads=spec.kv_heads,
+                      head_dim=spec.head_dim, layers=spec.layers, capacity=capacity, eps=spec.eps,
+                      rope_theta=spec.rope_theta, rope=rope)
+    dec = tgx.Decoder(ctx, shape, tgx.Batch(rows=rows, slots=slots or rows, blocks=blocks))
+    dec.load_all(stack_weights(spec))
+    return dec
+
+
+def oracle_stack(spec, capacity, rope=True, shift=0):
+    import oracle
+    from tgx.synth import bf16_round, stack_weights
+
+    # The GPU holds bf16 weights: the oracle runs over the same values.
+    w = {k: bf16_round(v) for k, v in stack_weights(spec).items()}
+    return oracle.Stack(spec, w, capacity, "f64", rope=rope, shift=shift)
+
+
+def inputs(spec, n, name="x"):
+    from tgx.synth import embeddings
+
+    return embeddings(spec.seed + 1, name, n, spec.hidden)
+
+
+def test_tiny_decoder_32_prefill_positions_and_16_steps_match_the_oracle(ctx):
+    """BASELINE config 1 run through decode steps: 4 layers, 32 positions then 16 steps."""
+    spec = tiny_spec()
+    cap = 64
+    dec = make_decoder(ctx, spec, cap)
+    ref = oracle_stack(spec, cap)
+    x = inputs(spec, 48)
+    worst = None
+    for t in range(48):
+        got = dec.step(t, x[t])
+        want = ref.decode(t, x[t])
+        d = distance(got, want)
+        assert within(d), f"step {t}: {d}"
+        if worst is None or d["cosine"] < worst["cosine"]:
+            worst = d
+    print(f"config 1 worst step: {worst}")
+    # The cache holds the oracle's keys and values (rounded to bf16).
+    k, v = dec.read_cache(0, 48)
+    for name, got, want in (("k", k, ref.k[:, :, :48]), ("v", v, ref.v[:, :, :48])):
+        d = distance(got, want)
+        assert d["cosine"] >= COSINE_MIN and d["rel_max"] <= REL_MAX, f"{name} cache: {d}"
+
+
+def test_positions_one_slot_on_fail_the_tolerance(ctx):
+    """Defect (crates/graph/tests/decode.rs:252-255): every position one slot on in the cache, so
+    that each query also attends to the empty position 0."""
+    spec = tiny_spec(layers=1)
+    cap = 64
+    dec = make_decoder(ctx, spec, cap)
+    ref = oracle_stack(spec, cap)
+    x = inputs(spec, 40)
+    failed = 0
+    for t in range(40):
+        d = distance(dec.step(t + 1, x[t]), ref.decode(t, x[t]))
+        failed += not within(d)
+    assert failed > 0, "positions one slot on pass"
+
+
+def test_a_stack_without_rope_matches_and_rotating_it_fails(ctx):
+    """The residual LM attends without RoPE (decode.rs:47-50); rotating it is a defect
+    (crates/graph/tests/decode.rs:372-378)."""
+    spec = tiny_spec(layers=2)
+    cap = 64
+    dec = make_decoder(ctx, spec, cap, rope=False)
+    ref = oracle_stack(spec, cap, rope=False)
+    rotated = oracle_stack(spec, cap, rope=True)
+    x = inputs(spec, 40)
+    failed = 0
+    for t in range(40):
+        got = dec.step(t, x[t])
+        d = distance(got, ref.decode(t, x[t]))
+        assert within(d), f"step {t}: {d}"
+        failed += not within(distance(got, rotated.decode(t, x[t])))
+    assert failed > 0
+
+
+def run_rows(ctx, spec, x, rows, cap, shift=0):
+    """crates/graph/tests/decode.rs:142-210: `rows` requests at once, request r from step 2r on
+    in slot rows - 1 - r, in a row that changes from step to step, the rows without one spare."""
+    import tgx
+
+    dec = make_decoder(ctx, spec, cap, rows=rows)
+    n = x.shape[0]
+    got = [[] for _ in range(rows)]
+    for t in range(n + 2 * (rows - 1)):
+        placed = [None] * rows
+        inp = np.zeros((rows, spec.hidden), dtype=np.float32)
+        for r in range(rows):
+            i = t - 2 * r
+            if not (0 <= i < n):
+                continue
+            row = (r + t) % rows
+            placed[row] = tgx.Row(i + shift, rows - 1 - r)
+            inp[row] = x[i]
+        out = dec.step_rows(placed, inp)
+        for r in range(rows):
+            if 2 * r <= t < 2 * r + n:
+                got[r].append(out[(r + t) % rows].copy())
+    dec.close()
+    return [np.stack(g) for g in got]
+
+
+@pytest.mark.parametrize("rows", [3, 16])
+def test_each_row_of_a_batch_is_bit_for_bit_as_it_is_alone(ctx, rows):
+    spec = tiny_spec(layers=2)
+    cap = 320
+    x = inputs(spec, 300)
+    alone = run_rows(ctx, spec, x, 1, cap)[0]
+    batched = run_rows(ctx, spec, x, rows, cap)
+    for r, got in enumerate(batched):
+        differ = int(np.sum(got.view(np.uint32) != alone.view(np.uint32)))
+        assert differ == 0, f"row {r} of {rows}: {differ} values differ from alone"
+
+
+def test_batch_of_64_rows_is_as_alone(ctx):
+    """The largest batch the kernels take: four column tiles of 16."""
+    import tgx
+
+    spec = tiny_spec(layers=1)
+    cap = 128
+    x = inputs(spec, 100)
+    alone = run_rows(ctx, spec, x[:70], 1, cap)[0]
+    dec = make_decoder(ctx, spec, cap, rows=64)
+    outs = []
+    for t in range(70):
+        rows = [tgx.Row(t, s) for s in range(64)]
+        inp = np.repeat(x[t : t + 1], 64, axis=0)
+        out = dec.step_rows(rows, inp)
+        outs.append(out)
+    outs = np.stack(outs)  # [t][row][hidden]
+    for r in (0, 17, 63):
+        assert np.array_equal(outs[:, r].view(np.uint32), alone.view(np.uint32)), f"row {r}"
+
+
+def test_spare_rows_write_no_cache_and_leave_others_alone(ctx):
+    import tgx
+
+    spec = tiny_spec(layers=1)
+    cap = 128
+    x = inputs(spec, 10)
+    dec = make_decoder(ctx, spec, cap, rows=2, slots=2)
+    alone = make_decoder(ctx, spec, cap, rows=1)
+    for t in range(10):
+        out = dec.step_rows([None, tgx.Row(t, 1)], np.stack([x[(t + 3) % 10], x[t]]))
+        a = alone.step(t, x[t])
+        assert np.array_equal(out[1].view(np.uint32), a.view(np.uint32))
+    # Slot 0 was never placed: it holds no blocks at all.
+    assert dec.free_blocks() == 2 * 2 - 1
+
+
+def test_placements_the_batch_cannot_hold_are_refused(ctx):
+    import tgx
+
+    spec = tiny_spec(layers=1)
+    dec = make_decoder(ctx, spec, 64, rows=3, slots=4)
+    x = np.zeros((3, spec.hidden), dtype=np.float32)
+    for rows in ([tgx.Row(5, 2), tgx.Row(9, 2), None], [tgx.Row(64, 0), None, None], [tgx.Row(1, 4), None, None]):
+        with pytest.raises(tgx.TgxError) as e:
+            dec.step_rows(rows, x)
+        assert e.value.kind == "shape"
+    with pytest.raises(tgx.TgxError):
+        dec.step_rows([None, None], x[:2])
+
+
+def test_a_pool_too_small_for_the_slots_is_refused_when_it_runs_out(ctx):
+    import tgx
+
+    spec = tiny_spec(layers=1)
+    dec = make_decoder(ctx, spec, 256, rows=2, slots=2, blocks=3)
+    x = np.zeros((2, spec.hidden), dtype=np.float32)
+    dec.step_rows([tgx.Row(127, 0), None], x)  # two blocks
+    dec.step_rows([None, tgx.Row(10, 1)], x)  # a third
+    with pytest.raises(tgx.TgxError) as e:
+        dec.step_rows([tgx.Row(128, 0), None], x)  # a fourth: none left
+    assert e.value.kind == "shape"
+    dec.release_slot(1)
+    dec.step_rows([tgx.Row(128, 0), None], x)

@@ -1,0 +1,73 @@
+// Arguments and launchers of the decode step's kernels (decode_kernels.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device.hpp"
+
+namespace tgx {
+
+// What every kernel of a step reads: the shape, and where each row runs (Batch::placement,
+// decode.rs:198-227, plus the paged cache's block table).
+struct DecodeArgs {
+    int hidden, inner, heads, kv_heads;
+    int rows;        // rows of the batch
+    int capacity;    // positions a slot may reach
+    int nslots;
+    int max_blocks;  // blocks per slot in the table
+    int nblocks;     // blocks in the pool
+    float eps, scale;
+    int rope;
+    const uint32_t* positions;  // [rows]
+    const uint32_t* slots;      // [rows]
+    const uint32_t* table;      // [nslots][max_blocks], UINT32_MAX where none
+    const float* cos;           // [capacity][32]
+    const float* sin;
+};
+
+// One layer's tensors.
+struct LayerArgs {
+    const float* x;           // layer input [rows][hidden] f32
+    const float* input_norm;  // [hidden] f32
+    const uint16_t* qkv;      // tiled bf16, rows permuted (qkv_row_of)
+    uint16_t* q;              // [rows][heads][64] bf16
+    uint16_t* kv;             // the layer's cache pool: [blocks][kv_heads][key tile, value tile]
+    uint16_t* attended;       // [rows][heads 64] bf16
+    const float* mid;         // [rows][hidden] f32, o_proj's output
+    const float* post_norm;   // [hidden] f32
+    const uint16_t* gate_up;  // tiled bf16 [2 inner][hidden]
+    uint16_t* mlp;            // [rows][inner] bf16
+};
+
+// out = residual + W x, W tiled [N][K].
+struct ResidualArgs {
+    const uint16_t* w;
+    const uint16_t* x;  // [rows][K] bf16
+    int K, N;
+    const float* residual;  // [rows][N]
+    float* out;             // [rows][N]
+};
+
+// Per-dispatch timing of a step launched without its graph: each dispatch takes the next pair of
+// events, recorded by the kernel's own dispatch (hipExtLaunchKernelGGL), so that the time between
+// them is the kernel's alone, as a profiler reports it.
+struct DispatchTimer {
+    hipEvent_t* start = nullptr;
+    hipEvent_t* stop = nullptr;
+    const char** labels = nullptr;
+    int used = 0, capacity = 0;
+};
+
+// Column tiles of 16 a batch of `rows` takes, the LDS a projection takes at that batch, and the
+// longest K the projections take.
+int decode_tiles(int rows);
+size_t decode_lds_bytes(int rows);
+int decode_max_k();
+// Lets the projections take up to `device_lds` bytes of LDS per workgroup.
+hipError_t decode_prepare(size_t device_lds);
+hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
+                               const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer = nullptr);
+hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out,
+                             uint32_t* positions, int advance, hipStream_t stream, DispatchTimer* timer = nullptr);
+
+}  // namespace tgx

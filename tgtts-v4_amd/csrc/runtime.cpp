@@ -1,0 +1,728 @@
+// The host side of the runtime (runtime.hpp): device selection, the decoder's memory, weight
+// tiling, the paged cache's block allocator, and the decode step recorded once as a HIP graph
+// and launched every step (crates/graph/src/step.rs:111-149 records a command buffer once; a
+// HIP graph is the MI355X counterpart).
+#include "runtime.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <thread>
+
+namespace tgx {
+
+namespace {
+thread_local std::string last_error_message;
+}
+
+tgx_status fail(tgx_status status, const std::string& message) {
+    last_error_message = message;
+    return status;
+}
+
+void clear_error() { last_error_message.clear(); }
+
+const char* last_error() { return last_error_message.c_str(); }
+
+// ---- numerics on the host ----
+
+float bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+float f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    uint32_t u;
+    if (exp == 0x1f) {
+        u = sign | 0x7f800000u | (man << 13);
+    } else if (exp == 0) {
+        if (man == 0) {
+            u = sign;
+        } else {  // subnormal: normalise
+            int e = -1;
+            do {
+                man <<= 1;
+                ++e;
+            } while (!(man & 0x400u));
+            u = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3ffu) << 13);
+        }
+    } else {
+        u = sign | ((exp + 127 - 15) << 23) | (man << 13);
+    }
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+void rope_tables(const Shape& s, std::vector<float>& cos, std::vector<float>& sin) {
+    // decode.rs:146-168: inv = 1 / theta^(i / dim) for even i, in f32; r = 1 / factor in f32;
+    // angle = t * r * inv, in that order.
+    const int half = s.head_dim / 2;
+    cos.assign((size_t)s.capacity * half, 0.f);
+    sin.assign((size_t)s.capacity * half, 0.f);
+    std::vector<float> inv(half), r(half);
+    for (int j = 0; j < half; ++j) {
+        inv[j] = 1.0f / std::pow(s.rope_theta, (float)(2 * j) / (float)s.head_dim);
+        r[j] = 1.0f / (float)(s.factors.empty() ? 1.0 : s.factors[j]);
+    }
+    for (int t = 0; t < s.capacity; ++t)
+        for (int j = 0; j < half; ++j) {
+            const float f = (float)t * r[j] * inv[j];
+            cos[(size_t)t * half + j] = std::cos(f);
+            sin[(size_t)t * half + j] = std::sin(f);
+        }
+}
+
+// ---- context ----
+
+tgx_status context_create(int device, Context** out) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(TGX_E_NO_DEVICE, "no HIP device");
+    if (device < 0 || device >= count)
+        return fail(TGX_E_NO_DEVICE, "device " + std::to_string(device) + " of " + std::to_string(count));
+    auto* ctx = new Context();
+    ctx->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipGetDeviceProperties(&ctx->prop, device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail(TGX_E_HIP, std::string("context: ") + hipGetErrorString(e));
+    }
+    ctx->lds_bytes = ctx->prop.sharedMemPerBlock;
+    e = decode_prepare(ctx->lds_bytes);
+    if (e != hipSuccess) {
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return fail(TGX_E_HIP, std::string("allowing ") + std::to_string(ctx->prop.sharedMemPerBlock) +
+                                   " bytes of LDS: " + hipGetErrorString(e));
+    }
+    if (std::strncmp(ctx->prop.gcnArchName, "gfx950", 6) != 0) {
+        std::string arch = ctx->prop.gcnArchName;
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return fail(TGX_E_KERNELS, "the kernels are built for gfx950, not " + arch);
+    }
+    *out = ctx;
+    return TGX_OK;
+}
+
+void context_destroy(Context* ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+// ---- shapes ----
+
+tgx_status check_shape(const tgx_shape* in, Shape* s) {
+    auto refuse = [](const std::string& why) { return fail(TGX_E_SHAPE, why); };
+    if (!in) return fail(TGX_E_ARG, "null shape");
+    s->hidden = in->hidden;
+    s->inner = in->inner;
+    s->heads = in->heads;
+    s->kv_heads = in->kv_heads;
+    s->head_dim = in->head_dim;
+    s->layers = in->layers;
+    s->capacity = in->capacity;
+    s->eps = in->eps;
+    s->rope_theta = in->rope_theta;
+    s->rope = in->rope != 0;
+    s->factors.clear();
+    if (in->rope_factors) s->factors.assign(in->rope_factors, in->rope_factors + in->head_dim / 2);
+    if (s->head_dim != HEAD_DIM) return refuse("head_dim " + std::to_string(s->head_dim) + ": the kernels take 64");
+    if (s->layers < 0 || s->capacity <= 0) return refuse("layers " + std::to_string(s->layers) + ", capacity " + std::to_string(s->capacity));
+    if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 16 || 16 % (s->heads / s->kv_heads) != 0)
+        return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) + " KV heads: a group of 1, 2, 4, 8 or 16");
+    // The projections take K in chunks of 1024 columns, up to 4096 (decode_kernels.hip).
+    const int most = decode_max_k();
+    for (auto [what, k] : {std::pair<const char*, int>{"hidden", s->hidden}, {"inner", s->inner}, {"heads x head_dim", s->heads * HEAD_DIM}})
+        if (k <= 0 || k % 1024 != 0 || k > most)
+            return refuse(std::string(what) + " " + std::to_string(k) + ": a multiple of 1024 up to " + std::to_string(most));
+    if (s->inner % 16 != 0 || s->hidden % 16 != 0) return refuse("rows in strips of 16");
+    if (!(s->eps >= 0.f)) return refuse("eps");
+    return TGX_OK;
+}
+
+tgx_status check_batch(const Shape& s, const tgx_batch* batch) {
+    if (!batch) return fail(TGX_E_ARG, "null batch");
+    const int block_tokens = batch->block_tokens == 0 ? BLOCK_TOKENS : batch->block_tokens;
+    if (batch->rows <= 0 || batch->rows > 64 || batch->rows > batch->slots)
+        return fail(TGX_E_SHAPE, std::to_string(batch->rows) + " rows in " + std::to_string(batch->slots) +
+                                     " slots (1 to 64 rows, no more than the slots)");
+    if (block_tokens != BLOCK_TOKENS)
+        return fail(TGX_E_SHAPE, "blocks of " + std::to_string(block_tokens) + " positions: the kernels take 64");
+    if (batch->blocks < 0) return fail(TGX_E_SHAPE, "a pool of " + std::to_string(batch->blocks) + " blocks");
+    const size_t lds = decode_lds_bytes(batch->rows);
+    if (lds > 160 * 1024)
+        return fail(TGX_E_SHAPE, std::to_string(batch->rows) + " rows stage " + std::to_string(lds) + " bytes, past 160 KiB of LDS");
+    return TGX_OK;
+}
+
+tgx_status placement(int slots, int capacity, const tgx_row* rows, int nrows, uint32_t* words) {
+    // Batch::placement (decode.rs:198-227): positions, then slots; a spare row past every position.
+    std::vector<char> taken(slots > 0 ? slots : 0, 0);
+    for (int b = 0; b < nrows; ++b) {
+        const tgx_row r = rows[b];
+        words[b] = TGX_SPARE;
+        words[nrows + b] = TGX_SPARE;
+        if (r.position == TGX_SPARE) continue;
+        if (r.position >= (uint32_t)capacity || r.slot >= (uint32_t)slots || taken[r.slot]) {
+            return fail(TGX_E_SHAPE, "row " + std::to_string(b) + " at position " + std::to_string(r.position) + " of " +
+                                         std::to_string(capacity) + " in slot " + std::to_string(r.slot) + " of " +
+                                         std::to_string(slots) + ", taken: " +
+                                         (r.slot < (uint32_t)slots && taken[r.slot] ? "true" : "false"));
+        }
+        taken[r.slot] = 1;
+        words[b] = r.position;
+        words[nrows + b] = r.slot;
+    }
+    return TGX_OK;
+}
+
+// ---- the decoder ----
+
+DecodeArgs Decoder::args() const {
+    DecodeArgs a{};
+    a.hidden = shape.hidden;
+    a.inner = shape.inner;
+    a.heads = shape.heads;
+    a.kv_heads = shape.kv_heads;
+    a.rows = rows;
+    a.capacity = shape.capacity;
+    a.nslots = slots;
+    a.max_blocks = max_blocks;
+    a.nblocks = nblocks;
+    a.eps = shape.eps;
+    a.scale = 1.0f / std::sqrt((float)shape.head_dim);
+    a.rope = shape.rope ? 1 : 0;
+    a.positions = positions;
+    a.slots = slot_of_row;
+    a.table = table;
+    a.cos = cos;
+    a.sin = sin;
+    return a;
+}
+
+LayerArgs Decoder::layer_args(int l, const float* x, float* mid) const {
+    LayerArgs la{};
+    la.x = x;
+    la.input_norm = layers[l].input_norm;
+    la.qkv = layers[l].qkv;
+    la.q = q;
+    la.kv = kv + (size_t)l * nblocks * shape.kv_heads * 2 * KV_TILE;
+    la.attended = attended;
+    la.mid = mid;
+    la.post_norm = layers[l].post_norm;
+    la.gate_up = layers[l].gate_up;
+    la.mlp = mlp;
+    return la;
+}
+
+ResidualArgs Decoder::o_args(int l, const float* residual, float* out_) const {
+    ResidualArgs r{};
+    r.w = layers[l].o;
+    r.x = attended;
+    r.K = shape.heads * HEAD_DIM;
+    r.N = shape.hidden;
+    r.residual = residual;
+    r.out = out_;
+    return r;
+}
+
+ResidualArgs Decoder::down_args(int l, const float* residual, float* out_) const {
+    ResidualArgs r{};
+    r.w = layers[l].down;
+    r.x = mlp;
+    r.K = shape.inner;
+    r.N = shape.hidden;
+    r.residual = residual;
+    r.out = out_;
+    return r;
+}
+
+namespace {
+
+template <typename T>
+tgx_status alloc(Decoder* d, T** out, size_t count, bool zero = true) {
+    void* p = nullptr;
+    const size_t bytes = count * sizeof(T);
+    if (bytes == 0) {
+        *out = nullptr;
+        return TGX_OK;
+    }
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(TGX_E_HIP, "hipMalloc of " + std::to_string(bytes) + " bytes: " + hipGetErrorString(e));
+    d->allocations.push_back({p, bytes});
+    d->device_bytes += bytes;
+    if (zero) {
+        e = hipMemset(p, 0, bytes);
+        if (e != hipSuccess) return fail(TGX_E_HIP, std::string("hipMemset: ") + hipGetErrorString(e));
+    }
+    *out = (T*)p;
+    return TGX_OK;
+}
+
+// The step's dispatches on the context's stream, in order (decode_batch_graph's ops,
+// decode.rs:630-723): five a layer, then the final norm.
+hipError_t enqueue_step(Decoder* d, int advance, DispatchTimer* timer, int* dispatches) {
+    hipStream_t s = d->ctx->stream;
+    const DecodeArgs a = d->args();
+    hipError_t err = hipSuccess;
+    int n = 0;
+    const float* x = d->x_in;
+    for (int l = 0; l < d->shape.layers && err == hipSuccess; ++l) {
+        // layer l: x -> mid (h_b) -> next (h_a); layer 0 reads x_in, which stays as written.
+        err = launch_decode_layer(a, d->layer_args(l, x, d->h_b), d->o_args(l, x, d->h_b),
+                                  d->down_args(l, d->h_b, d->h_a), s, timer);
+        n += 5;
+        x = d->h_a;
+    }
+    if (err == hipSuccess) {
+        err = launch_final_norm(a, x, d->final_norm, d->out, d->positions, advance, s, timer);
+        n += 1;
+    }
+    if (dispatches) *dispatches = n;
+    return err;
+}
+
+tgx_status record(Decoder* d, int advance, hipGraphExec_t* exec) {
+    hipStream_t s = d->ctx->stream;
+    TGX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int dispatches = 0;
+    hipError_t err = enqueue_step(d, advance, nullptr, &dispatches);
+    hipGraph_t graph = nullptr;
+    hipError_t end = hipStreamEndCapture(s, &graph);
+    if (err != hipSuccess) {
+        if (graph) hipGraphDestroy(graph);
+        return fail(TGX_E_HIP, std::string("recording the step: ") + hipGetErrorString(err));
+    }
+    if (end != hipSuccess) return fail(TGX_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(end));
+    hipError_t e = hipGraphInstantiate(exec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    if (e != hipSuccess) return fail(TGX_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    d->dispatches = dispatches;
+    return TGX_OK;
+}
+
+tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
+    const Shape& s = d->shape;
+    TGX_TRY(check_batch(s, batch));
+    if (decode_lds_bytes(batch->rows) + 1024 > d->ctx->lds_bytes)
+        return fail(TGX_E_SHAPE, std::to_string(batch->rows) + " rows stage " + std::to_string(decode_lds_bytes(batch->rows)) +
+                                     " bytes, past the device's " + std::to_string(d->ctx->lds_bytes) + " of LDS");
+    d->rows = batch->rows;
+    d->slots = batch->slots;
+    d->block_tokens = batch->block_tokens == 0 ? BLOCK_TOKENS : batch->block_tokens;
+    d->max_blocks = (s.capacity + BLOCK_TOKENS - 1) / BLOCK_TOKENS;
+    d->nblocks = batch->blocks > 0 ? batch->blocks : d->slots * d->max_blocks;
+
+    const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads;
+    const size_t qkv_rows = (size_t)(H + 2 * KV) * HEAD_DIM;
+    d->layers.resize(s.layers);
+    for (auto& L : d->layers) {
+        TGX_TRY(alloc(d, &L.qkv, qkv_rows * h));
+        TGX_TRY(alloc(d, &L.o, (size_t)h * H * HEAD_DIM));
+        TGX_TRY(alloc(d, &L.gate_up, (size_t)2 * I * h));
+        TGX_TRY(alloc(d, &L.down, (size_t)h * I));
+        TGX_TRY(alloc(d, &L.input_norm, (size_t)h));
+        TGX_TRY(alloc(d, &L.post_norm, (size_t)h));
+    }
+    TGX_TRY(alloc(d, &d->final_norm, (size_t)h));
+    const int R = d->rows;
+    TGX_TRY(alloc(d, &d->x_in, (size_t)R * h));
+    TGX_TRY(alloc(d, &d->h_a, (size_t)R * h));
+    TGX_TRY(alloc(d, &d->h_b, (size_t)R * h));
+    TGX_TRY(alloc(d, &d->out, (size_t)R * h));
+    TGX_TRY(alloc(d, &d->q, (size_t)R * H * HEAD_DIM));
+    TGX_TRY(alloc(d, &d->attended, (size_t)R * H * HEAD_DIM));
+    TGX_TRY(alloc(d, &d->mlp, (size_t)R * I));
+    TGX_TRY(alloc(d, &d->kv, (size_t)s.layers * d->nblocks * KV * 2 * KV_TILE));
+    TGX_TRY(alloc(d, &d->positions, (size_t)R));
+    TGX_TRY(alloc(d, &d->slot_of_row, (size_t)R));
+    TGX_TRY(alloc(d, &d->table, (size_t)d->slots * d->max_blocks));
+    TGX_TRY(alloc(d, &d->cos, (size_t)s.capacity * HEAD_DIM / 2));
+    TGX_TRY(alloc(d, &d->sin, (size_t)s.capacity * HEAD_DIM / 2));
+    // Norm gains start at one, so that an unloaded stack still runs finite.
+    std::vector<float> ones(h, 1.0f);
+    for (auto& L : d->layers) {
+        TGX_HIP(hipMemcpy(L.input_norm, ones.data(), h * 4, hipMemcpyHostToDevice));
+        TGX_HIP(hipMemcpy(L.post_norm, ones.data(), h * 4, hipMemcpyHostToDevice));
+    }
+    TGX_HIP(hipMemcpy(d->final_norm, ones.data(), h * 4, hipMemcpyHostToDevice));
+    std::vector<float> cos, sin;
+    rope_tables(s, cos, sin);
+    TGX_HIP(hipMemcpy(d->cos, cos.data(), cos.size() * 4, hipMemcpyHostToDevice));
+    TGX_HIP(hipMemcpy(d->sin, sin.data(), sin.size() * 4, hipMemcpyHostToDevice));
+
+    TGX_HIP(hipHostMalloc((void**)&d->x_host, (size_t)R * h * 4, hipHostMallocDefault));
+    TGX_HIP(hipHostMalloc((void**)&d->out_host, (size_t)R * h * 4, hipHostMallocDefault));
+    TGX_HIP(hipHostMalloc((void**)&d->placement_host, (size_t)2 * R * 4, hipHostMallocDefault));
+    TGX_HIP(hipHostMalloc((void**)&d->table_host, (size_t)d->slots * d->max_blocks * 4, hipHostMallocDefault));
+    std::memset(d->x_host, 0, (size_t)R * h * 4);
+    std::memset(d->out_host, 0, (size_t)R * h * 4);
+    for (int i = 0; i < 2 * R; ++i) d->placement_host[i] = TGX_SPARE;
+    for (size_t i = 0; i < (size_t)d->slots * d->max_blocks; ++i) d->table_host[i] = TGX_SPARE;
+    TGX_HIP(hipMemcpy(d->positions, d->placement_host, R * 4, hipMemcpyHostToDevice));
+    TGX_HIP(hipMemcpy(d->slot_of_row, d->placement_host + R, R * 4, hipMemcpyHostToDevice));
+    TGX_HIP(hipMemcpy(d->table, d->table_host, (size_t)d->slots * d->max_blocks * 4, hipMemcpyHostToDevice));
+    d->table_dirty = false;
+    d->slot_blocks.assign(d->slots, 0);
+    d->free_list.clear();
+    for (int b = d->nblocks - 1; b >= 0; --b) d->free_list.push_back((uint32_t)b);
+
+    const int dispatches = 5 * s.layers + 1;
+    d->timer_start.assign(dispatches, nullptr);
+    d->timer_stop.assign(dispatches, nullptr);
+    d->timer_labels.assign(dispatches, nullptr);
+    for (int i = 0; i < dispatches; ++i) {
+        TGX_HIP(hipEventCreate(&d->timer_start[i]));
+        TGX_HIP(hipEventCreate(&d->timer_stop[i]));
+    }
+    d->timer.start = d->timer_start.data();
+    d->timer.stop = d->timer_stop.data();
+    d->timer.labels = d->timer_labels.data();
+    d->timer.capacity = dispatches;
+    TGX_HIP(hipEventCreate(&d->ev_start));
+    TGX_HIP(hipEventCreate(&d->ev_end));
+    TGX_HIP(hipEventCreateWithFlags(&d->ev_done, hipEventDisableTiming));
+    TGX_HIP(hipDeviceSynchronize());
+    TGX_TRY(record(d, 0, &d->step_exec));
+    TGX_TRY(record(d, 1, &d->advance_exec));
+    return TGX_OK;
+}
+
+// Gives `slot` blocks for positions 0..positions-1.
+tgx_status hold(Decoder* d, uint32_t slot, uint32_t positions) {
+    const int need = (int)((positions + BLOCK_TOKENS - 1) / BLOCK_TOKENS);
+    while (d->slot_blocks[slot] < need) {
+        if (d->free_list.empty())
+            return fail(TGX_E_SHAPE, "the cache's " + std::to_string(d->nblocks) + " blocks are all taken");
+        const uint32_t blk = d->free_list.back();
+        d->free_list.pop_back();
+        d->table_host[(size_t)slot * d->max_blocks + d->slot_blocks[slot]] = blk;
+        d->slot_blocks[slot] += 1;
+        d->table_dirty = true;
+    }
+    return TGX_OK;
+}
+
+tgx_status sync_table(Decoder* d) {
+    if (!d->table_dirty) return TGX_OK;
+    TGX_HIP(hipMemcpyAsync(d->table, d->table_host, (size_t)d->slots * d->max_blocks * 4, hipMemcpyHostToDevice, d->ctx->stream));
+    d->table_dirty = false;
+    return TGX_OK;
+}
+
+}  // namespace
+
+tgx_status decoder_create(Context* ctx, const tgx_shape* shape, const tgx_batch* batch, Decoder** out) {
+    if (!ctx || !out) return fail(TGX_E_ARG, "null context or output");
+    Shape s;
+    TGX_TRY(check_shape(shape, &s));
+    TGX_HIP(hipSetDevice(ctx->device));
+    auto* d = new Decoder();
+    d->ctx = ctx;
+    d->shape = s;
+    tgx_status st = create_inner(d, batch);
+    if (st != TGX_OK) {
+        std::string msg = last_error_message;
+        decoder_destroy(d);
+        return fail(st, msg);
+    }
+    *out = d;
+    return TGX_OK;
+}
+
+void decoder_destroy(Decoder* d) {
+    if (!d) return;
+    hipSetDevice(d->ctx->device);
+    hipStreamSynchronize(d->ctx->stream);
+    if (d->step_exec) hipGraphExecDestroy(d->step_exec);
+    if (d->advance_exec) hipGraphExecDestroy(d->advance_exec);
+    if (d->ev_start) hipEventDestroy(d->ev_start);
+    if (d->ev_end) hipEventDestroy(d->ev_end);
+    if (d->ev_done) hipEventDestroy(d->ev_done);
+    for (auto e : d->timer_start)
+        if (e) hipEventDestroy(e);
+    for (auto e : d->timer_stop)
+        if (e) hipEventDestroy(e);
+    for (auto& b : d->allocations) hipFree(b.ptr);
+    if (d->x_host) hipHostFree(d->x_host);
+    if (d->out_host) hipHostFree(d->out_host);
+    if (d->placement_host) hipHostFree(d->placement_host);
+    if (d->table_host) hipHostFree(d->table_host);
+    delete d;
+}
+
+namespace {
+
+// The weight's values as f32, `count` of `dtype`.
+std::vector<float> as_f32(const void* data, tgx_dtype dtype, size_t count) {
+    std::vector<float> v(count);
+    if (dtype == TGX_F32) {
+        std::memcpy(v.data(), data, count * 4);
+    } else {
+        const uint16_t* h = (const uint16_t*)data;
+        for (size_t i = 0; i < count; ++i) v[i] = dtype == TGX_BF16 ? bf16_to_f32(h[i]) : f16_to_f32(h[i]);
+    }
+    return v;
+}
+
+// W [n][k] into MFMA tiles, rows taken through `row_of` (strip, r) -> source row.
+template <typename RowOf>
+std::vector<uint16_t> tile(const std::vector<float>& w, int n, int k, RowOf row_of) {
+    std::vector<uint16_t> t((size_t)n * k);
+    const int kblocks = k / 32;
+    for (int strip = 0; strip < n / 16; ++strip)
+        for (int kb = 0; kb < kblocks; ++kb) {
+            uint16_t* dst = t.data() + weight_tile_index(strip, kb, kblocks);
+            for (int lane = 0; lane < 64; ++lane) {
+                const int src_row = row_of(strip, lane % 16);
+                const float* src = w.data() + (size_t)src_row * k + kb * 32 + (lane / 16) * 8;
+                for (int j = 0; j < 8; ++j) dst[lane * 8 + j] = f32_to_bf16(src[j]);
+            }
+        }
+    return t;
+}
+
+}  // namespace
+
+tgx_status decoder_load(Decoder* d, const char* name, const void* data, tgx_dtype dtype, size_t count) {
+    if (!d || !name || !data) return fail(TGX_E_ARG, "null decoder, name or data");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (dtype != TGX_F32 && dtype != TGX_BF16 && dtype != TGX_F16) return fail(TGX_E_ARG, "dtype");
+    const Shape& s = d->shape;
+    const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads;
+    const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
+    std::string n = name;
+    auto want = [&](size_t expect) -> tgx_status {
+        if (count != expect)
+            return fail(TGX_E_WEIGHTS, n + ": " + std::to_string(count) + " values, not " + std::to_string(expect));
+        return TGX_OK;
+    };
+    auto upload = [&](void* dst, const void* src, size_t bytes) -> tgx_status {
+        TGX_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+        return TGX_OK;
+    };
+    if (n == "norm") {
+        TGX_TRY(want(h));
+        auto v = as_f32(data, dtype, count);
+        return upload(d->final_norm, v.data(), (size_t)h * 4);
+    }
+    int l = -1;
+    char what[128] = {0};
+    if (std::sscanf(name, "layers.%d.%127s", &l, what) != 2 || l < 0 || l >= s.layers)
+        return fail(TGX_E_WEIGHTS, n + ": no such tensor in a stack of " + std::to_string(s.layers) + " layers");
+    std::string w = what;
+    Layer& L = d->layers[l];
+    if (w == "input_layernorm" || w == "post_attention_layernorm") {
+        TGX_TRY(want(h));
+        auto v = as_f32(data, dtype, count);
+        return upload(w == "input_layernorm" ? L.input_norm : L.post_norm, v.data(), (size_t)h * 4);
+    }
+    if (w == "qkv_proj") {
+        TGX_TRY(want((size_t)qkv_rows * h));
+        auto v = as_f32(data, dtype, count);
+        auto t = tile(v, qkv_rows, h, [](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM); });
+        return upload(L.qkv, t.data(), t.size() * 2);
+    }
+    if (w == "o_proj") {
+        TGX_TRY(want((size_t)h * H * HEAD_DIM));
+        auto v = as_f32(data, dtype, count);
+        auto t = tile(v, h, H * HEAD_DIM, [](int strip, int r) { return strip * 16 + r; });
+        return upload(L.o, t.data(), t.size() * 2);
+    }
+    if (w == "gate_up_proj") {
+        TGX_TRY(want((size_t)2 * I * h));
+        auto v = as_f32(data, dtype, count);
+        auto t = tile(v, 2 * I, h, [](int strip, int r) { return strip * 16 + r; });
+        return upload(L.gate_up, t.data(), t.size() * 2);
+    }
+    if (w == "down_proj") {
+        TGX_TRY(want((size_t)h * I));
+        auto v = as_f32(data, dtype, count);
+        auto t = tile(v, h, I, [](int strip, int r) { return strip * 16 + r; });
+        return upload(L.down, t.data(), t.size() * 2);
+    }
+    return fail(TGX_E_WEIGHTS, n + ": no such tensor");
+}
+
+tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const float* x) {
+    if (!d || !rows || !x) return fail(TGX_E_ARG, "null decoder, rows or x");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (nrows != d->rows)
+        return fail(TGX_E_SHAPE, std::to_string(nrows) + " rows for a batch of " + std::to_string(d->rows));
+    std::vector<uint32_t> words(2 * (size_t)nrows);
+    TGX_TRY(placement(d->slots, d->shape.capacity, rows, nrows, words.data()));
+    for (int b = 0; b < nrows; ++b) {
+        const tgx_row r = rows[b];
+        if (r.position == TGX_SPARE) continue;
+        TGX_TRY(hold(d, r.slot, r.position + 1));
+    }
+    std::memcpy(d->placement_host, words.data(), words.size() * 4);
+    std::memcpy(d->x_host, x, (size_t)nrows * d->shape.hidden * 4);
+    hipStream_t s = d->ctx->stream;
+    TGX_TRY(sync_table(d));
+    TGX_HIP(hipMemcpyAsync(d->x_in, d->x_host, (size_t)nrows * d->shape.hidden * 4, hipMemcpyHostToDevice, s));
+    TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
+    TGX_HIP(hipMemcpyAsync(d->slot_of_row, d->placement_host + nrows, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
+    // The pinned buffers may not change until the copies have gone.
+    TGX_HIP(hipStreamSynchronize(s));
+    return TGX_OK;
+}
+
+tgx_status decoder_start(Decoder* d) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    hipStream_t s = d->ctx->stream;
+    TGX_TRY(sync_table(d));
+    TGX_HIP(hipEventRecord(d->ev_start, s));
+    if (d->timed) {
+        // Launched dispatch by dispatch, each timed by its own events (Decoder::timings).
+        d->timer.used = 0;
+        hipError_t e = enqueue_step(d, 0, &d->timer, nullptr);
+        if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the timed step: ") + hipGetErrorString(e));
+    } else {
+        TGX_HIP(hipGraphLaunch(d->step_exec, s));
+    }
+    TGX_HIP(hipEventRecord(d->ev_end, s));
+    TGX_HIP(hipMemcpyAsync(d->out_host, d->out, (size_t)d->rows * d->shape.hidden * 4, hipMemcpyDeviceToHost, s));
+    TGX_HIP(hipEventRecord(d->ev_done, s));
+    d->pending = true;
+    return TGX_OK;
+}
+
+tgx_status decoder_wait(Decoder* d) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    if (!d->pending) return TGX_OK;
+    // Spin, then sleep, for at most 60 s (crates/vulkan/src/context.rs:24,120-136).
+    const auto begin = std::chrono::steady_clock::now();
+    for (int i = 0;; ++i) {
+        hipError_t e = hipEventQuery(d->ev_done);
+        if (e == hipSuccess) break;
+        if (e != hipErrorNotReady) {
+            d->pending = false;
+            return fail(TGX_E_HIP, std::string("waiting for the step: ") + hipGetErrorString(e));
+        }
+        if (std::chrono::steady_clock::now() - begin > std::chrono::seconds(60))
+            return fail(TGX_E_TIMEOUT, "the step did not finish in 60 s");
+        if (i > 1000) std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+    d->pending = false;
+    return TGX_OK;
+}
+
+tgx_status decoder_output(Decoder* d, float* out) {
+    if (!d || !out) return fail(TGX_E_ARG, "null decoder or out");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    std::memcpy(out, d->out_host, (size_t)d->rows * d->shape.hidden * 4);
+    return TGX_OK;
+}
+
+tgx_status decoder_release_slot(Decoder* d, uint32_t slot) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (slot >= (uint32_t)d->slots) return fail(TGX_E_SHAPE, "slot " + std::to_string(slot) + " of " + std::to_string(d->slots));
+    for (int i = d->slot_blocks[slot] - 1; i >= 0; --i) {
+        uint32_t& e = d->table_host[(size_t)slot * d->max_blocks + i];
+        d->free_list.push_back(e);
+        e = TGX_SPARE;
+    }
+    d->slot_blocks[slot] = 0;
+    d->table_dirty = true;
+    return TGX_OK;
+}
+
+tgx_status decoder_reserve(Decoder* d, uint32_t slot, uint32_t positions) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (slot >= (uint32_t)d->slots) return fail(TGX_E_SHAPE, "slot " + std::to_string(slot) + " of " + std::to_string(d->slots));
+    if (positions > (uint32_t)d->shape.capacity)
+        return fail(TGX_E_SHAPE, std::to_string(positions) + " positions past a capacity of " + std::to_string(d->shape.capacity));
+    TGX_TRY(hold(d, slot, positions));
+    return sync_table(d);
+}
+
+tgx_status decoder_launch(Decoder* d, int times, int advance) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (times <= 0) return fail(TGX_E_ARG, "times");
+    hipStream_t s = d->ctx->stream;
+    TGX_TRY(sync_table(d));
+    TGX_HIP(hipEventRecord(d->ev_start, s));
+    for (int i = 0; i < times; ++i) {
+        if (d->timed) {
+            d->timer.used = 0;
+            hipError_t e = enqueue_step(d, advance, &d->timer, nullptr);
+            if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the timed step: ") + hipGetErrorString(e));
+        } else {
+            TGX_HIP(hipGraphLaunch(advance ? d->advance_exec : d->step_exec, s));
+        }
+    }
+    TGX_HIP(hipEventRecord(d->ev_end, s));
+    TGX_HIP(hipEventRecord(d->ev_done, s));
+    d->pending = true;
+    return TGX_OK;
+}
+
+tgx_status decoder_read_cache(Decoder* d, uint32_t slot, uint32_t positions, float* k, float* v) {
+    if (!d || !k || !v) return fail(TGX_E_ARG, "null argument");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (slot >= (uint32_t)d->slots || positions > (uint32_t)d->slot_blocks[slot] * BLOCK_TOKENS)
+        return fail(TGX_E_SHAPE, "slot " + std::to_string(slot) + " holds fewer than " + std::to_string(positions) + " positions");
+    const Shape& s = d->shape;
+    const int KV = s.kv_heads;
+    std::vector<uint16_t> tilebuf(2 * KV_TILE);
+    TGX_HIP(hipStreamSynchronize(d->ctx->stream));
+    for (int l = 0; l < s.layers; ++l)
+        for (int kv = 0; kv < KV; ++kv)
+            for (uint32_t p0 = 0; p0 < positions; p0 += BLOCK_TOKENS) {
+                const uint32_t blk = d->table_host[(size_t)slot * d->max_blocks + p0 / BLOCK_TOKENS];
+                const uint16_t* src = d->kv + (((size_t)l * d->nblocks + blk) * KV + kv) * 2 * KV_TILE;
+                TGX_HIP(hipMemcpy(tilebuf.data(), src, 2 * KV_TILE * 2, hipMemcpyDeviceToHost));
+                for (uint32_t p = p0; p < positions && p < p0 + BLOCK_TOKENS; ++p)
+                    for (int dd = 0; dd < HEAD_DIM; ++dd) {
+                        const size_t at = (((size_t)l * KV + kv) * positions + p) * HEAD_DIM + dd;
+                        k[at] = bf16_to_f32(tilebuf[key_index((int)(p - p0), dd)]);
+                        v[at] = bf16_to_f32(tilebuf[KV_TILE + value_index((int)(p - p0), dd)]);
+                    }
+            }
+    return TGX_OK;
+}
+
+tgx_status decoder_timings(Decoder* d, int max, tgx_timing* out, int* n) {
+    if (!d || !n) return fail(TGX_E_ARG, "null decoder or count");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (!d->timed) {
+        *n = 0;
+        return TGX_OK;
+    }
+    const int used = d->timer.used;
+    *n = used;
+    for (int i = 0; i < used && i < max && out; ++i) {
+        float ms = 0.f;
+        TGX_HIP(hipEventElapsedTime(&ms, d->timer.start[i], d->timer.stop[i]));
+        std::snprintf(out[i].label, sizeof out[i].label, "%s", d->timer.labels[i]);
+        out[i].ms = ms;
+    }
+    return TGX_OK;
+}
+
+}  // namespace tgx

@@ -1,0 +1,118 @@
+// The host side of the runtime: the context, the decoder's device memory and paged cache, and the
+// step recorded as a HIP graph. The C ABI (api.cpp) is a thin layer over these.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/tgx.h"
+#include "decode_kernels.hpp"
+
+namespace tgx {
+
+// The thread's last error message (tgx_last_error).
+tgx_status fail(tgx_status status, const std::string& message);
+void clear_error();
+#define TGX_HIP(call)                                                                        \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return ::tgx::fail(TGX_E_HIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+#define TGX_TRY(expr)                        \
+    do {                                     \
+        tgx_status s_ = (expr);              \
+        if (s_ != TGX_OK) return s_;         \
+    } while (0)
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipDeviceProp_t prop{};
+    size_t lds_bytes = 0;  // LDS a workgroup may take
+};
+
+// decode::Shape, checked against what the kernels cover.
+struct Shape {
+    int hidden, inner, heads, kv_heads, head_dim, layers, capacity;
+    float eps, rope_theta;
+    bool rope;
+    std::vector<double> factors;
+};
+
+// One allocation of device memory, freed with the decoder.
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct Layer {
+    uint16_t *qkv = nullptr, *o = nullptr, *gate_up = nullptr, *down = nullptr;
+    float *input_norm = nullptr, *post_norm = nullptr;
+};
+
+struct Decoder {
+    Context* ctx = nullptr;
+    Shape shape{};
+    int rows = 0, slots = 0, block_tokens = 64, nblocks = 0, max_blocks = 0;
+    std::vector<DeviceBuffer> allocations;
+    size_t device_bytes = 0;
+    std::vector<Layer> layers;
+    float* final_norm = nullptr;
+    // step tensors
+    float *x_in = nullptr, *h_a = nullptr, *h_b = nullptr, *out = nullptr;
+    uint16_t *q = nullptr, *attended = nullptr, *mlp = nullptr, *kv = nullptr;
+    uint32_t *positions = nullptr, *slot_of_row = nullptr, *table = nullptr;
+    float *cos = nullptr, *sin = nullptr;
+    // host mirrors, in pinned memory
+    float *x_host = nullptr, *out_host = nullptr;
+    uint32_t *placement_host = nullptr;  // [positions..., slots...]
+    uint32_t *table_host = nullptr;
+    bool table_dirty = true;
+    std::vector<int> slot_blocks;     // blocks each slot holds
+    std::vector<uint32_t> free_list;  // blocks nobody holds
+    // the recorded step
+    hipGraphExec_t step_exec = nullptr, advance_exec = nullptr;
+    int dispatches = 0;
+    hipEvent_t ev_start = nullptr, ev_end = nullptr, ev_done = nullptr;
+    bool pending = false;
+    bool timed = false;  // launch dispatch by dispatch, each timed (Decoder::new's `timed`)
+    DispatchTimer timer;
+    std::vector<hipEvent_t> timer_start, timer_stop;
+    std::vector<const char*> timer_labels;
+
+    DecodeArgs args() const;
+    LayerArgs layer_args(int l, const float* x, float* mid) const;
+    ResidualArgs o_args(int l, const float* residual, float* out) const;
+    ResidualArgs down_args(int l, const float* residual, float* out) const;
+};
+
+tgx_status context_create(int device, Context** out);
+void context_destroy(Context* ctx);
+
+tgx_status check_shape(const tgx_shape* in, Shape* out);
+tgx_status check_batch(const Shape& s, const tgx_batch* batch);
+tgx_status placement(int slots, int capacity, const tgx_row* rows, int nrows, uint32_t* words);
+tgx_status decoder_create(Context* ctx, const tgx_shape* shape, const tgx_batch* batch, Decoder** out);
+void decoder_destroy(Decoder* dec);
+tgx_status decoder_load(Decoder* dec, const char* name, const void* data, tgx_dtype dtype, size_t count);
+tgx_status decoder_set_rows(Decoder* dec, const tgx_row* rows, int nrows, const float* x);
+tgx_status decoder_start(Decoder* dec);
+tgx_status decoder_wait(Decoder* dec);
+tgx_status decoder_output(Decoder* dec, float* out);
+tgx_status decoder_release_slot(Decoder* dec, uint32_t slot);
+tgx_status decoder_reserve(Decoder* dec, uint32_t slot, uint32_t positions);
+tgx_status decoder_launch(Decoder* dec, int times, int advance);
+tgx_status decoder_timings(Decoder* d, int max, tgx_timing* out, int* n);
+tgx_status decoder_read_cache(Decoder* dec, uint32_t slot, uint32_t positions, float* k, float* v);
+
+// f32 <- bf16 / f16 bits; f32 -> bf16 bits, rounding to nearest even.
+float bf16_to_f32(uint16_t h);
+float f16_to_f32(uint16_t h);
+uint16_t f32_to_bf16(float f);
+
+// The RoPE tables in f32 as decode.rs:146-168 computes them.
+void rope_tables(const Shape& s, std::vector<float>& cos, std::vector<float>& sin);
+
+}  // namespace tgx

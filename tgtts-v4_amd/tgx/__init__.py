@@ -1,0 +1,458 @@
+"""Python bindings of libtgx's C ABI (include/tgx.h), shaped like the reference's model API:
+`Decoder` as crates/graph/src/decode.rs's (`new`/`with_batch`, `load`, `step`, `step_rows`,
+`set_rows`, `start`, `output`, `timings`), `Row` and `Batch` as its placement types, and
+`Decoder.prefill` as crates/graph/src/prefill.rs's `Prefill::run`.
+
+The library is the only thing that computes: if libtgx.so is missing these bindings raise, they
+never fall back to anything else.
+"""
+
+from __future__ import annotations
+
+import atexit
+import ctypes
+import os
+import sys
+import weakref
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("TGX_LIB", HERE.parent / "libtgx.so"))
+
+SPARE = 0xFFFFFFFF
+
+F32, BF16, F16 = 0, 1, 2
+
+STATUS = {
+    0: "ok",
+    1: "shape",
+    2: "hip",
+    3: "kernels",
+    4: "weights",
+    5: "not_finite",
+    6: "timeout",
+    7: "busy",
+    8: "arg",
+    9: "no_device",
+}
+
+
+class TgxError(RuntimeError):
+    """A failed call: `kind` names its status class (graph::Error's, crates/graph/src/lib.rs:41-59)."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.kind = STATUS.get(status, str(status))
+        super().__init__(f"{self.kind}: {message}")
+
+
+class _Shape(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int),
+        ("inner", ctypes.c_int),
+        ("heads", ctypes.c_int),
+        ("kv_heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("layers", ctypes.c_int),
+        ("capacity", ctypes.c_int),
+        ("eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+        ("rope", ctypes.c_int),
+        ("rope_factors", ctypes.POINTER(ctypes.c_double)),
+    ]
+
+
+class _Batch(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int),
+        ("slots", ctypes.c_int),
+        ("block_tokens", ctypes.c_int),
+        ("blocks", ctypes.c_int),
+    ]
+
+
+class _Row(ctypes.Structure):
+    _fields_ = [("position", ctypes.c_uint32), ("slot", ctypes.c_uint32)]
+
+
+class _Timing(ctypes.Structure):
+    _fields_ = [("label", ctypes.c_char * 32), ("ms", ctypes.c_float)]
+
+
+class _Report(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 64),
+        ("arch", ctypes.c_char * 32),
+        ("compute_units", ctypes.c_int),
+        ("clock_khz", ctypes.c_int),
+        ("memory_clock_khz", ctypes.c_int),
+        ("memory_bytes", ctypes.c_size_t),
+        ("wavefront", ctypes.c_int),
+    ]
+
+
+EXPORTS = [
+    "tgx_last_error",
+    "tgx_context_create",
+    "tgx_context_destroy",
+    "tgx_context_report",
+    "tgx_decoder_create",
+    "tgx_decoder_destroy",
+    "tgx_decoder_load",
+    "tgx_decoder_set_rows",
+    "tgx_decoder_start",
+    "tgx_decoder_wait",
+    "tgx_decoder_output",
+    "tgx_decoder_step_rows",
+    "tgx_decoder_step",
+    "tgx_decoder_release_slot",
+    "tgx_decoder_reserve",
+    "tgx_decoder_free_blocks",
+    "tgx_decoder_launch",
+    "tgx_decoder_elapsed_ms",
+    "tgx_decoder_dispatches",
+    "tgx_decoder_device_bytes",
+    "tgx_decoder_read_cache",
+    "tgx_decoder_set_timed",
+    "tgx_decoder_timings",
+    "tgx_shape_check",
+    "tgx_batch_placement",
+    "tgx_prefill_run",
+    "tgx_prefill_launch",
+]
+
+_lib: Optional[ctypes.CDLL] = None
+
+# Every open handle, closed before the interpreter exits: the HIP runtime tears itself down in the
+# C library's exit handlers, after which no handle may be freed. Decoders go before contexts.
+_open_decoders: "weakref.WeakSet" = weakref.WeakSet()
+_open_contexts: "weakref.WeakSet" = weakref.WeakSet()
+
+
+@atexit.register
+def _close_all() -> None:
+    for d in list(_open_decoders):
+        d.close()
+    for c in list(_open_contexts):
+        c.close()
+
+
+def library() -> ctypes.CDLL:
+    """libtgx.so, loaded once; raises when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise TgxError(3, f"{LIB_PATH} is not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    P = ctypes.c_void_p
+    lib.tgx_last_error.restype = ctypes.c_char_p
+    lib.tgx_context_create.argtypes = [ctypes.c_int, ctypes.POINTER(P)]
+    lib.tgx_context_destroy.argtypes = [P]
+    lib.tgx_context_destroy.restype = None
+    lib.tgx_context_report.argtypes = [P, ctypes.POINTER(_Report)]
+    lib.tgx_decoder_create.argtypes = [P, ctypes.POINTER(_Shape), ctypes.POINTER(_Batch), ctypes.POINTER(P)]
+    lib.tgx_decoder_destroy.argtypes = [P]
+    lib.tgx_decoder_destroy.restype = None
+    lib.tgx_decoder_load.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int, ctypes.c_size_t]
+    lib.tgx_decoder_set_rows.argtypes = [P, ctypes.POINTER(_Row), ctypes.c_int, P]
+    lib.tgx_decoder_start.argtypes = [P]
+    lib.tgx_decoder_wait.argtypes = [P]
+    lib.tgx_decoder_output.argtypes = [P, P]
+    lib.tgx_decoder_step_rows.argtypes = [P, ctypes.POINTER(_Row), ctypes.c_int, P, P]
+    lib.tgx_decoder_step.argtypes = [P, ctypes.c_uint32, P, P]
+    lib.tgx_decoder_release_slot.argtypes = [P, ctypes.c_uint32]
+    lib.tgx_decoder_reserve.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32]
+    lib.tgx_decoder_free_blocks.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_decoder_launch.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    lib.tgx_decoder_elapsed_ms.argtypes = [P, ctypes.POINTER(ctypes.c_float)]
+    lib.tgx_decoder_dispatches.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_decoder_device_bytes.argtypes = [P, ctypes.POINTER(ctypes.c_size_t)]
+    lib.tgx_decoder_read_cache.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, P, P]
+    lib.tgx_decoder_set_timed.argtypes = [P, ctypes.c_int]
+    lib.tgx_decoder_timings.argtypes = [P, ctypes.c_int, ctypes.POINTER(_Timing), ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_shape_check.argtypes = [ctypes.POINTER(_Shape), ctypes.POINTER(_Batch)]
+    lib.tgx_batch_placement.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(_Row), ctypes.c_int, ctypes.POINTER(ctypes.c_uint32)]
+    lib.tgx_prefill_run.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, P, P]
+    lib.tgx_prefill_launch.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
+    for name in EXPORTS:
+        if name.startswith("tgx_") and name not in ("tgx_last_error",):
+            fn = getattr(lib, name)
+            if fn.restype is not None and fn.restype is not ctypes.c_char_p:
+                fn.restype = ctypes.c_int
+    lib.tgx_context_destroy.restype = None
+    lib.tgx_decoder_destroy.restype = None
+    _lib = lib
+    return lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        msg = library().tgx_last_error().decode(errors="replace")
+        raise TgxError(status, msg)
+
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+@dataclass
+class Shape:
+    """decode::Shape (crates/graph/src/decode.rs:65-82)."""
+
+    hidden: int = 1024
+    inner: int = 4096
+    heads: int = 16
+    kv_heads: int = 2
+    head_dim: int = 64
+    layers: int = 24
+    capacity: int = 1024
+    eps: float = 1e-5
+    rope_theta: float = 10000.0
+    rope: bool = True
+    rope_factors: Optional[Sequence[float]] = None
+
+    def weight_bytes(self, element: int = 2) -> int:
+        """Shape::weight_bytes (decode.rs:130-135) for `element`-byte weights."""
+        h, i, d = self.hidden, self.inner, self.head_dim
+        qkv = (self.heads + 2 * self.kv_heads) * d * h
+        layer = qkv + self.heads * d * h + 2 * i * h + i * h + 2 * h
+        return element * (self.layers * layer + h)
+
+    def kv_bytes_per_position(self, element: int = 2) -> int:
+        """Keys and values of one position over every layer."""
+        return self.layers * 2 * self.kv_heads * self.head_dim * element
+
+
+def _shape_struct(shape: "Shape"):
+    s = _Shape(shape.hidden, shape.inner, shape.heads, shape.kv_heads, shape.head_dim, shape.layers,
+               shape.capacity, shape.eps, shape.rope_theta, 1 if shape.rope else 0, None)
+    keep = None
+    if shape.rope_factors is not None:
+        keep = np.ascontiguousarray(shape.rope_factors, dtype=np.float64)
+        s.rope_factors = keep.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
+    return s, keep
+
+
+def check_shape(shape: "Shape", batch: "Batch") -> None:
+    """The decoder's shape checks on the host alone (Shape::new, decode_batch_graph)."""
+    s, _keep = _shape_struct(shape)
+    b = _Batch(batch.rows, batch.slots, batch.block_tokens, batch.blocks)
+    _check(library().tgx_shape_check(ctypes.byref(s), ctypes.byref(b)))
+
+
+def placement(slots: int, capacity: int, rows: Sequence[Optional["Row"]]) -> list:
+    """Batch::placement (decode.rs:198-227) on the host: positions then slots, SPARE for spare rows."""
+    arr = (_Row * max(1, len(rows)))()
+    for i, r in enumerate(rows):
+        arr[i].position, arr[i].slot = (SPARE, SPARE) if r is None else (r.position, r.slot)
+    words = (ctypes.c_uint32 * max(1, 2 * len(rows)))()
+    _check(library().tgx_batch_placement(slots, capacity, arr, len(rows), words))
+    return list(words)[: 2 * len(rows)]
+
+
+@dataclass(frozen=True)
+class Row:
+    """decode::Row (decode.rs:230-235)."""
+
+    position: int
+    slot: int
+
+
+@dataclass(frozen=True)
+class Batch:
+    """decode::Batch (decode.rs:171-178) with the paged cache's block pool."""
+
+    rows: int = 1
+    slots: int = 1
+    blocks: int = 0
+    block_tokens: int = 64
+
+
+class Context:
+    """vulkan::Context (crates/vulkan/src/context.rs:237-540): a device and its stream."""
+
+    def __init__(self, device: int = 0):
+        lib = library()
+        self._h = ctypes.c_void_p()
+        _check(lib.tgx_context_create(device, ctypes.byref(self._h)))
+        _open_contexts.add(self)
+
+    def report(self) -> dict:
+        r = _Report()
+        _check(library().tgx_context_report(self._h, ctypes.byref(r)))
+        return {
+            "name": r.name.decode(),
+            "arch": r.arch.decode(),
+            "compute_units": r.compute_units,
+            "clock_khz": r.clock_khz,
+            "memory_clock_khz": r.memory_clock_khz,
+            "memory_bytes": r.memory_bytes,
+            "wavefront": r.wavefront,
+        }
+
+    def close(self) -> None:
+        if self._h:
+            for d in list(_open_decoders):
+                if d.ctx is self:
+                    d.close()
+            library().tgx_context_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Decoder:
+    """decode::Decoder (decode.rs:778-913): the stack's weights, its paged KV cache and the step
+    recorded as a HIP graph."""
+
+    def __init__(self, ctx: Context, shape: Shape, batch: Batch = Batch()):
+        self.ctx = ctx
+        self.shape = shape
+        self.batch = batch
+        s, self._factors = _shape_struct(shape)
+        b = _Batch(batch.rows, batch.slots, batch.block_tokens, batch.blocks)
+        self._h = ctypes.c_void_p()
+        _check(library().tgx_decoder_create(ctx._h, ctypes.byref(s), ctypes.byref(b), ctypes.byref(self._h)))
+        _open_decoders.add(self)
+
+    # -- weights --
+    def load(self, name: str, values: np.ndarray) -> None:
+        """load_stack's write of one tensor (decode.rs:740-776): f32, bf16 (uint16 bits) or f16."""
+        a = np.ascontiguousarray(values)
+        if a.dtype == np.float32:
+            dtype = F32
+        elif a.dtype == np.uint16:
+            dtype = BF16
+        elif a.dtype == np.float16:
+            dtype = F16
+        else:
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            dtype = F32
+        _check(library().tgx_decoder_load(self._h, name.encode(), _ptr(a), dtype, a.size))
+
+    def load_all(self, weights: dict) -> None:
+        for name, values in weights.items():
+            self.load(name, values)
+
+    # -- steps --
+    def _rows(self, rows: Sequence[Optional[Row]]):
+        arr = (_Row * len(rows))()
+        for i, r in enumerate(rows):
+            if r is None:
+                arr[i].position, arr[i].slot = SPARE, SPARE
+            else:
+                arr[i].position, arr[i].slot = r.position, r.slot
+        return arr
+
+    def set_rows(self, rows: Sequence[Optional[Row]], x: np.ndarray) -> None:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        _check(library().tgx_decoder_set_rows(self._h, self._rows(rows), len(rows), _ptr(x)))
+
+    def start(self) -> None:
+        _check(library().tgx_decoder_start(self._h))
+
+    def wait(self) -> None:
+        _check(library().tgx_decoder_wait(self._h))
+
+    def output(self) -> np.ndarray:
+        out = np.empty((self.batch.rows, self.shape.hidden), dtype=np.float32)
+        _check(library().tgx_decoder_output(self._h, _ptr(out)))
+        return out
+
+    def step_rows(self, rows: Sequence[Optional[Row]], x: np.ndarray) -> np.ndarray:
+        """Decoder::step_rows (decode.rs:849-853): x [rows][hidden] -> out [rows][hidden]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty((len(rows), self.shape.hidden), dtype=np.float32)
+        _check(library().tgx_decoder_step_rows(self._h, self._rows(rows), len(rows), _ptr(x), _ptr(out)))
+        return out
+
+    def step(self, position: int, x: np.ndarray) -> np.ndarray:
+        """Decoder::step (decode.rs:833-837): batch 1, slot 0."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(1, -1)
+        out = np.empty((1, self.shape.hidden), dtype=np.float32)
+        _check(library().tgx_decoder_step(self._h, position, _ptr(x), _ptr(out)))
+        return out[0]
+
+    def release_slot(self, slot: int) -> None:
+        _check(library().tgx_decoder_release_slot(self._h, slot))
+
+    def reserve(self, slot: int, positions: int) -> None:
+        _check(library().tgx_decoder_reserve(self._h, slot, positions))
+
+    def free_blocks(self) -> int:
+        n = ctypes.c_int()
+        _check(library().tgx_decoder_free_blocks(self._h, ctypes.byref(n)))
+        return n.value
+
+    def launch(self, times: int = 1, advance: bool = False) -> None:
+        _check(library().tgx_decoder_launch(self._h, times, 1 if advance else 0))
+
+    def elapsed_ms(self) -> float:
+        v = ctypes.c_float()
+        _check(library().tgx_decoder_elapsed_ms(self._h, ctypes.byref(v)))
+        return v.value
+
+    def set_timed(self, timed: bool) -> None:
+        """Decoder::new's `timed`: launch dispatch by dispatch, each timed."""
+        _check(library().tgx_decoder_set_timed(self._h, 1 if timed else 0))
+
+    def timings(self) -> list:
+        """Decoder::timings (decode.rs:891-893): [(label, ms)] of the last timed step."""
+        n = ctypes.c_int()
+        _check(library().tgx_decoder_timings(self._h, 0, None, ctypes.byref(n)))
+        arr = (_Timing * max(1, n.value))()
+        _check(library().tgx_decoder_timings(self._h, n.value, arr, ctypes.byref(n)))
+        return [(arr[i].label.decode(), arr[i].ms) for i in range(n.value)]
+
+    def dispatches(self) -> int:
+        v = ctypes.c_int()
+        _check(library().tgx_decoder_dispatches(self._h, ctypes.byref(v)))
+        return v.value
+
+    def device_bytes(self) -> int:
+        v = ctypes.c_size_t()
+        _check(library().tgx_decoder_device_bytes(self._h, ctypes.byref(v)))
+        return v.value
+
+    def read_cache(self, slot: int, positions: int):
+        s = self.shape
+        k = np.empty((s.layers, s.kv_heads, positions, s.head_dim), dtype=np.float32)
+        v = np.empty_like(k)
+        _check(library().tgx_decoder_read_cache(self._h, slot, positions, _ptr(k), _ptr(v)))
+        return k, v
+
+    # -- prefill --
+    def prefill(self, start: int, x: np.ndarray, slot: int = 0) -> np.ndarray:
+        """Prefill::run (prefill.rs:473-503): x [len][hidden] from `start` of `slot`."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n = x.shape[0]
+        out = np.empty((n, self.shape.hidden), dtype=np.float32)
+        _check(library().tgx_prefill_run(self._h, slot, start, n, _ptr(x), _ptr(out)))
+        return out
+
+    def prefill_launch(self, count: int, length: int, times: int = 1) -> None:
+        _check(library().tgx_prefill_launch(self._h, count, length, times))
+
+    def close(self) -> None:
+        if self._h:
+            library().tgx_decoder_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.close()
+        except Exception:
+            pass
