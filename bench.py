@@ -64,7 +64,7 @@ def kernel_bytes(shape, label: str, rows: int, kv_positions: int) -> int:
     qkv = (H + 2 * KV) * d
     if label == "gemv_qkv_rope":
         return qkv * h * 2 + rows * h * 4 + rows * qkv * 2
-    if label == "attention_split":
+    if label == "attention_decode":
         return kv_positions * KV * d * 2 * 2 + rows * H * d * 2 * 2
     if label == "o_proj":
         return h * H * d * 2 + rows * H * d * 2 + rows * h * 4 * 2
@@ -84,6 +84,9 @@ def step_bytes(shape, positions) -> int:
     return shape.weight_bytes() + sum(kvpp * (p + 1) for p in positions) + kvpp * len(positions)
 
 
+EAGER = False  # launch dispatch by dispatch instead of the recorded graph (for profilers)
+
+
 def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int, profile_steps: int = 4):
     """Decode `steps` steps of `rows` requests, request r from position contexts[r]; returns the
     timing record."""
@@ -92,22 +95,15 @@ def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int,
     capacity = int(np.ceil((max(contexts) + steps + warmup + 1) / 256.0) * 256)
     spec, shape = spec_and_shape(capacity)
     dec = tgx.Decoder(ctx, shape, tgx.Batch(rows=rows, slots=rows))
+    if EAGER:
+        dec.set_graph(False)
     load(dec, weights)
-    x = np.asarray(__import__("tgx.synth", fromlist=["embeddings"]).embeddings(7, "bench.x", rows, shape.hidden))
-    # Fill each request's cache up to its context: the rows walk their positions together, row r
-    # joining once the longest context has room for it.
-    longest = max(contexts)
-    for t in range(longest):
-        placed = [tgx.Row(t - (longest - c), r) if t >= longest - c else None for r, c in enumerate(contexts)]
-        if rows == 1:
-            break
-        dec.set_rows(placed, x)
-        dec.start()
-        dec.wait()
-    if rows == 1:
-        dec.set_rows([tgx.Row(0, 0)], x)
-        dec.launch(contexts[0], advance=True)
-        dec.wait()
+    from tgx.synth import embeddings
+
+    x = embeddings(7, "bench.x", rows, shape.hidden)
+    # Each request's prompt, prefilled at once into its slot.
+    prompt = embeddings(8, "bench.prompt", int(sum(contexts)), shape.hidden)
+    dec.prefill_runs([(r, 0, int(c)) for r, c in enumerate(contexts)], prompt)
     for r, c in enumerate(contexts):
         dec.reserve(r, c + steps + warmup + 1)
     start_rows = [tgx.Row(c, r) for r, c in enumerate(contexts)]
@@ -162,6 +158,84 @@ def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int,
     }
 
 
+MFMA_PEAK = 2.5e15  # MI355X dense bf16, FLOP/s
+
+
+def prefill_flops(shape, count: int, length: int) -> tuple[int, int]:
+    """Linear FLOPs (2 x every weight per position, norms aside) and causal attention FLOPs
+    (4 L H d (t + 1) at position t) of `count` runs of `length` positions from 0."""
+    linear_params = shape.weight_bytes(1) - shape.layers * 2 * shape.hidden - shape.hidden
+    linear = 2 * linear_params * count * length
+    attention = 4 * shape.layers * shape.heads * shape.head_dim * count * length * (length + 1) // 2
+    return linear, attention
+
+
+def gemm_flops(shape, label: str, rows: int) -> int:
+    h, i, H, KV, d = shape.hidden, shape.inner, shape.heads, shape.kv_heads, shape.head_dim
+    n_k = {"prefill_qkv": ((H + 2 * KV) * d, h), "prefill_o": (h, H * d), "prefill_gate_up": (2 * i, h),
+           "prefill_down": (h, i)}.get(label)
+    return 2 * rows * n_k[0] * n_k[1] if n_k else 0
+
+
+def run_prefill(ctx, weights, count: int, length: int, times: int, decode_steps: int):
+    """`count` runs of `length` positions prefilled at once, then `decode_steps` decode steps."""
+    import tgx
+    from tgx.synth import embeddings
+
+    capacity = int(np.ceil((length + decode_steps + 1) / 256.0) * 256)
+    spec, shape = spec_and_shape(capacity)
+    dec = tgx.Decoder(ctx, shape, tgx.Batch(rows=count, slots=count))
+    if EAGER:
+        dec.set_graph(False)
+    load(dec, weights)
+    x = embeddings(9, "bench.prefill", count * length, shape.hidden)
+    runs = [(s, 0, length) for s in range(count)]
+    out = dec.prefill_runs(runs, x)
+    finite = bool(np.all(np.isfinite(out)))
+    dec.prefill_launch(1)
+    dec.wait()
+    t0 = time.perf_counter()
+    dec.prefill_launch(times)
+    dec.wait()
+    wall = (time.perf_counter() - t0) / times
+    gpu = dec.elapsed_ms() / times * 1e-3
+    dec.set_timed(True)
+    dec.prefill_launch(1)
+    dec.wait()
+    per = {}
+    for label, ms in dec.timings():
+        per.setdefault(label, []).append(ms)
+    dec.set_timed(False)
+    # The decode steps that follow, every run at once.
+    xs = embeddings(10, "bench.after", count, shape.hidden)
+    for r in range(count):
+        dec.reserve(r, length + decode_steps + 1)
+    dec.set_rows([tgx.Row(length, r) for r in range(count)], xs)
+    t1 = time.perf_counter()
+    dec.launch(decode_steps, advance=True)
+    dec.wait()
+    dwall = time.perf_counter() - t1
+    dec.close()
+    linear, attention = prefill_flops(shape, count, length)
+    kernels = {}
+    rows = count * length
+    for label, ms in per.items():
+        avg = float(np.mean(ms))
+        f = gemm_flops(shape, label, rows)
+        kernels[label] = {"avg_us": avg * 1e3, "launches": len(ms), "TFLOP_s": f / (avg * 1e-3) / 1e12 if f else None,
+                          "flops": f}
+    return {
+        "tokens_per_s": rows / wall,
+        "ms": wall * 1e3,
+        "gpu_ms": gpu * 1e3,
+        "flops": linear + attention,
+        "mfma_fraction": (linear + attention) / wall / MFMA_PEAK,
+        "kernels": kernels,
+        "finite": finite,
+        "decode_steps_per_s": decode_steps / dwall,
+    }
+
+
 def cpu_baseline(weights, seconds: float):
     """The fp32 CPU path (the oracle in float32, OpenMP over the host's cores) on the same
     24-layer stack at batch 1, decode steps from position 256 of a zero-filled cache."""
@@ -199,8 +273,13 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=1, help="the batch the headline value is taken at")
     ap.add_argument("--no-extra", action="store_true", help="skip the batch-16/64 runs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 8 x 2048 prefill")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch each step dispatch by dispatch, not as the recorded graph (for profilers)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (requests would be routed to "
               "GPUs at admission, with no collective); run with --gpus 1.", file=sys.stderr)
@@ -233,11 +312,38 @@ def main() -> int:
             ctxs = [int(c) for c in np.random.default_rng(rows).integers(64, 1025, rows)]
             r = run_decode(ctx, weights, rows, ctxs, 200, 10)
             r.pop("shape")
+            for label, k in sorted(r["kernels"].items(), key=lambda kv: -kv[1]["per_step_us"]):
+                log(f"  [{rows:2d}] {label:16s} {k['avg_us']:8.2f} us/launch {k['per_step_us']:8.1f} us/step {k['GB_s'] or 0:8.1f} GB/s")
             batches[str(rows)] = {k: r[k] for k in ("steps_per_s", "ms_per_step", "hbm_fraction", "kernel_sum_us")}
+            batches[str(rows)]["kernels_us"] = {k: round(v["avg_us"], 3) for k, v in r["kernels"].items()}
             batches[str(rows)]["tokens_per_s"] = r["steps_per_s"] * rows
             batches[str(rows)]["contexts"] = "U[64,1024] seeded, 200 steps"
             log(f"batch {rows}: {r['steps_per_s']:.1f} steps/s ({r['steps_per_s']*rows:.0f} tok/s), "
                 f"{r['hbm_fraction']*100:.1f}% of HBM peak on algorithmic bytes")
+
+    prefill = None
+    if not args.no_prefill:
+        pf = run_prefill(ctx, weights, 8, 2048, 3, 32)
+        for label, k in sorted(pf["kernels"].items(), key=lambda kv: -kv[1]["avg_us"] * kv[1]["launches"]):
+            log(f"  [prefill] {label:18s} {k['avg_us']:10.1f} us x {k['launches']:3d}"
+                + (f"  {k['TFLOP_s']:8.1f} TFLOP/s" if k["TFLOP_s"] else ""))
+        log(f"prefill 8 x 2048: {pf['tokens_per_s']:.0f} tok/s, {pf['ms']:.2f} ms, "
+            f"{pf['mfma_fraction'] * 100:.1f}% of bf16 MFMA peak; then {pf['decode_steps_per_s']:.0f} steps/s at batch 8")
+        gemms = {k: v for k, v in pf["kernels"].items() if v["TFLOP_s"]}
+        dom = max(gemms.items(), key=lambda kv: kv[1]["avg_us"] * kv[1]["launches"])
+        prefill = {
+            "workload": "8 runs x 2048 positions, causal, 24 layers, bf16; then 32 decode steps at batch 8",
+            "tokens_per_s": round(pf["tokens_per_s"], 1),
+            "ms": round(pf["ms"], 3),
+            "flops": pf["flops"],
+            "mfma_fraction": round(pf["mfma_fraction"], 4),
+            "finite": pf["finite"],
+            "decode_steps_per_s_after": round(pf["decode_steps_per_s"], 1),
+            "roofline": {"bound": "mfma", "kernel": dom[0], "achieved": round(dom[1]["TFLOP_s"], 1),
+                         "peak": MFMA_PEAK / 1e12, "unit": "TFLOP/s", "frac": round(dom[1]["TFLOP_s"] * 1e12 / MFMA_PEAK, 4),
+                         "avg_us": round(dom[1]["avg_us"], 2)},
+            "kernels_us": {k: round(v["avg_us"], 2) for k, v in pf["kernels"].items()},
+        }
 
     # The roofline of the step's dominant kernel: the one with the most time per step.
     dom_label, dom = max(head["kernels"].items(), key=lambda kv: kv[1]["per_step_us"])
@@ -290,6 +396,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "batches": batches,
+        "prefill": prefill,
         "kernels_us": {k: round(v["avg_us"], 3) for k, v in head["kernels"].items()},
         "device": {"name": report["name"], "arch": report["arch"], "clock_khz": report["clock_khz"]},
     }

@@ -166,6 +166,10 @@ tgx_status tgx_decoder_elapsed_ms(const tgx_decoder* dec, float* out);
  * dispatch records, so that its time is the kernel's alone. */
 tgx_status tgx_decoder_set_timed(tgx_decoder* dec, int timed);
 
+/* Whether steps launch the recorded HIP graph (the default) or their dispatches one by one,
+ * as a profiler that follows single dispatches needs. The same kernels either way. */
+tgx_status tgx_decoder_set_graph(tgx_decoder* dec, int use_graph);
+
 /* Decoder::timings (decode.rs:891-893): each dispatch's label and GPU time in the last timed step,
  * in order; *n is the number of dispatches (0 when not timed), of which `max` are written. */
 typedef struct {
@@ -188,15 +192,24 @@ tgx_status tgx_decoder_read_cache(tgx_decoder* dec, uint32_t slot, uint32_t posi
 /* Prefill::run (prefill.rs:473-503): runs `len` positions from `start` of `slot` at once, their
  * hidden states x [len][hidden] f32, writing their keys and values into the decoder's cache for
  * its steps to go on from, each position attending over the slot up to itself. Returns the
- * outputs after the final norm, [len][hidden] f32. The reference runs slot 0 only; any slot
- * is taken here. */
+ * outputs after the final norm, [len][hidden] f32. The reference runs slot 0 only and at most
+ * 1024 positions a program; any slot and any length within the capacity are taken here. */
 tgx_status tgx_prefill_run(tgx_decoder* dec, uint32_t slot, uint32_t start, uint32_t len,
                            const float* x, float* out);
 
-/* Device-resident prefill for timing: `len` positions in each of `count` slots from position 0
- * (slots 0..count-1), the hidden states already on the device (the last x given to
- * tgx_prefill_run, repeated), launched `times` times. Returns when launched. */
-tgx_status tgx_prefill_launch(tgx_decoder* dec, uint32_t count, uint32_t len, int times);
+/* Several runs at once, each in its own slot, as one prefill: x holds their hidden states one run
+ * after another ([sum of len][hidden]), and out their outputs in the same order. */
+typedef struct {
+    uint32_t slot, start, len;
+} tgx_run;
+tgx_status tgx_prefill_runs(tgx_decoder* dec, const tgx_run* runs, int nruns, const float* x,
+                            float* out);
+
+/* Launches the last prefill again `times` times over its input still on the device, copying
+ * nothing in or out (what a caller whose inputs are already in HBM runs; it writes the same
+ * keys and values again). Returns when launched; tgx_decoder_wait waits, and
+ * tgx_decoder_elapsed_ms times it. */
+tgx_status tgx_prefill_launch(tgx_decoder* dec, int times);
 
 #ifdef __cplusplus
 }

@@ -158,6 +158,14 @@ tgx_status tgx_decoder_set_timed(tgx_decoder* dec, int timed) {
     return TGX_OK;
 }
 
+tgx_status tgx_decoder_set_graph(tgx_decoder* dec, int use_graph) {
+    clear_error();
+    if (!dec) return fail(TGX_E_ARG, "null decoder");
+    if (dec->dec->pending) return fail(TGX_E_BUSY, "a step is under way");
+    dec->dec->use_graph = use_graph != 0;
+    return TGX_OK;
+}
+
 tgx_status tgx_decoder_timings(tgx_decoder* dec, int max, tgx_timing* out, int* n) {
     clear_error();
     return decoder_timings(DEC(dec), max, out, n);
@@ -184,14 +192,18 @@ tgx_status tgx_decoder_read_cache(tgx_decoder* dec, uint32_t slot, uint32_t posi
 
 tgx_status tgx_prefill_run(tgx_decoder* dec, uint32_t slot, uint32_t start, uint32_t len, const float* x, float* out) {
     clear_error();
-    (void)dec; (void)slot; (void)start; (void)len; (void)x; (void)out;
-    return fail(TGX_E_KERNELS, "the prefill kernels are not built yet");
+    const tgx_run run{slot, start, len};
+    return prefill_runs(DEC(dec), &run, 1, x, out);
 }
 
-tgx_status tgx_prefill_launch(tgx_decoder* dec, uint32_t count, uint32_t len, int times) {
+tgx_status tgx_prefill_runs(tgx_decoder* dec, const tgx_run* runs, int nruns, const float* x, float* out) {
     clear_error();
-    (void)dec; (void)count; (void)len; (void)times;
-    return fail(TGX_E_KERNELS, "the prefill kernels are not built yet");
+    return prefill_runs(DEC(dec), runs, nruns, x, out);
+}
+
+tgx_status tgx_prefill_launch(tgx_decoder* dec, int times) {
+    clear_error();
+    return prefill_launch(DEC(dec), times);
 }
 
 }  // extern "C"

@@ -24,12 +24,17 @@ namespace tgx {
 
 namespace {
 
-// Projections: a workgroup of eight waves to a strip of 16 rows (two strips for gate/up).
+// Projections: a workgroup of eight waves to a strip of R rows (two strips of 16 for gate/up)
+// against one 16-row tile of the batch, the tile of blockIdx.y. R is 4 or 8 at small batches,
+// so that the strips of a projection fill the 256 CUs, and 16 at large ones, whose tiles fill
+// them instead; the workgroups of one strip sit on one XCD (their ids differ by a multiple of
+// the strips, a multiple of 8) and read its weights from there after the first.
 constexpr int GEMV_WAVES = 8;
 constexpr int GEMV_THREADS = GEMV_WAVES * WAVE;
 // K is taken in chunks of 32 k-blocks (1024 columns); wave w's chain runs over k-blocks
-// 32 c + 4 w .. 32 c + 4 w + 3 of chunk c, chunk after chunk, whatever the batch.
+// 32 c + 4 w .. 32 c + 4 w + 3 of chunk c, chunk after chunk, whatever the batch and strip.
 constexpr int CHUNK_KB = 32;
+constexpr int CHUNK_COLS = CHUNK_KB * 32;
 constexpr int PER_WAVE = CHUNK_KB / GEMV_WAVES;
 constexpr int MAX_CHUNKS = 4;  // K up to 4096; kernels are built for 1 chunk and for up to 4
 
@@ -39,94 +44,141 @@ constexpr int ATTN_THREADS = ATTN_WAVES * WAVE;
 
 __device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// The B operand in LDS: xs[(t CHUNK_KB + kb) 64 + 16 g + c] holds batch row 16 t + c, columns
-// 32 kb + 8 g .. + 7 of the chunk; rows past B are zero. col8 numbers the groups of 8 columns
-// of the chunk (0 .. 127).
-__device__ __forceinline__ int xs_index(int b, int col8) {
-    return ((b / 16) * CHUNK_KB + col8 / 4) * 64 + (col8 % 4) * 16 + b % 16;
-}
+// The B operand in LDS, one chunk of the tile's 16 rows: xs[kb 64 + 16 g + c] holds row c,
+// columns 32 kb + 8 g .. + 7 of the chunk. col8 numbers the groups of 8 columns (0 .. 127).
+__device__ __forceinline__ int xs_index(int c, int col8) { return (col8 / 4) * 64 + (col8 % 4) * 16 + c; }
 
-// The reciprocal root mean square of each of the batch's rows of x (norm.glsl:12-29), into
-// scales[b]: a wave to a row, lane l summing elements [l K/64, (l+1) K/64) in order, the lanes
-// added by a butterfly; the same arithmetic for a row whatever the batch.
-__device__ void row_scales(const float* __restrict__ x, float eps, int B, int K, float* scales) {
+// RMSNorm(x) gain of the tile's rows into xs, chunk by chunk through `each(chunk)` (norm.glsl:
+// 12-53): a wave to a row; lane l sums the squares of its 16 elements of each chunk in order,
+// chunk after chunk, and the lanes are added by a butterfly; the same arithmetic for a row
+// whatever the batch. The rows of the tile past B are zero.
+template <typename Each>
+__device__ void stage_normed(const float* __restrict__ x, const float* __restrict__ gain, float eps, int B, int K,
+                             int tile, uint4* xs, float* scales, Each each) {
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int per_lane = K / WAVE;
-    for (int b = w; b < B; b += GEMV_WAVES) {
-        const float* row = x + (size_t)b * K + lane * per_lane;
-        float squares = 0.f;
-        for (int e = 0; e < per_lane; e += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(row + e);
-            squares += v.x * v.x;
-            squares += v.y * v.y;
-            squares += v.z * v.z;
-            squares += v.w * v.w;
+    const int chunks = K / CHUNK_COLS;
+    if (chunks > 1) {
+        for (int c = w; c < 16; c += GEMV_WAVES) {
+            const int b = tile * 16 + c;
+            if (b >= B) continue;
+            float squares = 0.f;
+            for (int ch = 0; ch < chunks; ++ch) {
+                const float* row = x + (size_t)b * K + ch * CHUNK_COLS + lane * 16;
+#pragma unroll
+                for (int e = 0; e < 16; e += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(row + e);
+                    squares += v.x * v.x;
+                    squares += v.y * v.y;
+                    squares += v.z * v.z;
+                    squares += v.w * v.w;
+                }
+            }
+            const float total = wave_sum(squares);
+            if (lane == 0) scales[c] = 1.0f / sqrtf(total / (float)K + eps);
         }
-        const float total = wave_sum(squares);
-        if (lane == 0) scales[b] = 1.0f / sqrtf(total / (float)K + eps);
+        __syncthreads();
     }
-}
-
-// Chunk c of RMSNorm(x) gain, rows [0, NT 16), into xs (bf16).
-template <int NT>
-__device__ void stage_normed(const float* __restrict__ x, const float* __restrict__ gain, const float* scales,
-                             int B, int K, int c, uint4* xs) {
-    constexpr int groups = CHUNK_KB * 4;  // groups of 8 columns in a chunk
-    for (int i = threadIdx.x; i < NT * 16 * groups; i += GEMV_THREADS) {
-        const int b = i / groups, g8 = i % groups;
-        uint4 packed = make_uint4(0, 0, 0, 0);
-        if (b < B) {
-            const int k0 = c * CHUNK_KB * 32 + g8 * 8;
-            const float scale = scales[b];
-            const float4 a = *reinterpret_cast<const float4*>(x + (size_t)b * K + k0);
-            const float4 e = *reinterpret_cast<const float4*>(x + (size_t)b * K + k0 + 4);
-            const float4 ga = *reinterpret_cast<const float4*>(gain + k0);
-            const float4 gb = *reinterpret_cast<const float4*>(gain + k0 + 4);
-            packed.x = pack_bf16x2(a.x * scale * ga.x, a.y * scale * ga.y);
-            packed.y = pack_bf16x2(a.z * scale * ga.z, a.w * scale * ga.w);
-            packed.z = pack_bf16x2(e.x * scale * gb.x, e.y * scale * gb.y);
-            packed.w = pack_bf16x2(e.z * scale * gb.z, e.w * scale * gb.w);
+    for (int ch = 0; ch < chunks; ++ch) {
+        if (ch > 0) __syncthreads();
+        float4 g[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] = *reinterpret_cast<const float4*>(gain + ch * CHUNK_COLS + lane * 16 + 4 * e);
+        for (int c = w; c < 16; c += GEMV_WAVES) {
+            const int b = tile * 16 + c;
+            uint4 packed[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+            if (b < B) {
+                const float* row = x + (size_t)b * K + ch * CHUNK_COLS + lane * 16;
+                float4 v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = *reinterpret_cast<const float4*>(row + 4 * e);
+                float scale;
+                if (chunks == 1) {
+                    float squares = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        squares += v[e].x * v[e].x;
+                        squares += v[e].y * v[e].y;
+                        squares += v[e].z * v[e].z;
+                        squares += v[e].w * v[e].w;
+                    }
+                    scale = 1.0f / sqrtf(wave_sum(squares) / (float)K + eps);
+                } else {
+                    scale = scales[c];
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float4 a = v[2 * h], e2 = v[2 * h + 1], ga = g[2 * h], gb = g[2 * h + 1];
+                    packed[h].x = pack_bf16x2(a.x * scale * ga.x, a.y * scale * ga.y);
+                    packed[h].y = pack_bf16x2(a.z * scale * ga.z, a.w * scale * ga.w);
+                    packed[h].z = pack_bf16x2(e2.x * scale * gb.x, e2.y * scale * gb.y);
+                    packed[h].w = pack_bf16x2(e2.z * scale * gb.z, e2.w * scale * gb.w);
+                }
+            }
+            xs[xs_index(c, 2 * lane)] = packed[0];
+            xs[xs_index(c, 2 * lane + 1)] = packed[1];
         }
-        xs[xs_index(b, g8)] = packed;
+        __syncthreads();
+        each(ch);
     }
 }
 
-// Chunk c of bf16 vectors [B][K], rows [0, NT 16), into xs.
-template <int NT>
-__device__ void stage_raw(const uint16_t* __restrict__ xb, int B, int K, int c, uint4* xs) {
-    constexpr int groups = CHUNK_KB * 4;
-    for (int i = threadIdx.x; i < NT * 16 * groups; i += GEMV_THREADS) {
-        const int b = i / groups, g8 = i % groups;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (b < B) v = load16(xb + (size_t)b * K + (size_t)c * CHUNK_KB * 32 + g8 * 8);
-        xs[xs_index(b, g8)] = v;
+// Bf16 vectors [B][K] of the tile's rows into xs, chunk by chunk through `each(chunk)`. Every
+// chunk's vectors are loaded first (MAXC chunks at most), so that the chunks cost one round trip
+// to memory, not one each.
+template <int MAXC, typename Each>
+__device__ void stage_raw(const uint16_t* __restrict__ xb, int B, int K, int tile, uint4* xs, Each each) {
+    constexpr int per_thread = 16 * (CHUNK_COLS / 8) / GEMV_THREADS;  // uint4 per chunk
+    const int chunks = K / CHUNK_COLS;
+    uint4 v[MAXC][per_thread];
+#pragma unroll
+    for (int ch = 0; ch < MAXC; ++ch)
+#pragma unroll
+        for (int j = 0; j < per_thread; ++j) {
+            const int i = threadIdx.x + j * GEMV_THREADS;
+            const int c = i / (CHUNK_COLS / 8), g8 = i % (CHUNK_COLS / 8);
+            const int b = tile * 16 + c;
+            v[ch][j] = make_uint4(0, 0, 0, 0);
+            if (ch < chunks && b < B) v[ch][j] = load16(xb + (size_t)b * K + (size_t)ch * CHUNK_COLS + g8 * 8);
+        }
+#pragma unroll
+    for (int ch = 0; ch < MAXC; ++ch) {
+        if (ch >= chunks) break;
+        if (ch > 0) __syncthreads();
+#pragma unroll
+        for (int j = 0; j < per_thread; ++j) {
+            const int i = threadIdx.x + j * GEMV_THREADS;
+            xs[xs_index(i / (CHUNK_COLS / 8), i % (CHUNK_COLS / 8))] = v[ch][j];
+        }
+        __syncthreads();
+        each(ch);
     }
 }
 
-// One wave's chains for strips `strip[s]` of W [N][K] against the batch, over every chunk.
-// The weights of all its k-blocks are loaded first, so that they are in flight while the
+// One wave's chains for strips `strip[s]` (R rows each) of W [N][K] against the tile, over every
+// chunk. The weights of all its k-blocks are loaded first, so that they are in flight while the
 // vectors are staged; the products of chunk c follow its staging.
-template <int S, int NT, int MAXC>
+template <int S, int R, int MAXC>
 struct Gemv {
-    f32x4 acc[S][NT];
+    f32x4 acc[S];
     uint4 wf[MAXC][PER_WAVE][S];
-    int chunks;
 
     __device__ void load(const uint16_t* __restrict__ w, const int (&strip)[S], int kblocks) {
         const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-        chunks = kblocks / CHUNK_KB;
+        const int chunks = kblocks / CHUNK_KB;
+        const bool live = lane % 16 < R;
 #pragma unroll
         for (int c = 0; c < MAXC; ++c)
 #pragma unroll
             for (int j = 0; j < PER_WAVE; ++j)
 #pragma unroll
-                for (int s = 0; s < S; ++s)
-                    if (c < chunks)
-                        wf[c][j][s] = load16(w + weight_tile_index(strip[s], c * CHUNK_KB + wave * PER_WAVE + j, kblocks) + lane * 8);
+                for (int s = 0; s < S; ++s) {
+                    wf[c][j][s] = make_uint4(0, 0, 0, 0);
+                    if (c < chunks && live)
+                        wf[c][j][s] = load16(w + weight_tile_index(strip[s], c * CHUNK_KB + wave * PER_WAVE + j, kblocks, R) +
+                                             weight_lane_offset(lane, R));
+                }
 #pragma unroll
-        for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < S; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     // The products of chunk c, once it is staged.
@@ -137,38 +189,32 @@ struct Gemv {
             if (cc != c) continue;  // registers indexed by constants only
 #pragma unroll
             for (int j = 0; j < PER_WAVE; ++j) {
-                const int kb = wave * PER_WAVE + j;
+                const uint4 xv = xs[(wave * PER_WAVE + j) * 64 + lane];
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const uint4 xv = xs[(t * CHUNK_KB + kb) * 64 + lane];
-#pragma unroll
-                    for (int s = 0; s < S; ++s) acc[s][t] = mfma16(wf[cc][j][s], xv, acc[s][t]);
-                }
+                for (int s = 0; s < S; ++s) acc[s] = mfma16(wf[cc][j][s], xv, acc[s]);
             }
         }
     }
 };
 
-// Every wave's chains into red, [wave][s][t][lane] as f32x4, behind barriers (red shares memory
+// Every wave's chains into red, [wave][s][lane] as f32x4, behind barriers (red shares memory
 // with the staged vectors).
-template <int S, int NT>
-__device__ void spill(const f32x4 (&acc)[S][NT], f32x4* red) {
+template <int S>
+__device__ void spill(const f32x4 (&acc)[S], f32x4* red) {
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < S; ++s)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) red[((w * S + s) * NT + t) * 64 + lane] = acc[s][t];
+    for (int s = 0; s < S; ++s) red[(w * S + s) * 64 + lane] = acc[s];
     __syncthreads();
 }
 
-// Row r of strip s against batch row b: the waves' chains added in wave order.
-template <int S, int NT>
-__device__ __forceinline__ float reduced(const f32x4* red, int s, int r, int b) {
-    const int t = b / 16, lane = (r / 4) * 16 + b % 16, i = r % 4;
+// Row r of strip s against row c of the tile: the waves' chains added in wave order.
+template <int S>
+__device__ __forceinline__ float reduced(const f32x4* red, int s, int r, int c) {
+    const int lane = (r / 4) * 16 + c, i = r % 4;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < GEMV_WAVES; ++w) v += red[((w * S + s) * NT + t) * 64 + lane][i];
+    for (int w = 0; w < GEMV_WAVES; ++w) v += red[(w * S + s) * 64 + lane][i];
     return v;
 }
 
@@ -187,36 +233,31 @@ __device__ __forceinline__ long block_of(const DecodeArgs& a, uint32_t slot, uin
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
-// gemv_qkv_rope: a workgroup per strip of 16 permuted rows (8 RoPE pairs of one head).
-template <int NT, int MAXC>
+// gemv_qkv_rope: workgroup (strip, tile): a strip of R permuted rows (R/2 RoPE pairs of a head).
+template <int R, int MAXC>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, LayerArgs l) {
-    extern __shared__ uint4 smem[];
-    __shared__ float scales[64];
+    __shared__ uint4 xs[CHUNK_KB * 64];
+    __shared__ float scales[16];
     const int K = a.hidden, kblocks = K / 32;
-    const int strip_id = blockIdx.x;
+    const int strip_id = blockIdx.x, tile = blockIdx.y;
     const int strip[1] = {strip_id};
-    Gemv<1, NT, MAXC> g;
+    Gemv<1, R, MAXC> g;
     g.load(l.qkv, strip, kblocks);
-    row_scales(l.x, a.eps, a.rows, K, scales);
-    for (int c = 0; c < g.chunks; ++c) {
-        __syncthreads();
-        stage_normed<NT>(l.x, l.input_norm, scales, a.rows, K, c, smem);
-        __syncthreads();
-        g.chunk(c, smem);
-    }
-    f32x4* red = reinterpret_cast<f32x4*>(smem);
-    spill<1, NT>(g.acc, red);
+    stage_normed(l.x, l.input_norm, a.eps, a.rows, K, tile, xs, scales, [&](int ch) { g.chunk(ch, xs); });
+    f32x4* red = reinterpret_cast<f32x4*>(xs);
+    spill<1>(g.acc, red);
 
-    const int quarters = HEAD_DIM / 16;
-    const int head = strip_id / quarters;
+    const int per_head = HEAD_DIM / R;  // strips to a head
+    const int head = strip_id / per_head;
     const int H = a.heads, KV = a.kv_heads;
-    for (int idx = threadIdx.x; idx < 8 * a.rows; idx += GEMV_THREADS) {
-        const int p = idx % 8, b = idx / 8;
+    for (int idx = threadIdx.x; idx < (R / 2) * 16; idx += GEMV_THREADS) {
+        const int p = idx % (R / 2), c = idx / (R / 2);
+        const int b = tile * 16 + c;
         uint32_t pos, slot;
-        if (!placed(a, b, pos, slot)) continue;
-        const int i = (strip_id % quarters) * 8 + p;  // the pair's first dimension in the head
-        float va = reduced<1, NT>(red, 0, p, b);
-        float vc = reduced<1, NT>(red, 0, p + 8, b);
+        if (b >= a.rows || !placed(a, b, pos, slot)) continue;
+        const int i = (strip_id % per_head) * (R / 2) + p;  // the pair's first dimension in the head
+        float va = reduced<1>(red, 0, p, c);
+        float vc = reduced<1>(red, 0, p + R / 2, c);
         if (head < H + KV && a.rope) {
             // As upstream: x cos + rotate_half(x) sin (gemv_qkv_rope.comp:88-94).
             const float co = a.cos[(size_t)pos * (HEAD_DIM / 2) + i];
@@ -235,80 +276,74 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
         const long blk = block_of(a, slot, pos);
         if (blk < 0) continue;
         const int kv = head < H + KV ? head - H : head - H - KV;
-        uint16_t* tile = l.kv + ((size_t)blk * KV + kv) * 2 * KV_TILE;
+        uint16_t* tl = l.kv + ((size_t)blk * KV + kv) * 2 * KV_TILE;
         const int pp = (int)(pos % BLOCK_TOKENS);
         if (head < H + KV) {
-            tile[key_index(pp, i)] = (uint16_t)bf16_bits(va);
-            tile[key_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
+            tl[key_index(pp, i)] = (uint16_t)bf16_bits(va);
+            tl[key_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
         } else {
-            tile[KV_TILE + value_index(pp, i)] = (uint16_t)bf16_bits(va);
-            tile[KV_TILE + value_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
+            tl[KV_TILE + value_index(pp, i)] = (uint16_t)bf16_bits(va);
+            tl[KV_TILE + value_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
         }
     }
 }
 
 // ---------------------------------------------------------------------------------------------
-// gemv_gate_up: a workgroup per strip s of the gate and the same strip of up.
-template <int NT, int MAXC>
+// gemv_gate_up: workgroup (s, tile): strip s (16 rows) of the gate and the same strip of up.
+template <int MAXC>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_gate_up(DecodeArgs a, LayerArgs l) {
-    extern __shared__ uint4 smem[];
-    __shared__ float scales[64];
+    __shared__ uint4 xs[CHUNK_KB * 64];
+    __shared__ float scales[16];
     const int K = a.hidden, kblocks = K / 32;
-    const int s = blockIdx.x;
+    const int s = blockIdx.x, tile = blockIdx.y;
     const int strip[2] = {s, s + a.inner / 16};
-    Gemv<2, NT, MAXC> g;
+    Gemv<2, 16, MAXC> g;
     g.load(l.gate_up, strip, kblocks);
-    row_scales(l.mid, a.eps, a.rows, K, scales);
-    for (int c = 0; c < g.chunks; ++c) {
-        __syncthreads();
-        stage_normed<NT>(l.mid, l.post_norm, scales, a.rows, K, c, smem);
-        __syncthreads();
-        g.chunk(c, smem);
-    }
-    f32x4* red = reinterpret_cast<f32x4*>(smem);
-    spill<2, NT>(g.acc, red);
-    for (int idx = threadIdx.x; idx < 16 * a.rows; idx += GEMV_THREADS) {
-        const int r = idx % 16, b = idx / 16;
-        const float gate = reduced<2, NT>(red, 0, r, b);
-        const float up = reduced<2, NT>(red, 1, r, b);
+    stage_normed(l.mid, l.post_norm, a.eps, a.rows, K, tile, xs, scales, [&](int ch) { g.chunk(ch, xs); });
+    f32x4* red = reinterpret_cast<f32x4*>(xs);
+    spill<2>(g.acc, red);
+    for (int idx = threadIdx.x; idx < 16 * 16; idx += GEMV_THREADS) {
+        const int r = idx % 16, c = idx / 16;
+        const int b = tile * 16 + c;
+        if (b >= a.rows) continue;
+        const float gate = reduced<2>(red, 0, r, c);
+        const float up = reduced<2>(red, 1, r, c);
         l.mlp[(size_t)b * a.inner + s * 16 + r] = (uint16_t)bf16_bits(gate / (1.0f + __expf(-gate)) * up);
     }
 }
 
 // ---------------------------------------------------------------------------------------------
-// gemv_residual: out = residual + W x, a workgroup per strip of 16 rows over the whole of K.
-template <int NT, int MAXC>
+// gemv_residual: out = residual + W x; workgroup (strip, tile) over the whole of K.
+template <int R, int MAXC>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, ResidualArgs r) {
-    extern __shared__ uint4 smem[];
+    __shared__ uint4 xs[CHUNK_KB * 64];
     const int kblocks = r.K / 32;
-    const int strip_id = blockIdx.x;
+    const int strip_id = blockIdx.x, tile = blockIdx.y;
     const int strip[1] = {strip_id};
-    Gemv<1, NT, MAXC> g;
+    Gemv<1, R, MAXC> g;
     g.load(r.w, strip, kblocks);
-    for (int c = 0; c < g.chunks; ++c) {
-        __syncthreads();
-        stage_raw<NT>(r.x, a.rows, r.K, c, smem);
-        __syncthreads();
-        g.chunk(c, smem);
-    }
-    f32x4* red = reinterpret_cast<f32x4*>(smem);
-    spill<1, NT>(g.acc, red);
-    for (int idx = threadIdx.x; idx < 16 * a.rows; idx += GEMV_THREADS) {
-        const int row = idx % 16, b = idx / 16;
-        const size_t at = (size_t)b * r.N + strip_id * 16 + row;
-        r.out[at] = r.residual[at] + reduced<1, NT>(red, 0, row, b);
+    stage_raw<MAXC>(r.x, a.rows, r.K, tile, xs, [&](int ch) { g.chunk(ch, xs); });
+    f32x4* red = reinterpret_cast<f32x4*>(xs);
+    spill<1>(g.acc, red);
+    for (int idx = threadIdx.x; idx < R * 16; idx += GEMV_THREADS) {
+        const int row = idx % R, c = idx / R;
+        const int b = tile * 16 + c;
+        if (b >= a.rows) continue;
+        const size_t at = (size_t)b * r.N + strip_id * R + row;
+        r.out[at] = r.residual[at] + reduced<1>(red, 0, row, c);
     }
 }
 
 // ---------------------------------------------------------------------------------------------
 // attention_decode: workgroup (kv, b) attends the `group` query heads KV head kv serves of row b
-// over its slot's positions 0..pos; wave w takes blocks w, w + 8, ... with an online softmax.
+// over its slot's positions 0..pos; wave w takes blocks w, w + 8, ... with an online softmax, the
+// next block's keys and values loaded while the current one is taken.
 // Per block, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in bf16 straight
 // from the registers S^T left it in.
 __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
+    extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
     __shared__ float sm_m[ATTN_WAVES][16];
     __shared__ float sm_l[ATTN_WAVES][16];
-    __shared__ float sm_o[ATTN_WAVES][16][HEAD_DIM + 1];
     const int kv = blockIdx.x, b = blockIdx.y;
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int H = a.heads, KV = a.kv_heads, group = H / KV;
@@ -325,15 +360,22 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     }
     float m = -INFINITY, total = 0.f;
     f32x4 o[4] = {};
-    for (int bi = w; bi < blocks; bi += ATTN_WAVES) {
+    uint4 kf[8], vf[8], kn[8], vn[8];
+    // Loads block bi's tiles into (k, v); false when the slot holds no block there.
+    auto fetch = [&](int bi, uint4 (&k)[8], uint4 (&v)[8]) -> bool {
+        if (bi >= blocks) return false;
         const long blk = block_of(a, slot, (uint32_t)bi * BLOCK_TOKENS);
-        if (blk < 0) break;
+        if (blk < 0) return false;
         const uint16_t* kt = l.kv + ((size_t)blk * KV + kv) * 2 * KV_TILE;
-        uint4 kf[8], vf[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) kf[i] = load16(kt + (i * 64 + lane) * 8);
+        for (int i = 0; i < 8; ++i) k[i] = load16(kt + (i * 64 + lane) * 8);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vf[i] = load16(kt + KV_TILE + (i * 64 + lane) * 8);
+        for (int i = 0; i < 8; ++i) v[i] = load16(kt + KV_TILE + (i * 64 + lane) * 8);
+        return true;
+    };
+    bool have = fetch(w, kf, vf);
+    for (int bi = w; have; bi += ATTN_WAVES) {
+        const bool have_next = fetch(bi + ATTN_WAVES, kn, vn);
         const uint32_t p0 = (uint32_t)bi * BLOCK_TOKENS;
         f32x4 s[4];
 #pragma unroll
@@ -385,15 +427,23 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
         }
         total = total * rescale + sum;
         m = m_new;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            kf[i] = kn[i];
+            vf[i] = vn[i];
+        }
+        have = have_next;
     }
     if (lane < 16) {
         sm_m[w][h] = m;
         sm_l[w][h] = total;
     }
+    if (h < group) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm_o[w][h][dt * 16 + (lane / 16) * 4 + i] = o[dt][i];
+            for (int i = 0; i < 4; ++i) attn_lds[(w * group + h) * (HEAD_DIM + 1) + dt * 16 + (lane / 16) * 4 + i] = o[dt][i];
+    }
     __syncthreads();
     // The waves joined in order (wave 0 holds block 0, so M is finite).
     const size_t head0 = (size_t)b * H + kv * group;
@@ -405,7 +455,7 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
         for (int j = 0; j < ATTN_WAVES; ++j) {
             const float f = sm_l[j][hh] > 0.f ? __expf(sm_m[j][hh] - M) : 0.f;
             L += sm_l[j][hh] * f;
-            O += sm_o[j][hh][d] * f;
+            O += attn_lds[(j * group + hh) * (HEAD_DIM + 1) + d] * f;
         }
         l.attended[(head0 + hh) * HEAD_DIM + d] = (uint16_t)bf16_bits(O / L);
     }
@@ -446,14 +496,6 @@ __global__ void __launch_bounds__(WAVE) final_rmsnorm(DecodeArgs a, const float*
 
 namespace {
 
-// LDS of a projection: one chunk of the batch's vectors, or the waves' chains, the larger.
-template <int NT>
-size_t stage_bytes(int strips) {
-    const size_t xs = (size_t)NT * 16 * CHUNK_KB * 32 * 2;
-    const size_t red = (size_t)GEMV_WAVES * strips * NT * 64 * sizeof(f32x4);
-    return xs > red ? xs : red;
-}
-
 // Launches `kernel`, timed by the next pair of the timer's events when there is a timer.
 template <typename... KernelArgs, typename... Args>
 void dispatch(const char* label, void (*kernel)(KernelArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
@@ -467,84 +509,65 @@ void dispatch(const char* label, void (*kernel)(KernelArgs...), dim3 grid, dim3 
     }
 }
 
-template <int NT>
-hipError_t launch_layer_nt(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
-                           const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer) {
-    const int qkv_strips = (a.heads + 2 * a.kv_heads) * HEAD_DIM / 16;
-    const bool wide = a.hidden > CHUNK_KB * 32;
+size_t attention_lds(const DecodeArgs& a) { return (size_t)ATTN_WAVES * (a.heads / a.kv_heads) * (HEAD_DIM + 1) * 4; }
+
+template <int R>
+hipError_t launch_layer_r(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
+                          const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer) {
+    const int tiles = decode_tiles(a.rows);
+    const int qkv_strips = (a.heads + 2 * a.kv_heads) * HEAD_DIM / R;
+    const bool wide = a.hidden > CHUNK_COLS;
+    const dim3 block(GEMV_THREADS);
     if (wide)
-        dispatch("gemv_qkv_rope", gemv_qkv_rope<NT, MAX_CHUNKS>, dim3(qkv_strips), dim3(GEMV_THREADS), stage_bytes<NT>(1), stream, timer, a, l);
+        dispatch("gemv_qkv_rope", gemv_qkv_rope<R, MAX_CHUNKS>, dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
     else
-        dispatch("gemv_qkv_rope", gemv_qkv_rope<NT, 1>, dim3(qkv_strips), dim3(GEMV_THREADS), stage_bytes<NT>(1), stream, timer, a, l);
-    dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), 0, stream, timer, a, l);
-    if (o.K > CHUNK_KB * 32)
-        dispatch("o_proj", gemv_residual<NT, MAX_CHUNKS>, dim3(o.N / 16), dim3(GEMV_THREADS), stage_bytes<NT>(1), stream, timer, a, o);
+        dispatch("gemv_qkv_rope", gemv_qkv_rope<R, 1>, dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
+    dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), attention_lds(a), stream, timer, a, l);
+    if (o.K > CHUNK_COLS)
+        dispatch("o_proj", gemv_residual<R, MAX_CHUNKS>, dim3(o.N / R, tiles), block, 0, stream, timer, a, o);
     else
-        dispatch("o_proj", gemv_residual<NT, 1>, dim3(o.N / 16), dim3(GEMV_THREADS), stage_bytes<NT>(1), stream, timer, a, o);
+        dispatch("o_proj", gemv_residual<R, 1>, dim3(o.N / R, tiles), block, 0, stream, timer, a, o);
     if (wide)
-        dispatch("gemv_gate_up", gemv_gate_up<NT, MAX_CHUNKS>, dim3(a.inner / 16), dim3(GEMV_THREADS), stage_bytes<NT>(2), stream, timer, a, l);
+        dispatch("gemv_gate_up", gemv_gate_up<MAX_CHUNKS>, dim3(a.inner / 16, tiles), block, 0, stream, timer, a, l);
     else
-        dispatch("gemv_gate_up", gemv_gate_up<NT, 1>, dim3(a.inner / 16), dim3(GEMV_THREADS), stage_bytes<NT>(2), stream, timer, a, l);
-    if (down.K > CHUNK_KB * 32)
-        dispatch("down_proj", gemv_residual<NT, MAX_CHUNKS>, dim3(down.N / 16), dim3(GEMV_THREADS), stage_bytes<NT>(1), stream, timer, a, down);
+        dispatch("gemv_gate_up", gemv_gate_up<1>, dim3(a.inner / 16, tiles), block, 0, stream, timer, a, l);
+    if (down.K > CHUNK_COLS)
+        dispatch("down_proj", gemv_residual<R, MAX_CHUNKS>, dim3(down.N / R, tiles), block, 0, stream, timer, a, down);
     else
-        dispatch("down_proj", gemv_residual<NT, 1>, dim3(down.N / 16), dim3(GEMV_THREADS), stage_bytes<NT>(1), stream, timer, a, down);
+        dispatch("down_proj", gemv_residual<R, 1>, dim3(down.N / R, tiles), block, 0, stream, timer, a, down);
     return hipGetLastError();
 }
 
-// Lets `kernel` take dynamic LDS up to what the device allows a workgroup beside its static LDS.
-hipError_t allow_lds_for(const void* kernel, size_t device_most) {
-    hipFuncAttributes attr{};
-    hipError_t e = hipFuncGetAttributes(&attr, kernel);
-    if (e != hipSuccess) return e;
-    const int most = (int)(device_most - attr.sharedSizeBytes);
-    return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, most);
-}
-
-template <int NT>
-hipError_t allow_lds(size_t device_most) {
-    const void* kernels[] = {
-        (const void*)gemv_qkv_rope<NT, 1>, (const void*)gemv_qkv_rope<NT, MAX_CHUNKS>,
-        (const void*)gemv_gate_up<NT, 1>,  (const void*)gemv_gate_up<NT, MAX_CHUNKS>,
-        (const void*)gemv_residual<NT, 1>, (const void*)gemv_residual<NT, MAX_CHUNKS>,
-    };
-    for (const void* k : kernels) {
-        hipError_t e = allow_lds_for(k, device_most);
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
-}
 }  // namespace
 
 int decode_tiles(int rows) { return (rows + 15) / 16; }
 
-size_t decode_lds_bytes(int rows) {
-    switch (decode_tiles(rows)) {
-        case 1: return stage_bytes<1>(2);
-        case 2: return stage_bytes<2>(2);
-        case 3: return stage_bytes<3>(2);
-        default: return stage_bytes<4>(2);
-    }
+// Strips of 4 or 8 rows spread a small batch's projections over more CUs, but measured no faster
+// than 16 on MI355X (each launch's time is set by its chain of memory round trips, not by how
+// many CUs stream its weights), so every batch takes 16: one weight layout, the prefill's too.
+int decode_strip_rows(int rows) {
+    (void)rows;
+    return 16;
 }
 
-int decode_max_k() { return MAX_CHUNKS * CHUNK_KB * 32; }
+int decode_max_k() { return MAX_CHUNKS * CHUNK_COLS; }
 
 hipError_t decode_prepare(size_t device_lds) {
-    hipError_t e;
-    if ((e = allow_lds<1>(device_lds)) != hipSuccess) return e;
-    if ((e = allow_lds<2>(device_lds)) != hipSuccess) return e;
-    if ((e = allow_lds<3>(device_lds)) != hipSuccess) return e;
-    return allow_lds<4>(device_lds);
+    hipFuncAttributes attr{};
+    hipError_t e = hipFuncGetAttributes(&attr, (const void*)attention_decode);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void*)attention_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)(device_lds - attr.sharedSizeBytes));
 }
+
+size_t decode_attention_lds(int heads, int kv_heads) { return (size_t)ATTN_WAVES * (heads / kv_heads) * (HEAD_DIM + 1) * 4; }
 
 hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
                                const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer) {
-    switch (decode_tiles(a.rows)) {
-        case 1: return launch_layer_nt<1>(a, l, o, down, stream, timer);
-        case 2: return launch_layer_nt<2>(a, l, o, down, stream, timer);
-        case 3: return launch_layer_nt<3>(a, l, o, down, stream, timer);
-        case 4: return launch_layer_nt<4>(a, l, o, down, stream, timer);
-        default: return hipErrorInvalidValue;
+    switch (decode_strip_rows(a.rows)) {
+        case 4: return launch_layer_r<4>(a, l, o, down, stream, timer);
+        case 8: return launch_layer_r<8>(a, l, o, down, stream, timer);
+        default: return launch_layer_r<16>(a, l, o, down, stream, timer);
     }
 }
 

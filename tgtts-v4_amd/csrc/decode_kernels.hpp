@@ -58,12 +58,14 @@ struct DispatchTimer {
     int used = 0, capacity = 0;
 };
 
-// Column tiles of 16 a batch of `rows` takes, the LDS a projection takes at that batch, and the
-// longest K the projections take.
+// Tiles of 16 rows a batch of `rows` takes, the height of the projections' weight strips at
+// that batch (4, 8 or 16: the layout their weights are kept in), the longest K the projections
+// take, and the LDS the attention takes.
 int decode_tiles(int rows);
-size_t decode_lds_bytes(int rows);
+int decode_strip_rows(int rows);
 int decode_max_k();
-// Lets the projections take up to `device_lds` bytes of LDS per workgroup.
+size_t decode_attention_lds(int heads, int kv_heads);
+// Lets the attention take up to `device_lds` bytes of LDS per workgroup.
 hipError_t decode_prepare(size_t device_lds);
 hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
                                const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer = nullptr);

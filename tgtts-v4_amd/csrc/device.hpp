@@ -50,19 +50,25 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // ---- layouts ----
 //
-// Weights, [N][K] row-major in the checkpoint, are kept in MFMA A-operand tiles: tile (n, kb) of
-// 16 rows and 32 columns is 64 lanes x 8 bf16 (1 KiB), lane l holding row 16 n + l % 16, columns
-// 32 kb + 8 (l / 16) .. + 7. Tiles of one strip of 16 rows follow each other along K, so that a
-// wave reads its rows as whole 1 KiB runs.
-__host__ __device__ constexpr size_t weight_tile_index(int n_strip, int kb, int kblocks) {
-    return ((size_t)n_strip * kblocks + kb) * 512;  // in bf16 elements
+// Weights, [N][K] row-major in the checkpoint, are kept in MFMA A-operand tiles of R rows (R of
+// 4, 8 or 16, the strip height of the decoder's projections): tile (strip, kb) holds rows
+// R strip .. R strip + R - 1, columns 32 kb .. 32 kb + 31, as [g][r][8] — lane 16 g + r (r < R)
+// of a wave loads row r, columns 32 kb + 8 g .. + 7, 16 contiguous bytes; lanes with r >= R load
+// nothing and hold zero rows. Tiles of one strip follow each other along K, so that a wave reads
+// its rows as whole runs of R 64 bytes.
+__host__ __device__ constexpr size_t weight_tile_index(int strip, int kb, int kblocks, int R) {
+    return ((size_t)strip * kblocks + kb) * R * 32;  // in bf16 elements
+}
+__host__ __device__ constexpr int weight_lane_offset(int lane, int R) {
+    return ((lane / 16) * R + lane % 16) * 8;
 }
 
-// The q/k/v projection's rows are permuted so that each strip of 16 holds 8 of a head's RoPE
-// pairs: strip rows 0..7 are the head's rows 8 q .. 8 q + 7 and rows 8..15 those 32 further
-// (head_dim 64, four strips to a head). Row r of strip (head h, quarter q) is original row:
-__host__ __device__ constexpr int qkv_row_of(int strip, int r, int head_dim) {
-    return (strip / (head_dim / 16)) * head_dim + (strip % (head_dim / 16)) * 8 + (r < 8 ? r : head_dim / 2 + r - 8);
+// The q/k/v projection's rows are permuted so that each strip of R holds R/2 of a head's RoPE
+// pairs: strip rows 0..R/2-1 are the head's rows p0 .. p0 + R/2 - 1 and rows R/2..R-1 those
+// head_dim/2 further (head_dim 64: 64 / R strips to a head). Row r of strip s is original row:
+__host__ __device__ constexpr int qkv_row_of(int strip, int r, int head_dim, int R) {
+    return (strip / (head_dim / R)) * head_dim + (strip % (head_dim / R)) * (R / 2) +
+           (r < R / 2 ? r : head_dim / 2 + r - R / 2);
 }
 
 // The paged KV cache: per layer, block and KV head, a key tile and a value tile of 64 positions

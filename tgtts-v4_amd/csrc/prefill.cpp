@@ -1,0 +1,174 @@
+// The prefill's host side (Prefill::run, crates/graph/src/prefill.rs:473-503): runs of positions
+// laid out as rows of one set of tensors, the cache blocks they write handed to their slots, the
+// attention's tiles, and the kernels launched over the decoder's weights and cache.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "runtime.hpp"
+
+namespace tgx {
+
+namespace {
+
+constexpr int ROW_TILE = 128;  // the GEMM's rows per workgroup
+constexpr int ATTN_TILE = 32;  // the attention's positions per workgroup
+
+template <typename T>
+tgx_status prefill_alloc(Decoder* d, T** out, size_t count) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(count, 1) * sizeof(T);
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(TGX_E_HIP, "hipMalloc of " + std::to_string(bytes) + " bytes: " + hipGetErrorString(e));
+    d->pf.allocations.push_back({p, bytes});
+    *out = (T*)p;
+    return TGX_OK;
+}
+
+void prefill_free(Decoder* d) {
+    for (auto& b : d->pf.allocations) hipFree(b.ptr);
+    d->pf.allocations.clear();
+    d->pf.rows_held = 0;
+}
+
+// Tensors for `rows` rows (a multiple of ROW_TILE), kept until a longer prefill needs more.
+tgx_status hold_rows(Decoder* d, int rows, int tiles) {
+    if (rows <= d->pf.rows_held && tiles <= d->pf.tiles_held) return TGX_OK;
+    TGX_HIP(hipStreamSynchronize(d->ctx->stream));
+    prefill_free(d);
+    const Shape& s = d->shape;
+    const size_t h = s.hidden, att = (size_t)s.heads * HEAD_DIM;
+    PrefillState& p = d->pf;
+    TGX_TRY(prefill_alloc(d, &p.x, rows * h));
+    TGX_TRY(prefill_alloc(d, &p.h, rows * h));
+    TGX_TRY(prefill_alloc(d, &p.mid, rows * h));
+    TGX_TRY(prefill_alloc(d, &p.out, rows * h));
+    TGX_TRY(prefill_alloc(d, &p.normed, rows * h));
+    TGX_TRY(prefill_alloc(d, &p.q, rows * att));
+    TGX_TRY(prefill_alloc(d, &p.attended, rows * att));
+    TGX_TRY(prefill_alloc(d, &p.mlp, rows * (size_t)s.inner));
+    TGX_TRY(prefill_alloc(d, &p.tok_pos, (size_t)rows));
+    TGX_TRY(prefill_alloc(d, &p.tok_slot, (size_t)rows));
+    TGX_TRY(prefill_alloc(d, &p.tiles, (size_t)tiles));
+    // Rows past a run's are read by the GEMMs: keep them zero.
+    TGX_HIP(hipMemset(p.x, 0, rows * h * 4));
+    TGX_HIP(hipMemset(p.h, 0, rows * h * 4));
+    TGX_HIP(hipMemset(p.mid, 0, rows * h * 4));
+    TGX_HIP(hipMemset(p.normed, 0, rows * h * 2));
+    TGX_HIP(hipMemset(p.attended, 0, rows * att * 2));
+    TGX_HIP(hipMemset(p.mlp, 0, rows * (size_t)s.inner * 2));
+    p.rows_held = rows;
+    p.tiles_held = tiles;
+    return TGX_OK;
+}
+
+tgx_status launch(Decoder* d) {
+    const Shape& s = d->shape;
+    PrefillState& p = d->pf;
+    PrefillArgs a{};
+    a.M = p.M;
+    a.M_pad = p.M_pad;
+    a.hidden = s.hidden;
+    a.inner = s.inner;
+    a.heads = s.heads;
+    a.kv_heads = s.kv_heads;
+    a.capacity = s.capacity;
+    a.nslots = d->slots;
+    a.max_blocks = d->max_blocks;
+    a.nblocks = d->nblocks;
+    a.eps = s.eps;
+    a.scale = 1.0f / std::sqrt((float)HEAD_DIM);
+    a.rope = s.rope ? 1 : 0;
+    a.tok_pos = p.tok_pos;
+    a.tok_slot = p.tok_slot;
+    a.table = d->table;
+    a.cos = d->cos;
+    a.sin = d->sin;
+    std::vector<PrefillLayer> layers(s.layers);
+    for (int l = 0; l < s.layers; ++l) {
+        const Layer& L = d->layers[l];
+        layers[l] = PrefillLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm,
+                                 d->kv + (size_t)l * d->nblocks * s.kv_heads * 2 * KV_TILE};
+    }
+    PrefillBuffers b{p.x, p.h, p.mid, p.normed, p.q, p.attended, p.mlp, p.out, p.tiles, p.ntiles};
+    if (d->timed) d->timer.used = 0;
+    hipError_t e = launch_prefill(a, layers.data(), s.layers, d->final_norm, b, d->ctx->stream, d->timed ? &d->timer : nullptr);
+    if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the prefill: ") + hipGetErrorString(e));
+    return TGX_OK;
+}
+
+}  // namespace
+
+void prefill_release(Decoder* d) { prefill_free(d); }
+
+tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out) {
+    if (!d || !runs || !x || !out) return fail(TGX_E_ARG, "null decoder, runs, x or out");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (nruns <= 0) return fail(TGX_E_SHAPE, "no runs");
+    const Shape& s = d->shape;
+    std::vector<char> taken(d->slots, 0);
+    size_t M = 0;
+    for (int r = 0; r < nruns; ++r) {
+        const tgx_run& run = runs[r];
+        if (run.len == 0 || run.slot >= (uint32_t)d->slots || taken[run.slot] ||
+            (uint64_t)run.start + run.len > (uint64_t)s.capacity)
+            return fail(TGX_E_SHAPE, "run " + std::to_string(r) + ": " + std::to_string(run.len) + " positions from " +
+                                         std::to_string(run.start) + " in slot " + std::to_string(run.slot) + " of " +
+                                         std::to_string(d->slots) + ", a cache of " + std::to_string(s.capacity));
+        taken[run.slot] = 1;
+        M += run.len;
+    }
+    for (int r = 0; r < nruns; ++r) TGX_TRY(hold_slot(d, runs[r].slot, runs[r].start + runs[r].len));
+    const int M_pad = (int)((M + ROW_TILE - 1) / ROW_TILE * ROW_TILE);
+    // Rows and tiles: run after run; the tiles later in a run, which attend to more, first.
+    std::vector<uint32_t> pos(M_pad, TGX_SPARE), slot(M_pad, TGX_SPARE);
+    std::vector<PrefillTile> tiles;
+    size_t row = 0;
+    for (int r = 0; r < nruns; ++r) {
+        const tgx_run& run = runs[r];
+        for (uint32_t i = 0; i < run.len; ++i) {
+            pos[row + i] = run.start + i;
+            slot[row + i] = run.slot;
+        }
+        for (uint32_t t0 = 0; t0 < run.len; t0 += ATTN_TILE)
+            tiles.push_back(PrefillTile{(uint32_t)(row + t0), run.start + t0, std::min<uint32_t>(ATTN_TILE, run.len - t0), run.slot});
+        row += run.len;
+    }
+    std::stable_sort(tiles.begin(), tiles.end(), [](const PrefillTile& a, const PrefillTile& b) {
+        return a.pos0 + a.count > b.pos0 + b.count;
+    });
+    TGX_TRY(hold_rows(d, M_pad, (int)tiles.size()));
+    PrefillState& p = d->pf;
+    p.M = (int)M;
+    p.M_pad = M_pad;
+    p.ntiles = (int)tiles.size();
+    hipStream_t st = d->ctx->stream;
+    TGX_TRY(sync_slots(d));
+    TGX_HIP(hipMemcpyAsync(p.x, x, M * s.hidden * 4, hipMemcpyHostToDevice, st));
+    if ((size_t)M_pad > M) TGX_HIP(hipMemsetAsync(p.x + M * s.hidden, 0, (M_pad - M) * s.hidden * 4, st));
+    TGX_HIP(hipMemcpyAsync(p.tok_pos, pos.data(), M_pad * 4, hipMemcpyHostToDevice, st));
+    TGX_HIP(hipMemcpyAsync(p.tok_slot, slot.data(), M_pad * 4, hipMemcpyHostToDevice, st));
+    TGX_HIP(hipMemcpyAsync(p.tiles, tiles.data(), tiles.size() * sizeof(PrefillTile), hipMemcpyHostToDevice, st));
+    TGX_HIP(hipEventRecord(d->ev_start, st));
+    TGX_TRY(launch(d));
+    TGX_HIP(hipEventRecord(d->ev_end, st));
+    TGX_HIP(hipMemcpyAsync(out, p.out, M * s.hidden * 4, hipMemcpyDeviceToHost, st));
+    TGX_HIP(hipStreamSynchronize(st));
+    return TGX_OK;
+}
+
+tgx_status prefill_launch(Decoder* d, int times) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (d->pf.M == 0) return fail(TGX_E_SHAPE, "no prefill has run to launch again");
+    if (times <= 0) return fail(TGX_E_ARG, "times");
+    hipStream_t st = d->ctx->stream;
+    TGX_HIP(hipEventRecord(d->ev_start, st));
+    for (int i = 0; i < times; ++i) TGX_TRY(launch(d));
+    TGX_HIP(hipEventRecord(d->ev_end, st));
+    TGX_HIP(hipEventRecord(d->ev_done, st));
+    d->pending = true;
+    return TGX_OK;
+}
+
+}  // namespace tgx

@@ -1,0 +1,62 @@
+// Arguments and launchers of the prefill's kernels (prefill_kernels.hip): the causal run of many
+// positions at once (crates/graph/src/prefill.rs:218-413).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "decode_kernels.hpp"
+
+namespace tgx {
+
+// A tile of up to 32 positions of one run for the attention: rows row0 .. row0 + count - 1 of
+// the prefill's tensors are positions pos0 .. pos0 + count - 1 of `slot`.
+struct PrefillTile {
+    uint32_t row0, pos0, count, slot;
+};
+
+// What every prefill kernel reads.
+struct PrefillArgs {
+    int M;        // rows (positions over every run)
+    int M_pad;    // rows the tensors hold, a multiple of 128
+    int hidden, inner, heads, kv_heads;
+    int capacity, nslots, max_blocks, nblocks;
+    float eps, scale;
+    int rope;
+    const uint32_t* tok_pos;   // [M_pad], TGX_SPARE past M
+    const uint32_t* tok_slot;  // [M_pad]
+    const uint32_t* table;     // [nslots][max_blocks]
+    const float* cos;
+    const float* sin;
+};
+
+// One layer's tensors of a prefill.
+struct PrefillLayer {
+    const uint16_t* qkv;      // 16-row tiles, rows permuted (qkv_row_of)
+    const uint16_t* o;
+    const uint16_t* gate_up;
+    const uint16_t* down;
+    const float* input_norm;
+    const float* post_norm;
+    uint16_t* kv;  // the layer's cache pool
+};
+
+// The prefill's tensors, [M_pad] rows each.
+struct PrefillBuffers {
+    const float* x;     // the run's hidden states, f32 [M_pad][hidden], as written
+    float* h;           // residual stream, f32 [M_pad][hidden]
+    float* mid;         // after the attention, f32
+    uint16_t* normed;   // RMSNorm of the stream, bf16 [M_pad][hidden]
+    uint16_t* q;        // bf16 [M_pad][heads][64]
+    uint16_t* attended; // bf16 [M_pad][heads 64]
+    uint16_t* mlp;      // bf16 [M_pad][inner]
+    float* out;         // after the final norm, f32 [M_pad][hidden]
+    const PrefillTile* tiles;
+    int ntiles;
+};
+
+// Launches the whole prefill of the M rows of b.x (f32) through every layer into b.out.
+hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int nlayers, const float* final_norm,
+                          const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer = nullptr);
+hipError_t prefill_prepare(size_t device_lds);
+
+}  // namespace tgx

@@ -106,6 +106,7 @@ tgx_status context_create(int device, Context** out) {
     }
     ctx->lds_bytes = ctx->prop.sharedMemPerBlock;
     e = decode_prepare(ctx->lds_bytes);
+    if (e == hipSuccess) e = prefill_prepare(ctx->lds_bytes);
     if (e != hipSuccess) {
         hipStreamDestroy(ctx->stream);
         delete ctx;
@@ -169,9 +170,8 @@ tgx_status check_batch(const Shape& s, const tgx_batch* batch) {
     if (block_tokens != BLOCK_TOKENS)
         return fail(TGX_E_SHAPE, "blocks of " + std::to_string(block_tokens) + " positions: the kernels take 64");
     if (batch->blocks < 0) return fail(TGX_E_SHAPE, "a pool of " + std::to_string(batch->blocks) + " blocks");
-    const size_t lds = decode_lds_bytes(batch->rows);
-    if (lds > 160 * 1024)
-        return fail(TGX_E_SHAPE, std::to_string(batch->rows) + " rows stage " + std::to_string(lds) + " bytes, past 160 KiB of LDS");
+    if (decode_attention_lds(s.heads, s.kv_heads) > 160 * 1024)
+        return fail(TGX_E_SHAPE, "the attention of " + std::to_string(s.heads / s.kv_heads) + " heads to a KV head takes past 160 KiB of LDS");
     return TGX_OK;
 }
 
@@ -324,10 +324,10 @@ tgx_status record(Decoder* d, int advance, hipGraphExec_t* exec) {
 tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     const Shape& s = d->shape;
     TGX_TRY(check_batch(s, batch));
-    if (decode_lds_bytes(batch->rows) + 1024 > d->ctx->lds_bytes)
-        return fail(TGX_E_SHAPE, std::to_string(batch->rows) + " rows stage " + std::to_string(decode_lds_bytes(batch->rows)) +
-                                     " bytes, past the device's " + std::to_string(d->ctx->lds_bytes) + " of LDS");
+    if (decode_attention_lds(s.heads, s.kv_heads) + 4096 > d->ctx->lds_bytes)
+        return fail(TGX_E_SHAPE, "the attention's LDS is past the device's " + std::to_string(d->ctx->lds_bytes));
     d->rows = batch->rows;
+    d->strip_rows = decode_strip_rows(batch->rows);
     d->slots = batch->slots;
     d->block_tokens = batch->block_tokens == 0 ? BLOCK_TOKENS : batch->block_tokens;
     d->max_blocks = (s.capacity + BLOCK_TOKENS - 1) / BLOCK_TOKENS;
@@ -387,7 +387,7 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     d->free_list.clear();
     for (int b = d->nblocks - 1; b >= 0; --b) d->free_list.push_back((uint32_t)b);
 
-    const int dispatches = 5 * s.layers + 1;
+    const int dispatches = 7 * s.layers + 2;  // the prefill's, the most a run dispatches
     d->timer_start.assign(dispatches, nullptr);
     d->timer_stop.assign(dispatches, nullptr);
     d->timer_labels.assign(dispatches, nullptr);
@@ -408,8 +408,9 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     return TGX_OK;
 }
 
-// Gives `slot` blocks for positions 0..positions-1.
-tgx_status hold(Decoder* d, uint32_t slot, uint32_t positions) {
+}  // namespace
+
+tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions) {
     const int need = (int)((positions + BLOCK_TOKENS - 1) / BLOCK_TOKENS);
     while (d->slot_blocks[slot] < need) {
         if (d->free_list.empty())
@@ -423,14 +424,12 @@ tgx_status hold(Decoder* d, uint32_t slot, uint32_t positions) {
     return TGX_OK;
 }
 
-tgx_status sync_table(Decoder* d) {
+tgx_status sync_slots(Decoder* d) {
     if (!d->table_dirty) return TGX_OK;
     TGX_HIP(hipMemcpyAsync(d->table, d->table_host, (size_t)d->slots * d->max_blocks * 4, hipMemcpyHostToDevice, d->ctx->stream));
     d->table_dirty = false;
     return TGX_OK;
 }
-
-}  // namespace
 
 tgx_status decoder_create(Context* ctx, const tgx_shape* shape, const tgx_batch* batch, Decoder** out) {
     if (!ctx || !out) return fail(TGX_E_ARG, "null context or output");
@@ -454,6 +453,7 @@ void decoder_destroy(Decoder* d) {
     if (!d) return;
     hipSetDevice(d->ctx->device);
     hipStreamSynchronize(d->ctx->stream);
+    prefill_release(d);
     if (d->step_exec) hipGraphExecDestroy(d->step_exec);
     if (d->advance_exec) hipGraphExecDestroy(d->advance_exec);
     if (d->ev_start) hipEventDestroy(d->ev_start);
@@ -485,18 +485,20 @@ std::vector<float> as_f32(const void* data, tgx_dtype dtype, size_t count) {
     return v;
 }
 
-// W [n][k] into MFMA tiles, rows taken through `row_of` (strip, r) -> source row.
+// W [n][k] into MFMA tiles of R-row strips, rows taken through `row_of` (strip, r) -> source row.
 template <typename RowOf>
-std::vector<uint16_t> tile(const std::vector<float>& w, int n, int k, RowOf row_of) {
+std::vector<uint16_t> tile(const std::vector<float>& w, int n, int k, int R, RowOf row_of) {
     std::vector<uint16_t> t((size_t)n * k);
     const int kblocks = k / 32;
-    for (int strip = 0; strip < n / 16; ++strip)
+    for (int strip = 0; strip < n / R; ++strip)
         for (int kb = 0; kb < kblocks; ++kb) {
-            uint16_t* dst = t.data() + weight_tile_index(strip, kb, kblocks);
+            uint16_t* dst = t.data() + weight_tile_index(strip, kb, kblocks, R);
             for (int lane = 0; lane < 64; ++lane) {
+                if (lane % 16 >= R) continue;
                 const int src_row = row_of(strip, lane % 16);
                 const float* src = w.data() + (size_t)src_row * k + kb * 32 + (lane / 16) * 8;
-                for (int j = 0; j < 8; ++j) dst[lane * 8 + j] = f32_to_bf16(src[j]);
+                uint16_t* out = dst + weight_lane_offset(lane, R);
+                for (int j = 0; j < 8; ++j) out[j] = f32_to_bf16(src[j]);
             }
         }
     return t;
@@ -540,25 +542,28 @@ tgx_status decoder_load(Decoder* d, const char* name, const void* data, tgx_dtyp
     if (w == "qkv_proj") {
         TGX_TRY(want((size_t)qkv_rows * h));
         auto v = as_f32(data, dtype, count);
-        auto t = tile(v, qkv_rows, h, [](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM); });
+        const int R = d->strip_rows;
+        auto t = tile(v, qkv_rows, h, R, [R](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM, R); });
         return upload(L.qkv, t.data(), t.size() * 2);
     }
     if (w == "o_proj") {
         TGX_TRY(want((size_t)h * H * HEAD_DIM));
         auto v = as_f32(data, dtype, count);
-        auto t = tile(v, h, H * HEAD_DIM, [](int strip, int r) { return strip * 16 + r; });
+        const int R = d->strip_rows;
+        auto t = tile(v, h, H * HEAD_DIM, R, [R](int strip, int r) { return strip * R + r; });
         return upload(L.o, t.data(), t.size() * 2);
     }
     if (w == "gate_up_proj") {
         TGX_TRY(want((size_t)2 * I * h));
         auto v = as_f32(data, dtype, count);
-        auto t = tile(v, 2 * I, h, [](int strip, int r) { return strip * 16 + r; });
+        auto t = tile(v, 2 * I, h, 16, [](int strip, int r) { return strip * 16 + r; });
         return upload(L.gate_up, t.data(), t.size() * 2);
     }
     if (w == "down_proj") {
         TGX_TRY(want((size_t)h * I));
         auto v = as_f32(data, dtype, count);
-        auto t = tile(v, h, I, [](int strip, int r) { return strip * 16 + r; });
+        const int R = d->strip_rows;
+        auto t = tile(v, h, I, R, [R](int strip, int r) { return strip * R + r; });
         return upload(L.down, t.data(), t.size() * 2);
     }
     return fail(TGX_E_WEIGHTS, n + ": no such tensor");
@@ -574,12 +579,12 @@ tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const fl
     for (int b = 0; b < nrows; ++b) {
         const tgx_row r = rows[b];
         if (r.position == TGX_SPARE) continue;
-        TGX_TRY(hold(d, r.slot, r.position + 1));
+        TGX_TRY(hold_slot(d, r.slot, r.position + 1));
     }
     std::memcpy(d->placement_host, words.data(), words.size() * 4);
     std::memcpy(d->x_host, x, (size_t)nrows * d->shape.hidden * 4);
     hipStream_t s = d->ctx->stream;
-    TGX_TRY(sync_table(d));
+    TGX_TRY(sync_slots(d));
     TGX_HIP(hipMemcpyAsync(d->x_in, d->x_host, (size_t)nrows * d->shape.hidden * 4, hipMemcpyHostToDevice, s));
     TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
     TGX_HIP(hipMemcpyAsync(d->slot_of_row, d->placement_host + nrows, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
@@ -592,13 +597,13 @@ tgx_status decoder_start(Decoder* d) {
     if (!d) return fail(TGX_E_ARG, "null decoder");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     hipStream_t s = d->ctx->stream;
-    TGX_TRY(sync_table(d));
+    TGX_TRY(sync_slots(d));
     TGX_HIP(hipEventRecord(d->ev_start, s));
-    if (d->timed) {
-        // Launched dispatch by dispatch, each timed by its own events (Decoder::timings).
+    if (d->timed || !d->use_graph) {
+        // Launched dispatch by dispatch, each timed by its own events when timed (Decoder::timings).
         d->timer.used = 0;
-        hipError_t e = enqueue_step(d, 0, &d->timer, nullptr);
-        if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the timed step: ") + hipGetErrorString(e));
+        hipError_t e = enqueue_step(d, 0, d->timed ? &d->timer : nullptr, nullptr);
+        if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the step: ") + hipGetErrorString(e));
     } else {
         TGX_HIP(hipGraphLaunch(d->step_exec, s));
     }
@@ -656,8 +661,8 @@ tgx_status decoder_reserve(Decoder* d, uint32_t slot, uint32_t positions) {
     if (slot >= (uint32_t)d->slots) return fail(TGX_E_SHAPE, "slot " + std::to_string(slot) + " of " + std::to_string(d->slots));
     if (positions > (uint32_t)d->shape.capacity)
         return fail(TGX_E_SHAPE, std::to_string(positions) + " positions past a capacity of " + std::to_string(d->shape.capacity));
-    TGX_TRY(hold(d, slot, positions));
-    return sync_table(d);
+    TGX_TRY(hold_slot(d, slot, positions));
+    return sync_slots(d);
 }
 
 tgx_status decoder_launch(Decoder* d, int times, int advance) {
@@ -665,13 +670,13 @@ tgx_status decoder_launch(Decoder* d, int times, int advance) {
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (times <= 0) return fail(TGX_E_ARG, "times");
     hipStream_t s = d->ctx->stream;
-    TGX_TRY(sync_table(d));
+    TGX_TRY(sync_slots(d));
     TGX_HIP(hipEventRecord(d->ev_start, s));
     for (int i = 0; i < times; ++i) {
-        if (d->timed) {
+        if (d->timed || !d->use_graph) {
             d->timer.used = 0;
-            hipError_t e = enqueue_step(d, advance, &d->timer, nullptr);
-            if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the timed step: ") + hipGetErrorString(e));
+            hipError_t e = enqueue_step(d, advance, d->timed ? &d->timer : nullptr, nullptr);
+            if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the step: ") + hipGetErrorString(e));
         } else {
             TGX_HIP(hipGraphLaunch(advance ? d->advance_exec : d->step_exec, s));
         }

@@ -8,6 +8,7 @@
 
 #include "../../include/tgx.h"
 #include "decode_kernels.hpp"
+#include "prefill_kernels.hpp"
 
 namespace tgx {
 
@@ -52,10 +53,22 @@ struct Layer {
     float *input_norm = nullptr, *post_norm = nullptr;
 };
 
+// The prefill's tensors, kept between runs and grown to the longest seen.
+struct PrefillState {
+    std::vector<DeviceBuffer> allocations;
+    int rows_held = 0, tiles_held = 0;
+    int M = 0, M_pad = 0, ntiles = 0;  // the last prefill
+    float *x = nullptr, *h = nullptr, *mid = nullptr, *out = nullptr;
+    uint16_t *normed = nullptr, *q = nullptr, *attended = nullptr, *mlp = nullptr;
+    uint32_t *tok_pos = nullptr, *tok_slot = nullptr;
+    PrefillTile* tiles = nullptr;
+};
+
 struct Decoder {
     Context* ctx = nullptr;
     Shape shape{};
     int rows = 0, slots = 0, block_tokens = 64, nblocks = 0, max_blocks = 0;
+    int strip_rows = 16;  // weight strip height of qkv, o and down at this batch
     std::vector<DeviceBuffer> allocations;
     size_t device_bytes = 0;
     std::vector<Layer> layers;
@@ -78,9 +91,11 @@ struct Decoder {
     hipEvent_t ev_start = nullptr, ev_end = nullptr, ev_done = nullptr;
     bool pending = false;
     bool timed = false;  // launch dispatch by dispatch, each timed (Decoder::new's `timed`)
+    bool use_graph = true;  // launch the recorded graph (else dispatch by dispatch)
     DispatchTimer timer;
     std::vector<hipEvent_t> timer_start, timer_stop;
     std::vector<const char*> timer_labels;
+    PrefillState pf;
 
     DecodeArgs args() const;
     LayerArgs layer_args(int l, const float* x, float* mid) const;
@@ -104,6 +119,13 @@ tgx_status decoder_output(Decoder* dec, float* out);
 tgx_status decoder_release_slot(Decoder* dec, uint32_t slot);
 tgx_status decoder_reserve(Decoder* dec, uint32_t slot, uint32_t positions);
 tgx_status decoder_launch(Decoder* dec, int times, int advance);
+// Hands `slot` the blocks for positions 0..positions-1, and copies the block table to the device
+// when it changed.
+tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions);
+tgx_status sync_slots(Decoder* d);
+tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out);
+tgx_status prefill_launch(Decoder* d, int times);
+void prefill_release(Decoder* d);
 tgx_status decoder_timings(Decoder* d, int max, tgx_timing* out, int* n);
 tgx_status decoder_read_cache(Decoder* dec, uint32_t slot, uint32_t positions, float* k, float* v);
 

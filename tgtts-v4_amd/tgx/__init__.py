@@ -79,6 +79,10 @@ class _Row(ctypes.Structure):
     _fields_ = [("position", ctypes.c_uint32), ("slot", ctypes.c_uint32)]
 
 
+class _Run(ctypes.Structure):
+    _fields_ = [("slot", ctypes.c_uint32), ("start", ctypes.c_uint32), ("len", ctypes.c_uint32)]
+
+
 class _Timing(ctypes.Structure):
     _fields_ = [("label", ctypes.c_char * 32), ("ms", ctypes.c_float)]
 
@@ -118,10 +122,12 @@ EXPORTS = [
     "tgx_decoder_device_bytes",
     "tgx_decoder_read_cache",
     "tgx_decoder_set_timed",
+    "tgx_decoder_set_graph",
     "tgx_decoder_timings",
     "tgx_shape_check",
     "tgx_batch_placement",
     "tgx_prefill_run",
+    "tgx_prefill_runs",
     "tgx_prefill_launch",
 ]
 
@@ -174,11 +180,13 @@ def library() -> ctypes.CDLL:
     lib.tgx_decoder_device_bytes.argtypes = [P, ctypes.POINTER(ctypes.c_size_t)]
     lib.tgx_decoder_read_cache.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, P, P]
     lib.tgx_decoder_set_timed.argtypes = [P, ctypes.c_int]
+    lib.tgx_decoder_set_graph.argtypes = [P, ctypes.c_int]
     lib.tgx_decoder_timings.argtypes = [P, ctypes.c_int, ctypes.POINTER(_Timing), ctypes.POINTER(ctypes.c_int)]
     lib.tgx_shape_check.argtypes = [ctypes.POINTER(_Shape), ctypes.POINTER(_Batch)]
     lib.tgx_batch_placement.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(_Row), ctypes.c_int, ctypes.POINTER(ctypes.c_uint32)]
     lib.tgx_prefill_run.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, P, P]
-    lib.tgx_prefill_launch.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
+    lib.tgx_prefill_runs.argtypes = [P, ctypes.POINTER(_Run), ctypes.c_int, P, P]
+    lib.tgx_prefill_launch.argtypes = [P, ctypes.c_int]
     for name in EXPORTS:
         if name.startswith("tgx_") and name not in ("tgx_last_error",):
             fn = getattr(lib, name)
@@ -407,6 +415,10 @@ class Decoder:
         """Decoder::new's `timed`: launch dispatch by dispatch, each timed."""
         _check(library().tgx_decoder_set_timed(self._h, 1 if timed else 0))
 
+    def set_graph(self, use_graph: bool) -> None:
+        """Launch steps as the recorded HIP graph (default) or dispatch by dispatch."""
+        _check(library().tgx_decoder_set_graph(self._h, 1 if use_graph else 0))
+
     def timings(self) -> list:
         """Decoder::timings (decode.rs:891-893): [(label, ms)] of the last timed step."""
         n = ctypes.c_int()
@@ -441,8 +453,19 @@ class Decoder:
         _check(library().tgx_prefill_run(self._h, slot, start, n, _ptr(x), _ptr(out)))
         return out
 
-    def prefill_launch(self, count: int, length: int, times: int = 1) -> None:
-        _check(library().tgx_prefill_launch(self._h, count, length, times))
+    def prefill_runs(self, runs: Sequence[tuple], x: np.ndarray) -> np.ndarray:
+        """Several runs (slot, start, len) at once, x their hidden states one run after another."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        arr = (_Run * len(runs))()
+        for i, (slot, start, n) in enumerate(runs):
+            arr[i].slot, arr[i].start, arr[i].len = slot, start, n
+        out = np.empty_like(x)
+        _check(library().tgx_prefill_runs(self._h, arr, len(runs), _ptr(x), _ptr(out)))
+        return out
+
+    def prefill_launch(self, times: int = 1) -> None:
+        """The last prefill again, `times` times, over its input on the device."""
+        _check(library().tgx_prefill_launch(self._h, times))
 
     def close(self) -> None:
         if self._h:
