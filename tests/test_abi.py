@@ -1,0 +1,107 @@
+"""The C ABI on the CPU: the library loads and exports every entry point include/tgx.h declares,
+and the host-side decisions the reference unit-tests without a GPU — shape refusals
+(crates/graph/src/decode.rs:1011-1028), Batch::placement's words and refusals
+(decode.rs:1073-1092), Shape::weight_bytes (decode.rs:947) — hold here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def header_functions():
+    text = (ROOT / "include" / "tgx.h").read_text()
+    return sorted(set(re.findall(r"^(?:tgx_status|void|const char\*)\s+(tgx_\w+)\(", text, re.M)))
+
+
+def test_the_library_exports_every_function_the_header_declares():
+    import tgx
+
+    lib = tgx.library()
+    names = header_functions()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(tgx.EXPORTS) <= set(names)
+
+
+def test_without_a_device_a_context_is_refused_not_faked():
+    import tgx
+
+    try:
+        import torch
+
+        has_gpu = torch.cuda.is_available()
+    except Exception:
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a GPU is present")
+    with pytest.raises(tgx.TgxError) as e:
+        tgx.Context(0)
+    assert e.value.kind in ("no_device", "hip")
+
+
+def test_weight_bytes_as_the_reference_counts_them():
+    import tgx
+
+    ref = tgx.Shape(hidden=2048, inner=6144, heads=16, kv_heads=2, head_dim=128, layers=28)
+    assert ref.weight_bytes() == 2_642_644_992  # decode.rs:947
+    assert tgx.Shape().weight_bytes() == 717_326_336  # the 24-layer backbone at hidden 1024
+    assert tgx.Shape().kv_bytes_per_position() == 12_288
+
+
+def test_spare_rows_are_placed_past_every_position_and_a_slot_is_taken_once():
+    """decode.rs:1073-1092, word for word."""
+    import tgx
+
+    at = tgx.Row
+    assert tgx.placement(4, 64, [at(5, 2), None, at(0, 0)]) == [5, tgx.SPARE, 0, 2, tgx.SPARE, 0]
+    for rows in ([at(5, 2), at(9, 2), None], [at(64, 0), None, None], [at(1, 4), None, None]):
+        with pytest.raises(tgx.TgxError) as e:
+            tgx.placement(4, 64, rows)
+        assert e.value.kind == "shape"
+
+
+@pytest.mark.parametrize(
+    "change, batch",
+    [
+        (dict(head_dim=128), dict()),
+        (dict(heads=16, kv_heads=3), dict()),
+        (dict(heads=32, kv_heads=1), dict()),
+        (dict(capacity=0), dict()),
+        (dict(hidden=1000), dict()),
+        (dict(inner=5000), dict()),
+        (dict(inner=8192), dict()),
+        (dict(), dict(rows=3, slots=2)),
+        (dict(), dict(rows=65, slots=65)),
+        (dict(), dict(block_tokens=32)),
+        (dict(), dict(rows=0, slots=1)),
+    ],
+)
+def test_shapes_the_kernels_cannot_cover_are_refused(change, batch):
+    import tgx
+
+    shape = tgx.Shape(**change)
+    b = tgx.Batch(**{**dict(rows=1, slots=1), **batch})
+    with pytest.raises(tgx.TgxError) as e:
+        tgx.check_shape(shape, b)
+    assert e.value.kind == "shape"
+
+
+def test_the_backbone_shapes_are_taken():
+    import tgx
+
+    for rows in (1, 16, 17, 32, 64):
+        tgx.check_shape(tgx.Shape(capacity=2048), tgx.Batch(rows=rows, slots=rows))
+    tgx.check_shape(tgx.Shape(rope=False, layers=8), tgx.Batch(rows=4, slots=8))
+
+
+def test_null_arguments_are_refused_with_a_message():
+    import tgx
+
+    lib = tgx.library()
+    assert lib.tgx_decoder_step(None, 0, None, None) == 8
+    assert b"null" in lib.tgx_last_error()
