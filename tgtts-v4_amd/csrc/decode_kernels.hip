@@ -406,14 +406,13 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
                 const int pt = 2 * ks + half;
-                float e[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    e[i] = __uint_as_float(bf16_bits(__expf(s[pt][i] - m_new)) << 16);
-                    sum += e[i];
-                }
-                words[half * 2] = pack_bf16x2(e[0], e[1]);
-                words[half * 2 + 1] = pack_bf16x2(e[2], e[3]);
+                // P rounded to bf16 for the product, the sum taken over the rounded values.
+                words[half * 2] = pack_bf16x2(__expf(s[pt][0] - m_new), __expf(s[pt][1] - m_new));
+                words[half * 2 + 1] = pack_bf16x2(__expf(s[pt][2] - m_new), __expf(s[pt][3] - m_new));
+                sum += bf16_lo(words[half * 2]);
+                sum += bf16_hi(words[half * 2]);
+                sum += bf16_lo(words[half * 2 + 1]);
+                sum += bf16_hi(words[half * 2 + 1]);
             }
             pf[ks] = make_uint4(words[0], words[1], words[2], words[3]);
         }

@@ -11,8 +11,8 @@ namespace tgx {
 
 namespace {
 
-constexpr int ROW_TILE = 128;  // the GEMM's rows per workgroup
-constexpr int ATTN_TILE = 32;  // the attention's positions per workgroup
+constexpr int ROW_TILE = 256;  // the GEMM's rows per workgroup
+constexpr int ATTN_ROWS = 32;  // the attention's positions per workgroup
 
 template <typename T>
 tgx_status prefill_alloc(Decoder* d, T** out, size_t count) {
@@ -130,8 +130,8 @@ tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float*
             pos[row + i] = run.start + i;
             slot[row + i] = run.slot;
         }
-        for (uint32_t t0 = 0; t0 < run.len; t0 += ATTN_TILE)
-            tiles.push_back(PrefillTile{(uint32_t)(row + t0), run.start + t0, std::min<uint32_t>(ATTN_TILE, run.len - t0), run.slot});
+        for (uint32_t t0 = 0; t0 < run.len; t0 += ATTN_ROWS)
+            tiles.push_back(PrefillTile{(uint32_t)(row + t0), run.start + t0, std::min<uint32_t>(ATTN_ROWS, run.len - t0), run.slot});
         row += run.len;
     }
     std::stable_sort(tiles.begin(), tiles.end(), [](const PrefillTile& a, const PrefillTile& b) {

@@ -22,17 +22,25 @@ namespace {
 
 constexpr int PF_WAVES = 4;
 constexpr int PF_THREADS = PF_WAVES * WAVE;
-// The GEMM's workgroup tile: 256 rows of W (16 strips) by 128 rows of X, K 64 at a time (two
-// k-blocks); wave (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 64 wm .. + 63.
-constexpr int TN = 256, TM = 128, TKB = 2;
+// The GEMM's workgroup tile: 256 rows of W (16 strips) by 256 rows of X, K 64 at a time (two
+// k-blocks); wave (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 128 wm .. + 127
+// (8 tiles of 16): 64 accumulators of 16 x 16.
+constexpr int TN = 256, TM = 256, TKB = 2;
 constexpr int W_STRIPS = TN / 16;   // 16
-constexpr int X_TILES = TM / 16;    // 8
+constexpr int X_TILES = TM / 16;    // 16
+constexpr int WT = 8;               // a wave's X tiles
 constexpr int W_STAGE = W_STRIPS * TKB * 64;  // uint4 per stage: 32 KiB
-constexpr int X_STAGE = X_TILES * TKB * 64;   // 16 KiB
+constexpr int X_STAGE = X_TILES * TKB * 64;   // 32 KiB
 
 enum Epilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2 };
 
+constexpr uint32_t TGX_SPARE_POS = 0xffffffffu;
+static_assert(PF_THREADS == TM, "the q/k/v epilogue stages a row to a thread");
+
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
 
 struct GemmArgs {
     const uint16_t* w;  // 16-row tiles of [N][K]
@@ -76,71 +84,67 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
     const int stages = kblocks / TKB;
     const int m0 = mb * TM;
 
-    uint4 wreg[W_STAGE / PF_THREADS], xreg[X_STAGE / PF_THREADS];
-    auto fetch = [&](int st) {
+    // A stage is 32 weight fragments and 32 vector fragments of 1 KiB, eight of each to a wave,
+    // loaded straight from memory into LDS: lane l of a load writes bytes 16 l .. 16 l + 15 of
+    // the fragment, the MFMA operand order.
+    auto fetch = [&](int st, int buf) {
 #pragma unroll
-        for (int j = 0; j < W_STAGE / PF_THREADS; ++j) {
-            const int i = threadIdx.x + j * PF_THREADS;
-            const int sl = i / (TKB * 64), kbl = (i / 64) % TKB, ln = i % 64;
-            wreg[j] = load16(g.w + weight_tile_index(stage_strip<EPI>(nb, sl, g.N), st * TKB + kbl, kblocks, 16) + ln * 8);
+        for (int j = 0; j < 8; ++j) {
+            const int f = w * 8 + j;
+            const int sl = f / TKB, kbl = f % TKB;
+            const uint16_t* src = g.w + weight_tile_index(stage_strip<EPI>(nb, sl, g.N), st * TKB + kbl, kblocks, 16) + lane * 8;
+            __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&ws[buf * W_STAGE + f * 64], 16, 0, 0);
         }
 #pragma unroll
-        for (int j = 0; j < X_STAGE / PF_THREADS; ++j) {
-            const int i = threadIdx.x + j * PF_THREADS;
-            const int m = i / (TKB * 4), c8 = i % (TKB * 4);
-            xreg[j] = load16(g.x + (size_t)(m0 + m) * g.K + st * TKB * 32 + c8 * 8);
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < W_STAGE / PF_THREADS; ++j) ws[buf * W_STAGE + threadIdx.x + j * PF_THREADS] = wreg[j];
-#pragma unroll
-        for (int j = 0; j < X_STAGE / PF_THREADS; ++j) {
-            const int i = threadIdx.x + j * PF_THREADS;
-            const int m = i / (TKB * 4), c8 = i % (TKB * 4);
-            const int mt = m / 16, kbl = c8 / 4, gq = c8 % 4;
-            xs[buf * X_STAGE + (mt * TKB + kbl) * 64 + gq * 16 + m % 16] = xreg[j];
+        for (int j = 0; j < 8; ++j) {
+            const int f = w * 8 + j;
+            const int mt = f / TKB, kbl = f % TKB;
+            const uint16_t* src = g.x + (size_t)(m0 + mt * 16 + lane % 16) * g.K + (st * TKB + kbl) * 32 + (lane / 16) * 8;
+            __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&xs[buf * X_STAGE + f * 64], 16, 0, 0);
         }
     };
 
-    f32x4 acc[8][4];
+    f32x4 acc[8][WT];
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < WT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    fetch(0);
-    store(0);
+    fetch(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int st = 0; st < stages; ++st) {
         const int buf = st % 2;
-        if (st + 1 < stages) fetch(st + 1);
+        if (st + 1 < stages) fetch(st + 1, 1 - buf);
 #pragma unroll
         for (int kbl = 0; kbl < TKB; ++kbl) {
-            uint4 af[8], bf[4];
+            uint4 bf[WT], af[2];
 #pragma unroll
-            for (int s = 0; s < 8; ++s) af[s] = ws[buf * W_STAGE + ((wn * 8 + s) * TKB + kbl) * 64 + lane];
+            for (int t = 0; t < WT; ++t) bf[t] = xs[buf * X_STAGE + ((wm * WT + t) * TKB + kbl) * 64 + lane];
+            af[0] = ws[buf * W_STAGE + ((wn * 8) * TKB + kbl) * 64 + lane];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) bf[t] = xs[buf * X_STAGE + ((wm * 4 + t) * TKB + kbl) * 64 + lane];
+            for (int s = 0; s < 8; ++s) {
+                // The next strip's fragment is read while this one's products run.
+                if (s + 1 < 8) af[(s + 1) % 2] = ws[buf * W_STAGE + ((wn * 8 + s + 1) * TKB + kbl) * 64 + lane];
 #pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) acc[s][t] = mfma16(af[s], bf[t], acc[s][t]);
+                for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(af[s % 2], bf[t], acc[s][t]);
+            }
         }
-        if (st + 1 < stages) store(1 - buf);
+        // The next stage has landed (this wave's loads), and every wave is done with this one.
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 
     // Epilogue: tile (s, t) holds W rows 16 strip + 4 (lane / 16) + i against X row
-    // m0 + 64 wm + 16 t + lane % 16.
+    // m0 + 16 (WT wm + t) + lane % 16.
     const int quad = lane / 16;
     if (EPI == EPI_RESIDUAL) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int m = m0 + wm * 64 + t * 16 + lane % 16;
+            for (int t = 0; t < WT; ++t) {
+                const int m = m0 + (wm * WT + t) * 16 + lane % 16;
                 if (m >= a.M) continue;
                 const float4 r = *reinterpret_cast<const float4*>(g.residual + (size_t)m * g.N + n);
                 float4 o;
@@ -157,8 +161,8 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
         for (int s = 0; s < 4; ++s) {
             const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int m = m0 + wm * 64 + t * 16 + lane % 16;
+            for (int t = 0; t < WT; ++t) {
+                const int m = m0 + (wm * WT + t) * 16 + lane % 16;
                 if (m >= a.M) continue;
                 float v[4];
 #pragma unroll
@@ -171,55 +175,87 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
             }
         }
     } else {  // EPI_QKV: rows of a strip pair as r, r + 8 (lanes l and l ^ 32)
+        // Each of the tile's 256 rows' position, cache block and RoPE row, staged once in the LDS
+        // the main loop is done with: a thread to a row, two round trips to memory in all.
+        float* t_cos = reinterpret_cast<float*>(lds);          // [TM][32]
+        float* t_sin = t_cos + TM * (HEAD_DIM / 2);            // [TM][32]
+        uint32_t* t_pos = reinterpret_cast<uint32_t*>(t_sin + TM * (HEAD_DIM / 2));  // [TM]
+        uint32_t* t_blk = t_pos + TM;                           // [TM]
+        {
+            const int j = threadIdx.x;  // PF_THREADS == TM
+            const int m = m0 + j;
+            uint32_t pos = TGX_SPARE_POS, blk = TGX_SPARE_POS;
+            if (m < a.M) {
+                const uint32_t p = a.tok_pos[m], sl = a.tok_slot[m];
+                if (p < (uint32_t)a.capacity && sl < (uint32_t)a.nslots) {
+                    pos = p;
+                    blk = a.table[(size_t)sl * a.max_blocks + p / BLOCK_TOKENS];
+                    if (a.rope) {
+#pragma unroll
+                        for (int e = 0; e < HEAD_DIM / 2; e += 4) {
+                            *reinterpret_cast<float4*>(t_cos + j * (HEAD_DIM / 2) + e) =
+                                *reinterpret_cast<const float4*>(a.cos + (size_t)p * (HEAD_DIM / 2) + e);
+                            *reinterpret_cast<float4*>(t_sin + j * (HEAD_DIM / 2) + e) =
+                                *reinterpret_cast<const float4*>(a.sin + (size_t)p * (HEAD_DIM / 2) + e);
+                        }
+                    }
+                }
+            }
+            t_pos[j] = pos;
+            t_blk[j] = blk;
+        }
+        __syncthreads();
         const int H = a.heads, KV = a.kv_heads;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const int strip = strip_of<EPI>(nb, wn, s, g.N);
             const int head = strip / 4, qtr = strip % 4;
             const bool second = quad >= 2;  // rows 8..15: the pairs' second halves
+            const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
+            const int d0 = p0 + (second ? HEAD_DIM / 2 : 0);
+            const bool rotate = head < H + KV && a.rope;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int m = m0 + wm * 64 + t * 16 + lane % 16;
+            for (int t = 0; t < WT; ++t) {
+                const int j = (wm * WT + t) * 16 + lane % 16;  // the row within the tile
                 float own[4], other[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     own[i] = acc[s][t][i];
                     other[i] = __shfl_xor(own[i], 32, WAVE);
                 }
-                if (m >= a.M) continue;
-                const uint32_t pos = a.tok_pos[m];
-                const uint32_t slot = a.tok_slot[m];
-                if (pos >= (uint32_t)a.capacity || slot >= (uint32_t)a.nslots) continue;
-                const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
+                const uint32_t pos = t_pos[j];
+                if (pos == TGX_SPARE_POS) continue;
                 float v[4];
+                if (rotate) {
+                    const float4 co = *reinterpret_cast<const float4*>(t_cos + j * (HEAD_DIM / 2) + p0);
+                    const float4 si = *reinterpret_cast<const float4*>(t_sin + j * (HEAD_DIM / 2) + p0);
+                    const float c4[4] = {co.x, co.y, co.z, co.w}, s4[4] = {si.x, si.y, si.z, si.w};
+                    // As upstream: x cos + rotate_half(x) sin (rope_rows.comp:52-59).
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[i] = own[i];
-                    if (head < H + KV && a.rope) {
-                        const float co = a.cos[(size_t)pos * (HEAD_DIM / 2) + p0 + i];
-                        const float si = a.sin[(size_t)pos * (HEAD_DIM / 2) + p0 + i];
-                        // As upstream: x cos + rotate_half(x) sin (rope_rows.comp:52-59).
-                        v[i] = second ? own[i] * co + other[i] * si : own[i] * co - other[i] * si;
-                    }
+                    for (int i = 0; i < 4; ++i)
+                        v[i] = second ? own[i] * c4[i] + other[i] * s4[i] : own[i] * c4[i] - other[i] * s4[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = own[i];
                 }
-                const int d0 = p0 + (second ? HEAD_DIM / 2 : 0);
+                const int m = m0 + j;
                 if (head < H) {
                     uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                     *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * HEAD_DIM + d0) = packed;
                     continue;
                 }
-                const uint32_t blk = a.table[(size_t)slot * a.max_blocks + pos / BLOCK_TOKENS];
+                const uint32_t blk = t_blk[j];
                 if (blk >= (uint32_t)a.nblocks) continue;
                 const int kv = head < H + KV ? head - H : head - H - KV;
                 uint16_t* tl = g.kv + ((size_t)blk * KV + kv) * 2 * KV_TILE;
                 const int pp = (int)(pos % BLOCK_TOKENS);
+                if (head < H + KV) {
+                    // Four consecutive dimensions of a key sit side by side in its tile.
+                    *reinterpret_cast<uint2*>(tl + key_index(pp, d0)) =
+                        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint16_t bits = (uint16_t)bf16_bits(v[i]);
-                    if (head < H + KV)
-                        tl[key_index(pp, d0 + i)] = bits;
-                    else
-                        tl[KV_TILE + value_index(pp, d0 + i)] = bits;
+                    for (int i = 0; i < 4; ++i) tl[KV_TILE + value_index(pp, d0 + i)] = (uint16_t)bf16_bits(v[i]);
                 }
             }
         }
@@ -269,19 +305,25 @@ __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* 
 }
 
 // ---------------------------------------------------------------------------------------------
-// prefill_attention: workgroup (tile, kv): the tile's positions (up to 32, eight to a wave) for
-// the `group` query heads KV head kv serves. Columns of the MFMA are (position, head) pairs,
-// 16 / group positions to a column group, CG = group / 2 column groups to a wave. The slot's
-// blocks from 0 to the tile's last position are staged through LDS in turn; each column keeps
-// its running maximum, sum and output (attention_rows.comp:71-116).
-template <int CG>
-__global__ void __launch_bounds__(PF_THREADS) prefill_attention(PrefillArgs a, const uint16_t* __restrict__ q,
-                                                                const uint16_t* __restrict__ kvpool,
-                                                                uint16_t* __restrict__ attended,
-                                                                const PrefillTile* __restrict__ tiles) {
-    __shared__ uint4 stage[2][2 * KV_TILE / 8];  // two blocks of keys then values
-    constexpr int group = 2 * CG;
-    constexpr int per_col = 16 / group;  // positions to a column group
+// prefill_attention: workgroup (tile, kv): the tile's positions (up to 32, 32 / WAVES to a wave)
+// for the `group` query heads KV head kv serves. Columns of the MFMA are (position, head) pairs,
+// 16 / group positions to a column group, CG column groups to a wave. The slot's blocks from 0 to
+// the tile's last position are staged through LDS in turn; each column keeps its running maximum,
+// sum and output (attention_rows.comp:71-116).
+constexpr int ATTN_TILE = 32;
+
+template <int WAVES, int CG>
+__global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a, const uint16_t* __restrict__ q,
+                                                                 const uint16_t* __restrict__ kvpool,
+                                                                 uint16_t* __restrict__ attended,
+                                                                 const PrefillTile* __restrict__ tiles) {
+    constexpr int THREADS = WAVES * WAVE;
+    constexpr int TOK = ATTN_TILE / WAVES;     // positions to a wave
+    constexpr int per_col = TOK / CG;          // positions to a column group
+    constexpr int group = 16 / per_col;
+    constexpr int STAGE = 2 * KV_TILE / 8;     // uint4 of a block's keys then values
+    constexpr int PER_THREAD = STAGE / THREADS;
+    __shared__ uint4 stage[2][STAGE];
     const PrefillTile tile = tiles[blockIdx.x];
     const int kv = blockIdx.y;
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -294,7 +336,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_attention(PrefillArgs a, c
     uint32_t cpos[CG];
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
-        const int tok = w * 8 + cg * per_col + col / group;  // within the tile
+        const int tok = w * TOK + cg * per_col + col / group;  // within the tile
         const int head = kv * group + col % group;
         const size_t row = tile.row0 + (tok < (int)tile.count ? tok : 0);
         cpos[cg] = tile.pos0 + tok;
@@ -311,16 +353,16 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_attention(PrefillArgs a, c
         for (int dt = 0; dt < 4; ++dt) o[cg][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    auto fetch = [&](int bi, uint4 (&r)[4]) {
+    auto fetch = [&](int bi, uint4 (&r)[PER_THREAD]) {
         const uint32_t blk = a.table[(size_t)tile.slot * a.max_blocks + bi];
         const uint16_t* src = kvpool + ((size_t)(blk < (uint32_t)a.nblocks ? blk : 0) * KV + kv) * 2 * KV_TILE;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r[j] = load16(src + (size_t)(threadIdx.x + j * PF_THREADS) * 8);
+        for (int j = 0; j < PER_THREAD; ++j) r[j] = load16(src + (size_t)(threadIdx.x + j * THREADS) * 8);
     };
-    uint4 reg[4];
+    uint4 reg[PER_THREAD];
     fetch(0, reg);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) stage[0][threadIdx.x + j * PF_THREADS] = reg[j];
+    for (int j = 0; j < PER_THREAD; ++j) stage[0][threadIdx.x + j * THREADS] = reg[j];
     __syncthreads();
     for (int bi = 0; bi < blocks; ++bi) {
         const int buf = bi % 2;
@@ -363,14 +405,13 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_attention(PrefillArgs a, c
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
                     const int pt = 2 * ks + half;
-                    float e[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        e[i] = __uint_as_float(bf16_bits(__expf(s[pt][i] - m_new)) << 16);
-                        sum += e[i];
-                    }
-                    words[half * 2] = pack_bf16x2(e[0], e[1]);
-                    words[half * 2 + 1] = pack_bf16x2(e[2], e[3]);
+                    // P rounded to bf16 for the product, the sum taken over the rounded values.
+                    words[half * 2] = pack_bf16x2(__expf(s[pt][0] - m_new), __expf(s[pt][1] - m_new));
+                    words[half * 2 + 1] = pack_bf16x2(__expf(s[pt][2] - m_new), __expf(s[pt][3] - m_new));
+                    sum += bf16_lo(words[half * 2]);
+                    sum += bf16_hi(words[half * 2]);
+                    sum += bf16_lo(words[half * 2 + 1]);
+                    sum += bf16_hi(words[half * 2 + 1]);
                 }
                 pf[ks] = make_uint4(words[0], words[1], words[2], words[3]);
             }
@@ -387,13 +428,13 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_attention(PrefillArgs a, c
         }
         if (bi + 1 < blocks) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) stage[1 - buf][threadIdx.x + j * PF_THREADS] = reg[j];
+            for (int j = 0; j < PER_THREAD; ++j) stage[1 - buf][threadIdx.x + j * THREADS] = reg[j];
         }
         __syncthreads();
     }
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
-        const int tok = w * 8 + cg * per_col + col / group;
+        const int tok = w * TOK + cg * per_col + col / group;
         if (tok >= (int)tile.count) continue;
         const int head = kv * group + col % group;
         const size_t row = tile.row0 + tok;
@@ -454,10 +495,11 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
         GemmArgs qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, nullptr, b.q, L.kv};
         dispatch("prefill_qkv", prefill_gemm<EPI_QKV>, dim3(qkv_rows / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, qkv);
         switch (group) {
-            case 2: dispatch("prefill_attention", prefill_attention<1>, dim3(b.ntiles, a.kv_heads), dim3(PF_THREADS), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 4: dispatch("prefill_attention", prefill_attention<2>, dim3(b.ntiles, a.kv_heads), dim3(PF_THREADS), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 8: dispatch("prefill_attention", prefill_attention<4>, dim3(b.ntiles, a.kv_heads), dim3(PF_THREADS), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 16: dispatch("prefill_attention", prefill_attention<8>, dim3(b.ntiles, a.kv_heads), dim3(PF_THREADS), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 1: dispatch("prefill_attention", prefill_attention<2, 1>, dim3(b.ntiles, a.kv_heads), dim3(2 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 2: dispatch("prefill_attention", prefill_attention<4, 1>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 4: dispatch("prefill_attention", prefill_attention<8, 1>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 8: dispatch("prefill_attention", prefill_attention<8, 2>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 16: dispatch("prefill_attention", prefill_attention<8, 4>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
             default: return hipErrorInvalidValue;
         }
         GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr};

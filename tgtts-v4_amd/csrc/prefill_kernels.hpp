@@ -17,7 +17,7 @@ struct PrefillTile {
 // What every prefill kernel reads.
 struct PrefillArgs {
     int M;        // rows (positions over every run)
-    int M_pad;    // rows the tensors hold, a multiple of 128
+    int M_pad;    // rows the tensors hold, a multiple of 256
     int hidden, inner, heads, kv_heads;
     int capacity, nslots, max_blocks, nblocks;
     float eps, scale;
