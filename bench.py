@@ -96,7 +96,10 @@ def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int,
     spec, shape = spec_and_shape(capacity)
     dec = tgx.Decoder(ctx, shape, tgx.Batch(rows=rows, slots=rows))
     if EAGER:
+        # Every dispatch of the run launched on its own with its own events, as the per-kernel
+        # timings below are taken, so a profiler's averages over the run compare with them.
         dec.set_graph(False)
+        dec.set_timed(True)
     load(dec, weights)
     from tgx.synth import embeddings
 
@@ -127,7 +130,7 @@ def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int,
         dec.wait()
         for label, ms in dec.timings():
             per.setdefault(label, []).append(ms)
-    dec.set_timed(False)
+    dec.set_timed(EAGER)
     dec.close()
     positions_mid = [c + steps // 2 for c in contexts]
     bytes_mid = step_bytes(shape, positions_mid)
@@ -187,6 +190,7 @@ def run_prefill(ctx, weights, count: int, length: int, times: int, decode_steps:
     dec = tgx.Decoder(ctx, shape, tgx.Batch(rows=count, slots=count))
     if EAGER:
         dec.set_graph(False)
+        dec.set_timed(True)
     load(dec, weights)
     x = embeddings(9, "bench.prefill", count * length, shape.hidden)
     runs = [(s, 0, length) for s in range(count)]
@@ -205,7 +209,7 @@ def run_prefill(ctx, weights, count: int, length: int, times: int, decode_steps:
     per = {}
     for label, ms in dec.timings():
         per.setdefault(label, []).append(ms)
-    dec.set_timed(False)
+    dec.set_timed(EAGER)
     # The decode steps that follow, every run at once.
     xs = embeddings(10, "bench.after", count, shape.hidden)
     for r in range(count):
@@ -265,6 +269,36 @@ def cpu_baseline(weights, seconds: float):
     }
 
 
+COPY_BYTES = 256 << 20
+
+
+def copy_calibration() -> int:
+    """A plain elementwise copy (torch.neg, out=) of COPY_BYTES, five times: the kernel whose
+    FETCH_SIZE and WRITE_SIZE counters are known to be COPY_BYTES each."""
+    import torch
+
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log(f"copied {COPY_BYTES} bytes 5 times, check {float(dst[0])}")
+    return 0
+
+
+def measured_traffic(label: str, workload: str):
+    """HBM bytes per launch of `label` measured with rocprofv3's FETCH_SIZE and WRITE_SIZE on the
+    same workload, each scaled by the counter's reading of a copy of known size; None when no
+    measurement of this kernel on this workload is on record."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text()).get(label)
+    if not rec or rec.get("workload") != workload:
+        return None
+    return rec["bytes_per_launch"]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,11 +309,15 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 8 x 2048 prefill")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of 256 MiB five times (scales rocprofv3's HBM counters)")
     ap.add_argument("--eager", action="store_true",
                     help="launch each step dispatch by dispatch, not as the recorded graph (for profilers)")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (requests would be routed to "
               "GPUs at admission, with no collective); run with --gpus 1.", file=sys.stderr)
@@ -355,7 +393,7 @@ def main() -> int:
         "peak": HBM_PEAK / 1e9,
         "unit": "GB/s",
         "frac": round(achieved / (HBM_PEAK / 1e9), 4),
-        "traffic": None,
+        "traffic": measured_traffic(dom_label, f"batch {args.batch}"),
         "bytes_per_launch": dom["bytes_per_launch"],
         "avg_us": round(dom["avg_us"], 3),
     }
