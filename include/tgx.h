@@ -211,6 +211,99 @@ tgx_status tgx_prefill_runs(tgx_decoder* dec, const tgx_run* runs, int nruns, co
  * tgx_decoder_elapsed_ms times it. */
 tgx_status tgx_prefill_launch(tgx_decoder* dec, int times);
 
+/* ---- the patch sampler: crates/graph/src/local/dit.rs ---- */
+
+/* What sampler_graph takes besides the DiT's stack (dit.rs:114-131): a patch of `feat_dim`
+ * channels by `patch_size` frames, sampled in `timesteps` Euler steps, for `rows` rows at once.
+ * The DiT's sequences are MU_TOKENS (2) condition tokens, the time, the patch before and the
+ * noisy patch: 3 + 2 patch_size tokens. */
+typedef struct {
+    int feat_dim, patch_size, timesteps, rows;
+} tgx_patch_shape;
+
+typedef struct tgx_sampler tgx_sampler;
+
+/* euler_steps (dit.rs:61-79), in f32: the time and step length of each step the DiT runs at in
+ * `timesteps` steps (the first 4 %, at least one, run nothing); *n of them, `max` written. */
+tgx_status tgx_euler_steps(int timesteps, int max, float* t, float* dt, int* n);
+
+/* Sampler::new (dit.rs:270-282): the DiT's stack as a tgx_shape (head_dim 64; capacity is
+ * ignored, the sequence is the capacity), weights zero until loaded; records the sample, every
+ * Euler step with its DiT run, as one HIP graph. */
+tgx_status tgx_sampler_create(tgx_context* ctx, const tgx_shape* stack, const tgx_patch_shape* patch,
+                              tgx_sampler** out);
+void tgx_sampler_destroy(tgx_sampler* s);
+
+/* load_sampler (dit.rs:329-365), one tensor: the stack's as tgx_decoder_load names them
+ * ("layers.{l}.qkv_proj", ..., "norm"); "in_proj.weight" and "cond_proj.weight"
+ * ([hidden][feat_dim]), "out_proj.weight" ([feat_dim][hidden]) and their ".bias"; and the time
+ * MLPs "time_mlp.linear_1.weight", "time_mlp.linear_1.bias", "time_mlp.linear_2.weight",
+ * "time_mlp.linear_2.bias" and the same under "delta_time_mlp." ([hidden][hidden], [hidden]),
+ * from which each step's time token is computed in f64 on the host. */
+tgx_status tgx_sampler_load(tgx_sampler* s, const char* name, const void* data, tgx_dtype dtype,
+                            size_t count);
+
+/* Sampler::sample (dit.rs:294-309): each row's patch [feat_dim][patch_size] f32 from its
+ * conditions mu [MU_TOKENS][hidden] (lm_to_dit_proj's output, then res_to_dit_proj's), its patch
+ * before `cond` and its `noise` (both [feat_dim][patch_size]), at its temperature and guidance
+ * scale (`sampling` [rows][2]); every array a row after a row, f32. */
+tgx_status tgx_sampler_sample(tgx_sampler* s, const float* mu, const float* cond, const float* noise,
+                              const float* sampling, float* patch);
+/* Launches the sample `times` times over the inputs on the device, copying nothing (each from
+ * the same noise); tgx_sampler_wait waits, tgx_sampler_elapsed_ms times it. */
+tgx_status tgx_sampler_launch(tgx_sampler* s, int times);
+tgx_status tgx_sampler_wait(tgx_sampler* s);
+tgx_status tgx_sampler_elapsed_ms(const tgx_sampler* s, float* out);
+/* Sampler::timings (dit.rs:311-313): as tgx_decoder_set_timed / tgx_decoder_timings. */
+tgx_status tgx_sampler_set_timed(tgx_sampler* s, int timed);
+tgx_status tgx_sampler_timings(tgx_sampler* s, int max, tgx_timing* out, int* n);
+tgx_status tgx_sampler_dispatches(const tgx_sampler* s, int* out);
+
+/* ---- the LM side: crates/graph/src/lm_side.rs ---- */
+
+/* LmSideShape's widths besides the LMs' (lm_side.rs:59-72): the local encoder's (the step's
+ * input), the DiT's (mu is [rows][2 dit]), the scalar quantizer's bottleneck and its levels to a
+ * unit (scalar_quantization_scale). */
+typedef struct {
+    int encoder, dit, latent, levels;
+} tgx_heads_shape;
+
+typedef struct tgx_lm_side tgx_lm_side;
+
+/* lm_side_batch_graph (lm_side.rs:337-491): the base LM and the residual LM (a tgx_shape each;
+ * the residual's rope = 0, decode.rs:47-50) as decoders over one batch, and the layers between
+ * them; records the step as one HIP graph. */
+tgx_status tgx_lm_side_create(tgx_context* ctx, const tgx_shape* base, const tgx_shape* residual,
+                              const tgx_batch* batch, const tgx_heads_shape* heads, tgx_lm_side** out);
+void tgx_lm_side_destroy(tgx_lm_side* s);
+
+/* load_lm_side (lm_side.rs:496-533), one tensor: "base_lm.<name>" and "residual_lm.<name>" as
+ * tgx_decoder_load names them; "enc_to_lm_proj", "fsq_layer.in_proj", "fsq_layer.out_proj",
+ * "fusion_concat_proj", "lm_to_dit_proj", "res_to_dit_proj", "stop_proj" each ".weight"
+ * ([out][in]) and ".bias"; "stop_head.weight" (no bias, Heads::named, lm_side.rs:131-142). */
+tgx_status tgx_lm_side_load(tgx_lm_side* s, const char* name, const void* data, tgx_dtype dtype,
+                            size_t count);
+/* The decoder of the base LM (which = 0) or the residual LM (1), to prefill its cache or release
+ * its slots; owned by the LM side. */
+tgx_status tgx_lm_side_decoder(tgx_lm_side* s, int which, tgx_decoder** out);
+
+/* LmSide::step_rows (lm_side.rs:599-625): `enc` [rows][encoder] f32 at the rows' places
+ * (both LMs' caches written there); returns mu [rows][2 dit] and the stop logits [rows][2]. */
+tgx_status tgx_lm_side_step(tgx_lm_side* s, const tgx_row* rows, int nrows, const float* enc,
+                            float* mu, float* stop_logits);
+/* Places the rows and copies `enc` in without launching. */
+tgx_status tgx_lm_side_set_rows(tgx_lm_side* s, const tgx_row* rows, int nrows, const float* enc);
+/* Launches the step `times` times over what the device holds; with `advance` each moves every
+ * placed row on by a position (the slots must hold the blocks: tgx_decoder_reserve on both). */
+tgx_status tgx_lm_side_launch(tgx_lm_side* s, int times, int advance);
+tgx_status tgx_lm_side_wait(tgx_lm_side* s);
+tgx_status tgx_lm_side_elapsed_ms(const tgx_lm_side* s, float* out);
+/* One of the step's tensors after the last step, f32, `count` values: "embed" [rows][hidden],
+ * "base_out", "levels" [rows][latent], "lm_hidden", "residual_in", "residual_out",
+ * "stop_hidden" ([rows][hidden]), "mu" [rows][2 dit], "stop_logits" [rows][2]. */
+tgx_status tgx_lm_side_read(tgx_lm_side* s, const char* tensor, float* out, size_t count);
+tgx_status tgx_lm_side_dispatches(const tgx_lm_side* s, int* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,185 @@
+"""The patch oracle pinned on the CPU: the Euler schedule's ends and step counts
+(crates/graph/src/local/dit.rs:44-79), the time embedding's closed form (dit.rs:367-381),
+CFG-Zero*'s reductions (dit_euler.comp:81-110), the scalar quantizer's special cases
+(gemv_linear.comp:54-59), the local stack against an independent torch float64 model, and the
+whole sampler against the closed form it takes when out_proj reads nothing. The library's own
+schedule (host code, no GPU) must agree with the oracle's bit for bit."""
+
+import math
+
+import numpy as np
+import pytest
+
+import patch_oracle as po
+
+
+def test_ten_steps_run_the_dit_nine_times_from_one_towards_zero():
+    span = po.schedule(10)
+    assert span[0] == np.float32(1.0) and span[-1] == np.float32(0.0)
+    assert np.all(np.diff(span) < 0)
+    steps = po.euler_steps(10)
+    assert len(steps) == 9
+    # The first evaluation is at t_span[1], each dt the gap to the next time.
+    assert steps[0][0] == pytest.approx(float(span[1]), abs=1e-7)
+    for (t, dt), nxt in zip(steps, span[2:]):
+        assert t - dt == pytest.approx(float(nxt), abs=2e-7)
+    assert sum(dt for _, dt in steps) == pytest.approx(float(span[1]), abs=1e-6)
+
+
+@pytest.mark.parametrize("n, evaluations", [(1, 0), (2, 1), (10, 9), (24, 23), (25, 24), (49, 47), (50, 48)])
+def test_the_zero_init_steps_are_four_percent_but_at_least_one(n, evaluations):
+    assert len(po.euler_steps(n)) == evaluations
+
+
+def test_the_sway_is_the_closed_form_in_float64_to_float32_precision():
+    span = po.schedule(16)
+    t = np.linspace(1.0, 0.0, 17)
+    want = t + (np.cos(np.pi / 2 * t) - 1.0 + t)
+    assert np.max(np.abs(span - want)) < 4e-7
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 10, 25, 50])
+def test_the_library_schedule_is_the_oracles_bit_for_bit(n):
+    from tgx.patch import euler_steps
+
+    got = euler_steps(n)
+    want = po.euler_steps(n)
+    assert len(got) == len(want)
+    for (gt, gdt), (wt, wdt) in zip(got, want):
+        assert np.float32(gt) == np.float32(wt) and np.float32(gdt) == np.float32(wdt)
+
+
+def test_the_time_embedding_at_zero_is_sines_zero_then_cosines_one():
+    e = po.time_embedding(0.0, 1024)
+    assert np.all(e[:512] == 0.0) and np.all(e[512:] == 1.0)
+
+
+def test_the_time_embedding_follows_the_float64_closed_form():
+    h = 1024
+    e = po.time_embedding(0.37, h)
+    freqs = np.exp(np.arange(h // 2) * -(math.log(10000.0) / (h // 2 - 1)))
+    a = 370.0 * freqs
+    # f32 angles of magnitude up to 370: an ulp of 3e-5 there.
+    assert np.max(np.abs(e - np.concatenate([np.sin(a), np.cos(a)]))) < 1e-4
+
+
+def test_cfg_zero_star_reduces_as_its_algebra_says():
+    rng = np.random.default_rng(0)
+    vc, vu = rng.standard_normal(256), rng.standard_normal(256)
+    assert np.allclose(po.cfg_zero_star(vc, vu, 1.0), vc, atol=1e-12)
+    g = po.cfg_zero_star(vu, vu, 2.0)
+    alpha = vu @ vu / (vu @ vu + 1e-8)
+    assert np.allclose(g, vu * (alpha + 2.0 * (1 - alpha)), atol=1e-12)
+    assert np.allclose(po.cfg_zero_star(vc, np.zeros(256), 2.0), 2.0 * vc)
+    # A planted defect: guidance applied to the raw unconditional velocity differs.
+    plain = vu + 2.0 * (vc - vu)
+    assert not np.allclose(po.cfg_zero_star(vc, vu, 2.0), plain)
+
+
+def test_the_quantizer_rounds_tanh_to_its_levels_ties_to_even():
+    L = 9
+    assert po.quantize(np.array([0.0]), L)[0] == 0.0
+    assert np.all(po.quantize(np.array([40.0, -40.0]), L) == [1.0, -1.0])
+    v = np.linspace(-3, 3, 10001)
+    q = po.quantize(v, L)
+    assert np.allclose(q * L, np.rint(q * L))
+    assert np.max(np.abs(q - np.tanh(v))) <= 0.5 / L + 1e-12
+    assert np.all(np.diff(q) >= 0)
+    # Ties: tanh(v) L = k + 1/2 rounds to the even k.
+    for k in (0, 1, 2, 7):
+        tie = math.atanh((k + 0.5) / L)
+        got = po.quantize(np.array([tie]), L)[0] * L
+        assert round(got) in (k, k + 1)
+    assert np.rint(2.5) == 2.0 and np.rint(3.5) == 4.0
+
+
+def _torch_local_stack(w, s, x, T):
+    """An independent float64 model of the local stack from torch library ops."""
+    import torch
+    import torch.nn.functional as F
+
+    def t(n):
+        return torch.tensor(np.asarray(w[n], dtype=np.float64))
+
+    def norm(v, g):
+        return v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + s.eps) * g
+
+    import oracle
+
+    cos, sin = (torch.tensor(a.astype(np.float64)) for a in oracle.rope_tables(T, s.head_dim, s.rope_theta))
+    cos = torch.cat([cos, cos], -1)
+    sin = torch.cat([sin, sin], -1)
+
+    def rot(v):  # [seqs][heads][T][d]
+        half = v.shape[-1] // 2
+        return v * cos + torch.cat([-v[..., half:], v[..., :half]], -1) * sin
+
+    H, KV, d = s.heads, s.kv_heads, s.head_dim
+    xt = torch.tensor(x)
+    seqs = xt.shape[0] // T
+    for l in range(s.layers):
+        n = norm(xt, t(f"layers.{l}.input_layernorm"))
+        qkv = n @ t(f"layers.{l}.qkv_proj").T
+        q = qkv[:, : H * d].reshape(seqs, T, H, d).transpose(1, 2)
+        k = qkv[:, H * d : (H + KV) * d].reshape(seqs, T, KV, d).transpose(1, 2)
+        v = qkv[:, (H + KV) * d :].reshape(seqs, T, KV, d).transpose(1, 2)
+        q, k = rot(q), rot(k)
+        k = k.repeat_interleave(H // KV, dim=1)
+        v = v.repeat_interleave(H // KV, dim=1)
+        a = F.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(-1, H * d)
+        xt = xt + a @ t(f"layers.{l}.o_proj").T
+        n = norm(xt, t(f"layers.{l}.post_attention_layernorm"))
+        gate, up = (n @ t(f"layers.{l}.gate_up_proj").T).split(s.inner, -1)
+        xt = xt + (F.silu(gate) * up) @ t(f"layers.{l}.down_proj").T
+    return norm(xt, t("norm")).numpy()
+
+
+def _small_dit(layers=2):
+    from tgx.synth import StackSpec, sampler_weights
+
+    spec = StackSpec(layers=layers, hidden=1024, inner=1024, dtype="f32", seed=3)
+    return spec, sampler_weights(spec, 64)
+
+
+def test_the_local_stack_matches_an_independent_torch_model():
+    spec, w = _small_dit(2)
+    s = po.StackShape(hidden=spec.hidden, inner=spec.inner, layers=spec.layers)
+    T = 11
+    x = np.random.default_rng(1).standard_normal((2 * T, spec.hidden))
+    got = po.local_stack(w, s, x, T)
+    want = _torch_local_stack(w, s, x, T)
+    assert np.max(np.abs(got - want)) < 1e-9
+    # Planted defects: RoPE left out, or positions counted across sequences, must show.
+    assert np.max(np.abs(po.local_stack(w, s, x, T, rope_on=False) - want)) > 1e-3
+
+
+def test_sequences_do_not_see_each_other():
+    spec, w = _small_dit(1)
+    s = po.StackShape(hidden=spec.hidden, inner=spec.inner, layers=spec.layers)
+    T = 11
+    x = np.random.default_rng(2).standard_normal((3 * T, spec.hidden))
+    both = po.local_stack(w, s, x, T)
+    alone = po.local_stack(w, s, x[T : 2 * T], T)
+    assert np.allclose(both[T : 2 * T], alone, atol=1e-12)
+
+
+def test_the_sampler_is_the_euler_closed_form_when_out_proj_reads_nothing():
+    """out_proj.weight = 0: both velocities are the bias b, guided = (alpha + cfg (1 - alpha)) b,
+    and the patch is x0 - (sum of dt) guided whatever the DiT computes."""
+    spec, w = _small_dit(1)
+    w = dict(w)
+    w["out_proj.weight"] = np.zeros_like(w["out_proj.weight"])
+    s = po.StackShape(hidden=spec.hidden, inner=spec.inner, layers=spec.layers)
+    rows, feat, frames, n = 2, 64, 4, 10
+    rng = np.random.default_rng(3)
+    mu = rng.standard_normal((rows, 2, spec.hidden))
+    cond = rng.standard_normal((rows, feat, frames))
+    noise = rng.standard_normal((rows, feat, frames))
+    sampling = np.array([[0.8, 2.0], [1.0, 1.5]])
+    x0, patch = po.sample(w, s, feat, frames, n, mu, cond, noise, sampling)
+    b = np.asarray(w["out_proj.bias"], np.float64)[None, :, None] * np.ones((1, 1, frames))
+    total = sum(dt for _, dt in po.euler_steps(n))
+    for r in range(rows):
+        g = po.cfg_zero_star(b[0], b[0], sampling[r, 1])
+        assert np.allclose(patch[r], x0[r] - total * g, atol=1e-12)
+        assert np.allclose(x0[r], sampling[r, 0] * noise[r])

@@ -34,9 +34,14 @@ HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-Wno-unus
 SOURCES = {
     "decode_kernels.hip": DEVICE_FLAGS,
     "prefill_kernels.hip": DEVICE_FLAGS,
+    "local_kernels.hip": DEVICE_FLAGS,
+    "heads_kernels.hip": DEVICE_FLAGS,
     "runtime.cpp": HOST_FLAGS,
     "prefill.cpp": HOST_FLAGS,
     "api.cpp": HOST_FLAGS,
+    "sampler.cpp": HOST_FLAGS,
+    "lm_side.cpp": HOST_FLAGS,
+    "api_patch.cpp": HOST_FLAGS,
 }
 
 

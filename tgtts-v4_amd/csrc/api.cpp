@@ -1,17 +1,11 @@
 // The C ABI (include/tgx.h) over the runtime: argument checks, the thread's error message, and
 // nothing else.
-#include "runtime.hpp"
+#include "handles.hpp"
 
 namespace tgx {
 const char* last_error();
 }
 
-struct tgx_context {
-    tgx::Context* ctx;
-};
-struct tgx_decoder {
-    tgx::Decoder* dec;
-};
 
 using namespace tgx;
 
@@ -72,7 +66,7 @@ tgx_status tgx_decoder_create(tgx_context* ctx, const tgx_shape* shape, const tg
 }
 
 void tgx_decoder_destroy(tgx_decoder* dec) {
-    if (!dec) return;
+    if (!dec || dec->borrowed) return;
     decoder_destroy(dec->dec);
     delete dec;
 }

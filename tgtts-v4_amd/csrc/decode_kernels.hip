@@ -16,8 +16,8 @@
 // No workgroup waits for another: every output is finished by the workgroup that sums it, so
 // that a kernel ends when its slowest workgroup does.
 #include "decode_kernels.hpp"
+#include "dispatch.hpp"
 
-#include <hip/hip_ext.h>
 #include <math.h>
 
 namespace tgx {
@@ -495,18 +495,6 @@ __global__ void __launch_bounds__(WAVE) final_rmsnorm(DecodeArgs a, const float*
 
 namespace {
 
-// Launches `kernel`, timed by the next pair of the timer's events when there is a timer.
-template <typename... KernelArgs, typename... Args>
-void dispatch(const char* label, void (*kernel)(KernelArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
-              DispatchTimer* timer, Args... args) {
-    if (timer && timer->used < timer->capacity) {
-        const int i = timer->used++;
-        timer->labels[i] = label;
-        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, timer->start[i], timer->stop[i], 0, args...);
-    } else {
-        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
-    }
-}
 
 size_t attention_lds(const DecodeArgs& a) { return (size_t)ATTN_WAVES * (a.heads / a.kv_heads) * (HEAD_DIM + 1) * 4; }
 

@@ -1,0 +1,29 @@
+// The linear layers between VoxCPM2's LMs (gemv_linear.comp; crates/graph/src/lm_side.rs:246-297).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "decode_kernels.hpp"
+
+namespace tgx {
+
+enum LinearAct { ACT_NONE = 0, ACT_SILU = 1, ACT_LEVELS = 2 };
+
+// out[b][offset + n] = act(sum_k W[n][k] [x0; x1][b][k] + bias[n]) for rows b < rows: W in 16-row
+// MFMA tiles of [N_pad][K0 + K1] (rows past N zero), x0 [rows][K0] and x1 [rows][K1] in f32,
+// out rows `stride` apart.
+struct LinearArgs {
+    const uint16_t* w;
+    const float* bias;  // [N]
+    const float* x0;
+    const float* x1;
+    float* out;
+    int K0, K1, N, rows, offset, stride, act;
+    float levels;
+};
+
+constexpr int LINEAR_MAX_K = 2048;
+
+hipError_t launch_linear(const char* label, const LinearArgs& a, hipStream_t stream, DispatchTimer* timer);
+
+}  // namespace tgx

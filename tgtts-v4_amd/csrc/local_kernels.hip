@@ -1,0 +1,488 @@
+// The local stack and the patch sampler on gfx950 (crates/graph/src/local/mod.rs:354-656 with
+// local_{norm,qkv_rope,attention,partial,add_norm,gate_up}.comp; crates/graph/src/local/dit.rs
+// with local_embed.comp, dit_euler.comp and cfm_noise.comp):
+//
+//   local_gemm      C = X W^T over a few hundred tokens, bf16 in, f32 accumulate, a 64-row by
+//                   128-token tile to a workgroup of four waves, staged through LDS by direct
+//                   global-to-LDS loads, with the epilogue fused: RoPE at each token's place in
+//                   its sequence (local_qkv_rope.comp), SiLU(gate) up (local_gate_up.comp), or
+//                   the f32 sums of one part of the columns (local_partial.comp)
+//   local_attention every token of a sequence attends to every token of it, a workgroup to a
+//                   sequence (local_attention.comp)
+//   local_add_norm  residual + the parts' sums in their order, then RMSNorm (local_add_norm.comp,
+//                   local_norm.comp)
+//   local_embed     a linear layer over a patch's frames into tokens, and tokens copied beside
+//                   them (local_embed.comp)
+//   dit_euler       out_proj's velocities, CFG-Zero* guidance and the Euler step (dit_euler.comp)
+//   cfm_noise       x = temperature noise (cfm_noise.comp)
+//
+// The projections read each weight once for every token of a workgroup's tile, and a token's
+// sums run in the same order whatever else is in its tile, so a row samples the same patch beside
+// other rows as it does alone.
+#include "local_kernels.hpp"
+
+#include <math.h>
+
+#include "dispatch.hpp"
+
+namespace tgx {
+
+namespace {
+
+constexpr int LG_THREADS = 256;
+constexpr int LG_TKB = 2;                             // k-blocks of 32 to a stage
+constexpr int LG_W_STAGE = 4 * LG_TKB * 64;            // uint4 per stage: 4 strips, 8 KiB
+constexpr int LG_X_STAGE = 8 * LG_TKB * 64;            // 8 token tiles, 16 KiB
+constexpr int LG_FRAGS = (LG_W_STAGE + LG_X_STAGE) / 64 / 4;  // 1 KiB fragments a wave loads a stage
+
+enum LocalEpilogue { LEPI_QKV = 0, LEPI_PARTIAL = 1, LEPI_SILU = 2 };
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+struct LocalGemm {
+    const uint16_t* w;  // 16-row tiles of [N][K]
+    const uint16_t* x;  // bf16 [M_pad][K]
+    int K, N;
+    float* partial;     // LEPI_PARTIAL: f32 [parts][M_pad][N]
+    uint16_t* mlp;      // LEPI_SILU: bf16 [M_pad][N / 2]
+    uint16_t *q, *k, *v;
+};
+
+// Strip s (0, 1) of wave row wn of n-block nb: two strips of W in a row, or for the gate/up
+// projection a strip of the gate and the same rows of up.
+template <int EPI>
+__device__ __forceinline__ int local_strip(int nb, int wn, int s, int N) {
+    if (EPI == LEPI_SILU) {
+        const int gate = nb * 2 + wn;
+        return s == 0 ? gate : gate + N / 32;
+    }
+    return nb * 4 + wn * 2 + s;
+}
+
+// Grid (n-blocks, token blocks, parts): part z sums k-blocks z K/32/parts .. of every row.
+template <int EPI>
+__global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm g) {
+    __shared__ uint4 ws[2 * LG_W_STAGE];
+    __shared__ uint4 xs[2 * LG_X_STAGE];
+    const int nb = blockIdx.x, m0 = blockIdx.y * LOCAL_TOKEN_TILE, part = blockIdx.z;
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int wn = w / 2, wm = w % 2;
+    const int kblocks = g.K / 32;
+    const int part_kb = kblocks / gridDim.z;
+    const int kb0 = part * part_kb;
+    const int stages = part_kb / LG_TKB;
+
+    // Fragments 0..7 of a stage are W's (strip f / 2, k-block f % 2), 8..23 the tokens' (tile
+    // (f - 8) / 2): lane l of a load writes bytes 16 l .. of the fragment, the MFMA operand order.
+    auto fetch = [&](int st, int buf) {
+#pragma unroll
+        for (int j = 0; j < LG_FRAGS; ++j) {
+            const int f = w * LG_FRAGS + j;
+            const int kb = kb0 + st * LG_TKB + f % 2;
+            if (f < 8) {
+                const int sl = f / 2;
+                const uint16_t* src = g.w + weight_tile_index(local_strip<EPI>(nb, sl / 2, sl % 2, g.N), kb, kblocks, 16) + lane * 8;
+                __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&ws[buf * LG_W_STAGE + f * 64], 16, 0, 0);
+            } else {
+                const int mt = (f - 8) / 2;
+                const uint16_t* src = g.x + (size_t)(m0 + mt * 16 + lane % 16) * g.K + kb * 32 + (lane / 16) * 8;
+                __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&xs[buf * LG_X_STAGE + (f - 8) * 64], 16, 0, 0);
+            }
+        }
+    };
+
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    fetch(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int st = 0; st < stages; ++st) {
+        const int buf = st % 2;
+        if (st + 1 < stages) fetch(st + 1, 1 - buf);
+#pragma unroll
+        for (int kbl = 0; kbl < LG_TKB; ++kbl) {
+            uint4 af[2], bf[4];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) af[s] = ws[buf * LG_W_STAGE + ((wn * 2 + s) * LG_TKB + kbl) * 64 + lane];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bf[t] = xs[buf * LG_X_STAGE + ((wm * 4 + t) * LG_TKB + kbl) * 64 + lane];
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[s][t] = mfma16(af[s], bf[t], acc[s][t]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    // Tile (s, t) holds W rows 16 strip + 4 (lane / 16) + i against token m0 + 16 (4 wm + t) + lane % 16.
+    const int quad = lane / 16;
+    if (EPI == LEPI_PARTIAL) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int n = local_strip<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int m = m0 + (wm * 4 + t) * 16 + lane % 16;
+                *reinterpret_cast<float4*>(g.partial + ((size_t)part * a.M_pad + m) * g.N + n) =
+                    make_float4(acc[s][t][0], acc[s][t][1], acc[s][t][2], acc[s][t][3]);
+            }
+        }
+    } else if (EPI == LEPI_SILU) {
+        const int inner = g.N / 2;
+        const int n = local_strip<EPI>(nb, wn, 0, g.N) * 16 + quad * 4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int m = m0 + (wm * 4 + t) * 16 + lane % 16;
+            if (m >= a.M) continue;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float gate = acc[0][t][i], up = acc[1][t][i];
+                v[i] = gate / (1.0f + __expf(-gate)) * up;
+            }
+            *reinterpret_cast<uint2*>(g.mlp + (size_t)m * inner + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        }
+    } else {  // LEPI_QKV: a strip's rows pair as r, r + 8 (lanes l and l ^ 32)
+        const int H = a.heads, KV = a.kv_heads;
+        const bool second = quad >= 2;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int strip = local_strip<EPI>(nb, wn, s, g.N);
+            const int head = strip / 4, qtr = strip % 4;
+            const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
+            const int d0 = p0 + (second ? HEAD_DIM / 2 : 0);
+            const bool rotate = head < H + KV && a.rope;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float own[4], other[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    own[i] = acc[s][t][i];
+                    other[i] = __shfl_xor(own[i], 32, WAVE);
+                }
+                const int m = m0 + (wm * 4 + t) * 16 + lane % 16;
+                if (m >= a.M) continue;
+                float v[4];
+                if (rotate) {
+                    const int place = m % a.T;
+                    const float4 co = *reinterpret_cast<const float4*>(a.cos + place * (HEAD_DIM / 2) + p0);
+                    const float4 si = *reinterpret_cast<const float4*>(a.sin + place * (HEAD_DIM / 2) + p0);
+                    const float c4[4] = {co.x, co.y, co.z, co.w}, s4[4] = {si.x, si.y, si.z, si.w};
+                    // As upstream: x cos + rotate_half(x) sin (local_qkv_rope.comp:71-76).
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        v[i] = second ? own[i] * c4[i] + other[i] * s4[i] : own[i] * c4[i] - other[i] * s4[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = own[i];
+                }
+                const uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                if (head < H)
+                    *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * HEAD_DIM + d0) = packed;
+                else if (head < H + KV)
+                    *reinterpret_cast<uint2*>(g.k + ((size_t)m * KV + head - H) * HEAD_DIM + d0) = packed;
+                else
+                    *reinterpret_cast<uint2*>(g.v + ((size_t)m * KV + head - H - KV) * HEAD_DIM + d0) = packed;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// local_attention: a workgroup to a sequence; thread i < T heads takes query head i % heads of
+// token i / heads, against the sequence's keys and values staged in LDS in f32. Scores in f32,
+// max-subtracted exponentials summed in key order, the weighted values divided by the sum.
+__global__ void __launch_bounds__(256) local_attention(LocalArgs a, const uint16_t* __restrict__ q,
+                                                       const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                       uint16_t* __restrict__ attended) {
+    __shared__ float ks[LOCAL_MAX_T * 2 * HEAD_DIM * 2];  // [T][kv_heads][64], kv_heads <= 4 at T 16
+    __shared__ float vs[LOCAL_MAX_T * 2 * HEAD_DIM * 2];
+    const int seq = blockIdx.x, T = a.T, H = a.heads, KV = a.kv_heads;
+    const int first = seq * T;
+    const int n = T * KV * HEAD_DIM;
+    for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
+        const uint32_t kw = reinterpret_cast<const uint32_t*>(k + (size_t)first * KV * HEAD_DIM)[i];
+        const uint32_t vw = reinterpret_cast<const uint32_t*>(v + (size_t)first * KV * HEAD_DIM)[i];
+        ks[2 * i] = bf16_lo(kw);
+        ks[2 * i + 1] = bf16_hi(kw);
+        vs[2 * i] = bf16_lo(vw);
+        vs[2 * i + 1] = bf16_hi(vw);
+    }
+    __syncthreads();
+    const int item = threadIdx.x;
+    if (item >= T * H) return;
+    const int t = item / H, head = item % H, kv = head / (H / KV);
+    const int m = first + t;
+    float qv[HEAD_DIM];
+    const uint4* qrow = reinterpret_cast<const uint4*>(q + ((size_t)m * H + head) * HEAD_DIM);
+#pragma unroll
+    for (int c = 0; c < HEAD_DIM / 8; ++c) {
+        const uint4 w4 = qrow[c];
+        const uint32_t ws4[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            qv[8 * c + 2 * j] = bf16_lo(ws4[j]);
+            qv[8 * c + 2 * j + 1] = bf16_hi(ws4[j]);
+        }
+    }
+    float scores[LOCAL_MAX_T];
+    float top = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < LOCAL_MAX_T; ++j) {
+        if (j >= T) break;
+        const float* kr = ks + (j * KV + kv) * HEAD_DIM;
+        float s = 0.f;
+#pragma unroll
+        for (int d = 0; d < HEAD_DIM; ++d) s += qv[d] * kr[d];
+        scores[j] = s * a.scale;
+        top = fmaxf(top, scores[j]);
+    }
+    float total = 0.f;
+#pragma unroll
+    for (int j = 0; j < LOCAL_MAX_T; ++j) {
+        if (j >= T) break;
+        scores[j] = __expf(scores[j] - top);
+        total += scores[j];
+    }
+    const float inv = 1.0f / total;
+    uint4* orow = reinterpret_cast<uint4*>(attended + (size_t)m * H * HEAD_DIM + head * HEAD_DIM);
+#pragma unroll
+    for (int c = 0; c < HEAD_DIM / 8; ++c) {
+        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < T; ++j) {
+            const float* vr = vs + (j * KV + kv) * HEAD_DIM + 8 * c;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] += scores[j] * vr[e];
+        }
+        orow[c] = make_uint4(pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv),
+                             pack_bf16x2(o[4] * inv, o[5] * inv), pack_bf16x2(o[6] * inv, o[7] * inv));
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// local_add_norm: a wave to a token. sum = residual + the parts' sums in part order (written to
+// `sum` when given), then RMSNorm with gain g: lane l squares its hidden / 64 values in order, the
+// lanes added by a butterfly. FINAL writes the normed row in f32, else in bf16.
+template <bool FINAL>
+__global__ void __launch_bounds__(256) local_add_norm(LocalArgs a, const float* __restrict__ partial, int parts,
+                                                      const float* __restrict__ residual, float* __restrict__ sum,
+                                                      const float* __restrict__ gain, uint16_t* __restrict__ normed,
+                                                      float* __restrict__ out) {
+    const int m = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (m >= a.M) return;
+    const int K = a.hidden, per = K / WAVE;  // 16 at hidden 1024
+    float v[32];
+    const int base = lane * per;
+#pragma unroll
+    for (int e = 0; e < 32; e += 4) {
+        if (e >= per) break;
+        float4 r = *reinterpret_cast<const float4*>(residual + (size_t)m * K + base + e);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int p = 0; p < parts; ++p) {
+            const float4 s = *reinterpret_cast<const float4*>(partial + ((size_t)p * a.M_pad + m) * K + base + e);
+            acc.x += s.x;
+            acc.y += s.y;
+            acc.z += s.z;
+            acc.w += s.w;
+        }
+        v[e] = r.x + acc.x;
+        v[e + 1] = r.y + acc.y;
+        v[e + 2] = r.z + acc.z;
+        v[e + 3] = r.w + acc.w;
+        if (sum) *reinterpret_cast<float4*>(sum + (size_t)m * K + base + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
+    }
+    float squares = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+        if (e >= per) break;
+        squares += v[e] * v[e];
+    }
+    const float scale = 1.0f / sqrtf(wave_sum(squares) / (float)K + a.eps);
+#pragma unroll
+    for (int e = 0; e < 32; e += 8) {
+        if (e >= per) break;
+        float n[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) n[i] = v[e + i] * scale * gain[base + e + i];
+        if (FINAL) {
+            *reinterpret_cast<float4*>(out + (size_t)m * K + base + e) = make_float4(n[0], n[1], n[2], n[3]);
+            *reinterpret_cast<float4*>(out + (size_t)m * K + base + e + 4) = make_float4(n[4], n[5], n[6], n[7]);
+        } else {
+            *reinterpret_cast<uint4*>(normed + (size_t)m * K + base + e) =
+                make_uint4(pack_bf16x2(n[0], n[1]), pack_bf16x2(n[2], n[3]), pack_bf16x2(n[4], n[5]), pack_bf16x2(n[6], n[7]));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// local_embed: grid (hidden / 256, rows); thread n of the row: acc_f = bias[n] + sum_c W[n][c]
+// frame_f[c] in channel order, for each of the row's frames, written as tokens first + f of both
+// of the row's sequences; and the copied tokens.
+constexpr int EMBED_MAX = 1024;  // channels x frames a row's patch may hold
+
+__global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
+    __shared__ float frames[EMBED_MAX];  // [frames][channels]
+    const int row = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
+    const int C = e.channels, F = e.frames;
+    for (int i = threadIdx.x; i < C * F; i += 256) {
+        const int f = i / C, c = i % C;
+        frames[i] = e.src[((size_t)row * C + c) * F + f];
+    }
+    __syncthreads();
+    if (n >= a.hidden) return;
+    float acc[8];
+    const float b = e.bias[n];
+#pragma unroll
+    for (int f = 0; f < 8; ++f) acc[f] = b;
+    const float* wr = e.w + (size_t)n * C;
+    for (int c = 0; c < C; ++c) {
+        const float wc = wr[c];
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+            if (f < F) acc[f] += wc * frames[f * C + c];
+    }
+    const int K = a.hidden;
+    for (int s = 0; s < 2; ++s) {
+        const size_t seq0 = (size_t)(row * 2 + s) * a.T;
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+            if (f < F) e.x0[(seq0 + e.first + f) * K + n] = acc[f];
+        for (int t = 0; t < e.copies; ++t) {
+            const float* src = e.copy_src + ((size_t)(e.shared ? 0 : row * e.copies) + t) * K;
+            e.x0[(seq0 + e.copy_at + t) * K + n] = (e.guided && s > 0) ? 0.f : src[n];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// dit_euler: a workgroup to a row. The 2 frames tokens (conditional sequence, then the
+// unconditional) staged in LDS; wave w takes channels w, w + 4, ...: lane l sums hidden / 64
+// columns of each token in order, the lanes added by a butterfly. Then CFG-Zero*
+// (dit_euler.comp:81-110): alpha = <v_c, v_u> / (|v_u|^2 + 1e-8), guided = alpha v_u +
+// cfg (v_c - alpha v_u), state -= dt guided.
+constexpr int EULER_MAX_TOKENS = 8;  // 2 x frames
+constexpr int EULER_MAX_LEN = 512;   // channels x frames
+
+__global__ void __launch_bounds__(256) dit_euler(LocalArgs a, EulerArgs e) {
+    __shared__ float tok[EULER_MAX_TOKENS * 1024];
+    __shared__ float vel[2 * EULER_MAX_LEN];
+    __shared__ float red[2][4];
+    const int row = blockIdx.x, K = a.hidden, F = e.frames, C = e.channels;
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    for (int i = threadIdx.x; i < 2 * F * K; i += 256) {
+        const int tm = i / K, s = tm / F, f = tm % F;
+        tok[i] = e.out[((size_t)(row * 2 + s) * a.T + e.first + f) * K + i % K];
+    }
+    __syncthreads();
+    const int per = K / WAVE;
+    for (int c = w; c < C; c += 4) {
+        const float* wr = e.w + (size_t)c * K + lane * per;
+        float part[EULER_MAX_TOKENS];
+#pragma unroll
+        for (int tm = 0; tm < EULER_MAX_TOKENS; ++tm) part[tm] = 0.f;
+        for (int j = 0; j < per; ++j) {
+            const float wv = wr[j];
+#pragma unroll
+            for (int tm = 0; tm < EULER_MAX_TOKENS; ++tm)
+                if (tm < 2 * F) part[tm] += wv * tok[tm * K + lane * per + j];
+        }
+#pragma unroll
+        for (int tm = 0; tm < EULER_MAX_TOKENS; ++tm) {
+            if (tm >= 2 * F) break;
+            const float total = wave_sum(part[tm]);
+            if (lane == 0) vel[(tm / F) * C * F + c * F + tm % F] = total + e.bias[c];
+        }
+    }
+    __syncthreads();
+    const int len = C * F;
+    float dot = 0.f, norm = 0.f;
+    for (int i = threadIdx.x; i < len; i += 256) {
+        dot += vel[i] * vel[len + i];
+        norm += vel[len + i] * vel[len + i];
+    }
+    dot = wave_sum(dot);
+    norm = wave_sum(norm);
+    if (lane == 0) {
+        red[0][w] = dot;
+        red[1][w] = norm;
+    }
+    __syncthreads();
+    dot = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    norm = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    const float alpha = dot / (norm + 1e-8f);
+    const float cfg = e.sampling[row * 2 + 1];
+    for (int i = threadIdx.x; i < len; i += 256) {
+        const float scaled = vel[len + i] * alpha;
+        const float guided = scaled + cfg * (vel[i] - scaled);
+        e.state[(size_t)row * len + i] -= guided * e.dt;
+    }
+}
+
+__global__ void __launch_bounds__(256) cfm_noise(const float* __restrict__ noise, const float* __restrict__ sampling,
+                                                 float* __restrict__ state, int rows, int len) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < rows * len) state[i] = sampling[(i / len) * 2] * noise[i];
+}
+
+}  // namespace
+
+hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int nlayers, const float* final_norm,
+                              const LocalBuffers& b, hipStream_t stream, DispatchTimer* timer) {
+    const dim3 block(LG_THREADS);
+    const int mblocks = a.M_pad / LOCAL_TOKEN_TILE;
+    const dim3 rows4((a.M + 3) / 4);
+    const int H = a.heads, KV = a.kv_heads;
+    const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
+    // The first layer's input norm.
+    dispatch("local_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0, b.x0,
+             (float*)nullptr, layers[0].input_norm, b.normed, (float*)nullptr);
+    for (int l = 0; l < nlayers; ++l) {
+        const LocalLayer& L = layers[l];
+        const float* input = l == 0 ? b.x0 : b.x;
+        LocalGemm qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, b.q, b.k, b.v};
+        dispatch("local_qkv_rope", local_gemm<LEPI_QKV>, dim3(qkv_rows / LOCAL_ROW_TILE, mblocks), block, 0, stream, timer, a, qkv);
+        dispatch("local_attention", local_attention, dim3(a.M / a.T), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
+                 (const uint16_t*)b.k, (const uint16_t*)b.v, b.attended);
+        LocalGemm o{L.o, b.attended, H * HEAD_DIM, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
+        dispatch("local_o_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.o_parts), block, 0, stream,
+                 timer, a, o);
+        dispatch("local_o_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial, b.o_parts,
+                 input, b.h, L.post_norm, b.normed, (float*)nullptr);
+        LocalGemm gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, b.mlp, nullptr, nullptr, nullptr};
+        dispatch("local_gate_up", local_gemm<LEPI_SILU>, dim3(a.inner / 32, mblocks), block, 0, stream, timer, a, gu);
+        LocalGemm down{L.down, b.mlp, a.inner, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
+        dispatch("local_down_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.down_parts), block, 0,
+                 stream, timer, a, down);
+        if (l + 1 < nlayers)
+            dispatch("local_down_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
+                     b.down_parts, (const float*)b.h, b.x, layers[l + 1].input_norm, b.normed, (float*)nullptr);
+        else
+            dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
+                     b.down_parts, (const float*)b.h, b.x, final_norm, (uint16_t*)nullptr, b.out);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer) {
+    dispatch("local_embed", local_embed, dim3((a.hidden + 255) / 256, rows), dim3(256), 0, stream, timer, a, e);
+    return hipGetLastError();
+}
+
+hipError_t launch_dit_euler(const LocalArgs& a, const EulerArgs& e, int rows, hipStream_t stream, DispatchTimer* timer) {
+    dispatch("dit_euler", dit_euler, dim3(rows), dim3(256), 0, stream, timer, a, e);
+    return hipGetLastError();
+}
+
+hipError_t launch_cfm_noise(const float* noise, const float* sampling, float* state, int rows, int len, hipStream_t stream,
+                            DispatchTimer* timer) {
+    dispatch("cfm_noise", cfm_noise, dim3((rows * len + 255) / 256), dim3(256), 0, stream, timer, noise, sampling, state, rows, len);
+    return hipGetLastError();
+}
+
+}  // namespace tgx

@@ -1,0 +1,80 @@
+// The local stack's and the patch sampler's kernels (crates/graph/src/local/mod.rs,
+// crates/graph/src/local/dit.rs): a bidirectional MiniCPM-4 stack over sequences of a few tokens,
+// the embeddings of a patch's frames, and the Euler step with CFG-Zero* guidance.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "decode_kernels.hpp"
+#include "device.hpp"
+
+namespace tgx {
+
+// The tokens a local stack runs over: `seqs` sequences of T tokens, token m at place m % T.
+struct LocalArgs {
+    int M;      // tokens
+    int M_pad;  // rows of the token tensors, a multiple of LOCAL_TOKEN_TILE; rows past M hold zeros
+    int T;      // tokens to a sequence
+    int hidden, inner, heads, kv_heads;
+    float eps, scale;
+    int rope;
+    const float* cos;  // [T][HEAD_DIM / 2]
+    const float* sin;
+};
+
+constexpr int LOCAL_TOKEN_TILE = 128;  // the GEMM's tokens per workgroup
+constexpr int LOCAL_ROW_TILE = 64;     // the GEMM's weight rows per workgroup
+constexpr int LOCAL_MAX_T = 16;        // the longest sequence local_attention stages
+constexpr int LOCAL_MAX_PARTS = 4;
+
+struct LocalLayer {
+    const uint16_t *qkv, *o, *gate_up, *down;  // 16-row MFMA tiles, q/k/v rows RoPE-paired
+    const float *input_norm, *post_norm;
+};
+
+// The stack's tensors, [M_pad][...] each.
+struct LocalBuffers {
+    const float* x0;     // the embedded tokens, the first layer's residual
+    float *x, *h;        // the residual stream after each layer / after each attention
+    uint16_t* normed;    // bf16 [M_pad][hidden]
+    uint16_t *q, *k, *v; // bf16 [M_pad][heads | kv_heads][64]
+    uint16_t* attended;  // bf16 [M_pad][heads 64]
+    uint16_t* mlp;       // bf16 [M_pad][inner]
+    float* partial;      // f32 [LOCAL_MAX_PARTS][M_pad][hidden]
+    float* out;          // f32 [M_pad][hidden]: the last layer's output after the final norm
+    int o_parts, down_parts;
+};
+
+// A linear layer over a patch's frames, `src` [rows][channels][frames] (channel-major, as the
+// sampler keeps a patch): W f32 [hidden][channels] and bias [hidden]; the FRAMES results are
+// written as tokens `first` .. of both of the row's sequences, and `copies` tokens of `copy_src`
+// at `copy_at` (per row unless `shared`; zero in the second sequence when `guided`).
+struct EmbedArgs {
+    const float* src;
+    const float* w;
+    const float* bias;
+    const float* copy_src;
+    float* x0;
+    int channels, frames, first, copy_at, copies, guided, shared;
+};
+
+// One Euler step: velocities out_proj(out[tokens first..]) + b of the conditional and the
+// unconditional sequence, guided as CFG-Zero* guides them, and state -= dt * guided.
+struct EulerArgs {
+    const float* out;   // f32 [M_pad][hidden], the stack's output after the final norm
+    const float* w;     // f32 [channels][hidden]
+    const float* bias;  // [channels]
+    const float* sampling;  // [rows][2]: temperature, guidance scale
+    float* state;       // [rows][channels][frames]
+    int channels, frames, first;
+    float dt;
+};
+
+hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int nlayers, const float* final_norm,
+                              const LocalBuffers& b, hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_dit_euler(const LocalArgs& a, const EulerArgs& e, int rows, hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_cfm_noise(const float* noise, const float* sampling, float* state, int rows, int len,
+                            hipStream_t stream, DispatchTimer* timer);
+
+}  // namespace tgx

@@ -1,0 +1,106 @@
+// The host side of what runs around the LMs for each patch: the patch sampler over the local
+// DiT (crates/graph/src/local/dit.rs) and the LM side (crates/graph/src/lm_side.rs).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "heads_kernels.hpp"
+#include "local_kernels.hpp"
+#include "runtime.hpp"
+
+namespace tgx {
+
+// The condition tokens leading the DiT's sequence (dit.rs:36), and where the time token and the
+// patch before start (dit.rs:40-41).
+constexpr int MU_TOKENS = 2;
+constexpr int TIME_AT = MU_TOKENS;
+constexpr int COND_AT = TIME_AT + 1;
+
+// schedule and euler_steps (dit.rs:44-79) in f32: the (t, dt) of each DiT evaluation.
+std::vector<float> euler_schedule(int timesteps);
+void euler_steps(int timesteps, std::vector<float>& t, std::vector<float>& dt);
+
+// A timestep embedding's MLP, linear_2(SiLU(linear_1(x))), in f64 on the host (dit.rs:390-422).
+struct TimeMlp {
+    std::vector<double> w1, b1, w2, b2;
+    int loaded = 0;  // a bit per tensor
+    std::vector<double> forward(const std::vector<double>& x, int hidden) const;
+};
+
+struct Sampler {
+    Context* ctx = nullptr;
+    Shape shape{};  // the DiT's stack; capacity = T
+    int feat = 0, frames = 0, timesteps = 0, rows = 0;
+    int T = 0, M = 0, M_pad = 0, o_parts = 2, down_parts = 4;
+    std::vector<float> step_t, step_dt;
+    std::vector<DeviceBuffer> allocations;
+    size_t device_bytes = 0;
+    std::vector<Layer> layers;
+    float* final_norm = nullptr;
+    float *in_w = nullptr, *in_b = nullptr, *cond_w = nullptr, *cond_b = nullptr, *out_w = nullptr, *out_b = nullptr;
+    float* time_tokens = nullptr;  // [steps][hidden]
+    bool times_dirty = true;
+    TimeMlp time_mlp, delta_mlp;
+    float *cos = nullptr, *sin = nullptr;
+    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr;
+    uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
+    float *mu = nullptr, *cond = nullptr, *noise = nullptr, *state = nullptr, *sampling = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool exec_dirty = true;
+    int dispatches = 0;
+    hipEvent_t ev_start = nullptr, ev_end = nullptr;
+    bool pending = false, timed = false, use_graph = true;
+    DispatchTimer timer;
+    std::vector<hipEvent_t> timer_start, timer_stop;
+    std::vector<const char*> timer_labels;
+
+    LocalArgs args() const;
+};
+
+tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_shape* patch, Sampler** out);
+void sampler_destroy(Sampler* s);
+tgx_status sampler_load(Sampler* s, const char* name, const void* data, tgx_dtype dtype, size_t count);
+// Copies the inputs in (mu [rows][MU_TOKENS][hidden], cond / noise [rows][feat][frames],
+// sampling [rows][2]); any may be null to keep what the device holds.
+tgx_status sampler_set_inputs(Sampler* s, const float* mu, const float* cond, const float* noise, const float* sampling);
+tgx_status sampler_launch(Sampler* s, int times);
+tgx_status sampler_wait(Sampler* s);
+tgx_status sampler_read(Sampler* s, float* patch);
+// The sample's dispatches on the context's stream (timed when `timer`), mu read from `mu`.
+hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, int* dispatches);
+tgx_status sampler_prepare(Sampler* s);
+
+// The LM side: both LMs' decoders, the heads, and the tensors between them.
+struct Linear {
+    uint16_t* w = nullptr;  // 16-row tiles of [N_pad][K]
+    float* b = nullptr;     // [N]
+    int N = 0, K = 0;
+};
+
+struct LmSide {
+    Context* ctx = nullptr;
+    Decoder* base = nullptr;
+    Decoder* residual = nullptr;
+    int rows = 0, hidden = 0, encoder = 0, dit = 0, latent = 0, levels = 0;
+    std::vector<DeviceBuffer> allocations;
+    Linear enc_to_lm, fsq_in, fsq_out, fusion, lm_to_dit, res_to_dit, stop_proj, stop_head;
+    float *enc = nullptr, *levels_out = nullptr, *lm_hidden = nullptr, *stop_hidden = nullptr;
+    float *mu = nullptr, *stop_logits = nullptr;
+    hipGraphExec_t exec = nullptr, advance_exec = nullptr;
+    int dispatches = 0;
+    hipEvent_t ev_start = nullptr, ev_end = nullptr;
+    bool pending = false, use_graph = true;
+};
+
+tgx_status lm_side_create(Context* ctx, const tgx_shape* base, const tgx_shape* residual, const tgx_batch* batch,
+                          const tgx_heads_shape* heads, LmSide** out);
+void lm_side_destroy(LmSide* s);
+tgx_status lm_side_load(LmSide* s, const char* name, const void* data, tgx_dtype dtype, size_t count);
+tgx_status lm_side_set_rows(LmSide* s, const tgx_row* rows, int nrows, const float* enc);
+tgx_status lm_side_launch(LmSide* s, int times, int advance);
+tgx_status lm_side_wait(LmSide* s);
+tgx_status lm_side_read(LmSide* s, const char* tensor, float* out, size_t count);
+hipError_t lm_side_enqueue(LmSide* s, int advance, DispatchTimer* timer, int* dispatches);
+
+}  // namespace tgx

@@ -12,8 +12,8 @@
 //                      workgroup, keys and values staged through LDS a 64-position block at a time
 //                      with an online softmax (attention_rows.comp)
 #include "prefill_kernels.hpp"
+#include "dispatch.hpp"
 
-#include <hip/hip_ext.h>
 #include <math.h>
 
 namespace tgx {
@@ -449,17 +449,6 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
     }
 }
 
-template <typename... KernelArgs, typename... Args>
-void dispatch(const char* label, void (*kernel)(KernelArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
-              DispatchTimer* timer, Args... args) {
-    if (timer && timer->used < timer->capacity) {
-        const int i = timer->used++;
-        timer->labels[i] = label;
-        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, timer->start[i], timer->stop[i], 0, args...);
-    } else {
-        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
-    }
-}
 
 constexpr size_t GEMM_LDS = (size_t)2 * (W_STAGE + X_STAGE) * sizeof(uint4);
 

@@ -8,6 +8,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <thread>
 
 namespace tgx {
@@ -410,6 +411,10 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
 
 }  // namespace
 
+hipError_t decoder_enqueue(Decoder* d, int advance, DispatchTimer* timer, int* dispatches) {
+    return enqueue_step(d, advance, timer, dispatches);
+}
+
 tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions) {
     const int need = (int)((positions + BLOCK_TOKENS - 1) / BLOCK_TOKENS);
     while (d->slot_blocks[slot] < need) {
@@ -471,8 +476,6 @@ void decoder_destroy(Decoder* d) {
     delete d;
 }
 
-namespace {
-
 // The weight's values as f32, `count` of `dtype`.
 std::vector<float> as_f32(const void* data, tgx_dtype dtype, size_t count) {
     std::vector<float> v(count);
@@ -485,9 +488,8 @@ std::vector<float> as_f32(const void* data, tgx_dtype dtype, size_t count) {
     return v;
 }
 
-// W [n][k] into MFMA tiles of R-row strips, rows taken through `row_of` (strip, r) -> source row.
-template <typename RowOf>
-std::vector<uint16_t> tile(const std::vector<float>& w, int n, int k, int R, RowOf row_of) {
+std::vector<uint16_t> tile_rows(const std::vector<float>& w, int n, int k, int R,
+                                const std::function<int(int, int)>& row_of) {
     std::vector<uint16_t> t((size_t)n * k);
     const int kblocks = k / 32;
     for (int strip = 0; strip < n / R; ++strip)
@@ -504,73 +506,71 @@ std::vector<uint16_t> tile(const std::vector<float>& w, int n, int k, int R, Row
     return t;
 }
 
-}  // namespace
-
-tgx_status decoder_load(Decoder* d, const char* name, const void* data, tgx_dtype dtype, size_t count) {
-    if (!d || !name || !data) return fail(TGX_E_ARG, "null decoder, name or data");
-    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
-    if (dtype != TGX_F32 && dtype != TGX_BF16 && dtype != TGX_F16) return fail(TGX_E_ARG, "dtype");
-    const Shape& s = d->shape;
+tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, const std::string& what,
+                             const void* data, tgx_dtype dtype, size_t count, int R) {
     const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads;
     const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
-    std::string n = name;
     auto want = [&](size_t expect) -> tgx_status {
         if (count != expect)
-            return fail(TGX_E_WEIGHTS, n + ": " + std::to_string(count) + " values, not " + std::to_string(expect));
+            return fail(TGX_E_WEIGHTS, name + ": " + std::to_string(count) + " values, not " + std::to_string(expect));
         return TGX_OK;
     };
     auto upload = [&](void* dst, const void* src, size_t bytes) -> tgx_status {
         TGX_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
         return TGX_OK;
     };
-    if (n == "norm") {
+    if (what == "input_layernorm" || what == "post_attention_layernorm") {
         TGX_TRY(want(h));
         auto v = as_f32(data, dtype, count);
-        return upload(d->final_norm, v.data(), (size_t)h * 4);
+        return upload(what == "input_layernorm" ? L.input_norm : L.post_norm, v.data(), (size_t)h * 4);
+    }
+    if (what == "qkv_proj") {
+        TGX_TRY(want((size_t)qkv_rows * h));
+        auto t = tile_rows(as_f32(data, dtype, count), qkv_rows, h, R,
+                           [R](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM, R); });
+        return upload(L.qkv, t.data(), t.size() * 2);
+    }
+    auto plain = [R](int strip, int r) { return strip * R + r; };
+    if (what == "o_proj") {
+        TGX_TRY(want((size_t)h * H * HEAD_DIM));
+        auto t = tile_rows(as_f32(data, dtype, count), h, H * HEAD_DIM, R, plain);
+        return upload(L.o, t.data(), t.size() * 2);
+    }
+    if (what == "gate_up_proj") {
+        TGX_TRY(want((size_t)2 * I * h));
+        auto t = tile_rows(as_f32(data, dtype, count), 2 * I, h, 16, [](int strip, int r) { return strip * 16 + r; });
+        return upload(L.gate_up, t.data(), t.size() * 2);
+    }
+    if (what == "down_proj") {
+        TGX_TRY(want((size_t)h * I));
+        auto t = tile_rows(as_f32(data, dtype, count), h, I, R, plain);
+        return upload(L.down, t.data(), t.size() * 2);
+    }
+    return fail(TGX_E_WEIGHTS, name + ": no such tensor");
+}
+
+tgx_status decoder_load(Decoder* d, const char* name, const void* data, tgx_dtype dtype, size_t count) {
+    if (!d || !name || !data) return fail(TGX_E_ARG, "null decoder, name or data");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (dtype != TGX_F32 && dtype != TGX_BF16 && dtype != TGX_F16) return fail(TGX_E_ARG, "dtype");
+    const Shape& s = d->shape;
+    std::string n = name;
+    if (n == "norm") {
+        if (count != (size_t)s.hidden)
+            return fail(TGX_E_WEIGHTS, n + ": " + std::to_string(count) + " values, not " + std::to_string(s.hidden));
+        auto v = as_f32(data, dtype, count);
+        TGX_HIP(hipMemcpy(d->final_norm, v.data(), (size_t)s.hidden * 4, hipMemcpyHostToDevice));
+        return TGX_OK;
     }
     int l = -1;
     char what[128] = {0};
     if (std::sscanf(name, "layers.%d.%127s", &l, what) != 2 || l < 0 || l >= s.layers)
         return fail(TGX_E_WEIGHTS, n + ": no such tensor in a stack of " + std::to_string(s.layers) + " layers");
-    std::string w = what;
-    Layer& L = d->layers[l];
-    if (w == "input_layernorm" || w == "post_attention_layernorm") {
-        TGX_TRY(want(h));
-        auto v = as_f32(data, dtype, count);
-        return upload(w == "input_layernorm" ? L.input_norm : L.post_norm, v.data(), (size_t)h * 4);
-    }
-    if (w == "qkv_proj") {
-        TGX_TRY(want((size_t)qkv_rows * h));
-        auto v = as_f32(data, dtype, count);
-        const int R = d->strip_rows;
-        auto t = tile(v, qkv_rows, h, R, [R](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM, R); });
-        return upload(L.qkv, t.data(), t.size() * 2);
-    }
-    if (w == "o_proj") {
-        TGX_TRY(want((size_t)h * H * HEAD_DIM));
-        auto v = as_f32(data, dtype, count);
-        const int R = d->strip_rows;
-        auto t = tile(v, h, H * HEAD_DIM, R, [R](int strip, int r) { return strip * R + r; });
-        return upload(L.o, t.data(), t.size() * 2);
-    }
-    if (w == "gate_up_proj") {
-        TGX_TRY(want((size_t)2 * I * h));
-        auto v = as_f32(data, dtype, count);
-        auto t = tile(v, 2 * I, h, 16, [](int strip, int r) { return strip * 16 + r; });
-        return upload(L.gate_up, t.data(), t.size() * 2);
-    }
-    if (w == "down_proj") {
-        TGX_TRY(want((size_t)h * I));
-        auto v = as_f32(data, dtype, count);
-        const int R = d->strip_rows;
-        auto t = tile(v, h, I, R, [R](int strip, int r) { return strip * R + r; });
-        return upload(L.down, t.data(), t.size() * 2);
-    }
-    return fail(TGX_E_WEIGHTS, n + ": no such tensor");
+    return load_layer_tensor(d->layers[l], s, n, what, data, dtype, count, d->strip_rows);
 }
 
-tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const float* x) {
-    if (!d || !rows || !x) return fail(TGX_E_ARG, "null decoder, rows or x");
+tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {
+    if (!d || !rows) return fail(TGX_E_ARG, "null decoder or rows");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (nrows != d->rows)
         return fail(TGX_E_SHAPE, std::to_string(nrows) + " rows for a batch of " + std::to_string(d->rows));
@@ -582,13 +582,21 @@ tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const fl
         TGX_TRY(hold_slot(d, r.slot, r.position + 1));
     }
     std::memcpy(d->placement_host, words.data(), words.size() * 4);
-    std::memcpy(d->x_host, x, (size_t)nrows * d->shape.hidden * 4);
     hipStream_t s = d->ctx->stream;
     TGX_TRY(sync_slots(d));
-    TGX_HIP(hipMemcpyAsync(d->x_in, d->x_host, (size_t)nrows * d->shape.hidden * 4, hipMemcpyHostToDevice, s));
     TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
     TGX_HIP(hipMemcpyAsync(d->slot_of_row, d->placement_host + nrows, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
-    // The pinned buffers may not change until the copies have gone.
+    // The pinned buffer may not change until the copies have gone.
+    TGX_HIP(hipStreamSynchronize(s));
+    return TGX_OK;
+}
+
+tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const float* x) {
+    if (!d || !rows || !x) return fail(TGX_E_ARG, "null decoder, rows or x");
+    TGX_TRY(decoder_place(d, rows, nrows));
+    std::memcpy(d->x_host, x, (size_t)nrows * d->shape.hidden * 4);
+    hipStream_t s = d->ctx->stream;
+    TGX_HIP(hipMemcpyAsync(d->x_in, d->x_host, (size_t)nrows * d->shape.hidden * 4, hipMemcpyHostToDevice, s));
     TGX_HIP(hipStreamSynchronize(s));
     return TGX_OK;
 }

@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -113,6 +114,10 @@ tgx_status decoder_create(Context* ctx, const tgx_shape* shape, const tgx_batch*
 void decoder_destroy(Decoder* dec);
 tgx_status decoder_load(Decoder* dec, const char* name, const void* data, tgx_dtype dtype, size_t count);
 tgx_status decoder_set_rows(Decoder* dec, const tgx_row* rows, int nrows, const float* x);
+// set_rows without the input: places the rows (positions, slots, blocks) alone.
+tgx_status decoder_place(Decoder* dec, const tgx_row* rows, int nrows);
+// The step's dispatches on the context's stream, reading x_in and writing out.
+hipError_t decoder_enqueue(Decoder* d, int advance, DispatchTimer* timer, int* dispatches);
 tgx_status decoder_start(Decoder* dec);
 tgx_status decoder_wait(Decoder* dec);
 tgx_status decoder_output(Decoder* dec, float* out);
@@ -128,6 +133,15 @@ tgx_status prefill_launch(Decoder* d, int times);
 void prefill_release(Decoder* d);
 tgx_status decoder_timings(Decoder* d, int max, tgx_timing* out, int* n);
 tgx_status decoder_read_cache(Decoder* dec, uint32_t slot, uint32_t positions, float* k, float* v);
+
+// A weight's values as f32; W [n][k] in MFMA tiles of R-row strips, rows through `row_of`
+// (strip, r) -> source row; and one layer's tensor `what` of a stack ("qkv_proj", "o_proj",
+// "gate_up_proj", "down_proj", "input_layernorm", "post_attention_layernorm").
+std::vector<float> as_f32(const void* data, tgx_dtype dtype, size_t count);
+std::vector<uint16_t> tile_rows(const std::vector<float>& w, int n, int k, int R,
+                                const std::function<int(int, int)>& row_of);
+tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, const std::string& what,
+                             const void* data, tgx_dtype dtype, size_t count, int R);
 
 // f32 <- bf16 / f16 bits; f32 -> bf16 bits, rounding to nearest even.
 float bf16_to_f32(uint16_t h);

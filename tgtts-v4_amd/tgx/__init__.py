@@ -83,6 +83,14 @@ class _Run(ctypes.Structure):
     _fields_ = [("slot", ctypes.c_uint32), ("start", ctypes.c_uint32), ("len", ctypes.c_uint32)]
 
 
+class _PatchShape(ctypes.Structure):
+    _fields_ = [("feat_dim", ctypes.c_int), ("patch_size", ctypes.c_int), ("timesteps", ctypes.c_int), ("rows", ctypes.c_int)]
+
+
+class _HeadsShape(ctypes.Structure):
+    _fields_ = [("encoder", ctypes.c_int), ("dit", ctypes.c_int), ("latent", ctypes.c_int), ("levels", ctypes.c_int)]
+
+
 class _Timing(ctypes.Structure):
     _fields_ = [("label", ctypes.c_char * 32), ("ms", ctypes.c_float)]
 
@@ -129,12 +137,35 @@ EXPORTS = [
     "tgx_prefill_run",
     "tgx_prefill_runs",
     "tgx_prefill_launch",
+    "tgx_euler_steps",
+    "tgx_sampler_create",
+    "tgx_sampler_destroy",
+    "tgx_sampler_load",
+    "tgx_sampler_sample",
+    "tgx_sampler_launch",
+    "tgx_sampler_wait",
+    "tgx_sampler_elapsed_ms",
+    "tgx_sampler_set_timed",
+    "tgx_sampler_timings",
+    "tgx_sampler_dispatches",
+    "tgx_lm_side_create",
+    "tgx_lm_side_destroy",
+    "tgx_lm_side_load",
+    "tgx_lm_side_decoder",
+    "tgx_lm_side_set_rows",
+    "tgx_lm_side_step",
+    "tgx_lm_side_launch",
+    "tgx_lm_side_wait",
+    "tgx_lm_side_elapsed_ms",
+    "tgx_lm_side_read",
+    "tgx_lm_side_dispatches",
 ]
 
 _lib: Optional[ctypes.CDLL] = None
 
 # Every open handle, closed before the interpreter exits: the HIP runtime tears itself down in the
-# C library's exit handlers, after which no handle may be freed. Decoders go before contexts.
+# C library's exit handlers, after which no handle may be freed. Decoders, samplers and LM sides
+# (everything made from a context) go before contexts.
 _open_decoders: "weakref.WeakSet" = weakref.WeakSet()
 _open_contexts: "weakref.WeakSet" = weakref.WeakSet()
 
@@ -187,6 +218,32 @@ def library() -> ctypes.CDLL:
     lib.tgx_prefill_run.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, P, P]
     lib.tgx_prefill_runs.argtypes = [P, ctypes.POINTER(_Run), ctypes.c_int, P, P]
     lib.tgx_prefill_launch.argtypes = [P, ctypes.c_int]
+    FP = ctypes.POINTER(ctypes.c_float)
+    lib.tgx_euler_steps.argtypes = [ctypes.c_int, ctypes.c_int, FP, FP, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_sampler_create.argtypes = [P, ctypes.POINTER(_Shape), ctypes.POINTER(_PatchShape), ctypes.POINTER(P)]
+    lib.tgx_sampler_destroy.argtypes = [P]
+    lib.tgx_sampler_destroy.restype = None
+    lib.tgx_sampler_load.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int, ctypes.c_size_t]
+    lib.tgx_sampler_sample.argtypes = [P, P, P, P, P, P]
+    lib.tgx_sampler_launch.argtypes = [P, ctypes.c_int]
+    lib.tgx_sampler_wait.argtypes = [P]
+    lib.tgx_sampler_elapsed_ms.argtypes = [P, FP]
+    lib.tgx_sampler_set_timed.argtypes = [P, ctypes.c_int]
+    lib.tgx_sampler_timings.argtypes = [P, ctypes.c_int, ctypes.POINTER(_Timing), ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_sampler_dispatches.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_lm_side_create.argtypes = [P, ctypes.POINTER(_Shape), ctypes.POINTER(_Shape), ctypes.POINTER(_Batch),
+                                       ctypes.POINTER(_HeadsShape), ctypes.POINTER(P)]
+    lib.tgx_lm_side_destroy.argtypes = [P]
+    lib.tgx_lm_side_destroy.restype = None
+    lib.tgx_lm_side_load.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int, ctypes.c_size_t]
+    lib.tgx_lm_side_decoder.argtypes = [P, ctypes.c_int, ctypes.POINTER(P)]
+    lib.tgx_lm_side_set_rows.argtypes = [P, ctypes.POINTER(_Row), ctypes.c_int, P]
+    lib.tgx_lm_side_step.argtypes = [P, ctypes.POINTER(_Row), ctypes.c_int, P, P, P]
+    lib.tgx_lm_side_launch.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    lib.tgx_lm_side_wait.argtypes = [P]
+    lib.tgx_lm_side_elapsed_ms.argtypes = [P, FP]
+    lib.tgx_lm_side_read.argtypes = [P, ctypes.c_char_p, P, ctypes.c_size_t]
+    lib.tgx_lm_side_dispatches.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:
         if name.startswith("tgx_") and name not in ("tgx_last_error",):
             fn = getattr(lib, name)
@@ -194,6 +251,8 @@ def library() -> ctypes.CDLL:
                 fn.restype = ctypes.c_int
     lib.tgx_context_destroy.restype = None
     lib.tgx_decoder_destroy.restype = None
+    lib.tgx_sampler_destroy.restype = None
+    lib.tgx_lm_side_destroy.restype = None
     _lib = lib
     return lib
 

@@ -144,3 +144,59 @@ def stack_weights(spec: StackSpec) -> dict:
 def embeddings(seed: int, name: str, rows: int, hidden: int) -> np.ndarray:
     """Seeded N(0, 1) hidden states [rows][hidden] in float32."""
     return normal(seed, name, rows * hidden).astype(np.float32).reshape(rows, hidden)
+
+
+def linear_layer(seed: int, name: str, n: int, k: int, std: float = 0.02, bias: bool = True, dtype: str = "bf16") -> dict:
+    """A linear layer's weight [n][k] and bias [n], N(0, std), bf16-rounded when dtype is "bf16"."""
+    out = {}
+    w = (np.float32(std) * normal(seed, f"{name}.weight", n * k, np.float32)).astype(np.float32).reshape(n, k)
+    out[f"{name}.weight"] = bf16_round(w) if dtype == "bf16" else w
+    if bias:
+        b = (np.float32(std) * normal(seed, f"{name}.bias", n, np.float32)).astype(np.float32)
+        out[f"{name}.bias"] = bf16_round(b) if dtype == "bf16" else b
+    return out
+
+
+@lru_cache(maxsize=4)
+def sampler_weights(stack: StackSpec, feat_dim: int = 64) -> dict:
+    """The local DiT's tensors by the names Sampler.load takes: the stack's, in_proj and cond_proj
+    ([hidden][feat_dim]), out_proj ([feat_dim][hidden]) and the two time MLPs."""
+    out = dict(stack_weights(stack))
+    h, s = stack.hidden, stack.seed
+    out.update(linear_layer(s, "in_proj", h, feat_dim, dtype=stack.dtype))
+    out.update(linear_layer(s, "cond_proj", h, feat_dim, dtype=stack.dtype))
+    out.update(linear_layer(s, "out_proj", feat_dim, h, dtype=stack.dtype))
+    for m in ("time_mlp", "delta_time_mlp"):
+        out.update(linear_layer(s, f"{m}.linear_1", h, h, dtype=stack.dtype))
+        out.update(linear_layer(s, f"{m}.linear_2", h, h, dtype=stack.dtype))
+    return out
+
+
+HEADS = (
+    # name, out, in (as multiples of: h hidden, e encoder, d dit, l latent), bias
+    ("enc_to_lm_proj", "h", "e", True),
+    ("fsq_layer.in_proj", "l", "h", True),
+    ("fsq_layer.out_proj", "h", "l", True),
+    ("fusion_concat_proj", "h", "2h", True),
+    ("lm_to_dit_proj", "d", "h", True),
+    ("res_to_dit_proj", "d", "h", True),
+    ("stop_proj", "h", "h", True),
+    ("stop_head", "2", "h", False),
+)
+
+
+def heads_weights(seed: int, hidden: int, encoder: int, dit: int, latent: int, dtype: str = "bf16") -> dict:
+    """The layers between the LMs (lm_side.rs:113-141), N(0, 0.02)."""
+    size = {"h": hidden, "e": encoder, "d": dit, "l": latent, "2h": 2 * hidden, "2": 2}
+    out = {}
+    for name, n, k, bias in HEADS:
+        out.update(linear_layer(seed, name, size[n], size[k], bias=bias, dtype=dtype))
+    return out
+
+
+def lm_side_weights(base: StackSpec, residual: StackSpec, encoder: int, dit: int, latent: int) -> dict:
+    """Every tensor of the LM side by the names LmSide.load takes."""
+    out = {f"base_lm.{k}": v for k, v in stack_weights(base).items()}
+    out.update({f"residual_lm.{k}": v for k, v in stack_weights(residual).items()})
+    out.update(heads_weights(base.seed + 7, base.hidden, encoder, dit, latent, base.dtype))
+    return out
