@@ -11,7 +11,10 @@ Beside it on the same JSON line:
 - "roofline": the dominant kernel of the step, its algorithmic bytes per launch over its average
   duration from per-dispatch HIP events (each recorded by the kernel's own dispatch);
 - "cpu_baseline": the fp32 CPU path (the oracle, OpenMP over the host's cores) on a bounded
-  sample of the same workload.
+  sample of the same workload;
+- "prefill": 8 runs of 2048 positions at once, tok/s and the GEMMs' share of bf16 MFMA peak;
+- "tts_step": the full per-patch pipeline at 16 requests (LM side with both LMs, then the LocDiT
+  sampler's 10 Euler steps with guidance), patch steps per second.
 """
 
 from __future__ import annotations
@@ -240,6 +243,74 @@ def run_prefill(ctx, weights, count: int, length: int, times: int, decode_steps:
     }
 
 
+def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
+    """The full per-patch pipeline at `rows` requests: the LM side (the 24-layer backbone and the
+    8-layer residual LM without RoPE, with the heads between them) and the sampler (a 4-layer
+    LocDiT, 10 Euler steps with CFG-Zero* guidance 2.0 over both sequences of every row) on its
+    mu, `steps` patch steps, each request's caches filled to `context` positions first."""
+    import tgx
+    from tgx.patch import HeadsShape, LmSide, PatchShape, Sampler, patch_elapsed_ms, patch_launch
+    from tgx.synth import StackSpec, embeddings, lm_side_weights, sampler_weights
+
+    # Positions run on through the warm-up, the timed steps and the LM side's steps alone.
+    reach = context + warmup + 2 * steps + 2
+    capacity = int(np.ceil(reach / 256.0) * 256)
+    base = tgx.Shape(layers=24, capacity=capacity)
+    residual = tgx.Shape(layers=8, capacity=capacity, rope=False)
+    heads = HeadsShape(1024, 1024, 256, 9)
+    side = LmSide(ctx, base, residual, tgx.Batch(rows=rows, slots=rows), heads)
+    side.load_all(lm_side_weights(StackSpec(layers=24, seed=0), StackSpec(layers=8, seed=1), 1024, 1024, 256))
+    dit = StackSpec(layers=4, seed=2)
+    sampler = Sampler(ctx, tgx.Shape(layers=4, capacity=16), PatchShape(64, 4, 10, rows))
+    sampler.load_all(sampler_weights(dit, 64))
+    for which in (0, 1):
+        d = side.decoder(which)
+        d.prefill_runs([(r, 0, context) for r in range(rows)], embeddings(12 + which, "tts.prompt", rows * context, 1024))
+        for r in range(rows):
+            d.reserve(r, reach)
+    rng = np.random.default_rng(5)
+    sampling = np.array([[1.0, 2.0]] * rows, dtype=np.float32)
+    cond = rng.standard_normal((rows, 64, 4)).astype(np.float32)
+    noise = rng.standard_normal((rows, 64, 4)).astype(np.float32)
+    mu = np.zeros((rows, 2, 1024), dtype=np.float32)
+    sampler.sample(mu, cond, noise, sampling)  # inputs in place, the graph recorded
+    side.set_rows([tgx.Row(context, r) for r in range(rows)], embeddings(14, "tts.enc", rows, 1024))
+    patch_launch(side, sampler, warmup)
+    side.wait()
+    t0 = time.perf_counter()
+    patch_launch(side, sampler, steps)
+    side.wait()
+    wall = time.perf_counter() - t0
+    gpu = patch_elapsed_ms(side)
+    # The two halves alone, for the split.
+    side.launch(steps, advance=True)
+    side.wait()
+    side_ms = side.elapsed_ms() / steps
+    sampler.launch(steps)
+    sampler.wait()
+    sampler_ms = sampler.elapsed_ms() / steps
+    dispatches = side.dispatches() + sampler.dispatches()
+    side.close()
+    sampler.close()
+    # Algorithmic bytes: every weight once a step (the DiT's once per Euler evaluation).
+    dit_bytes = dit.layers * (tgx.Shape(layers=1).weight_bytes() - 2 * 1024) + 2 * 1024
+    lm_bytes = base.weight_bytes() + residual.weight_bytes()
+    return {
+        "workload": f"{rows} requests: 24-layer backbone + 8-layer residual LM (no RoPE) + heads, then a 4-layer "
+                    f"LocDiT over 4 x 64 latents, 10 Euler steps (9 DiT evaluations) with CFG-Zero* 2.0; contexts "
+                    f"from {context}",
+        "rows": rows,
+        "steps": steps,
+        "steps_per_s": steps / wall,
+        "ms_per_step": wall * 1e3 / steps,
+        "gpu_ms_per_step": gpu / steps,
+        "lm_side_ms": side_ms,
+        "sampler_ms": sampler_ms,
+        "dispatches_per_step": dispatches + 1,
+        "weight_bytes_per_step": lm_bytes + 9 * dit_bytes,
+    }
+
+
 def cpu_baseline(weights, seconds: float):
     """The fp32 CPU path (the oracle in float32, OpenMP over the host's cores) on the same
     24-layer stack at batch 1, decode steps from position 256 of a zero-filled cache."""
@@ -308,6 +379,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the batch-16/64 runs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 8 x 2048 prefill")
+    ap.add_argument("--no-tts", action="store_true", help="skip the full per-patch pipeline at 16 requests")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 256 MiB five times (scales rocprofv3's HBM counters)")
@@ -383,6 +455,13 @@ def main() -> int:
             "kernels_us": {k: round(v["avg_us"], 2) for k, v in pf["kernels"].items()},
         }
 
+    tts = None
+    if not args.no_tts:
+        tts = run_tts(ctx, 16, 30, 3)
+        log(f"tts step at 16 requests: {tts['steps_per_s']:.1f} patch steps/s ({tts['ms_per_step']:.2f} ms; LM side "
+            f"{tts['lm_side_ms']:.2f} ms, sampler {tts['sampler_ms']:.2f} ms)")
+        tts = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in tts.items()}
+
     # The roofline of the step's dominant kernel: the one with the most time per step.
     dom_label, dom = max(head["kernels"].items(), key=lambda kv: kv[1]["per_step_us"])
     achieved = dom["bytes_per_launch"] / (dom["avg_us"] * 1e-6) / 1e9
@@ -435,6 +514,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "batches": batches,
         "prefill": prefill,
+        "tts_step": tts,
         "kernels_us": {k: round(v["avg_us"], 3) for k, v in head["kernels"].items()},
         "device": {"name": report["name"], "arch": report["arch"], "clock_khz": report["clock_khz"]},
     }

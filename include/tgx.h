@@ -304,6 +304,17 @@ tgx_status tgx_lm_side_elapsed_ms(const tgx_lm_side* s, float* out);
 tgx_status tgx_lm_side_read(tgx_lm_side* s, const char* tensor, float* out, size_t count);
 tgx_status tgx_lm_side_dispatches(const tgx_lm_side* s, int* out);
 
+/* ---- a patch step: the LM side, then the sampler on its mu (crates/graph/src/patch.rs) ---- */
+
+/* Launches `times` patch steps back to back on the context's stream over what the devices hold:
+ * each runs the LM side with advance (every placed row moves on a position) and the sampler on
+ * the LM side's mu, copied on the device (PatchStep's order, patch.rs:356-415, without the local
+ * encoder: each step's `enc` stays as last set). The two must share a context and a row count,
+ * and the sampler's width must be the LM side's DiT width. tgx_lm_side_wait waits; the time is
+ * tgx_patch_elapsed_ms's. */
+tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times);
+tgx_status tgx_patch_elapsed_ms(const tgx_lm_side* side, float* out);
+
 #ifdef __cplusplus
 }
 #endif

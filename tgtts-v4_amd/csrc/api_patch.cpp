@@ -2,6 +2,7 @@
 // error message, and nothing else.
 #include <cmath>
 #include <cstdio>
+#include <string>
 
 #include "handles.hpp"
 
@@ -198,5 +199,41 @@ tgx_status tgx_lm_side_dispatches(const tgx_lm_side* s, int* out) {
     *out = s->s->dispatches;
     return TGX_OK;
 }
+
+// ---- a patch step ----
+
+tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times) {
+    clear_error();
+    if (!side || !sampler) return fail(TGX_E_ARG, "null LM side or sampler");
+    LmSide* l = side->s;
+    Sampler* s = sampler->s;
+    if (l->ctx != s->ctx) return fail(TGX_E_ARG, "the LM side and the sampler are on different contexts");
+    if (l->rows != s->rows || l->dit != s->shape.hidden)
+        return fail(TGX_E_SHAPE, "an LM side of " + std::to_string(l->rows) + " rows and mu of " + std::to_string(l->dit) +
+                                     " wide for a sampler of " + std::to_string(s->rows) + " rows " + std::to_string(s->shape.hidden) + " wide");
+    if (times <= 0) return fail(TGX_E_ARG, "times");
+    if (l->pending || s->pending) return fail(TGX_E_BUSY, "a step is under way");
+    TGX_TRY(sampler_prepare(s));
+    // The sampler's graph is recorded on its first launch; launch it once alone first if need be.
+    if (s->exec_dirty) {
+        TGX_TRY(sampler_launch(s, 1));
+        TGX_TRY(sampler_wait(s));
+    }
+    hipStream_t st = l->ctx->stream;
+    TGX_TRY(sync_slots(l->base));
+    TGX_TRY(sync_slots(l->residual));
+    const size_t mu_bytes = (size_t)l->rows * 2 * l->dit * 4;
+    TGX_HIP(hipEventRecord(l->ev_start, st));
+    for (int i = 0; i < times; ++i) {
+        TGX_HIP(hipGraphLaunch(l->advance_exec, st));
+        TGX_HIP(hipMemcpyAsync(s->mu, l->mu, mu_bytes, hipMemcpyDeviceToDevice, st));
+        TGX_HIP(hipGraphLaunch(s->exec, st));
+    }
+    TGX_HIP(hipEventRecord(l->ev_end, st));
+    l->pending = true;
+    return TGX_OK;
+}
+
+tgx_status tgx_patch_elapsed_ms(const tgx_lm_side* side, float* out) { return tgx_lm_side_elapsed_ms(side, out); }
 
 }  // extern "C"

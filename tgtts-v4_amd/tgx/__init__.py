@@ -159,6 +159,8 @@ EXPORTS = [
     "tgx_lm_side_elapsed_ms",
     "tgx_lm_side_read",
     "tgx_lm_side_dispatches",
+    "tgx_patch_launch",
+    "tgx_patch_elapsed_ms",
 ]
 
 _lib: Optional[ctypes.CDLL] = None
@@ -244,6 +246,8 @@ def library() -> ctypes.CDLL:
     lib.tgx_lm_side_elapsed_ms.argtypes = [P, FP]
     lib.tgx_lm_side_read.argtypes = [P, ctypes.c_char_p, P, ctypes.c_size_t]
     lib.tgx_lm_side_dispatches.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_patch_launch.argtypes = [P, P, ctypes.c_int]
+    lib.tgx_patch_elapsed_ms.argtypes = [P, FP]
     for name in EXPORTS:
         if name.startswith("tgx_") and name not in ("tgx_last_error",):
             fn = getattr(lib, name)

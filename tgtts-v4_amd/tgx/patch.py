@@ -253,3 +253,16 @@ class LmSide:
             self.close()
         except Exception:
             pass
+
+
+def patch_launch(side: LmSide, sampler: Sampler, times: int = 1) -> None:
+    """`times` patch steps back to back over what the device holds: the LM side (rows moving on a
+    position each step), then the sampler on its mu (patch.rs:356-415, without the local encoder).
+    side.wait() waits; patch_elapsed_ms(side) times them."""
+    _check(library().tgx_patch_launch(side._h, sampler._h, times))
+
+
+def patch_elapsed_ms(side: LmSide) -> float:
+    v = ctypes.c_float()
+    _check(library().tgx_patch_elapsed_ms(side._h, ctypes.byref(v)))
+    return v.value
