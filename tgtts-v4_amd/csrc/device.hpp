@@ -42,6 +42,69 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __shfl(v, 0, WAVE);
 }
 
+// ---- LDS staged by direct global-to-LDS loads, several stages in flight ----
+//
+// A stage of fragments lands in LDS by global_load_lds (lane l writes bytes 16 l .. of the
+// fragment's 1 KiB). The compiler, seeing LDS written by such loads, waits for every load in
+// flight before any ordinary LDS read; reading fragments through ds_read_b128 in asm instead
+// leaves the waits to the kernel: wait_vm<N>() until at most N of this wave's loads are in flight
+// (the later stages'), a barrier so that every wave's have landed, then lds_read16 and
+// lds_landed() before the values are used.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ uint4 lds_read16(const uint4* p) {
+    uint4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_offset(p)) : "memory");
+    return v;
+}
+__device__ __forceinline__ void wait_lgkm() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// The values lds_read16 gave, usable: the wait, then each value passed through an asm the
+// compiler must run after it, so that nothing reads a register before its load has returned.
+template <int N>
+__device__ __forceinline__ void lds_landed(uint4 (&v)[N]) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    wait_lgkm();
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        u32x4 t = __builtin_bit_cast(u32x4, v[i]);
+        asm volatile("" : "+v"(t));
+        v[i] = __builtin_bit_cast(uint4, t);
+    }
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+__device__ __forceinline__ void load_to_lds(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)lds, 16, 0, 0);
+}
+
+// The same kind of sum from DPP moves within each row of 16 lanes (adjacent pairs, then quads,
+// then the mirrored half row, then the mirrored row: each step adds two equal-order partial
+// sums, so every lane of a row ends with the same value), then the four rows' sums read out and
+// added in row order. No LDS round trip; the result is uniform across the wave.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_move<0x141>(v);  // row_half_mirror
+    v += dpp_move<0x140>(v);  // row_mirror
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return ((r0 + r1) + r2) + r3;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));

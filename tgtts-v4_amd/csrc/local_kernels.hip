@@ -34,11 +34,10 @@ constexpr int LG_TKB = 2;                             // k-blocks of 32 to a sta
 constexpr int LG_W_STAGE = 4 * LG_TKB * 64;            // uint4 per stage: 4 strips, 8 KiB
 constexpr int LG_X_STAGE = 8 * LG_TKB * 64;            // 8 token tiles, 16 KiB
 constexpr int LG_FRAGS = (LG_W_STAGE + LG_X_STAGE) / 64 / 4;  // 1 KiB fragments a wave loads a stage
+constexpr int LG_NBUF = 4;  // stages in the LDS ring: three in flight while one is multiplied
+constexpr size_t LG_LDS = (size_t)LG_NBUF * (LG_W_STAGE + LG_X_STAGE) * sizeof(uint4);  // 96 KiB
 
 enum LocalEpilogue { LEPI_QKV = 0, LEPI_PARTIAL = 1, LEPI_SILU = 2 };
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void global_void;
 
 struct LocalGemm {
     const uint16_t* w;  // 16-row tiles of [N][K]
@@ -63,8 +62,9 @@ __device__ __forceinline__ int local_strip(int nb, int wn, int s, int N) {
 // Grid (n-blocks, token blocks, parts): part z sums k-blocks z K/32/parts .. of every row.
 template <int EPI>
 __global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm g) {
-    __shared__ uint4 ws[2 * LG_W_STAGE];
-    __shared__ uint4 xs[2 * LG_X_STAGE];
+    extern __shared__ uint4 lds[];
+    uint4* ws = lds;                         // [LG_NBUF][LG_W_STAGE]
+    uint4* xs = lds + LG_NBUF * LG_W_STAGE;  // [LG_NBUF][LG_X_STAGE]
     const int nb = blockIdx.x, m0 = blockIdx.y * LOCAL_TOKEN_TILE, part = blockIdx.z;
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int wn = w / 2, wm = w % 2;
@@ -75,7 +75,10 @@ __global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm 
 
     // Fragments 0..7 of a stage are W's (strip f / 2, k-block f % 2), 8..23 the tokens' (tile
     // (f - 8) / 2): lane l of a load writes bytes 16 l .. of the fragment, the MFMA operand order.
-    auto fetch = [&](int st, int buf) {
+    // Each wave issues exactly LG_FRAGS loads a stage (the branch is uniform across the wave), so
+    // its count of loads in flight says which stages have landed.
+    auto fetch = [&](int st) {
+        const int buf = st % LG_NBUF;
 #pragma unroll
         for (int j = 0; j < LG_FRAGS; ++j) {
             const int f = w * LG_FRAGS + j;
@@ -83,11 +86,11 @@ __global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm 
             if (f < 8) {
                 const int sl = f / 2;
                 const uint16_t* src = g.w + weight_tile_index(local_strip<EPI>(nb, sl / 2, sl % 2, g.N), kb, kblocks, 16) + lane * 8;
-                __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&ws[buf * LG_W_STAGE + f * 64], 16, 0, 0);
+                load_to_lds(src, &ws[buf * LG_W_STAGE + f * 64]);
             } else {
                 const int mt = (f - 8) / 2;
                 const uint16_t* src = g.x + (size_t)(m0 + mt * 16 + lane % 16) * g.K + kb * 32 + (lane / 16) * 8;
-                __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&xs[buf * LG_X_STAGE + (f - 8) * 64], 16, 0, 0);
+                load_to_lds(src, &xs[buf * LG_X_STAGE + (f - 8) * 64]);
             }
         }
     };
@@ -98,26 +101,39 @@ __global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm 
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    fetch(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < LG_NBUF - 1; ++p)
+        if (p < stages) fetch(p);
     for (int st = 0; st < stages; ++st) {
-        const int buf = st % 2;
-        if (st + 1 < stages) fetch(st + 1, 1 - buf);
+        // Stage st has landed once no more than the later stages' loads are in flight; the barrier
+        // makes it so for every wave, and says every wave is done with stage st - 1, whose buffer
+        // the next fetch takes.
+        const int ahead = min(LG_NBUF - 2, stages - 1 - st);
+        if (ahead >= 2)
+            wait_vm<2 * LG_FRAGS>();
+        else if (ahead == 1)
+            wait_vm<LG_FRAGS>();
+        else
+            wait_vm<0>();
+        stage_barrier();
+        if (st + LG_NBUF - 1 < stages) fetch(st + LG_NBUF - 1);
+        const int buf = st % LG_NBUF;
+        // fr[6 kbl + s]: W strip s; fr[6 kbl + 2 + t]: token tile t; of k-block kbl.
+        uint4 fr[LG_TKB * 6];
 #pragma unroll
         for (int kbl = 0; kbl < LG_TKB; ++kbl) {
-            uint4 af[2], bf[4];
 #pragma unroll
-            for (int s = 0; s < 2; ++s) af[s] = ws[buf * LG_W_STAGE + ((wn * 2 + s) * LG_TKB + kbl) * 64 + lane];
+            for (int s = 0; s < 2; ++s) fr[kbl * 6 + s] = lds_read16(&ws[buf * LG_W_STAGE + ((wn * 2 + s) * LG_TKB + kbl) * 64 + lane]);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) bf[t] = xs[buf * LG_X_STAGE + ((wm * 4 + t) * LG_TKB + kbl) * 64 + lane];
+            for (int t = 0; t < 4; ++t) fr[kbl * 6 + 2 + t] = lds_read16(&xs[buf * LG_X_STAGE + ((wm * 4 + t) * LG_TKB + kbl) * 64 + lane]);
+        }
+        lds_landed(fr);
+#pragma unroll
+        for (int kbl = 0; kbl < LG_TKB; ++kbl)
 #pragma unroll
             for (int s = 0; s < 2; ++s)
 #pragma unroll
-                for (int t = 0; t < 4; ++t) acc[s][t] = mfma16(af[s], bf[t], acc[s][t]);
-        }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+                for (int t = 0; t < 4; ++t) acc[s][t] = mfma16(fr[kbl * 6 + s], fr[kbl * 6 + 2 + t], acc[s][t]);
     }
 
     // Tile (s, t) holds W rows 16 strip + 4 (lane / 16) + i against token m0 + 16 (4 wm + t) + lane % 16.
@@ -324,35 +340,45 @@ __global__ void __launch_bounds__(256) local_add_norm(LocalArgs a, const float* 
 // local_embed: grid (hidden / 256, rows); thread n of the row: acc_f = bias[n] + sum_c W[n][c]
 // frame_f[c] in channel order, for each of the row's frames, written as tokens first + f of both
 // of the row's sequences; and the copied tokens.
-constexpr int EMBED_MAX = 1024;  // channels x frames a row's patch may hold
+constexpr int EMBED_MAX = 1024;     // channels x frames a row's patch may hold
+constexpr int EMBED_CHANNELS = 64;  // channels at most (a row of W in 16 float4 loads)
 
+// F frames to a patch, a template parameter so that every loop over them unrolls without a
+// branch (a branch around a load makes the compiler wait for it where the paths join).
+template <int F>
 __global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
     __shared__ float frames[EMBED_MAX];  // [frames][channels]
-    const int row = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
-    const int C = e.channels, F = e.frames;
+    const int row = blockIdx.y, n = min(blockIdx.x * 256 + threadIdx.x, a.hidden - 1);
+    const int C = e.channels;
+    // The thread's row of W, every load in flight at once (indices clamped, not branched).
+    float4 wq[EMBED_CHANNELS / 4];
+#pragma unroll
+    for (int v = 0; v < EMBED_CHANNELS / 4; ++v)
+        wq[v] = *reinterpret_cast<const float4*>(e.w + (size_t)n * C + 4 * min(v, C / 4 - 1));
     for (int i = threadIdx.x; i < C * F; i += 256) {
         const int f = i / C, c = i % C;
         frames[i] = e.src[((size_t)row * C + c) * F + f];
     }
     __syncthreads();
-    if (n >= a.hidden) return;
-    float acc[8];
+    if (blockIdx.x * 256 + threadIdx.x >= a.hidden) return;
+    float acc[F];
     const float b = e.bias[n];
 #pragma unroll
-    for (int f = 0; f < 8; ++f) acc[f] = b;
-    const float* wr = e.w + (size_t)n * C;
-    for (int c = 0; c < C; ++c) {
-        const float wc = wr[c];
+    for (int f = 0; f < F; ++f) acc[f] = b;
 #pragma unroll
-        for (int f = 0; f < 8; ++f)
-            if (f < F) acc[f] += wc * frames[f * C + c];
+    for (int v = 0; v < EMBED_CHANNELS / 4; ++v) {
+        if (4 * v >= C) break;
+        const float w4[4] = {wq[v].x, wq[v].y, wq[v].z, wq[v].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int f = 0; f < F; ++f) acc[f] += w4[i] * frames[f * C + 4 * v + i];
     }
     const int K = a.hidden;
     for (int s = 0; s < 2; ++s) {
         const size_t seq0 = (size_t)(row * 2 + s) * a.T;
 #pragma unroll
-        for (int f = 0; f < 8; ++f)
-            if (f < F) e.x0[(seq0 + e.first + f) * K + n] = acc[f];
+        for (int f = 0; f < F; ++f) e.x0[(seq0 + e.first + f) * K + n] = acc[f];
         for (int t = 0; t < e.copies; ++t) {
             const float* src = e.copy_src + ((size_t)(e.shared ? 0 : row * e.copies) + t) * K;
             e.x0[(seq0 + e.copy_at + t) * K + n] = (e.guided && s > 0) ? 0.f : src[n];
@@ -361,63 +387,93 @@ __global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// dit_euler: a workgroup to a row. The 2 frames tokens (conditional sequence, then the
-// unconditional) staged in LDS; wave w takes channels w, w + 4, ...: lane l sums hidden / 64
-// columns of each token in order, the lanes added by a butterfly. Then CFG-Zero*
-// (dit_euler.comp:81-110): alpha = <v_c, v_u> / (|v_u|^2 + 1e-8), guided = alpha v_u +
-// cfg (v_c - alpha v_u), state -= dt guided.
-constexpr int EULER_MAX_TOKENS = 8;  // 2 x frames
-constexpr int EULER_MAX_LEN = 512;   // channels x frames
+// dit_euler: a workgroup of 8 waves to a row. out_proj's velocities are a 16-token product on
+// the MFMA unit: W in 16-row bf16 tiles (the channels), the row's 2 frames tokens (the
+// conditional sequence's, then the unconditional's; bf16, the other columns of the tile zero);
+// wave w sums k-blocks 4 w .. 4 w + 3 with every load in flight at once, and the waves' tiles are
+// added in wave order. Then CFG-Zero* (dit_euler.comp:81-110): alpha = <v_c, v_u> /
+// (|v_u|^2 + 1e-8), guided = alpha v_u + cfg (v_c - alpha v_u), state -= dt guided.
+constexpr int EULER_MAX_LEN = 512;  // channels x frames
+constexpr int EULER_WAVES = 8;
+constexpr int EULER_THREADS = EULER_WAVES * WAVE;
+constexpr int EULER_STRIPS = 4;  // channels / 16 at most
+constexpr int EULER_K = 1024;    // the DiT's width
+constexpr int EULER_KB = EULER_K / 32 / EULER_WAVES;  // k-blocks to a wave
 
-__global__ void __launch_bounds__(256) dit_euler(LocalArgs a, EulerArgs e) {
-    __shared__ float tok[EULER_MAX_TOKENS * 1024];
+template <int F>
+__global__ void __launch_bounds__(EULER_THREADS) dit_euler(LocalArgs a, EulerArgs e) {
+    constexpr int TOKENS = 2 * F, K = EULER_K, KB = K / 32;
+    __shared__ f32x4 red[EULER_WAVES][EULER_STRIPS][WAVE];
     __shared__ float vel[2 * EULER_MAX_LEN];
-    __shared__ float red[2][4];
-    const int row = blockIdx.x, K = a.hidden, F = e.frames, C = e.channels;
+    __shared__ float sums[2][EULER_WAVES];
+    const int row = blockIdx.x, C = e.channels, strips = C / 16;
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    for (int i = threadIdx.x; i < 2 * F * K; i += 256) {
-        const int tm = i / K, s = tm / F, f = tm % F;
-        tok[i] = e.out[((size_t)(row * 2 + s) * a.T + e.first + f) * K + i % K];
+    // B operand: lane l holds token l % 16 (zero past the 2 F), columns 32 kb + 8 (l / 16) .. + 7.
+    const int tm = lane % 16;
+    const bool real = tm < TOKENS;
+    const int tmc = real ? tm : 0;
+    const float* src = e.out + ((size_t)(row * 2 + tmc / F) * a.T + e.first + tmc % F) * K + (lane / 16) * 8;
+    float4 lo[EULER_KB], hi[EULER_KB];
+    uint4 wf[EULER_KB][EULER_STRIPS];
+#pragma unroll
+    for (int j = 0; j < EULER_KB; ++j) {
+        const int kb = w * EULER_KB + j;
+        lo[j] = *reinterpret_cast<const float4*>(src + kb * 32);
+        hi[j] = *reinterpret_cast<const float4*>(src + kb * 32 + 4);
+#pragma unroll
+        for (int s = 0; s < EULER_STRIPS; ++s)
+            wf[j][s] = *reinterpret_cast<const uint4*>(e.w + weight_tile_index(min(s, strips - 1), kb, KB, 16) + lane * 8);
     }
+    f32x4 acc[EULER_STRIPS];
+#pragma unroll
+    for (int s = 0; s < EULER_STRIPS; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < EULER_KB; ++j) {
+        const uint4 b = real ? make_uint4(pack_bf16x2(lo[j].x, lo[j].y), pack_bf16x2(lo[j].z, lo[j].w),
+                                          pack_bf16x2(hi[j].x, hi[j].y), pack_bf16x2(hi[j].z, hi[j].w))
+                             : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < EULER_STRIPS; ++s) acc[s] = mfma16(wf[j][s], b, acc[s]);
+    }
+#pragma unroll
+    for (int s = 0; s < EULER_STRIPS; ++s) red[w][s][lane] = acc[s];
     __syncthreads();
-    const int per = K / WAVE;
-    for (int c = w; c < C; c += 4) {
-        const float* wr = e.w + (size_t)c * K + lane * per;
-        float part[EULER_MAX_TOKENS];
+    // Wave s < strips adds strip s over the waves in order: lane l holds token l % 16, channels
+    // 16 s + 4 (l / 16) + i.
+    if (w < strips && real) {
+        f32x4 total = red[0][w][lane];
 #pragma unroll
-        for (int tm = 0; tm < EULER_MAX_TOKENS; ++tm) part[tm] = 0.f;
-        for (int j = 0; j < per; ++j) {
-            const float wv = wr[j];
+        for (int v = 1; v < EULER_WAVES; ++v) total += red[v][w][lane];
 #pragma unroll
-            for (int tm = 0; tm < EULER_MAX_TOKENS; ++tm)
-                if (tm < 2 * F) part[tm] += wv * tok[tm * K + lane * per + j];
-        }
-#pragma unroll
-        for (int tm = 0; tm < EULER_MAX_TOKENS; ++tm) {
-            if (tm >= 2 * F) break;
-            const float total = wave_sum(part[tm]);
-            if (lane == 0) vel[(tm / F) * C * F + c * F + tm % F] = total + e.bias[c];
+        for (int i = 0; i < 4; ++i) {
+            const int c = w * 16 + (lane / 16) * 4 + i;
+            vel[(tm / F) * C * F + c * F + tm % F] = total[i] + e.bias[c];
         }
     }
     __syncthreads();
     const int len = C * F;
     float dot = 0.f, norm = 0.f;
-    for (int i = threadIdx.x; i < len; i += 256) {
+    for (int i = threadIdx.x; i < len; i += EULER_THREADS) {
         dot += vel[i] * vel[len + i];
         norm += vel[len + i] * vel[len + i];
     }
     dot = wave_sum(dot);
     norm = wave_sum(norm);
     if (lane == 0) {
-        red[0][w] = dot;
-        red[1][w] = norm;
+        sums[0][w] = dot;
+        sums[1][w] = norm;
     }
     __syncthreads();
-    dot = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    norm = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    dot = 0.f;
+    norm = 0.f;
+#pragma unroll
+    for (int v = 0; v < EULER_WAVES; ++v) {
+        dot += sums[0][v];
+        norm += sums[1][v];
+    }
     const float alpha = dot / (norm + 1e-8f);
     const float cfg = e.sampling[row * 2 + 1];
-    for (int i = threadIdx.x; i < len; i += 256) {
+    for (int i = threadIdx.x; i < len; i += EULER_THREADS) {
         const float scaled = vel[len + i] * alpha;
         const float guided = scaled + cfg * (vel[i] - scaled);
         e.state[(size_t)row * len + i] -= guided * e.dt;
@@ -446,18 +502,18 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
         const LocalLayer& L = layers[l];
         const float* input = l == 0 ? b.x0 : b.x;
         LocalGemm qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, b.q, b.k, b.v};
-        dispatch("local_qkv_rope", local_gemm<LEPI_QKV>, dim3(qkv_rows / LOCAL_ROW_TILE, mblocks), block, 0, stream, timer, a, qkv);
+        dispatch("local_qkv_rope", local_gemm<LEPI_QKV>, dim3(qkv_rows / LOCAL_ROW_TILE, mblocks), block, LG_LDS, stream, timer, a, qkv);
         dispatch("local_attention", local_attention, dim3(a.M / a.T), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
                  (const uint16_t*)b.k, (const uint16_t*)b.v, b.attended);
         LocalGemm o{L.o, b.attended, H * HEAD_DIM, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
-        dispatch("local_o_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.o_parts), block, 0, stream,
+        dispatch("local_o_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.o_parts), block, LG_LDS, stream,
                  timer, a, o);
         dispatch("local_o_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial, b.o_parts,
                  input, b.h, L.post_norm, b.normed, (float*)nullptr);
         LocalGemm gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, b.mlp, nullptr, nullptr, nullptr};
-        dispatch("local_gate_up", local_gemm<LEPI_SILU>, dim3(a.inner / 32, mblocks), block, 0, stream, timer, a, gu);
+        dispatch("local_gate_up", local_gemm<LEPI_SILU>, dim3(a.inner / 32, mblocks), block, LG_LDS, stream, timer, a, gu);
         LocalGemm down{L.down, b.mlp, a.inner, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
-        dispatch("local_down_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.down_parts), block, 0,
+        dispatch("local_down_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.down_parts), block, LG_LDS,
                  stream, timer, a, down);
         if (l + 1 < nlayers)
             dispatch("local_down_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
@@ -469,13 +525,36 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
     return hipGetLastError();
 }
 
+hipError_t local_prepare() {
+    for (const void* k : {(const void*)local_gemm<LEPI_QKV>, (const void*)local_gemm<LEPI_PARTIAL>, (const void*)local_gemm<LEPI_SILU>}) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LG_LDS);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer) {
-    dispatch("local_embed", local_embed, dim3((a.hidden + 255) / 256, rows), dim3(256), 0, stream, timer, a, e);
+    const dim3 grid((a.hidden + 255) / 256, rows), block(256);
+    switch (e.frames) {
+        case 1: dispatch("local_embed", local_embed<1>, grid, block, 0, stream, timer, a, e); break;
+        case 2: dispatch("local_embed", local_embed<2>, grid, block, 0, stream, timer, a, e); break;
+        case 3: dispatch("local_embed", local_embed<3>, grid, block, 0, stream, timer, a, e); break;
+        case 4: dispatch("local_embed", local_embed<4>, grid, block, 0, stream, timer, a, e); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_dit_euler(const LocalArgs& a, const EulerArgs& e, int rows, hipStream_t stream, DispatchTimer* timer) {
-    dispatch("dit_euler", dit_euler, dim3(rows), dim3(256), 0, stream, timer, a, e);
+    if (a.hidden != EULER_K) return hipErrorInvalidValue;
+    const dim3 grid(rows), block(EULER_THREADS);
+    switch (e.frames) {
+        case 1: dispatch("dit_euler", dit_euler<1>, grid, block, 0, stream, timer, a, e); break;
+        case 2: dispatch("dit_euler", dit_euler<2>, grid, block, 0, stream, timer, a, e); break;
+        case 3: dispatch("dit_euler", dit_euler<3>, grid, block, 0, stream, timer, a, e); break;
+        case 4: dispatch("dit_euler", dit_euler<4>, grid, block, 0, stream, timer, a, e); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

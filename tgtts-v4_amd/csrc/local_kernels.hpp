@@ -62,7 +62,7 @@ struct EmbedArgs {
 // unconditional sequence, guided as CFG-Zero* guides them, and state -= dt * guided.
 struct EulerArgs {
     const float* out;   // f32 [M_pad][hidden], the stack's output after the final norm
-    const float* w;     // f32 [channels][hidden]
+    const uint16_t* w;  // bf16 [channels][hidden] in 16-row MFMA tiles
     const float* bias;  // [channels]
     const float* sampling;  // [rows][2]: temperature, guidance scale
     float* state;       // [rows][channels][frames]
@@ -70,6 +70,8 @@ struct EulerArgs {
     float dt;
 };
 
+// Lets the projections take their LDS ring (96 KiB) per workgroup; once per process.
+hipError_t local_prepare();
 hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int nlayers, const float* final_norm,
                               const LocalBuffers& b, hipStream_t stream, DispatchTimer* timer);
 hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer);

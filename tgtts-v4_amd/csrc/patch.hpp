@@ -38,7 +38,8 @@ struct Sampler {
     size_t device_bytes = 0;
     std::vector<Layer> layers;
     float* final_norm = nullptr;
-    float *in_w = nullptr, *in_b = nullptr, *cond_w = nullptr, *cond_b = nullptr, *out_w = nullptr, *out_b = nullptr;
+    float *in_w = nullptr, *in_b = nullptr, *cond_w = nullptr, *cond_b = nullptr, *out_b = nullptr;
+    uint16_t* out_w = nullptr;  // bf16 16-row tiles
     float* time_tokens = nullptr;  // [steps][hidden]
     bool times_dirty = true;
     TimeMlp time_mlp, delta_mlp;

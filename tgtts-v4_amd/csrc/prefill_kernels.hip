@@ -22,15 +22,18 @@ namespace {
 
 constexpr int PF_WAVES = 4;
 constexpr int PF_THREADS = PF_WAVES * WAVE;
-// The GEMM's workgroup tile: 256 rows of W (16 strips) by 256 rows of X, K 64 at a time (two
-// k-blocks); wave (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 128 wm .. + 127
-// (8 tiles of 16): 64 accumulators of 16 x 16.
-constexpr int TN = 256, TM = 256, TKB = 2;
+// The GEMM's workgroup tile: 256 rows of W (16 strips) by 256 rows of X, K 32 at a time (a
+// k-block to a stage, four stages in an LDS ring, three in flight while one is multiplied);
+// wave (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 128 wm .. + 127 (8 tiles of
+// 16): 64 accumulators of 16 x 16.
+constexpr int TN = 256, TM = 256;
 constexpr int W_STRIPS = TN / 16;   // 16
 constexpr int X_TILES = TM / 16;    // 16
 constexpr int WT = 8;               // a wave's X tiles
-constexpr int W_STAGE = W_STRIPS * TKB * 64;  // uint4 per stage: 32 KiB
-constexpr int X_STAGE = X_TILES * TKB * 64;   // 32 KiB
+constexpr int W_STAGE = W_STRIPS * 64;  // uint4 per stage: 16 KiB
+constexpr int X_STAGE = X_TILES * 64;   // 16 KiB
+constexpr int NBUF = 4;
+constexpr int FRAGS = (W_STRIPS + X_TILES) / PF_WAVES;  // 1 KiB loads a wave issues a stage
 
 enum Epilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2 };
 
@@ -38,9 +41,6 @@ constexpr uint32_t TGX_SPARE_POS = 0xffffffffu;
 static_assert(PF_THREADS == TM, "the q/k/v epilogue stages a row to a thread");
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void global_void;
 
 struct GemmArgs {
     const uint16_t* w;  // 16-row tiles of [N][K]
@@ -75,32 +75,32 @@ __device__ __forceinline__ int stage_strip(int nb, int sl, int N) {
 template <int EPI>
 __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmArgs g) {
     extern __shared__ uint4 lds[];
-    uint4* ws = lds;                  // [2][W_STAGE]
-    uint4* xs = lds + 2 * W_STAGE;    // [2][X_STAGE]
+    uint4* ws = lds;                     // [NBUF][W_STAGE]
+    uint4* xs = lds + NBUF * W_STAGE;    // [NBUF][X_STAGE]
     const int nb = blockIdx.x, mb = blockIdx.y;
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int wn = w / 2, wm = w % 2;
     const int kblocks = g.K / 32;
-    const int stages = kblocks / TKB;
+    const int stages = kblocks;
     const int m0 = mb * TM;
 
-    // A stage is 32 weight fragments and 32 vector fragments of 1 KiB, eight of each to a wave,
-    // loaded straight from memory into LDS: lane l of a load writes bytes 16 l .. 16 l + 15 of
-    // the fragment, the MFMA operand order.
-    auto fetch = [&](int st, int buf) {
+    // A stage is 16 weight fragments and 16 vector fragments of 1 KiB, eight to a wave (the
+    // first two waves W's, the last two X's), loaded straight from memory into LDS: lane l of a
+    // load writes bytes 16 l .. 16 l + 15 of the fragment, the MFMA operand order. Each wave
+    // issues exactly FRAGS loads a stage, so its count in flight says which stages have landed.
+    auto fetch = [&](int st) {
+        const int buf = st % NBUF;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int f = w * 8 + j;
-            const int sl = f / TKB, kbl = f % TKB;
-            const uint16_t* src = g.w + weight_tile_index(stage_strip<EPI>(nb, sl, g.N), st * TKB + kbl, kblocks, 16) + lane * 8;
-            __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&ws[buf * W_STAGE + f * 64], 16, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int f = w * 8 + j;
-            const int mt = f / TKB, kbl = f % TKB;
-            const uint16_t* src = g.x + (size_t)(m0 + mt * 16 + lane % 16) * g.K + (st * TKB + kbl) * 32 + (lane / 16) * 8;
-            __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)&xs[buf * X_STAGE + f * 64], 16, 0, 0);
+        for (int j = 0; j < FRAGS; ++j) {
+            const int f = w * FRAGS + j;
+            if (f < W_STRIPS) {
+                const uint16_t* src = g.w + weight_tile_index(stage_strip<EPI>(nb, f, g.N), st, kblocks, 16) + lane * 8;
+                load_to_lds(src, &ws[buf * W_STAGE + f * 64]);
+            } else {
+                const int mt = f - W_STRIPS;
+                const uint16_t* src = g.x + (size_t)(m0 + mt * 16 + lane % 16) * g.K + st * 32 + (lane / 16) * 8;
+                load_to_lds(src, &xs[buf * X_STAGE + mt * 64]);
+            }
         }
     };
 
@@ -110,30 +110,37 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
 #pragma unroll
         for (int t = 0; t < WT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    fetch(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < NBUF - 1; ++p)
+        if (p < stages) fetch(p);
     for (int st = 0; st < stages; ++st) {
-        const int buf = st % 2;
-        if (st + 1 < stages) fetch(st + 1, 1 - buf);
+        // Stage st has landed once no more than the later stages' loads are in flight; the barrier
+        // makes it so for every wave, and says every wave is done with stage st - 1, whose buffer
+        // the next fetch takes.
+        const int ahead = min(NBUF - 2, stages - 1 - st);
+        if (ahead >= 2)
+            wait_vm<2 * FRAGS>();
+        else if (ahead == 1)
+            wait_vm<FRAGS>();
+        else
+            wait_vm<0>();
+        stage_barrier();
+        if (st + NBUF - 1 < stages) fetch(st + NBUF - 1);
+        const int buf = st % NBUF;
+        // fr[t]: X tile t; fr[WT + s]: W strip s.
+        uint4 fr[WT + 8];
 #pragma unroll
-        for (int kbl = 0; kbl < TKB; ++kbl) {
-            uint4 bf[WT], af[2];
+        for (int t = 0; t < WT; ++t) fr[t] = lds_read16(&xs[buf * X_STAGE + (wm * WT + t) * 64 + lane]);
 #pragma unroll
-            for (int t = 0; t < WT; ++t) bf[t] = xs[buf * X_STAGE + ((wm * WT + t) * TKB + kbl) * 64 + lane];
-            af[0] = ws[buf * W_STAGE + ((wn * 8) * TKB + kbl) * 64 + lane];
+        for (int s = 0; s < 8; ++s) fr[WT + s] = lds_read16(&ws[buf * W_STAGE + (wn * 8 + s) * 64 + lane]);
+        lds_landed(fr);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                // The next strip's fragment is read while this one's products run.
-                if (s + 1 < 8) af[(s + 1) % 2] = ws[buf * W_STAGE + ((wn * 8 + s + 1) * TKB + kbl) * 64 + lane];
+        for (int s = 0; s < 8; ++s)
 #pragma unroll
-                for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(af[s % 2], bf[t], acc[s][t]);
-            }
-        }
-        // The next stage has landed (this wave's loads), and every wave is done with this one.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+            for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(fr[WT + s], fr[t], acc[s][t]);
     }
+    // The epilogue below may reuse the LDS: every wave is done with the ring.
+    stage_barrier();
 
     // Epilogue: tile (s, t) holds W rows 16 strip + 4 (lane / 16) + i against X row
     // m0 + 16 (WT wm + t) + lane % 16.
@@ -449,8 +456,7 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
     }
 }
 
-
-constexpr size_t GEMM_LDS = (size_t)2 * (W_STAGE + X_STAGE) * sizeof(uint4);
+constexpr size_t GEMM_LDS = (size_t)NBUF * (W_STAGE + X_STAGE) * sizeof(uint4);  // 128 KiB
 
 hipError_t allow(const void* kernel, size_t device_lds) {
     hipFuncAttributes attr{};

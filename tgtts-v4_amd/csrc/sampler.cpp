@@ -126,11 +126,15 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     if (patch->rows < 1) return shape_fail("no rows");
     if (patch->timesteps < 1) return shape_fail("no timesteps");
     if (F < 1 || F > 4) return shape_fail(std::to_string(F) + " frames to a patch (1 to 4)");
-    if (C < 8 || C % 8 || C * F > 512) return shape_fail(std::to_string(C) + " channels of " + std::to_string(F) + " frames");
-    if (s.hidden > 1024 || s.hidden % 512) return shape_fail("a stack " + std::to_string(s.hidden) + " wide (512 or 1024)");
+    // dit_euler takes the channels as up to 4 MFMA strips of 16.
+    if (C < 16 || C % 16 || C > 64)
+        return shape_fail(std::to_string(C) + " channels of " + std::to_string(F) + " frames (16, 32, 48 or 64)");
+    if (s.hidden != 1024) return shape_fail("a stack " + std::to_string(s.hidden) + " wide (the kernels take 1024)");
     if (T * H > 256 || T * KV * HEAD_DIM > LOCAL_MAX_T * 2 * HEAD_DIM * 2 || T > LOCAL_MAX_T)
         return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads over " + std::to_string(KV));
     if (s.inner % 256) return shape_fail("an FFN " + std::to_string(s.inner) + " wide");
+    hipError_t pe = local_prepare();
+    if (pe != hipSuccess) return fail(TGX_E_HIP, std::string("the local stack's LDS: ") + hipGetErrorString(pe));
     Sampler* smp = new Sampler();
     smp->ctx = ctx;
     smp->shape = s;
@@ -239,7 +243,12 @@ tgx_status sampler_load(Sampler* s, const char* name, const void* data, tgx_dtyp
     if (n == "in_proj.bias") return upload(s->in_b, h);
     if (n == "cond_proj.weight") return upload(s->cond_w, h * C);
     if (n == "cond_proj.bias") return upload(s->cond_b, h);
-    if (n == "out_proj.weight") return upload(s->out_w, C * h);
+    if (n == "out_proj.weight") {
+        TGX_TRY(want(C * h));
+        auto t = tile_rows(as_f32(data, dtype, count), (int)C, (int)h, 16, [](int strip, int r) { return strip * 16 + r; });
+        TGX_HIP(hipMemcpy(s->out_w, t.data(), t.size() * 2, hipMemcpyHostToDevice));
+        return TGX_OK;
+    }
     if (n == "out_proj.bias") return upload(s->out_b, C);
     for (int which = 0; which < 2; ++which) {
         const std::string prefix = which == 0 ? "time_mlp." : "delta_time_mlp.";
