@@ -9,7 +9,8 @@
 //   attention_decode  attention over the paged cache, a workgroup to each (row, KV head), its
 //                     waves taking the 64-position blocks in turn with an online softmax and
 //                     joined in wave order (attention_split.comp:52-111 + attention_combine.comp:29-57)
-//   gemv_residual     out = residual + W x, o_proj and down_proj (gemv_residual.comp:28-45)
+//   gemv_residual     out = residual + W x, o_proj and down_proj (gemv_residual.comp:28-45), which
+//                     also leave out as the next norm takes it (out gain in bf16, sums of squares)
 //   gemv_gate_up      RMSNorm(mid) -> gate, up -> SiLU(gate) up (gemv_gate_up.comp:31-52)
 //   final_rmsnorm     the final norm (rmsnorm.comp:15-21)
 //
@@ -24,11 +25,11 @@ namespace tgx {
 
 namespace {
 
-// Projections: a workgroup of eight waves to a strip of R rows (two strips of 16 for gate/up)
-// against one 16-row tile of the batch, the tile of blockIdx.y. R is 4 or 8 at small batches,
-// so that the strips of a projection fill the 256 CUs, and 16 at large ones, whose tiles fill
-// them instead; the workgroups of one strip sit on one XCD (their ids differ by a multiple of
-// the strips, a multiple of 8) and read its weights from there after the first.
+// Projections: a workgroup of eight waves to a strip of W (16 rows for q/k/v, 2 x 16 for gate/up,
+// 4 or 16 for o_proj and down_proj) against one 16-row tile of the batch, the tile of blockIdx.y;
+// the workgroups of one strip sit on one XCD (their ids differ by a multiple of the strips, a
+// multiple of 8) and read its weights from there after the first. A workgroup issues every load
+// it makes at its start, so that it waits for memory once.
 constexpr int GEMV_WAVES = 8;
 constexpr int GEMV_THREADS = GEMV_WAVES * WAVE;
 // K is taken in chunks of 32 k-blocks (1024 columns); wave w's chain runs over k-blocks
@@ -37,174 +38,178 @@ constexpr int CHUNK_KB = 32;
 constexpr int CHUNK_COLS = CHUNK_KB * 32;
 constexpr int PER_WAVE = CHUNK_KB / GEMV_WAVES;
 constexpr int MAX_CHUNKS = 4;  // K up to 4096; kernels are built for 1 chunk and for up to 4
+// A norm's input carries a sum of squares for each SQ_COLS columns of a row.
+constexpr int SQ_COLS = 4;
 
 // Attention: a workgroup of eight waves to each (row, KV head).
 constexpr int ATTN_WAVES = 8;
 constexpr int ATTN_THREADS = ATTN_WAVES * WAVE;
 
 __device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ float4 load_f4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
-// The B operand in LDS, one chunk of the tile's 16 rows: xs[kb 64 + 16 g + c] holds row c,
-// columns 32 kb + 8 g .. + 7 of the chunk. col8 numbers the groups of 8 columns (0 .. 127).
-__device__ __forceinline__ int xs_index(int c, int col8) { return (col8 / 4) * 64 + (col8 % 4) * 16 + c; }
+// Loads below are never branched around per lane: rows past the batch are read from the last row
+// instead, and the chunk counts are template parameters. What such rows give lands in MFMA rows
+// or columns that nothing reads (a row of C depends on that row of A alone, a column on that
+// column of B alone).
+//
+// all_issued() ends the issue of a kernel's loads: the scheduler may move nothing across it, so
+// that every load is in flight before the first value is used (left to itself it interleaves the
+// loads with the MFMAs to save registers, one memory round trip after another).
+__device__ __forceinline__ void all_issued() { __builtin_amdgcn_sched_barrier(0); }
 
-// RMSNorm(x) gain of the tile's rows into xs, chunk by chunk through `each(chunk)` (norm.glsl:
-// 12-53): a wave to a row; lane l sums the squares of its 16 elements of each chunk in order,
-// chunk after chunk, and the lanes are added by a butterfly; the same arithmetic for a row
-// whatever the batch. The rows of the tile past B are zero.
-template <typename Each>
-__device__ void stage_normed(const float* __restrict__ x, const float* __restrict__ gain, float eps, int B, int K,
-                             int tile, uint4* xs, float* scales, Each each) {
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int chunks = K / CHUNK_COLS;
-    if (chunks > 1) {
-        for (int c = w; c < 16; c += GEMV_WAVES) {
-            const int b = tile * 16 + c;
-            if (b >= B) continue;
-            float squares = 0.f;
-            for (int ch = 0; ch < chunks; ++ch) {
-                const float* row = x + (size_t)b * K + ch * CHUNK_COLS + lane * 16;
+// The MFMA's B operand straight from memory, no LDS: wave w's k-blocks are 32 c + 4 w + j of
+// chunk c (j < 4), and lane 16 g + t of a k-block holds row t of the tile (batch row
+// 16 tile + t), columns 32 kb + 8 g .. + 7. Each wave reads only the columns of its own
+// k-blocks, so the vectors need no sharing between waves.
+template <int CH>
+struct Operand {
+    static constexpr int KB = CH * PER_WAVE;  // k-blocks to a wave
+    uint4 xf[KB];
+
+    __device__ static int kblock(int i) { return (i / PER_WAVE) * CHUNK_KB + (int)(threadIdx.x / WAVE) * PER_WAVE + i % PER_WAVE; }
+    __device__ static int column(int i) { return kblock(i) * 32 + ((threadIdx.x % WAVE) / 16) * 8; }
+    __device__ static int row(int B, int tile) { return min(tile * 16 + (int)(threadIdx.x % 16), B - 1); }
+};
+
+// Bf16 rows [B][K].
+template <int CH>
+struct RawRows : Operand<CH> {
+    using Operand<CH>::KB;
+
+    __device__ void load(const uint16_t* __restrict__ x, int B, int tile) {
+        const uint16_t* row = x + (size_t)Operand<CH>::row(B, tile) * (CH * CHUNK_COLS);
 #pragma unroll
-                for (int e = 0; e < 16; e += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(row + e);
-                    squares += v.x * v.x;
-                    squares += v.y * v.y;
-                    squares += v.z * v.z;
-                    squares += v.w * v.w;
-                }
+        for (int i = 0; i < KB; ++i) this->xf[i] = load16(row + Operand<CH>::column(i));
+    }
+};
+
+// RMSNorm's rows (norm.glsl:12-53) from the f32 rows: x gain in bf16, the row's scale 1 / rms(x)
+// applied to the products afterwards, RMSNorm(x) W^T = s (x gain) W^T. `squares` is the lane's
+// sum of x^2 over its columns, in k-block order; row_scales adds the lanes' in a fixed order.
+template <int CH>
+struct NormedRows : Operand<CH> {
+    using Operand<CH>::KB;
+    float4 xr[KB][2], gr[KB][2];
+    float squares;
+
+    __device__ void load(const float* __restrict__ x, const float* __restrict__ gain, int B, int tile) {
+        const float* row = x + (size_t)Operand<CH>::row(B, tile) * (CH * CHUNK_COLS);
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) xr[i][h] = load_f4(row + Operand<CH>::column(i) + 4 * h);
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) gr[i][h] = load_f4(gain + Operand<CH>::column(i) + 4 * h);
+    }
+    __device__ void finish() {
+        float sq = 0.f;
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+            const float4 a = xr[i][0], c = xr[i][1], ga = gr[i][0], gc = gr[i][1];
+            sq += a.x * a.x;
+            sq += a.y * a.y;
+            sq += a.z * a.z;
+            sq += a.w * a.w;
+            sq += c.x * c.x;
+            sq += c.y * c.y;
+            sq += c.z * c.z;
+            sq += c.w * c.w;
+            this->xf[i] = make_uint4(pack_bf16x2(a.x * ga.x, a.y * ga.y), pack_bf16x2(a.z * ga.z, a.w * ga.w),
+                                     pack_bf16x2(c.x * gc.x, c.y * gc.y), pack_bf16x2(c.z * gc.z, c.w * gc.w));
+        }
+        squares = sq;
+    }
+};
+
+// The tile's rows' scales 1 / sqrt(sum / K + eps) from their sums of squares over each SQ_COLS
+// columns, sq [B][K / SQ_COLS] (K = CH 1024: 256 CH sums a row): wave w takes tile rows 2 w and
+// 2 w + 1, lane l sums 4 l .. 4 l + 3 of each 256 in order, and the lanes' totals are added in
+// a fixed order (wave_sum). The same arithmetic for a row whatever the batch.
+template <int CH>
+struct RowSquares {
+    float4 part[2][CH];
+
+    __device__ void load(const float* __restrict__ sq, int B, int tile) {
+        const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int b = min(tile * 16 + 2 * w + h, B - 1);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) part[h][c] = load_f4(sq + (size_t)b * (CH * 256) + c * 256 + lane * 4);
+        }
+    }
+    // scale[2 w + h], behind the caller's next barrier.
+    __device__ void finish(float eps, float* scale) {
+        const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float t = 0.f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                t += part[h][c].x;
+                t += part[h][c].y;
+                t += part[h][c].z;
+                t += part[h][c].w;
             }
-            const float total = wave_sum(squares);
-            if (lane == 0) scales[c] = 1.0f / sqrtf(total / (float)K + eps);
-        }
-        __syncthreads();
-    }
-    for (int ch = 0; ch < chunks; ++ch) {
-        if (ch > 0) __syncthreads();
-        float4 g[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) g[e] = *reinterpret_cast<const float4*>(gain + ch * CHUNK_COLS + lane * 16 + 4 * e);
-        for (int c = w; c < 16; c += GEMV_WAVES) {
-            const int b = tile * 16 + c;
-            uint4 packed[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-            if (b < B) {
-                const float* row = x + (size_t)b * K + ch * CHUNK_COLS + lane * 16;
-                float4 v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = *reinterpret_cast<const float4*>(row + 4 * e);
-                float scale;
-                if (chunks == 1) {
-                    float squares = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        squares += v[e].x * v[e].x;
-                        squares += v[e].y * v[e].y;
-                        squares += v[e].z * v[e].z;
-                        squares += v[e].w * v[e].w;
-                    }
-                    scale = 1.0f / sqrtf(wave_sum(squares) / (float)K + eps);
-                } else {
-                    scale = scales[c];
-                }
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const float4 a = v[2 * h], e2 = v[2 * h + 1], ga = g[2 * h], gb = g[2 * h + 1];
-                    packed[h].x = pack_bf16x2(a.x * scale * ga.x, a.y * scale * ga.y);
-                    packed[h].y = pack_bf16x2(a.z * scale * ga.z, a.w * scale * ga.w);
-                    packed[h].z = pack_bf16x2(e2.x * scale * gb.x, e2.y * scale * gb.y);
-                    packed[h].w = pack_bf16x2(e2.z * scale * gb.z, e2.w * scale * gb.w);
-                }
-            }
-            xs[xs_index(c, 2 * lane)] = packed[0];
-            xs[xs_index(c, 2 * lane + 1)] = packed[1];
-        }
-        __syncthreads();
-        each(ch);
-    }
-}
-
-// Bf16 vectors [B][K] of the tile's rows into xs, chunk by chunk through `each(chunk)`. Every
-// chunk's vectors are loaded first (MAXC chunks at most), so that the chunks cost one round trip
-// to memory, not one each.
-template <int MAXC, typename Each>
-__device__ void stage_raw(const uint16_t* __restrict__ xb, int B, int K, int tile, uint4* xs, Each each) {
-    constexpr int per_thread = 16 * (CHUNK_COLS / 8) / GEMV_THREADS;  // uint4 per chunk
-    const int chunks = K / CHUNK_COLS;
-    uint4 v[MAXC][per_thread];
-#pragma unroll
-    for (int ch = 0; ch < MAXC; ++ch)
-#pragma unroll
-        for (int j = 0; j < per_thread; ++j) {
-            const int i = threadIdx.x + j * GEMV_THREADS;
-            const int c = i / (CHUNK_COLS / 8), g8 = i % (CHUNK_COLS / 8);
-            const int b = tile * 16 + c;
-            v[ch][j] = make_uint4(0, 0, 0, 0);
-            if (ch < chunks && b < B) v[ch][j] = load16(xb + (size_t)b * K + (size_t)ch * CHUNK_COLS + g8 * 8);
-        }
-#pragma unroll
-    for (int ch = 0; ch < MAXC; ++ch) {
-        if (ch >= chunks) break;
-        if (ch > 0) __syncthreads();
-#pragma unroll
-        for (int j = 0; j < per_thread; ++j) {
-            const int i = threadIdx.x + j * GEMV_THREADS;
-            xs[xs_index(i / (CHUNK_COLS / 8), i % (CHUNK_COLS / 8))] = v[ch][j];
-        }
-        __syncthreads();
-        each(ch);
-    }
-}
-
-// One wave's chains for strips `strip[s]` (R rows each) of W [N][K] against the tile, over every
-// chunk. The weights of all its k-blocks are loaded first, so that they are in flight while the
-// vectors are staged; the products of chunk c follow its staging.
-template <int S, int R, int MAXC>
-struct Gemv {
-    f32x4 acc[S];
-    uint4 wf[MAXC][PER_WAVE][S];
-
-    __device__ void load(const uint16_t* __restrict__ w, const int (&strip)[S], int kblocks) {
-        const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-        const int chunks = kblocks / CHUNK_KB;
-        const bool live = lane % 16 < R;
-#pragma unroll
-        for (int c = 0; c < MAXC; ++c)
-#pragma unroll
-            for (int j = 0; j < PER_WAVE; ++j)
-#pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    wf[c][j][s] = make_uint4(0, 0, 0, 0);
-                    if (c < chunks && live)
-                        wf[c][j][s] = load16(w + weight_tile_index(strip[s], c * CHUNK_KB + wave * PER_WAVE + j, kblocks, R) +
-                                             weight_lane_offset(lane, R));
-                }
-#pragma unroll
-        for (int s = 0; s < S; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    // The products of chunk c, once it is staged.
-    __device__ void chunk(int c, const uint4* xs) {
-        const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-#pragma unroll
-        for (int cc = 0; cc < MAXC; ++cc) {
-            if (cc != c) continue;  // registers indexed by constants only
-#pragma unroll
-            for (int j = 0; j < PER_WAVE; ++j) {
-                const uint4 xv = xs[(wave * PER_WAVE + j) * 64 + lane];
-#pragma unroll
-                for (int s = 0; s < S; ++s) acc[s] = mfma16(wf[cc][j][s], xv, acc[s]);
-            }
+            const float total = wave_sum(t);
+            if (lane == 0) scale[2 * w + h] = 1.0f / sqrtf(total / (float)(CH * CHUNK_COLS) + eps);
         }
     }
 };
 
-// Every wave's chains into red, [wave][s][lane] as f32x4, behind barriers (red shares memory
-// with the staged vectors).
+// One wave's chains for strips `strip[s]` (R rows each, in MFMA rows 0..R-1) of W [N][CH chunks]
+// against its k-blocks of the tile, k-block after k-block.
+template <int S, int CH, int R = 16>
+struct Gemv {
+    static constexpr int KB = CH * PER_WAVE;
+    f32x4 acc[S];
+    uint4 wf[KB][S];
+
+    __device__ void load(const uint16_t* __restrict__ w, const int (&strip)[S]) {
+        constexpr int kblocks = CH * CHUNK_KB;
+        const int lane = threadIdx.x % WAVE;
+        // Lanes past the strip's rows read its last row again.
+        const int off = weight_lane_offset((lane / 16) * 16 + min(lane % 16, R - 1), R);
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+#pragma unroll
+            for (int s = 0; s < S; ++s) wf[i][s] = load16(w + weight_tile_index(strip[s], Operand<CH>::kblock(i), kblocks, R) + off);
+    }
+
+    __device__ void run(const uint4 (&xf)[KB]) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+#pragma unroll
+            for (int s = 0; s < S; ++s) acc[s] = mfma16(wf[i][s], xf[i], acc[s]);
+    }
+};
+
+// Every wave's chains into red, [wave][s][lane] as f32x4 (and, when sq is set, every lane's
+// squares into sq), behind a barrier.
 template <int S>
-__device__ void spill(const f32x4 (&acc)[S], f32x4* red) {
+__device__ void spill(const f32x4 (&acc)[S], f32x4* red, float* sq = nullptr, float squares = 0.f) {
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    __syncthreads();
 #pragma unroll
     for (int s = 0; s < S; ++s) red[(w * S + s) * 64 + lane] = acc[s];
+    if (sq) sq[threadIdx.x] = squares;
+    __syncthreads();
+}
+
+// The tile's rows' scales from every lane's squares in sq (lane 16 g + t of wave w: row t), added
+// wave by wave, g within a wave, into scale[t] = 1 / sqrt(sum / K + eps), behind a barrier.
+__device__ void row_scales(const float* sq, int K, float eps, float* scale) {
+    if (threadIdx.x < 16) {
+        float total = 0.f;
+        for (int w = 0; w < GEMV_WAVES; ++w)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) total += sq[w * WAVE + g * 16 + threadIdx.x];
+        scale[threadIdx.x] = 1.0f / sqrtf(total / (float)K + eps);
+    }
     __syncthreads();
 }
 
@@ -233,104 +238,167 @@ __device__ __forceinline__ long block_of(const DecodeArgs& a, uint32_t slot, uin
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
-// gemv_qkv_rope: workgroup (strip, tile): a strip of R permuted rows (R/2 RoPE pairs of a head).
-template <int R, int MAXC>
+// gemv_qkv_rope: workgroup (strip, tile): a strip of 16 permuted rows (8 RoPE pairs of a head).
+// PRENORMED: the input comes as x input_norm in bf16 with its sums of squares (every layer past
+// the first), else as the f32 rows. The epilogue's thread (p, c) (pair p, tile row c; the first
+// 128 threads) loads its row's position and slot first of all, and the RoPE factors and cache
+// block that hang on them while the products' operands are on their way.
+template <int CH, bool PRENORMED>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, LayerArgs l) {
-    __shared__ uint4 xs[CHUNK_KB * 64];
-    __shared__ float scales[16];
-    const int K = a.hidden, kblocks = K / 32;
+    constexpr int R = QKV_ROWS;
+    constexpr int EPI = (R / 2) * 16;  // epilogue threads
+    __shared__ f32x4 red[GEMV_WAVES * 64];
+    __shared__ float sq[GEMV_THREADS], scale[16];
     const int strip_id = blockIdx.x, tile = blockIdx.y;
     const int strip[1] = {strip_id};
-    Gemv<1, R, MAXC> g;
-    g.load(l.qkv, strip, kblocks);
-    stage_normed(l.x, l.input_norm, a.eps, a.rows, K, tile, xs, scales, [&](int ch) { g.chunk(ch, xs); });
-    f32x4* red = reinterpret_cast<f32x4*>(xs);
-    spill<1>(g.acc, red);
-
+    const int p = threadIdx.x % (R / 2), c = (threadIdx.x / (R / 2)) % 16;
+    const int b = tile * 16 + c;
     const int per_head = HEAD_DIM / R;  // strips to a head
     const int head = strip_id / per_head;
+    const int i = (strip_id % per_head) * (R / 2) + p;  // the pair's first dimension in the head
+    uint32_t pos = 0, slot = 0;
+    if (threadIdx.x < EPI) {  // whole waves
+        pos = a.positions[min(b, a.rows - 1)];
+        slot = a.slots[min(b, a.rows - 1)];
+    }
+    RowSquares<CH> squares;
+    RawRows<CH> xb;
+    NormedRows<CH> xn;
+    if constexpr (PRENORMED) {
+        squares.load(l.x_sq, a.rows, tile);
+        xb.load(l.xn, a.rows, tile);
+    } else {
+        xn.load(l.x, l.input_norm, a.rows, tile);
+    }
+    Gemv<1, CH, R> g;
+    g.load(l.qkv, strip);
+    if (PRENORMED || CH <= 2) all_issued();  // past two chunks the f32 rows would take too many registers
+    float co = 1.f, si = 0.f;
+    uint32_t entry = UINT32_MAX;
+    if (threadIdx.x < EPI) {
+        // 32-bit indexes (the tables hold far fewer than 2^32 entries)
+        const uint32_t pc = min(pos, (uint32_t)a.capacity - 1), sc = min(slot, (uint32_t)a.nslots - 1);
+        const uint32_t at = pc * (HEAD_DIM / 2) + (uint32_t)i;
+        co = a.cos[at];
+        si = a.sin[at];
+        // The product kept apart from the add: fused, they make a 64-bit multiply-add whose unused
+        // high half the register allocator takes from a register a load in flight is to fill, so
+        // that it waits for every load before this one.
+        uint32_t row = sc * (uint32_t)a.max_blocks;
+        asm volatile("" : "+v"(row));
+        entry = a.table[row + pc / BLOCK_TOKENS];
+    }
+    if constexpr (PRENORMED) {
+        squares.finish(a.eps, scale);
+        g.run(xb.xf);
+        spill<1>(g.acc, red);
+    } else {
+        xn.finish();
+        g.run(xn.xf);
+        spill<1>(g.acc, red, sq, xn.squares);
+        row_scales(sq, a.hidden, a.eps, scale);
+    }
+
     const int H = a.heads, KV = a.kv_heads;
-    for (int idx = threadIdx.x; idx < (R / 2) * 16; idx += GEMV_THREADS) {
-        const int p = idx % (R / 2), c = idx / (R / 2);
-        const int b = tile * 16 + c;
-        uint32_t pos, slot;
-        if (b >= a.rows || !placed(a, b, pos, slot)) continue;
-        const int i = (strip_id % per_head) * (R / 2) + p;  // the pair's first dimension in the head
-        float va = reduced<1>(red, 0, p, c);
-        float vc = reduced<1>(red, 0, p + R / 2, c);
-        if (head < H + KV && a.rope) {
-            // As upstream: x cos + rotate_half(x) sin (gemv_qkv_rope.comp:88-94).
-            const float co = a.cos[(size_t)pos * (HEAD_DIM / 2) + i];
-            const float si = a.sin[(size_t)pos * (HEAD_DIM / 2) + i];
-            const float ra = va * co - vc * si;
-            const float rc = vc * co + va * si;
-            va = ra;
-            vc = rc;
-        }
-        if (head < H) {
-            uint16_t* q = l.q + ((size_t)b * H + head) * HEAD_DIM;
-            q[i] = (uint16_t)bf16_bits(va);
-            q[i + HEAD_DIM / 2] = (uint16_t)bf16_bits(vc);
-            continue;
-        }
-        const long blk = block_of(a, slot, pos);
-        if (blk < 0) continue;
-        const int kv = head < H + KV ? head - H : head - H - KV;
-        uint16_t* tl = l.kv + ((size_t)blk * KV + kv) * 2 * KV_TILE;
-        const int pp = (int)(pos % BLOCK_TOKENS);
-        if (head < H + KV) {
-            tl[key_index(pp, i)] = (uint16_t)bf16_bits(va);
-            tl[key_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
-        } else {
-            tl[KV_TILE + value_index(pp, i)] = (uint16_t)bf16_bits(va);
-            tl[KV_TILE + value_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
-        }
+    if (threadIdx.x >= EPI || b >= a.rows || pos >= (uint32_t)a.capacity || slot >= (uint32_t)a.nslots) return;
+    float va = reduced<1>(red, 0, p, c) * scale[c];
+    float vc = reduced<1>(red, 0, p + R / 2, c) * scale[c];
+    if (head < H + KV && a.rope) {
+        // As upstream: x cos + rotate_half(x) sin (gemv_qkv_rope.comp:88-94).
+        const float ra = va * co - vc * si;
+        const float rc = vc * co + va * si;
+        va = ra;
+        vc = rc;
+    }
+    if (head < H) {
+        uint16_t* q = l.q + ((size_t)b * H + head) * HEAD_DIM;
+        q[i] = (uint16_t)bf16_bits(va);
+        q[i + HEAD_DIM / 2] = (uint16_t)bf16_bits(vc);
+        return;
+    }
+    if (entry >= (uint32_t)a.nblocks) return;  // the slot holds no block there
+    const int kv = head < H + KV ? head - H : head - H - KV;
+    uint16_t* tl = l.kv + ((size_t)entry * KV + kv) * 2 * KV_TILE;
+    const int pp = (int)(pos % BLOCK_TOKENS);
+    if (head < H + KV) {
+        tl[key_index(pp, i)] = (uint16_t)bf16_bits(va);
+        tl[key_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
+    } else {
+        tl[KV_TILE + value_index(pp, i)] = (uint16_t)bf16_bits(va);
+        tl[KV_TILE + value_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
     }
 }
 
 // ---------------------------------------------------------------------------------------------
-// gemv_gate_up: workgroup (s, tile): strip s (16 rows) of the gate and the same strip of up.
-template <int MAXC>
+// gemv_gate_up: workgroup (s, tile): strip s (16 rows) of the gate and the same strip of up,
+// against mid post_norm in bf16 and mid's sums of squares.
+template <int CH>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_gate_up(DecodeArgs a, LayerArgs l) {
-    __shared__ uint4 xs[CHUNK_KB * 64];
-    __shared__ float scales[16];
-    const int K = a.hidden, kblocks = K / 32;
+    __shared__ f32x4 red[GEMV_WAVES * 2 * 64];
+    __shared__ float scale[16];
     const int s = blockIdx.x, tile = blockIdx.y;
     const int strip[2] = {s, s + a.inner / 16};
-    Gemv<2, 16, MAXC> g;
-    g.load(l.gate_up, strip, kblocks);
-    stage_normed(l.mid, l.post_norm, a.eps, a.rows, K, tile, xs, scales, [&](int ch) { g.chunk(ch, xs); });
-    f32x4* red = reinterpret_cast<f32x4*>(xs);
+    RowSquares<CH> squares;
+    RawRows<CH> x;
+    Gemv<2, CH> g;
+    squares.load(l.mid_sq, a.rows, tile);
+    x.load(l.mid_n, a.rows, tile);
+    g.load(l.gate_up, strip);
+    all_issued();
+    squares.finish(a.eps, scale);
+    g.run(x.xf);
     spill<2>(g.acc, red);
     for (int idx = threadIdx.x; idx < 16 * 16; idx += GEMV_THREADS) {
         const int r = idx % 16, c = idx / 16;
         const int b = tile * 16 + c;
         if (b >= a.rows) continue;
-        const float gate = reduced<2>(red, 0, r, c);
-        const float up = reduced<2>(red, 1, r, c);
+        const float gate = reduced<2>(red, 0, r, c) * scale[c];
+        const float up = reduced<2>(red, 1, r, c) * scale[c];
         l.mlp[(size_t)b * a.inner + s * 16 + r] = (uint16_t)bf16_bits(gate / (1.0f + __expf(-gate)) * up);
     }
 }
 
 // ---------------------------------------------------------------------------------------------
-// gemv_residual: out = residual + W x; workgroup (strip, tile) over the whole of K.
-template <int R, int MAXC>
+// gemv_residual: out = residual + W x, workgroup (strip, tile): a strip of R rows over the whole
+// of K. The epilogue's thread (c, q) (tile row c, rows 4 q .. 4 q + 3 of the strip; the first
+// 4 R threads) loads its residual and next-norm gains first of all, and with
+// next_norm set also writes out next_norm in bf16 and the 4 rows' sum of squares, in row order.
+template <int CH, int R>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, ResidualArgs r) {
-    __shared__ uint4 xs[CHUNK_KB * 64];
-    const int kblocks = r.K / 32;
+    constexpr int EPI = 16 * (R / SQ_COLS);
+    constexpr int LOADERS = EPI < WAVE ? WAVE : EPI;  // whole waves load (past EPI, the same again)
+    static_assert(LOADERS % WAVE == 0, "whole waves");
+    __shared__ f32x4 red[GEMV_WAVES * 64];
     const int strip_id = blockIdx.x, tile = blockIdx.y;
     const int strip[1] = {strip_id};
-    Gemv<1, R, MAXC> g;
-    g.load(r.w, strip, kblocks);
-    stage_raw<MAXC>(r.x, a.rows, r.K, tile, xs, [&](int ch) { g.chunk(ch, xs); });
-    f32x4* red = reinterpret_cast<f32x4*>(xs);
+    const int c = threadIdx.x % 16, q = (threadIdx.x / 16) % (R / SQ_COLS);
+    const int b = tile * 16 + c;
+    const int n0 = strip_id * R + q * SQ_COLS;
+    float4 res = make_float4(0.f, 0.f, 0.f, 0.f), gain = res;
+    if (threadIdx.x < LOADERS) {
+        res = load_f4(r.residual + (size_t)min(b, a.rows - 1) * r.N + n0);
+        gain = load_f4((r.next_norm ? r.next_norm : r.residual) + n0);
+    }
+    RawRows<CH> x;
+    Gemv<1, CH, R> g;
+    x.load(r.x, a.rows, tile);
+    g.load(r.w, strip);
+    all_issued();
+    g.run(x.xf);
     spill<1>(g.acc, red);
-    for (int idx = threadIdx.x; idx < R * 16; idx += GEMV_THREADS) {
-        const int row = idx % R, c = idx / R;
-        const int b = tile * 16 + c;
-        if (b >= a.rows) continue;
-        const size_t at = (size_t)b * r.N + strip_id * R + row;
-        r.out[at] = r.residual[at] + reduced<1>(red, 0, row, c);
+    if (threadIdx.x >= EPI || b >= a.rows) return;
+    const float4 v = make_float4(res.x + reduced<1>(red, 0, q * 4, c), res.y + reduced<1>(red, 0, q * 4 + 1, c),
+                                 res.z + reduced<1>(red, 0, q * 4 + 2, c), res.w + reduced<1>(red, 0, q * 4 + 3, c));
+    const size_t at = (size_t)b * r.N + n0;
+    *reinterpret_cast<float4*>(r.out + at) = v;
+    if (r.next_norm) {
+        *reinterpret_cast<uint2*>(r.out_n + at) =
+            make_uint2(pack_bf16x2(v.x * gain.x, v.y * gain.y), pack_bf16x2(v.z * gain.z, v.w * gain.w));
+        float s2 = v.x * v.x;
+        s2 += v.y * v.y;
+        s2 += v.z * v.z;
+        s2 += v.w * v.w;
+        r.out_sq[(size_t)b * (r.N / SQ_COLS) + n0 / SQ_COLS] = s2;
     }
 }
 
@@ -461,29 +529,33 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
 }
 
 // ---------------------------------------------------------------------------------------------
-// final_rmsnorm: the final norm, a wave to a row; with `advance`, moves each placed row on by one
-// position once the step is done with it.
-__global__ void __launch_bounds__(WAVE) final_rmsnorm(DecodeArgs a, const float* __restrict__ x,
-                                                      const float* __restrict__ gain, float* __restrict__ out,
-                                                      uint32_t* positions, int advance) {
+// final_rmsnorm: the final norm, a wave to a row, for hidden = CH 1024; with `advance`, moves each
+// placed row on by one position once the step is done with it.
+template <int CH>
+__global__ void __launch_bounds__(WAVE) final_rmsnorm(DecodeArgs a, const float* __restrict__ x, const float* __restrict__ gain,
+                                                      float* __restrict__ out, uint32_t* positions, int advance) {
+    constexpr int K = CH * CHUNK_COLS, V = K / WAVE / 4;  // float4 to a lane
     const int b = blockIdx.x, lane = threadIdx.x;
-    const int K = a.hidden, per_lane = K / WAVE;
-    const float* row = x + (size_t)b * K + lane * per_lane;
+    const size_t at = (size_t)b * K + lane * (K / WAVE);
+    float4 v[V], g[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        v[e] = *reinterpret_cast<const float4*>(x + at + 4 * e);
+        g[e] = *reinterpret_cast<const float4*>(gain + lane * (K / WAVE) + 4 * e);
+    }
     float squares = 0.f;
-    for (int e = 0; e < per_lane; e += 4) {
-        float4 v = *reinterpret_cast<const float4*>(row + e);
-        squares += v.x * v.x;
-        squares += v.y * v.y;
-        squares += v.z * v.z;
-        squares += v.w * v.w;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        squares += v[e].x * v[e].x;
+        squares += v[e].y * v[e].y;
+        squares += v[e].z * v[e].z;
+        squares += v[e].w * v[e].w;
     }
     const float scale = 1.0f / sqrtf(wave_sum(squares) / (float)K + a.eps);
-    for (int e = 0; e < per_lane; e += 4) {
-        float4 v = *reinterpret_cast<const float4*>(row + e);
-        float4 g = *reinterpret_cast<const float4*>(gain + lane * per_lane + e);
-        float4 r = make_float4(v.x * scale * g.x, v.y * scale * g.y, v.z * scale * g.z, v.w * scale * g.w);
-        *reinterpret_cast<float4*>(out + (size_t)b * K + lane * per_lane + e) = r;
-    }
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+        *reinterpret_cast<float4*>(out + at + 4 * e) =
+            make_float4(v[e].x * scale * g[e].x, v[e].y * scale * g[e].y, v[e].z * scale * g[e].z, v[e].w * scale * g[e].w);
     if (advance && lane == 0) {
         const uint32_t pos = positions[b];
         if (pos < (uint32_t)a.capacity) positions[b] = pos + 1;
@@ -495,47 +567,60 @@ __global__ void __launch_bounds__(WAVE) final_rmsnorm(DecodeArgs a, const float*
 
 namespace {
 
-
 size_t attention_lds(const DecodeArgs& a) { return (size_t)ATTN_WAVES * (a.heads / a.kv_heads) * (HEAD_DIM + 1) * 4; }
 
-template <int R>
-hipError_t launch_layer_r(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
-                          const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer) {
-    const int tiles = decode_tiles(a.rows);
-    const int qkv_strips = (a.heads + 2 * a.kv_heads) * HEAD_DIM / R;
-    const bool wide = a.hidden > CHUNK_COLS;
-    const dim3 block(GEMV_THREADS);
-    if (wide)
-        dispatch("gemv_qkv_rope", gemv_qkv_rope<R, MAX_CHUNKS>, dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
+// The kernel instantiated for `chunks` chunks of K (1 to MAX_CHUNKS, checked by the shape).
+template <template <int> class Pick>
+auto by_chunks(int chunks) -> decltype(Pick<1>::get()) {
+    switch (chunks) {
+        case 2: return Pick<2>::get();
+        case 3: return Pick<3>::get();
+        case 4: return Pick<4>::get();
+        default: return Pick<1>::get();
+    }
+}
+template <int CH> struct PickQkv { static auto get() { return gemv_qkv_rope<CH, false>; } };
+template <int CH> struct PickQkvNormed { static auto get() { return gemv_qkv_rope<CH, true>; } };
+template <int CH> struct PickGateUp { static auto get() { return gemv_gate_up<CH>; } };
+template <int CH> struct PickResidual4 { static auto get() { return gemv_residual<CH, 4>; } };
+template <int CH> struct PickResidual16 { static auto get() { return gemv_residual<CH, 16>; } };
+template <int CH> struct PickFinal { static auto get() { return final_rmsnorm<CH>; } };
+
+hipError_t residual(const char* label, const DecodeArgs& a, const ResidualArgs& r, hipStream_t stream, DispatchTimer* timer) {
+    const dim3 grid(r.N / r.R, decode_tiles(a.rows)), block(GEMV_THREADS);
+    const int chunks = r.K / CHUNK_COLS;
+    if (r.R == 4)
+        dispatch(label, by_chunks<PickResidual4>(chunks), grid, block, 0, stream, timer, a, r);
+    else if (r.R == 16)
+        dispatch(label, by_chunks<PickResidual16>(chunks), grid, block, 0, stream, timer, a, r);
     else
-        dispatch("gemv_qkv_rope", gemv_qkv_rope<R, 1>, dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
-    dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), attention_lds(a), stream, timer, a, l);
-    if (o.K > CHUNK_COLS)
-        dispatch("o_proj", gemv_residual<R, MAX_CHUNKS>, dim3(o.N / R, tiles), block, 0, stream, timer, a, o);
-    else
-        dispatch("o_proj", gemv_residual<R, 1>, dim3(o.N / R, tiles), block, 0, stream, timer, a, o);
-    if (wide)
-        dispatch("gemv_gate_up", gemv_gate_up<MAX_CHUNKS>, dim3(a.inner / 16, tiles), block, 0, stream, timer, a, l);
-    else
-        dispatch("gemv_gate_up", gemv_gate_up<1>, dim3(a.inner / 16, tiles), block, 0, stream, timer, a, l);
-    if (down.K > CHUNK_COLS)
-        dispatch("down_proj", gemv_residual<R, MAX_CHUNKS>, dim3(down.N / R, tiles), block, 0, stream, timer, a, down);
-    else
-        dispatch("down_proj", gemv_residual<R, 1>, dim3(down.N / R, tiles), block, 0, stream, timer, a, down);
-    return hipGetLastError();
+        return hipErrorInvalidValue;
+    return hipSuccess;
 }
 
 }  // namespace
 
+hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o, const ResidualArgs& down,
+                               hipStream_t stream, DispatchTimer* timer) {
+    const int tiles = decode_tiles(a.rows);
+    const int qkv_strips = (a.heads + 2 * a.kv_heads) * HEAD_DIM / QKV_ROWS;
+    const dim3 block(GEMV_THREADS);
+    const int hidden_chunks = a.hidden / CHUNK_COLS;
+    if (l.xn)
+        dispatch("gemv_qkv_rope", by_chunks<PickQkvNormed>(hidden_chunks), dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
+    else
+        dispatch("gemv_qkv_rope", by_chunks<PickQkv>(hidden_chunks), dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
+    dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), attention_lds(a), stream, timer, a, l);
+    hipError_t e = residual("o_proj", a, o, stream, timer);
+    if (e != hipSuccess) return e;
+    dispatch("gemv_gate_up", by_chunks<PickGateUp>(hidden_chunks), dim3(a.inner / 16, tiles), block, 0, stream, timer, a, l);
+    if ((e = residual("down_proj", a, down, stream, timer)) != hipSuccess) return e;
+    return hipGetLastError();
+}
+
 int decode_tiles(int rows) { return (rows + 15) / 16; }
 
-// Strips of 4 or 8 rows spread a small batch's projections over more CUs, but measured no faster
-// than 16 on MI355X (each launch's time is set by its chain of memory round trips, not by how
-// many CUs stream its weights), so every batch takes 16: one weight layout, the prefill's too.
-int decode_strip_rows(int rows) {
-    (void)rows;
-    return 16;
-}
+int decode_residual_rows(int rows) { return rows <= 16 ? 4 : 16; }
 
 int decode_max_k() { return MAX_CHUNKS * CHUNK_COLS; }
 
@@ -549,18 +634,10 @@ hipError_t decode_prepare(size_t device_lds) {
 
 size_t decode_attention_lds(int heads, int kv_heads) { return (size_t)ATTN_WAVES * (heads / kv_heads) * (HEAD_DIM + 1) * 4; }
 
-hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
-                               const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer) {
-    switch (decode_strip_rows(a.rows)) {
-        case 4: return launch_layer_r<4>(a, l, o, down, stream, timer);
-        case 8: return launch_layer_r<8>(a, l, o, down, stream, timer);
-        default: return launch_layer_r<16>(a, l, o, down, stream, timer);
-    }
-}
-
-hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out,
-                             uint32_t* positions, int advance, hipStream_t stream, DispatchTimer* timer) {
-    dispatch("final_norm", final_rmsnorm, dim3(a.rows), dim3(WAVE), 0, stream, timer, a, x, gain, out, positions, advance);
+hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out, uint32_t* positions,
+                             int advance, hipStream_t stream, DispatchTimer* timer) {
+    dispatch("final_norm", by_chunks<PickFinal>(a.hidden / CHUNK_COLS), dim3(a.rows), dim3(WAVE), 0, stream, timer, a, x, gain,
+             out, positions, advance);
     return hipGetLastError();
 }
 

@@ -25,28 +25,43 @@ struct DecodeArgs {
     const float* sin;
 };
 
-// One layer's tensors.
+// One layer's tensors. A norm's input comes as the f32 rows and, past layer 0, also as the rows
+// times the norm's gain in bf16 with their sums of squares over each 4 columns, which the
+// projection that wrote the rows left (ResidualArgs::next_norm): the consumer then reads 2 bytes a
+// column and adds the row's sums in a fixed order.
 struct LayerArgs {
     const float* x;           // layer input [rows][hidden] f32
+    const uint16_t* xn;       // x input_norm in bf16 [rows][hidden], or null: taken from x
+    const float* x_sq;        // [rows][hidden / 4]
     const float* input_norm;  // [hidden] f32
     const uint16_t* qkv;      // tiled bf16, rows permuted (qkv_row_of)
     uint16_t* q;              // [rows][heads][64] bf16
     uint16_t* kv;             // the layer's cache pool: [blocks][kv_heads][key tile, value tile]
     uint16_t* attended;       // [rows][heads 64] bf16
-    const float* mid;         // [rows][hidden] f32, o_proj's output
-    const float* post_norm;   // [hidden] f32
+    const uint16_t* mid_n;    // o_proj's output times post_norm in bf16 [rows][hidden]
+    const float* mid_sq;      // [rows][hidden / 4]
     const uint16_t* gate_up;  // tiled bf16 [2 inner][hidden]
     uint16_t* mlp;            // [rows][inner] bf16
 };
 
-// out = residual + W x, W tiled [N][K].
+// out = residual + W x, W in R-row tiles of [N][K]; with next_norm set, also out next_norm in
+// bf16 and out's sums of squares over each 4 columns, for the norm that reads out next.
 struct ResidualArgs {
     const uint16_t* w;
     const uint16_t* x;  // [rows][K] bf16
     int K, N;
+    int R;                  // strip height of w: 4 or 16
     const float* residual;  // [rows][N]
     float* out;             // [rows][N]
+    const float* next_norm; // [N], or null
+    uint16_t* out_n;        // [rows][N]
+    float* out_sq;          // [rows][N / 4]
 };
+
+// The strip height of o_proj and down_proj for a batch of `rows`: 4 while the batch is one
+// 16-row tile (spreading their few output rows over every CU), 16 past it (each workgroup's
+// vectors then serve 16 rows).
+int decode_residual_rows(int rows);
 
 // Per-dispatch timing of a step launched without its graph: each dispatch takes the next pair of
 // events, recorded by the kernel's own dispatch (hipExtLaunchKernelGGL), so that the time between
@@ -58,18 +73,16 @@ struct DispatchTimer {
     int used = 0, capacity = 0;
 };
 
-// Tiles of 16 rows a batch of `rows` takes, the height of the projections' weight strips at
-// that batch (4, 8 or 16: the layout their weights are kept in), the longest K the projections
-// take, and the LDS the attention takes.
+// Tiles of 16 rows a batch of `rows` takes, the longest K the projections take, and the LDS the
+// attention takes.
 int decode_tiles(int rows);
-int decode_strip_rows(int rows);
 int decode_max_k();
 size_t decode_attention_lds(int heads, int kv_heads);
 // Lets the attention take up to `device_lds` bytes of LDS per workgroup.
 hipError_t decode_prepare(size_t device_lds);
-hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o,
-                               const ResidualArgs& down, hipStream_t stream, DispatchTimer* timer = nullptr);
-hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out,
-                             uint32_t* positions, int advance, hipStream_t stream, DispatchTimer* timer = nullptr);
+hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o, const ResidualArgs& down,
+                               hipStream_t stream, DispatchTimer* timer = nullptr);
+hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out, uint32_t* positions,
+                             int advance, hipStream_t stream, DispatchTimer* timer = nullptr);
 
 }  // namespace tgx

@@ -34,12 +34,24 @@ __device__ __forceinline__ uint32_t bf16_bits(float f) { return pack_bf16x2(f, 0
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// The sum over the wave's 64 lanes, the same in every lane: a butterfly, then lane 0's value
-// broadcast, so that every lane uses one rounding of it.
+// The sum over the wave's 64 lanes, the same in every lane, in a fixed order: DPP moves within
+// each row of 16 lanes (adjacent pairs, then quads, then the mirrored half row, then the
+// mirrored row; each step adds two partial sums taken in the same order, so every lane of a row
+// ends with the same value), then the four rows' sums read out and added in row order. No LDS
+// round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
-    return __shfl(v, 0, WAVE);
+    v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_move<0x141>(v);  // row_half_mirror
+    v += dpp_move<0x140>(v);  // row_mirror
+    return ((lane_value(v, 0) + lane_value(v, 16)) + lane_value(v, 32)) + lane_value(v, 48);
 }
 
 // ---- LDS staged by direct global-to-LDS loads, several stages in flight ----
@@ -85,26 +97,6 @@ __device__ __forceinline__ void load_to_lds(const void* src, void* lds) {
     __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)lds, 16, 0, 0);
 }
 
-// The same kind of sum from DPP moves within each row of 16 lanes (adjacent pairs, then quads,
-// then the mirrored half row, then the mirrored row: each step adds two equal-order partial
-// sums, so every lane of a row ends with the same value), then the four rows' sums read out and
-// added in row order. No LDS round trip; the result is uniform across the wave.
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-    v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-    v += dpp_move<0x141>(v);  // row_half_mirror
-    v += dpp_move<0x140>(v);  // row_mirror
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return ((r0 + r1) + r2) + r3;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
@@ -124,6 +116,18 @@ __host__ __device__ constexpr size_t weight_tile_index(int strip, int kb, int kb
 }
 __host__ __device__ constexpr int weight_lane_offset(int lane, int R) {
     return ((lane / 16) * R + lane % 16) * 8;
+}
+
+// The strip height of q/k/v and gate/up (the MFMA's rows); o_proj and down_proj take 4 or 16 by
+// the batch (decode_residual_rows).
+constexpr int QKV_ROWS = 16;
+
+// Lane `lane`'s 16 bytes of the full 16-row fragment (strip S of 16 rows, k-block kb) of W kept
+// in R-row strips: its rows r come from strip 16 S / R + r / R. For R = 16 this is lane 8.
+template <int R>
+__host__ __device__ constexpr size_t fragment_index(int S, int kb, int kblocks, int lane) {
+    return weight_tile_index(S * (16 / R) + (lane % 16) / R, kb, kblocks, R) +
+           weight_lane_offset((lane / 16) * 16 + (lane % 16) % R, R);
 }
 
 // The q/k/v projection's rows are permuted so that each strip of R holds R/2 of a head's RoPE

@@ -88,7 +88,7 @@ tgx_status launch(Decoder* d) {
     for (int l = 0; l < s.layers; ++l) {
         const Layer& L = d->layers[l];
         layers[l] = PrefillLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm,
-                                 d->kv + (size_t)l * d->nblocks * s.kv_heads * 2 * KV_TILE};
+                                 d->kv + (size_t)l * d->nblocks * s.kv_heads * 2 * KV_TILE, d->od_rows};
     }
     PrefillBuffers b{p.x, p.h, p.mid, p.normed, p.q, p.attended, p.mlp, p.out, p.tiles, p.ntiles};
     if (d->timed) d->timer.used = 0;

@@ -43,7 +43,7 @@ static_assert(PF_THREADS == TM, "the q/k/v epilogue stages a row to a thread");
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
 struct GemmArgs {
-    const uint16_t* w;  // 16-row tiles of [N][K]
+    const uint16_t* w;  // tiles of [N][K] in WR-row strips (the kernel's template argument)
     const uint16_t* x;  // bf16 [M_pad][K]
     int K, N;
     // epilogues
@@ -72,7 +72,9 @@ __device__ __forceinline__ int stage_strip(int nb, int sl, int N) {
     return strip_of<EPI>(nb, sl / 8, sl % 8, N);
 }
 
-template <int EPI>
+// W in strips of WR rows (o_proj and down_proj: 4 or 16, the rest 16), gathered into 16-row
+// fragments as it lands in LDS.
+template <int EPI, int WR = QKV_ROWS>
 __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmArgs g) {
     extern __shared__ uint4 lds[];
     uint4* ws = lds;                     // [NBUF][W_STAGE]
@@ -94,7 +96,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
         for (int j = 0; j < FRAGS; ++j) {
             const int f = w * FRAGS + j;
             if (f < W_STRIPS) {
-                const uint16_t* src = g.w + weight_tile_index(stage_strip<EPI>(nb, f, g.N), st, kblocks, 16) + lane * 8;
+                const uint16_t* src = g.w + fragment_index<WR>(stage_strip<EPI>(nb, f, g.N), st, kblocks, lane);
                 load_to_lds(src, &ws[buf * W_STAGE + f * 64]);
             } else {
                 const int mt = f - W_STRIPS;
@@ -470,7 +472,8 @@ hipError_t allow(const void* kernel, size_t device_lds) {
 hipError_t prefill_prepare(size_t device_lds) {
     hipError_t e;
     if ((e = allow((const void*)prefill_gemm<EPI_QKV>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16>, device_lds)) != hipSuccess) return e;
     return allow((const void*)prefill_gemm<EPI_SILU>, device_lds);
 }
 
@@ -497,14 +500,16 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
             case 16: dispatch("prefill_attention", prefill_attention<8, 4>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
             default: return hipErrorInvalidValue;
         }
+        auto residual_gemm = L.od_rows == 4 ? prefill_gemm<EPI_RESIDUAL, 4> : prefill_gemm<EPI_RESIDUAL, 16>;
+        if (L.od_rows != 4 && L.od_rows != 16) return hipErrorInvalidValue;
         GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr};
-        dispatch("prefill_o", prefill_gemm<EPI_RESIDUAL>, dim3(a.hidden / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, o);
+        dispatch("prefill_o", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, o);
         dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.mid, L.post_norm,
                  b.normed, (float*)nullptr);
         GemmArgs gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, nullptr, b.mlp, nullptr, nullptr};
         dispatch("prefill_gate_up", prefill_gemm<EPI_SILU>, dim3(2 * a.inner / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, gu);
         GemmArgs down{L.down, b.mlp, a.inner, a.hidden, b.mid, b.h, nullptr, nullptr, nullptr};
-        dispatch("prefill_down", prefill_gemm<EPI_RESIDUAL>, dim3(a.hidden / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, down);
+        dispatch("prefill_down", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, down);
         input = b.h;
         if (l + 1 < nlayers)
             dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.h,

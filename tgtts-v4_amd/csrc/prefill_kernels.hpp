@@ -38,6 +38,7 @@ struct PrefillLayer {
     const float* input_norm;
     const float* post_norm;
     uint16_t* kv;  // the layer's cache pool
+    int od_rows;   // strip height of o and down: 4 or 16 (qkv and gate_up: 16)
 };
 
 // The prefill's tensors, [M_pad] rows each.

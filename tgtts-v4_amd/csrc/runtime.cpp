@@ -221,40 +221,52 @@ DecodeArgs Decoder::args() const {
     return a;
 }
 
-LayerArgs Decoder::layer_args(int l, const float* x, float* mid) const {
+LayerArgs Decoder::layer_args(int l) const {
     LayerArgs la{};
-    la.x = x;
+    la.x = l == 0 ? x_in : h_a;
+    la.xn = l == 0 ? nullptr : xn_a;
+    la.x_sq = sq_a;
     la.input_norm = layers[l].input_norm;
     la.qkv = layers[l].qkv;
     la.q = q;
     la.kv = kv + (size_t)l * nblocks * shape.kv_heads * 2 * KV_TILE;
     la.attended = attended;
-    la.mid = mid;
-    la.post_norm = layers[l].post_norm;
+    la.mid_n = xn_b;
+    la.mid_sq = sq_b;
     la.gate_up = layers[l].gate_up;
     la.mlp = mlp;
     return la;
 }
 
-ResidualArgs Decoder::o_args(int l, const float* residual, float* out_) const {
+ResidualArgs Decoder::o_args(int l) const {
     ResidualArgs r{};
     r.w = layers[l].o;
     r.x = attended;
     r.K = shape.heads * HEAD_DIM;
     r.N = shape.hidden;
-    r.residual = residual;
-    r.out = out_;
+    r.R = od_rows;
+    r.residual = l == 0 ? x_in : h_a;
+    r.out = h_b;
+    r.next_norm = layers[l].post_norm;
+    r.out_n = xn_b;
+    r.out_sq = sq_b;
     return r;
 }
 
-ResidualArgs Decoder::down_args(int l, const float* residual, float* out_) const {
+ResidualArgs Decoder::down_args(int l) const {
     ResidualArgs r{};
     r.w = layers[l].down;
     r.x = mlp;
     r.K = shape.inner;
     r.N = shape.hidden;
-    r.residual = residual;
-    r.out = out_;
+    r.R = od_rows;
+    r.residual = h_b;
+    r.out = h_a;
+    // The next layer's input norm; the last layer's output goes to the final norm, which takes the
+    // f32 rows.
+    r.next_norm = l + 1 < shape.layers ? layers[l + 1].input_norm : nullptr;
+    r.out_n = xn_a;
+    r.out_sq = sq_a;
     return r;
 }
 
@@ -287,14 +299,12 @@ hipError_t enqueue_step(Decoder* d, int advance, DispatchTimer* timer, int* disp
     const DecodeArgs a = d->args();
     hipError_t err = hipSuccess;
     int n = 0;
-    const float* x = d->x_in;
     for (int l = 0; l < d->shape.layers && err == hipSuccess; ++l) {
-        // layer l: x -> mid (h_b) -> next (h_a); layer 0 reads x_in, which stays as written.
-        err = launch_decode_layer(a, d->layer_args(l, x, d->h_b), d->o_args(l, x, d->h_b),
-                                  d->down_args(l, d->h_b, d->h_a), s, timer);
+        // layer 0 reads x_in, which stays as written
+        err = launch_decode_layer(a, d->layer_args(l), d->o_args(l), d->down_args(l), s, timer);
         n += 5;
-        x = d->h_a;
     }
+    const float* x = d->shape.layers > 0 ? d->h_a : d->x_in;
     if (err == hipSuccess) {
         err = launch_final_norm(a, x, d->final_norm, d->out, d->positions, advance, s, timer);
         n += 1;
@@ -328,7 +338,7 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     if (decode_attention_lds(s.heads, s.kv_heads) + 4096 > d->ctx->lds_bytes)
         return fail(TGX_E_SHAPE, "the attention's LDS is past the device's " + std::to_string(d->ctx->lds_bytes));
     d->rows = batch->rows;
-    d->strip_rows = decode_strip_rows(batch->rows);
+    d->od_rows = decode_residual_rows(batch->rows);
     d->slots = batch->slots;
     d->block_tokens = batch->block_tokens == 0 ? BLOCK_TOKENS : batch->block_tokens;
     d->max_blocks = (s.capacity + BLOCK_TOKENS - 1) / BLOCK_TOKENS;
@@ -350,6 +360,10 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_TRY(alloc(d, &d->x_in, (size_t)R * h));
     TGX_TRY(alloc(d, &d->h_a, (size_t)R * h));
     TGX_TRY(alloc(d, &d->h_b, (size_t)R * h));
+    TGX_TRY(alloc(d, &d->xn_a, (size_t)R * h));
+    TGX_TRY(alloc(d, &d->xn_b, (size_t)R * h));
+    TGX_TRY(alloc(d, &d->sq_a, (size_t)R * h / 4));
+    TGX_TRY(alloc(d, &d->sq_b, (size_t)R * h / 4));
     TGX_TRY(alloc(d, &d->out, (size_t)R * h));
     TGX_TRY(alloc(d, &d->q, (size_t)R * H * HEAD_DIM));
     TGX_TRY(alloc(d, &d->attended, (size_t)R * H * HEAD_DIM));
@@ -507,7 +521,7 @@ std::vector<uint16_t> tile_rows(const std::vector<float>& w, int n, int k, int R
 }
 
 tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, const std::string& what,
-                             const void* data, tgx_dtype dtype, size_t count, int R) {
+                             const void* data, tgx_dtype dtype, size_t count, int o_rows, int down_rows) {
     const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads;
     const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
     auto want = [&](size_t expect) -> tgx_status {
@@ -526,14 +540,13 @@ tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, 
     }
     if (what == "qkv_proj") {
         TGX_TRY(want((size_t)qkv_rows * h));
-        auto t = tile_rows(as_f32(data, dtype, count), qkv_rows, h, R,
-                           [R](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM, R); });
+        auto t = tile_rows(as_f32(data, dtype, count), qkv_rows, h, QKV_ROWS,
+                           [](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM, QKV_ROWS); });
         return upload(L.qkv, t.data(), t.size() * 2);
     }
-    auto plain = [R](int strip, int r) { return strip * R + r; };
     if (what == "o_proj") {
         TGX_TRY(want((size_t)h * H * HEAD_DIM));
-        auto t = tile_rows(as_f32(data, dtype, count), h, H * HEAD_DIM, R, plain);
+        auto t = tile_rows(as_f32(data, dtype, count), h, H * HEAD_DIM, o_rows, [o_rows](int strip, int r) { return strip * o_rows + r; });
         return upload(L.o, t.data(), t.size() * 2);
     }
     if (what == "gate_up_proj") {
@@ -543,7 +556,8 @@ tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, 
     }
     if (what == "down_proj") {
         TGX_TRY(want((size_t)h * I));
-        auto t = tile_rows(as_f32(data, dtype, count), h, I, R, plain);
+        auto t = tile_rows(as_f32(data, dtype, count), h, I, down_rows,
+                           [down_rows](int strip, int r) { return strip * down_rows + r; });
         return upload(L.down, t.data(), t.size() * 2);
     }
     return fail(TGX_E_WEIGHTS, name + ": no such tensor");
@@ -566,7 +580,7 @@ tgx_status decoder_load(Decoder* d, const char* name, const void* data, tgx_dtyp
     char what[128] = {0};
     if (std::sscanf(name, "layers.%d.%127s", &l, what) != 2 || l < 0 || l >= s.layers)
         return fail(TGX_E_WEIGHTS, n + ": no such tensor in a stack of " + std::to_string(s.layers) + " layers");
-    return load_layer_tensor(d->layers[l], s, n, what, data, dtype, count, d->strip_rows);
+    return load_layer_tensor(d->layers[l], s, n, what, data, dtype, count, d->od_rows, d->od_rows);
 }
 
 tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {

@@ -69,13 +69,16 @@ struct Decoder {
     Context* ctx = nullptr;
     Shape shape{};
     int rows = 0, slots = 0, block_tokens = 64, nblocks = 0, max_blocks = 0;
-    int strip_rows = 16;  // weight strip height of qkv, o and down at this batch
     std::vector<DeviceBuffer> allocations;
     size_t device_bytes = 0;
     std::vector<Layer> layers;
     float* final_norm = nullptr;
     // step tensors
     float *x_in = nullptr, *h_a = nullptr, *h_b = nullptr, *out = nullptr;
+    // h_a, h_b times the next norm's gain in bf16, and their sums of squares [rows][hidden / 4]
+    uint16_t *xn_a = nullptr, *xn_b = nullptr;
+    float *sq_a = nullptr, *sq_b = nullptr;
+    int od_rows = 4;  // strip height of o_proj and down_proj (decode_residual_rows)
     uint16_t *q = nullptr, *attended = nullptr, *mlp = nullptr, *kv = nullptr;
     uint32_t *positions = nullptr, *slot_of_row = nullptr, *table = nullptr;
     float *cos = nullptr, *sin = nullptr;
@@ -99,9 +102,11 @@ struct Decoder {
     PrefillState pf;
 
     DecodeArgs args() const;
-    LayerArgs layer_args(int l, const float* x, float* mid) const;
-    ResidualArgs o_args(int l, const float* residual, float* out) const;
-    ResidualArgs down_args(int l, const float* residual, float* out) const;
+    // Layer l's tensors: its input is x_in at layer 0, else h_a (with xn_a, sq_a); o_proj writes
+    // mid to h_b (with xn_b, sq_b), down_proj the next input to h_a.
+    LayerArgs layer_args(int l) const;
+    ResidualArgs o_args(int l) const;
+    ResidualArgs down_args(int l) const;
 };
 
 tgx_status context_create(int device, Context** out);
@@ -136,12 +141,13 @@ tgx_status decoder_read_cache(Decoder* dec, uint32_t slot, uint32_t positions, f
 
 // A weight's values as f32; W [n][k] in MFMA tiles of R-row strips, rows through `row_of`
 // (strip, r) -> source row; and one layer's tensor `what` of a stack ("qkv_proj", "o_proj",
-// "gate_up_proj", "down_proj", "input_layernorm", "post_attention_layernorm").
+// "gate_up_proj", "down_proj", "input_layernorm", "post_attention_layernorm"), q/k/v and gate/up
+// in 16-row strips, o_proj in `o_rows` and down_proj in `down_rows`.
 std::vector<float> as_f32(const void* data, tgx_dtype dtype, size_t count);
 std::vector<uint16_t> tile_rows(const std::vector<float>& w, int n, int k, int R,
                                 const std::function<int(int, int)>& row_of);
 tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, const std::string& what,
-                             const void* data, tgx_dtype dtype, size_t count, int R);
+                             const void* data, tgx_dtype dtype, size_t count, int o_rows, int down_rows);
 
 // f32 <- bf16 / f16 bits; f32 -> bf16 bits, rounding to nearest even.
 float bf16_to_f32(uint16_t h);

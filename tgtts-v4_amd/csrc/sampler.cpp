@@ -272,7 +272,7 @@ tgx_status sampler_load(Sampler* s, const char* name, const void* data, tgx_dtyp
     int l = -1;
     char what[128] = {0};
     if (std::sscanf(name, "layers.%d.%127s", &l, what) == 2 && l >= 0 && l < s->shape.layers)
-        return load_layer_tensor(s->layers[l], s->shape, n, what, data, dtype, count, 16);
+        return load_layer_tensor(s->layers[l], s->shape, n, what, data, dtype, count, 16, 16);
     return fail(TGX_E_WEIGHTS, n + ": no such tensor of the sampler");
 }
 
