@@ -404,47 +404,26 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
 
 // ---------------------------------------------------------------------------------------------
 // attention_decode: workgroup (kv, b) attends the `group` query heads KV head kv serves of row b
-// over its slot's positions 0..pos; wave w takes blocks w, w + 8, ... with an online softmax, the
-// next block's keys and values loaded while the current one is taken.
+// over its slot's positions 0..pos; wave w takes blocks w, w + 8, ... (its turns) with an online
+// softmax, two turns' keys and values in flight at once.
 // Per block, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in bf16 straight
 // from the registers S^T left it in.
-__global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
-    extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
-    __shared__ float sm_m[ATTN_WAVES][16];
-    __shared__ float sm_l[ATTN_WAVES][16];
-    const int kv = blockIdx.x, b = blockIdx.y;
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int H = a.heads, KV = a.kv_heads, group = H / KV;
-    uint32_t pos, slot;
-    if (!placed(a, b, pos, slot)) return;
-    const int blocks = (int)(pos / BLOCK_TOKENS) + 1;
-    const int h = lane % 16;
+// Two memory round trips before the first product: the row's position, the cache blocks of the
+// wave's turns (lane j: block w + 8 j, from the row's copy of its slot's table) and q together,
+// then the first two turns' keys and values.
 
-    uint4 qf[2];
-#pragma unroll
-    for (int ds = 0; ds < 2; ++ds) {
-        qf[ds] = make_uint4(0, 0, 0, 0);
-        if (h < group) qf[ds] = load16(l.q + ((size_t)b * H + kv * group + h) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
-    }
+namespace {
+
+// The online softmax state of one wave: its running max and sum for each head (column) of its
+// lanes, and O^T for the 64 dimensions (lane 16 g + h: head h, dimensions 16 dt + 4 g .. + 3).
+struct Softmax {
     float m = -INFINITY, total = 0.f;
     f32x4 o[4] = {};
-    uint4 kf[8], vf[8], kn[8], vn[8];
-    // Loads block bi's tiles into (k, v); false when the slot holds no block there.
-    auto fetch = [&](int bi, uint4 (&k)[8], uint4 (&v)[8]) -> bool {
-        if (bi >= blocks) return false;
-        const long blk = block_of(a, slot, (uint32_t)bi * BLOCK_TOKENS);
-        if (blk < 0) return false;
-        const uint16_t* kt = l.kv + ((size_t)blk * KV + kv) * 2 * KV_TILE;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) k[i] = load16(kt + (i * 64 + lane) * 8);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = load16(kt + KV_TILE + (i * 64 + lane) * 8);
-        return true;
-    };
-    bool have = fetch(w, kf, vf);
-    for (int bi = w; have; bi += ATTN_WAVES) {
-        const bool have_next = fetch(bi + ATTN_WAVES, kn, vn);
-        const uint32_t p0 = (uint32_t)bi * BLOCK_TOKENS;
+
+    // One block of 64 positions p0 .. p0 + 63, those past pos masked.
+    __device__ void block(const uint4 (&kf)[8], const uint4 (&vf)[8], const uint4 (&qf)[2], uint32_t p0, uint32_t pos,
+                          float scale) {
+        const int lane = threadIdx.x % WAVE;
         f32x4 s[4];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
@@ -458,13 +437,13 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t p = p0 + pt * 16 + (lane / 16) * 4 + i;
-                const float v = p <= pos ? s[pt][i] * a.scale : -INFINITY;
+                const float v = p <= pos ? s[pt][i] * scale : -INFINITY;
                 s[pt][i] = v;
                 mx = fmaxf(mx, v);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
         mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-        const float m_new = fmaxf(m, mx);
+        const float m_new = fmaxf(m, mx);  // finite: position p0 <= pos is in the block
         const float rescale = __expf(m - m_new);
         float sum = 0.f;
         uint4 pf[2];
@@ -494,22 +473,71 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
         }
         total = total * rescale + sum;
         m = m_new;
+    }
+};
+
+}  // namespace
+
+__global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
+    extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
+    __shared__ float sm_m[ATTN_WAVES][16];
+    __shared__ float sm_l[ATTN_WAVES][16];
+    const int kv = blockIdx.x, b = blockIdx.y;
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int H = a.heads, KV = a.kv_heads, group = H / KV;
+    const int h = lane % 16;
+    const uint32_t pos = a.positions[b];
+    const uint32_t turn_block =
+        a.row_table[(uint32_t)b * (uint32_t)a.max_blocks + (uint32_t)min(w + ATTN_WAVES * lane, a.max_blocks - 1)];
+    // Columns past the group read its last head again; nothing reads what they give.
+    uint4 qf[2];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            kf[i] = kn[i];
-            vf[i] = vn[i];
-        }
-        have = have_next;
+    for (int ds = 0; ds < 2; ++ds) qf[ds] = load16(l.q + ((size_t)b * H + kv * group + min(h, group - 1)) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
+    all_issued();
+    if (pos >= (uint32_t)a.capacity) return;  // a spare row
+    const int blocks = (int)(pos / BLOCK_TOKENS) + 1;
+
+    // Turn j's block, and whether the wave has it (the slot may hold no block there).
+    auto block_of_turn = [&](int j) { return (uint32_t)__builtin_amdgcn_readlane((int)turn_block, min(j, WAVE - 1)); };
+    auto has = [&](int j) { return w + ATTN_WAVES * j < blocks && block_of_turn(j) < (uint32_t)a.nblocks; };
+    // Turn j's keys and values. Without the turn (`real` false) the same 1 KiB at the pool's start
+    // is read 16 times over instead, from the caches: the loads are made either way, so that the
+    // waits for them can be counted exactly (a load under a branch makes the compiler wait for
+    // every load before its first use).
+    auto fetch = [&](int j, bool real, uint4 (&k)[8], uint4 (&v)[8]) {
+        const uint16_t* kt = real ? l.kv + ((size_t)block_of_turn(j) * KV + kv) * 2 * KV_TILE : l.kv;
+        const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) k[i] = load16(kt + i * stride + lane * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + lane * 8);
+    };
+    Softmax sm;
+    // Two buffers: the first two turns straight (every context up to 16 blocks), then the rest
+    // two at a time, each pair's loads issued once the last pair is taken.
+    uint4 ka[8], va[8], kb[8], vb[8];
+    const bool t0 = has(0), t1 = has(1);
+    fetch(0, t0, ka, va);
+    fetch(1, t1, kb, vb);
+    if (t0) sm.block(ka, va, qf, (uint32_t)w * BLOCK_TOKENS, pos, a.scale);
+    if (t1) sm.block(kb, vb, qf, (uint32_t)(w + ATTN_WAVES) * BLOCK_TOKENS, pos, a.scale);
+    for (int j = 2; t1 && has(j); j += 2) {
+        const bool next = has(j + 1);
+        fetch(j, true, ka, va);
+        fetch(j + 1, next, kb, vb);
+        sm.block(ka, va, qf, (uint32_t)(w + ATTN_WAVES * j) * BLOCK_TOKENS, pos, a.scale);
+        if (!next) break;
+        sm.block(kb, vb, qf, (uint32_t)(w + ATTN_WAVES * (j + 1)) * BLOCK_TOKENS, pos, a.scale);
     }
     if (lane < 16) {
-        sm_m[w][h] = m;
-        sm_l[w][h] = total;
+        sm_m[w][h] = sm.m;
+        sm_l[w][h] = sm.total;
     }
     if (h < group) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) attn_lds[(w * group + h) * (HEAD_DIM + 1) + dt * 16 + (lane / 16) * 4 + i] = o[dt][i];
+            for (int i = 0; i < 4; ++i) attn_lds[(w * group + h) * (HEAD_DIM + 1) + dt * 16 + (lane / 16) * 4 + i] = sm.o[dt][i];
     }
     __syncthreads();
     // The waves joined in order (wave 0 holds block 0, so M is finite).
@@ -623,6 +651,8 @@ int decode_tiles(int rows) { return (rows + 15) / 16; }
 int decode_residual_rows(int rows) { return rows <= 16 ? 4 : 16; }
 
 int decode_max_k() { return MAX_CHUNKS * CHUNK_COLS; }
+
+int decode_max_capacity() { return ATTN_WAVES * WAVE * BLOCK_TOKENS; }
 
 hipError_t decode_prepare(size_t device_lds) {
     hipFuncAttributes attr{};

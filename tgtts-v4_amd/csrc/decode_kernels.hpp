@@ -21,6 +21,7 @@ struct DecodeArgs {
     const uint32_t* positions;  // [rows]
     const uint32_t* slots;      // [rows]
     const uint32_t* table;      // [nslots][max_blocks], UINT32_MAX where none
+    const uint32_t* row_table;  // [rows][max_blocks]: each row's slot's table row (UINT32_MAX for a spare row)
     const float* cos;           // [capacity][32]
     const float* sin;
 };
@@ -77,6 +78,8 @@ struct DispatchTimer {
 // attention takes.
 int decode_tiles(int rows);
 int decode_max_k();
+// The longest capacity the attention takes: a lane to each block a wave reads.
+int decode_max_capacity();
 size_t decode_attention_lds(int heads, int kv_heads);
 // Lets the attention take up to `device_lds` bytes of LDS per workgroup.
 hipError_t decode_prepare(size_t device_lds);

@@ -150,6 +150,8 @@ tgx_status check_shape(const tgx_shape* in, Shape* s) {
     if (in->rope_factors) s->factors.assign(in->rope_factors, in->rope_factors + in->head_dim / 2);
     if (s->head_dim != HEAD_DIM) return refuse("head_dim " + std::to_string(s->head_dim) + ": the kernels take 64");
     if (s->layers < 0 || s->capacity <= 0) return refuse("layers " + std::to_string(s->layers) + ", capacity " + std::to_string(s->capacity));
+    if (s->capacity > decode_max_capacity())
+        return refuse("capacity " + std::to_string(s->capacity) + " past the attention's " + std::to_string(decode_max_capacity()));
     if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 16 || 16 % (s->heads / s->kv_heads) != 0)
         return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) + " KV heads: a group of 1, 2, 4, 8 or 16");
     // The projections take K in chunks of 1024 columns, up to 4096 (decode_kernels.hip).
@@ -216,6 +218,7 @@ DecodeArgs Decoder::args() const {
     a.positions = positions;
     a.slots = slot_of_row;
     a.table = table;
+    a.row_table = row_table;
     a.cos = cos;
     a.sin = sin;
     return a;
@@ -372,6 +375,7 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_TRY(alloc(d, &d->positions, (size_t)R));
     TGX_TRY(alloc(d, &d->slot_of_row, (size_t)R));
     TGX_TRY(alloc(d, &d->table, (size_t)d->slots * d->max_blocks));
+    TGX_TRY(alloc(d, &d->row_table, (size_t)R * d->max_blocks));
     TGX_TRY(alloc(d, &d->cos, (size_t)s.capacity * HEAD_DIM / 2));
     TGX_TRY(alloc(d, &d->sin, (size_t)s.capacity * HEAD_DIM / 2));
     // Norm gains start at one, so that an unloaded stack still runs finite.
@@ -390,6 +394,7 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_HIP(hipHostMalloc((void**)&d->out_host, (size_t)R * h * 4, hipHostMallocDefault));
     TGX_HIP(hipHostMalloc((void**)&d->placement_host, (size_t)2 * R * 4, hipHostMallocDefault));
     TGX_HIP(hipHostMalloc((void**)&d->table_host, (size_t)d->slots * d->max_blocks * 4, hipHostMallocDefault));
+    TGX_HIP(hipHostMalloc((void**)&d->row_table_host, (size_t)R * d->max_blocks * 4, hipHostMallocDefault));
     std::memset(d->x_host, 0, (size_t)R * h * 4);
     std::memset(d->out_host, 0, (size_t)R * h * 4);
     for (int i = 0; i < 2 * R; ++i) d->placement_host[i] = TGX_SPARE;
@@ -398,6 +403,7 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_HIP(hipMemcpy(d->slot_of_row, d->placement_host + R, R * 4, hipMemcpyHostToDevice));
     TGX_HIP(hipMemcpy(d->table, d->table_host, (size_t)d->slots * d->max_blocks * 4, hipMemcpyHostToDevice));
     d->table_dirty = false;
+    d->rows_dirty = true;
     d->slot_blocks.assign(d->slots, 0);
     d->free_list.clear();
     for (int b = d->nblocks - 1; b >= 0; --b) d->free_list.push_back((uint32_t)b);
@@ -444,9 +450,20 @@ tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions) {
 }
 
 tgx_status sync_slots(Decoder* d) {
-    if (!d->table_dirty) return TGX_OK;
-    TGX_HIP(hipMemcpyAsync(d->table, d->table_host, (size_t)d->slots * d->max_blocks * 4, hipMemcpyHostToDevice, d->ctx->stream));
+    if (!d->table_dirty && !d->rows_dirty) return TGX_OK;
+    hipStream_t s = d->ctx->stream;
+    const size_t mb = (size_t)d->max_blocks;
+    if (d->table_dirty) TGX_HIP(hipMemcpyAsync(d->table, d->table_host, d->slots * mb * 4, hipMemcpyHostToDevice, s));
+    for (int b = 0; b < d->rows; ++b) {
+        const uint32_t slot = d->placement_host[d->rows + b];
+        for (size_t i = 0; i < mb; ++i)
+            d->row_table_host[b * mb + i] = slot < (uint32_t)d->slots ? d->table_host[slot * mb + i] : TGX_SPARE;
+    }
+    TGX_HIP(hipMemcpyAsync(d->row_table, d->row_table_host, d->rows * mb * 4, hipMemcpyHostToDevice, s));
+    // The pinned buffers may not change until the copies have gone.
+    TGX_HIP(hipStreamSynchronize(s));
     d->table_dirty = false;
+    d->rows_dirty = false;
     return TGX_OK;
 }
 
@@ -487,6 +504,7 @@ void decoder_destroy(Decoder* d) {
     if (d->out_host) hipHostFree(d->out_host);
     if (d->placement_host) hipHostFree(d->placement_host);
     if (d->table_host) hipHostFree(d->table_host);
+    if (d->row_table_host) hipHostFree(d->row_table_host);
     delete d;
 }
 
@@ -596,6 +614,7 @@ tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {
         TGX_TRY(hold_slot(d, r.slot, r.position + 1));
     }
     std::memcpy(d->placement_host, words.data(), words.size() * 4);
+    d->rows_dirty = true;
     hipStream_t s = d->ctx->stream;
     TGX_TRY(sync_slots(d));
     TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)nrows * 4, hipMemcpyHostToDevice, s));

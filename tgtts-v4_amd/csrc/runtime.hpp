@@ -81,12 +81,13 @@ struct Decoder {
     int od_rows = 4;  // strip height of o_proj and down_proj (decode_residual_rows)
     uint16_t *q = nullptr, *attended = nullptr, *mlp = nullptr, *kv = nullptr;
     uint32_t *positions = nullptr, *slot_of_row = nullptr, *table = nullptr;
+    uint32_t* row_table = nullptr;  // [rows][max_blocks]: each row's slot's table row
     float *cos = nullptr, *sin = nullptr;
     // host mirrors, in pinned memory
     float *x_host = nullptr, *out_host = nullptr;
     uint32_t *placement_host = nullptr;  // [positions..., slots...]
-    uint32_t *table_host = nullptr;
-    bool table_dirty = true;
+    uint32_t *table_host = nullptr, *row_table_host = nullptr;
+    bool table_dirty = true, rows_dirty = true;
     std::vector<int> slot_blocks;     // blocks each slot holds
     std::vector<uint32_t> free_list;  // blocks nobody holds
     // the recorded step
@@ -129,8 +130,8 @@ tgx_status decoder_output(Decoder* dec, float* out);
 tgx_status decoder_release_slot(Decoder* dec, uint32_t slot);
 tgx_status decoder_reserve(Decoder* dec, uint32_t slot, uint32_t positions);
 tgx_status decoder_launch(Decoder* dec, int times, int advance);
-// Hands `slot` the blocks for positions 0..positions-1, and copies the block table to the device
-// when it changed.
+// Hands `slot` the blocks for positions 0..positions-1; copies the block table, and the rows'
+// copies of their slots' rows of it, to the device when they changed.
 tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions);
 tgx_status sync_slots(Decoder* d);
 tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out);
