@@ -441,8 +441,8 @@ struct Softmax {
                 s[pt][i] = v;
                 mx = fmaxf(mx, v);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+        mx = fmaxf(mx, lane_xor16(mx));
+        mx = fmaxf(mx, lane_xor32(mx));
         const float m_new = fmaxf(m, mx);  // finite: position p0 <= pos is in the block
         const float rescale = __expf(m - m_new);
         float sum = 0.f;
@@ -463,8 +463,8 @@ struct Softmax {
             }
             pf[ks] = make_uint4(words[0], words[1], words[2], words[3]);
         }
-        sum += __shfl_xor(sum, 16, WAVE);
-        sum += __shfl_xor(sum, 32, WAVE);
+        sum += lane_xor16(sum);
+        sum += lane_xor32(sum);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
             o[dt] *= rescale;

@@ -97,6 +97,19 @@ __device__ __forceinline__ void load_to_lds(const void* src, void* lds) {
     __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)lds, 16, 0, 0);
 }
 
+// Lane l's value at lane l ^ 16 and l ^ 32, from the VALU's lane swaps (v_permlane16_swap: the
+// odd rows of 16 of the first operand trade places with the even rows of the second;
+// v_permlane32_swap: the upper half of the first with the lower half of the second), with no
+// LDS round trip.
+__device__ __forceinline__ float lane_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));

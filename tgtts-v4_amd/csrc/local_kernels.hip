@@ -180,7 +180,7 @@ __global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     own[i] = acc[s][t][i];
-                    other[i] = __shfl_xor(own[i], 32, WAVE);
+                    other[i] = lane_xor32(own[i]);
                 }
                 const int m = m0 + (wm * 4 + t) * 16 + lane % 16;
                 if (m >= a.M) continue;

@@ -20,25 +20,28 @@ namespace tgx {
 
 namespace {
 
-constexpr int PF_WAVES = 4;
-constexpr int PF_THREADS = PF_WAVES * WAVE;
-// The GEMM's workgroup tile: 256 rows of W (16 strips) by 256 rows of X, K 32 at a time (a
-// k-block to a stage, four stages in an LDS ring, three in flight while one is multiplied);
-// wave (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 128 wm .. + 127 (8 tiles of
-// 16): 64 accumulators of 16 x 16.
+// The GEMM's workgroup: eight waves, two to a SIMD, so that one wave's products run while the
+// other waits for LDS or the barrier. Its tile: 256 rows of W (16 strips) by 256 rows of X, K 32
+// at a time (a k-block to a stage, four stages in an LDS ring, three in flight while one is
+// multiplied); wave (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 64 wm .. + 63
+// (4 tiles of 16): 32 accumulators of 16 x 16.
+constexpr int GEMM_WAVES = 8;
+constexpr int GEMM_THREADS = GEMM_WAVES * WAVE;
 constexpr int TN = 256, TM = 256;
 constexpr int W_STRIPS = TN / 16;   // 16
 constexpr int X_TILES = TM / 16;    // 16
-constexpr int WT = 8;               // a wave's X tiles
+constexpr int WS = 8;               // a wave's W strips
+constexpr int WT = 4;               // a wave's X tiles
 constexpr int W_STAGE = W_STRIPS * 64;  // uint4 per stage: 16 KiB
 constexpr int X_STAGE = X_TILES * 64;   // 16 KiB
 constexpr int NBUF = 4;
-constexpr int FRAGS = (W_STRIPS + X_TILES) / PF_WAVES;  // 1 KiB loads a wave issues a stage
+constexpr int FRAGS = (W_STRIPS + X_TILES) / GEMM_WAVES;  // 1 KiB loads a wave issues a stage
+static_assert(W_STRIPS % FRAGS == 0, "a wave loads W fragments or X fragments, not both");
 
 enum Epilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2 };
 
 constexpr uint32_t TGX_SPARE_POS = 0xffffffffu;
-static_assert(PF_THREADS == TM, "the q/k/v epilogue stages a row to a thread");
+static_assert(GEMM_THREADS >= TM, "the q/k/v epilogue stages a row to a thread");
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -72,16 +75,36 @@ __device__ __forceinline__ int stage_strip(int nb, int sl, int N) {
     return strip_of<EPI>(nb, sl / 8, sl % 8, N);
 }
 
+// The workgroup's tile (nb, mb). Workgroups go to the 8 XCDs in turn (id % 8), each XCD with its
+// own L2; the ids are renumbered so that XCD x takes a contiguous eighth of the tiles, and the
+// tiles in groups of GROUP_M M-tiles by every N-tile: an X tile (a band of positions) is then
+// read only on its own XCD, by the N-tiles that share it there. A grid of fewer than a multiple
+// of 8 workgroups keeps the plain order.
+constexpr int GROUP_M = 4;
+__device__ __forceinline__ void tile_of(int& nb, int& mb) {
+    const int NB = gridDim.x, G = gridDim.x * gridDim.y;
+    const int id = blockIdx.x + blockIdx.y * gridDim.x;
+    const int v = G % 8 == 0 ? (id % 8) * (G / 8) + id / 8 : id;
+    const int per_group = GROUP_M * NB;
+    const int group = v / per_group, in = v % per_group;
+    const int rows = min(GROUP_M, (int)gridDim.y - group * GROUP_M);  // the last group may be short
+    mb = group * GROUP_M + in % rows;
+    nb = in / rows;
+}
+
 // W in strips of WR rows (o_proj and down_proj: 4 or 16, the rest 16), gathered into 16-row
 // fragments as it lands in LDS.
 template <int EPI, int WR = QKV_ROWS>
-__global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmArgs g) {
+__global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, GemmArgs g) {
     extern __shared__ uint4 lds[];
     uint4* ws = lds;                     // [NBUF][W_STAGE]
     uint4* xs = lds + NBUF * W_STAGE;    // [NBUF][X_STAGE]
-    const int nb = blockIdx.x, mb = blockIdx.y;
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int wn = w / 2, wm = w % 2;
+    int nb, mb;
+    tile_of(nb, mb);
+    // The wave's index, uniform: the branches on it below are the whole wave's.
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    const int lane = threadIdx.x % WAVE;
+    const int wn = w / 4, wm = w % 4;
     const int kblocks = g.K / 32;
     const int stages = kblocks;
     const int m0 = mb * TM;
@@ -90,25 +113,46 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
     // first two waves W's, the last two X's), loaded straight from memory into LDS: lane l of a
     // load writes bytes 16 l .. 16 l + 15 of the fragment, the MFMA operand order. Each wave
     // issues exactly FRAGS loads a stage, so its count in flight says which stages have landed.
-    auto fetch = [&](int st) {
-        const int buf = st % NBUF;
+    // Fragment j of stage st is lane's src[j] + st * step (a k-block further along K).
+    const bool loads_w = w * FRAGS < W_STRIPS;
+    const uint16_t* src[FRAGS];
+    int step_elems;
+    uint4* dst0;
+    if (loads_w) {
 #pragma unroll
-        for (int j = 0; j < FRAGS; ++j) {
-            const int f = w * FRAGS + j;
-            if (f < W_STRIPS) {
-                const uint16_t* src = g.w + fragment_index<WR>(stage_strip<EPI>(nb, f, g.N), st, kblocks, lane);
-                load_to_lds(src, &ws[buf * W_STAGE + f * 64]);
-            } else {
-                const int mt = f - W_STRIPS;
-                const uint16_t* src = g.x + (size_t)(m0 + mt * 16 + lane % 16) * g.K + st * 32 + (lane / 16) * 8;
-                load_to_lds(src, &xs[buf * X_STAGE + mt * 64]);
-            }
-        }
+        for (int j = 0; j < FRAGS; ++j) src[j] = g.w + fragment_index<WR>(stage_strip<EPI>(nb, w * FRAGS + j, g.N), 0, kblocks, lane);
+        step_elems = WR * 32;
+        dst0 = ws + w * FRAGS * 64;
+    } else {
+#pragma unroll
+        for (int j = 0; j < FRAGS; ++j)
+            src[j] = g.x + (size_t)(m0 + (w * FRAGS + j - W_STRIPS) * 16 + lane % 16) * g.K + (lane / 16) * 8;
+        step_elems = 32;
+        dst0 = xs + (w * FRAGS - W_STRIPS) * 64;
+    }
+    const int stage_stride = loads_w ? W_STAGE : X_STAGE;
+    auto fetch = [&](int st) __attribute__((always_inline)) {
+        uint4* dst = dst0 + (st % NBUF) * stage_stride;
+#pragma unroll
+        for (int j = 0; j < FRAGS; ++j) load_to_lds(src[j] + (size_t)st * step_elems, dst + j * 64);
+    };
+    // Waits until stage st has landed for every wave: no more than the stages fetched after it
+    // in flight for this wave, then the barrier, which also says that every wave is done with
+    // stage st - 1, whose buffer the next fetch takes.
+    auto landed = [&](int st) __attribute__((always_inline)) {
+        const int after = min(NBUF - 2, stages - 1 - st);
+        if (after >= 2)
+            wait_vm<2 * FRAGS>();
+        else if (after == 1)
+            wait_vm<FRAGS>();
+        else
+            wait_vm<0>();
+        stage_barrier();
     };
 
-    f32x4 acc[8][WT];
+    f32x4 acc[WS][WT];
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < WS; ++s)
 #pragma unroll
         for (int t = 0; t < WT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -116,28 +160,18 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
     for (int p = 0; p < NBUF - 1; ++p)
         if (p < stages) fetch(p);
     for (int st = 0; st < stages; ++st) {
-        // Stage st has landed once no more than the later stages' loads are in flight; the barrier
-        // makes it so for every wave, and says every wave is done with stage st - 1, whose buffer
-        // the next fetch takes.
-        const int ahead = min(NBUF - 2, stages - 1 - st);
-        if (ahead >= 2)
-            wait_vm<2 * FRAGS>();
-        else if (ahead == 1)
-            wait_vm<FRAGS>();
-        else
-            wait_vm<0>();
-        stage_barrier();
+        landed(st);
         if (st + NBUF - 1 < stages) fetch(st + NBUF - 1);
         const int buf = st % NBUF;
         // fr[t]: X tile t; fr[WT + s]: W strip s.
-        uint4 fr[WT + 8];
+        uint4 fr[WT + WS];
 #pragma unroll
         for (int t = 0; t < WT; ++t) fr[t] = lds_read16(&xs[buf * X_STAGE + (wm * WT + t) * 64 + lane]);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) fr[WT + s] = lds_read16(&ws[buf * W_STAGE + (wn * 8 + s) * 64 + lane]);
+        for (int s = 0; s < WS; ++s) fr[WT + s] = lds_read16(&ws[buf * W_STAGE + (wn * WS + s) * 64 + lane]);
         lds_landed(fr);
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+        for (int s = 0; s < WS; ++s)
 #pragma unroll
             for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(fr[WT + s], fr[t], acc[s][t]);
     }
@@ -190,8 +224,8 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
         float* t_sin = t_cos + TM * (HEAD_DIM / 2);            // [TM][32]
         uint32_t* t_pos = reinterpret_cast<uint32_t*>(t_sin + TM * (HEAD_DIM / 2));  // [TM]
         uint32_t* t_blk = t_pos + TM;                           // [TM]
-        {
-            const int j = threadIdx.x;  // PF_THREADS == TM
+        if (threadIdx.x < TM) {
+            const int j = threadIdx.x;
             const int m = m0 + j;
             uint32_t pos = TGX_SPARE_POS, blk = TGX_SPARE_POS;
             if (m < a.M) {
@@ -230,7 +264,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_gemm(PrefillArgs a, GemmAr
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     own[i] = acc[s][t][i];
-                    other[i] = __shfl_xor(own[i], 32, WAVE);
+                    other[i] = lane_xor32(own[i]);
                 }
                 const uint32_t pos = t_pos[j];
                 if (pos == TGX_SPARE_POS) continue;
@@ -401,8 +435,8 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
                     s[pt][i] = v;
                     mx = fmaxf(mx, v);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+            mx = fmaxf(mx, lane_xor16(mx));
+            mx = fmaxf(mx, lane_xor32(mx));
             // Block 0 holds position 0, which every column sees, so m is finite after it.
             const float m_new = fmaxf(m[cg], mx);
             const float rescale = __expf(m[cg] - m_new);
@@ -424,8 +458,8 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
                 }
                 pf[ks] = make_uint4(words[0], words[1], words[2], words[3]);
             }
-            sum += __shfl_xor(sum, 16, WAVE);
-            sum += __shfl_xor(sum, 32, WAVE);
+            sum += lane_xor16(sum);
+            sum += lane_xor32(sum);
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
                 o[cg][dt] *= rescale;
@@ -491,7 +525,7 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
     for (int l = 0; l < nlayers; ++l) {
         const PrefillLayer& L = layers[l];
         GemmArgs qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, nullptr, b.q, L.kv};
-        dispatch("prefill_qkv", prefill_gemm<EPI_QKV>, dim3(qkv_rows / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, qkv);
+        dispatch("prefill_qkv", prefill_gemm<EPI_QKV>, dim3(qkv_rows / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, qkv);
         switch (group) {
             case 1: dispatch("prefill_attention", prefill_attention<2, 1>, dim3(b.ntiles, a.kv_heads), dim3(2 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
             case 2: dispatch("prefill_attention", prefill_attention<4, 1>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
@@ -503,13 +537,13 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
         auto residual_gemm = L.od_rows == 4 ? prefill_gemm<EPI_RESIDUAL, 4> : prefill_gemm<EPI_RESIDUAL, 16>;
         if (L.od_rows != 4 && L.od_rows != 16) return hipErrorInvalidValue;
         GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr};
-        dispatch("prefill_o", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, o);
+        dispatch("prefill_o", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, o);
         dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.mid, L.post_norm,
                  b.normed, (float*)nullptr);
         GemmArgs gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, nullptr, b.mlp, nullptr, nullptr};
-        dispatch("prefill_gate_up", prefill_gemm<EPI_SILU>, dim3(2 * a.inner / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, gu);
+        dispatch("prefill_gate_up", prefill_gemm<EPI_SILU>, dim3(2 * a.inner / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, gu);
         GemmArgs down{L.down, b.mlp, a.inner, a.hidden, b.mid, b.h, nullptr, nullptr, nullptr};
-        dispatch("prefill_down", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(PF_THREADS), GEMM_LDS, stream, timer, a, down);
+        dispatch("prefill_down", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, down);
         input = b.h;
         if (l + 1 < nlayers)
             dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.h,
