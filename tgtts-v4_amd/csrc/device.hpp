@@ -131,6 +131,15 @@ __host__ __device__ constexpr int weight_lane_offset(int lane, int R) {
     return ((lane / 16) * R + lane % 16) * 8;
 }
 
+// The prefill's activations that feed a GEMM (the normed rows, the attention's output, the MLP's
+// product), [M][K] bf16 kept as MFMA B-operand fragments of 16 rows by 32 columns, 1 KiB each,
+// along K: (m, k) at fragment (m / 16, k / 32), lane 16 ((k % 32) / 8) + m % 16, slot k % 8. A
+// GEMM reads each fragment as 1 KiB in a row; 8 columns k .. k + 7 (k a multiple of 8) sit
+// together, as do 4.
+__host__ __device__ constexpr size_t act_index(int m, int k, int K) {
+    return ((size_t)(m / 16) * (K / 32) + k / 32) * 512 + (size_t)((((k % 32) / 8) * 16 + m % 16) * 8 + k % 8);
+}
+
 // The strip height of q/k/v and gate/up (the MFMA's rows); o_proj and down_proj take 4 or 16 by
 // the batch (decode_residual_rows).
 constexpr int QKV_ROWS = 16;

@@ -47,12 +47,12 @@ __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cas
 
 struct GemmArgs {
     const uint16_t* w;  // tiles of [N][K] in WR-row strips (the kernel's template argument)
-    const uint16_t* x;  // bf16 [M_pad][K]
+    const uint16_t* x;  // bf16 [M_pad][K] in fragment order (act_index)
     int K, N;
     // epilogues
     const float* residual;  // EPI_RESIDUAL: f32 [M_pad][N]
     float* out;             // EPI_RESIDUAL: f32 [M_pad][N]
-    uint16_t* mlp;          // EPI_SILU: bf16 [M_pad][N / 2]
+    uint16_t* mlp;          // EPI_SILU: bf16 [M_pad][N / 2] in fragment order
     uint16_t* q;            // EPI_QKV
     uint16_t* kv;           // EPI_QKV: the layer's cache pool
 };
@@ -126,8 +126,8 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
     } else {
 #pragma unroll
         for (int j = 0; j < FRAGS; ++j)
-            src[j] = g.x + (size_t)(m0 + (w * FRAGS + j - W_STRIPS) * 16 + lane % 16) * g.K + (lane / 16) * 8;
-        step_elems = 32;
+            src[j] = g.x + (size_t)(m0 / 16 + w * FRAGS + j - W_STRIPS) * kblocks * 512 + lane * 8;
+        step_elems = 512;
         dst0 = xs + (w * FRAGS - W_STRIPS) * 64;
     }
     const int stage_stride = loads_w ? W_STAGE : X_STAGE;
@@ -156,24 +156,46 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
 #pragma unroll
         for (int t = 0; t < WT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-    for (int p = 0; p < NBUF - 1; ++p)
-        if (p < stages) fetch(p);
-    for (int st = 0; st < stages; ++st) {
-        landed(st);
-        if (st + NBUF - 1 < stages) fetch(st + NBUF - 1);
+    // The wave's fragments of stage st from LDS: fr[t] X tile t, fr[WT + s] W strip s.
+    auto read = [&](int st, uint4 (&fr)[WT + WS]) __attribute__((always_inline)) {
         const int buf = st % NBUF;
-        // fr[t]: X tile t; fr[WT + s]: W strip s.
-        uint4 fr[WT + WS];
 #pragma unroll
         for (int t = 0; t < WT; ++t) fr[t] = lds_read16(&xs[buf * X_STAGE + (wm * WT + t) * 64 + lane]);
 #pragma unroll
         for (int s = 0; s < WS; ++s) fr[WT + s] = lds_read16(&ws[buf * W_STAGE + (wn * WS + s) * 64 + lane]);
-        lds_landed(fr);
+    };
+    // Step st: the products of stage st from `cur` (read in the step before) while stage st + 1's
+    // fragments are read into `next`, so that the LDS reads overlap the products. Stage
+    // st + NBUF - 1 is fetched first, into the buffer of stage st - 1, which every wave had read
+    // by the end of step st - 2 (the prologue, for stage 0), before the barrier of step st - 1.
+    auto step = [&](int st, uint4 (&cur)[WT + WS], uint4 (&next)[WT + WS]) __attribute__((always_inline)) {
+        if (st + NBUF - 1 < stages) fetch(st + NBUF - 1);
+        const bool more = st + 1 < stages;
+        if (more) {
+            landed(st + 1);
+            read(st + 1, next);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < WS; ++s)
 #pragma unroll
-            for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(fr[WT + s], fr[t], acc[s][t]);
+            for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(cur[WT + s], cur[t], acc[s][t]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) lds_landed(next);
+    };
+
+    uint4 fa[WT + WS], fb[WT + WS];
+#pragma unroll
+    for (int p = 0; p < NBUF - 1; ++p)
+        if (p < stages) fetch(p);
+    landed(0);
+    read(0, fa);
+    lds_landed(fa);
+    // K is a multiple of 1024: the stages come in pairs, and the accumulators flow through no
+    // branch (a branch around a step makes the compiler copy them out of their registers).
+    for (int st = 0; st < stages; st += 2) {
+        step(st, fa, fb);
+        step(st + 1, fb, fa);
     }
     // The epilogue below may reuse the LDS: every wave is done with the ring.
     stage_barrier();
@@ -214,7 +236,7 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
                     v[i] = gate / (1.0f + __expf(-gate)) * up;
                 }
                 uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-                *reinterpret_cast<uint2*>(g.mlp + (size_t)m * inner + n) = packed;
+                *reinterpret_cast<uint2*>(g.mlp + act_index(m, n, inner)) = packed;
             }
         }
     } else {  // EPI_QKV: rows of a strip pair as r, r + 8 (lanes l and l ^ 32)
@@ -317,7 +339,7 @@ __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* 
     if (row >= a.M) {
         if (!FINAL)
             for (int e = 0; e < per_lane; e += 8)
-                *reinterpret_cast<uint4*>(out_bf16 + (size_t)row * K + lane * per_lane + e) = make_uint4(0, 0, 0, 0);
+                *reinterpret_cast<uint4*>(out_bf16 + act_index(row, lane * per_lane + e, K)) = make_uint4(0, 0, 0, 0);
         return;
     }
     const float* r = x + (size_t)row * K + lane * per_lane;
@@ -341,7 +363,7 @@ __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* 
             *reinterpret_cast<float4*>(out_f32 + (size_t)row * K + lane * per_lane + e) = make_float4(n[0], n[1], n[2], n[3]);
             *reinterpret_cast<float4*>(out_f32 + (size_t)row * K + lane * per_lane + e + 4) = make_float4(n[4], n[5], n[6], n[7]);
         } else {
-            *reinterpret_cast<uint4*>(out_bf16 + (size_t)row * K + lane * per_lane + e) =
+            *reinterpret_cast<uint4*>(out_bf16 + act_index(row, lane * per_lane + e, K)) =
                 make_uint4(pack_bf16x2(n[0], n[1]), pack_bf16x2(n[2], n[3]), pack_bf16x2(n[4], n[5]), pack_bf16x2(n[6], n[7]));
         }
     }
@@ -487,7 +509,7 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
             const int d = dt * 16 + (lane / 16) * 4;
             uint2 packed = make_uint2(pack_bf16x2(o[cg][dt][0] * inv, o[cg][dt][1] * inv),
                                       pack_bf16x2(o[cg][dt][2] * inv, o[cg][dt][3] * inv));
-            *reinterpret_cast<uint2*>(attended + (row * H + head) * HEAD_DIM + d) = packed;
+            *reinterpret_cast<uint2*>(attended + act_index((int)row, head * HEAD_DIM + d, H * HEAD_DIM)) = packed;
         }
     }
 }

@@ -46,10 +46,10 @@ struct PrefillBuffers {
     const float* x;     // the run's hidden states, f32 [M_pad][hidden], as written
     float* h;           // residual stream, f32 [M_pad][hidden]
     float* mid;         // after the attention, f32
-    uint16_t* normed;   // RMSNorm of the stream, bf16 [M_pad][hidden]
+    uint16_t* normed;   // RMSNorm of the stream, bf16 [M_pad][hidden] in fragment order (act_index)
     uint16_t* q;        // bf16 [M_pad][heads][64]
-    uint16_t* attended; // bf16 [M_pad][heads 64]
-    uint16_t* mlp;      // bf16 [M_pad][inner]
+    uint16_t* attended; // bf16 [M_pad][heads 64] in fragment order
+    uint16_t* mlp;      // bf16 [M_pad][inner] in fragment order
     float* out;         // after the final norm, f32 [M_pad][hidden]
     const PrefillTile* tiles;
     int ntiles;
