@@ -44,6 +44,7 @@ tgx_status hold_rows(Decoder* d, int rows, int tiles) {
     TGX_TRY(prefill_alloc(d, &p.mid, rows * h));
     TGX_TRY(prefill_alloc(d, &p.out, rows * h));
     TGX_TRY(prefill_alloc(d, &p.normed, rows * h));
+    TGX_TRY(prefill_alloc(d, &p.row_sq, rows * h / 128));
     TGX_TRY(prefill_alloc(d, &p.q, rows * att));
     TGX_TRY(prefill_alloc(d, &p.attended, rows * att));
     TGX_TRY(prefill_alloc(d, &p.mlp, rows * (size_t)s.inner));
@@ -55,6 +56,7 @@ tgx_status hold_rows(Decoder* d, int rows, int tiles) {
     TGX_HIP(hipMemset(p.h, 0, rows * h * 4));
     TGX_HIP(hipMemset(p.mid, 0, rows * h * 4));
     TGX_HIP(hipMemset(p.normed, 0, rows * h * 2));
+    TGX_HIP(hipMemset(p.row_sq, 0, rows * h / 128 * 4));
     TGX_HIP(hipMemset(p.attended, 0, rows * att * 2));
     TGX_HIP(hipMemset(p.mlp, 0, rows * (size_t)s.inner * 2));
     p.rows_held = rows;
@@ -90,7 +92,7 @@ tgx_status launch(Decoder* d) {
         layers[l] = PrefillLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm,
                                  d->kv + (size_t)l * d->nblocks * s.kv_heads * 2 * KV_TILE, d->od_rows};
     }
-    PrefillBuffers b{p.x, p.h, p.mid, p.normed, p.q, p.attended, p.mlp, p.out, p.tiles, p.ntiles};
+    PrefillBuffers b{p.x, p.h, p.mid, p.normed, p.q, p.attended, p.mlp, p.row_sq, p.out, p.tiles, p.ntiles};
     if (d->timed) d->timer.used = 0;
     hipError_t e = launch_prefill(a, layers.data(), s.layers, d->final_norm, b, d->ctx->stream, d->timed ? &d->timer : nullptr);
     if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the prefill: ") + hipGetErrorString(e));

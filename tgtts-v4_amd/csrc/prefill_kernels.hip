@@ -55,6 +55,58 @@ struct GemmArgs {
     uint16_t* mlp;          // EPI_SILU: bf16 [M_pad][N / 2] in fragment order
     uint16_t* q;            // EPI_QKV
     uint16_t* kv;           // EPI_QKV: the layer's cache pool
+    // X as an RMSNorm's input times its gain, the rows' scales still to apply (EPI_QKV,
+    // EPI_SILU): row m's sums of squares over each SQ_SPAN columns, [M_pad][K / SQ_SPAN]; null
+    // when X is normed already.
+    const float* row_sq;
+    // EPI_RESIDUAL, when set: out next_gain in bf16 in fragment order into out_n, and out's sums
+    // of squares over each SQ_SPAN columns into out_sq, for the norm that reads out next.
+    const float* next_gain;
+    uint16_t* out_n;
+    float* out_sq;
+};
+
+// The columns a sum of squares spans: a wave's 128 columns of W.
+constexpr int SQ_SPAN = WS * 16;
+
+// The scales 1 / rms of the tile's TM rows from their sums of squares (K / SQ_SPAN parts of
+// SQ_SPAN columns, at most MAX_PARTS, added in order), a thread to a row; each 1 without
+// row_sq. The parts are loaded at once, before the GEMM's own loads.
+constexpr int MAX_PARTS = 4096 / SQ_SPAN;
+struct RowScale {
+    float4 p[MAX_PARTS / 4];
+    __device__ void load(const GemmArgs& g, int m0) {
+        const int quads = g.K / SQ_SPAN / 4;
+        const float* row = g.row_sq ? g.row_sq + (size_t)(m0 + threadIdx.x % TM) * (g.K / SQ_SPAN) : nullptr;
+        if (!row) return;  // uniform
+#pragma unroll
+        for (int i = 0; i < MAX_PARTS / 4; ++i) p[i] = *reinterpret_cast<const float4*>(row + 4 * min(i, quads - 1));
+    }
+    // The loaded values pinned here: nothing computed from them moves above this point (the
+    // compiler would otherwise wait for them before the GEMM's own loads are issued).
+    __device__ void settle() {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int i = 0; i < MAX_PARTS / 4; ++i) {
+            u32x4 t = __builtin_bit_cast(u32x4, p[i]);
+            asm volatile("" : "+v"(t));
+            p[i] = __builtin_bit_cast(float4, t);
+        }
+    }
+    __device__ float scale(const PrefillArgs& a, const GemmArgs& g) const {
+        if (!g.row_sq) return 1.f;
+        const int quads = g.K / SQ_SPAN / 4;
+        float total = 0.f;
+#pragma unroll
+        for (int i = 0; i < MAX_PARTS / 4; ++i) {
+            if (i >= quads) break;
+            total += p[i].x;
+            total += p[i].y;
+            total += p[i].z;
+            total += p[i].w;
+        }
+        return 1.0f / sqrtf(total / (float)g.K + a.eps);
+    }
 };
 
 // The global strip of W that strip `s` (0..7) of wave row `wn` of n-block `nb` takes.
@@ -99,6 +151,7 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
     extern __shared__ uint4 lds[];
     uint4* ws = lds;                     // [NBUF][W_STAGE]
     uint4* xs = lds + NBUF * W_STAGE;    // [NBUF][X_STAGE]
+    float* row_scale = reinterpret_cast<float*>(lds + NBUF * (W_STAGE + X_STAGE));  // [TM]
     int nb, mb;
     tile_of(nb, mb);
     // The wave's index, uniform: the branches on it below are the whole wave's.
@@ -185,10 +238,19 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
     };
 
     uint4 fa[WT + WS], fb[WT + WS];
+    // The rows' scales (q/k/v, gate/up): their loads go first, the GEMM's behind them, and the
+    // scales are taken once the first stage has landed (so have they), reaching LDS long before
+    // the epilogue, past every barrier of the main loop.
+    RowScale rs;
+    const bool scales = EPI != EPI_RESIDUAL && threadIdx.x < TM;  // whole waves
+    if (scales) rs.load(g, m0);
 #pragma unroll
-    for (int p = 0; p < NBUF - 1; ++p)
-        if (p < stages) fetch(p);
+    for (int p = 0; p < NBUF - 1; ++p) fetch(p);  // K >= 1024: 32 stages at least
     landed(0);
+    if (scales) {
+        rs.settle();
+        row_scale[threadIdx.x] = rs.scale(a, g);
+    }
     read(0, fa);
     lds_landed(fa);
     // K is a multiple of 1024: the stages come in pairs, and the accumulators flow through no
@@ -204,35 +266,75 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
     // m0 + 16 (WT wm + t) + lane % 16.
     const int quad = lane / 16;
     if (EPI == EPI_RESIDUAL) {
+        // With next_gain: each lane's squares of its row's 32 values of the wave's 128 columns,
+        // in strip order, then the 4 lanes of a row added (lanes l ^ 16, l ^ 32). The residual
+        // rows of four strips are loaded at once (rows past M read row M - 1, never stored).
+        float sq[WT] = {};
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
+        for (int half = 0; half < 2; ++half) {
+            float4 r[4][WT], gn[4];
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int n = strip_of<EPI>(nb, wn, 4 * half + s4, g.N) * 16 + quad * 4;
+                gn[s4] = *reinterpret_cast<const float4*>((g.next_gain ? g.next_gain : g.residual) + n);
+#pragma unroll
+                for (int t = 0; t < WT; ++t) {
+                    const int m = min(m0 + (wm * WT + t) * 16 + lane % 16, a.M - 1);
+                    r[s4][t] = *reinterpret_cast<const float4*>(g.residual + (size_t)m * g.N + n);
+                }
+            }
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int s = 4 * half + s4;
+                const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
+#pragma unroll
+                for (int t = 0; t < WT; ++t) {
+                    const int m = m0 + (wm * WT + t) * 16 + lane % 16;
+                    if (m >= a.M) continue;
+                    float4 o;
+                    o.x = r[s4][t].x + acc[s][t][0];
+                    o.y = r[s4][t].y + acc[s][t][1];
+                    o.z = r[s4][t].z + acc[s][t][2];
+                    o.w = r[s4][t].w + acc[s][t][3];
+                    *reinterpret_cast<float4*>(g.out + (size_t)m * g.N + n) = o;
+                    if (g.next_gain) {
+                        *reinterpret_cast<uint2*>(g.out_n + act_index(m, n, g.N)) =
+                            make_uint2(pack_bf16x2(o.x * gn[s4].x, o.y * gn[s4].y), pack_bf16x2(o.z * gn[s4].z, o.w * gn[s4].w));
+                        sq[t] += o.x * o.x;
+                        sq[t] += o.y * o.y;
+                        sq[t] += o.z * o.z;
+                        sq[t] += o.w * o.w;
+                    }
+                }
+            }
+        }
+        if (g.next_gain) {
+            const int parts = g.N / SQ_SPAN;
 #pragma unroll
             for (int t = 0; t < WT; ++t) {
+                float v = sq[t];
+                v += lane_xor16(v);
+                v += lane_xor32(v);
                 const int m = m0 + (wm * WT + t) * 16 + lane % 16;
-                if (m >= a.M) continue;
-                const float4 r = *reinterpret_cast<const float4*>(g.residual + (size_t)m * g.N + n);
-                float4 o;
-                o.x = r.x + acc[s][t][0];
-                o.y = r.y + acc[s][t][1];
-                o.z = r.z + acc[s][t][2];
-                o.w = r.w + acc[s][t][3];
-                *reinterpret_cast<float4*>(g.out + (size_t)m * g.N + n) = o;
+                if (quad == 0 && m < a.M) g.out_sq[(size_t)m * parts + nb * (TN / SQ_SPAN) + wn] = v;
             }
         }
     } else if (EPI == EPI_SILU) {
         const int inner = g.N / 2;
+        const float* scale = row_scale;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
 #pragma unroll
             for (int t = 0; t < WT; ++t) {
-                const int m = m0 + (wm * WT + t) * 16 + lane % 16;
+                const int j = (wm * WT + t) * 16 + lane % 16;
+                const int m = m0 + j;
                 if (m >= a.M) continue;
+                const float rs = scale[j];
                 float v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float gate = acc[s][t][i], up = acc[s + 4][t][i];
+                    const float gate = acc[s][t][i] * rs, up = acc[s + 4][t][i] * rs;
                     v[i] = gate / (1.0f + __expf(-gate)) * up;
                 }
                 uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -246,6 +348,7 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
         float* t_sin = t_cos + TM * (HEAD_DIM / 2);            // [TM][32]
         uint32_t* t_pos = reinterpret_cast<uint32_t*>(t_sin + TM * (HEAD_DIM / 2));  // [TM]
         uint32_t* t_blk = t_pos + TM;                           // [TM]
+        const float* t_scale = row_scale;
         if (threadIdx.x < TM) {
             const int j = threadIdx.x;
             const int m = m0 + j;
@@ -282,10 +385,11 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
 #pragma unroll
             for (int t = 0; t < WT; ++t) {
                 const int j = (wm * WT + t) * 16 + lane % 16;  // the row within the tile
+                const float rs = t_scale[j];
                 float own[4], other[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    own[i] = acc[s][t][i];
+                    own[i] = acc[s][t][i] * rs;
                     other[i] = lane_xor32(own[i]);
                 }
                 const uint32_t pos = t_pos[j];
@@ -514,7 +618,8 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
     }
 }
 
-constexpr size_t GEMM_LDS = (size_t)NBUF * (W_STAGE + X_STAGE) * sizeof(uint4);  // 128 KiB
+// The ring (128 KiB) and the rows' scales.
+constexpr size_t GEMM_LDS = (size_t)NBUF * (W_STAGE + X_STAGE) * sizeof(uint4) + TM * sizeof(float);
 
 hipError_t allow(const void* kernel, size_t device_lds) {
     hipFuncAttributes attr{};
@@ -539,14 +644,16 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
     const dim3 rows4((a.M_pad + 3) / 4);
     const int group = a.heads / a.kv_heads;
     const int qkv_rows = (a.heads + 2 * a.kv_heads) * HEAD_DIM;
-    // Layer 0's input norm; each later norm follows the down projection that feeds it.
+    // Layer 0's input norm; each later norm's input (the rows times the gain, and their sums of
+    // squares) comes from the projection before it, the rows' scales applied by the GEMM after.
     if (nlayers > 0)
         dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, b.x,
                  layers[0].input_norm, b.normed, (float*)nullptr);
     const float* input = b.x;  // layer 0 reads the run's states, which stay as written
     for (int l = 0; l < nlayers; ++l) {
         const PrefillLayer& L = layers[l];
-        GemmArgs qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, nullptr, b.q, L.kv};
+        GemmArgs qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, nullptr, b.q, L.kv,
+                     l == 0 ? nullptr : b.row_sq, nullptr, nullptr, nullptr};
         dispatch("prefill_qkv", prefill_gemm<EPI_QKV>, dim3(qkv_rows / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, qkv);
         switch (group) {
             case 1: dispatch("prefill_attention", prefill_attention<2, 1>, dim3(b.ntiles, a.kv_heads), dim3(2 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
@@ -558,18 +665,17 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
         }
         auto residual_gemm = L.od_rows == 4 ? prefill_gemm<EPI_RESIDUAL, 4> : prefill_gemm<EPI_RESIDUAL, 16>;
         if (L.od_rows != 4 && L.od_rows != 16) return hipErrorInvalidValue;
-        GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr};
+        GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr,
+                   nullptr, L.post_norm, b.normed, b.row_sq};
         dispatch("prefill_o", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, o);
-        dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.mid, L.post_norm,
-                 b.normed, (float*)nullptr);
-        GemmArgs gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, nullptr, b.mlp, nullptr, nullptr};
+        GemmArgs gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, nullptr, b.mlp, nullptr, nullptr,
+                    b.row_sq, nullptr, nullptr, nullptr};
         dispatch("prefill_gate_up", prefill_gemm<EPI_SILU>, dim3(2 * a.inner / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, gu);
-        GemmArgs down{L.down, b.mlp, a.inner, a.hidden, b.mid, b.h, nullptr, nullptr, nullptr};
+        // The last layer's output goes to the final norm, which reads the f32 rows.
+        GemmArgs down{L.down, b.mlp, a.inner, a.hidden, b.mid, b.h, nullptr, nullptr, nullptr,
+                      nullptr, l + 1 < nlayers ? layers[l + 1].input_norm : nullptr, b.normed, b.row_sq};
         dispatch("prefill_down", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, down);
         input = b.h;
-        if (l + 1 < nlayers)
-            dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.h,
-                     layers[l + 1].input_norm, b.normed, (float*)nullptr);
     }
     dispatch("prefill_final_norm", prefill_norm<true>, rows4, dim3(256), 0, stream, timer, a, input, final_norm,
              (uint16_t*)nullptr, b.out);

@@ -50,6 +50,7 @@ struct PrefillBuffers {
     uint16_t* q;        // bf16 [M_pad][heads][64]
     uint16_t* attended; // bf16 [M_pad][heads 64] in fragment order
     uint16_t* mlp;      // bf16 [M_pad][inner] in fragment order
+    float* row_sq;      // a norm's input's sums of squares over each 128 columns, [M_pad][hidden / 128]
     float* out;         // after the final norm, f32 [M_pad][hidden]
     const PrefillTile* tiles;
     int ntiles;

@@ -61,6 +61,7 @@ struct PrefillState {
     int M = 0, M_pad = 0, ntiles = 0;  // the last prefill
     float *x = nullptr, *h = nullptr, *mid = nullptr, *out = nullptr;
     uint16_t *normed = nullptr, *q = nullptr, *attended = nullptr, *mlp = nullptr;
+    float* row_sq = nullptr;
     uint32_t *tok_pos = nullptr, *tok_slot = nullptr;
     PrefillTile* tiles = nullptr;
 };
