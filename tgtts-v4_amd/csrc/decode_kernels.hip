@@ -412,72 +412,6 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
 // wave's turns (lane j: block w + 8 j, from the row's copy of its slot's table) and q together,
 // then the first two turns' keys and values.
 
-namespace {
-
-// The online softmax state of one wave: its running max and sum for each head (column) of its
-// lanes, and O^T for the 64 dimensions (lane 16 g + h: head h, dimensions 16 dt + 4 g .. + 3).
-struct Softmax {
-    float m = -INFINITY, total = 0.f;
-    f32x4 o[4] = {};
-
-    // One block of 64 positions p0 .. p0 + 63, those past pos masked.
-    __device__ void block(const uint4 (&kf)[8], const uint4 (&vf)[8], const uint4 (&qf)[2], uint32_t p0, uint32_t pos,
-                          float scale) {
-        const int lane = threadIdx.x % WAVE;
-        f32x4 s[4];
-#pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
-            s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(kf[pt * 2 + ds], qf[ds], s[pt]);
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t p = p0 + pt * 16 + (lane / 16) * 4 + i;
-                const float v = p <= pos ? s[pt][i] * scale : -INFINITY;
-                s[pt][i] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = fmaxf(mx, lane_xor16(mx));
-        mx = fmaxf(mx, lane_xor32(mx));
-        const float m_new = fmaxf(m, mx);  // finite: position p0 <= pos is in the block
-        const float rescale = __expf(m - m_new);
-        float sum = 0.f;
-        uint4 pf[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            uint32_t words[4];
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int pt = 2 * ks + half;
-                // P rounded to bf16 for the product, the sum taken over the rounded values.
-                words[half * 2] = pack_bf16x2(__expf(s[pt][0] - m_new), __expf(s[pt][1] - m_new));
-                words[half * 2 + 1] = pack_bf16x2(__expf(s[pt][2] - m_new), __expf(s[pt][3] - m_new));
-                sum += bf16_lo(words[half * 2]);
-                sum += bf16_hi(words[half * 2]);
-                sum += bf16_lo(words[half * 2 + 1]);
-                sum += bf16_hi(words[half * 2 + 1]);
-            }
-            pf[ks] = make_uint4(words[0], words[1], words[2], words[3]);
-        }
-        sum += lane_xor16(sum);
-        sum += lane_xor32(sum);
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-            o[dt] *= rescale;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) o[dt] = mfma16(vf[dt * 2 + ks], pf[ks], o[dt]);
-        }
-        total = total * rescale + sum;
-        m = m_new;
-    }
-};
-
-}  // namespace
-
 __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
     extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
     __shared__ float sm_m[ATTN_WAVES][16];
@@ -512,26 +446,43 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + lane * 8);
     };
-    Softmax sm;
+    OnlineSoftmax sm;
+    const float scale_log2 = log2_scale(a.scale);
+    // S^T = K Q^T for a turn's block, then its softmax step (masked only in the block holding
+    // the position).
+    auto take = [&](const uint4 (&k)[8], const uint4 (&v)[8], int j) __attribute__((always_inline)) {
+        f32x4 s[4];
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+            s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(k[pt * 2 + ds], qf[ds], s[pt]);
+        }
+        const uint32_t p0 = (uint32_t)(w + ATTN_WAVES * j) * BLOCK_TOKENS;
+        if (p0 + BLOCK_TOKENS - 1 <= pos)
+            sm.block<false>(s, v, p0, pos, scale_log2);
+        else
+            sm.block<true>(s, v, p0, pos, scale_log2);
+    };
     // Two buffers: the first two turns straight (every context up to 16 blocks), then the rest
     // two at a time, each pair's loads issued once the last pair is taken.
     uint4 ka[8], va[8], kb[8], vb[8];
     const bool t0 = has(0), t1 = has(1);
     fetch(0, t0, ka, va);
     fetch(1, t1, kb, vb);
-    if (t0) sm.block(ka, va, qf, (uint32_t)w * BLOCK_TOKENS, pos, a.scale);
-    if (t1) sm.block(kb, vb, qf, (uint32_t)(w + ATTN_WAVES) * BLOCK_TOKENS, pos, a.scale);
+    if (t0) take(ka, va, 0);
+    if (t1) take(kb, vb, 1);
     for (int j = 2; t1 && has(j); j += 2) {
         const bool next = has(j + 1);
         fetch(j, true, ka, va);
         fetch(j + 1, next, kb, vb);
-        sm.block(ka, va, qf, (uint32_t)(w + ATTN_WAVES * j) * BLOCK_TOKENS, pos, a.scale);
+        take(ka, va, j);
         if (!next) break;
-        sm.block(kb, vb, qf, (uint32_t)(w + ATTN_WAVES * (j + 1)) * BLOCK_TOKENS, pos, a.scale);
+        take(kb, vb, j + 1);
     }
     if (lane < 16) {
         sm_m[w][h] = sm.m;
-        sm_l[w][h] = sm.total;
+        sm_l[w][h] = sm.l;
     }
     if (h < group) {
 #pragma unroll
@@ -548,7 +499,7 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
         for (int j = 0; j < ATTN_WAVES; ++j) M = fmaxf(M, sm_m[j][hh]);
         float L = 0.f, O = 0.f;
         for (int j = 0; j < ATTN_WAVES; ++j) {
-            const float f = sm_l[j][hh] > 0.f ? __expf(sm_m[j][hh] - M) : 0.f;
+            const float f = sm_l[j][hh] > 0.f ? __builtin_amdgcn_exp2f(sm_m[j][hh] - M) : 0.f;
             L += sm_l[j][hh] * f;
             O += attn_lds[(j * group + hh) * (HEAD_DIM + 1) + d] * f;
         }

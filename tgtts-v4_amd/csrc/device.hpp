@@ -110,6 +110,66 @@ __device__ __forceinline__ float lane_xor32(float v) {
     return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// Attention's online softmax over blocks of 64 keys for the 16 columns (query heads or
+// (position, head) pairs) of a wave, from S^T = K Q^T in s[pt] (key 16 pt + 4 (lane / 16) + i,
+// column lane % 16) and the block's value tiles: the running max m, kept in log2 units
+// (scores times scale log2(e)), the running sum l of P and O^T in o (lane 16 g + c: column c,
+// dimensions 16 dt + 4 g .. + 3). P is rounded to bf16 for the product P V and summed as
+// rounded, by an MFMA against ones. MASK: keys past the column's position `pos` count for
+// nothing (blocks wholly at or below every column's position need no mask). The first block a
+// column sees holds key 0 <= pos, so m is finite after it.
+struct OnlineSoftmax {
+    float m = -INFINITY, l = 0.f;
+    f32x4 o[4] = {};
+
+    template <bool MASK>
+    __device__ __forceinline__ void block(f32x4 (&s)[4], const uint4 (&vf)[8], uint32_t p0, uint32_t pos, float scale_log2) {
+        const int lane = threadIdx.x % WAVE;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (MASK && p0 + pt * 16 + (lane / 16) * 4 + i > pos) s[pt][i] = -INFINITY;
+                mx = fmaxf(mx, s[pt][i]);
+            }
+        mx = fmaxf(mx, lane_xor16(mx));
+        mx = fmaxf(mx, lane_xor32(mx));
+        const float m_new = fmaxf(m, mx * scale_log2);
+        const float rescale = __builtin_amdgcn_exp2f(m - m_new);
+        uint4 pf[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            uint32_t words[4];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const f32x4 v = s[2 * ks + half];
+                words[half * 2] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(v[0], scale_log2, -m_new)),
+                                              __builtin_amdgcn_exp2f(fmaf(v[1], scale_log2, -m_new)));
+                words[half * 2 + 1] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(v[2], scale_log2, -m_new)),
+                                                  __builtin_amdgcn_exp2f(fmaf(v[3], scale_log2, -m_new)));
+            }
+            pf[ks] = make_uint4(words[0], words[1], words[2], words[3]);
+        }
+        // Column sums of P: every row of ones^T P is the sum (bf16 1.0 is 0x3f80).
+        const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+        f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) sum = mfma16(ones, pf[ks], sum);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            o[dt] *= rescale;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) o[dt] = mfma16(vf[dt * 2 + ks], pf[ks], o[dt]);
+        }
+        l = l * rescale + sum[0];
+        m = m_new;
+    }
+};
+
+// scale log2(e): scores times this are in the units v_exp_f32 (2^x) takes.
+__host__ __device__ constexpr float log2_scale(float scale) { return scale * 1.4426950408889634f; }
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));

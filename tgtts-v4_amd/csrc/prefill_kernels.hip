@@ -512,15 +512,10 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
 #pragma unroll
         for (int ds = 0; ds < 2; ++ds) qf[cg][ds] = load16(q + (row * H + head) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
     }
-    float m[CG], l[CG];
-    f32x4 o[CG][4];
-#pragma unroll
-    for (int cg = 0; cg < CG; ++cg) {
-        m[cg] = -INFINITY;
-        l[cg] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[cg][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    OnlineSoftmax sm[CG];
+    const float scale_log2 = log2_scale(a.scale);
+    // The wave's first position: blocks wholly at or below it need no mask.
+    const uint32_t first = tile.pos0 + w * TOK;
 
     auto fetch = [&](int bi, uint4 (&r)[PER_THREAD]) {
         const uint32_t blk = a.table[(size_t)tile.slot * a.max_blocks + bi];
@@ -542,6 +537,7 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
 #pragma unroll
         for (int i = 0; i < 8; ++i) vf[i] = stage[buf][KV_TILE / 8 + i * 64 + lane];
         const uint32_t p0 = (uint32_t)bi * BLOCK_TOKENS;
+        const bool full = p0 + BLOCK_TOKENS - 1 <= first;
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
             f32x4 s[4];
@@ -551,49 +547,10 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
 #pragma unroll
                 for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(kf[pt * 2 + ds], qf[cg][ds], s[pt]);
             }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int pt = 0; pt < 4; ++pt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t p = p0 + pt * 16 + (lane / 16) * 4 + i;
-                    const float v = p <= cpos[cg] ? s[pt][i] * a.scale : -INFINITY;
-                    s[pt][i] = v;
-                    mx = fmaxf(mx, v);
-                }
-            mx = fmaxf(mx, lane_xor16(mx));
-            mx = fmaxf(mx, lane_xor32(mx));
-            // Block 0 holds position 0, which every column sees, so m is finite after it.
-            const float m_new = fmaxf(m[cg], mx);
-            const float rescale = __expf(m[cg] - m_new);
-            float sum = 0.f;
-            uint4 pf[2];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                uint32_t words[4];
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const int pt = 2 * ks + half;
-                    // P rounded to bf16 for the product, the sum taken over the rounded values.
-                    words[half * 2] = pack_bf16x2(__expf(s[pt][0] - m_new), __expf(s[pt][1] - m_new));
-                    words[half * 2 + 1] = pack_bf16x2(__expf(s[pt][2] - m_new), __expf(s[pt][3] - m_new));
-                    sum += bf16_lo(words[half * 2]);
-                    sum += bf16_hi(words[half * 2]);
-                    sum += bf16_lo(words[half * 2 + 1]);
-                    sum += bf16_hi(words[half * 2 + 1]);
-                }
-                pf[ks] = make_uint4(words[0], words[1], words[2], words[3]);
-            }
-            sum += lane_xor16(sum);
-            sum += lane_xor32(sum);
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                o[cg][dt] *= rescale;
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) o[cg][dt] = mfma16(vf[dt * 2 + ks], pf[ks], o[cg][dt]);
-            }
-            l[cg] = l[cg] * rescale + sum;
-            m[cg] = m_new;
+            if (full)
+                sm[cg].template block<false>(s, vf, p0, cpos[cg], scale_log2);
+            else
+                sm[cg].template block<true>(s, vf, p0, cpos[cg], scale_log2);
         }
         if (bi + 1 < blocks) {
 #pragma unroll
@@ -607,12 +564,12 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
         if (tok >= (int)tile.count) continue;
         const int head = kv * group + col % group;
         const size_t row = tile.row0 + tok;
-        const float inv = 1.0f / l[cg];
+        const float inv = 1.0f / sm[cg].l;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
             const int d = dt * 16 + (lane / 16) * 4;
-            uint2 packed = make_uint2(pack_bf16x2(o[cg][dt][0] * inv, o[cg][dt][1] * inv),
-                                      pack_bf16x2(o[cg][dt][2] * inv, o[cg][dt][3] * inv));
+            const f32x4 o = sm[cg].o[dt];
+            uint2 packed = make_uint2(pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv));
             *reinterpret_cast<uint2*>(attended + act_index((int)row, head * HEAD_DIM + d, H * HEAD_DIM)) = packed;
         }
     }
