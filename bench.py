@@ -8,8 +8,10 @@ kernels launched as one recorded HIP graph. `value` is decode steps per second.
 
 Beside it on the same JSON line:
 - "batches": decode at 16 and 64 requests, contexts drawn U[64, 1024] (seeded), 200 steps;
-- "roofline": the dominant kernel of the step, its algorithmic bytes per launch over its average
-  duration from per-dispatch HIP events (each recorded by the kernel's own dispatch);
+- "roofline": the step's dominant kernel for HBM, the one whose launches move the most
+  algorithmic bytes per step (gate/up: 56 % of the weights), its algorithmic bytes per launch over
+  its average duration from per-dispatch HIP events (each recorded by the kernel's own dispatch);
+  "roofline_longest" the same for the kernel with the most time per step;
 - "cpu_baseline": the fp32 CPU path (the oracle, OpenMP over the host's cores) on a bounded
   sample of the same workload;
 - "prefill": 8 runs of 2048 positions at once, tok/s and the GEMMs' share of bf16 MFMA peak;
@@ -406,7 +408,7 @@ def main() -> int:
     log(f"device {report['name']} {report['arch']} {report['compute_units']} CUs {report['clock_khz']} kHz")
 
     rng = np.random.default_rng(1234)
-    headline_contexts = [PROMPT] * args.batch if args.batch == 1 else list(rng.integers(64, 1025, args.batch))
+    headline_contexts = [PROMPT] * args.batch if args.batch == 1 else [int(c) for c in np.random.default_rng(args.batch).integers(64, 1025, args.batch)]
     head = run_decode(ctx, weights, args.batch, headline_contexts, args.steps, args.warmup)
     shape = head.pop("shape")
     log(f"batch {args.batch}: {head['steps_per_s']:.1f} steps/s, {head['ms_per_step']*1e3:.1f} us/step, "
@@ -462,20 +464,27 @@ def main() -> int:
             f"{tts['lm_side_ms']:.2f} ms, sampler {tts['sampler_ms']:.2f} ms)")
         tts = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in tts.items()}
 
-    # The roofline of the step's dominant kernel: the one with the most time per step.
-    dom_label, dom = max(head["kernels"].items(), key=lambda kv: kv[1]["per_step_us"])
-    achieved = dom["bytes_per_launch"] / (dom["avg_us"] * 1e-6) / 1e9
-    roofline = {
-        "bound": "hbm",
-        "kernel": dom_label,
-        "achieved": round(achieved, 1),
-        "peak": HBM_PEAK / 1e9,
-        "unit": "GB/s",
-        "frac": round(achieved / (HBM_PEAK / 1e9), 4),
-        "traffic": measured_traffic(dom_label, f"batch {args.batch}"),
-        "bytes_per_launch": dom["bytes_per_launch"],
-        "avg_us": round(dom["avg_us"], 3),
-    }
+    # The roofline of the step's dominant kernel for HBM: the one whose launches move the most
+    # algorithmic bytes per step; beside it, the kernel with the most time per step.
+    def kernel_roofline(label, k):
+        achieved = k["bytes_per_launch"] / (k["avg_us"] * 1e-6) / 1e9
+        return {
+            "bound": "hbm",
+            "kernel": label,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(achieved / (HBM_PEAK / 1e9), 4),
+            "traffic": measured_traffic(label, f"batch {args.batch}"),
+            "bytes_per_launch": k["bytes_per_launch"],
+            "avg_us": round(k["avg_us"], 3),
+        }
+
+    kernels = head["kernels"]
+    by_bytes = max(kernels.items(), key=lambda kv: kv[1]["bytes_per_launch"] * kv[1]["per_step_us"] / kv[1]["avg_us"])
+    by_time = max(kernels.items(), key=lambda kv: kv[1]["per_step_us"])
+    roofline = kernel_roofline(*by_bytes)
+    roofline_longest = kernel_roofline(*by_time)
 
     cpu = None
     if not args.no_cpu:
@@ -511,6 +520,7 @@ def main() -> int:
         "hbm_fraction_step": round(head["hbm_fraction"], 4),
         "gpu_ms_per_step": round(head["gpu_ms_per_step"], 4),
         "roofline": roofline,
+        "roofline_longest": roofline_longest,
         "cpu_baseline": cpu,
         "batches": batches,
         "prefill": prefill,
