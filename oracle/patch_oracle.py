@@ -22,9 +22,11 @@ Pinning (tests/test_patch_oracle.py): the schedule's closed-form ends (t_span[0]
 t_span[n] = 0), its 9 evaluations for 10 steps and the zero-init count for other step counts;
 the time embedding's t = 0 closed form; CFG-Zero*'s reductions (guidance 1 gives the conditional
 velocity, equal velocities give it back, a zero unconditional velocity gives cfg v_c); the
-quantizer's special cases (0, saturation, ties to even, levels on the 1/L grid); and the local
+quantizer's special cases (0, saturation, ties to even, levels on the 1/L grid); the local
 stack against an independent torch float64 model built from library ops
-(scaled_dot_product_attention without a mask, silu, rms_norm by hand).
+(scaled_dot_product_attention without a mask, silu, rms_norm by hand); time_mlp and the layers
+between the LMs against torch's linear and silu (a transposed weight must fail); and the whole
+sampler against the closed form it takes when out_proj reads nothing.
 """
 
 from __future__ import annotations

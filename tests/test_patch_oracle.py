@@ -183,3 +183,36 @@ def test_the_sampler_is_the_euler_closed_form_when_out_proj_reads_nothing():
         g = po.cfg_zero_star(b[0], b[0], sampling[r, 1])
         assert np.allclose(patch[r], x0[r] - total * g, atol=1e-12)
         assert np.allclose(x0[r], sampling[r, 0] * noise[r])
+
+
+def test_the_time_mlp_and_the_heads_match_torch_library_ops():
+    """time_mlp (dit.rs:409-421) and the layers between the LMs (lm_side.rs:405-460) against
+    torch's linear and silu in float64: the weights' orientation (y = x W^T + b), the bias and the
+    SiLU are the library's. A planted defect (W taken transposed) must show."""
+    import torch
+    import torch.nn.functional as F
+
+    from tgx.synth import heads_weights
+
+    _, w = _small_dit(1)
+    t = lambda a: torch.as_tensor(np.asarray(a, np.float64))
+    x = po.time_embedding(0.37, 1024).astype(np.float64)
+    want = F.linear(F.silu(F.linear(t(x), t(w["time_mlp.linear_1.weight"]), t(w["time_mlp.linear_1.bias"]))),
+                    t(w["time_mlp.linear_2.weight"]), t(w["time_mlp.linear_2.bias"])).numpy()
+    assert np.max(np.abs(po.time_mlp(w, "time_mlp", x) - want)) < 1e-12
+
+    h = heads_weights(5, 1024, 1024, 256, 64, dtype="f32")
+    rng = np.random.default_rng(4)
+    lv = rng.standard_normal((3, 64))
+    embed = rng.standard_normal((3, 1024))
+    got = po.heads_after_levels(h, lv, embed)
+    lin = lambda name, v, bias=True: F.linear(v, t(h[f"{name}.weight"]), t(h[f"{name}.bias"]) if bias else None)
+    lm_hidden = lin("fsq_layer.out_proj", t(lv))
+    stop_hidden = F.silu(lin("stop_proj", lm_hidden))
+    want = (lm_hidden, lin("fusion_concat_proj", torch.cat([lm_hidden, t(embed)], dim=-1)),
+            lin("lm_to_dit_proj", lm_hidden), stop_hidden, lin("stop_head", stop_hidden, bias=False))
+    for g_, w_ in zip(got, want):
+        assert np.max(np.abs(g_ - w_.numpy())) < 1e-12
+    wrong = dict(h)
+    wrong["stop_proj.weight"] = np.ascontiguousarray(h["stop_proj.weight"].T)
+    assert np.max(np.abs(po.heads_after_levels(wrong, lv, embed)[3] - want[3].numpy())) > 1e-3
