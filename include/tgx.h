@@ -315,6 +315,49 @@ tgx_status tgx_lm_side_dispatches(const tgx_lm_side* s, int* out);
 tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times);
 tgx_status tgx_patch_elapsed_ms(const tgx_lm_side* side, float* out);
 
+/* ---- the local encoder: crates/graph/src/local/encoder.rs ---- */
+
+typedef struct tgx_encoder tgx_encoder;
+
+/* Encoder::new (encoder.rs:171-183): the encoder's stack as a tgx_shape (head_dim 64; capacity
+ * is ignored, a row's sequence is its learned token and the patch's frames, 1 + patch_size
+ * tokens), for patches of patch->feat_dim channels by patch->patch_size frames, patch->rows rows
+ * at once (patch->timesteps is ignored); weights zero until loaded. */
+tgx_status tgx_encoder_create(tgx_context* ctx, const tgx_shape* stack, const tgx_patch_shape* patch,
+                              tgx_encoder** out);
+void tgx_encoder_destroy(tgx_encoder* e);
+/* load_encoder (encoder.rs:133-162), one tensor: the stack's as tgx_decoder_load names them,
+ * "special_token" [hidden], "in_proj.weight" [hidden][feat_dim] and "in_proj.bias" [hidden]. */
+tgx_status tgx_encoder_load(tgx_encoder* e, const char* name, const void* data, tgx_dtype dtype,
+                            size_t count);
+/* Encoder::encode (encoder.rs:194-198): each row's embedding [rows][hidden] f32 from its patch
+ * [feat_dim][patch_size] f32, a row after a row; waits. */
+tgx_status tgx_encoder_encode(tgx_encoder* e, const float* patch, float* out);
+tgx_status tgx_encoder_dispatches(const tgx_encoder* e, int* out);
+
+/* ---- the patch step with its encoder: crates/graph/src/patch.rs ---- */
+
+typedef struct tgx_patch_step tgx_patch_step;
+
+/* patch_batch_graph (patch.rs:98-166) over an encoder, an LM side and a sampler made alike (one
+ * context, one row count, the encoder as wide as the LM side's encoder width, the sampler as wide
+ * as its DiT width, one patch shape): each step embeds the patches before, steps the LM side on
+ * the embeddings and samples on its mu, nothing leaving the device between them. The three stay
+ * owned by the caller and must outlive the step. */
+tgx_status tgx_patch_step_create(tgx_encoder* e, tgx_lm_side* side, tgx_sampler* sampler, tgx_patch_step** out);
+void tgx_patch_step_destroy(tgx_patch_step* p);
+/* PatchStep::run_rows (patch.rs:356-415): the rows' places (spare ones TGX_SPARE), each row's
+ * patch before `cond` and `noise` ([rows][feat_dim][patch_size]) and `sampling` ([rows][2]:
+ * temperature, guidance scale); returns each row's patch and stop logits [rows][2]. Waits. */
+tgx_status tgx_patch_step_run(tgx_patch_step* p, const tgx_row* rows, int nrows, const float* cond,
+                              const float* noise, const float* sampling, float* patch, float* stop_logits);
+/* Launches `times` steps back to back over what the device holds (with `advance` every placed row
+ * moves on a position each step; the slots must hold the blocks); tgx_patch_step_wait waits and
+ * tgx_patch_step_elapsed_ms times them. */
+tgx_status tgx_patch_step_launch(tgx_patch_step* p, int times, int advance);
+tgx_status tgx_patch_step_wait(tgx_patch_step* p);
+tgx_status tgx_patch_step_elapsed_ms(const tgx_patch_step* p, float* out);
+
 #ifdef __cplusplus
 }
 #endif

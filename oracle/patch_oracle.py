@@ -6,6 +6,9 @@ A CPU restatement of what runs around the LMs for each patch:
                           the reference computes them on the host
   time_embedding          dit.rs:367-381 (float32 recipe with libm's expf/sinf/cosf)
   time_mlp                dit.rs:390-422, linear_2(SiLU(linear_1(x))) in float64
+  encode                  crates/graph/src/local/encoder.rs:42-128: the learned token and
+                          in_proj of the patch's frames through the local stack, the learned
+                          token's output
   local_stack             crates/graph/src/local/mod.rs:549-656 with local_{norm,qkv_rope,
                           attention,partial,add_norm,gate_up}.comp: a bidirectional MiniCPM-4
                           stack over sequences of T tokens, RoPE at each token's place m % T
@@ -169,6 +172,20 @@ def local_stack(w: dict, s, x: np.ndarray, T: int, rope_on: bool = True) -> np.n
         gate, up = gu[:, : s.inner], gu[:, s.inner :]
         x = x + (gate / (1.0 + np.exp(-gate)) * up) @ W(f"layers.{l}.down_proj").T
     return rmsnorm(x, w["norm"], s.eps)
+
+
+def encode(w: dict, s, feat: int, frames: int, patches) -> np.ndarray:
+    """VoxCPMLocEnc for each row (crates/graph/src/local/encoder.rs:42-128): the learned token,
+    then in_proj of the patch's frames, through the local stack (a sequence of 1 + frames tokens
+    to a row); the learned token's output after the final norm, [rows][hidden] float64."""
+    patches = np.asarray(patches, dtype=np.float64).reshape(-1, feat, frames)
+    rows, h = patches.shape[0], s.hidden
+    W = lambda n: np.asarray(w[n], dtype=np.float64)
+    tokens = np.zeros((rows, 1 + frames, h))
+    tokens[:, 0] = W("special_token")
+    tokens[:, 1:] = (W("in_proj.weight") @ patches).transpose(0, 2, 1) + W("in_proj.bias")
+    out = local_stack(w, s, tokens.reshape(rows * (1 + frames), h), 1 + frames).reshape(rows, 1 + frames, h)
+    return out[:, 0]
 
 
 def cfg_zero_star(v_c: np.ndarray, v_u: np.ndarray, cfg: float) -> np.ndarray:

@@ -251,3 +251,87 @@ def test_a_row_of_the_lm_side_is_the_same_beside_others_as_alone(ctx):
         mu, stop = one.step_rows([tgx.Row(s, 0)], encs[s][2:3])
         assert np.array_equal(mu[0], outs[s][0][2]) and np.array_equal(stop[0], outs[s][1][2]), s
     one.close()
+
+
+# ---- the local encoder and the whole patch step ----
+
+def _encoder(ctx, rows, spec, weights):
+    import tgx
+    from tgx.patch import Encoder, PatchShape
+
+    shape = tgx.Shape(hidden=spec.hidden, inner=spec.inner, heads=spec.heads, kv_heads=spec.kv_heads,
+                      head_dim=spec.head_dim, layers=spec.layers, capacity=16, eps=spec.eps,
+                      rope_theta=spec.rope_theta)
+    e = Encoder(ctx, shape, PatchShape(FEAT, FRAMES, STEPS, rows))
+    e.load_all(weights)
+    return e
+
+
+def _encoder_spec(layers=4):
+    from tgx.synth import StackSpec
+
+    return StackSpec(layers=layers, hidden=1024, inner=4096, dtype="bf16", seed=13)
+
+
+def test_the_encoder_matches_the_oracle_and_a_row_encodes_as_alone(ctx):
+    """Encoder::encode (crates/graph/src/local/encoder.rs:194-198) against the oracle within the
+    tolerance; the frames reversed (which only RoPE tells apart) must fail it; a row beside others
+    is bit for bit as alone."""
+    import patch_oracle as po
+    from tgx.synth import encoder_weights
+
+    spec = _encoder_spec()
+    w = encoder_weights(spec, FEAT)
+    rng = np.random.default_rng(14)
+    patches = rng.standard_normal((3, FEAT, FRAMES)).astype(np.float32)
+    e = _encoder(ctx, 3, spec, w)
+    print(f"[encoder] rows 3, {e.dispatches()} dispatches", flush=True)
+    got = e.encode(patches)
+    assert np.array_equal(got, e.encode(patches))
+    s = po.StackShape(hidden=spec.hidden, inner=spec.inner, heads=spec.heads, kv_heads=spec.kv_heads,
+                      layers=spec.layers, eps=spec.eps, rope_theta=spec.rope_theta)
+    want = po.encode(w, s, FEAT, FRAMES, patches)
+    for r in range(3):
+        d = distance(got[r], want[r])
+        print(f"[encoder] row {r}: {d}", flush=True)
+        assert within(d), (r, d)
+    wrong = po.encode(w, s, FEAT, FRAMES, patches[:, :, ::-1])
+    assert not all(within(distance(got[r], wrong[r])) for r in range(3))
+    e.close()
+    one = _encoder(ctx, 1, spec, w)
+    assert np.array_equal(one.encode(patches[2:3])[0], got[2])
+    one.close()
+
+
+def test_the_patch_step_is_the_encoder_the_lm_side_and_the_sampler_in_turn(ctx):
+    """PatchStep::run_rows (crates/graph/src/patch.rs:356-415) on the device throughout gives, bit
+    for bit, what the three give when each is run alone and the host hands their outputs on:
+    the encoder's embedding of the patch before to the LM side, its mu to the sampler."""
+    import tgx
+    from tgx.patch import PatchStep
+    from tgx.synth import encoder_weights, sampler_weights
+
+    rows = 3
+    espec, dspec = _encoder_spec(2), _dit_spec(2)
+    enc = _encoder(ctx, rows, espec, encoder_weights(espec, FEAT))
+    smp = _sampler(ctx, rows, dspec, sampler_weights(dspec, FEAT))
+    _, _, w = _lm_weights()
+    side = _lm_side(ctx, rows, w)
+    _, cond, noise, sampling = _inputs(rows, seed=15)
+    at = [tgx.Row(0, r) for r in range(rows)]
+    embedding = enc.encode(cond)
+    mu, stop = side.step_rows(at, embedding)
+    patch = smp.sample(mu, cond, noise, sampling)
+    step = PatchStep(enc, side, smp)
+    got_patch, got_stop = step.run_rows(at, cond, noise, sampling)
+    assert np.array_equal(got_stop, stop)
+    assert np.array_equal(got_patch, patch)
+    # On to the next position, launched over what the device holds, then read back.
+    at1 = [tgx.Row(1, r) for r in range(rows)]
+    mu1, stop1 = side.step_rows(at1, embedding)
+    patch1 = smp.sample(mu1, cond, noise, sampling)
+    got_patch1, got_stop1 = step.run_rows(at1, cond, noise, sampling)
+    assert np.array_equal(got_patch1, patch1) and np.array_equal(got_stop1, stop1)
+    step.close()
+    for o in (enc, smp, side):
+        o.close()

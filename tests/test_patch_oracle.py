@@ -216,3 +216,30 @@ def test_the_time_mlp_and_the_heads_match_torch_library_ops():
     wrong = dict(h)
     wrong["stop_proj.weight"] = np.ascontiguousarray(h["stop_proj.weight"].T)
     assert np.max(np.abs(po.heads_after_levels(wrong, lv, embed)[3] - want[3].numpy())) > 1e-3
+
+
+def test_the_encoder_matches_an_independent_torch_model():
+    """encode (crates/graph/src/local/encoder.rs:42-128) against the torch stack model fed
+    [special; in_proj(frames)] built with torch's linear; a row's embedding is its own alone; the
+    frames reversed, which only RoPE tells apart, must change it (the reference's defect check,
+    crates/graph/tests/local.rs:496-505)."""
+    import torch
+    import torch.nn.functional as F
+
+    from tgx.synth import StackSpec, encoder_weights
+
+    spec = StackSpec(layers=2, hidden=1024, inner=1024, dtype="f32", seed=6)
+    w = encoder_weights(spec, 64)
+    s = po.StackShape(hidden=spec.hidden, inner=spec.inner, layers=spec.layers)
+    rng = np.random.default_rng(12)
+    patches = rng.standard_normal((3, 64, 4))
+    got = po.encode(w, s, 64, 4, patches)
+    t = lambda a: torch.as_tensor(np.asarray(a, np.float64))
+    frames = F.linear(t(patches).transpose(1, 2), t(w["in_proj.weight"]), t(w["in_proj.bias"]))  # [rows][4][h]
+    tokens = torch.cat([t(w["special_token"]).expand(3, 1, -1), frames], dim=1).reshape(15, -1).numpy()
+    want = _torch_local_stack(w, s, tokens, 5).reshape(3, 5, -1)[:, 0]
+    assert np.max(np.abs(got - want)) < 1e-9
+    alone = po.encode(w, s, 64, 4, patches[1:2])
+    assert np.allclose(alone[0], got[1], atol=1e-12)
+    reversed_ = po.encode(w, s, 64, 4, patches[:, :, ::-1])
+    assert np.max(np.abs(reversed_ - got)) > 1e-3

@@ -40,6 +40,7 @@ SOURCES = {
     "prefill.cpp": HOST_FLAGS,
     "api.cpp": HOST_FLAGS,
     "sampler.cpp": HOST_FLAGS,
+    "encoder.cpp": HOST_FLAGS,
     "lm_side.cpp": HOST_FLAGS,
     "api_patch.cpp": HOST_FLAGS,
 }

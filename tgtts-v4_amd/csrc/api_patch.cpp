@@ -236,4 +236,86 @@ tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times) 
 
 tgx_status tgx_patch_elapsed_ms(const tgx_lm_side* side, float* out) { return tgx_lm_side_elapsed_ms(side, out); }
 
+// ---- the encoder ----
+
+tgx_status tgx_encoder_create(tgx_context* ctx, const tgx_shape* stack, const tgx_patch_shape* patch, tgx_encoder** out) {
+    clear_error();
+    if (!ctx || !out) return fail(TGX_E_ARG, "null context or output");
+    *out = nullptr;
+    Encoder* e = nullptr;
+    TGX_TRY(encoder_create(ctx->ctx, stack, patch, &e));
+    *out = new tgx_encoder{e};
+    return TGX_OK;
+}
+
+void tgx_encoder_destroy(tgx_encoder* e) {
+    if (!e) return;
+    encoder_destroy(e->e);
+    delete e;
+}
+
+tgx_status tgx_encoder_load(tgx_encoder* e, const char* name, const void* data, tgx_dtype dtype, size_t count) {
+    clear_error();
+    if (!e) return fail(TGX_E_ARG, "null encoder");
+    return encoder_load(e->e, name, data, dtype, count);
+}
+
+tgx_status tgx_encoder_encode(tgx_encoder* e, const float* patch, float* out) {
+    clear_error();
+    if (!e) return fail(TGX_E_ARG, "null encoder");
+    return encoder_encode(e->e, patch, out);
+}
+
+tgx_status tgx_encoder_dispatches(const tgx_encoder* e, int* out) {
+    clear_error();
+    if (!e || !out) return fail(TGX_E_ARG, "null encoder or output");
+    *out = e->e->dispatches;
+    return TGX_OK;
+}
+
+// ---- the patch step with its encoder ----
+
+tgx_status tgx_patch_step_create(tgx_encoder* e, tgx_lm_side* side, tgx_sampler* sampler, tgx_patch_step** out) {
+    clear_error();
+    if (!e || !side || !sampler || !out) return fail(TGX_E_ARG, "null encoder, LM side, sampler or output");
+    *out = nullptr;
+    PatchStep* p = nullptr;
+    TGX_TRY(patch_step_create(e->e, side->s, sampler->s, &p));
+    *out = new tgx_patch_step{p};
+    return TGX_OK;
+}
+
+void tgx_patch_step_destroy(tgx_patch_step* p) {
+    if (!p) return;
+    patch_step_destroy(p->p);
+    delete p;
+}
+
+tgx_status tgx_patch_step_run(tgx_patch_step* p, const tgx_row* rows, int nrows, const float* cond, const float* noise,
+                              const float* sampling, float* patch, float* stop_logits) {
+    clear_error();
+    if (!p) return fail(TGX_E_ARG, "null patch step");
+    return patch_step_run(p->p, rows, nrows, cond, noise, sampling, patch, stop_logits);
+}
+
+tgx_status tgx_patch_step_launch(tgx_patch_step* p, int times, int advance) {
+    clear_error();
+    if (!p) return fail(TGX_E_ARG, "null patch step");
+    return patch_step_launch(p->p, times, advance);
+}
+
+tgx_status tgx_patch_step_wait(tgx_patch_step* p) {
+    clear_error();
+    if (!p) return fail(TGX_E_ARG, "null patch step");
+    return patch_step_wait(p->p);
+}
+
+tgx_status tgx_patch_step_elapsed_ms(const tgx_patch_step* p, float* out) {
+    clear_error();
+    if (!p || !out) return fail(TGX_E_ARG, "null patch step or output");
+    if (p->p->pending) return fail(TGX_E_BUSY, "a step is under way");
+    TGX_HIP(hipEventElapsedTime(out, p->p->ev_start, p->p->ev_end));
+    return TGX_OK;
+}
+
 }  // extern "C"

@@ -17,3 +17,9 @@ struct tgx_lm_side {
     tgx::LmSide* s;
     tgx_decoder base, residual;
 };
+struct tgx_encoder {
+    tgx::Encoder* e;
+};
+struct tgx_patch_step {
+    tgx::PatchStep* p;
+};

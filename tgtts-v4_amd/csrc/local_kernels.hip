@@ -375,8 +375,8 @@ __global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
             for (int f = 0; f < F; ++f) acc[f] += w4[i] * frames[f * C + 4 * v + i];
     }
     const int K = a.hidden;
-    for (int s = 0; s < 2; ++s) {
-        const size_t seq0 = (size_t)(row * 2 + s) * a.T;
+    for (int s = 0; s < e.seqs; ++s) {
+        const size_t seq0 = (size_t)(row * e.seqs + s) * a.T;
 #pragma unroll
         for (int f = 0; f < F; ++f) e.x0[(seq0 + e.first + f) * K + n] = acc[f];
         for (int t = 0; t < e.copies; ++t) {

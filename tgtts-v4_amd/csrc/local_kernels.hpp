@@ -47,8 +47,9 @@ struct LocalBuffers {
 
 // A linear layer over a patch's frames, `src` [rows][channels][frames] (channel-major, as the
 // sampler keeps a patch): W f32 [hidden][channels] and bias [hidden]; the FRAMES results are
-// written as tokens `first` .. of both of the row's sequences, and `copies` tokens of `copy_src`
-// at `copy_at` (per row unless `shared`; zero in the second sequence when `guided`).
+// written as tokens `first` .. of each of the row's `seqs` sequences (2 for the sampler's
+// conditional and unconditional ones, 1 for the encoder), and `copies` tokens of `copy_src` at
+// `copy_at` (per row unless `shared`; zero in the second sequence when `guided`).
 struct EmbedArgs {
     const float* src;
     const float* w;
@@ -56,6 +57,7 @@ struct EmbedArgs {
     const float* copy_src;
     float* x0;
     int channels, frames, first, copy_at, copies, guided, shared;
+    int seqs;
 };
 
 // One Euler step: velocities out_proj(out[tokens first..]) + b of the conditional and the

@@ -71,6 +71,43 @@ tgx_status sampler_read(Sampler* s, float* patch);
 // The sample's dispatches on the context's stream (timed when `timer`), mu read from `mu`.
 hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, int* dispatches);
 tgx_status sampler_prepare(Sampler* s);
+// Records the sample as the sampler's graph.
+tgx_status sampler_record(Sampler* s);
+
+// The local encoder (crates/graph/src/local/encoder.rs:42-128): each row's patch before, its
+// frames through in_proj after a learned token, through a bidirectional local stack (a sequence
+// of 1 + frames tokens to a row); the learned token's output after the final norm is the row's
+// embedding.
+struct Encoder {
+    Context* ctx = nullptr;
+    Shape shape{};  // the stack; capacity = T
+    int feat = 0, frames = 0, rows = 0;
+    int T = 0, M = 0, M_pad = 0, o_parts = 2, down_parts = 4;
+    std::vector<DeviceBuffer> allocations;
+    size_t device_bytes = 0;
+    std::vector<Layer> layers;
+    float* final_norm = nullptr;
+    float *in_w = nullptr, *in_b = nullptr, *special = nullptr;  // f32 [hidden][feat], [hidden], [hidden]
+    float *cos = nullptr, *sin = nullptr;
+    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr;
+    uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
+    float *patch = nullptr, *embedding = nullptr;  // [rows][feat][frames], [rows][hidden]
+    hipGraphExec_t exec = nullptr;  // patch -> embedding
+    int dispatches = 0;
+    hipEvent_t ev_start = nullptr, ev_end = nullptr;
+    bool pending = false;
+
+    LocalArgs args() const;
+};
+
+tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_shape* patch, Encoder** out);
+void encoder_destroy(Encoder* e);
+tgx_status encoder_load(Encoder* e, const char* name, const void* data, tgx_dtype dtype, size_t count);
+// The encoding's dispatches on the context's stream: the patches read from `patch`
+// ([rows][feat][frames]), the embeddings written to `dst` ([rows][hidden]).
+hipError_t encoder_enqueue(Encoder* e, const float* patch, float* dst, int* dispatches);
+// Embeds the rows' patches (host arrays) and waits: Encoder::encode (encoder.rs:194-198).
+tgx_status encoder_encode(Encoder* e, const float* patch, float* out);
 
 // The LM side: both LMs' decoders, the heads, and the tensors between them.
 struct Linear {
@@ -103,5 +140,29 @@ tgx_status lm_side_launch(LmSide* s, int times, int advance);
 tgx_status lm_side_wait(LmSide* s);
 tgx_status lm_side_read(LmSide* s, const char* tensor, float* out, size_t count);
 hipError_t lm_side_enqueue(LmSide* s, int advance, DispatchTimer* timer, int* dispatches);
+
+// A patch step (crates/graph/src/patch.rs:98-166, 356-415): the encoder embeds each row's patch
+// before, the LM side steps on the embeddings, the sampler samples on the LM side's mu and the
+// same patch before. The three share a context and a row count; nothing leaves the device
+// between them.
+struct PatchStep {
+    Encoder* encoder = nullptr;
+    LmSide* side = nullptr;
+    Sampler* sampler = nullptr;
+    hipGraphExec_t encode = nullptr;  // the sampler's cond -> the LM side's enc
+    hipEvent_t ev_start = nullptr, ev_end = nullptr;
+    bool pending = false;
+};
+
+tgx_status patch_step_create(Encoder* e, LmSide* side, Sampler* s, PatchStep** out);
+void patch_step_destroy(PatchStep* p);
+// PatchStep::run_rows (patch.rs:356-415): places the rows, copies the patches before, the noise
+// and the sampling in, runs the step and waits; the patches and the stop logits out.
+tgx_status patch_step_run(PatchStep* p, const tgx_row* rows, int nrows, const float* cond, const float* noise,
+                          const float* sampling, float* patch, float* stop_logits);
+// `times` steps back to back over what the device holds (with `advance` every placed row moves
+// on a position each step).
+tgx_status patch_step_launch(PatchStep* p, int times, int advance);
+tgx_status patch_step_wait(PatchStep* p);
 
 }  // namespace tgx

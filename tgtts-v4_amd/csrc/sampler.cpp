@@ -303,7 +303,7 @@ hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, in
     ++n;
     // The condition's tokens: cond_proj of the patch before at COND_AT, mu at 0 (zero in the
     // unconditional sequence), the same in every step (dit.rs:206-211).
-    EmbedArgs cond{s->cond, s->cond_w, s->cond_b, mu, s->x0, C, F, COND_AT, 0, MU_TOKENS, 1, 0};
+    EmbedArgs cond{s->cond, s->cond_w, s->cond_b, mu, s->x0, C, F, COND_AT, 0, MU_TOKENS, 1, 0, 2};
     if (e == hipSuccess) e = launch_local_embed(a, cond, rows, st, timer), ++n;
     std::vector<LocalLayer> layers(s->shape.layers);
     for (int l = 0; l < s->shape.layers; ++l) {
@@ -315,7 +315,7 @@ hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, in
     const int x_at = COND_AT + F;
     for (size_t i = 0; i < s->step_t.size() && e == hipSuccess; ++i) {
         // in_proj of the patch so far at x_at, and the step's time token (dit.rs:213-219).
-        EmbedArgs step{s->state, s->in_w, s->in_b, s->time_tokens + i * s->shape.hidden, s->x0, C, F, x_at, TIME_AT, 1, 0, 1};
+        EmbedArgs step{s->state, s->in_w, s->in_b, s->time_tokens + i * s->shape.hidden, s->x0, C, F, x_at, TIME_AT, 1, 0, 1, 2};
         e = launch_local_embed(a, step, rows, st, timer);
         ++n;
         if (e == hipSuccess) e = launch_local_stack(a, layers.data(), s->shape.layers, s->final_norm, b, st, timer);
@@ -327,8 +327,6 @@ hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, in
     if (dispatches) *dispatches = n;
     return e;
 }
-
-namespace {
 
 tgx_status sampler_record(Sampler* s) {
     if (s->exec) {
@@ -367,8 +365,6 @@ tgx_status sampler_record(Sampler* s) {
     }
     return TGX_OK;
 }
-
-}  // namespace
 
 tgx_status sampler_set_inputs(Sampler* s, const float* mu, const float* cond, const float* noise, const float* sampling) {
     if (!s) return fail(TGX_E_ARG, "null sampler");

@@ -161,6 +161,17 @@ EXPORTS = [
     "tgx_lm_side_dispatches",
     "tgx_patch_launch",
     "tgx_patch_elapsed_ms",
+    "tgx_encoder_create",
+    "tgx_encoder_destroy",
+    "tgx_encoder_load",
+    "tgx_encoder_encode",
+    "tgx_encoder_dispatches",
+    "tgx_patch_step_create",
+    "tgx_patch_step_destroy",
+    "tgx_patch_step_run",
+    "tgx_patch_step_launch",
+    "tgx_patch_step_wait",
+    "tgx_patch_step_elapsed_ms",
 ]
 
 _lib: Optional[ctypes.CDLL] = None
@@ -248,6 +259,19 @@ def library() -> ctypes.CDLL:
     lib.tgx_lm_side_dispatches.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
     lib.tgx_patch_launch.argtypes = [P, P, ctypes.c_int]
     lib.tgx_patch_elapsed_ms.argtypes = [P, FP]
+    lib.tgx_encoder_create.argtypes = [P, ctypes.POINTER(_Shape), ctypes.POINTER(_PatchShape), ctypes.POINTER(P)]
+    lib.tgx_encoder_destroy.argtypes = [P]
+    lib.tgx_encoder_destroy.restype = None
+    lib.tgx_encoder_load.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int, ctypes.c_size_t]
+    lib.tgx_encoder_encode.argtypes = [P, P, P]
+    lib.tgx_encoder_dispatches.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_patch_step_create.argtypes = [P, P, P, ctypes.POINTER(P)]
+    lib.tgx_patch_step_destroy.argtypes = [P]
+    lib.tgx_patch_step_destroy.restype = None
+    lib.tgx_patch_step_run.argtypes = [P, ctypes.POINTER(_Row), ctypes.c_int, P, P, P, P, P]
+    lib.tgx_patch_step_launch.argtypes = [P, ctypes.c_int, ctypes.c_int]
+    lib.tgx_patch_step_wait.argtypes = [P]
+    lib.tgx_patch_step_elapsed_ms.argtypes = [P, FP]
     for name in EXPORTS:
         if name.startswith("tgx_") and name not in ("tgx_last_error",):
             fn = getattr(lib, name)
@@ -257,6 +281,8 @@ def library() -> ctypes.CDLL:
     lib.tgx_decoder_destroy.restype = None
     lib.tgx_sampler_destroy.restype = None
     lib.tgx_lm_side_destroy.restype = None
+    lib.tgx_encoder_destroy.restype = None
+    lib.tgx_patch_step_destroy.restype = None
     _lib = lib
     return lib
 

@@ -266,3 +266,101 @@ def patch_elapsed_ms(side: LmSide) -> float:
     v = ctypes.c_float()
     _check(library().tgx_patch_elapsed_ms(side._h, ctypes.byref(v)))
     return v.value
+
+
+class Encoder:
+    """local::encoder::Encoder (crates/graph/src/local/encoder.rs:164-198): each row's patch to
+    its embedding through the local encoder's stack, recorded as one HIP graph."""
+
+    def __init__(self, ctx: Context, stack: Shape, patch: PatchShape):
+        self.ctx = ctx
+        self.stack = stack
+        self.patch = patch
+        s, self._factors = _shape_struct(stack)
+        p = _PatchShape(patch.feat_dim, patch.patch_size, patch.timesteps, patch.rows)
+        self._h = ctypes.c_void_p()
+        _check(library().tgx_encoder_create(ctx._h, ctypes.byref(s), ctypes.byref(p), ctypes.byref(self._h)))
+        _open_decoders.add(self)
+
+    def load(self, name: str, values: np.ndarray) -> None:
+        a, dtype = _weights(values)
+        _check(library().tgx_encoder_load(self._h, name.encode(), _ptr(a), dtype, a.size))
+
+    def load_all(self, weights: dict) -> None:
+        for name, values in weights.items():
+            self.load(name, values)
+
+    def encode(self, patches) -> np.ndarray:
+        """Encoder::encode (encoder.rs:194-198): [rows][feat_dim][patch_size] -> [rows][hidden]."""
+        P = self.patch
+        patches = np.ascontiguousarray(patches, dtype=np.float32).reshape(P.rows, P.feat_dim, P.patch_size)
+        out = np.empty((P.rows, self.stack.hidden), dtype=np.float32)
+        _check(library().tgx_encoder_encode(self._h, _ptr(patches), _ptr(out)))
+        return out
+
+    def dispatches(self) -> int:
+        v = ctypes.c_int()
+        _check(library().tgx_encoder_dispatches(self._h, ctypes.byref(v)))
+        return v.value
+
+    def close(self) -> None:
+        if self._h:
+            library().tgx_encoder_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class PatchStep:
+    """patch::PatchStep (crates/graph/src/patch.rs:98-166, 356-415) over an encoder, an LM side and
+    a sampler made alike: each step embeds the patches before, steps the LM side on them and
+    samples on its mu, on the device throughout. The three must outlive it."""
+
+    def __init__(self, encoder: Encoder, side: "LmSide", sampler: Sampler):
+        self.encoder, self.side, self.sampler = encoder, side, sampler
+        self._h = ctypes.c_void_p()
+        _check(library().tgx_patch_step_create(encoder._h, side._h, sampler._h, ctypes.byref(self._h)))
+        _open_decoders.add(self)
+
+    def run_rows(self, rows: Sequence[Optional[Row]], cond, noise, sampling):
+        """PatchStep::run_rows (patch.rs:356-415): -> (patches [rows][feat_dim][patch_size],
+        stop logits [rows][2])."""
+        P = self.sampler.patch
+        cond = np.ascontiguousarray(cond, dtype=np.float32).reshape(P.rows, P.feat_dim, P.patch_size)
+        noise = np.ascontiguousarray(noise, dtype=np.float32).reshape(P.rows, P.feat_dim, P.patch_size)
+        sampling = np.ascontiguousarray(sampling, dtype=np.float32).reshape(P.rows, 2)
+        patch = np.empty_like(noise)
+        stop = np.empty((P.rows, 2), dtype=np.float32)
+        _check(library().tgx_patch_step_run(self._h, self.side._rows(rows), len(rows), _ptr(cond), _ptr(noise),
+                                            _ptr(sampling), _ptr(patch), _ptr(stop)))
+        return patch, stop
+
+    def launch(self, times: int = 1, advance: bool = True) -> None:
+        _check(library().tgx_patch_step_launch(self._h, times, 1 if advance else 0))
+
+    def wait(self) -> None:
+        _check(library().tgx_patch_step_wait(self._h))
+
+    def elapsed_ms(self) -> float:
+        v = ctypes.c_float()
+        _check(library().tgx_patch_step_elapsed_ms(self._h, ctypes.byref(v)))
+        return v.value
+
+    def close(self) -> None:
+        if self._h:
+            library().tgx_patch_step_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.close()
+        except Exception:
+            pass

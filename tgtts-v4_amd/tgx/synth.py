@@ -172,6 +172,17 @@ def sampler_weights(stack: StackSpec, feat_dim: int = 64) -> dict:
     return out
 
 
+def encoder_weights(stack: StackSpec, feat_dim: int = 64) -> dict:
+    """The local encoder's tensors by the names Encoder.load takes: the stack's, the learned token
+    ("special_token" [hidden], N(0, 1)) and in_proj ([hidden][feat_dim])."""
+    out = dict(stack_weights(stack))
+    h, s = stack.hidden, stack.seed
+    out.update(linear_layer(s, "in_proj", h, feat_dim, dtype=stack.dtype))
+    special = normal(s, "special_token", h, np.float32).astype(np.float32)
+    out["special_token"] = bf16_round(special) if stack.dtype == "bf16" else special
+    return out
+
+
 HEADS = (
     # name, out, in (as multiples of: h hidden, e encoder, d dit, l latent), bias
     ("enc_to_lm_proj", "h", "e", True),
