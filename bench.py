@@ -246,13 +246,14 @@ def run_prefill(ctx, weights, count: int, length: int, times: int, decode_steps:
 
 
 def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
-    """The full per-patch pipeline at `rows` requests: the LM side (the 24-layer backbone and the
-    8-layer residual LM without RoPE, with the heads between them) and the sampler (a 4-layer
-    LocDiT, 10 Euler steps with CFG-Zero* guidance 2.0 over both sequences of every row) on its
-    mu, `steps` patch steps, each request's caches filled to `context` positions first."""
+    """The full per-patch pipeline at `rows` requests, on the device throughout: the local encoder
+    (a 4-layer stack over the patch before), the LM side (the 24-layer backbone and the 8-layer
+    residual LM without RoPE, with the heads between them) and the sampler (a 4-layer LocDiT, 10
+    Euler steps with CFG-Zero* guidance 2.0 over both sequences of every row) on its mu, `steps`
+    patch steps, each request's caches filled to `context` positions first."""
     import tgx
-    from tgx.patch import HeadsShape, LmSide, PatchShape, Sampler, patch_elapsed_ms, patch_launch
-    from tgx.synth import StackSpec, embeddings, lm_side_weights, sampler_weights
+    from tgx.patch import Encoder, HeadsShape, LmSide, PatchShape, PatchStep, Sampler
+    from tgx.synth import StackSpec, embeddings, encoder_weights, lm_side_weights, sampler_weights
 
     # Positions run on through the warm-up, the timed steps and the LM side's steps alone.
     reach = context + warmup + 2 * steps + 2
@@ -260,11 +261,15 @@ def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
     base = tgx.Shape(layers=24, capacity=capacity)
     residual = tgx.Shape(layers=8, capacity=capacity, rope=False)
     heads = HeadsShape(1024, 1024, 256, 9)
+    patch = PatchShape(64, 4, 10, rows)
     side = LmSide(ctx, base, residual, tgx.Batch(rows=rows, slots=rows), heads)
     side.load_all(lm_side_weights(StackSpec(layers=24, seed=0), StackSpec(layers=8, seed=1), 1024, 1024, 256))
     dit = StackSpec(layers=4, seed=2)
-    sampler = Sampler(ctx, tgx.Shape(layers=4, capacity=16), PatchShape(64, 4, 10, rows))
+    sampler = Sampler(ctx, tgx.Shape(layers=4, capacity=16), patch)
     sampler.load_all(sampler_weights(dit, 64))
+    local = StackSpec(layers=4, seed=3)
+    encoder = Encoder(ctx, tgx.Shape(layers=4, capacity=16), patch)
+    encoder.load_all(encoder_weights(local, 64))
     for which in (0, 1):
         d = side.decoder(which)
         d.prefill_runs([(r, 0, context) for r in range(rows)], embeddings(12 + which, "tts.prompt", rows * context, 1024))
@@ -277,30 +282,34 @@ def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
     mu = np.zeros((rows, 2, 1024), dtype=np.float32)
     sampler.sample(mu, cond, noise, sampling)  # inputs in place, the graph recorded
     side.set_rows([tgx.Row(context, r) for r in range(rows)], embeddings(14, "tts.enc", rows, 1024))
-    patch_launch(side, sampler, warmup)
-    side.wait()
+    step = PatchStep(encoder, side, sampler)
+    step.launch(warmup)
+    step.wait()
     t0 = time.perf_counter()
-    patch_launch(side, sampler, steps)
-    side.wait()
+    step.launch(steps)
+    step.wait()
     wall = time.perf_counter() - t0
-    gpu = patch_elapsed_ms(side)
-    # The two halves alone, for the split.
+    gpu = step.elapsed_ms()
+    # The parts alone, for the split.
     side.launch(steps, advance=True)
     side.wait()
     side_ms = side.elapsed_ms() / steps
     sampler.launch(steps)
     sampler.wait()
     sampler_ms = sampler.elapsed_ms() / steps
-    dispatches = side.dispatches() + sampler.dispatches()
-    side.close()
-    sampler.close()
+    dispatches = encoder.dispatches() + side.dispatches() + sampler.dispatches()
+    step.close()
+    for o in (side, sampler, encoder):
+        o.close()
     # Algorithmic bytes: every weight once a step (the DiT's once per Euler evaluation).
-    dit_bytes = dit.layers * (tgx.Shape(layers=1).weight_bytes() - 2 * 1024) + 2 * 1024
+    layer = tgx.Shape(layers=1).weight_bytes() - 2 * 1024
+    dit_bytes = dit.layers * layer + 2 * 1024
+    enc_bytes = local.layers * layer + 2 * 1024 + 2 * 1024 * 64
     lm_bytes = base.weight_bytes() + residual.weight_bytes()
     return {
-        "workload": f"{rows} requests: 24-layer backbone + 8-layer residual LM (no RoPE) + heads, then a 4-layer "
-                    f"LocDiT over 4 x 64 latents, 10 Euler steps (9 DiT evaluations) with CFG-Zero* 2.0; contexts "
-                    f"from {context}",
+        "workload": f"{rows} requests: 4-layer local encoder over the patch before, 24-layer backbone + 8-layer "
+                    f"residual LM (no RoPE) + heads, then a 4-layer LocDiT over 4 x 64 latents, 10 Euler steps "
+                    f"(9 DiT evaluations) with CFG-Zero* 2.0; contexts from {context}",
         "rows": rows,
         "steps": steps,
         "steps_per_s": steps / wall,
@@ -308,8 +317,9 @@ def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
         "gpu_ms_per_step": gpu / steps,
         "lm_side_ms": side_ms,
         "sampler_ms": sampler_ms,
+        "encoder_and_copies_ms": gpu / steps - side_ms - sampler_ms,
         "dispatches_per_step": dispatches + 1,
-        "weight_bytes_per_step": lm_bytes + 9 * dit_bytes,
+        "weight_bytes_per_step": lm_bytes + 9 * dit_bytes + enc_bytes,
     }
 
 
@@ -461,7 +471,8 @@ def main() -> int:
     if not args.no_tts:
         tts = run_tts(ctx, 16, 30, 3)
         log(f"tts step at 16 requests: {tts['steps_per_s']:.1f} patch steps/s ({tts['ms_per_step']:.2f} ms; LM side "
-            f"{tts['lm_side_ms']:.2f} ms, sampler {tts['sampler_ms']:.2f} ms)")
+            f"{tts['lm_side_ms']:.2f} ms, sampler {tts['sampler_ms']:.2f} ms, encoder and copies "
+            f"{tts['encoder_and_copies_ms']:.2f} ms)")
         tts = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in tts.items()}
 
     # The roofline of the step's dominant kernel for HBM: the one whose launches move the most
