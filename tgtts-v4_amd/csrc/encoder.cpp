@@ -95,7 +95,7 @@ tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     if (patch->rows < 1) return shape_fail("no rows");
     if (F < 1 || F > 4) return shape_fail(std::to_string(F) + " frames to a patch (1 to 4)");
     if (C < 16 || C % 16 || C > 64) return shape_fail(std::to_string(C) + " channels (16, 32, 48 or 64)");
-    if (T * H > 256 || T > LOCAL_MAX_T) return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads");
+    if (T > LOCAL_MAX_T || H % 4) return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads");
     if (s.inner % 256) return shape_fail("an FFN " + std::to_string(s.inner) + " wide");
     hipError_t pe = local_prepare();
     if (pe != hipSuccess) return fail(TGX_E_HIP, std::string("the local stack's LDS: ") + hipGetErrorString(pe));

@@ -7,8 +7,8 @@
 //                   global-to-LDS loads, with the epilogue fused: RoPE at each token's place in
 //                   its sequence (local_qkv_rope.comp), SiLU(gate) up (local_gate_up.comp), or
 //                   the f32 sums of one part of the columns (local_partial.comp)
-//   local_attention every token of a sequence attends to every token of it, a workgroup to a
-//                   sequence (local_attention.comp)
+//   local_attention every token of a sequence attends to every token of it, a wave to a
+//                   sequence and query head, both products on MFMA (local_attention.comp)
 //   local_add_norm  residual + the parts' sums in their order, then RMSNorm (local_add_norm.comp,
 //                   local_norm.comp)
 //   local_embed     a linear layer over a patch's frames into tokens, and tokens copied beside
@@ -211,74 +211,68 @@ __global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm 
 }
 
 // ---------------------------------------------------------------------------------------------
-// local_attention: a workgroup to a sequence; thread i < T heads takes query head i % heads of
-// token i / heads, against the sequence's keys and values staged in LDS in f32. Scores in f32,
-// max-subtracted exponentials summed in key order, the weighted values divided by the sum.
+// local_attention: a wave to a (sequence, query head), 4 heads of one sequence to a workgroup.
+// S^T = K Q^T by two MFMAs (keys as rows, the sequence's T <= 16 queries as columns, d in two
+// halves of 32): lane l then holds query l % 16 against keys 4 (l / 16) .. + 3. The softmax over
+// a query's keys is in-lane and across lanes l ^ 16, l ^ 32; P is rounded to bf16 and summed as
+// rounded, and O^T = V^T P takes P straight from those registers as its B operand (k slots 0..3 =
+// keys 4 (l / 16) + i, slots 4..7 zero), V^T gathered per lane as 4 keys of one dimension.
+// Rows past T are read at the sequence's first token (in bounds) and masked or never written.
 __global__ void __launch_bounds__(256) local_attention(LocalArgs a, const uint16_t* __restrict__ q,
                                                        const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                        uint16_t* __restrict__ attended) {
-    __shared__ float ks[LOCAL_MAX_T * 2 * HEAD_DIM * 2];  // [T][kv_heads][64], kv_heads <= 4 at T 16
-    __shared__ float vs[LOCAL_MAX_T * 2 * HEAD_DIM * 2];
     const int seq = blockIdx.x, T = a.T, H = a.heads, KV = a.kv_heads;
-    const int first = seq * T;
-    const int n = T * KV * HEAD_DIM;
-    for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
-        const uint32_t kw = reinterpret_cast<const uint32_t*>(k + (size_t)first * KV * HEAD_DIM)[i];
-        const uint32_t vw = reinterpret_cast<const uint32_t*>(v + (size_t)first * KV * HEAD_DIM)[i];
-        ks[2 * i] = bf16_lo(kw);
-        ks[2 * i + 1] = bf16_hi(kw);
-        vs[2 * i] = bf16_lo(vw);
-        vs[2 * i + 1] = bf16_hi(vw);
+    const int lane = threadIdx.x % WAVE, head = blockIdx.y * 4 + threadIdx.x / WAVE;
+    const int kv = head / (H / KV), first = seq * T;
+    const int r = lane % 16, g = lane / 16;
+    const int row = first + (r < T ? r : 0);  // key row r, query column r
+    const uint4* krow = reinterpret_cast<const uint4*>(k + ((size_t)row * KV + kv) * HEAD_DIM);
+    const uint4* qrow = reinterpret_cast<const uint4*>(q + ((size_t)row * H + head) * HEAD_DIM);
+    const uint4 ka = krow[g], kb = krow[4 + g], qa = qrow[g], qb = qrow[4 + g];
+    // V^T rows: dimension 16 dt + r of keys 4 g + i.
+    uint32_t vw[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+        const int k0 = 4 * g + i < T ? first + 4 * g + i : first, k1 = 4 * g + i + 1 < T ? first + 4 * g + i + 1 : first;
+        const uint16_t* v0 = v + ((size_t)k0 * KV + kv) * HEAD_DIM + r;
+        const uint16_t* v1 = v + ((size_t)k1 * KV + kv) * HEAD_DIM + r;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) vw[dt][i / 2] = (uint32_t)v0[16 * dt] | ((uint32_t)v1[16 * dt] << 16);
     }
-    __syncthreads();
-    const int item = threadIdx.x;
-    if (item >= T * H) return;
-    const int t = item / H, head = item % H, kv = head / (H / KV);
-    const int m = first + t;
-    float qv[HEAD_DIM];
-    const uint4* qrow = reinterpret_cast<const uint4*>(q + ((size_t)m * H + head) * HEAD_DIM);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    s = mfma16(ka, qa, s);
+    s = mfma16(kb, qb, s);
+    const float scale_log2 = log2_scale(a.scale);
+    float mx = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < HEAD_DIM / 8; ++c) {
-        const uint4 w4 = qrow[c];
-        const uint32_t ws4[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            qv[8 * c + 2 * j] = bf16_lo(ws4[j]);
-            qv[8 * c + 2 * j + 1] = bf16_hi(ws4[j]);
-        }
+    for (int i = 0; i < 4; ++i) {
+        if (4 * g + i >= T) s[i] = -INFINITY;
+        mx = fmaxf(mx, s[i]);
     }
-    float scores[LOCAL_MAX_T];
-    float top = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < LOCAL_MAX_T; ++j) {
-        if (j >= T) break;
-        const float* kr = ks + (j * KV + kv) * HEAD_DIM;
-        float s = 0.f;
-#pragma unroll
-        for (int d = 0; d < HEAD_DIM; ++d) s += qv[d] * kr[d];
-        scores[j] = s * a.scale;
-        top = fmaxf(top, scores[j]);
-    }
+    mx = fmaxf(mx, lane_xor16(mx));
+    mx = fmaxf(mx, lane_xor32(mx));
+    const float top = mx * scale_log2;
+    uint32_t pw[2];
     float total = 0.f;
 #pragma unroll
-    for (int j = 0; j < LOCAL_MAX_T; ++j) {
-        if (j >= T) break;
-        scores[j] = __expf(scores[j] - top);
-        total += scores[j];
+    for (int i = 0; i < 4; i += 2) {
+        pw[i / 2] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[i], scale_log2, -top)),
+                                __builtin_amdgcn_exp2f(fmaf(s[i + 1], scale_log2, -top)));
+        total += bf16_lo(pw[i / 2]) + bf16_hi(pw[i / 2]);
     }
+    total += lane_xor16(total);
+    total += lane_xor32(total);
     const float inv = 1.0f / total;
-    uint4* orow = reinterpret_cast<uint4*>(attended + (size_t)m * H * HEAD_DIM + head * HEAD_DIM);
+    const uint4 pf = make_uint4(pw[0], pw[1], 0u, 0u);
+    f32x4 o[4];
 #pragma unroll
-    for (int c = 0; c < HEAD_DIM / 8; ++c) {
-        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < T; ++j) {
-            const float* vr = vs + (j * KV + kv) * HEAD_DIM + 8 * c;
+    for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16(make_uint4(vw[dt][0], vw[dt][1], 0u, 0u), pf, f32x4{0.f, 0.f, 0.f, 0.f});
+    if (r >= T) return;
+    uint16_t* out = attended + ((size_t)(first + r) * H + head) * HEAD_DIM;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] += scores[j] * vr[e];
-        }
-        orow[c] = make_uint4(pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv),
-                             pack_bf16x2(o[4] * inv, o[5] * inv), pack_bf16x2(o[6] * inv, o[7] * inv));
-    }
+    for (int dt = 0; dt < 4; ++dt)
+        *reinterpret_cast<uint2*>(out + 16 * dt + 4 * g) =
+            make_uint2(pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv), pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -503,7 +497,7 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
         const float* input = l == 0 ? b.x0 : b.x;
         LocalGemm qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, b.q, b.k, b.v};
         dispatch("local_qkv_rope", local_gemm<LEPI_QKV>, dim3(qkv_rows / LOCAL_ROW_TILE, mblocks), block, LG_LDS, stream, timer, a, qkv);
-        dispatch("local_attention", local_attention, dim3(a.M / a.T), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
+        dispatch("local_attention", local_attention, dim3(a.M / a.T, H / 4), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
                  (const uint16_t*)b.k, (const uint16_t*)b.v, b.attended);
         LocalGemm o{L.o, b.attended, H * HEAD_DIM, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
         dispatch("local_o_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.o_parts), block, LG_LDS, stream,

@@ -24,7 +24,7 @@ struct LocalArgs {
 
 constexpr int LOCAL_TOKEN_TILE = 128;  // the GEMM's tokens per workgroup
 constexpr int LOCAL_ROW_TILE = 64;     // the GEMM's weight rows per workgroup
-constexpr int LOCAL_MAX_T = 16;        // the longest sequence local_attention stages
+constexpr int LOCAL_MAX_T = 16;        // the longest sequence: local_attention takes one as an MFMA tile
 constexpr int LOCAL_MAX_PARTS = 4;
 
 struct LocalLayer {

@@ -130,7 +130,8 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     if (C < 16 || C % 16 || C > 64)
         return shape_fail(std::to_string(C) + " channels of " + std::to_string(F) + " frames (16, 32, 48 or 64)");
     if (s.hidden != 1024) return shape_fail("a stack " + std::to_string(s.hidden) + " wide (the kernels take 1024)");
-    if (T * H > 256 || T * KV * HEAD_DIM > LOCAL_MAX_T * 2 * HEAD_DIM * 2 || T > LOCAL_MAX_T)
+    // local_attention: a sequence's tokens as one MFMA tile, its query heads 4 to a workgroup.
+    if (T > LOCAL_MAX_T || H % 4)
         return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads over " + std::to_string(KV));
     if (s.inner % 256) return shape_fail("an FFN " + std::to_string(s.inner) + " wide");
     hipError_t pe = local_prepare();
