@@ -96,16 +96,18 @@ def test_a_row_samples_the_same_patch_beside_others_as_alone(ctx):
 
     spec = _dit_spec()
     w = sampler_weights(spec, FEAT)
-    mu, cond, noise, sampling = _inputs(5, seed=9)
-    many = _sampler(ctx, 5, spec, w)
-    got = many.sample(mu, cond, noise, sampling)
-    again = many.sample(mu, cond, noise, sampling)
-    assert np.array_equal(got, again)
-    many.close()
+    mu, cond, noise, sampling = _inputs(16, seed=9)
     one = _sampler(ctx, 1, spec, w)
-    for r in (0, 3):
-        alone = one.sample(mu[r : r + 1], cond[r : r + 1], noise[r : r + 1], sampling[r : r + 1])
-        assert np.array_equal(alone[0], got[r]), r
+    # 1 row takes the direct GEMMs, 5 and 16 rows the shared ones with 1 to 4 waves a workgroup.
+    for rows, picks in ((5, (0, 3)), (16, (0, 9, 15))):
+        many = _sampler(ctx, rows, spec, w)
+        got = many.sample(mu[:rows], cond[:rows], noise[:rows], sampling[:rows])
+        again = many.sample(mu[:rows], cond[:rows], noise[:rows], sampling[:rows])
+        assert np.array_equal(got, again)
+        many.close()
+        for r in picks:
+            alone = one.sample(mu[r : r + 1], cond[r : r + 1], noise[r : r + 1], sampling[r : r + 1])
+            assert np.array_equal(alone[0], got[r]), (rows, r)
     one.close()
 
 

@@ -92,6 +92,17 @@ __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// wait_vm<N> as the compiler's own s_waitcnt, which its count of loads in flight takes in: after it
+// the compiler knows the direct-to-LDS loads issued before the last N loads have landed, and
+// waits for the later ones no more than their uses need (behind an asm wait it would wait for
+// every load in flight before the first use of any).
+template <int N>
+__device__ __forceinline__ void wait_vm_seen() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    // gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14; expcnt (6:4) and lgkmcnt (11:8) at
+    // their maxima, waiting for nothing.
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 __device__ __forceinline__ void load_to_lds(const void* src, void* lds) {
     __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)lds, 16, 0, 0);

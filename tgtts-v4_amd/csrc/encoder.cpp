@@ -96,7 +96,8 @@ tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     if (F < 1 || F > 4) return shape_fail(std::to_string(F) + " frames to a patch (1 to 4)");
     if (C < 16 || C % 16 || C > 64) return shape_fail(std::to_string(C) + " channels (16, 32, 48 or 64)");
     if (T > LOCAL_MAX_T || H % 4) return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads");
-    if (s.inner % 256) return shape_fail("an FFN " + std::to_string(s.inner) + " wide");
+    if (s.inner % 256 || !local_supported(s.hidden, s.inner, H, KV, LOCAL_O_PARTS, LOCAL_DOWN_PARTS))
+        return shape_fail("a local stack " + std::to_string(s.hidden) + " wide with an FFN " + std::to_string(s.inner) + " wide");
     hipError_t pe = local_prepare();
     if (pe != hipSuccess) return fail(TGX_E_HIP, std::string("the local stack's LDS: ") + hipGetErrorString(pe));
     Encoder* e = new Encoder();
@@ -107,7 +108,7 @@ tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     e->rows = patch->rows;
     e->T = T;
     e->M = patch->rows * T;
-    e->M_pad = (e->M + LOCAL_TOKEN_TILE - 1) / LOCAL_TOKEN_TILE * LOCAL_TOKEN_TILE;
+    e->M_pad = local_rows_padded(e->M);
     auto done = [&](tgx_status r) {
         if (r != TGX_OK) encoder_destroy(e);
         return r;

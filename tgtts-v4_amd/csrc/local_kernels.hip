@@ -2,11 +2,13 @@
 // local_{norm,qkv_rope,attention,partial,add_norm,gate_up}.comp; crates/graph/src/local/dit.rs
 // with local_embed.comp, dit_euler.comp and cfm_noise.comp):
 //
-//   local_gemm      C = X W^T over a few hundred tokens, bf16 in, f32 accumulate, a 64-row by
-//                   128-token tile to a workgroup of four waves, staged through LDS by direct
-//                   global-to-LDS loads, with the epilogue fused: RoPE at each token's place in
-//                   its sequence (local_qkv_rope.comp), SiLU(gate) up (local_gate_up.comp), or
-//                   the f32 sums of one part of the columns (local_partial.comp)
+//   local_gemm      C = X W^T over up to a few hundred tokens, bf16 in, f32 accumulate: up to 64
+//                   tokens straight from memory into each wave's registers beside its strips of
+//                   W; more in 64-token tiles held in LDS, read by the waves of a workgroup that
+//                   each stream their own strips of W. The epilogue fused: RoPE at each token's
+//                   place in its sequence (local_qkv_rope.comp), SiLU(gate) up
+//                   (local_gate_up.comp), or the f32 sums of one part of the columns
+//                   (local_partial.comp)
 //   local_attention every token of a sequence attends to every token of it, a wave to a
 //                   sequence and query head, both products on MFMA (local_attention.comp)
 //   local_add_norm  residual + the parts' sums in their order, then RMSNorm (local_add_norm.comp,
@@ -29,14 +31,6 @@ namespace tgx {
 
 namespace {
 
-constexpr int LG_THREADS = 256;
-constexpr int LG_TKB = 2;                             // k-blocks of 32 to a stage
-constexpr int LG_W_STAGE = 4 * LG_TKB * 64;            // uint4 per stage: 4 strips, 8 KiB
-constexpr int LG_X_STAGE = 8 * LG_TKB * 64;            // 8 token tiles, 16 KiB
-constexpr int LG_FRAGS = (LG_W_STAGE + LG_X_STAGE) / 64 / 4;  // 1 KiB fragments a wave loads a stage
-constexpr int LG_NBUF = 4;  // stages in the LDS ring: three in flight while one is multiplied
-constexpr size_t LG_LDS = (size_t)LG_NBUF * (LG_W_STAGE + LG_X_STAGE) * sizeof(uint4);  // 96 KiB
-
 enum LocalEpilogue { LEPI_QKV = 0, LEPI_PARTIAL = 1, LEPI_SILU = 2 };
 
 struct LocalGemm {
@@ -48,166 +42,257 @@ struct LocalGemm {
     uint16_t *q, *k, *v;
 };
 
-// Strip s (0, 1) of wave row wn of n-block nb: two strips of W in a row, or for the gate/up
-// projection a strip of the gate and the same rows of up.
-template <int EPI>
-__device__ __forceinline__ int local_strip(int nb, int wn, int s, int N) {
+// A wave's strips of W for work unit u: SW strips in a row, or for the gate/up projection (SW 2)
+// gate strip u and the same rows of up, N / 32 strips on.
+template <int EPI, int SW>
+__device__ __forceinline__ void local_strips(int u, int N, int (&strip)[SW]) {
+    static_assert(EPI != LEPI_SILU || SW == 2, "gate/up takes a gate strip and its up strip");
     if (EPI == LEPI_SILU) {
-        const int gate = nb * 2 + wn;
-        return s == 0 ? gate : gate + N / 32;
+        strip[0] = u;
+        strip[SW - 1] = u + N / 32;
+    } else {
+#pragma unroll
+        for (int s = 0; s < SW; ++s) strip[s] = u * SW + s;
     }
-    return nb * 4 + wn * 2 + s;
 }
 
-// Grid (n-blocks, token blocks, parts): part z sums k-blocks z K/32/parts .. of every row.
+// The epilogue of one 16 x 16 block: W rows 16 strip + 4 (lane / 16) + i against token
+// mt + lane % 16. SILU takes the gate's block in `acc` and the up's in `up`.
 template <int EPI>
-__global__ void __launch_bounds__(LG_THREADS) local_gemm(LocalArgs a, LocalGemm g) {
-    extern __shared__ uint4 lds[];
-    uint4* ws = lds;                         // [LG_NBUF][LG_W_STAGE]
-    uint4* xs = lds + LG_NBUF * LG_W_STAGE;  // [LG_NBUF][LG_X_STAGE]
-    const int nb = blockIdx.x, m0 = blockIdx.y * LOCAL_TOKEN_TILE, part = blockIdx.z;
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int wn = w / 2, wm = w % 2;
-    const int kblocks = g.K / 32;
-    const int part_kb = kblocks / gridDim.z;
-    const int kb0 = part * part_kb;
-    const int stages = part_kb / LG_TKB;
-
-    // Fragments 0..7 of a stage are W's (strip f / 2, k-block f % 2), 8..23 the tokens' (tile
-    // (f - 8) / 2): lane l of a load writes bytes 16 l .. of the fragment, the MFMA operand order.
-    // Each wave issues exactly LG_FRAGS loads a stage (the branch is uniform across the wave), so
-    // its count of loads in flight says which stages have landed.
-    auto fetch = [&](int st) {
-        const int buf = st % LG_NBUF;
-#pragma unroll
-        for (int j = 0; j < LG_FRAGS; ++j) {
-            const int f = w * LG_FRAGS + j;
-            const int kb = kb0 + st * LG_TKB + f % 2;
-            if (f < 8) {
-                const int sl = f / 2;
-                const uint16_t* src = g.w + weight_tile_index(local_strip<EPI>(nb, sl / 2, sl % 2, g.N), kb, kblocks, 16) + lane * 8;
-                load_to_lds(src, &ws[buf * LG_W_STAGE + f * 64]);
-            } else {
-                const int mt = (f - 8) / 2;
-                const uint16_t* src = g.x + (size_t)(m0 + mt * 16 + lane % 16) * g.K + kb * 32 + (lane / 16) * 8;
-                load_to_lds(src, &xs[buf * LG_X_STAGE + (f - 8) * 64]);
-            }
-        }
-    };
-
-    f32x4 acc[2][4];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll
-    for (int p = 0; p < LG_NBUF - 1; ++p)
-        if (p < stages) fetch(p);
-    for (int st = 0; st < stages; ++st) {
-        // Stage st has landed once no more than the later stages' loads are in flight; the barrier
-        // makes it so for every wave, and says every wave is done with stage st - 1, whose buffer
-        // the next fetch takes.
-        const int ahead = min(LG_NBUF - 2, stages - 1 - st);
-        if (ahead >= 2)
-            wait_vm<2 * LG_FRAGS>();
-        else if (ahead == 1)
-            wait_vm<LG_FRAGS>();
-        else
-            wait_vm<0>();
-        stage_barrier();
-        if (st + LG_NBUF - 1 < stages) fetch(st + LG_NBUF - 1);
-        const int buf = st % LG_NBUF;
-        // fr[6 kbl + s]: W strip s; fr[6 kbl + 2 + t]: token tile t; of k-block kbl.
-        uint4 fr[LG_TKB * 6];
-#pragma unroll
-        for (int kbl = 0; kbl < LG_TKB; ++kbl) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s) fr[kbl * 6 + s] = lds_read16(&ws[buf * LG_W_STAGE + ((wn * 2 + s) * LG_TKB + kbl) * 64 + lane]);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) fr[kbl * 6 + 2 + t] = lds_read16(&xs[buf * LG_X_STAGE + ((wm * 4 + t) * LG_TKB + kbl) * 64 + lane]);
-        }
-        lds_landed(fr);
-#pragma unroll
-        for (int kbl = 0; kbl < LG_TKB; ++kbl)
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) acc[s][t] = mfma16(fr[kbl * 6 + s], fr[kbl * 6 + 2 + t], acc[s][t]);
-    }
-
-    // Tile (s, t) holds W rows 16 strip + 4 (lane / 16) + i against token m0 + 16 (4 wm + t) + lane % 16.
-    const int quad = lane / 16;
+__device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm& g, int strip, int mt, const f32x4& acc,
+                                            const f32x4& up) {
+    const int lane = threadIdx.x % WAVE, quad = lane / 16;
+    const int m = mt + lane % 16;
     if (EPI == LEPI_PARTIAL) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int n = local_strip<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int m = m0 + (wm * 4 + t) * 16 + lane % 16;
-                *reinterpret_cast<float4*>(g.partial + ((size_t)part * a.M_pad + m) * g.N + n) =
-                    make_float4(acc[s][t][0], acc[s][t][1], acc[s][t][2], acc[s][t][3]);
-            }
-        }
+        const int n = strip * 16 + quad * 4;
+        *reinterpret_cast<float4*>(g.partial + ((size_t)blockIdx.z * a.M_pad + m) * g.N + n) =
+            make_float4(acc[0], acc[1], acc[2], acc[3]);
     } else if (EPI == LEPI_SILU) {
-        const int inner = g.N / 2;
-        const int n = local_strip<EPI>(nb, wn, 0, g.N) * 16 + quad * 4;
+        if (m >= a.M) return;
+        const int inner = g.N / 2, n = strip * 16 + quad * 4;
+        float v[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int m = m0 + (wm * 4 + t) * 16 + lane % 16;
-            if (m >= a.M) continue;
-            float v[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float gate = acc[0][t][i], up = acc[1][t][i];
-                v[i] = gate / (1.0f + __expf(-gate)) * up;
-            }
-            *reinterpret_cast<uint2*>(g.mlp + (size_t)m * inner + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-        }
+        for (int i = 0; i < 4; ++i) v[i] = acc[i] / (1.0f + __expf(-acc[i])) * up[i];
+        *reinterpret_cast<uint2*>(g.mlp + (size_t)m * inner + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     } else {  // LEPI_QKV: a strip's rows pair as r, r + 8 (lanes l and l ^ 32)
         const int H = a.heads, KV = a.kv_heads;
         const bool second = quad >= 2;
+        const int head = strip / 4, qtr = strip % 4;
+        const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
+        const int d0 = p0 + (second ? HEAD_DIM / 2 : 0);
+        float own[4], other[4];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int strip = local_strip<EPI>(nb, wn, s, g.N);
-            const int head = strip / 4, qtr = strip % 4;
-            const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
-            const int d0 = p0 + (second ? HEAD_DIM / 2 : 0);
-            const bool rotate = head < H + KV && a.rope;
+        for (int i = 0; i < 4; ++i) {
+            own[i] = acc[i];
+            other[i] = lane_xor32(own[i]);
+        }
+        if (m >= a.M) return;
+        float v[4];
+        if (head < H + KV && a.rope) {
+            const int place = m % a.T;
+            const float4 co = *reinterpret_cast<const float4*>(a.cos + place * (HEAD_DIM / 2) + p0);
+            const float4 si = *reinterpret_cast<const float4*>(a.sin + place * (HEAD_DIM / 2) + p0);
+            const float c4[4] = {co.x, co.y, co.z, co.w}, s4[4] = {si.x, si.y, si.z, si.w};
+            // As upstream: x cos + rotate_half(x) sin (local_qkv_rope.comp:71-76).
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                float own[4], other[4];
+            for (int i = 0; i < 4; ++i) v[i] = second ? own[i] * c4[i] + other[i] * s4[i] : own[i] * c4[i] - other[i] * s4[i];
+        } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    own[i] = acc[s][t][i];
-                    other[i] = lane_xor32(own[i]);
-                }
-                const int m = m0 + (wm * 4 + t) * 16 + lane % 16;
-                if (m >= a.M) continue;
-                float v[4];
-                if (rotate) {
-                    const int place = m % a.T;
-                    const float4 co = *reinterpret_cast<const float4*>(a.cos + place * (HEAD_DIM / 2) + p0);
-                    const float4 si = *reinterpret_cast<const float4*>(a.sin + place * (HEAD_DIM / 2) + p0);
-                    const float c4[4] = {co.x, co.y, co.z, co.w}, s4[4] = {si.x, si.y, si.z, si.w};
-                    // As upstream: x cos + rotate_half(x) sin (local_qkv_rope.comp:71-76).
+            for (int i = 0; i < 4; ++i) v[i] = own[i];
+        }
+        const uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        if (head < H)
+            *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * HEAD_DIM + d0) = packed;
+        else if (head < H + KV)
+            *reinterpret_cast<uint2*>(g.k + ((size_t)m * KV + head - H) * HEAD_DIM + d0) = packed;
+        else
+            *reinterpret_cast<uint2*>(g.v + ((size_t)m * KV + head - H - KV) * HEAD_DIM + d0) = packed;
+    }
+}
+
+template <int EPI, int SW, int TT>
+__device__ __forceinline__ void local_epilogue(const LocalArgs& a, const LocalGemm& g, const int (&strip)[SW], int m0,
+                                               const f32x4 (&acc)[SW][TT]) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        v[i] = second ? own[i] * c4[i] + other[i] * s4[i] : own[i] * c4[i] - other[i] * s4[i];
-                } else {
+    for (int t = 0; t < TT; ++t) {
+        if (EPI == LEPI_SILU) {
+            local_store<EPI>(a, g, strip[0], m0 + 16 * t, acc[0][t], acc[SW - 1][t]);
+        } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) v[i] = own[i];
-                }
-                const uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-                if (head < H)
-                    *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * HEAD_DIM + d0) = packed;
-                else if (head < H + KV)
-                    *reinterpret_cast<uint2*>(g.k + ((size_t)m * KV + head - H) * HEAD_DIM + d0) = packed;
-                else
-                    *reinterpret_cast<uint2*>(g.v + ((size_t)m * KV + head - H - KV) * HEAD_DIM + d0) = packed;
-            }
+            for (int s = 0; s < SW; ++s) local_store<EPI>(a, g, strip[s], m0 + 16 * t, acc[s][t], acc[s][t]);
         }
     }
+}
+
+__device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// The scheduler may move nothing across this: every load above it is in flight before any value
+// is used (left to itself it sinks loads towards their use to save registers).
+__device__ __forceinline__ void all_issued() { __builtin_amdgcn_sched_barrier(0); }
+
+// In both GEMMs below each output is one MFMA chain over its part's KBP k-blocks in k-block order,
+// whatever tile it sits in, so that a token's sums are the same beside any other tokens. A wave
+// keeps at most LG_INFLIGHT loads in flight, within its 6-bit count of them.
+constexpr int LG_INFLIGHT = 48;
+
+// A wave's ring of W fragments: its SW strips, DEPTH k-blocks ahead of the one it multiplies. The
+// fragments are fetched in k-block order through one pointer a strip, moved on 1 KiB a fetch
+// behind an asm the compiler cannot see through, so that it keeps one address a strip instead of
+// one for every k-block of the unrolled loop.
+template <int SW, int KBP, int DEPTH>
+struct WeightRing {
+    uint4 wf[DEPTH][SW];
+    const uint16_t* next[SW];
+
+    __device__ void start(const LocalGemm& g, const int (&strip)[SW], int kb0, int lane) {
+#pragma unroll
+        for (int s = 0; s < SW; ++s) next[s] = g.w + weight_tile_index(strip[s], kb0, g.K / 32, 16) + lane * 8;
+    }
+    // k-blocks [from, to) into their slots; calls follow each other in k-block order from 0
+    __device__ void fetch(int from, int to) {
+#pragma unroll
+        for (int kb = from; kb < to; ++kb)
+#pragma unroll
+            for (int s = 0; s < SW; ++s) {
+                wf[kb % DEPTH][s] = load16(next[s]);
+                next[s] += 512;
+                asm volatile("" : "+v"(next[s]));
+            }
+    }
+};
+
+// local_gemm_direct, for at most 64 tokens (M_pad = 16 TT): a workgroup of TT waves to a work unit
+// (SW strips of W), wave t against token tile t, both operands straight from memory into
+// registers, DEPTH k-blocks ahead (the waves read the same W; all but the first find it in cache).
+// Grid (units, 1, parts).
+template <int EPI, int SW, int TT, int KBP>
+__global__ void __launch_bounds__(TT * WAVE) local_gemm_direct(LocalArgs a, LocalGemm g) {
+    constexpr int DEPTH = LG_INFLIGHT / (SW + 1) < KBP ? LG_INFLIGHT / (SW + 1) : KBP;
+    const int t = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int kb0 = blockIdx.z * KBP;
+    int strip[SW];
+    local_strips<EPI, SW>(blockIdx.x, g.N, strip);
+    WeightRing<SW, KBP, DEPTH> w;
+    w.start(g, strip, kb0, lane);
+    const uint16_t* xp = g.x + (size_t)(16 * t + lane % 16) * g.K + kb0 * 32 + (lane / 16) * 8;
+    uint4 xf[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {  // k-block by k-block, so that the first MFMA waits for the first loads only
+        w.fetch(d, d + 1);
+        xf[d] = load16(xp + d * 32);
+    }
+    all_issued();
+    f32x4 acc[SW][1];
+#pragma unroll
+    for (int s = 0; s < SW; ++s) acc[s][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KBP; ++kb) {
+        const int r = kb % DEPTH;
+#pragma unroll
+        for (int s = 0; s < SW; ++s) acc[s][0] = mfma16(w.wf[r][s], xf[r], acc[s][0]);
+        if (kb + DEPTH < KBP) {
+            w.fetch(kb + DEPTH, kb + DEPTH + 1);
+            xf[r] = load16(xp + (kb + DEPTH) * 32);
+        }
+        all_issued();  // each k-block's refill stays where it is, DEPTH k-blocks ahead of its use
+    }
+    local_epilogue<EPI, SW, 1>(a, g, strip, 16 * t, acc);
+}
+
+// local_gemm_shared, for more tokens (M_pad a multiple of 64): a workgroup of 4 waves to 64 tokens
+// (4 token tiles) and 4 work units. The token tile goes through LDS in phases of LG_PHASE_KB
+// k-blocks ([4][LG_PHASE_KB][64 lanes] fragments of 16 bytes, 64 KiB, so that two workgroups fit a
+// CU), each landing by direct global-to-LDS loads; each wave streams its own strips of W into
+// registers, DEPTH k-blocks ahead, and reads the tokens' fragments from LDS a k-block ahead.
+// Grid (units / 4, M_pad / 64, parts).
+constexpr int LG_PHASE_KB = 16;
+constexpr int LG_RING = 24;  // k-blocks of W a wave of one strip has in flight
+constexpr size_t LG_SHARED_LDS = (size_t)4 * LG_PHASE_KB * 64 * sizeof(uint4);
+
+template <int EPI, int SW, int KBP>
+__global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2))) local_gemm_shared(LocalArgs a, LocalGemm g) {
+    static_assert(KBP % LG_PHASE_KB == 0, "whole phases");
+    constexpr int XL = LG_PHASE_KB;  // tile loads a wave a phase: 4 LG_PHASE_KB over 4 waves
+    // W's k-blocks in flight: LG_RING fragments of one strip, 8 k-blocks of two (as many as leave
+    // the registers of two workgroups to a CU), and as many as fit beside a phase's tile loads
+    // within the wave's count of loads.
+    constexpr int RING = SW == 1 ? LG_RING : 8;
+    constexpr int ROOM = (63 - XL) / SW < RING ? (63 - XL) / SW : RING;
+    constexpr int DEPTH = ROOM < KBP ? ROOM : KBP;
+    extern __shared__ uint4 xs[];  // [4][LG_PHASE_KB][64]
+    const int wv = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int m0 = blockIdx.y * 64, kb0 = blockIdx.z * KBP;
+    int strip[SW];
+    local_strips<EPI, SW>(blockIdx.x * 4 + wv, g.N, strip);
+    WeightRing<SW, KBP, DEPTH> w;
+    w.start(g, strip, kb0, lane);
+    w.fetch(0, DEPTH);
+    f32x4 acc[SW][4];
+#pragma unroll
+    for (int s = 0; s < SW; ++s)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ph = 0; ph < KBP / LG_PHASE_KB; ++ph) {
+        if (ph > 0) stage_barrier();  // every wave is done with the last phase's tile
+#pragma unroll
+        for (int j = 0; j < XL; ++j) {
+            const int f = wv + 4 * j, t = f / LG_PHASE_KB, kb = ph * LG_PHASE_KB + f % LG_PHASE_KB;
+            load_to_lds(g.x + (size_t)(m0 + 16 * t + lane % 16) * g.K + (kb0 + kb) * 32 + (lane / 16) * 8, &xs[f * 64]);
+        }
+        all_issued();
+        // The tile's phase has landed once nothing is in flight: a wait the compiler sees, so that
+        // it knows as much and waits for W's refills no more than their uses need (behind an asm
+        // wait it would wait for every load before the first use of any). The barrier says the
+        // same of every wave's part. The tile is read through asm (lds_read16), whose waits the
+        // kernel keeps itself.
+        wait_vm_seen<0>();
+        stage_barrier();
+        uint4 xf[2][4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) xf[0][t] = lds_read16(&xs[(t * LG_PHASE_KB) * 64 + lane]);
+#pragma unroll
+        for (int k = 0; k < LG_PHASE_KB; ++k) {
+            const int kb = ph * LG_PHASE_KB + k, r = kb % DEPTH, b = k % 2;
+            lds_landed(xf[b]);
+            if (k + 1 < LG_PHASE_KB) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xf[1 - b][t] = lds_read16(&xs[(t * LG_PHASE_KB + k + 1) * 64 + lane]);
+            }
+#pragma unroll
+            for (int s = 0; s < SW; ++s)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[s][t] = mfma16(w.wf[r][s], xf[b][t], acc[s][t]);
+            if (kb + DEPTH < KBP) w.fetch(kb + DEPTH, kb + DEPTH + 1);
+            all_issued();  // each k-block's refill stays where it is, DEPTH k-blocks ahead of its use
+        }
+    }
+    local_epilogue<EPI, SW, 4>(a, g, strip, m0, acc);
+}
+
+// The GEMM of a projection: `units` work units of SW strips (gate/up: pairs of strips), each output
+// summed over the KBP k-blocks of its part. At most 64 tokens take the direct GEMM, more the
+// shared one.
+template <int EPI, int SW, int KBP>
+void local_gemm(const char* label, const LocalArgs& a, const LocalGemm& g, int units, int parts, hipStream_t stream,
+                DispatchTimer* timer) {
+    if (a.M_pad <= 64) {
+        const dim3 grid(units, 1, parts);
+        switch (a.M_pad / 16) {
+            case 1: dispatch(label, local_gemm_direct<EPI, SW, 1, KBP>, grid, dim3(WAVE), 0, stream, timer, a, g); break;
+            case 2: dispatch(label, local_gemm_direct<EPI, SW, 2, KBP>, grid, dim3(2 * WAVE), 0, stream, timer, a, g); break;
+            case 3: dispatch(label, local_gemm_direct<EPI, SW, 3, KBP>, grid, dim3(3 * WAVE), 0, stream, timer, a, g); break;
+            default: dispatch(label, local_gemm_direct<EPI, SW, 4, KBP>, grid, dim3(4 * WAVE), 0, stream, timer, a, g); break;
+        }
+        return;
+    }
+    const dim3 grid(units / 4, a.M_pad / 64, parts);
+    dispatch(label, local_gemm_shared<EPI, SW, KBP>, grid, dim3(4 * WAVE), LG_SHARED_LDS, stream, timer, a, g);
+}
+
+template <int EPI, int SW, int KBP>
+hipError_t local_gemm_lds() {
+    return hipFuncSetAttribute((const void*)local_gemm_shared<EPI, SW, KBP>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)LG_SHARED_LDS);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -484,11 +569,12 @@ __global__ void __launch_bounds__(256) cfm_noise(const float* __restrict__ noise
 
 hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int nlayers, const float* final_norm,
                               const LocalBuffers& b, hipStream_t stream, DispatchTimer* timer) {
-    const dim3 block(LG_THREADS);
-    const int mblocks = a.M_pad / LOCAL_TOKEN_TILE;
+    if (!local_supported(a.hidden, a.inner, a.heads, a.kv_heads, b.o_parts, b.down_parts) || a.M_pad != local_rows_padded(a.M))
+        return hipErrorInvalidValue;
     const dim3 rows4((a.M + 3) / 4);
     const int H = a.heads, KV = a.kv_heads;
     const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
+    const int o_kbp = H * HEAD_DIM / 32 / b.o_parts, down_kbp = a.inner / 32 / b.down_parts;
     // The first layer's input norm.
     dispatch("local_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0, b.x0,
              (float*)nullptr, layers[0].input_norm, b.normed, (float*)nullptr);
@@ -496,19 +582,23 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
         const LocalLayer& L = layers[l];
         const float* input = l == 0 ? b.x0 : b.x;
         LocalGemm qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, b.q, b.k, b.v};
-        dispatch("local_qkv_rope", local_gemm<LEPI_QKV>, dim3(qkv_rows / LOCAL_ROW_TILE, mblocks), block, LG_LDS, stream, timer, a, qkv);
+        local_gemm<LEPI_QKV, 1, 32>("local_qkv_rope", a, qkv, qkv_rows / 16, 1, stream, timer);
         dispatch("local_attention", local_attention, dim3(a.M / a.T, H / 4), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
                  (const uint16_t*)b.k, (const uint16_t*)b.v, b.attended);
         LocalGemm o{L.o, b.attended, H * HEAD_DIM, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
-        dispatch("local_o_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.o_parts), block, LG_LDS, stream,
-                 timer, a, o);
+        if (o_kbp == 16)
+            local_gemm<LEPI_PARTIAL, 1, 16>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
+        else
+            local_gemm<LEPI_PARTIAL, 1, 32>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
         dispatch("local_o_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial, b.o_parts,
                  input, b.h, L.post_norm, b.normed, (float*)nullptr);
         LocalGemm gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, b.mlp, nullptr, nullptr, nullptr};
-        dispatch("local_gate_up", local_gemm<LEPI_SILU>, dim3(a.inner / 32, mblocks), block, LG_LDS, stream, timer, a, gu);
+        local_gemm<LEPI_SILU, 2, 32>("local_gate_up", a, gu, a.inner / 16, 1, stream, timer);
         LocalGemm down{L.down, b.mlp, a.inner, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
-        dispatch("local_down_proj", local_gemm<LEPI_PARTIAL>, dim3(a.hidden / LOCAL_ROW_TILE, mblocks, b.down_parts), block, LG_LDS,
-                 stream, timer, a, down);
+        if (down_kbp == 16)
+            local_gemm<LEPI_PARTIAL, 1, 16>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
+        else
+            local_gemm<LEPI_PARTIAL, 1, 32>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
         if (l + 1 < nlayers)
             dispatch("local_down_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
                      b.down_parts, (const float*)b.h, b.x, layers[l + 1].input_norm, b.normed, (float*)nullptr);
@@ -519,12 +609,22 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
     return hipGetLastError();
 }
 
+bool local_supported(int hidden, int inner, int heads, int kv_heads, int o_parts, int down_parts) {
+    auto kbp_ok = [](int K, int parts) {
+        return parts >= 1 && parts <= LOCAL_MAX_PARTS && K % (32 * parts) == 0 && (K / 32 / parts == 16 || K / 32 / parts == 32);
+    };
+    return hidden == 1024 && heads % 4 == 0 && kv_heads >= 1 && inner % 64 == 0 && kbp_ok(heads * HEAD_DIM, o_parts) &&
+           kbp_ok(inner, down_parts);
+}
+
+int local_rows_padded(int M) { return M <= 64 ? (M + 15) / 16 * 16 : (M + 63) / 64 * 64; }
+
 hipError_t local_prepare() {
-    for (const void* k : {(const void*)local_gemm<LEPI_QKV>, (const void*)local_gemm<LEPI_PARTIAL>, (const void*)local_gemm<LEPI_SILU>}) {
-        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LG_LDS);
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
+    hipError_t e = local_gemm_lds<LEPI_QKV, 1, 32>();
+    if (e == hipSuccess) e = local_gemm_lds<LEPI_SILU, 2, 32>();
+    if (e == hipSuccess) e = local_gemm_lds<LEPI_PARTIAL, 1, 32>();
+    if (e == hipSuccess) e = local_gemm_lds<LEPI_PARTIAL, 1, 16>();
+    return e;
 }
 
 hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer) {

@@ -13,7 +13,7 @@ namespace tgx {
 // The tokens a local stack runs over: `seqs` sequences of T tokens, token m at place m % T.
 struct LocalArgs {
     int M;      // tokens
-    int M_pad;  // rows of the token tensors, a multiple of LOCAL_TOKEN_TILE; rows past M hold zeros
+    int M_pad;  // rows of the token tensors, local_rows_padded(M); rows past M hold zeros
     int T;      // tokens to a sequence
     int hidden, inner, heads, kv_heads;
     float eps, scale;
@@ -22,10 +22,10 @@ struct LocalArgs {
     const float* sin;
 };
 
-constexpr int LOCAL_TOKEN_TILE = 128;  // the GEMM's tokens per workgroup
-constexpr int LOCAL_ROW_TILE = 64;     // the GEMM's weight rows per workgroup
 constexpr int LOCAL_MAX_T = 16;        // the longest sequence: local_attention takes one as an MFMA tile
 constexpr int LOCAL_MAX_PARTS = 4;
+constexpr int LOCAL_O_PARTS = 2;     // o_proj's columns summed in 2 parts, down_proj's in 4, in part order
+constexpr int LOCAL_DOWN_PARTS = 4;
 
 struct LocalLayer {
     const uint16_t *qkv, *o, *gate_up, *down;  // 16-row MFMA tiles, q/k/v rows RoPE-paired
@@ -72,8 +72,13 @@ struct EulerArgs {
     float dt;
 };
 
-// Lets the projections take their LDS ring (96 KiB) per workgroup; once per process.
+// Lets the projections take their token tiles (64 KiB) in LDS; once per process.
 hipError_t local_prepare();
+// The stacks the kernels take: hidden 1024, query heads a multiple of 4, and o_proj's and
+// down_proj's parts 16 or 32 k-blocks of 32 columns each.
+bool local_supported(int hidden, int inner, int heads, int kv_heads, int o_parts, int down_parts);
+// The rows the token tensors of M tokens take: a multiple of 16 up to 64 tokens, else of 64.
+int local_rows_padded(int M);
 hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int nlayers, const float* final_norm,
                               const LocalBuffers& b, hipStream_t stream, DispatchTimer* timer);
 hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer);

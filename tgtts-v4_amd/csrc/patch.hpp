@@ -32,7 +32,7 @@ struct Sampler {
     Context* ctx = nullptr;
     Shape shape{};  // the DiT's stack; capacity = T
     int feat = 0, frames = 0, timesteps = 0, rows = 0;
-    int T = 0, M = 0, M_pad = 0, o_parts = 2, down_parts = 4;
+    int T = 0, M = 0, M_pad = 0, o_parts = LOCAL_O_PARTS, down_parts = LOCAL_DOWN_PARTS;
     std::vector<float> step_t, step_dt;
     std::vector<DeviceBuffer> allocations;
     size_t device_bytes = 0;
@@ -82,7 +82,7 @@ struct Encoder {
     Context* ctx = nullptr;
     Shape shape{};  // the stack; capacity = T
     int feat = 0, frames = 0, rows = 0;
-    int T = 0, M = 0, M_pad = 0, o_parts = 2, down_parts = 4;
+    int T = 0, M = 0, M_pad = 0, o_parts = LOCAL_O_PARTS, down_parts = LOCAL_DOWN_PARTS;
     std::vector<DeviceBuffer> allocations;
     size_t device_bytes = 0;
     std::vector<Layer> layers;

@@ -133,7 +133,8 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     // local_attention: a sequence's tokens as one MFMA tile, its query heads 4 to a workgroup.
     if (T > LOCAL_MAX_T || H % 4)
         return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads over " + std::to_string(KV));
-    if (s.inner % 256) return shape_fail("an FFN " + std::to_string(s.inner) + " wide");
+    if (s.inner % 256 || !local_supported(s.hidden, s.inner, H, KV, LOCAL_O_PARTS, LOCAL_DOWN_PARTS))
+        return shape_fail("a local stack " + std::to_string(s.hidden) + " wide with an FFN " + std::to_string(s.inner) + " wide");
     hipError_t pe = local_prepare();
     if (pe != hipSuccess) return fail(TGX_E_HIP, std::string("the local stack's LDS: ") + hipGetErrorString(pe));
     Sampler* smp = new Sampler();
@@ -145,7 +146,7 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     smp->rows = patch->rows;
     smp->T = T;
     smp->M = patch->rows * 2 * T;
-    smp->M_pad = (smp->M + LOCAL_TOKEN_TILE - 1) / LOCAL_TOKEN_TILE * LOCAL_TOKEN_TILE;
+    smp->M_pad = local_rows_padded(smp->M);
     euler_steps(patch->timesteps, smp->step_t, smp->step_dt);
     auto done = [&](tgx_status st) {
         if (st != TGX_OK) sampler_destroy(smp);
