@@ -358,6 +358,39 @@ tgx_status tgx_patch_step_launch(tgx_patch_step* p, int times, int advance);
 tgx_status tgx_patch_step_wait(tgx_patch_step* p);
 tgx_status tgx_patch_step_elapsed_ms(const tgx_patch_step* p, float* out);
 
+/* ---- weights from a safetensors checkpoint: crates/graph/src/checkpoint.rs ---- */
+
+typedef struct tgx_checkpoint tgx_checkpoint;
+
+/* Checkpoint::open (checkpoint.rs:36-71): parses the header (at most 100 MiB) and checks every
+ * entry (BF16, F16 or F32; bytes equal to its shape's) against the file; tensors are read from
+ * their offsets when asked for. TGX_E_WEIGHTS (graph::Error::Checkpoint) with the reason. */
+tgx_status tgx_checkpoint_open(const char* path, tgx_checkpoint** out);
+void tgx_checkpoint_close(tgx_checkpoint* ck);
+/* The tensors' names in order (the header is a BTreeMap, checkpoint.rs:31): count, then name i. */
+tgx_status tgx_checkpoint_count(const tgx_checkpoint* ck, int* out);
+tgx_status tgx_checkpoint_name(const tgx_checkpoint* ck, int index, char* out, size_t capacity);
+/* Checkpoint::shape (checkpoint.rs:74-76): the dims (up to `max`), their number and the dtype. */
+tgx_status tgx_checkpoint_shape(const tgx_checkpoint* ck, const char* name, int64_t* dims, int max, int* ndims,
+                                tgx_dtype* dtype);
+/* Checkpoint::f16 (checkpoint.rs:106-125), in f32: exact from BF16 and F16. `count` must be the
+ * tensor's. */
+tgx_status tgx_checkpoint_read(const tgx_checkpoint* ck, const char* name, float* out, size_t count);
+/* Checkpoint::gather_f16 (checkpoint.rs:127-139), in f32: rows `rows` of a 2-D tensor one after
+ * another (an embedding lookup reading those rows alone); a row past the tensor is refused. */
+tgx_status tgx_checkpoint_gather(const tgx_checkpoint* ck, const char* name, const int64_t* rows, int n, float* out);
+
+/* load_stack (decode.rs:738-776): the decoder's layers from `prefix` ("base_lm.", "residual_lm."
+ * or ""): q/k/v and gate/up joined along their rows, the norms, then norm.weight. */
+tgx_status tgx_decoder_load_checkpoint(tgx_decoder* dec, const tgx_checkpoint* ck, const char* prefix);
+/* load_lm_side (lm_side.rs:496-533): both stacks and the layers between them. */
+tgx_status tgx_lm_side_load_checkpoint(tgx_lm_side* s, const tgx_checkpoint* ck);
+/* load_sampler (local/dit.rs:329-365): feat_decoder.estimator.{decoder.*, in_proj, cond_proj,
+ * out_proj, time_mlp, delta_time_mlp}. */
+tgx_status tgx_sampler_load_checkpoint(tgx_sampler* s, const tgx_checkpoint* ck);
+/* load_encoder (local/encoder.rs:129-162): feat_encoder.{encoder.*, special_token, in_proj}. */
+tgx_status tgx_encoder_load_checkpoint(tgx_encoder* e, const tgx_checkpoint* ck);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,7 @@ SOURCES = {
     "encoder.cpp": HOST_FLAGS,
     "lm_side.cpp": HOST_FLAGS,
     "api_patch.cpp": HOST_FLAGS,
+    "checkpoint.cpp": HOST_FLAGS,
 }
 
 

@@ -218,6 +218,12 @@ tgx_status lm_side_load(LmSide* s, const char* name, const void* data, tgx_dtype
     return fail(TGX_E_WEIGHTS, n + ": no such tensor of the LM side");
 }
 
+std::vector<LmHead> lm_side_heads() {
+    std::vector<LmHead> out;
+    for (const Head& h : HEADS) out.push_back({h.name, h.bias});
+    return out;
+}
+
 tgx_status lm_side_set_rows(LmSide* s, const tgx_row* rows, int nrows, const float* enc) {
     if (!s || !rows) return fail(TGX_E_ARG, "null LM side or rows");
     if (s->pending) return fail(TGX_E_BUSY, "a step is under way");

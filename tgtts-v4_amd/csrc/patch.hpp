@@ -135,6 +135,12 @@ tgx_status lm_side_create(Context* ctx, const tgx_shape* base, const tgx_shape* 
                           const tgx_heads_shape* heads, LmSide** out);
 void lm_side_destroy(LmSide* s);
 tgx_status lm_side_load(LmSide* s, const char* name, const void* data, tgx_dtype dtype, size_t count);
+// The layers between the LMs by name (Heads::named, lm_side.rs:127-140), and whether each has a bias.
+struct LmHead {
+    const char* name;
+    bool bias;
+};
+std::vector<LmHead> lm_side_heads();
 tgx_status lm_side_set_rows(LmSide* s, const tgx_row* rows, int nrows, const float* enc);
 tgx_status lm_side_launch(LmSide* s, int times, int advance);
 tgx_status lm_side_wait(LmSide* s);

@@ -172,6 +172,17 @@ EXPORTS = [
     "tgx_patch_step_launch",
     "tgx_patch_step_wait",
     "tgx_patch_step_elapsed_ms",
+    "tgx_checkpoint_open",
+    "tgx_checkpoint_close",
+    "tgx_checkpoint_count",
+    "tgx_checkpoint_name",
+    "tgx_checkpoint_shape",
+    "tgx_checkpoint_read",
+    "tgx_checkpoint_gather",
+    "tgx_decoder_load_checkpoint",
+    "tgx_lm_side_load_checkpoint",
+    "tgx_sampler_load_checkpoint",
+    "tgx_encoder_load_checkpoint",
 ]
 
 _lib: Optional[ctypes.CDLL] = None
@@ -272,6 +283,19 @@ def library() -> ctypes.CDLL:
     lib.tgx_patch_step_launch.argtypes = [P, ctypes.c_int, ctypes.c_int]
     lib.tgx_patch_step_wait.argtypes = [P]
     lib.tgx_patch_step_elapsed_ms.argtypes = [P, FP]
+    lib.tgx_checkpoint_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(P)]
+    lib.tgx_checkpoint_close.argtypes = [P]
+    lib.tgx_checkpoint_close.restype = None
+    lib.tgx_checkpoint_count.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_checkpoint_name.argtypes = [P, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]
+    lib.tgx_checkpoint_shape.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_checkpoint_read.argtypes = [P, ctypes.c_char_p, P, ctypes.c_size_t]
+    lib.tgx_checkpoint_gather.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int, P]
+    lib.tgx_decoder_load_checkpoint.argtypes = [P, P, ctypes.c_char_p]
+    lib.tgx_lm_side_load_checkpoint.argtypes = [P, P]
+    lib.tgx_sampler_load_checkpoint.argtypes = [P, P]
+    lib.tgx_encoder_load_checkpoint.argtypes = [P, P]
     for name in EXPORTS:
         if name.startswith("tgx_") and name not in ("tgx_last_error",):
             fn = getattr(lib, name)
@@ -283,6 +307,7 @@ def library() -> ctypes.CDLL:
     lib.tgx_lm_side_destroy.restype = None
     lib.tgx_encoder_destroy.restype = None
     lib.tgx_patch_step_destroy.restype = None
+    lib.tgx_checkpoint_close.restype = None
     _lib = lib
     return lib
 
@@ -424,6 +449,11 @@ class Decoder:
         _open_decoders.add(self)
 
     # -- weights --
+    def load_checkpoint(self, checkpoint, prefix: str = "") -> None:
+        """load_stack (decode.rs:738-776) from a tgx.checkpoint.Checkpoint: the layers under
+        `prefix` ("base_lm.", "residual_lm." or ""), q/k/v and gate/up joined along their rows."""
+        _check(library().tgx_decoder_load_checkpoint(self._h, checkpoint._h, prefix.encode()))
+
     def load(self, name: str, values: np.ndarray) -> None:
         """load_stack's write of one tensor (decode.rs:740-776): f32, bf16 (uint16 bits) or f16."""
         a = np.ascontiguousarray(values)

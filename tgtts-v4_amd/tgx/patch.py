@@ -93,6 +93,10 @@ class Sampler:
         for name, values in weights.items():
             self.load(name, values)
 
+    def load_checkpoint(self, checkpoint) -> None:
+        """load_sampler (crates/graph/src/local/dit.rs:329-365): feat_decoder.estimator.* from a tgx.checkpoint.Checkpoint."""
+        _check(library().tgx_sampler_load_checkpoint(self._h, checkpoint._h))
+
     def _inputs(self, mu, cond, noise, sampling):
         P = self.patch
         mu = np.ascontiguousarray(mu, dtype=np.float32).reshape(P.rows, MU_TOKENS, self.stack.hidden)
@@ -186,6 +190,10 @@ class LmSide:
     def load_all(self, weights: dict) -> None:
         for name, values in weights.items():
             self.load(name, values)
+
+    def load_checkpoint(self, checkpoint) -> None:
+        """load_lm_side (crates/graph/src/lm_side.rs:496-533): base_lm.*, residual_lm.* and the heads from a tgx.checkpoint.Checkpoint."""
+        _check(library().tgx_lm_side_load_checkpoint(self._h, checkpoint._h))
 
     def decoder(self, which: int) -> Decoder:
         """The base LM's (0) or the residual LM's (1) decoder, owned by the LM side."""
@@ -289,6 +297,10 @@ class Encoder:
     def load_all(self, weights: dict) -> None:
         for name, values in weights.items():
             self.load(name, values)
+
+    def load_checkpoint(self, checkpoint) -> None:
+        """load_encoder (crates/graph/src/local/encoder.rs:129-162): feat_encoder.* from a tgx.checkpoint.Checkpoint."""
+        _check(library().tgx_encoder_load_checkpoint(self._h, checkpoint._h))
 
     def encode(self, patches) -> np.ndarray:
         """Encoder::encode (encoder.rs:194-198): [rows][feat_dim][patch_size] -> [rows][hidden]."""
