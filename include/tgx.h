@@ -391,6 +391,58 @@ tgx_status tgx_sampler_load_checkpoint(tgx_sampler* s, const tgx_checkpoint* ck)
 /* load_encoder (local/encoder.rs:129-162): feat_encoder.{encoder.*, special_token, in_proj}. */
 tgx_status tgx_encoder_load_checkpoint(tgx_encoder* e, const tgx_checkpoint* ck);
 
+/* ---- a prompt into the patch step's caches: crates/graph/src/prompt.rs ---- */
+
+typedef struct tgx_prompter tgx_prompter;
+typedef struct tgx_prompt_cache tgx_prompt_cache;
+
+/* prompt::Prompt (prompt.rs:322-332): each position's token (read where it is text), patch
+ * ([patch_size][feat_dim] f32, read where it is audio) and whether it is audio (0 or 1). */
+typedef struct {
+    const uint32_t* tokens;
+    const float* patches;
+    const uint8_t* audio;
+    int len;
+} tgx_prompt;
+
+/* Prompter::new (prompt.rs:527-552) over a patch step's encoder and LM side: runs of up to
+ * `max_rows` positions at a time. */
+tgx_status tgx_prompter_create(tgx_patch_step* step, int max_rows, tgx_prompter** out);
+void tgx_prompter_destroy(tgx_prompter* p);
+tgx_status tgx_prompter_max_rows(const tgx_prompter* p, int* out);
+/* Prompter::embed (prompt.rs:559-566): a patch [patch_size][feat_dim] -> [hidden] as the base LM
+ * takes it (the encoder, then enc_to_lm_proj). */
+tgx_status tgx_prompter_embed(tgx_prompter* p, const float* patch, float* out);
+/* Prompter::embeddings (prompt.rs:636-648): the prompt's positions but its last, [len - 1][hidden],
+ * and those of its audio positions (zero at text): a token's row of base_lm.embed_tokens.weight
+ * read from `ck`, a patch's embedding once for each distinct patch. */
+tgx_status tgx_prompter_embeddings(tgx_prompter* p, const tgx_checkpoint* ck, const tgx_prompt* prompt, float* x,
+                                   float* audio_x);
+/* Prompter::run_rows (prompt.rs:692-752): `len` positions from `at` through the base LM, the
+ * quantizer at the audio positions, fusion_concat_proj beside the audio embeddings and the
+ * residual LM, both LMs' keys and values into the slot's caches; max_rows at a time. */
+tgx_status tgx_prompter_run_rows(tgx_prompter* p, tgx_row at, const float* x, const float* audio_x, const uint8_t* audio,
+                                 int len);
+/* Prompter::run (prompt.rs:568-583): every position of a prompt that ends in audio but the last,
+ * from position 0 of `slot`; the first patch step after it runs the last as the patch before. */
+tgx_status tgx_prompter_run(tgx_prompter* p, uint32_t slot, const tgx_checkpoint* ck, const tgx_prompt* prompt);
+/* Prompter::run_cached (prompt.rs:585-641): as tgx_prompter_run in the voice whose latent frames
+ * are `voice`: from the positions it begins with that `cache` keeps of the voice (their keys and
+ * values copied back into the slot), with the patches' embeddings it keeps; keeps there what the
+ * next prompts in the voice can use. `ran`: the positions that ran through the LMs, the last
+ * among them. */
+tgx_status tgx_prompter_run_cached(tgx_prompter* p, uint32_t slot, const tgx_checkpoint* ck, const tgx_prompt* prompt,
+                                   const float* voice, size_t voice_len, tgx_prompt_cache* cache, int* ran);
+/* The last run's last piece: "base_out", "levels", "quantized", "lm_hidden", "residual_in" or
+ * "residual_out", [rows][width] f32 (the stage-by-stage view the tests compare). */
+tgx_status tgx_prompter_read(tgx_prompter* p, const char* tensor, float* out, size_t count);
+/* PromptCache::new (prompt.rs:414-424): keeps at most `budget` bytes, host and device together;
+ * the voices used longest ago make room for others. */
+tgx_status tgx_prompt_cache_create(tgx_context* ctx, size_t budget, tgx_prompt_cache** out);
+void tgx_prompt_cache_destroy(tgx_prompt_cache* c);
+tgx_status tgx_prompt_cache_bytes(const tgx_prompt_cache* c, size_t* out);
+tgx_status tgx_prompt_cache_voices(const tgx_prompt_cache* c, int* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,7 @@ SOURCES = {
     "lm_side.cpp": HOST_FLAGS,
     "api_patch.cpp": HOST_FLAGS,
     "checkpoint.cpp": HOST_FLAGS,
+    "prompt.cpp": HOST_FLAGS,
 }
 
 

@@ -356,6 +356,25 @@ tgx_status checkpoint_rows(const Checkpoint* ck, const std::vector<std::string>&
     return TGX_OK;
 }
 
+tgx_status checkpoint_gather(const Checkpoint* ck, const std::string& name, const int64_t* rows, int n, float* out,
+                             int64_t* columns_out) {
+    auto it = ck->entries.find(name);
+    if (it == ck->entries.end()) return bad(ck->path, name + ": no such tensor");
+    const CheckpointEntry& e = it->second;
+    if (e.shape.size() != 2) return bad(ck->path, name + ": not 2-D");
+    const int64_t count = e.shape[0], columns = e.shape[1];
+    *columns_out = columns;
+    std::vector<uint8_t> bytes((size_t)columns * e.width);
+    for (int i = 0; i < n; ++i) {
+        if (rows[i] < 0 || rows[i] >= count) return bad(ck->path, name + ": row " + std::to_string(rows[i]) + " of " + std::to_string(count));
+        if (!read_at(ck->fd, bytes.data(), bytes.size(), ck->data + e.begin + (uint64_t)rows[i] * bytes.size()))
+            return bad(ck->path, name + ": a short read");
+        const std::vector<float> v = as_f32(bytes.data(), e.dtype, (size_t)columns);
+        std::memcpy(out + (size_t)i * columns, v.data(), v.size() * 4);
+    }
+    return TGX_OK;
+}
+
 namespace {
 
 using Loader = tgx_status (*)(void* target, const char* name, const void* data, tgx_dtype dtype, size_t count);
@@ -457,10 +476,6 @@ tgx_status encoder_load_checkpoint(Encoder* e, const Checkpoint* ck) {
 
 using namespace tgx;
 
-struct tgx_checkpoint {
-    Checkpoint* ck;
-};
-
 extern "C" {
 
 tgx_status tgx_checkpoint_open(const char* path, tgx_checkpoint** out) {
@@ -523,21 +538,8 @@ tgx_status tgx_checkpoint_read(const tgx_checkpoint* ck, const char* name, float
 tgx_status tgx_checkpoint_gather(const tgx_checkpoint* ck, const char* name, const int64_t* rows, int n, float* out) {
     clear_error();
     if (!ck || !name || (n > 0 && (!rows || !out))) return fail(TGX_E_ARG, "null checkpoint, name, rows or output");
-    auto it = ck->ck->entries.find(name);
-    if (it == ck->ck->entries.end()) return bad(ck->ck->path, std::string(name) + ": no such tensor");
-    const CheckpointEntry& e = it->second;
-    if (e.shape.size() != 2) return bad(ck->ck->path, std::string(name) + ": not 2-D");
-    const int64_t count = e.shape[0], columns = e.shape[1];
-    std::vector<uint8_t> bytes((size_t)columns * e.width);
-    for (int i = 0; i < n; ++i) {
-        if (rows[i] < 0 || rows[i] >= count)
-            return bad(ck->ck->path, std::string(name) + ": row " + std::to_string(rows[i]) + " of " + std::to_string(count));
-        if (!read_at(ck->ck->fd, bytes.data(), bytes.size(), ck->ck->data + e.begin + (uint64_t)rows[i] * bytes.size()))
-            return bad(ck->ck->path, std::string(name) + ": a short read");
-        const std::vector<float> v = as_f32(bytes.data(), e.dtype, (size_t)columns);
-        std::memcpy(out + (size_t)i * columns, v.data(), v.size() * 4);
-    }
-    return TGX_OK;
+    int64_t columns = 0;
+    return checkpoint_gather(ck->ck, name, rows, n, out, &columns);
 }
 
 tgx_status tgx_decoder_load_checkpoint(tgx_decoder* dec, const tgx_checkpoint* ck, const char* prefix) {

@@ -38,6 +38,11 @@ tgx_status checkpoint_bytes(const Checkpoint* ck, const std::string& name, const
 tgx_status checkpoint_rows(const Checkpoint* ck, const std::vector<std::string>& names, std::vector<uint8_t>& bytes,
                            tgx_dtype* dtype, size_t* count);
 
+// Rows `rows` of the 2-D tensor `name` in f32, one after another (checkpoint.rs:127-139): an
+// embedding lookup reading those rows alone; `columns` their width.
+tgx_status checkpoint_gather(const Checkpoint* ck, const std::string& name, const int64_t* rows, int n, float* out,
+                             int64_t* columns);
+
 struct Decoder;
 struct LmSide;
 struct Sampler;

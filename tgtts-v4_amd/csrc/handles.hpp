@@ -1,5 +1,6 @@
 // The C ABI's opaque handles (include/tgx.h) over the runtime's objects.
 #pragma once
+#include "checkpoint.hpp"
 #include "patch.hpp"
 #include "runtime.hpp"
 
@@ -22,4 +23,7 @@ struct tgx_encoder {
 };
 struct tgx_patch_step {
     tgx::PatchStep* p;
+};
+struct tgx_checkpoint {
+    tgx::Checkpoint* ck;
 };

@@ -1,4 +1,4 @@
-// gemv_linear.comp on gfx950: a workgroup of four waves to a strip of 16 rows of W and a tile of
+// gemv_linear.comp on gfx950 (and select_rows.comp beside it): a workgroup of four waves to a strip of 16 rows of W and a tile of
 // 16 batch rows. The batch rows' inputs are staged in LDS in bf16 in the MFMA's B-operand order;
 // wave w sums the k-blocks w, w + 4, ... and the four waves' sums are added in wave order, so a
 // row's result does not depend on the batch around it.
@@ -62,7 +62,25 @@ __global__ void __launch_bounds__(256) gemv_linear(LinearArgs a) {
     }
 }
 
+// select_rows.comp: out[r] = flags[r] ? a[r] : b[r] over rows of K f32 values, a thread to 4.
+__global__ void __launch_bounds__(256) select_rows(const uint32_t* __restrict__ flags, const float* __restrict__ a,
+                                                   const float* __restrict__ b, float* __restrict__ out, int rows, int K) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= (size_t)rows * K) return;
+    const int r = (int)(i / K);
+    const float* src = flags[r] ? a : b;
+    *reinterpret_cast<float4*>(out + i) = *reinterpret_cast<const float4*>(src + i);
+}
+
 }  // namespace
+
+hipError_t launch_select_rows(const uint32_t* flags, const float* a, const float* b, float* out, int rows, int K,
+                              hipStream_t stream, DispatchTimer* timer) {
+    if (K % 4) return hipErrorInvalidValue;
+    const size_t threads = (size_t)rows * K / 4;
+    dispatch("select_rows", select_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, timer, flags, a, b, out, rows, K);
+    return hipGetLastError();
+}
 
 hipError_t launch_linear(const char* label, const LinearArgs& a, hipStream_t stream, DispatchTimer* timer) {
     dispatch(label, gemv_linear, dim3((a.N + 15) / 16, (a.rows + 15) / 16), dim3(256), 0, stream, timer, a);

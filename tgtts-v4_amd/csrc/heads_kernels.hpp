@@ -25,5 +25,9 @@ struct LinearArgs {
 constexpr int LINEAR_MAX_K = 2048;
 
 hipError_t launch_linear(const char* label, const LinearArgs& a, hipStream_t stream, DispatchTimer* timer);
+// out[r] = flags[r] ? a[r] : b[r], rows of K f32 values (K a multiple of 4): the quantizer's output at
+// a prompt's audio positions and the base LM's at its text (select_rows.comp).
+hipError_t launch_select_rows(const uint32_t* flags, const float* a, const float* b, float* out, int rows, int K,
+                              hipStream_t stream, DispatchTimer* timer);
 
 }  // namespace tgx

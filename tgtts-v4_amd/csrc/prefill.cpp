@@ -104,7 +104,15 @@ tgx_status launch(Decoder* d) {
 void prefill_release(Decoder* d) { prefill_free(d); }
 
 tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out) {
-    if (!d || !runs || !x || !out) return fail(TGX_E_ARG, "null decoder, runs, x or out");
+    if (!out) return fail(TGX_E_ARG, "null out");
+    TGX_TRY(prefill_device(d, runs, nruns, x, false));
+    TGX_HIP(hipMemcpyAsync(out, d->pf.out, (size_t)d->pf.M * d->shape.hidden * 4, hipMemcpyDeviceToHost, d->ctx->stream));
+    TGX_HIP(hipStreamSynchronize(d->ctx->stream));
+    return TGX_OK;
+}
+
+tgx_status prefill_device(Decoder* d, const tgx_run* runs, int nruns, const float* x, bool x_on_device) {
+    if (!d || !runs || !x) return fail(TGX_E_ARG, "null decoder, runs or x");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (nruns <= 0) return fail(TGX_E_SHAPE, "no runs");
     const Shape& s = d->shape;
@@ -146,7 +154,7 @@ tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float*
     p.ntiles = (int)tiles.size();
     hipStream_t st = d->ctx->stream;
     TGX_TRY(sync_slots(d));
-    TGX_HIP(hipMemcpyAsync(p.x, x, M * s.hidden * 4, hipMemcpyHostToDevice, st));
+    TGX_HIP(hipMemcpyAsync(p.x, x, M * s.hidden * 4, x_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
     if ((size_t)M_pad > M) TGX_HIP(hipMemsetAsync(p.x + M * s.hidden, 0, (M_pad - M) * s.hidden * 4, st));
     TGX_HIP(hipMemcpyAsync(p.tok_pos, pos.data(), M_pad * 4, hipMemcpyHostToDevice, st));
     TGX_HIP(hipMemcpyAsync(p.tok_slot, slot.data(), M_pad * 4, hipMemcpyHostToDevice, st));
@@ -154,8 +162,6 @@ tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float*
     TGX_HIP(hipEventRecord(d->ev_start, st));
     TGX_TRY(launch(d));
     TGX_HIP(hipEventRecord(d->ev_end, st));
-    TGX_HIP(hipMemcpyAsync(out, p.out, M * s.hidden * 4, hipMemcpyDeviceToHost, st));
-    TGX_HIP(hipStreamSynchronize(st));
     return TGX_OK;
 }
 

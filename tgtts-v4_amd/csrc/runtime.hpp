@@ -136,6 +136,9 @@ tgx_status decoder_launch(Decoder* dec, int times, int advance);
 tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions);
 tgx_status sync_slots(Decoder* d);
 tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out);
+// The same, enqueued on the context's stream without waiting: x from the host, or from the device
+// when x_on_device; the output, [rows of the runs in order][hidden] f32, left in d->pf.out.
+tgx_status prefill_device(Decoder* d, const tgx_run* runs, int nruns, const float* x, bool x_on_device);
 tgx_status prefill_launch(Decoder* d, int times);
 void prefill_release(Decoder* d);
 tgx_status decoder_timings(Decoder* d, int max, tgx_timing* out, int* n);

@@ -183,6 +183,19 @@ EXPORTS = [
     "tgx_lm_side_load_checkpoint",
     "tgx_sampler_load_checkpoint",
     "tgx_encoder_load_checkpoint",
+    "tgx_prompter_create",
+    "tgx_prompter_destroy",
+    "tgx_prompter_max_rows",
+    "tgx_prompter_embed",
+    "tgx_prompter_embeddings",
+    "tgx_prompter_run_rows",
+    "tgx_prompter_run",
+    "tgx_prompter_run_cached",
+    "tgx_prompter_read",
+    "tgx_prompt_cache_create",
+    "tgx_prompt_cache_destroy",
+    "tgx_prompt_cache_bytes",
+    "tgx_prompt_cache_voices",
 ]
 
 _lib: Optional[ctypes.CDLL] = None
@@ -296,6 +309,21 @@ def library() -> ctypes.CDLL:
     lib.tgx_lm_side_load_checkpoint.argtypes = [P, P]
     lib.tgx_sampler_load_checkpoint.argtypes = [P, P]
     lib.tgx_encoder_load_checkpoint.argtypes = [P, P]
+    lib.tgx_prompter_create.argtypes = [P, ctypes.c_int, ctypes.POINTER(P)]
+    lib.tgx_prompter_destroy.argtypes = [P]
+    lib.tgx_prompter_destroy.restype = None
+    lib.tgx_prompter_max_rows.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_prompter_embed.argtypes = [P, P, P]
+    lib.tgx_prompter_embeddings.argtypes = [P, P, P, P, P]
+    lib.tgx_prompter_run_rows.argtypes = [P, _Row, P, P, P, ctypes.c_int]
+    lib.tgx_prompter_run.argtypes = [P, ctypes.c_uint32, P, P]
+    lib.tgx_prompter_run_cached.argtypes = [P, ctypes.c_uint32, P, P, P, ctypes.c_size_t, P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_prompter_read.argtypes = [P, ctypes.c_char_p, P, ctypes.c_size_t]
+    lib.tgx_prompt_cache_create.argtypes = [P, ctypes.c_size_t, ctypes.POINTER(P)]
+    lib.tgx_prompt_cache_destroy.argtypes = [P]
+    lib.tgx_prompt_cache_destroy.restype = None
+    lib.tgx_prompt_cache_bytes.argtypes = [P, ctypes.POINTER(ctypes.c_size_t)]
+    lib.tgx_prompt_cache_voices.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:
         if name.startswith("tgx_") and name not in ("tgx_last_error",):
             fn = getattr(lib, name)
@@ -308,6 +336,8 @@ def library() -> ctypes.CDLL:
     lib.tgx_encoder_destroy.restype = None
     lib.tgx_patch_step_destroy.restype = None
     lib.tgx_checkpoint_close.restype = None
+    lib.tgx_prompter_destroy.restype = None
+    lib.tgx_prompt_cache_destroy.restype = None
     _lib = lib
     return lib
 
@@ -420,7 +450,7 @@ class Context:
     def close(self) -> None:
         if self._h:
             for d in list(_open_decoders):
-                if d.ctx is self:
+                if getattr(d, "ctx", None) is self:
                     d.close()
             library().tgx_context_destroy(self._h)
             self._h = ctypes.c_void_p()

@@ -336,6 +336,7 @@ class PatchStep:
 
     def __init__(self, encoder: Encoder, side: "LmSide", sampler: Sampler):
         self.encoder, self.side, self.sampler = encoder, side, sampler
+        self.ctx = side.ctx
         self._h = ctypes.c_void_p()
         _check(library().tgx_patch_step_create(encoder._h, side._h, sampler._h, ctypes.byref(self._h)))
         _open_decoders.add(self)
