@@ -443,6 +443,66 @@ void tgx_prompt_cache_destroy(tgx_prompt_cache* c);
 tgx_status tgx_prompt_cache_bytes(const tgx_prompt_cache* c, size_t* out);
 tgx_status tgx_prompt_cache_voices(const tgx_prompt_cache* c, int* out);
 
+/* ---- the engine the service's GPU thread drives: crates/tgtts/src/rt.rs, crates/graph/src/generator.rs ---- */
+
+typedef struct tgx_engine tgx_engine;
+
+/* generator::Settings (generator.rs:35-56): the requests at once (the patch step's rows, a row to
+ * a slot), the positions a slot's caches hold, a prompt's positions one run takes, the Euler
+ * steps, and the prompt cache's bytes. */
+typedef struct {
+    int slots, capacity, max_rows, timesteps;
+    size_t prompt_cache_bytes;
+} tgx_engine_settings;
+
+/* What a step gave the request in `slot` (generator::Outcome, generator.rs:76): TGX_OK and its
+ * patch (in the step's frames), or TGX_E_NOT_FINITE, after which it has ended; `last` when it was
+ * the request's last (the stop head's argmax, or its most patches sampled). */
+typedef struct {
+    int slot;
+    tgx_status status;
+    int last;
+    float stop_logits[2];
+} tgx_engine_outcome;
+
+/* Generator::new (generator.rs:130-193) over the shapes config.json gives (the base LM, the
+ * residual LM, the layers between them, the local encoder's and the DiT's stacks, the latent
+ * frames of a patch) and the weights in `ck`, which the engine reads token embeddings from and
+ * which must outlive it. The audio VAE is not part of the engine: it hands back latent frames. */
+tgx_status tgx_engine_create(tgx_context* ctx, const tgx_checkpoint* ck, const tgx_shape* base, const tgx_shape* residual,
+                             const tgx_heads_shape* heads, const tgx_shape* encoder, const tgx_shape* dit, int feat_dim,
+                             int patch_size, const tgx_engine_settings* settings, tgx_engine** out);
+/* Engine::close (rt.rs:108-110). */
+void tgx_engine_destroy(tgx_engine* e);
+/* Engine::slots (rt.rs:96). */
+tgx_status tgx_engine_slots(const tgx_engine* e, int* out);
+/* Engine::start (rt.rs:98-100; Generator::start, generator.rs:205-262): ends any request in the
+ * slot and runs `prompt` into it from what the prompt cache keeps of the voice (its latent frames,
+ * feat_dim values each), to sample up to `max_patches` patches at `temperature` and guidance
+ * `cfg`; `prefilled`: the prompt's positions that ran through the LMs. */
+tgx_status tgx_engine_start(tgx_engine* e, int slot, const tgx_prompt* prompt, const float* voice, size_t voice_len,
+                            int max_patches, float temperature, float cfg, int* prefilled);
+/* Generator::sample_after (generator.rs:264-279): the slot's next patch sampled after `frames`,
+ * [patch_size][feat_dim], rather than its last (teacher forcing). */
+tgx_status tgx_engine_sample_after(tgx_engine* e, int slot, const float* frames);
+/* Engine::step (rt.rs:102-104; Generator::step, generator.rs:281-334): a patch of every request
+ * under way in one patch step, each from its slot's noise (`noise` [slots][feat_dim][patch_size],
+ * read for the slots under way); `n` outcomes, each request's patch in `frames`
+ * [slots][patch_size][feat_dim] at its slot. A request whose last patch was sampled waits in its
+ * slot to be finished. */
+tgx_status tgx_engine_step(tgx_engine* e, const float* noise, tgx_engine_outcome* outcomes, float* frames, int* n);
+/* Generator::levels (generator.rs:336-362): the quantizer's levels (integers) the slot's last
+ * patch was sampled after, [latent]. */
+tgx_status tgx_engine_levels(tgx_engine* e, int slot, float* out);
+/* Generator::take_audio (generator.rs:364-369) for the latent frames: those sampled since last
+ * taken, `n` frames of feat_dim values (at most `max`). */
+tgx_status tgx_engine_take_frames(tgx_engine* e, int slot, float* out, int max, int* n);
+/* Engine::finish (rt.rs:106-107; Generator::finish, generator.rs:395-403): ends the request,
+ * giving the frames not yet taken. */
+tgx_status tgx_engine_finish(tgx_engine* e, int slot, float* out, int max, int* n);
+/* What the prompt cache keeps (Generator::prompt_cache, generator.rs:364-367). */
+tgx_status tgx_engine_prompt_cache(const tgx_engine* e, size_t* bytes, int* voices);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ SOURCES = {
     "api_patch.cpp": HOST_FLAGS,
     "checkpoint.cpp": HOST_FLAGS,
     "prompt.cpp": HOST_FLAGS,
+    "engine.cpp": HOST_FLAGS,
 }
 
 

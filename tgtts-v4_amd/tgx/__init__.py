@@ -196,6 +196,16 @@ EXPORTS = [
     "tgx_prompt_cache_destroy",
     "tgx_prompt_cache_bytes",
     "tgx_prompt_cache_voices",
+    "tgx_engine_create",
+    "tgx_engine_destroy",
+    "tgx_engine_slots",
+    "tgx_engine_start",
+    "tgx_engine_sample_after",
+    "tgx_engine_step",
+    "tgx_engine_levels",
+    "tgx_engine_take_frames",
+    "tgx_engine_finish",
+    "tgx_engine_prompt_cache",
 ]
 
 _lib: Optional[ctypes.CDLL] = None
@@ -324,6 +334,18 @@ def library() -> ctypes.CDLL:
     lib.tgx_prompt_cache_destroy.restype = None
     lib.tgx_prompt_cache_bytes.argtypes = [P, ctypes.POINTER(ctypes.c_size_t)]
     lib.tgx_prompt_cache_voices.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_engine_create.argtypes = [P, P, P, P, P, P, P, ctypes.c_int, ctypes.c_int, P, ctypes.POINTER(P)]
+    lib.tgx_engine_destroy.argtypes = [P]
+    lib.tgx_engine_destroy.restype = None
+    lib.tgx_engine_slots.argtypes = [P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_engine_start.argtypes = [P, ctypes.c_int, P, P, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                     ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_engine_sample_after.argtypes = [P, ctypes.c_int, P]
+    lib.tgx_engine_step.argtypes = [P, P, P, P, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_engine_levels.argtypes = [P, ctypes.c_int, P]
+    lib.tgx_engine_take_frames.argtypes = [P, ctypes.c_int, P, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_engine_finish.argtypes = [P, ctypes.c_int, P, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+    lib.tgx_engine_prompt_cache.argtypes = [P, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_int)]
     for name in EXPORTS:
         if name.startswith("tgx_") and name not in ("tgx_last_error",):
             fn = getattr(lib, name)
@@ -338,6 +360,7 @@ def library() -> ctypes.CDLL:
     lib.tgx_checkpoint_close.restype = None
     lib.tgx_prompter_destroy.restype = None
     lib.tgx_prompt_cache_destroy.restype = None
+    lib.tgx_engine_destroy.restype = None
     _lib = lib
     return lib
 
