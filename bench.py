@@ -369,6 +369,40 @@ def copy_calibration() -> int:
     return 0
 
 
+def sampler_profile(rows: int, samples: int) -> int:
+    """The sampler alone (a 4-layer LocDiT, 10 Euler steps over 4 x 64 latents, CFG-Zero* 2.0) at
+    `rows` requests, launched dispatch by dispatch with events around each (what a kernel-trace
+    profiler sees), `samples` times after one to warm up: each kernel's mean time a launch."""
+    import collections
+
+    import tgx
+    from tgx.patch import PatchShape, Sampler
+    from tgx.synth import StackSpec, sampler_weights
+
+    ctx = tgx.Context(0)
+    s = Sampler(ctx, tgx.Shape(layers=4, capacity=16), PatchShape(64, 4, 10, rows))
+    s.load_all(sampler_weights(StackSpec(layers=4, seed=2), 64))
+    rng = np.random.default_rng(5)
+    mu = rng.standard_normal((rows, 2, 1024)).astype(np.float32)
+    cond = rng.standard_normal((rows, 64, 4)).astype(np.float32)
+    noise = rng.standard_normal((rows, 64, 4)).astype(np.float32)
+    sampling = np.array([[1.0, 2.0]] * rows, dtype=np.float32)
+    s.set_timed(True)
+    s.sample(mu, cond, noise, sampling)
+    total, count = collections.defaultdict(float), collections.Counter()
+    for _ in range(samples):
+        s.sample(mu, cond, noise, sampling)
+        for label, ms in s.timings():
+            total[label] += ms
+            count[label] += 1
+    log(f"sampler at {rows} rows: {sum(total.values()) / samples * 1e3:.1f} us a sample of dispatch-timed kernels")
+    for label in sorted(total, key=lambda k: -total[k]):
+        log(f"  {label:20s} {total[label] / count[label] * 1e3:8.2f} us a launch x {count[label] // samples:3d}")
+    s.close()
+    ctx.close()
+    return 0
+
+
 def measured_traffic(label: str, workload: str):
     """HBM bytes per launch of `label` measured with rocprofv3's FETCH_SIZE and WRITE_SIZE on the
     same workload, each scaled by the counter's reading of a copy of known size; None when no
@@ -397,11 +431,15 @@ def main() -> int:
                     help="only run a plain device copy of 256 MiB five times (scales rocprofv3's HBM counters)")
     ap.add_argument("--eager", action="store_true",
                     help="launch each step dispatch by dispatch, not as the recorded graph (for profilers)")
+    ap.add_argument("--sampler", action="store_true",
+                    help="only the sampler at --batch rows, dispatch by dispatch, --steps samples (for profilers)")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
     if args.copy_calibration:
         return copy_calibration()
+    if args.sampler:
+        return sampler_profile(args.batch, args.steps)
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (requests would be routed to "
               "GPUs at admission, with no collective); run with --gpus 1.", file=sys.stderr)
