@@ -130,7 +130,7 @@ def run_rows(ctx, spec, x, rows, cap, shift=0):
     return [np.stack(g) for g in got]
 
 
-@pytest.mark.parametrize("rows", [3, 16])
+@pytest.mark.parametrize("rows", [3, 16, 20, 40])  # one tile, a full one, two tiles, three (ragged)
 def test_each_row_of_a_batch_is_bit_for_bit_as_it_is_alone(ctx, rows):
     spec = tiny_spec(layers=2)
     cap = 320

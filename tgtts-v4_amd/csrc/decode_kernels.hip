@@ -72,15 +72,20 @@ struct Operand {
     __device__ static int row(int B, int tile) { return min(tile * 16 + (int)(threadIdx.x % 16), B - 1); }
 };
 
-// Bf16 rows [B][K].
+// Where the projections' bf16 operands keep row b, column k: k-block by k-block, the batch's rows
+// one after another in each, [K / 32][B][32]. A k-block of a tile's 16 rows is then 1 KiB in one
+// piece (every cache line read whole), and a tile of one row the same 64 bytes 16 times over.
+__device__ __forceinline__ size_t operand_index(int b, int k, int B) { return ((size_t)(k / 32) * B + b) * 32 + k % 32; }
+
+// Bf16 rows [B][K] in operand order.
 template <int CH>
 struct RawRows : Operand<CH> {
     using Operand<CH>::KB;
 
     __device__ void load(const uint16_t* __restrict__ x, int B, int tile) {
-        const uint16_t* row = x + (size_t)Operand<CH>::row(B, tile) * (CH * CHUNK_COLS);
+        const int b = Operand<CH>::row(B, tile);
 #pragma unroll
-        for (int i = 0; i < KB; ++i) this->xf[i] = load16(row + Operand<CH>::column(i));
+        for (int i = 0; i < KB; ++i) this->xf[i] = load16(x + operand_index(b, Operand<CH>::column(i), B));
     }
 };
 
@@ -330,31 +335,54 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
 }
 
 // ---------------------------------------------------------------------------------------------
-// gemv_gate_up: workgroup (s, tile): strip s (16 rows) of the gate and the same strip of up,
-// against mid post_norm in bf16 and mid's sums of squares.
-template <int CH>
+// gemv_gate_up: workgroup (s, group): strip s (16 rows) of the gate and the same strip of up,
+// against TT 16-row tiles of mid post_norm in bf16 (tiles TT group .. TT group + TT - 1) and mid's
+// sums of squares. The strips' weights are read once for the TT tiles, and each tile's products
+// are the same chains as with one tile to a workgroup; the tiles' partial sums go through LDS two
+// at a time.
+template <int CH, int TT>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_gate_up(DecodeArgs a, LayerArgs l) {
-    __shared__ f32x4 red[GEMV_WAVES * 2 * 64];
-    __shared__ float scale[16];
-    const int s = blockIdx.x, tile = blockIdx.y;
+    constexpr int TS = TT < 2 ? TT : 2;  // tiles reduced at once
+    __shared__ f32x4 red[TS][GEMV_WAVES * 2 * 64];
+    __shared__ float scale[TT][16];
+    const int s = blockIdx.x, tile0 = blockIdx.y * TT;
     const int strip[2] = {s, s + a.inner / 16};
-    RowSquares<CH> squares;
-    RawRows<CH> x;
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    RowSquares<CH> squares[TT];
+    RawRows<CH> x[TT];
     Gemv<2, CH> g;
-    squares.load(l.mid_sq, a.rows, tile);
-    x.load(l.mid_n, a.rows, tile);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) squares[t].load(l.mid_sq, a.rows, tile0 + t);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) x[t].load(l.mid_n, a.rows, tile0 + t);
     g.load(l.gate_up, strip);
     all_issued();
-    squares.finish(a.eps, scale);
-    g.run(x.xf);
-    spill<2>(g.acc, red);
-    for (int idx = threadIdx.x; idx < 16 * 16; idx += GEMV_THREADS) {
-        const int r = idx % 16, c = idx / 16;
-        const int b = tile * 16 + c;
-        if (b >= a.rows) continue;
-        const float gate = reduced<2>(red, 0, r, c) * scale[c];
-        const float up = reduced<2>(red, 1, r, c) * scale[c];
-        l.mlp[(size_t)b * a.inner + s * 16 + r] = (uint16_t)bf16_bits(gate / (1.0f + __expf(-gate)) * up);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) squares[t].finish(a.eps, scale[t]);
+    f32x4 acc[TT][2];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        g.run(x[t].xf);
+        acc[t][0] = g.acc[0];
+        acc[t][1] = g.acc[1];
+    }
+#pragma unroll
+    for (int t0 = 0; t0 < TT; t0 += TS) {
+        if (t0) __syncthreads();  // the last tiles' sums are read
+#pragma unroll
+        for (int t = 0; t < TS; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) red[t][(w * 2 + h) * 64 + lane] = acc[t0 + t][h];
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < TS * 16 * 16; idx += GEMV_THREADS) {
+            const int r = idx % 16, c = (idx / 16) % 16, t = idx / 256;
+            const int b = (tile0 + t0 + t) * 16 + c;
+            if (b >= a.rows) continue;
+            const float sc = scale[t0 + t][c];
+            const float gate = reduced<2>(red[t], 0, r, c) * sc;
+            const float up = reduced<2>(red[t], 1, r, c) * sc;
+            l.mlp[operand_index(b, s * 16 + r, a.rows)] = (uint16_t)bf16_bits(gate / (1.0f + __expf(-gate)) * up);
+        }
     }
 }
 
@@ -392,7 +420,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
     const size_t at = (size_t)b * r.N + n0;
     *reinterpret_cast<float4*>(r.out + at) = v;
     if (r.next_norm) {
-        *reinterpret_cast<uint2*>(r.out_n + at) =
+        *reinterpret_cast<uint2*>(r.out_n + operand_index(b, n0, a.rows)) =
             make_uint2(pack_bf16x2(v.x * gain.x, v.y * gain.y), pack_bf16x2(v.z * gain.z, v.w * gain.w));
         float s2 = v.x * v.x;
         s2 += v.y * v.y;
@@ -492,7 +520,6 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     }
     __syncthreads();
     // The waves joined in order (wave 0 holds block 0, so M is finite).
-    const size_t head0 = (size_t)b * H + kv * group;
     for (int idx = threadIdx.x; idx < group * HEAD_DIM; idx += ATTN_THREADS) {
         const int hh = idx / HEAD_DIM, d = idx % HEAD_DIM;
         float M = -INFINITY;
@@ -503,7 +530,7 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
             L += sm_l[j][hh] * f;
             O += attn_lds[(j * group + hh) * (HEAD_DIM + 1) + d] * f;
         }
-        l.attended[(head0 + hh) * HEAD_DIM + d] = (uint16_t)bf16_bits(O / L);
+        l.attended[operand_index(b, (kv * group + hh) * HEAD_DIM + d, a.rows)] = (uint16_t)bf16_bits(O / L);
     }
 }
 
@@ -560,7 +587,7 @@ auto by_chunks(int chunks) -> decltype(Pick<1>::get()) {
 }
 template <int CH> struct PickQkv { static auto get() { return gemv_qkv_rope<CH, false>; } };
 template <int CH> struct PickQkvNormed { static auto get() { return gemv_qkv_rope<CH, true>; } };
-template <int CH> struct PickGateUp { static auto get() { return gemv_gate_up<CH>; } };
+template <int CH> struct PickGateUp { static auto get() { return gemv_gate_up<CH, 1>; } };
 template <int CH> struct PickResidual4 { static auto get() { return gemv_residual<CH, 4>; } };
 template <int CH> struct PickResidual16 { static auto get() { return gemv_residual<CH, 16>; } };
 template <int CH> struct PickFinal { static auto get() { return final_rmsnorm<CH>; } };
@@ -592,7 +619,16 @@ hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const Re
     dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), attention_lds(a), stream, timer, a, l);
     hipError_t e = residual("o_proj", a, o, stream, timer);
     if (e != hipSuccess) return e;
-    dispatch("gemv_gate_up", by_chunks<PickGateUp>(hidden_chunks), dim3(a.inner / 16, tiles), block, 0, stream, timer, a, l);
+    // Past one tile a workgroup takes two or four, reading the strips' weights once for them (for a
+    // hidden size of one chunk: more would not fit the registers).
+    const int per = hidden_chunks > 1 || tiles == 1 ? 1 : tiles == 2 ? 2 : 4;
+    const dim3 gu_grid(a.inner / 16, (tiles + per - 1) / per);
+    if (per == 1)
+        dispatch("gemv_gate_up", by_chunks<PickGateUp>(hidden_chunks), gu_grid, block, 0, stream, timer, a, l);
+    else if (per == 2)
+        dispatch("gemv_gate_up", gemv_gate_up<1, 2>, gu_grid, block, 0, stream, timer, a, l);
+    else
+        dispatch("gemv_gate_up", gemv_gate_up<1, 4>, gu_grid, block, 0, stream, timer, a, l);
     if ((e = residual("down_proj", a, down, stream, timer)) != hipSuccess) return e;
     return hipGetLastError();
 }

@@ -32,6 +32,8 @@ struct DecodeArgs {
 // column and adds the row's sums in a fixed order.
 struct LayerArgs {
     const float* x;           // layer input [rows][hidden] f32
+    // The projections' bf16 operands (xn, attended, mid_n, mlp) are kept in operand order: k-block
+    // by k-block, [K / 32][rows][32].
     const uint16_t* xn;       // x input_norm in bf16 [rows][hidden], or null: taken from x
     const float* x_sq;        // [rows][hidden / 4]
     const float* input_norm;  // [hidden] f32
@@ -49,13 +51,13 @@ struct LayerArgs {
 // bf16 and out's sums of squares over each 4 columns, for the norm that reads out next.
 struct ResidualArgs {
     const uint16_t* w;
-    const uint16_t* x;  // [rows][K] bf16
+    const uint16_t* x;  // [rows][K] bf16 in operand order
     int K, N;
     int R;                  // strip height of w: 4 or 16
     const float* residual;  // [rows][N]
     float* out;             // [rows][N]
     const float* next_norm; // [N], or null
-    uint16_t* out_n;        // [rows][N]
+    uint16_t* out_n;        // [rows][N] in operand order
     float* out_sq;          // [rows][N / 4]
 };
 
