@@ -20,28 +20,42 @@ namespace tgx {
 
 namespace {
 
-// The GEMM's workgroup: eight waves, two to a SIMD, so that one wave's products run while the
-// other waits for LDS or the barrier. Its tile: 256 rows of W (16 strips) by 256 rows of X, K 32
-// at a time (a k-block to a stage, four stages in an LDS ring, three in flight while one is
-// multiplied); wave (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 64 wm .. + 63
-// (4 tiles of 16): 32 accumulators of 16 x 16.
-constexpr int GEMM_WAVES = 8;
-constexpr int GEMM_THREADS = GEMM_WAVES * WAVE;
-constexpr int TN = 256, TM = 256;
+// The GEMM's tile: 256 rows of W (16 strips) by TM rows of X, K 32 at a time (a k-block to a
+// stage, in a ring of NBUF stages in LDS, all but one in flight while one is multiplied); wave
+// (wn, wm) takes W rows 128 wn .. + 127 (8 strips) by X rows 64 wm .. + 63 (4 tiles of 16):
+// 32 accumulators of 16 x 16. Two waves to a SIMD, so that one wave's products run while the
+// other waits for LDS or the barrier:
+//   TM 256: eight waves, a ring of four 32 KiB stages, a workgroup to a CU;
+//   TM 128: four waves, a ring of three 24 KiB stages, two workgroups to a CU, so that one's
+//           epilogue (its memory traffic) runs beside the other's products.
+constexpr int TN = 256;
 constexpr int W_STRIPS = TN / 16;   // 16
-constexpr int X_TILES = TM / 16;    // 16
 constexpr int WS = 8;               // a wave's W strips
 constexpr int WT = 4;               // a wave's X tiles
 constexpr int W_STAGE = W_STRIPS * 64;  // uint4 per stage: 16 KiB
-constexpr int X_STAGE = X_TILES * 64;   // 16 KiB
-constexpr int NBUF = 4;
-constexpr int FRAGS = (W_STRIPS + X_TILES) / GEMM_WAVES;  // 1 KiB loads a wave issues a stage
-static_assert(W_STRIPS % FRAGS == 0, "a wave loads W fragments or X fragments, not both");
+constexpr int ROW_TILE_MAX = 256;   // M_pad is a multiple of this
+
+template <int TM_>
+struct GemmTile {
+    static constexpr int TM = TM_;
+    static constexpr int WAVES = TM / 32;  // 2 wave rows of W by TM / 64 of X
+    static constexpr int THREADS = WAVES * WAVE;
+    static constexpr int X_TILES = TM / 16;
+    static constexpr int X_STAGE = X_TILES * 64;
+    static constexpr int NBUF = TM == 256 ? 4 : 3;
+    // The first half of the waves load W's fragments, the second half X's: FW and FX 1 KiB loads
+    // a wave issues a stage.
+    static constexpr int FW = W_STRIPS / (WAVES / 2);
+    static constexpr int FX = X_TILES / (WAVES / 2);
+    static constexpr size_t LDS = (size_t)NBUF * (W_STAGE + X_STAGE) * 16 + TM * sizeof(float);
+    static_assert(THREADS >= TM, "the q/k/v epilogue stages a row to a thread");
+    static_assert(ROW_TILE_MAX % TM == 0, "M_pad is a multiple of TM");
+    static_assert((NBUF - 1) * FW < 64, "the loads in flight fit the wave's counter");
+};
 
 enum Epilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2 };
 
 constexpr uint32_t TGX_SPARE_POS = 0xffffffffu;
-static_assert(GEMM_THREADS >= TM, "the q/k/v epilogue stages a row to a thread");
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -73,6 +87,7 @@ constexpr int SQ_SPAN = WS * 16;
 // SQ_SPAN columns, at most MAX_PARTS, added in order), a thread to a row; each 1 without
 // row_sq. The parts are loaded at once, before the GEMM's own loads.
 constexpr int MAX_PARTS = 4096 / SQ_SPAN;
+template <int TM>
 struct RowScale {
     float4 p[MAX_PARTS / 4];
     __device__ void load(const GemmArgs& g, int m0) {
@@ -146,8 +161,11 @@ __device__ __forceinline__ void tile_of(int& nb, int& mb) {
 
 // W in strips of WR rows (o_proj and down_proj: 4 or 16, the rest 16), gathered into 16-row
 // fragments as it lands in LDS.
-template <int EPI, int WR = QKV_ROWS>
-__global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, GemmArgs g) {
+template <int EPI, int WR, int TM>
+__global__ void __launch_bounds__(GemmTile<TM>::THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+prefill_gemm(PrefillArgs a, GemmArgs g) {
+    using T = GemmTile<TM>;
+    constexpr int NBUF = T::NBUF, X_STAGE = T::X_STAGE, FW = T::FW, FX = T::FX;
     extern __shared__ uint4 lds[];
     uint4* ws = lds;                     // [NBUF][W_STAGE]
     uint4* xs = lds + NBUF * W_STAGE;    // [NBUF][X_STAGE]
@@ -157,49 +175,67 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
     // The wave's index, uniform: the branches on it below are the whole wave's.
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     const int lane = threadIdx.x % WAVE;
-    const int wn = w / 4, wm = w % 4;
+    const int wn = w / (T::WAVES / 2), wm = w % (T::WAVES / 2);
     const int kblocks = g.K / 32;
     const int stages = kblocks;
     const int m0 = mb * TM;
 
-    // A stage is 16 weight fragments and 16 vector fragments of 1 KiB, eight to a wave (the
-    // first two waves W's, the last two X's), loaded straight from memory into LDS: lane l of a
-    // load writes bytes 16 l .. 16 l + 15 of the fragment, the MFMA operand order. Each wave
-    // issues exactly FRAGS loads a stage, so its count in flight says which stages have landed.
-    // Fragment j of stage st is lane's src[j] + st * step (a k-block further along K).
-    const bool loads_w = w * FRAGS < W_STRIPS;
-    const uint16_t* src[FRAGS];
-    int step_elems;
+    // A stage is 16 weight fragments and TM / 16 vector fragments of 1 KiB (the first half of
+    // the waves load W's, FW each, the second half X's, FX each), loaded straight from memory
+    // into LDS: lane l of a load writes bytes 16 l .. 16 l + 15 of the fragment, the MFMA operand
+    // order. A wave issues the same number of loads every stage, so its count in flight says
+    // which stages have landed. Fragment j of stage st is lane's base + off[j] + st * step (a
+    // k-block further along K), the offsets 32-bit (a tensor holds fewer than 2^32 elements).
+    const bool loads_w = w < T::WAVES / 2;
+    constexpr int FMAX = FW > FX ? FW : FX;
+    const uint16_t* base = loads_w ? g.w : g.x;
+    uint32_t off[FMAX];
+    uint32_t step_elems;
     uint4* dst0;
     if (loads_w) {
 #pragma unroll
-        for (int j = 0; j < FRAGS; ++j) src[j] = g.w + fragment_index<WR>(stage_strip<EPI>(nb, w * FRAGS + j, g.N), 0, kblocks, lane);
+        for (int j = 0; j < FW; ++j) off[j] = (uint32_t)fragment_index<WR>(stage_strip<EPI>(nb, w * FW + j, g.N), 0, kblocks, lane);
         step_elems = WR * 32;
-        dst0 = ws + w * FRAGS * 64;
+        dst0 = ws + w * FW * 64;
     } else {
+        const int x0 = (w - T::WAVES / 2) * FX;  // the wave's first X tile
 #pragma unroll
-        for (int j = 0; j < FRAGS; ++j)
-            src[j] = g.x + (size_t)(m0 / 16 + w * FRAGS + j - W_STRIPS) * kblocks * 512 + lane * 8;
+        for (int j = 0; j < FX; ++j) off[j] = (uint32_t)(m0 / 16 + x0 + j) * (uint32_t)kblocks * 512u + (uint32_t)lane * 8u;
         step_elems = 512;
-        dst0 = xs + (w * FRAGS - W_STRIPS) * 64;
+        dst0 = xs + x0 * 64;
     }
     const int stage_stride = loads_w ? W_STAGE : X_STAGE;
     auto fetch = [&](int st) __attribute__((always_inline)) {
         uint4* dst = dst0 + (st % NBUF) * stage_stride;
+        const uint32_t along = (uint32_t)st * step_elems;
+        if (loads_w) {
 #pragma unroll
-        for (int j = 0; j < FRAGS; ++j) load_to_lds(src[j] + (size_t)st * step_elems, dst + j * 64);
+            for (int j = 0; j < FW; ++j) load_to_lds(base + (off[j] + along), dst + j * 64);
+        } else {
+#pragma unroll
+            for (int j = 0; j < FX; ++j) load_to_lds(base + (off[j] + along), dst + j * 64);
+        }
     };
     // Waits until stage st has landed for every wave: no more than the stages fetched after it
     // in flight for this wave, then the barrier, which also says that every wave is done with
     // stage st - 1, whose buffer the next fetch takes.
     auto landed = [&](int st) __attribute__((always_inline)) {
         const int after = min(NBUF - 2, stages - 1 - st);
-        if (after >= 2)
-            wait_vm<2 * FRAGS>();
-        else if (after == 1)
-            wait_vm<FRAGS>();
-        else
-            wait_vm<0>();
+        if (loads_w) {
+            if (after >= 2)
+                wait_vm<2 * FW>();
+            else if (after == 1)
+                wait_vm<FW>();
+            else
+                wait_vm<0>();
+        } else {
+            if (after >= 2)
+                wait_vm<2 * FX>();
+            else if (after == 1)
+                wait_vm<FX>();
+            else
+                wait_vm<0>();
+        }
         stage_barrier();
     };
 
@@ -241,7 +277,7 @@ __global__ void __launch_bounds__(GEMM_THREADS) prefill_gemm(PrefillArgs a, Gemm
     // The rows' scales (q/k/v, gate/up): their loads go first, the GEMM's behind them, and the
     // scales are taken once the first stage has landed (so have they), reaching LDS long before
     // the epilogue, past every barrier of the main loop.
-    RowScale rs;
+    RowScale<TM> rs;
     const bool scales = EPI != EPI_RESIDUAL && threadIdx.x < TM;  // whole waves
     if (scales) rs.load(g, m0);
 #pragma unroll
@@ -575,8 +611,17 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
     }
 }
 
-// The ring (128 KiB) and the rows' scales.
-constexpr size_t GEMM_LDS = (size_t)NBUF * (W_STAGE + X_STAGE) * sizeof(uint4) + TM * sizeof(float);
+// Each projection's X rows to a workgroup. 128 for all: with two workgroups to a CU, one's
+// epilogue (10 bytes an output for o_proj and down_proj: the f32 residual in and out, the next
+// norm's bf16 operand) and prologue run beside the other's products, which at 8 x 2048 positions
+// beats one 256-row workgroup to a CU for every projection (gate/up by a tenth).
+constexpr int QKV_TM = 128, O_TM = 128, GATE_UP_TM = 128, DOWN_TM = 128;
+
+template <int EPI, int WR, int TM>
+void gemm(const char* label, const PrefillArgs& a, const GemmArgs& g, hipStream_t stream, DispatchTimer* timer) {
+    dispatch(label, prefill_gemm<EPI, WR, TM>, dim3(g.N / TN, a.M_pad / TM), dim3(GemmTile<TM>::THREADS), GemmTile<TM>::LDS,
+             stream, timer, a, g);
+}
 
 hipError_t allow(const void* kernel, size_t device_lds) {
     hipFuncAttributes attr{};
@@ -589,15 +634,16 @@ hipError_t allow(const void* kernel, size_t device_lds) {
 
 hipError_t prefill_prepare(size_t device_lds) {
     hipError_t e;
-    if ((e = allow((const void*)prefill_gemm<EPI_QKV>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16>, device_lds)) != hipSuccess) return e;
-    return allow((const void*)prefill_gemm<EPI_SILU>, device_lds);
+    if ((e = allow((const void*)prefill_gemm<EPI_QKV, QKV_ROWS, QKV_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4, O_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16, O_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4, DOWN_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16, DOWN_TM>, device_lds)) != hipSuccess) return e;
+    return allow((const void*)prefill_gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>, device_lds);
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int nlayers, const float* final_norm,
                           const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer) {
-    const int mblocks = a.M_pad / TM;
     const dim3 rows4((a.M_pad + 3) / 4);
     const int group = a.heads / a.kv_heads;
     const int qkv_rows = (a.heads + 2 * a.kv_heads) * HEAD_DIM;
@@ -611,7 +657,7 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
         const PrefillLayer& L = layers[l];
         GemmArgs qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, nullptr, b.q, L.kv,
                      l == 0 ? nullptr : b.row_sq, nullptr, nullptr, nullptr};
-        dispatch("prefill_qkv", prefill_gemm<EPI_QKV>, dim3(qkv_rows / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, qkv);
+        gemm<EPI_QKV, QKV_ROWS, QKV_TM>("prefill_qkv", a, qkv, stream, timer);
         switch (group) {
             case 1: dispatch("prefill_attention", prefill_attention<2, 1>, dim3(b.ntiles, a.kv_heads), dim3(2 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
             case 2: dispatch("prefill_attention", prefill_attention<4, 1>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
@@ -620,18 +666,23 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
             case 16: dispatch("prefill_attention", prefill_attention<8, 4>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
             default: return hipErrorInvalidValue;
         }
-        auto residual_gemm = L.od_rows == 4 ? prefill_gemm<EPI_RESIDUAL, 4> : prefill_gemm<EPI_RESIDUAL, 16>;
         if (L.od_rows != 4 && L.od_rows != 16) return hipErrorInvalidValue;
         GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr,
                    nullptr, L.post_norm, b.normed, b.row_sq};
-        dispatch("prefill_o", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, o);
+        if (L.od_rows == 4)
+            gemm<EPI_RESIDUAL, 4, O_TM>("prefill_o", a, o, stream, timer);
+        else
+            gemm<EPI_RESIDUAL, 16, O_TM>("prefill_o", a, o, stream, timer);
         GemmArgs gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, nullptr, b.mlp, nullptr, nullptr,
                     b.row_sq, nullptr, nullptr, nullptr};
-        dispatch("prefill_gate_up", prefill_gemm<EPI_SILU>, dim3(2 * a.inner / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, gu);
+        gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>("prefill_gate_up", a, gu, stream, timer);
         // The last layer's output goes to the final norm, which reads the f32 rows.
         GemmArgs down{L.down, b.mlp, a.inner, a.hidden, b.mid, b.h, nullptr, nullptr, nullptr,
                       nullptr, l + 1 < nlayers ? layers[l + 1].input_norm : nullptr, b.normed, b.row_sq};
-        dispatch("prefill_down", residual_gemm, dim3(a.hidden / TN, mblocks), dim3(GEMM_THREADS), GEMM_LDS, stream, timer, a, down);
+        if (L.od_rows == 4)
+            gemm<EPI_RESIDUAL, 4, DOWN_TM>("prefill_down", a, down, stream, timer);
+        else
+            gemm<EPI_RESIDUAL, 16, DOWN_TM>("prefill_down", a, down, stream, timer);
         input = b.h;
     }
     dispatch("prefill_final_norm", prefill_norm<true>, rows4, dim3(256), 0, stream, timer, a, input, final_norm,
