@@ -162,6 +162,41 @@ def test_batch_of_64_rows_is_as_alone(ctx):
         assert np.array_equal(outs[:, r].view(np.uint32), alone.view(np.uint32)), f"row {r}"
 
 
+def test_long_contexts_match_the_oracle_and_each_row_is_as_alone(ctx):
+    """Past 512 positions each of the attention's waves takes more than one 64-position block
+    (its turns, two at a time): a row at 1100 positions (18 blocks, three turns) matches the
+    oracle step by step, and each row of a batch of long and short contexts is bit for bit as it
+    is alone."""
+    import tgx
+
+    spec = tiny_spec(layers=1)
+    cap = 1280
+    n = 1100
+    x = inputs(spec, n + 6)
+    ref = oracle_stack(spec, cap)
+    ref.prefill(0, x[:n])
+    dec = make_decoder(ctx, spec, cap)
+    dec.prefill_runs([(0, 0, n)], x[:n])
+    for t in range(n, n + 6):
+        d = distance(dec.step(t, x[t]), ref.decode(t, x[t]))
+        assert within(d), f"step {t}: {d}"
+    dec.close()
+    lens = [1100, 70, 600, 513]  # 18 blocks, 2, 10, 9
+    xs = [inputs(spec, L + 4, name=f"row{r}") for r, L in enumerate(lens)]
+    batch = make_decoder(ctx, spec, cap, rows=len(lens))
+    batch.prefill_runs([(r, 0, L) for r, L in enumerate(lens)], np.concatenate([xr[:L] for xr, L in zip(xs, lens)]))
+    together = [batch.step_rows([tgx.Row(L + k, r) for r, L in enumerate(lens)], np.stack([xr[L + k] for xr, L in zip(xs, lens)]))
+                for k in range(4)]
+    batch.close()
+    for r, L in enumerate(lens):
+        alone = make_decoder(ctx, spec, cap)
+        alone.prefill_runs([(0, 0, L)], xs[r][:L])
+        for k in range(4):
+            got = alone.step(L + k, xs[r][L + k])
+            assert np.array_equal(got.view(np.uint32), together[k][r].view(np.uint32)), f"row {r} ({L} positions), step {k}"
+        alone.close()
+
+
 def test_spare_rows_write_no_cache_and_leave_others_alone(ctx):
     import tgx
 
