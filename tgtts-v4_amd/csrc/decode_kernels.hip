@@ -130,27 +130,28 @@ struct NormedRows : Operand<CH> {
 };
 
 // The tile's rows' scales 1 / sqrt(sum / K + eps) from their sums of squares over each SQ_COLS
-// columns, sq [B][K / SQ_COLS] (K = CH 1024: 256 CH sums a row): wave w takes tile rows 2 w and
-// 2 w + 1, lane l sums 4 l .. 4 l + 3 of each 256 in order, and the lanes' totals are added in
-// a fixed order (wave_sum). The same arithmetic for a row whatever the batch.
+// columns, sq [B][K / SQ_COLS] (K = CH 1024: 256 CH sums a row): wave w takes tile rows
+// RPW w .. RPW w + RPW - 1, lane l sums 4 l .. 4 l + 3 of each 256 in order, and the lanes'
+// totals are added in a fixed order (wave_sum). The same arithmetic for a row whatever the batch.
 template <int CH>
 struct RowSquares {
-    float4 part[2][CH];
+    static constexpr int RPW = 16 / GEMV_WAVES;  // rows to a wave
+    float4 part[RPW][CH];
 
     __device__ void load(const float* __restrict__ sq, int B, int tile) {
         const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int b = min(tile * 16 + 2 * w + h, B - 1);
+        for (int h = 0; h < RPW; ++h) {
+            const int b = min(tile * 16 + RPW * w + h, B - 1);
 #pragma unroll
             for (int c = 0; c < CH; ++c) part[h][c] = load_f4(sq + (size_t)b * (CH * 256) + c * 256 + lane * 4);
         }
     }
-    // scale[2 w + h], behind the caller's next barrier.
+    // scale[RPW w + h], behind the caller's next barrier.
     __device__ void finish(float eps, float* scale) {
         const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < RPW; ++h) {
             float t = 0.f;
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
@@ -160,7 +161,7 @@ struct RowSquares {
                 t += part[h][c].w;
             }
             const float total = wave_sum(t);
-            if (lane == 0) scale[2 * w + h] = 1.0f / sqrtf(total / (float)(CH * CHUNK_COLS) + eps);
+            if (lane == 0) scale[RPW * w + h] = 1.0f / sqrtf(total / (float)(CH * CHUNK_COLS) + eps);
         }
     }
 };
