@@ -348,7 +348,11 @@ tgx_status tgx_patch_step_create(tgx_encoder* e, tgx_lm_side* side, tgx_sampler*
 void tgx_patch_step_destroy(tgx_patch_step* p);
 /* PatchStep::run_rows (patch.rs:356-415): the rows' places (spare ones TGX_SPARE), each row's
  * patch before `cond` and `noise` ([rows][feat_dim][patch_size]) and `sampling` ([rows][2]:
- * temperature, guidance scale); returns each row's patch and stop logits [rows][2]. Waits. */
+ * temperature, guidance scale); returns each row's patch and stop logits [rows][2]. Waits.
+ * `nrows` may be fewer than the step's rows: the step runs on its program of the fewest rows that
+ * holds them (each power of two below its rows, then its rows: generator.rs:115-123), the rest
+ * spare, each row's results as on any other program. The encoder's, LM side's and sampler's own
+ * entry points take their whole batch again. */
 tgx_status tgx_patch_step_run(tgx_patch_step* p, const tgx_row* rows, int nrows, const float* cond,
                               const float* noise, const float* sampling, float* patch, float* stop_logits);
 /* Launches `times` steps back to back over what the device holds (with `advance` every placed row

@@ -337,3 +337,36 @@ def test_the_patch_step_is_the_encoder_the_lm_side_and_the_sampler_in_turn(ctx):
     step.close()
     for o in (enc, smp, side):
         o.close()
+
+
+def test_a_step_of_fewer_rows_runs_on_the_fewest_program_each_row_as_on_the_largest(ctx):
+    """Generator::step (crates/graph/src/generator.rs:115-123, 286-318): a patch step has a
+    program for each power of two below its rows and for its rows; a step of n rows runs on the
+    fewest that holds them, the rest spare, and each row comes out bit for bit as on the largest
+    beside the others, in whichever row it runs."""
+    import tgx
+    from tgx.patch import PatchStep
+    from tgx.synth import encoder_weights, sampler_weights
+
+    rows = 5  # programs of 1, 2, 4 and 5 rows
+    espec, dspec = _encoder_spec(1), _dit_spec(1)
+    enc = _encoder(ctx, rows, espec, encoder_weights(espec, FEAT))
+    smp = _sampler(ctx, rows, dspec, sampler_weights(dspec, FEAT))
+    _, _, w = _lm_weights()
+    side = _lm_side(ctx, rows, w)
+    step = PatchStep(enc, side, smp)
+    _, cond, noise, sampling = _inputs(rows, seed=16)
+    # Every run at position 0, which each run rewrites with the same keys and values.
+    full_patch, full_stop = step.run_rows([tgx.Row(0, r) for r in range(rows)], cond, noise, sampling)
+    for pick in ([3], [1, 4], [0, 2, 4], [4, 3, 2, 1, 0]):
+        patch, stop = step.run_rows([tgx.Row(0, r) for r in pick], cond[pick], noise[pick], sampling[pick])
+        for k, r in enumerate(pick):
+            assert np.array_equal(patch[k], full_patch[r]) and np.array_equal(stop[k], full_stop[r]), (pick, r)
+    # The components' own entry points take the whole batch again.
+    embedding = enc.encode(cond)
+    mu, stop = side.step_rows([tgx.Row(0, r) for r in range(rows)], embedding)
+    assert np.array_equal(stop, full_stop)
+    assert np.array_equal(smp.sample(mu, cond, noise, sampling), full_patch)
+    step.close()
+    for o in (enc, smp, side):
+        o.close()

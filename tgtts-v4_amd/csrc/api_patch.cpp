@@ -56,6 +56,8 @@ tgx_status tgx_sampler_sample(tgx_sampler* s, const float* mu, const float* cond
                               float* patch) {
     clear_error();
     if (!s || !mu || !cond || !noise || !sampling || !patch) return fail(TGX_E_ARG, "null sampler or array");
+    // The whole batch: the program of all the rows (a patch step may have run fewer).
+    TGX_TRY(sampler_use_rows(s->s, s->s->max_rows));
     TGX_TRY(sampler_set_inputs(s->s, mu, cond, noise, sampling));
     TGX_TRY(sampler_launch(s->s, 1));
     TGX_TRY(sampler_wait(s->s));
@@ -149,13 +151,17 @@ tgx_status tgx_lm_side_decoder(tgx_lm_side* s, int which, tgx_decoder** out) {
 
 tgx_status tgx_lm_side_set_rows(tgx_lm_side* s, const tgx_row* rows, int nrows, const float* enc) {
     clear_error();
-    return lm_side_set_rows(SIDE(s), rows, nrows, enc);
+    if (!s) return fail(TGX_E_ARG, "null LM side");
+    // The whole batch: the program of all the rows (a patch step may have run fewer).
+    TGX_TRY(lm_side_use_rows(s->s, s->s->max_rows));
+    return lm_side_set_rows(s->s, rows, nrows, enc);
 }
 
 tgx_status tgx_lm_side_step(tgx_lm_side* s, const tgx_row* rows, int nrows, const float* enc, float* mu, float* stop_logits) {
     clear_error();
     if (!s || !rows || !enc || !mu || !stop_logits) return fail(TGX_E_ARG, "null LM side or array");
     LmSide* p = s->s;
+    TGX_TRY(lm_side_use_rows(p, p->max_rows));
     TGX_TRY(lm_side_set_rows(p, rows, nrows, enc));
     TGX_TRY(lm_side_launch(p, 1, 0));
     TGX_TRY(lm_side_wait(p));
@@ -263,6 +269,7 @@ tgx_status tgx_encoder_load(tgx_encoder* e, const char* name, const void* data, 
 tgx_status tgx_encoder_encode(tgx_encoder* e, const float* patch, float* out) {
     clear_error();
     if (!e) return fail(TGX_E_ARG, "null encoder");
+    TGX_TRY(encoder_use_rows(e->e, e->e->max_rows));
     return encoder_encode(e->e, patch, out);
 }
 

@@ -106,6 +106,7 @@ tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     e->feat = C;
     e->frames = F;
     e->rows = patch->rows;
+    e->max_rows = patch->rows;
     e->T = T;
     e->M = patch->rows * T;
     e->M_pad = local_rows_padded(e->M);
@@ -161,7 +162,7 @@ tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
 void encoder_destroy(Encoder* e) {
     if (!e) return;
     if (e->ctx) hipStreamSynchronize(e->ctx->stream);
-    if (e->exec) hipGraphExecDestroy(e->exec);
+    destroy_programs(e->programs);
     for (auto& b : e->allocations) hipFree(b.ptr);
     if (e->ev_start) hipEventDestroy(e->ev_start);
     if (e->ev_end) hipEventDestroy(e->ev_end);
@@ -223,8 +224,13 @@ tgx_status encoder_encode(Encoder* e, const float* patch, float* out) {
     hipStream_t st = e->ctx->stream;
     const size_t len = (size_t)e->rows * e->feat * e->frames;
     TGX_HIP(hipMemcpyAsync(e->patch, patch, len * 4, hipMemcpyHostToDevice, st));
-    if (!e->exec)
+    if (!e->exec) {
         TGX_TRY(record(st, "the encoder", [&] { return encoder_enqueue(e, e->patch, e->embedding, &e->dispatches); }, &e->exec));
+        RowProgram prog;
+        prog.exec = e->exec;
+        prog.dispatches = e->dispatches;
+        e->programs[e->rows] = prog;
+    }
     TGX_HIP(hipEventRecord(e->ev_start, st));
     TGX_HIP(hipGraphLaunch(e->exec, st));
     TGX_HIP(hipEventRecord(e->ev_end, st));
@@ -236,15 +242,70 @@ tgx_status encoder_encode(Encoder* e, const float* patch, float* out) {
     return TGX_OK;
 }
 
+tgx_status encoder_use_rows(Encoder* e, int rows) {
+    if (!e) return fail(TGX_E_ARG, "null encoder");
+    if (e->pending) return fail(TGX_E_BUSY, "an encoding is under way");
+    if (rows < 1 || rows > e->max_rows)
+        return fail(TGX_E_SHAPE, std::to_string(rows) + " rows in an encoder of " + std::to_string(e->max_rows));
+    if (rows == e->rows) return TGX_OK;
+    e->rows = rows;
+    e->M = rows * e->T;
+    e->M_pad = local_rows_padded(e->M);
+    auto it = e->programs.find(rows);
+    e->exec = it == e->programs.end() ? nullptr : it->second.exec;
+    e->dispatches = it == e->programs.end() ? 0 : it->second.dispatches;
+    return TGX_OK;
+}
+
 // ---- the patch step ----
+
+std::vector<int> program_rows(int rows) {
+    std::vector<int> out;
+    for (int r = 1; r < rows; r *= 2) out.push_back(r);
+    out.push_back(rows);
+    return out;
+}
+
+int program_for(int rows, int n) {
+    for (int r : program_rows(rows))
+        if (r >= n) return r;
+    return rows;
+}
+
+namespace {
+
+// The current rows' embedding of the sampler's cond into the LM side's input, recorded if need be.
+tgx_status step_encode_program(PatchStep* p) {
+    Encoder* e = p->encoder;
+    auto it = p->encodes.find(e->rows);
+    if (it == p->encodes.end()) {
+        RowProgram prog;
+        TGX_TRY(record(p->side->ctx->stream, "the encoder",
+                       [&] { return encoder_enqueue(e, p->sampler->cond, p->side->enc, &prog.dispatches); }, &prog.exec));
+        it = p->encodes.emplace(e->rows, prog).first;
+    }
+    p->encode = it->second.exec;
+    return TGX_OK;
+}
+
+}  // namespace
+
+tgx_status patch_step_use_rows(PatchStep* p, int rows) {
+    if (!p) return fail(TGX_E_ARG, "null patch step");
+    if (p->pending) return fail(TGX_E_BUSY, "a step is under way");
+    TGX_TRY(encoder_use_rows(p->encoder, rows));
+    TGX_TRY(lm_side_use_rows(p->side, rows));
+    TGX_TRY(sampler_use_rows(p->sampler, rows));
+    return step_encode_program(p);
+}
 
 tgx_status patch_step_create(Encoder* e, LmSide* side, Sampler* s, PatchStep** out) {
     if (!e || !side || !s || !out) return fail(TGX_E_ARG, "null encoder, LM side, sampler or out");
     *out = nullptr;
     if (e->ctx != side->ctx || s->ctx != side->ctx) return fail(TGX_E_ARG, "the three are on different contexts");
-    if (e->rows != side->rows || s->rows != side->rows)
-        return fail(TGX_E_SHAPE, "an encoder of " + std::to_string(e->rows) + " rows, an LM side of " + std::to_string(side->rows) +
-                                     " and a sampler of " + std::to_string(s->rows));
+    if (e->max_rows != side->max_rows || s->max_rows != side->max_rows)
+        return fail(TGX_E_SHAPE, "an encoder of " + std::to_string(e->max_rows) + " rows, an LM side of " +
+                                     std::to_string(side->max_rows) + " and a sampler of " + std::to_string(s->max_rows));
     if (e->shape.hidden != side->encoder)
         return fail(TGX_E_SHAPE, "an encoder " + std::to_string(e->shape.hidden) + " wide for an LM side taking " +
                                      std::to_string(side->encoder));
@@ -255,8 +316,10 @@ tgx_status patch_step_create(Encoder* e, LmSide* side, Sampler* s, PatchStep** o
     p->encoder = e;
     p->side = side;
     p->sampler = s;
-    hipStream_t st = side->ctx->stream;
-    tgx_status r = record(st, "the encoder", [&] { return encoder_enqueue(e, s->cond, side->enc, nullptr); }, &p->encode);
+    // The three at the same program: the LM side's.
+    tgx_status r = encoder_use_rows(e, side->rows);
+    if (r == TGX_OK) r = sampler_use_rows(s, side->rows);
+    if (r == TGX_OK) r = step_encode_program(p);
     if (r == TGX_OK && hipEventCreate(&p->ev_start) != hipSuccess) r = fail(TGX_E_HIP, "hipEventCreate");
     if (r == TGX_OK && hipEventCreate(&p->ev_end) != hipSuccess) r = fail(TGX_E_HIP, "hipEventCreate");
     if (r != TGX_OK) {
@@ -270,7 +333,7 @@ tgx_status patch_step_create(Encoder* e, LmSide* side, Sampler* s, PatchStep** o
 void patch_step_destroy(PatchStep* p) {
     if (!p) return;
     if (p->side && p->side->ctx) hipStreamSynchronize(p->side->ctx->stream);
-    if (p->encode) hipGraphExecDestroy(p->encode);
+    destroy_programs(p->encodes);
     if (p->ev_start) hipEventDestroy(p->ev_start);
     if (p->ev_end) hipEventDestroy(p->ev_end);
     delete p;
@@ -317,13 +380,28 @@ tgx_status patch_step_run(PatchStep* p, const tgx_row* rows, int nrows, const fl
     if (p->pending) return fail(TGX_E_BUSY, "a step is under way");
     LmSide* l = p->side;
     Sampler* s = p->sampler;
-    if (nrows != l->rows) return fail(TGX_E_SHAPE, std::to_string(nrows) + " rows for a step of " + std::to_string(l->rows));
-    TGX_TRY(lm_side_set_rows(l, rows, nrows, nullptr));
-    TGX_TRY(sampler_set_inputs(s, nullptr, cond, noise, sampling));
+    if (nrows < 1 || nrows > l->max_rows)
+        return fail(TGX_E_SHAPE, std::to_string(nrows) + " rows for a step of " + std::to_string(l->max_rows));
+    const int R = program_for(l->max_rows, nrows);
+    TGX_TRY(patch_step_use_rows(p, R));
+    // The program's rows past the given ones are spare: no cache written, nothing read back.
+    const size_t len = (size_t)s->feat * s->frames;
+    std::vector<tgx_row> all(rows, rows + nrows);
+    all.resize(R, tgx_row{TGX_SPARE, 0});
+    std::vector<float> c(cond, cond + nrows * len), z(noise, noise + nrows * len), g(sampling, sampling + nrows * 2);
+    c.resize(R * len, 0.f);
+    z.resize(R * len, 0.f);
+    g.resize((size_t)R * 2, 0.f);
+    TGX_TRY(lm_side_set_rows(l, all.data(), R, nullptr));
+    TGX_TRY(sampler_set_inputs(s, nullptr, c.data(), z.data(), g.data()));
     TGX_TRY(patch_step_launch(p, 1, 0));
     TGX_TRY(patch_step_wait(p));
-    TGX_TRY(sampler_read(s, patch));
-    return lm_side_read(l, "stop_logits", stop_logits, (size_t)l->rows * 2);
+    std::vector<float> out(R * len), logits((size_t)R * 2);
+    TGX_TRY(sampler_read(s, out.data()));
+    TGX_TRY(lm_side_read(l, "stop_logits", logits.data(), logits.size()));
+    std::copy(out.begin(), out.begin() + nrows * len, patch);
+    std::copy(logits.begin(), logits.begin() + (size_t)nrows * 2, stop_logits);
+    return TGX_OK;
 }
 
 }  // namespace tgx

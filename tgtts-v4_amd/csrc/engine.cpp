@@ -154,30 +154,38 @@ tgx_status engine_step(Engine* e, const float* noise, tgx_engine_outcome* outcom
     if (!e || !noise || !outcomes || !frames || !n) return fail(TGX_E_ARG, "null engine, noise or output");
     *n = 0;
     const int S = e->slots, P = e->feat * e->frames;
-    std::vector<tgx_row> rows(S, tgx_row{TGX_SPARE, TGX_SPARE});
-    std::vector<float> cond((size_t)S * P, 0.f), sampling((size_t)S * 2, 0.f);
+    // The requests under way, a row each in slot order; the patch step runs them on its program
+    // of the fewest rows that holds them (generator.rs:286-318).
     std::vector<int> under_way;
     for (int s = 0; s < S; ++s) {
         const Request* r = e->requests[s].get();
-        if (!r || r->left <= 0) continue;
-        under_way.push_back(s);
-        rows[s] = tgx_row{r->position, (uint32_t)s};
-        std::memcpy(&cond[(size_t)s * P], r->before.data(), (size_t)P * 4);
-        sampling[2 * s] = r->temperature;
-        sampling[2 * s + 1] = r->cfg;
+        if (r && r->left > 0) under_way.push_back(s);
     }
     if (under_way.empty()) return TGX_OK;
-    std::vector<float> patch((size_t)S * P), stop((size_t)S * 2);
-    TGX_TRY(patch_step_run(e->step, rows.data(), S, cond.data(), noise, sampling.data(), patch.data(), stop.data()));
+    const int N = (int)under_way.size();
+    std::vector<tgx_row> rows(N);
+    std::vector<float> cond((size_t)N * P), noises((size_t)N * P), sampling((size_t)N * 2);
+    for (int k = 0; k < N; ++k) {
+        const int s = under_way[k];
+        const Request* r = e->requests[s].get();
+        rows[k] = tgx_row{r->position, (uint32_t)s};
+        std::memcpy(&cond[(size_t)k * P], r->before.data(), (size_t)P * 4);
+        std::memcpy(&noises[(size_t)k * P], noise + (size_t)s * P, (size_t)P * 4);
+        sampling[2 * k] = r->temperature;
+        sampling[2 * k + 1] = r->cfg;
+    }
+    std::vector<float> patch((size_t)N * P), stop((size_t)N * 2);
+    TGX_TRY(patch_step_run(e->step, rows.data(), N, cond.data(), noises.data(), sampling.data(), patch.data(), stop.data()));
     std::fill(e->last_rows.begin(), e->last_rows.end(), -1);
-    for (int s : under_way) {
+    for (int k = 0; k < N; ++k) {
+        const int s = under_way[k];
         Request& r = *e->requests[s];
-        e->last_rows[s] = s;
+        e->last_rows[s] = k;
         tgx_engine_outcome& o = outcomes[(*n)++];
         o.slot = s;
-        o.stop_logits[0] = stop[2 * s];
-        o.stop_logits[1] = stop[2 * s + 1];
-        const float* p = &patch[(size_t)s * P];
+        o.stop_logits[0] = stop[2 * k];
+        o.stop_logits[1] = stop[2 * k + 1];
+        const float* p = &patch[(size_t)k * P];
         bool finite = std::isfinite(o.stop_logits[0]) && std::isfinite(o.stop_logits[1]);
         for (int i = 0; i < P && finite; ++i) finite = std::isfinite(p[i]);
         if (!finite) {
@@ -207,7 +215,7 @@ tgx_status engine_levels(Engine* e, int slot, float* out) {
     if (!e || !out) return fail(TGX_E_ARG, "null engine or output");
     if (slot < 0 || slot >= e->slots || !e->requests[slot] || e->last_rows[slot] < 0) return no_request(slot);
     const int L = e->side->latent;
-    std::vector<float> all((size_t)e->slots * L);
+    std::vector<float> all((size_t)e->side->rows * L);  // the last step's program's rows
     TGX_TRY(lm_side_read(e->side, "levels", all.data(), all.size()));
     for (int i = 0; i < L; ++i) out[i] = std::nearbyint(all[(size_t)e->last_rows[slot] * L + i] * (float)e->side->levels);
     return TGX_OK;

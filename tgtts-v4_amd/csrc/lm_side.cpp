@@ -73,6 +73,7 @@ LinearArgs linear_args(const Linear& l, const float* x0, const float* x1, int k0
 }
 
 tgx_status side_record(LmSide* s, int advance, hipGraphExec_t* exec) {
+    *exec = nullptr;
     hipStream_t st = s->ctx->stream;
     TGX_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
     int n = 0;
@@ -91,7 +92,47 @@ tgx_status side_record(LmSide* s, int advance, hipGraphExec_t* exec) {
     return TGX_OK;
 }
 
+// The program of s->rows rows as the current one, recorded if it has not been.
+tgx_status side_program(LmSide* s) {
+    auto it = s->programs.find(s->rows);
+    if (it == s->programs.end()) {
+        RowProgram p;
+        tgx_status st = side_record(s, 0, &p.exec);
+        if (st == TGX_OK) st = side_record(s, 1, &p.advance);
+        if (st != TGX_OK) {
+            if (p.exec) hipGraphExecDestroy(p.exec);
+            return st;
+        }
+        p.dispatches = s->dispatches;
+        it = s->programs.emplace(s->rows, p).first;
+    }
+    s->exec = it->second.exec;
+    s->advance_exec = it->second.advance;
+    s->dispatches = it->second.dispatches;
+    return TGX_OK;
+}
+
 }  // namespace
+
+void destroy_programs(std::map<int, RowProgram>& programs) {
+    for (auto& [rows, p] : programs) {
+        if (p.exec) hipGraphExecDestroy(p.exec);
+        if (p.advance) hipGraphExecDestroy(p.advance);
+    }
+    programs.clear();
+}
+
+tgx_status lm_side_use_rows(LmSide* s, int rows) {
+    if (!s) return fail(TGX_E_ARG, "null LM side");
+    if (s->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (rows < 1 || rows > s->max_rows)
+        return fail(TGX_E_SHAPE, std::to_string(rows) + " rows in a batch of " + std::to_string(s->max_rows));
+    if (rows == s->rows) return TGX_OK;
+    TGX_TRY(decoder_use_rows(s->base, rows));
+    TGX_TRY(decoder_use_rows(s->residual, rows));
+    s->rows = rows;
+    return side_program(s);
+}
 
 hipError_t lm_side_enqueue(LmSide* s, int advance, DispatchTimer* timer, int* dispatches) {
     hipStream_t st = s->ctx->stream;
@@ -142,6 +183,7 @@ tgx_status lm_side_create(Context* ctx, const tgx_shape* base, const tgx_shape* 
     if ((r = decoder_create(ctx, base, batch, &s->base)) != TGX_OK) return done(r);
     if ((r = decoder_create(ctx, residual, batch, &s->residual)) != TGX_OK) return done(r);
     s->rows = batch->rows;
+    s->max_rows = batch->rows;
     s->hidden = base->hidden;
     s->encoder = heads->encoder;
     s->dit = heads->dit;
@@ -166,8 +208,7 @@ tgx_status lm_side_create(Context* ctx, const tgx_shape* base, const tgx_shape* 
     hipError_t e = hipEventCreate(&s->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&s->ev_end);
     if (e != hipSuccess) return done(fail(TGX_E_HIP, std::string("hipEventCreate: ") + hipGetErrorString(e)));
-    if ((r = side_record(s, 0, &s->exec)) != TGX_OK) return done(r);
-    if ((r = side_record(s, 1, &s->advance_exec)) != TGX_OK) return done(r);
+    if ((r = side_program(s)) != TGX_OK) return done(r);
     *out = s;
     return TGX_OK;
 }
@@ -175,8 +216,7 @@ tgx_status lm_side_create(Context* ctx, const tgx_shape* base, const tgx_shape* 
 void lm_side_destroy(LmSide* s) {
     if (!s) return;
     if (s->ctx) hipStreamSynchronize(s->ctx->stream);
-    if (s->exec) hipGraphExecDestroy(s->exec);
-    if (s->advance_exec) hipGraphExecDestroy(s->advance_exec);
+    destroy_programs(s->programs);
     for (auto& b : s->allocations) hipFree(b.ptr);
     if (s->ev_start) hipEventDestroy(s->ev_start);
     if (s->ev_end) hipEventDestroy(s->ev_end);

@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <vector>
 
 #include "heads_kernels.hpp"
@@ -16,6 +17,14 @@ namespace tgx {
 constexpr int MU_TOKENS = 2;
 constexpr int TIME_AT = MU_TOKENS;
 constexpr int COND_AT = TIME_AT + 1;
+
+// A component's recorded graphs for one row count (a program, patch.rs:98-166 keeps one per row
+// count): the step and, where it has one, the step that moves the rows on a position.
+struct RowProgram {
+    hipGraphExec_t exec = nullptr, advance = nullptr;
+    int dispatches = 0;
+};
+void destroy_programs(std::map<int, RowProgram>& programs);
 
 // schedule and euler_steps (dit.rs:44-79) in f32: the (t, dt) of each DiT evaluation.
 std::vector<float> euler_schedule(int timesteps);
@@ -31,7 +40,9 @@ struct TimeMlp {
 struct Sampler {
     Context* ctx = nullptr;
     Shape shape{};  // the DiT's stack; capacity = T
-    int feat = 0, frames = 0, timesteps = 0, rows = 0;
+    // rows: the current program's rows (1..max_rows), M and M_pad its tokens; max_rows: the
+    // rows the tensors hold.
+    int feat = 0, frames = 0, timesteps = 0, rows = 0, max_rows = 0;
     int T = 0, M = 0, M_pad = 0, o_parts = LOCAL_O_PARTS, down_parts = LOCAL_DOWN_PARTS;
     std::vector<float> step_t, step_dt;
     std::vector<DeviceBuffer> allocations;
@@ -47,7 +58,8 @@ struct Sampler {
     float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr;
     uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
     float *mu = nullptr, *cond = nullptr, *noise = nullptr, *state = nullptr, *sampling = nullptr;
-    hipGraphExec_t exec = nullptr;
+    std::map<int, RowProgram> programs;  // recorded on first launch; dropped when the times change
+    hipGraphExec_t exec = nullptr;  // the current program's
     bool exec_dirty = true;
     int dispatches = 0;
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
@@ -65,6 +77,8 @@ tgx_status sampler_load(Sampler* s, const char* name, const void* data, tgx_dtyp
 // Copies the inputs in (mu [rows][MU_TOKENS][hidden], cond / noise [rows][feat][frames],
 // sampling [rows][2]); any may be null to keep what the device holds.
 tgx_status sampler_set_inputs(Sampler* s, const float* mu, const float* cond, const float* noise, const float* sampling);
+// The program of `rows` rows (1 to the rows it was created for).
+tgx_status sampler_use_rows(Sampler* s, int rows);
 tgx_status sampler_launch(Sampler* s, int times);
 tgx_status sampler_wait(Sampler* s);
 tgx_status sampler_read(Sampler* s, float* patch);
@@ -81,7 +95,7 @@ tgx_status sampler_record(Sampler* s);
 struct Encoder {
     Context* ctx = nullptr;
     Shape shape{};  // the stack; capacity = T
-    int feat = 0, frames = 0, rows = 0;
+    int feat = 0, frames = 0, rows = 0, max_rows = 0;  // as the sampler's
     int T = 0, M = 0, M_pad = 0, o_parts = LOCAL_O_PARTS, down_parts = LOCAL_DOWN_PARTS;
     std::vector<DeviceBuffer> allocations;
     size_t device_bytes = 0;
@@ -92,7 +106,8 @@ struct Encoder {
     float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr;
     uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
     float *patch = nullptr, *embedding = nullptr;  // [rows][feat][frames], [rows][hidden]
-    hipGraphExec_t exec = nullptr;  // patch -> embedding
+    std::map<int, RowProgram> programs;  // patch -> embedding, by rows
+    hipGraphExec_t exec = nullptr;       // the current program's
     int dispatches = 0;
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
     bool pending = false;
@@ -108,6 +123,8 @@ tgx_status encoder_load(Encoder* e, const char* name, const void* data, tgx_dtyp
 hipError_t encoder_enqueue(Encoder* e, const float* patch, float* dst, int* dispatches);
 // Embeds the rows' patches (host arrays) and waits: Encoder::encode (encoder.rs:194-198).
 tgx_status encoder_encode(Encoder* e, const float* patch, float* out);
+// The program of `rows` rows (1 to the rows it was created for).
+tgx_status encoder_use_rows(Encoder* e, int rows);
 
 // The LM side: both LMs' decoders, the heads, and the tensors between them.
 struct Linear {
@@ -120,12 +137,14 @@ struct LmSide {
     Context* ctx = nullptr;
     Decoder* base = nullptr;
     Decoder* residual = nullptr;
-    int rows = 0, hidden = 0, encoder = 0, dit = 0, latent = 0, levels = 0;
+    // rows: the current program's rows (1..max_rows); max_rows: the rows the tensors hold.
+    int rows = 0, max_rows = 0, hidden = 0, encoder = 0, dit = 0, latent = 0, levels = 0;
     std::vector<DeviceBuffer> allocations;
     Linear enc_to_lm, fsq_in, fsq_out, fusion, lm_to_dit, res_to_dit, stop_proj, stop_head;
     float *enc = nullptr, *levels_out = nullptr, *lm_hidden = nullptr, *stop_hidden = nullptr;
     float *mu = nullptr, *stop_logits = nullptr;
-    hipGraphExec_t exec = nullptr, advance_exec = nullptr;
+    std::map<int, RowProgram> programs;
+    hipGraphExec_t exec = nullptr, advance_exec = nullptr;  // the current program's
     int dispatches = 0;
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
     bool pending = false, use_graph = true;
@@ -142,6 +161,8 @@ struct LmHead {
 };
 std::vector<LmHead> lm_side_heads();
 tgx_status lm_side_set_rows(LmSide* s, const tgx_row* rows, int nrows, const float* enc);
+// The program of `rows` rows for both LMs and the heads (decoder_use_rows).
+tgx_status lm_side_use_rows(LmSide* s, int rows);
 tgx_status lm_side_launch(LmSide* s, int times, int advance);
 tgx_status lm_side_wait(LmSide* s);
 tgx_status lm_side_read(LmSide* s, const char* tensor, float* out, size_t count);
@@ -155,15 +176,23 @@ struct PatchStep {
     Encoder* encoder = nullptr;
     LmSide* side = nullptr;
     Sampler* sampler = nullptr;
-    hipGraphExec_t encode = nullptr;  // the sampler's cond -> the LM side's enc
+    std::map<int, RowProgram> encodes;  // the sampler's cond -> the LM side's enc, by rows
+    hipGraphExec_t encode = nullptr;    // the current program's
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
     bool pending = false;
 };
 
 tgx_status patch_step_create(Encoder* e, LmSide* side, Sampler* s, PatchStep** out);
 void patch_step_destroy(PatchStep* p);
-// PatchStep::run_rows (patch.rs:356-415): places the rows, copies the patches before, the noise
-// and the sampling in, runs the step and waits; the patches and the stop logits out.
+// The row counts of a patch step's programs (generator.rs:115-123): each power of two below
+// `rows`, then `rows`; and the fewest of them that holds `n` rows.
+std::vector<int> program_rows(int rows);
+int program_for(int rows, int n);
+// The program of `rows` rows for the encoder, the LM side and the sampler.
+tgx_status patch_step_use_rows(PatchStep* p, int rows);
+// PatchStep::run_rows (patch.rs:356-415): on the program of the fewest rows that holds the
+// `nrows` rows (the rest spare), places the rows, copies the patches before, the noise and the
+// sampling in ([nrows][...]), runs the step and waits; the rows' patches and stop logits out.
 tgx_status patch_step_run(PatchStep* p, const tgx_row* rows, int nrows, const float* cond, const float* noise,
                           const float* sampling, float* patch, float* stop_logits);
 // `times` steps back to back over what the device holds (with `advance` every placed row moves

@@ -190,8 +190,8 @@ tgx_status prompter_create(PatchStep* step, int max_rows, Prompter** out) {
     A(&p->residual_in, R * h);
     A(&p->audio_x, R * h);
     A(&p->flags, R);
-    A(&p->enc_out, (size_t)e->rows * s->encoder);
-    A(&p->embedded, (size_t)e->rows * h);
+    A(&p->enc_out, (size_t)e->max_rows * s->encoder);
+    A(&p->embedded, (size_t)e->max_rows * h);
     if (r != TGX_OK) {
         prompter_destroy(p);
         return r;
@@ -214,6 +214,7 @@ tgx_status prompter_embed(Prompter* p, const float* patches, int n, float* out) 
     if (busy(p)) return fail(TGX_E_BUSY, "a step is under way");
     Encoder* e = p->step->encoder;
     LmSide* s = p->step->side;
+    TGX_TRY(encoder_use_rows(e, e->max_rows));  // all its rows at a time
     const int R = e->rows, C = e->feat, F = e->frames, h = p->hidden;
     hipStream_t st = s->ctx->stream;
     std::vector<float> cond((size_t)R * C * F);

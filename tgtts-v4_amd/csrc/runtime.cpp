@@ -317,6 +317,7 @@ hipError_t enqueue_step(Decoder* d, int advance, DispatchTimer* timer, int* disp
 }
 
 tgx_status record(Decoder* d, int advance, hipGraphExec_t* exec) {
+    *exec = nullptr;
     hipStream_t s = d->ctx->stream;
     TGX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int dispatches = 0;
@@ -335,12 +336,33 @@ tgx_status record(Decoder* d, int advance, hipGraphExec_t* exec) {
     return TGX_OK;
 }
 
+// The program of d->rows rows as the current one, recorded if it has not been.
+tgx_status use_program(Decoder* d) {
+    auto it = d->programs.find(d->rows);
+    if (it == d->programs.end()) {
+        Decoder::Program p;
+        tgx_status st = record(d, 0, &p.step);
+        if (st == TGX_OK) st = record(d, 1, &p.advance);
+        if (st != TGX_OK) {
+            if (p.step) hipGraphExecDestroy(p.step);
+            return st;
+        }
+        p.dispatches = d->dispatches;
+        it = d->programs.emplace(d->rows, p).first;
+    }
+    d->step_exec = it->second.step;
+    d->advance_exec = it->second.advance;
+    d->dispatches = it->second.dispatches;
+    return TGX_OK;
+}
+
 tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     const Shape& s = d->shape;
     TGX_TRY(check_batch(s, batch));
     if (decode_attention_lds(s.heads, s.kv_heads) + 4096 > d->ctx->lds_bytes)
         return fail(TGX_E_SHAPE, "the attention's LDS is past the device's " + std::to_string(d->ctx->lds_bytes));
     d->rows = batch->rows;
+    d->max_rows = batch->rows;
     d->od_rows = decode_residual_rows(batch->rows);
     d->slots = batch->slots;
     d->block_tokens = batch->block_tokens == 0 ? BLOCK_TOKENS : batch->block_tokens;
@@ -424,9 +446,7 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_HIP(hipEventCreate(&d->ev_end));
     TGX_HIP(hipEventCreateWithFlags(&d->ev_done, hipEventDisableTiming));
     TGX_HIP(hipDeviceSynchronize());
-    TGX_TRY(record(d, 0, &d->step_exec));
-    TGX_TRY(record(d, 1, &d->advance_exec));
-    return TGX_OK;
+    return use_program(d);
 }
 
 }  // namespace
@@ -490,8 +510,10 @@ void decoder_destroy(Decoder* d) {
     hipSetDevice(d->ctx->device);
     hipStreamSynchronize(d->ctx->stream);
     prefill_release(d);
-    if (d->step_exec) hipGraphExecDestroy(d->step_exec);
-    if (d->advance_exec) hipGraphExecDestroy(d->advance_exec);
+    for (auto& [rows, p] : d->programs) {
+        if (p.step) hipGraphExecDestroy(p.step);
+        if (p.advance) hipGraphExecDestroy(p.advance);
+    }
     if (d->ev_start) hipEventDestroy(d->ev_start);
     if (d->ev_end) hipEventDestroy(d->ev_end);
     if (d->ev_done) hipEventDestroy(d->ev_done);
@@ -622,6 +644,22 @@ tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {
     // The pinned buffer may not change until the copies have gone.
     TGX_HIP(hipStreamSynchronize(s));
     return TGX_OK;
+}
+
+tgx_status decoder_use_rows(Decoder* d, int rows) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
+    if (rows < 1 || rows > d->max_rows)
+        return fail(TGX_E_SHAPE, std::to_string(rows) + " rows in a batch of " + std::to_string(d->max_rows));
+    if (rows == d->rows) return TGX_OK;
+    d->rows = rows;
+    for (int i = 0; i < 2 * rows; ++i) d->placement_host[i] = TGX_SPARE;
+    d->rows_dirty = true;
+    hipStream_t s = d->ctx->stream;
+    TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+    TGX_HIP(hipMemcpyAsync(d->slot_of_row, d->placement_host + rows, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+    TGX_HIP(hipStreamSynchronize(s));
+    return use_program(d);
 }
 
 tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const float* x) {

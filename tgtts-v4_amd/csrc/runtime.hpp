@@ -5,6 +5,7 @@
 
 #include <functional>
 #include <string>
+#include <map>
 #include <vector>
 
 #include "../../include/tgx.h"
@@ -69,7 +70,9 @@ struct PrefillState {
 struct Decoder {
     Context* ctx = nullptr;
     Shape shape{};
-    int rows = 0, slots = 0, block_tokens = 64, nblocks = 0, max_blocks = 0;
+    // rows: the batch the step runs (its program, 1..max_rows); max_rows: the rows the tensors
+    // hold, the batch it was created for.
+    int rows = 0, max_rows = 0, slots = 0, block_tokens = 64, nblocks = 0, max_blocks = 0;
     std::vector<DeviceBuffer> allocations;
     size_t device_bytes = 0;
     std::vector<Layer> layers;
@@ -91,7 +94,12 @@ struct Decoder {
     bool table_dirty = true, rows_dirty = true;
     std::vector<int> slot_blocks;     // blocks each slot holds
     std::vector<uint32_t> free_list;  // blocks nobody holds
-    // the recorded step
+    // the recorded step, a program per row count run (step_exec, advance_exec: the current one's)
+    struct Program {
+        hipGraphExec_t step = nullptr, advance = nullptr;
+        int dispatches = 0;
+    };
+    std::map<int, Program> programs;
     hipGraphExec_t step_exec = nullptr, advance_exec = nullptr;
     int dispatches = 0;
     hipEvent_t ev_start = nullptr, ev_end = nullptr, ev_done = nullptr;
@@ -121,6 +129,10 @@ tgx_status decoder_create(Context* ctx, const tgx_shape* shape, const tgx_batch*
 void decoder_destroy(Decoder* dec);
 tgx_status decoder_load(Decoder* dec, const char* name, const void* data, tgx_dtype dtype, size_t count);
 tgx_status decoder_set_rows(Decoder* dec, const tgx_row* rows, int nrows, const float* x);
+// Runs the next steps at `rows` rows (1 to the rows it was created for): the program of that many
+// rows, recorded on its first use; every row spare until placed again. A row's results are the
+// same whatever the program (the kernels' batch invariance).
+tgx_status decoder_use_rows(Decoder* dec, int rows);
 // set_rows without the input: places the rows (positions, slots, blocks) alone.
 tgx_status decoder_place(Decoder* dec, const tgx_row* rows, int nrows);
 // The step's dispatches on the context's stream, reading x_in and writing out.

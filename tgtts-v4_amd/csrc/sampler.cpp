@@ -144,6 +144,7 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     smp->frames = F;
     smp->timesteps = patch->timesteps;
     smp->rows = patch->rows;
+    smp->max_rows = patch->rows;
     smp->T = T;
     smp->M = patch->rows * 2 * T;
     smp->M_pad = local_rows_padded(smp->M);
@@ -214,7 +215,7 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
 void sampler_destroy(Sampler* s) {
     if (!s) return;
     if (s->ctx) hipStreamSynchronize(s->ctx->stream);
-    if (s->exec) hipGraphExecDestroy(s->exec);
+    destroy_programs(s->programs);
     for (auto& b : s->allocations) hipFree(b.ptr);
     for (auto e : s->timer_start) hipEventDestroy(e);
     for (auto e : s->timer_stop) hipEventDestroy(e);
@@ -330,11 +331,29 @@ hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, in
     return e;
 }
 
+tgx_status sampler_use_rows(Sampler* s, int rows) {
+    if (!s) return fail(TGX_E_ARG, "null sampler");
+    if (s->pending) return fail(TGX_E_BUSY, "a sample is under way");
+    if (rows < 1 || rows > s->max_rows)
+        return fail(TGX_E_SHAPE, std::to_string(rows) + " rows in a sampler of " + std::to_string(s->max_rows));
+    if (rows == s->rows) return TGX_OK;
+    s->rows = rows;
+    s->M = rows * 2 * s->T;
+    s->M_pad = local_rows_padded(s->M);
+    auto it = s->programs.find(rows);
+    s->exec = it == s->programs.end() ? nullptr : it->second.exec;
+    s->dispatches = it == s->programs.end() ? 0 : it->second.dispatches;
+    s->exec_dirty = it == s->programs.end();
+    return TGX_OK;
+}
+
 tgx_status sampler_record(Sampler* s) {
-    if (s->exec) {
-        hipGraphExecDestroy(s->exec);
-        s->exec = nullptr;
+    auto old = s->programs.find(s->rows);
+    if (old != s->programs.end()) {
+        hipGraphExecDestroy(old->second.exec);
+        s->programs.erase(old);
     }
+    s->exec = nullptr;
     hipStream_t st = s->ctx->stream;
     TGX_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
     int n = 0;
@@ -348,9 +367,16 @@ tgx_status sampler_record(Sampler* s) {
     if (end != hipSuccess) return fail(TGX_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(end));
     hipError_t e = hipGraphInstantiate(&s->exec, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
-    if (e != hipSuccess) return fail(TGX_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    if (e != hipSuccess) {
+        s->exec = nullptr;
+        return fail(TGX_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
     s->dispatches = n;
     s->exec_dirty = false;
+    RowProgram p;
+    p.exec = s->exec;
+    p.dispatches = n;
+    s->programs[s->rows] = p;
     if ((int)s->timer_start.size() < n) {
         for (int i = (int)s->timer_start.size(); i < n; ++i) {
             hipEvent_t a = nullptr, b = nullptr;

@@ -342,14 +342,16 @@ class PatchStep:
         _open_decoders.add(self)
 
     def run_rows(self, rows: Sequence[Optional[Row]], cond, noise, sampling):
-        """PatchStep::run_rows (patch.rs:356-415): -> (patches [rows][feat_dim][patch_size],
-        stop logits [rows][2])."""
+        """PatchStep::run_rows (patch.rs:356-415): up to the step's rows, run on its program of the
+        fewest rows that holds them -> (patches [rows][feat_dim][patch_size], stop logits
+        [rows][2])."""
         P = self.sampler.patch
-        cond = np.ascontiguousarray(cond, dtype=np.float32).reshape(P.rows, P.feat_dim, P.patch_size)
-        noise = np.ascontiguousarray(noise, dtype=np.float32).reshape(P.rows, P.feat_dim, P.patch_size)
-        sampling = np.ascontiguousarray(sampling, dtype=np.float32).reshape(P.rows, 2)
+        n = len(rows)
+        cond = np.ascontiguousarray(cond, dtype=np.float32).reshape(n, P.feat_dim, P.patch_size)
+        noise = np.ascontiguousarray(noise, dtype=np.float32).reshape(n, P.feat_dim, P.patch_size)
+        sampling = np.ascontiguousarray(sampling, dtype=np.float32).reshape(n, 2)
         patch = np.empty_like(noise)
-        stop = np.empty((P.rows, 2), dtype=np.float32)
+        stop = np.empty((n, 2), dtype=np.float32)
         _check(library().tgx_patch_step_run(self._h, self.side._rows(rows), len(rows), _ptr(cond), _ptr(noise),
                                             _ptr(sampling), _ptr(patch), _ptr(stop)))
         return patch, stop
