@@ -170,14 +170,6 @@ tgx_status tgx_decoder_set_timed(tgx_decoder* dec, int timed);
  * as a profiler that follows single dispatches needs. The same kernels either way. */
 tgx_status tgx_decoder_set_graph(tgx_decoder* dec, int use_graph);
 
-/* How the attention takes a row's parts of 512 positions (attention_split.comp +
- * attention_combine.comp, whose split the reference fixes by its Tuning): -1 (the default) chooses
- * at each launch, a workgroup to each part and a second kernel to fold them when the batch gives
- * few workgroups (rows x KV heads up to 64) and a row reaches 1024 positions, else a workgroup to
- * each row taking its parts in turn; 0 never splits, 1 always does. A row's results are the same
- * bits either way. */
-tgx_status tgx_decoder_set_attention_split(tgx_decoder* dec, int mode);
-
 /* Decoder::timings (decode.rs:891-893): each dispatch's label and GPU time in the last timed step,
  * in order; *n is the number of dispatches (0 when not timed), of which `max` are written. */
 typedef struct {

@@ -163,48 +163,38 @@ def test_batch_of_64_rows_is_as_alone(ctx):
 
 
 def test_long_contexts_match_the_oracle_and_each_row_is_as_alone(ctx):
-    """The attention takes a row in parts of eight 64-position blocks (512 positions), either a
-    workgroup to the row taking its parts in turn or a workgroup to each part and a second kernel
-    folding them (attention_split.comp + attention_combine.comp): a row at 1700 positions (four
-    parts) matches the oracle step by step both ways with the same bits, and each row of a batch of
-    long and short contexts taken one way is bit for bit as it is alone taken the other."""
+    """Past 512 positions each of the attention's waves takes more than one 64-position block
+    (its turns, two at a time): a row at 1100 positions (18 blocks, three turns) matches the
+    oracle step by step, and each row of a batch of long and short contexts is bit for bit as it
+    is alone."""
     import tgx
 
     spec = tiny_spec(layers=1)
-    cap = 1792
-    n = 1700
+    cap = 1280
+    n = 1100
     x = inputs(spec, n + 6)
     ref = oracle_stack(spec, cap)
     ref.prefill(0, x[:n])
-    runs = {}
-    for mode in (0, 1):
-        dec = make_decoder(ctx, spec, cap)
-        dec.set_attention_split(mode)
-        dec.prefill_runs([(0, 0, n)], x[:n])
-        runs[mode] = [dec.step(t, x[t]) for t in range(n, n + 6)]
-        dec.close()
-    for k, t in enumerate(range(n, n + 6)):
-        d = distance(runs[0][k], ref.decode(t, x[t]))
+    dec = make_decoder(ctx, spec, cap)
+    dec.prefill_runs([(0, 0, n)], x[:n])
+    for t in range(n, n + 6):
+        d = distance(dec.step(t, x[t]), ref.decode(t, x[t]))
         assert within(d), f"step {t}: {d}"
-        assert np.array_equal(runs[0][k].view(np.uint32), runs[1][k].view(np.uint32)), f"step {t}: split differs"
-    lens = [1700, 70, 600, 513]  # 27 blocks (four parts), 2 (one), 10 (two), 9 (two)
+    dec.close()
+    lens = [1100, 70, 600, 513]  # 18 blocks, 2, 10, 9
     xs = [inputs(spec, L + 4, name=f"row{r}") for r, L in enumerate(lens)]
-    for batch_mode, alone_mode in ((0, 1), (1, 0)):
-        batch = make_decoder(ctx, spec, cap, rows=len(lens))
-        batch.set_attention_split(batch_mode)
-        batch.prefill_runs([(r, 0, L) for r, L in enumerate(lens)], np.concatenate([xr[:L] for xr, L in zip(xs, lens)]))
-        together = [batch.step_rows([tgx.Row(L + k, r) for r, L in enumerate(lens)],
-                                    np.stack([xr[L + k] for xr, L in zip(xs, lens)])) for k in range(4)]
-        batch.close()
-        for r, L in enumerate(lens):
-            alone = make_decoder(ctx, spec, cap)
-            alone.set_attention_split(alone_mode)
-            alone.prefill_runs([(0, 0, L)], xs[r][:L])
-            for k in range(4):
-                got = alone.step(L + k, xs[r][L + k])
-                assert np.array_equal(got.view(np.uint32), together[k][r].view(np.uint32)), \
-                    f"row {r} ({L} positions), step {k}, batch split {batch_mode}"
-            alone.close()
+    batch = make_decoder(ctx, spec, cap, rows=len(lens))
+    batch.prefill_runs([(r, 0, L) for r, L in enumerate(lens)], np.concatenate([xr[:L] for xr, L in zip(xs, lens)]))
+    together = [batch.step_rows([tgx.Row(L + k, r) for r, L in enumerate(lens)], np.stack([xr[L + k] for xr, L in zip(xs, lens)]))
+                for k in range(4)]
+    batch.close()
+    for r, L in enumerate(lens):
+        alone = make_decoder(ctx, spec, cap)
+        alone.prefill_runs([(0, 0, L)], xs[r][:L])
+        for k in range(4):
+            got = alone.step(L + k, xs[r][L + k])
+            assert np.array_equal(got.view(np.uint32), together[k][r].view(np.uint32)), f"row {r} ({L} positions), step {k}"
+        alone.close()
 
 
 def test_spare_rows_write_no_cache_and_leave_others_alone(ctx):

@@ -160,15 +160,6 @@ tgx_status tgx_decoder_set_graph(tgx_decoder* dec, int use_graph) {
     return TGX_OK;
 }
 
-tgx_status tgx_decoder_set_attention_split(tgx_decoder* dec, int mode) {
-    clear_error();
-    if (!dec) return fail(TGX_E_ARG, "null decoder");
-    if (dec->dec->pending) return fail(TGX_E_BUSY, "a step is under way");
-    if (mode < -1 || mode > 1) return fail(TGX_E_ARG, "attention split mode " + std::to_string(mode) + " (-1, 0 or 1)");
-    dec->dec->split_mode = mode;
-    return TGX_OK;
-}
-
 tgx_status tgx_decoder_timings(tgx_decoder* dec, int max, tgx_timing* out, int* n) {
     clear_error();
     return decoder_timings(DEC(dec), max, out, n);

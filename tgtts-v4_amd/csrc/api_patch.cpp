@@ -226,7 +226,6 @@ tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times) 
         TGX_TRY(sampler_wait(s));
     }
     hipStream_t st = l->ctx->stream;
-    TGX_TRY(lm_side_use_split_for(l, times));
     TGX_TRY(sync_slots(l->base));
     TGX_TRY(sync_slots(l->residual));
     const size_t mu_bytes = (size_t)l->rows * 2 * l->dit * 4;
@@ -238,8 +237,6 @@ tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times) 
     }
     TGX_HIP(hipEventRecord(l->ev_end, st));
     l->pending = true;
-    decoder_advanced(l->base, times);
-    decoder_advanced(l->residual, times);
     return TGX_OK;
 }
 

@@ -432,90 +432,82 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
 }
 
 // ---------------------------------------------------------------------------------------------
-// The decode attention over a row's slot's positions 0..pos, for the `group` query heads KV head
-// kv serves, in parts of ATTN_WAVES 64-position blocks (512 positions): in a part each wave takes
-// a block with an online softmax, and the waves are joined in wave order into the part's maximum,
-// sum and unnormalised output for each (head, dimension); the parts are folded in part order into
-// the row's. Either one workgroup to a (KV head, row) takes every part in turn (attention_decode),
-// or one to a part (attention_parts) leaves each part's join in a.attn_parts and attention_join
-// folds them: the same arithmetic in the same order, so that a row's result is the same bits
-// whichever runs, and so whatever rows run beside it (attention_split.comp:52-111 +
-// attention_combine.comp:29-57).
+// attention_decode: workgroup (kv, b) attends the `group` query heads KV head kv serves of row b
+// over its slot's positions 0..pos; wave w takes blocks w, w + 8, ... (its turns) with an online
+// softmax, two turns' keys and values in flight at once.
 // Per block, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in bf16 straight
-// from the registers S^T left it in. Two memory round trips before the first product: the row's
-// position, the waves' cache blocks (from the row's copy of its slot's table) and q together, then
-// the blocks' keys and values.
+// from the registers S^T left it in.
+// Two memory round trips before the first product: the row's position, the cache blocks of the
+// wave's turns (lane j: block w + 8 j, from the row's copy of its slot's table) and q together,
+// then the first two turns' keys and values.
 
-struct Joined {
-    float M, L, O;
-};
-
-// The part's join for output (hh, d) from the waves' states in LDS, and the fold of a part into a
-// row's running join; every product and sum rounded on its own (no contraction), so that each
-// kernel's copy of them gives the same bits.
-__device__ __forceinline__ Joined join_waves(const float (*sm_m)[16], const float (*sm_l)[16], const float* attn_lds, int group,
-                                             int hh, int d) {
-#pragma clang fp contract(off)
-    float M = -INFINITY;
-    for (int j = 0; j < ATTN_WAVES; ++j) M = fmaxf(M, sm_m[j][hh]);
-    float L = 0.f, O = 0.f;
-    for (int j = 0; j < ATTN_WAVES; ++j) {
-        const float f = sm_l[j][hh] > 0.f ? __builtin_amdgcn_exp2f(sm_m[j][hh] - M) : 0.f;
-        L = L + sm_l[j][hh] * f;
-        O = O + attn_lds[(j * group + hh) * (HEAD_DIM + 1) + d] * f;
-    }
-    return Joined{M, L, O};
-}
-
-__device__ __forceinline__ void fold(Joined& row, const Joined& part) {
-#pragma clang fp contract(off)
-    const float M = fmaxf(row.M, part.M);
-    const float fr = row.L > 0.f ? __builtin_amdgcn_exp2f(row.M - M) : 0.f;
-    const float fp = part.L > 0.f ? __builtin_amdgcn_exp2f(part.M - M) : 0.f;
-    row.L = row.L * fr + part.L * fp;
-    row.O = row.O * fr + part.O * fp;
-    row.M = M;
-}
-
-// A block's keys and values, and whether the wave has the block. Without it (past the row's, or
-// none in the slot there) the same 1 KiB at the pool's start is read 16 times over instead, from
-// the caches: the loads are made either way, so that the waits for them can be counted exactly (a
-// load under a branch makes the compiler wait for every load before its first use).
-struct Block {
-    uint4 k[8], v[8];
-};
-
-__device__ __forceinline__ void fetch_block(const LayerArgs& l, int KV, int kv, uint32_t block, bool real, Block& f) {
-    const int lane = threadIdx.x % WAVE;
-    const uint16_t* kt = real ? l.kv + ((size_t)block * KV + kv) * 2 * KV_TILE : l.kv;
-    const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0;
+__global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
+    extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
+    __shared__ float sm_m[ATTN_WAVES][16];
+    __shared__ float sm_l[ATTN_WAVES][16];
+    const int kv = blockIdx.x, b = blockIdx.y;
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int H = a.heads, KV = a.kv_heads, group = H / KV;
+    const int h = lane % 16;
+    const uint32_t pos = a.positions[b];
+    const uint32_t turn_block =
+        a.row_table[(uint32_t)b * (uint32_t)a.max_blocks + (uint32_t)min(w + ATTN_WAVES * lane, a.max_blocks - 1)];
+    // Columns past the group read its last head again; nothing reads what they give.
+    uint4 qf[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f.k[i] = load16(kt + i * stride + lane * 8);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f.v[i] = load16(kt + vt + i * stride + lane * 8);
-}
+    for (int ds = 0; ds < 2; ++ds) qf[ds] = load16(l.q + ((size_t)b * H + kv * group + min(h, group - 1)) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
+    all_issued();
+    if (pos >= (uint32_t)a.capacity) return;  // a spare row
+    const int blocks = (int)(pos / BLOCK_TOKENS) + 1;
 
-// Part `part`: wave w's softmax over its block (ATTN_WAVES part + w) when it has it, its state
-// into LDS for the join, behind a barrier.
-__device__ __forceinline__ void part_states(const DecodeArgs& a, int group, const uint4 (&qf)[2], const Block& f, bool real,
-                                            int part, uint32_t pos, float* attn_lds, float (*sm_m)[16], float (*sm_l)[16]) {
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, h = lane % 16;
+    // Turn j's block, and whether the wave has it (the slot may hold no block there).
+    auto block_of_turn = [&](int j) { return (uint32_t)__builtin_amdgcn_readlane((int)turn_block, min(j, WAVE - 1)); };
+    auto has = [&](int j) { return w + ATTN_WAVES * j < blocks && block_of_turn(j) < (uint32_t)a.nblocks; };
+    // Turn j's keys and values. Without the turn (`real` false) the same 1 KiB at the pool's start
+    // is read 16 times over instead, from the caches: the loads are made either way, so that the
+    // waits for them can be counted exactly (a load under a branch makes the compiler wait for
+    // every load before its first use).
+    auto fetch = [&](int j, bool real, uint4 (&k)[8], uint4 (&v)[8]) {
+        const uint16_t* kt = real ? l.kv + ((size_t)block_of_turn(j) * KV + kv) * 2 * KV_TILE : l.kv;
+        const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) k[i] = load16(kt + i * stride + lane * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + lane * 8);
+    };
     OnlineSoftmax sm;
-    if (real) {
+    const float scale_log2 = log2_scale(a.scale);
+    // S^T = K Q^T for a turn's block, then its softmax step (masked only in the block holding
+    // the position).
+    auto take = [&](const uint4 (&k)[8], const uint4 (&v)[8], int j) __attribute__((always_inline)) {
         f32x4 s[4];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
             s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(f.k[pt * 2 + ds], qf[ds], s[pt]);
+            for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(k[pt * 2 + ds], qf[ds], s[pt]);
         }
-        const uint32_t p0 = (uint32_t)(part * ATTN_WAVES + w) * BLOCK_TOKENS;
-        const float scale_log2 = log2_scale(a.scale);
-        // Masked only in the block holding the position.
+        const uint32_t p0 = (uint32_t)(w + ATTN_WAVES * j) * BLOCK_TOKENS;
         if (p0 + BLOCK_TOKENS - 1 <= pos)
-            sm.block<false>(s, f.v, p0, pos, scale_log2);
+            sm.block<false>(s, v, p0, pos, scale_log2);
         else
-            sm.block<true>(s, f.v, p0, pos, scale_log2);
+            sm.block<true>(s, v, p0, pos, scale_log2);
+    };
+    // Two buffers: the first two turns straight (every context up to 16 blocks), then the rest
+    // two at a time, each pair's loads issued once the last pair is taken.
+    uint4 ka[8], va[8], kb[8], vb[8];
+    const bool t0 = has(0), t1 = has(1);
+    fetch(0, t0, ka, va);
+    fetch(1, t1, kb, vb);
+    if (t0) take(ka, va, 0);
+    if (t1) take(kb, vb, 1);
+    for (int j = 2; t1 && has(j); j += 2) {
+        const bool next = has(j + 1);
+        fetch(j, true, ka, va);
+        fetch(j + 1, next, kb, vb);
+        take(ka, va, j);
+        if (!next) break;
+        take(kb, vb, j + 1);
     }
     if (lane < 16) {
         sm_m[w][h] = sm.m;
@@ -528,142 +520,18 @@ __device__ __forceinline__ void part_states(const DecodeArgs& a, int group, cons
             for (int i = 0; i < 4; ++i) attn_lds[(w * group + h) * (HEAD_DIM + 1) + dt * 16 + (lane / 16) * 4 + i] = sm.o[dt][i];
     }
     __syncthreads();
-}
-
-// Row b's q for KV head kv's query heads as the MFMA's B operand; columns past the group read its
-// last head again (nothing reads what they give).
-__device__ __forceinline__ void load_q(const DecodeArgs& a, const LayerArgs& l, int kv, int b, uint4 (&qf)[2]) {
-    const int lane = threadIdx.x % WAVE, group = a.heads / a.kv_heads;
-#pragma unroll
-    for (int ds = 0; ds < 2; ++ds)
-        qf[ds] = load16(l.q + ((size_t)b * a.heads + kv * group + min(lane % 16, group - 1)) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
-}
-
-// The outputs a thread joins: group * 64 of them over the workgroup (group up to 16).
-constexpr int ATTN_OUTS = 2;
-static_assert(ATTN_OUTS * ATTN_THREADS >= 16 * HEAD_DIM, "a thread's outputs");
-
-// attention_decode: workgroup (kv, b), every part of row b in turn, the next part's keys and values
-// in flight while one is taken. Lane j of wave w holds block w + ATTN_WAVES j of the row (its block
-// of part j).
-__global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
-    extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
-    __shared__ float sm_m[ATTN_WAVES][16];
-    __shared__ float sm_l[ATTN_WAVES][16];
-    const int kv = blockIdx.x, b = blockIdx.y;
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int KV = a.kv_heads, group = a.heads / KV;
-    const uint32_t pos = a.positions[b];
-    const uint32_t part_block =
-        a.row_table[(uint32_t)b * (uint32_t)a.max_blocks + (uint32_t)min(w + ATTN_WAVES * lane, a.max_blocks - 1)];
-    uint4 qf[2];
-    load_q(a, l, kv, b, qf);
-    all_issued();
-    if (pos >= (uint32_t)a.capacity) return;  // a spare row
-    const int blocks = (int)(pos / BLOCK_TOKENS) + 1;
-    const int parts = (blocks + ATTN_WAVES - 1) / ATTN_WAVES;
-    auto block_of = [&](int p) { return (uint32_t)__builtin_amdgcn_readlane((int)part_block, min(p, WAVE - 1)); };
-    auto has = [&](int p) { return w + ATTN_WAVES * p < blocks && block_of(p) < (uint32_t)a.nblocks; };
-    Joined row[ATTN_OUTS];
-#pragma unroll
-    for (int k = 0; k < ATTN_OUTS; ++k) row[k] = Joined{-INFINITY, 0.f, 0.f};
-    auto take = [&](const Block& f, int p) __attribute__((always_inline)) {
-        part_states(a, group, qf, f, has(p), p, pos, attn_lds, sm_m, sm_l);
-#pragma unroll
-        for (int k = 0; k < ATTN_OUTS; ++k) {
-            const int idx = threadIdx.x + k * ATTN_THREADS;
-            if (idx < group * HEAD_DIM) fold(row[k], join_waves(sm_m, sm_l, attn_lds, group, idx / HEAD_DIM, idx % HEAD_DIM));
-        }
-        __syncthreads();  // the LDS is the next part's
-    };
-    // Two buffers: the first two parts straight (every context up to 16 blocks), then the rest two
-    // at a time, each pair's loads issued once the last pair is taken.
-    Block fa, fb;
-    fetch_block(l, KV, kv, block_of(0), has(0), fa);
-    fetch_block(l, KV, kv, block_of(1), has(1), fb);
-    take(fa, 0);
-    if (parts > 1) take(fb, 1);
-    for (int p = 2; p < parts; p += 2) {
-        fetch_block(l, KV, kv, block_of(p), has(p), fa);
-        fetch_block(l, KV, kv, block_of(p + 1), has(p + 1), fb);
-        take(fa, p);
-        if (p + 1 < parts) take(fb, p + 1);
-    }
-#pragma unroll
-    for (int k = 0; k < ATTN_OUTS; ++k) {
-        const int idx = threadIdx.x + k * ATTN_THREADS;
-        if (idx < group * HEAD_DIM)
-            l.attended[operand_index(b, kv * group * HEAD_DIM + idx, a.rows)] = (uint16_t)bf16_bits(row[k].O / row[k].L);
-    }
-}
-
-// attention_parts: workgroup (kv, b, part), one part of row b. A row of one part is finished here;
-// past one, the part's join goes to a.attn_parts, [rows][kv_heads][max_parts][group][64 outputs,
-// maximum, sum], for attention_join.
-constexpr int PART_STRIDE = HEAD_DIM + 2;
-
-__global__ void __launch_bounds__(ATTN_THREADS) attention_parts(DecodeArgs a, LayerArgs l) {
-    extern __shared__ float attn_lds[];
-    __shared__ float sm_m[ATTN_WAVES][16];
-    __shared__ float sm_l[ATTN_WAVES][16];
-    const int kv = blockIdx.x, b = blockIdx.y, part = blockIdx.z;
-    const int w = threadIdx.x / WAVE;
-    const int KV = a.kv_heads, group = a.heads / KV;
-    const uint32_t pos = a.positions[b];
-    const int bi = part * ATTN_WAVES + w;
-    const uint32_t block = a.row_table[(uint32_t)b * (uint32_t)a.max_blocks + (uint32_t)min(bi, a.max_blocks - 1)];
-    uint4 qf[2];
-    load_q(a, l, kv, b, qf);
-    all_issued();
-    if (pos >= (uint32_t)a.capacity) return;
-    const int blocks = (int)(pos / BLOCK_TOKENS) + 1;
-    const int parts = (blocks + ATTN_WAVES - 1) / ATTN_WAVES;
-    if (part >= parts) return;
-    const bool real = bi < blocks && block < (uint32_t)a.nblocks;
-    Block f;
-    fetch_block(l, KV, kv, block, real, f);
-    part_states(a, group, qf, f, real, part, pos, attn_lds, sm_m, sm_l);
-    float* mine = a.attn_parts + (((size_t)b * KV + kv) * a.max_parts + part) * group * PART_STRIDE;
-#pragma unroll
-    for (int k = 0; k < ATTN_OUTS; ++k) {
-        const int idx = threadIdx.x + k * ATTN_THREADS;
-        if (idx >= group * HEAD_DIM) continue;
+    // The waves joined in order (wave 0 holds block 0, so M is finite).
+    for (int idx = threadIdx.x; idx < group * HEAD_DIM; idx += ATTN_THREADS) {
         const int hh = idx / HEAD_DIM, d = idx % HEAD_DIM;
-        const Joined j = join_waves(sm_m, sm_l, attn_lds, group, hh, d);
-        if (parts == 1) {
-            Joined row{-INFINITY, 0.f, 0.f};
-            fold(row, j);
-            l.attended[operand_index(b, kv * group * HEAD_DIM + idx, a.rows)] = (uint16_t)bf16_bits(row.O / row.L);
-        } else {
-            mine[hh * PART_STRIDE + d] = j.O;
-            if (d == 0) {
-                mine[hh * PART_STRIDE + HEAD_DIM] = j.M;
-                mine[hh * PART_STRIDE + HEAD_DIM + 1] = j.L;
-            }
+        float M = -INFINITY;
+        for (int j = 0; j < ATTN_WAVES; ++j) M = fmaxf(M, sm_m[j][hh]);
+        float L = 0.f, O = 0.f;
+        for (int j = 0; j < ATTN_WAVES; ++j) {
+            const float f = sm_l[j][hh] > 0.f ? __builtin_amdgcn_exp2f(sm_m[j][hh] - M) : 0.f;
+            L += sm_l[j][hh] * f;
+            O += attn_lds[(j * group + hh) * (HEAD_DIM + 1) + d] * f;
         }
-    }
-}
-
-// attention_join: workgroup (kv, b): row b's parts folded in part order, when it has more than one.
-__global__ void __launch_bounds__(ATTN_THREADS) attention_join(DecodeArgs a, LayerArgs l) {
-    const int kv = blockIdx.x, b = blockIdx.y;
-    const int KV = a.kv_heads, group = a.heads / KV;
-    const uint32_t pos = a.positions[b];
-    if (pos >= (uint32_t)a.capacity) return;
-    const int parts = ((int)(pos / BLOCK_TOKENS) + ATTN_WAVES) / ATTN_WAVES;
-    if (parts <= 1) return;
-    const float* all = a.attn_parts + ((size_t)b * KV + kv) * a.max_parts * group * PART_STRIDE;
-#pragma unroll
-    for (int k = 0; k < ATTN_OUTS; ++k) {
-        const int idx = threadIdx.x + k * ATTN_THREADS;
-        if (idx >= group * HEAD_DIM) continue;
-        const int hh = idx / HEAD_DIM, d = idx % HEAD_DIM;
-        Joined row{-INFINITY, 0.f, 0.f};
-        for (int p = 0; p < parts; ++p) {
-            const float* pr = all + ((size_t)p * group + hh) * PART_STRIDE;
-            fold(row, Joined{pr[HEAD_DIM], pr[HEAD_DIM + 1], pr[d]});
-        }
-        l.attended[operand_index(b, kv * group * HEAD_DIM + idx, a.rows)] = (uint16_t)bf16_bits(row.O / row.L);
+        l.attended[operand_index(b, (kv * group + hh) * HEAD_DIM + d, a.rows)] = (uint16_t)bf16_bits(O / L);
     }
 }
 
@@ -749,14 +617,7 @@ hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const Re
         dispatch("gemv_qkv_rope", by_chunks<PickQkvNormed>(hidden_chunks), dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
     else
         dispatch("gemv_qkv_rope", by_chunks<PickQkv>(hidden_chunks), dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
-    if (a.split) {
-        dispatch("attention_parts", attention_parts, dim3(a.kv_heads, a.rows, a.max_parts), dim3(ATTN_THREADS), attention_lds(a),
-                 stream, timer, a, l);
-        dispatch("attention_join", attention_join, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), 0, stream, timer, a, l);
-    } else {
-        dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), attention_lds(a), stream,
-                 timer, a, l);
-    }
+    dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), attention_lds(a), stream, timer, a, l);
     hipError_t e = residual("o_proj", a, o, stream, timer);
     if (e != hipSuccess) return e;
     // Past one tile a workgroup takes two or four, reading the strips' weights once for them (for a
@@ -782,17 +643,12 @@ int decode_max_k() { return MAX_CHUNKS * CHUNK_COLS; }
 int decode_max_capacity() { return ATTN_WAVES * WAVE * BLOCK_TOKENS; }
 
 hipError_t decode_prepare(size_t device_lds) {
-    for (const void* kernel : {(const void*)attention_decode, (const void*)attention_parts}) {
-        hipFuncAttributes attr{};
-        hipError_t e = hipFuncGetAttributes(&attr, kernel);
-        if (e != hipSuccess) return e;
-        e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(device_lds - attr.sharedSizeBytes));
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
+    hipFuncAttributes attr{};
+    hipError_t e = hipFuncGetAttributes(&attr, (const void*)attention_decode);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void*)attention_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)(device_lds - attr.sharedSizeBytes));
 }
-
-int decode_attention_parts(int max_blocks) { return (max_blocks + ATTN_WAVES - 1) / ATTN_WAVES; }
 
 size_t decode_attention_lds(int heads, int kv_heads) { return (size_t)ATTN_WAVES * (heads / kv_heads) * (HEAD_DIM + 1) * 4; }
 

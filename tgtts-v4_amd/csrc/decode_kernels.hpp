@@ -24,12 +24,6 @@ struct DecodeArgs {
     const uint32_t* row_table;  // [rows][max_blocks]: each row's slot's table row (UINT32_MAX for a spare row)
     const float* cos;           // [capacity][32]
     const float* sin;
-    // The attention in parts of 512 positions (decode_attention_parts of max_blocks): with split,
-    // a workgroup to each part and a second kernel that folds a row's parts, through attn_parts
-    // [rows][kv_heads][max_parts][group][66]; else a workgroup to each row takes its parts in turn.
-    // The same bits either way.
-    int split, max_parts;
-    float* attn_parts;
 };
 
 // One layer's tensors. A norm's input comes as the f32 rows and, past layer 0, also as the rows
@@ -88,8 +82,6 @@ int decode_tiles(int rows);
 int decode_max_k();
 // The longest capacity the attention takes: a lane to each block a wave reads.
 int decode_max_capacity();
-// The parts of up to 512 positions (eight 64-position blocks) the attention takes a row in.
-int decode_attention_parts(int max_blocks);
 size_t decode_attention_lds(int heads, int kv_heads);
 // Lets the attention take up to `device_lds` bytes of LDS per workgroup.
 hipError_t decode_prepare(size_t device_lds);

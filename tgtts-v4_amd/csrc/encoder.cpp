@@ -348,7 +348,6 @@ tgx_status patch_step_launch(PatchStep* p, int times, int advance) {
     TGX_TRY(sampler_prepare(s));
     if (s->exec_dirty) TGX_TRY(sampler_record(s));
     hipStream_t st = l->ctx->stream;
-    TGX_TRY(lm_side_use_split_for(l, advance ? times : 1));
     TGX_TRY(sync_slots(l->base));
     TGX_TRY(sync_slots(l->residual));
     const size_t mu_bytes = (size_t)l->rows * 2 * l->dit * 4;
@@ -363,10 +362,6 @@ tgx_status patch_step_launch(PatchStep* p, int times, int advance) {
     }
     TGX_HIP(hipEventRecord(p->ev_end, st));
     p->pending = true;
-    if (advance) {
-        decoder_advanced(l->base, times);
-        decoder_advanced(l->residual, times);
-    }
     return TGX_OK;
 }
 

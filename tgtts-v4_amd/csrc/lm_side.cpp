@@ -94,8 +94,7 @@ tgx_status side_record(LmSide* s, int advance, hipGraphExec_t* exec) {
 
 // The program of s->rows rows as the current one, recorded if it has not been.
 tgx_status side_program(LmSide* s) {
-    const int key = program_key(s->rows, s->split);
-    auto it = s->programs.find(key);
+    auto it = s->programs.find(s->rows);
     if (it == s->programs.end()) {
         RowProgram p;
         tgx_status st = side_record(s, 0, &p.exec);
@@ -105,7 +104,7 @@ tgx_status side_program(LmSide* s) {
             return st;
         }
         p.dispatches = s->dispatches;
-        it = s->programs.emplace(key, p).first;
+        it = s->programs.emplace(s->rows, p).first;
     }
     s->exec = it->second.exec;
     s->advance_exec = it->second.advance;
@@ -132,17 +131,6 @@ tgx_status lm_side_use_rows(LmSide* s, int rows) {
     TGX_TRY(decoder_use_rows(s->base, rows));
     TGX_TRY(decoder_use_rows(s->residual, rows));
     s->rows = rows;
-    return side_program(s);
-}
-
-tgx_status lm_side_use_split_for(LmSide* s, int steps) {
-    if (!s) return fail(TGX_E_ARG, "null LM side");
-    if (s->pending) return fail(TGX_E_BUSY, "a step is under way");
-    const bool split = decoder_wants_split(s->base, steps);
-    if (split == s->split) return TGX_OK;
-    TGX_TRY(decoder_use_split(s->base, split));
-    TGX_TRY(decoder_use_split(s->residual, split));
-    s->split = split;
     return side_program(s);
 }
 
@@ -293,7 +281,6 @@ tgx_status lm_side_launch(LmSide* s, int times, int advance) {
     if (s->pending || s->base->pending || s->residual->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (times <= 0) return fail(TGX_E_ARG, "times");
     hipStream_t st = s->ctx->stream;
-    TGX_TRY(lm_side_use_split_for(s, advance ? times : 1));
     TGX_TRY(sync_slots(s->base));
     TGX_TRY(sync_slots(s->residual));
     TGX_HIP(hipEventRecord(s->ev_start, st));
@@ -307,10 +294,6 @@ tgx_status lm_side_launch(LmSide* s, int times, int advance) {
     }
     TGX_HIP(hipEventRecord(s->ev_end, st));
     s->pending = true;
-    if (advance) {
-        decoder_advanced(s->base, times);
-        decoder_advanced(s->residual, times);
-    }
     return TGX_OK;
 }
 

@@ -139,7 +139,6 @@ struct LmSide {
     Decoder* residual = nullptr;
     // rows: the current program's rows (1..max_rows); max_rows: the rows the tensors hold.
     int rows = 0, max_rows = 0, hidden = 0, encoder = 0, dit = 0, latent = 0, levels = 0;
-    bool split = false;  // the LMs' attention split (Decoder::split)
     std::vector<DeviceBuffer> allocations;
     Linear enc_to_lm, fsq_in, fsq_out, fusion, lm_to_dit, res_to_dit, stop_proj, stop_head;
     float *enc = nullptr, *levels_out = nullptr, *lm_hidden = nullptr, *stop_hidden = nullptr;
@@ -164,9 +163,6 @@ std::vector<LmHead> lm_side_heads();
 tgx_status lm_side_set_rows(LmSide* s, const tgx_row* rows, int nrows, const float* enc);
 // The program of `rows` rows for both LMs and the heads (decoder_use_rows).
 tgx_status lm_side_use_rows(LmSide* s, int rows);
-// The program whose LMs' attention is split or not (decoder_use_split), as a launch of `steps`
-// steps wants it (decoder_wants_split of the base LM's places).
-tgx_status lm_side_use_split_for(LmSide* s, int steps);
 tgx_status lm_side_launch(LmSide* s, int times, int advance);
 tgx_status lm_side_wait(LmSide* s);
 tgx_status lm_side_read(LmSide* s, const char* tensor, float* out, size_t count);

@@ -219,9 +219,6 @@ DecodeArgs Decoder::args() const {
     a.slots = slot_of_row;
     a.table = table;
     a.row_table = row_table;
-    a.split = split ? 1 : 0;
-    a.max_parts = decode_attention_parts(max_blocks);
-    a.attn_parts = attn_parts;
     a.cos = cos;
     a.sin = sin;
     return a;
@@ -308,7 +305,7 @@ hipError_t enqueue_step(Decoder* d, int advance, DispatchTimer* timer, int* disp
     for (int l = 0; l < d->shape.layers && err == hipSuccess; ++l) {
         // layer 0 reads x_in, which stays as written
         err = launch_decode_layer(a, d->layer_args(l), d->o_args(l), d->down_args(l), s, timer);
-        n += a.split ? 6 : 5;
+        n += 5;
     }
     const float* x = d->shape.layers > 0 ? d->h_a : d->x_in;
     if (err == hipSuccess) {
@@ -341,8 +338,7 @@ tgx_status record(Decoder* d, int advance, hipGraphExec_t* exec) {
 
 // The program of d->rows rows as the current one, recorded if it has not been.
 tgx_status use_program(Decoder* d) {
-    const int key = program_key(d->rows, d->split);
-    auto it = d->programs.find(key);
+    auto it = d->programs.find(d->rows);
     if (it == d->programs.end()) {
         Decoder::Program p;
         tgx_status st = record(d, 0, &p.step);
@@ -352,7 +348,7 @@ tgx_status use_program(Decoder* d) {
             return st;
         }
         p.dispatches = d->dispatches;
-        it = d->programs.emplace(key, p).first;
+        it = d->programs.emplace(d->rows, p).first;
     }
     d->step_exec = it->second.step;
     d->advance_exec = it->second.advance;
@@ -402,7 +398,6 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_TRY(alloc(d, &d->slot_of_row, (size_t)R));
     TGX_TRY(alloc(d, &d->table, (size_t)d->slots * d->max_blocks));
     TGX_TRY(alloc(d, &d->row_table, (size_t)R * d->max_blocks));
-    TGX_TRY(alloc(d, &d->attn_parts, (size_t)R * KV * decode_attention_parts(d->max_blocks) * (H / KV) * (HEAD_DIM + 2)));
     TGX_TRY(alloc(d, &d->cos, (size_t)s.capacity * HEAD_DIM / 2));
     TGX_TRY(alloc(d, &d->sin, (size_t)s.capacity * HEAD_DIM / 2));
     // Norm gains start at one, so that an unloaded stack still runs finite.
@@ -651,38 +646,6 @@ tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {
     return TGX_OK;
 }
 
-int program_key(int rows, bool split) { return rows * 2 + (split ? 1 : 0); }
-
-// From this position a row has three parts or more, and unless the batch fills the CUs already a
-// workgroup to each part (and a second kernel to fold them) beats one to each row taking them in
-// turn (measured at 1 to 64 rows: 25.2 against 22.9 us a layer at one row from 1024 positions,
-// 34.1 against 24.3 from 3072; 37.6 against 37.3 at 64 rows from 1024, and behind below 1024).
-constexpr uint32_t SPLIT_FROM = 1024;
-constexpr int SPLIT_MAX_WORKGROUPS = 64;
-
-bool decoder_wants_split(const Decoder* d, int steps) {
-    if (d->split_mode >= 0) return d->split_mode == 1;
-    if (d->rows * d->shape.kv_heads > SPLIT_MAX_WORKGROUPS) return false;
-    uint32_t last = 0;
-    for (int b = 0; b < d->rows; ++b) {
-        const uint32_t p = d->placement_host[b];
-        if (p != TGX_SPARE) last = std::max(last, p + (uint32_t)std::max(steps, 1) - 1);
-    }
-    return last >= SPLIT_FROM;
-}
-
-void decoder_advanced(Decoder* d, int steps) {
-    for (int b = 0; b < d->rows; ++b)
-        if (d->placement_host[b] != TGX_SPARE) d->placement_host[b] += (uint32_t)steps;
-}
-
-tgx_status decoder_use_split(Decoder* d, bool split) {
-    if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
-    if (split == d->split) return TGX_OK;
-    d->split = split;
-    return use_program(d);
-}
-
 tgx_status decoder_use_rows(Decoder* d, int rows) {
     if (!d) return fail(TGX_E_ARG, "null decoder");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
@@ -713,7 +676,6 @@ tgx_status decoder_start(Decoder* d) {
     if (!d) return fail(TGX_E_ARG, "null decoder");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     hipStream_t s = d->ctx->stream;
-    TGX_TRY(decoder_use_split(d, decoder_wants_split(d, 1)));
     TGX_TRY(sync_slots(d));
     TGX_HIP(hipEventRecord(d->ev_start, s));
     if (d->timed || !d->use_graph) {
@@ -787,7 +749,6 @@ tgx_status decoder_launch(Decoder* d, int times, int advance) {
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (times <= 0) return fail(TGX_E_ARG, "times");
     hipStream_t s = d->ctx->stream;
-    TGX_TRY(decoder_use_split(d, decoder_wants_split(d, advance ? times : 1)));
     TGX_TRY(sync_slots(d));
     TGX_HIP(hipEventRecord(d->ev_start, s));
     for (int i = 0; i < times; ++i) {
@@ -802,7 +763,6 @@ tgx_status decoder_launch(Decoder* d, int times, int advance) {
     TGX_HIP(hipEventRecord(d->ev_end, s));
     TGX_HIP(hipEventRecord(d->ev_done, s));
     d->pending = true;
-    if (advance) decoder_advanced(d, times);
     return TGX_OK;
 }
 

@@ -86,11 +86,6 @@ struct Decoder {
     uint16_t *q = nullptr, *attended = nullptr, *mlp = nullptr, *kv = nullptr;
     uint32_t *positions = nullptr, *slot_of_row = nullptr, *table = nullptr;
     uint32_t* row_table = nullptr;  // [rows][max_blocks]: each row's slot's table row
-    float* attn_parts = nullptr;    // DecodeArgs::attn_parts
-    // The attention in a workgroup to each part and a kernel that folds them (DecodeArgs::split):
-    // split_mode -1 chooses by the launch (decoder_wants_split), 0 never, 1 always.
-    int split_mode = -1;
-    bool split = false;
     float *cos = nullptr, *sin = nullptr;
     // host mirrors, in pinned memory
     float *x_host = nullptr, *out_host = nullptr;
@@ -99,8 +94,7 @@ struct Decoder {
     bool table_dirty = true, rows_dirty = true;
     std::vector<int> slot_blocks;     // blocks each slot holds
     std::vector<uint32_t> free_list;  // blocks nobody holds
-    // the recorded step, a program per row count run and attention split (program_key; step_exec,
-    // advance_exec: the current one's)
+    // the recorded step, a program per row count run (step_exec, advance_exec: the current one's)
     struct Program {
         hipGraphExec_t step = nullptr, advance = nullptr;
         int dispatches = 0;
@@ -139,15 +133,6 @@ tgx_status decoder_set_rows(Decoder* dec, const tgx_row* rows, int nrows, const 
 // rows, recorded on its first use; every row spare until placed again. A row's results are the
 // same whatever the program (the kernels' batch invariance).
 tgx_status decoder_use_rows(Decoder* dec, int rows);
-// Whether a launch of `steps` steps from the rows' places wants the attention split: up to 64
-// workgroups (rows x KV heads) and a row at 1024 positions or past (three parts or more) by its
-// end.
-bool decoder_wants_split(const Decoder* d, int steps);
-// The program with the attention split or not (a row's results are the same either way).
-tgx_status decoder_use_split(Decoder* d, bool split);
-// The host's copy of the rows' places after `steps` steps that moved them on (as the device's).
-void decoder_advanced(Decoder* d, int steps);
-int program_key(int rows, bool split);
 // set_rows without the input: places the rows (positions, slots, blocks) alone.
 tgx_status decoder_place(Decoder* dec, const tgx_row* rows, int nrows);
 // The step's dispatches on the context's stream, reading x_in and writing out.

@@ -131,7 +131,6 @@ EXPORTS = [
     "tgx_decoder_read_cache",
     "tgx_decoder_set_timed",
     "tgx_decoder_set_graph",
-    "tgx_decoder_set_attention_split",
     "tgx_decoder_timings",
     "tgx_shape_check",
     "tgx_batch_placement",
@@ -260,7 +259,6 @@ def library() -> ctypes.CDLL:
     lib.tgx_decoder_read_cache.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, P, P]
     lib.tgx_decoder_set_timed.argtypes = [P, ctypes.c_int]
     lib.tgx_decoder_set_graph.argtypes = [P, ctypes.c_int]
-    lib.tgx_decoder_set_attention_split.argtypes = [P, ctypes.c_int]
     lib.tgx_decoder_timings.argtypes = [P, ctypes.c_int, ctypes.POINTER(_Timing), ctypes.POINTER(ctypes.c_int)]
     lib.tgx_shape_check.argtypes = [ctypes.POINTER(_Shape), ctypes.POINTER(_Batch)]
     lib.tgx_batch_placement.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(_Row), ctypes.c_int, ctypes.POINTER(ctypes.c_uint32)]
@@ -592,11 +590,6 @@ class Decoder:
     def set_graph(self, use_graph: bool) -> None:
         """Launch steps as the recorded HIP graph (default) or dispatch by dispatch."""
         _check(library().tgx_decoder_set_graph(self._h, 1 if use_graph else 0))
-
-    def set_attention_split(self, mode: int) -> None:
-        """-1: chosen at each launch; 0: a workgroup to each row; 1: a workgroup to each part of
-        512 positions and a kernel that folds them. The same bits either way."""
-        _check(library().tgx_decoder_set_attention_split(self._h, mode))
 
     def timings(self) -> list:
         """Decoder::timings (decode.rs:891-893): [(label, ms)] of the last timed step."""
