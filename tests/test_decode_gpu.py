@@ -197,6 +197,42 @@ def test_long_contexts_match_the_oracle_and_each_row_is_as_alone(ctx):
         alone.close()
 
 
+def test_launched_steps_move_the_rows_on_as_single_steps_do(ctx):
+    """The recorded step replayed (Decoder::launch with advance, each placed row moved on a
+    position by the step itself; the benchmark's path): k launched steps and one more leave the
+    output and the caches that k + 1 single steps leave, bit for bit."""
+    import tgx
+
+    spec = tiny_spec(layers=2)
+    cap = 128
+    x = inputs(spec, 2)
+    prompt = inputs(spec, 14, name="prompt")
+    decs = []
+    for _ in range(2):
+        d = make_decoder(ctx, spec, cap, rows=2)
+        d.prefill_runs([(0, 0, 5), (1, 0, 9)], prompt)
+        for slot in range(2):
+            d.reserve(slot, 40)
+        decs.append(d)
+    a, b = decs
+    k = 6
+    a.set_rows([tgx.Row(5, 0), tgx.Row(9, 1)], x)
+    a.launch(k, advance=True)
+    a.wait()
+    a.start()
+    a.wait()
+    got = a.output()
+    for t in range(k + 1):
+        want = b.step_rows([tgx.Row(5 + t, 0), tgx.Row(9 + t, 1)], x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for slot, n in ((0, 5 + k + 1), (1, 9 + k + 1)):
+        ka, va = a.read_cache(slot, n)
+        kb, vb = b.read_cache(slot, n)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"slot {slot}"
+    for d in decs:
+        d.close()
+
+
 def test_spare_rows_write_no_cache_and_leave_others_alone(ctx):
     import tgx
 

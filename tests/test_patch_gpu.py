@@ -339,6 +339,39 @@ def test_the_patch_step_is_the_encoder_the_lm_side_and_the_sampler_in_turn(ctx):
         o.close()
 
 
+def test_launched_patch_steps_move_the_rows_on_as_single_runs_do(ctx):
+    """PatchStep launched over what the device holds (the benchmark's path: each placed row moved
+    on a position by the step): a run at position p, k launched steps (p again, then on) and a run
+    at p + k give what runs at p, p + 1, ..., p + k give, bit for bit."""
+    import tgx
+    from tgx.patch import PatchStep
+    from tgx.synth import encoder_weights, sampler_weights
+
+    rows, k = 2, 3
+    espec, dspec = _encoder_spec(1), _dit_spec(1)
+    _, _, w = _lm_weights()
+    _, cond, noise, sampling = _inputs(rows, seed=17)
+    steps = []
+    for _ in range(2):
+        enc = _encoder(ctx, rows, espec, encoder_weights(espec, FEAT))
+        smp = _sampler(ctx, rows, dspec, sampler_weights(dspec, FEAT))
+        side = _lm_side(ctx, rows, w)
+        steps.append((PatchStep(enc, side, smp), enc, smp, side))
+    a, b = steps[0][0], steps[1][0]
+    at = lambda t: [tgx.Row(t, r) for r in range(rows)]
+    a.run_rows(at(0), cond, noise, sampling)
+    a.launch(k, advance=True)
+    a.wait()
+    got = a.run_rows(at(k), cond, noise, sampling)
+    for t in range(k + 1):
+        want = b.run_rows(at(t), cond, noise, sampling)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    for step, *parts in steps:
+        step.close()
+        for o in parts:
+            o.close()
+
+
 def test_a_step_of_fewer_rows_runs_on_the_fewest_program_each_row_as_on_the_largest(ctx):
     """Generator::step (crates/graph/src/generator.rs:115-123, 286-318): a patch step has a
     program for each power of two below its rows and for its rows; a step of n rows runs on the
