@@ -128,10 +128,23 @@ tgx_status lm_side_use_rows(LmSide* s, int rows) {
     if (rows < 1 || rows > s->max_rows)
         return fail(TGX_E_SHAPE, std::to_string(rows) + " rows in a batch of " + std::to_string(s->max_rows));
     if (rows == s->rows) return TGX_OK;
-    TGX_TRY(decoder_use_rows(s->base, rows));
-    TGX_TRY(decoder_use_rows(s->residual, rows));
-    s->rows = rows;
-    return side_program(s);
+    const int before = s->rows;
+    tgx_status st = decoder_use_rows(s->base, rows);
+    if (st == TGX_OK) st = decoder_use_rows(s->residual, rows);
+    if (st == TGX_OK) {
+        s->rows = rows;
+        st = side_program(s);
+    }
+    if (st != TGX_OK) {
+        // Back to the program it had (recorded already), with its message kept.
+        const std::string msg = last_error();
+        s->rows = before;
+        decoder_use_rows(s->base, before);
+        decoder_use_rows(s->residual, before);
+        side_program(s);
+        return fail(st, msg);
+    }
+    return TGX_OK;
 }
 
 hipError_t lm_side_enqueue(LmSide* s, int advance, DispatchTimer* timer, int* dispatches) {

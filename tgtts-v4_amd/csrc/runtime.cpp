@@ -652,14 +652,21 @@ tgx_status decoder_use_rows(Decoder* d, int rows) {
     if (rows < 1 || rows > d->max_rows)
         return fail(TGX_E_SHAPE, std::to_string(rows) + " rows in a batch of " + std::to_string(d->max_rows));
     if (rows == d->rows) return TGX_OK;
+    const int before = d->rows;
     d->rows = rows;
+    tgx_status st = use_program(d);
+    if (st != TGX_OK) {
+        d->rows = before;  // the program it had stays
+        return st;
+    }
+    // Every row spare until placed again.
     for (int i = 0; i < 2 * rows; ++i) d->placement_host[i] = TGX_SPARE;
     d->rows_dirty = true;
     hipStream_t s = d->ctx->stream;
     TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)rows * 4, hipMemcpyHostToDevice, s));
     TGX_HIP(hipMemcpyAsync(d->slot_of_row, d->placement_host + rows, (size_t)rows * 4, hipMemcpyHostToDevice, s));
     TGX_HIP(hipStreamSynchronize(s));
-    return use_program(d);
+    return TGX_OK;
 }
 
 tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const float* x) {

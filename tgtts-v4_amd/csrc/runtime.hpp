@@ -17,6 +17,7 @@ namespace tgx {
 // The thread's last error message (tgx_last_error).
 tgx_status fail(tgx_status status, const std::string& message);
 void clear_error();
+const char* last_error();
 #define TGX_HIP(call)                                                                        \
     do {                                                                                     \
         hipError_t e_ = (call);                                                              \
