@@ -5,7 +5,7 @@
 //   prefill_norm       RMSNorm of each row of the f32 stream into bf16 (norm_rows.comp, and the
 //                      norm half of add_norm_rows.comp; the residual add is the GEMM's epilogue)
 //   prefill_gemm       C = X W^T, bf16 in, f32 accumulate, a 256 x 128 tile to a workgroup of
-//                      four waves staged through LDS twice buffered, with the epilogue fused:
+//                      four waves staged through a ring of LDS stages, with the epilogue fused:
 //                      RoPE and the cache write (rope_rows.comp), the residual add
 //                      (add_norm_rows.comp), or SiLU(gate) up (silu_mul_rows.comp)
 //   prefill_attention  causal attention over the paged cache, 32 positions of a run to a
