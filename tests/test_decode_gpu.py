@@ -49,7 +49,8 @@ def inputs(spec, n, name="x"):
 
 
 def test_tiny_decoder_32_prefill_positions_and_16_steps_match_the_oracle(ctx):
-    """BASELINE config 1 run through decode steps: 4 layers, 32 positions then 16 steps."""
+    """The tiny MiniCPM-4-shaped decoder (4 layers, fp32 weights drawn from a seed) through decode
+    steps: 32 positions then 16 teacher-forced steps, the CPU-runnable case."""
     spec = tiny_spec()
     cap = 64
     dec = make_decoder(ctx, spec, cap)

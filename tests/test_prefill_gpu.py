@@ -27,7 +27,8 @@ def check_rows(got, want, what):
 
 
 def test_tiny_decoder_32_position_prefill_then_16_steps_match_the_oracle(ctx):
-    """4 layers, a 32-position prefill, then 16 teacher-forced decode steps."""
+    """The tiny MiniCPM-4-shaped decoder (4 layers): a 32-position prefill, then 16 teacher-forced
+    decode steps, the CPU-runnable case."""
     spec = tiny_spec()
     cap = 64
     dec = make_decoder(ctx, spec, cap)
