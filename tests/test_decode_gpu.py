@@ -64,7 +64,7 @@ def test_tiny_decoder_32_prefill_positions_and_16_steps_match_the_oracle(ctx):
         assert within(d), f"step {t}: {d}"
         if worst is None or d["cosine"] < worst["cosine"]:
             worst = d
-    print(f"config 1 worst step: {worst}")
+    print(f"tiny decoder, worst step: {worst}")
     # The cache holds the oracle's keys and values (rounded to bf16).
     k, v = dec.read_cache(0, 48)
     for name, got, want in (("k", k, ref.k[:, :, :48]), ("v", v, ref.v[:, :, :48])):

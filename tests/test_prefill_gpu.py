@@ -40,7 +40,7 @@ def test_tiny_decoder_32_position_prefill_then_16_steps_match_the_oracle(ctx):
     for t in range(32, 48):
         d = distance(dec.step(t, x[t]), ref.decode(t, x[t]))
         assert within(d), f"step {t}: {d}"
-    print(f"config 1 prefill worst row: {worst}")
+    print(f"tiny decoder, prefill worst row: {worst}")
     k, v = dec.read_cache(0, 48)
     assert within(distance(k, ref.k[:, :, :48])) and within(distance(v, ref.v[:, :, :48]))
 
