@@ -11,7 +11,8 @@
  * does not contain).
  *
  * Only tests/, the smoke check and the benchmark's CPU-baseline leg may load this library, and
- * only as the checker. The GPU library never links or calls it.
+ * only to hold results against (or as the CPU path timed beside the GPU). The GPU library never
+ * links or calls it.
  *
  * Pinning (each function's checks live in tests/test_oracle.py):
  *   orc_rope_tables   — identity at t = 0, cos(1)/sin(1) at t = 1 for frequency 0

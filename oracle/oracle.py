@@ -1,7 +1,7 @@
 """TEST INFRASTRUCTURE ONLY — ctypes bindings of the oracle (liboracle.so, oracle.c).
 
-Only tests/, the smoke check and the benchmark's CPU-baseline leg import this, as the checker or
-the CPU path timed beside the GPU; the GPU library never does.
+Only tests/, the smoke check and the benchmark's CPU-baseline leg import this, to hold results
+against or as the CPU path timed beside the GPU; the GPU library never does.
 """
 
 from __future__ import annotations

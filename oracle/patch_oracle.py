@@ -18,8 +18,8 @@ A CPU restatement of what runs around the LMs for each patch:
   lm_side_step            crates/graph/src/lm_side.rs:385-478: enc_to_lm_proj, the base LM,
                           fsq in/out, fusion_concat_proj, lm_to_dit / res_to_dit, stop head
 
-Only tests/, the smoke check and the benchmark's CPU-baseline leg import this, as the checker;
-the GPU library never does.
+Only tests/, the smoke check and the benchmark's CPU-baseline leg import this, to hold results
+against; the GPU library never does.
 
 Pinning (tests/test_patch_oracle.py): the schedule's closed-form ends (t_span[0] = 1,
 t_span[n] = 0), its 9 evaluations for 10 steps and the zero-init count for other step counts;
