@@ -441,8 +441,8 @@ def main() -> int:
     if args.sampler:
         return sampler_profile(args.batch, args.steps)
     if args.gpus != 1:
-        print("bench.py runs on one GPU: this build has no multi-GPU path (requests would be routed to "
-              "GPUs at admission, with no collective); run with --gpus 1.", file=sys.stderr)
+        print("bench.py runs on one GPU: tgx has no multi-GPU path (requests would be routed to GPUs "
+              "at admission, with no collective); run with --gpus 1.", file=sys.stderr)
         return 2
 
     import tgx
