@@ -155,6 +155,60 @@ class Stack:
             raise ValueError(f"oracle prefill of {x.shape[0]} from {start} in {self.capacity}")
         return out
 
+    def prefill_rows(self, start: int, x: np.ndarray) -> np.ndarray:
+        """`prefill` restated layer by layer over all the run's positions at once, with numpy's
+        float64 matrix products (prefill.rs:137-504 runs the same op order a layer at a time):
+        thousands of positions in seconds where position by position takes minutes. The products
+        sum in BLAS's order, so it agrees with `prefill` to float64 rounding, not bit for bit
+        (tests/test_oracle.py pins it there). float64 only; writes the caches as `prefill`."""
+        if self.precision != "f64":
+            raise ValueError("prefill_rows runs in float64")
+        s = self.spec
+        x = np.asarray(x, dtype=np.float64)
+        n = x.shape[0]
+        if start < 0 or n <= 0 or start + n > self.capacity:
+            raise ValueError(f"oracle prefill of {n} from {start} in {self.capacity}")
+        H, KV, d, I = s.heads, s.kv_heads, s.head_dim, s.inner
+        group, half, end = H // KV, d // 2, start + n
+        pos = np.arange(start, end)
+        co = self.cos[pos].astype(np.float64)[:, None, :]  # [n][1][d/2]
+        si = self.sin[pos].astype(np.float64)[:, None, :]
+        rope = self.shape.rope != 0
+        scale = 1.0 / np.sqrt(float(d))
+        future = np.arange(end)[None, :] > pos[:, None]  # [n][end]: keys past each position
+
+        def norm(v, g):
+            return v / np.sqrt(np.mean(v * v, axis=-1, keepdims=True) + s.eps) * g.astype(np.float64)
+
+        def rotate(v):  # [n][heads][d]: a' = a cos - c sin, c' = c cos + a sin
+            a, c = v[..., :half], v[..., half:]
+            return np.concatenate([a * co - c * si, c * co + a * si], axis=-1)
+
+        hs = x.copy()
+        for l in range(s.layers):
+            W = lambda name: self.w[f"layers.{l}.{name}"].astype(np.float64)
+            qkv = norm(hs, self.w[f"layers.{l}.input_layernorm"]) @ W("qkv_proj").T
+            q = qkv[:, : H * d].reshape(n, H, d)
+            k = qkv[:, H * d : (H + KV) * d].reshape(n, KV, d)
+            v = qkv[:, (H + KV) * d :].reshape(n, KV, d)
+            if rope:
+                q, k = rotate(q), rotate(k)
+            self.k[l, :, start:end] = k.transpose(1, 0, 2)
+            self.v[l, :, start:end] = v.transpose(1, 0, 2)
+            att = np.empty((n, H, d))
+            for h in range(H):
+                keys, values = self.k[l, h // group, :end], self.v[l, h // group, :end]
+                sc = (q[:, h] @ keys.T) * scale
+                sc[future] = -np.inf
+                sc -= sc.max(axis=1, keepdims=True)
+                p = np.exp(sc)
+                att[:, h] = (p @ values) / p.sum(axis=1, keepdims=True)
+            hs = hs + att.reshape(n, H * d) @ W("o_proj").T
+            gu = norm(hs, self.w[f"layers.{l}.post_attention_layernorm"]) @ W("gate_up_proj").T
+            gate, up = gu[:, :I], gu[:, I:]
+            hs = hs + (gate / (1.0 + np.exp(-gate)) * up) @ W("down_proj").T
+        return norm(hs, self.norm)
+
 
 def set_threads(n: int) -> None:
     library().orc_set_threads(n)

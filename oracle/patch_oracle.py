@@ -28,8 +28,12 @@ velocity, equal velocities give it back, a zero unconditional velocity gives cfg
 quantizer's special cases (0, saturation, ties to even, levels on the 1/L grid); the local
 stack against an independent torch float64 model built from library ops
 (scaled_dot_product_attention without a mask, silu, rms_norm by hand); time_mlp and the layers
-between the LMs against torch's linear and silu (a transposed weight must fail); and the whole
-sampler against the closed form it takes when out_proj reads nothing.
+between the LMs against torch's linear and silu (a transposed weight must fail); the whole
+sampler against the closed form it takes when out_proj reads nothing; and the DiT's sequence
+(mu 0..1 in the conditional sequence only, time 2, cond 3..6, x 7..10, the velocity read from x):
+one Euler step against the sequence assembled by hand through the torch model, the velocity of
+x alone when the stack is made per-token, mu moving v_c and not v_u; planted layouts (cond and x
+traded, the velocity read from cond, mu in both sequences) fail them.
 """
 
 from __future__ import annotations
@@ -196,12 +200,24 @@ def cfg_zero_star(v_c: np.ndarray, v_u: np.ndarray, cfg: float) -> np.ndarray:
     return scaled + cfg * (v_c - scaled)
 
 
-def sample(w: dict, s, feat: int, frames: int, timesteps: int, mu, cond, noise, sampling, rope_on: bool = True):
+def layout(frames: int) -> dict:
+    """Where each part of the DiT's sequence sits (dit.rs:36-41): mu at tokens 0..1 (in the
+    conditional sequence only), the time token at 2, the patch before (cond) at 3..3 + frames - 1,
+    the state x after it; the velocity is read from x's tokens."""
+    x_at = COND_AT + frames
+    return {"mu": 0, "time": TIME_AT, "cond": COND_AT, "x": x_at, "read": x_at}
+
+
+def sample(w: dict, s, feat: int, frames: int, timesteps: int, mu, cond, noise, sampling, rope_on: bool = True,
+           places: dict | None = None, velocities: bool = False):
     """Sampler::sample (dit.rs:178-258, 294-309) for every row: returns (x0, patch), each
-    [rows][feat][frames] float64, x0 the starting point temperature * noise."""
+    [rows][feat][frames] float64, x0 the starting point temperature * noise; with `velocities`
+    also each evaluation's (v_c, v_u), [evaluations][rows][2][feat][frames]. `places` overrides
+    `layout` (the tests plant a misplaced sequence with it; "mu_both" puts mu in both sequences)."""
     rows = noise.shape[0]
     T = COND_AT + 2 * frames
     h = s.hidden
+    at = places or layout(frames)
     W = lambda n: np.asarray(w[n], dtype=np.float64)
     mu = np.asarray(mu, dtype=np.float64).reshape(rows, MU_TOKENS, h)
     cond = np.asarray(cond, dtype=np.float64).reshape(rows, feat, frames)
@@ -210,20 +226,24 @@ def sample(w: dict, s, feat: int, frames: int, timesteps: int, mu, cond, noise, 
     tokens = np.zeros((rows, 2, T, h))
     cond_tok = (W("cond_proj.weight") @ cond).transpose(0, 2, 1) + W("cond_proj.bias")  # [rows][frames][h]
     for s_ in range(2):
-        tokens[:, s_, COND_AT : COND_AT + frames] = cond_tok
-    tokens[:, 0, :MU_TOKENS] = mu  # zero in the unconditional sequence
+        tokens[:, s_, at["cond"] : at["cond"] + frames] = cond_tok
+    seqs_with_mu = slice(None) if at.get("mu_both") else 0  # zero in the unconditional sequence
+    tokens[:, seqs_with_mu, at["mu"] : at["mu"] + MU_TOKENS] = mu[:, None] if at.get("mu_both") else mu
     times = time_tokens(w, timesteps, h)
-    x_at = COND_AT + frames
+    vs = []
     for i, (t, dt) in enumerate(euler_steps(timesteps)):
-        tokens[:, :, TIME_AT] = times[i]
+        tokens[:, :, at["time"]] = times[i]
         x_tok = (W("in_proj.weight") @ state).transpose(0, 2, 1) + W("in_proj.bias")
-        tokens[:, :, x_at : x_at + frames] = x_tok[:, None]
+        tokens[:, :, at["x"] : at["x"] + frames] = x_tok[:, None]
         out = local_stack(w, s, tokens.reshape(rows * 2 * T, h), T, rope_on).reshape(rows, 2, T, h)
-        vel = out[:, :, x_at : x_at + frames] @ W("out_proj.weight").T + W("out_proj.bias")  # [rows][2][frames][feat]
+        vel = out[:, :, at["read"] : at["read"] + frames] @ W("out_proj.weight").T + W("out_proj.bias")  # [rows][2][frames][feat]
         vel = vel.transpose(0, 1, 3, 2)  # [rows][2][feat][frames]
+        vs.append(vel)
         for r in range(rows):
             g = cfg_zero_star(vel[r, 0], vel[r, 1], float(sampling[r][1]))
             state[r] -= dt * g
+    if velocities:
+        return x0, state, np.stack(vs) if vs else np.zeros((0, rows, 2, feat, frames))
     return x0, state
 
 

@@ -167,7 +167,7 @@ def test_attention_over_one_position_returns_its_value():
 # ---- the whole stack against an independent float64 model --------------------------------------
 
 
-def torch_stack(spec, weights, x, rope=True, start=0):
+def torch_stack(spec, weights, x, rope=True, start=0, causal=True):
     """MiniCPM-4 layers over a run of positions from library ops in float64: RMSNorm written out,
     RoPE by rotate_half, torch's scaled_dot_product_attention (causal, GQA by repeat), SiLU."""
     import torch
@@ -203,7 +203,7 @@ def torch_stack(spec, weights, x, rope=True, start=0):
             k = k * cos + rotate_half(k) * sin
         k = k.repeat_interleave(H // KV, dim=1)
         v = v.repeat_interleave(H // KV, dim=1)
-        att = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), is_causal=True)
+        att = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), is_causal=causal)
         att = att.transpose(0, 1).reshape(T, H * d)
         h = h + att @ w[f"layers.{l}.o_proj"].T
         n = norm(h, w[f"layers.{l}.post_attention_layernorm"])
@@ -247,6 +247,37 @@ def test_prefill_matches_the_model_and_decode_goes_on_from_its_cache(tiny):
     steps = np.stack([st.decode(t, x[t]) for t in range(32, 48)])
     got = np.concatenate([out, steps])
     assert np.max(np.abs(got - want)) <= 1e-10 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("rope", [True, False])
+def test_the_layer_by_layer_prefill_is_the_position_by_position_one(tiny, rope):
+    """prefill_rows (a layer over every position at once, numpy's float64 products) against the
+    pinned position-by-position path and the torch model: a run from 0, then a second run from
+    where it ended in the same cache; outputs and both caches to float64 rounding. Planted
+    defects must show: the causal mask left out, and the second run placed one position on."""
+    import oracle
+    from tgx.synth import embeddings
+
+    spec, w = tiny
+    x = embeddings(5, "x", 56, spec.hidden).astype(np.float64)
+    want = torch_stack(spec, w, x, rope=rope)
+    scale = np.max(np.abs(want))
+    steps = oracle.Stack(spec, w, 64, rope=rope)
+    rows = oracle.Stack(spec, w, 64, rope=rope)
+    a = np.concatenate([steps.prefill(0, x[:37]), steps.prefill(37, x[37:])])
+    b = np.concatenate([rows.prefill_rows(0, x[:37]), rows.prefill_rows(37, x[37:])])
+    assert np.max(np.abs(b - a)) <= 1e-12 * scale
+    assert np.max(np.abs(b - want)) <= 1e-10 * scale
+    for cache in ("k", "v"):
+        ca, cb = getattr(steps, cache), getattr(rows, cache)
+        assert np.max(np.abs(cb - ca)) <= 1e-12 * np.max(np.abs(ca)), cache
+    # Defects the comparison must see: every key visible to every position (the causal mask left
+    # out), and the second run written one position on.
+    leaky = torch_stack(spec, w, x[:37], rope=rope, causal=False)
+    assert np.max(np.abs(leaky - a[:37])) > 1e-3 * scale
+    shifted = oracle.Stack(spec, w, 64, rope=rope)
+    s = np.concatenate([shifted.prefill_rows(0, x[:37]), shifted.prefill_rows(38, x[37:55])])
+    assert np.max(np.abs(s - want[:55])) > 1e-3 * scale
 
 
 def test_a_stack_without_rope_and_its_defects(tiny):

@@ -243,3 +243,127 @@ def test_the_encoder_matches_an_independent_torch_model():
     assert np.allclose(alone[0], got[1], atol=1e-12)
     reversed_ = po.encode(w, s, 64, 4, patches[:, :, ::-1])
     assert np.max(np.abs(reversed_ - got)) > 1e-3
+
+
+# ---- the DiT's sequence: where mu, the time, the patch before and the state sit -----------------
+
+# Planted defects: the patch before (cond) and the state x trading places, the velocity read where
+# x now sits (a layout consistent with itself, which only the positions RoPE sees tell apart); and
+# the same trade with the velocity read at x's proper place, that is from cond's outputs.
+SWAPPED = {"mu": 0, "time": 2, "cond": 7, "x": 3, "read": 3}
+MISREAD = {"mu": 0, "time": 2, "cond": 7, "x": 3, "read": 7}
+
+
+def _dit_case(rows=2, seed=21, hidden=1024):
+    rng = np.random.default_rng(seed)
+    mu = rng.standard_normal((rows, 2, hidden))
+    cond = rng.standard_normal((rows, 64, 4))
+    noise = rng.standard_normal((rows, 64, 4))
+    sampling = np.array([[0.9, 2.0], [1.0, 1.5], [0.7, 3.0]])[:rows]
+    return mu, cond, noise, sampling
+
+
+def _shape(spec):
+    return po.StackShape(hidden=spec.hidden, inner=spec.inner, layers=spec.layers)
+
+
+def test_the_dit_sequence_assembled_by_hand_gives_the_oracles_euler_step():
+    """crates/graph/src/local/dit.rs:36-41, 178-258: each row's conditional sequence is
+    [mu_0, mu_1, time, cond_0..3, x_0..3] and its unconditional one the same with mu zero, the
+    velocity out_proj of x's four outputs. Assembled here token by token with torch's linear,
+    through the independent torch float64 model of the local stack, CFG-Zero* and one Euler step
+    by their formulas (dit_euler.comp:81-110): with 2 timesteps the DiT runs once. A sequence
+    with cond and x trading places (read where x sits) must fail it."""
+    import torch
+    import torch.nn.functional as F
+
+    spec, w = _small_dit(2)
+    s = _shape(spec)
+    h, rows = spec.hidden, 2
+    mu, cond, noise, sampling = _dit_case(rows)
+    ((t, dt),) = po.euler_steps(2)
+    time_token = po.time_tokens(w, 2, h)[0]  # pinned above: the embedding's closed form, time_mlp
+    tt = lambda a: torch.as_tensor(np.asarray(a, np.float64))
+    x0 = sampling[:, 0][:, None, None] * noise
+    seqs = []
+    for r in range(rows):
+        cond_tokens = F.linear(tt(cond[r]).T, tt(w["cond_proj.weight"]), tt(w["cond_proj.bias"]))  # [4][h]
+        x_tokens = F.linear(tt(x0[r]).T, tt(w["in_proj.weight"]), tt(w["in_proj.bias"]))
+        for conditional in (True, False):
+            m = tt(mu[r]) if conditional else torch.zeros(2, h, dtype=torch.float64)
+            seqs.append(torch.cat([m, tt(time_token)[None], cond_tokens, x_tokens]))
+    assert seqs[0].shape == (11, h)
+    out = _torch_local_stack(w, s, torch.cat(seqs).numpy(), 11).reshape(rows, 2, 11, h)
+    vel = F.linear(tt(out[:, :, 7:11]), tt(w["out_proj.weight"]), tt(w["out_proj.bias"])).numpy().transpose(0, 1, 3, 2)
+    want = np.empty_like(x0)
+    for r in range(rows):
+        vc, vu = vel[r, 0], vel[r, 1]
+        alpha = np.sum(vc * vu) / (np.sum(vu * vu) + 1e-8)
+        want[r] = x0[r] - dt * (alpha * vu + sampling[r, 1] * (vc - alpha * vu))
+    _, got = po.sample(w, s, 64, 4, 2, mu, cond, noise, sampling)
+    scale = np.max(np.abs(want - x0))
+    assert np.max(np.abs(got - want)) <= 1e-9 * scale
+    _, wrong = po.sample(w, s, 64, 4, 2, mu, cond, noise, sampling, places=SWAPPED)
+    assert np.max(np.abs(wrong - want)) > 1e-4 * scale
+
+
+def _per_token_dit(spec, w):
+    """The DiT with every layer's o_proj and down_proj zero: attention and MLP add nothing, so the
+    stack maps each token alone through the final norm."""
+    w = dict(w)
+    for l in range(spec.layers):
+        for name in ("o_proj", "down_proj"):
+            w[f"layers.{l}.{name}"] = np.zeros_like(w[f"layers.{l}.{name}"])
+    return w
+
+
+def test_with_the_stack_per_token_the_velocity_is_x_alone():
+    """With the stack per token, each evaluation's velocities are
+    out_proj(norm(in_proj(x) + b)) + b of the state x alone, the same in both sequences, and mu,
+    the patch before and the time do not move them. Reading the velocity from cond's outputs
+    (MISREAD) must fail it."""
+    spec, w = _small_dit(2)
+    w = _per_token_dit(spec, w)
+    s = _shape(spec)
+    mu, cond, noise, sampling = _dit_case(2)
+    x0, _, vs = po.sample(w, s, 64, 4, 10, mu, cond, noise, sampling, velocities=True)
+    W = lambda n: np.asarray(w[n], np.float64)
+    tokens = (W("in_proj.weight") @ x0).transpose(0, 2, 1) + W("in_proj.bias")  # [rows][4][h]
+    normed = tokens / np.sqrt(np.mean(tokens * tokens, axis=-1, keepdims=True) + spec.eps) * W("norm")
+    want = (normed @ W("out_proj.weight").T + W("out_proj.bias")).transpose(0, 2, 1)  # [rows][feat][4]
+    for c in (0, 1):
+        assert np.max(np.abs(vs[0][:, c] - want)) <= 1e-10 * np.max(np.abs(want))
+    rng = np.random.default_rng(5)
+    _, _, moved = po.sample(w, s, 64, 4, 10, rng.standard_normal(mu.shape), rng.standard_normal(cond.shape), noise,
+                            sampling, velocities=True)
+    assert np.allclose(moved, vs, rtol=0, atol=1e-12)
+    _, _, misread = po.sample(w, s, 64, 4, 10, mu, cond, noise, sampling, places=MISREAD, velocities=True)
+    assert np.max(np.abs(misread[0][:, 0] - want)) > 1e-3 * np.max(np.abs(want))
+
+
+def test_mu_reaches_the_conditional_sequence_only():
+    """mu tokens sit in the conditional sequence and are zero in the unconditional one
+    (dit.rs:36-41): at the first evaluation (the state x0 the same either way) another mu leaves
+    v_u exactly as it was and moves v_c. With mu zero the two sequences are the same, so v_c = v_u
+    at every evaluation and each Euler step moves x by dt (alpha + cfg (1 - alpha)) v_c."""
+    spec, w = _small_dit(2)
+    s = _shape(spec)
+    mu, cond, noise, sampling = _dit_case(2)
+    _, _, vs = po.sample(w, s, 64, 4, 10, mu, cond, noise, sampling, velocities=True)
+    _, _, other = po.sample(w, s, 64, 4, 10, 3.0 * mu[::-1], cond, noise, sampling, velocities=True)
+    assert np.allclose(other[0][:, 1], vs[0][:, 1], rtol=0, atol=1e-12)
+    assert np.max(np.abs(other[0][:, 0] - vs[0][:, 0])) > 1e-3 * np.max(np.abs(vs[0][:, 0]))
+    x0, patch, zero = po.sample(w, s, 64, 4, 10, np.zeros_like(mu), cond, noise, sampling, velocities=True)
+    assert np.allclose(zero[:, :, 0], zero[:, :, 1], rtol=0, atol=1e-12)
+    x = x0.copy()
+    for (t, dt), v in zip(po.euler_steps(10), zero):
+        for r in range(2):
+            vc = v[r, 0]
+            alpha = np.sum(vc * vc) / (np.sum(vc * vc) + 1e-8)
+            x[r] -= dt * (alpha + sampling[r, 1] * (1 - alpha)) * vc
+    assert np.max(np.abs(patch - x)) <= 1e-12 * np.max(np.abs(x))
+    # Planted: mu written into both sequences must break the first check.
+    both = {**po.layout(4), "mu_both": True}
+    _, _, a = po.sample(w, s, 64, 4, 10, mu, cond, noise, sampling, places=both, velocities=True)
+    _, _, b = po.sample(w, s, 64, 4, 10, 3.0 * mu[::-1], cond, noise, sampling, places=both, velocities=True)
+    assert np.max(np.abs(a[0][:, 1] - b[0][:, 1])) > 1e-3 * np.max(np.abs(a[0][:, 1]))

@@ -226,6 +226,8 @@ tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times) 
         TGX_TRY(sampler_wait(s));
     }
     hipStream_t st = l->ctx->stream;
+    TGX_TRY(hold_ahead(l->base, times, 1));
+    TGX_TRY(hold_ahead(l->residual, times, 1));
     TGX_TRY(sync_slots(l->base));
     TGX_TRY(sync_slots(l->residual));
     const size_t mu_bytes = (size_t)l->rows * 2 * l->dit * 4;
@@ -234,6 +236,8 @@ tgx_status tgx_patch_launch(tgx_lm_side* side, tgx_sampler* sampler, int times) 
         TGX_HIP(hipGraphLaunch(l->advance_exec, st));
         TGX_HIP(hipMemcpyAsync(s->mu, l->mu, mu_bytes, hipMemcpyDeviceToDevice, st));
         TGX_HIP(hipGraphLaunch(s->exec, st));
+        moved_on(l->base, 1);
+        moved_on(l->residual, 1);
     }
     TGX_HIP(hipEventRecord(l->ev_end, st));
     l->pending = true;

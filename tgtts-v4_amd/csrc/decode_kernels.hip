@@ -489,9 +489,9 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
         }
         const uint32_t p0 = (uint32_t)(w + ATTN_WAVES * j) * BLOCK_TOKENS;
         if (p0 + BLOCK_TOKENS - 1 <= pos)
-            sm.block<false>(s, v, p0, pos, scale_log2);
+            sm.block<false>(s, v, p0, pos, pos, scale_log2);
         else
-            sm.block<true>(s, v, p0, pos, scale_log2);
+            sm.block<true>(s, v, p0, pos, pos, scale_log2);
     };
     // Two buffers: the first two turns straight (every context up to 16 blocks), then the rest
     // two at a time, each pair's loads issued once the last pair is taken.

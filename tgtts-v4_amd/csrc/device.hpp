@@ -127,15 +127,44 @@ __device__ __forceinline__ float lane_xor32(float v) {
 // (scores times scale log2(e)), the running sum l of P and O^T in o (lane 16 g + c: column c,
 // dimensions 16 dt + 4 g .. + 3). P is rounded to bf16 for the product P V and summed as
 // rounded, by an MFMA against ones. MASK: keys past the column's position `pos` count for
-// nothing (blocks wholly at or below every column's position need no mask). The first block a
-// column sees holds key 0 <= pos, so m is finite after it.
+// nothing, and the values past `vlast` (the last position any column of the wave may see) read
+// as zero: P is zero there, but a cache block past the position may hold anything, NaN included
+// (a block handed on from a request that ended not finite), and 0 NaN is NaN. Blocks wholly at
+// or below every column's position need no mask. The first block a column sees holds key
+// 0 <= pos, so m is finite after it.
 struct OnlineSoftmax {
     float m = -INFINITY, l = 0.f;
     f32x4 o[4] = {};
 
     template <bool MASK>
-    __device__ __forceinline__ void block(f32x4 (&s)[4], const uint4 (&vf)[8], uint32_t p0, uint32_t pos, float scale_log2) {
+    __device__ __forceinline__ void block(f32x4 (&s)[4], const uint4 (&vin)[8], uint32_t p0, uint32_t pos, uint32_t vlast,
+                                          float scale_log2) {
         const int lane = threadIdx.x % WAVE;
+        uint4 vf[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vf[i] = vin[i];
+        if (MASK) {
+            // Lane 16 g + d % 16 of value fragment 2 dt + ks holds in its slot j the position
+            // 32 ks + 16 (j / 4) + 4 g + j % 4 (value_index); word w holds slots 2 w and 2 w + 1.
+            const uint32_t g = (uint32_t)lane / 16;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                uint32_t keep[4];
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t p = p0 + 32 * ks + 16 * (w / 2) + 4 * g + 2 * (w % 2);
+                    keep[w] = (p <= vlast ? 0x0000ffffu : 0u) | (p + 1 <= vlast ? 0xffff0000u : 0u);
+                }
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    uint4& f = vf[dt * 2 + ks];
+                    f.x &= keep[0];
+                    f.y &= keep[1];
+                    f.z &= keep[2];
+                    f.w &= keep[3];
+                }
+            }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt)

@@ -293,10 +293,23 @@ tgx_status step_encode_program(PatchStep* p) {
 tgx_status patch_step_use_rows(PatchStep* p, int rows) {
     if (!p) return fail(TGX_E_ARG, "null patch step");
     if (p->pending) return fail(TGX_E_BUSY, "a step is under way");
-    TGX_TRY(encoder_use_rows(p->encoder, rows));
+    // The LM side first: it keeps its program when it cannot switch. Past it, a part that cannot
+    // switch takes all three back to the program they had (recorded already), so that they never
+    // run at different row counts.
+    const int before = p->side->rows;
     TGX_TRY(lm_side_use_rows(p->side, rows));
-    TGX_TRY(sampler_use_rows(p->sampler, rows));
-    return step_encode_program(p);
+    tgx_status st = encoder_use_rows(p->encoder, rows);
+    if (st == TGX_OK) st = sampler_use_rows(p->sampler, rows);
+    if (st == TGX_OK) st = step_encode_program(p);
+    if (st != TGX_OK) {
+        const std::string msg = last_error();
+        lm_side_use_rows(p->side, before);
+        encoder_use_rows(p->encoder, before);
+        sampler_use_rows(p->sampler, before);
+        step_encode_program(p);
+        return fail(st, msg);
+    }
+    return TGX_OK;
 }
 
 tgx_status patch_step_create(Encoder* e, LmSide* side, Sampler* s, PatchStep** out) {
@@ -348,6 +361,8 @@ tgx_status patch_step_launch(PatchStep* p, int times, int advance) {
     TGX_TRY(sampler_prepare(s));
     if (s->exec_dirty) TGX_TRY(sampler_record(s));
     hipStream_t st = l->ctx->stream;
+    TGX_TRY(hold_ahead(l->base, times, advance));
+    TGX_TRY(hold_ahead(l->residual, times, advance));
     TGX_TRY(sync_slots(l->base));
     TGX_TRY(sync_slots(l->residual));
     const size_t mu_bytes = (size_t)l->rows * 2 * l->dit * 4;
@@ -359,6 +374,10 @@ tgx_status patch_step_launch(PatchStep* p, int times, int advance) {
         TGX_HIP(hipGraphLaunch(advance ? l->advance_exec : l->exec, st));
         TGX_HIP(hipMemcpyAsync(s->mu, l->mu, mu_bytes, hipMemcpyDeviceToDevice, st));
         TGX_HIP(hipGraphLaunch(s->exec, st));
+        if (advance) {
+            moved_on(l->base, 1);
+            moved_on(l->residual, 1);
+        }
     }
     TGX_HIP(hipEventRecord(p->ev_end, st));
     p->pending = true;

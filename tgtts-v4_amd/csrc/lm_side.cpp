@@ -294,6 +294,8 @@ tgx_status lm_side_launch(LmSide* s, int times, int advance) {
     if (s->pending || s->base->pending || s->residual->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (times <= 0) return fail(TGX_E_ARG, "times");
     hipStream_t st = s->ctx->stream;
+    TGX_TRY(hold_ahead(s->base, times, advance));
+    TGX_TRY(hold_ahead(s->residual, times, advance));
     TGX_TRY(sync_slots(s->base));
     TGX_TRY(sync_slots(s->residual));
     TGX_HIP(hipEventRecord(s->ev_start, st));
@@ -303,6 +305,10 @@ tgx_status lm_side_launch(LmSide* s, int times, int advance) {
         } else {
             hipError_t e = lm_side_enqueue(s, advance, nullptr, nullptr);
             if (e != hipSuccess) return fail(TGX_E_HIP, std::string("launching the LM side: ") + hipGetErrorString(e));
+        }
+        if (advance) {
+            moved_on(s->base, 1);
+            moved_on(s->residual, 1);
         }
     }
     TGX_HIP(hipEventRecord(s->ev_end, st));

@@ -583,10 +583,12 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
 #pragma unroll
                 for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(kf[pt * 2 + ds], qf[cg][ds], s[pt]);
             }
+            // Values past the tile's last position read as zero (attention_rows.comp:1-13): every
+            // position up to it was written by this run or before it.
             if (full)
-                sm[cg].template block<false>(s, vf, p0, cpos[cg], scale_log2);
+                sm[cg].template block<false>(s, vf, p0, cpos[cg], last, scale_log2);
             else
-                sm[cg].template block<true>(s, vf, p0, cpos[cg], scale_log2);
+                sm[cg].template block<true>(s, vf, p0, cpos[cg], last, scale_log2);
         }
         if (bi + 1 < blocks) {
 #pragma unroll

@@ -469,6 +469,27 @@ tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions) {
     return TGX_OK;
 }
 
+tgx_status hold_ahead(Decoder* d, int times, int advance) {
+    // Each placed row writes its key and value at its position, and with `advance` at the next
+    // times - 1 after it too: its slot must hold blocks for all of them (decode.rs:198-227 refuses
+    // a placement past the cache on the host; here the blocks are held, the capacity refused).
+    const uint64_t reach = advance ? (uint64_t)times : 1;
+    for (int b = 0; b < d->rows; ++b) {
+        const uint32_t pos = d->placement_host[b];
+        if (pos == TGX_SPARE) continue;
+        if ((uint64_t)pos + reach > (uint64_t)d->shape.capacity)
+            return fail(TGX_E_SHAPE, "row " + std::to_string(b) + " at position " + std::to_string(pos) + " run " +
+                                         std::to_string(reach) + " steps on passes a capacity of " + std::to_string(d->shape.capacity));
+        TGX_TRY(hold_slot(d, d->placement_host[d->rows + b], (uint32_t)(pos + reach)));
+    }
+    return TGX_OK;
+}
+
+void moved_on(Decoder* d, int times) {
+    for (int b = 0; b < d->rows; ++b)
+        if (d->placement_host[b] != TGX_SPARE) d->placement_host[b] += (uint32_t)times;
+}
+
 tgx_status sync_slots(Decoder* d) {
     if (!d->table_dirty && !d->rows_dirty) return TGX_OK;
     hipStream_t s = d->ctx->stream;
@@ -683,6 +704,7 @@ tgx_status decoder_start(Decoder* d) {
     if (!d) return fail(TGX_E_ARG, "null decoder");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     hipStream_t s = d->ctx->stream;
+    TGX_TRY(hold_ahead(d, 1, 0));
     TGX_TRY(sync_slots(d));
     TGX_HIP(hipEventRecord(d->ev_start, s));
     if (d->timed || !d->use_graph) {
@@ -756,6 +778,7 @@ tgx_status decoder_launch(Decoder* d, int times, int advance) {
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (times <= 0) return fail(TGX_E_ARG, "times");
     hipStream_t s = d->ctx->stream;
+    TGX_TRY(hold_ahead(d, times, advance));
     TGX_TRY(sync_slots(d));
     TGX_HIP(hipEventRecord(d->ev_start, s));
     for (int i = 0; i < times; ++i) {
@@ -766,6 +789,7 @@ tgx_status decoder_launch(Decoder* d, int times, int advance) {
         } else {
             TGX_HIP(hipGraphLaunch(advance ? d->advance_exec : d->step_exec, s));
         }
+        if (advance) moved_on(d, 1);
     }
     TGX_HIP(hipEventRecord(d->ev_end, s));
     TGX_HIP(hipEventRecord(d->ev_done, s));

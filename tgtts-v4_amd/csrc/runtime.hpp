@@ -148,6 +148,12 @@ tgx_status decoder_launch(Decoder* dec, int times, int advance);
 // copies of their slots' rows of it, to the device when they changed.
 tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions);
 tgx_status sync_slots(Decoder* d);
+// Before `times` steps (each placed row moved on a position a step with `advance`): holds every
+// placed row's blocks up to the last position the steps write, refusing (TGX_E_SHAPE) a row the
+// steps would take past the capacity, or a pool that runs out.
+tgx_status hold_ahead(Decoder* d, int times, int advance);
+// The host's copy of the placement moved on as an advancing step moves the rows on the device.
+void moved_on(Decoder* d, int times);
 tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out);
 // The same, enqueued on the context's stream without waiting: x from the host, or from the device
 // when x_on_device; the output, [rows of the runs in order][hidden] f32, left in d->pf.out.
