@@ -277,3 +277,85 @@ def test_a_pool_too_small_for_the_slots_is_refused_when_it_runs_out(ctx):
     assert e.value.kind == "shape"
     dec.release_slot(1)
     dec.step_rows([tgx.Row(128, 0), None], x)
+
+
+def test_nan_left_in_a_reused_block_past_the_position_never_reaches_the_output(ctx):
+    """crates/vulkan/tests/glsl.rs:690-699: what lies past the position must not reach the output,
+    NaN included. A request fed NaN leaves NaN keys and values at positions 0..99 of its slot's
+    blocks; the slot is released and the next request, handed the same blocks, runs positions
+    0..69 (every step's block holds NaN past its position): each step finite and bit for bit as
+    on a fresh decoder."""
+    spec = tiny_spec(layers=2)
+    cap = 128
+    x = inputs(spec, 70)
+    dec = make_decoder(ctx, spec, cap)
+    fresh = make_decoder(ctx, spec, cap)
+    poison = np.full(spec.hidden, np.nan, dtype=np.float32)
+    for t in range(100):
+        dec.step(t, poison)
+    k, v = dec.read_cache(0, 100)
+    assert np.isnan(k).all() and np.isnan(v).all()
+    dec.release_slot(0)
+    for t in range(70):
+        got, want = dec.step(t, x[t]), fresh.step(t, x[t])
+        assert np.all(np.isfinite(got)), f"step {t}"
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"step {t}"
+    k, v = dec.read_cache(0, 128)
+    assert np.isfinite(k[:, :, :70]).all() and np.isnan(k[:, :, 70:100]).all()
+    dec.close()
+    fresh.close()
+
+
+def test_a_step_writes_its_own_position_and_no_other(ctx):
+    """glsl.rs:590-597: a cache row past the position is never written. Positions 0..63 hold
+    known values (a prefill of 64); a step at 20 then rewrites row 20 alone, in every layer."""
+    spec = tiny_spec(layers=2)
+    cap = 128
+    x = inputs(spec, 65)
+    dec = make_decoder(ctx, spec, cap)
+    dec.prefill_runs([(0, 0, 64)], x[:64])
+    k0, v0 = dec.read_cache(0, 64)
+    dec.step(20, x[64])
+    k1, v1 = dec.read_cache(0, 64)
+    for before, after in ((k0, k1), (v0, v1)):
+        changed = np.any(before != after, axis=(0, 1, 3))
+        assert changed[20] and changed.sum() == 1, np.flatnonzero(changed)
+    dec.close()
+
+
+def test_launched_steps_past_the_reserved_blocks_hold_them_and_match_single_steps(ctx):
+    """Decoder::launch with advance past what reserve held: the launch holds the blocks each row's
+    positions reach (positions 60..139 of a slot reserved to 64), so that the launched steps leave
+    the output and the caches single steps leave, bit for bit; a launch that would take a row past
+    the capacity is refused on the host, before anything runs."""
+    import tgx
+
+    spec = tiny_spec(layers=2)
+    cap = 192
+    x = inputs(spec, 1)
+    prompt = inputs(spec, 60, name="prompt")
+    a = make_decoder(ctx, spec, cap)
+    b = make_decoder(ctx, spec, cap)
+    for d in (a, b):
+        d.prefill_runs([(0, 0, 60)], prompt)
+    k = 80
+    a.set_rows([tgx.Row(60, 0)], x)
+    a.launch(k, advance=True)
+    a.wait()
+    a.start()  # at 60 + k: the host follows the rows the device moved on
+    a.wait()
+    got = a.output()[0]
+    for t in range(k + 1):
+        want = b.step(60 + t, x[0])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ka, va = a.read_cache(0, 60 + k + 1)
+    kb, vb = b.read_cache(0, 60 + k + 1)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a.set_rows([tgx.Row(150, 0)], x)
+    with pytest.raises(tgx.TgxError) as e:
+        a.launch(cap - 150 + 1, advance=True)
+    assert e.value.kind == "shape"
+    a.launch(cap - 150, advance=True)  # up to the last position: allowed
+    a.wait()
+    a.close()
+    b.close()

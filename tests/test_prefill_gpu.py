@@ -103,3 +103,25 @@ def test_runs_the_cache_cannot_hold_are_refused(ctx):
         with pytest.raises(tgx.TgxError) as e:
             dec.prefill_runs(runs, x[: max(n, 1)])
         assert e.value.kind == "shape"
+
+
+def test_nan_left_in_a_reused_block_past_the_run_never_reaches_its_outputs(ctx):
+    """attention_rows.comp:1-13: keys and values past the workgroup's last position read as zero.
+    A request fed NaN leaves NaN at positions 0..149 of its slot's blocks; released, the next
+    request in the same blocks prefills 0..99 (a run ending inside a NaN block) and steps on:
+    finite, and bit for bit as on a fresh decoder."""
+    spec = tiny_spec(layers=2)
+    cap = 256
+    x = inputs(spec, 104)
+    dec = make_decoder(ctx, spec, cap)
+    fresh = make_decoder(ctx, spec, cap)
+    dec.prefill(0, np.full((150, spec.hidden), np.nan, dtype=np.float32))
+    dec.release_slot(0)
+    got, want = dec.prefill(0, x[:100]), fresh.prefill(0, x[:100])
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for t in range(100, 104):
+        a, b = dec.step(t, x[t]), fresh.step(t, x[t])
+        assert np.all(np.isfinite(a)) and np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
+    dec.close()
+    fresh.close()
