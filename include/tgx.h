@@ -211,6 +211,18 @@ tgx_status tgx_prefill_runs(tgx_decoder* dec, const tgx_run* runs, int nruns, co
  * tgx_decoder_elapsed_ms times it. */
 tgx_status tgx_prefill_launch(tgx_decoder* dec, int times);
 
+/* tgx_prefill_runs without allocating: no counterpart in the reference. It is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc), where tgx_prefill_runs grows its tensors on a call longer than any before it.
+ * The same runs, outputs and cache writes, bit for bit; the tensors live in a fixed array of
+ * 32 MiB on each GPU (held until the process ends), which at the backbone's shape (hidden 1024,
+ * inner 4096, 16 heads) holds 1024 positions a call: runs past it are refused with TGX_E_SHAPE
+ * before anything runs. Every call on a GPU shares that GPU's array, so calls that overlap on one
+ * GPU (from several threads, or decoders on one device) race; the call returns when its output is
+ * copied out. */
+tgx_status tgx_prefill_runs_noalloc(tgx_decoder* dec, const tgx_run* runs, int nruns, const float* x,
+                                    float* out);
+
 /* ---- the patch sampler: crates/graph/src/local/dit.rs ---- */
 
 /* What sampler_graph takes besides the DiT's stack (dit.rs:114-131): a patch of `feat_dim`

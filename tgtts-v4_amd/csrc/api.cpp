@@ -175,7 +175,7 @@ tgx_status tgx_decoder_dispatches(const tgx_decoder* dec, int* out) {
 tgx_status tgx_decoder_device_bytes(const tgx_decoder* dec, size_t* out) {
     clear_error();
     if (!dec || !out) return fail(TGX_E_ARG, "null decoder or output");
-    *out = dec->dec->device_bytes;
+    *out = dec->dec->device_bytes + prefill_bytes(dec->dec);
     return TGX_OK;
 }
 
@@ -198,6 +198,11 @@ tgx_status tgx_prefill_runs(tgx_decoder* dec, const tgx_run* runs, int nruns, co
 tgx_status tgx_prefill_launch(tgx_decoder* dec, int times) {
     clear_error();
     return prefill_launch(DEC(dec), times);
+}
+
+tgx_status tgx_prefill_runs_noalloc(tgx_decoder* dec, const tgx_run* runs, int nruns, const float* x, float* out) {
+    clear_error();
+    return prefill_runs_noalloc(DEC(dec), runs, nruns, x, out);
 }
 
 }  // extern "C"

@@ -3,6 +3,7 @@
 // attention's tiles, and the kernels launched over the decoder's weights and cache.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "runtime.hpp"
@@ -64,9 +65,9 @@ tgx_status hold_rows(Decoder* d, int rows, int tiles) {
     return TGX_OK;
 }
 
-tgx_status launch(Decoder* d) {
+// The prefill's kernels over the tensors p points at.
+tgx_status launch(Decoder* d, const PrefillState& p) {
     const Shape& s = d->shape;
-    PrefillState& p = d->pf;
     PrefillArgs a{};
     a.M = p.M;
     a.M_pad = p.M_pad;
@@ -111,8 +112,20 @@ tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float*
     return TGX_OK;
 }
 
-tgx_status prefill_device(Decoder* d, const tgx_run* runs, int nruns, const float* x, bool x_on_device) {
-    if (!d || !runs || !x) return fail(TGX_E_ARG, "null decoder, runs or x");
+namespace {
+
+// The rows and the attention's tiles of `runs`, checked against the decoder: each run's positions
+// as rows one after another (M of them, M_pad padded to the GEMM's rows), the tiles later in a run,
+// which attend to more, first.
+struct Plan {
+    size_t M = 0;
+    int M_pad = 0;
+    std::vector<uint32_t> pos, slot;
+    std::vector<PrefillTile> tiles;
+};
+
+tgx_status make_plan(Decoder* d, const tgx_run* runs, int nruns, Plan& plan) {
+    if (!d || !runs) return fail(TGX_E_ARG, "null decoder or runs");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (nruns <= 0) return fail(TGX_E_SHAPE, "no runs");
     const Shape& s = d->shape;
@@ -128,40 +141,129 @@ tgx_status prefill_device(Decoder* d, const tgx_run* runs, int nruns, const floa
         taken[run.slot] = 1;
         M += run.len;
     }
-    for (int r = 0; r < nruns; ++r) TGX_TRY(hold_slot(d, runs[r].slot, runs[r].start + runs[r].len));
-    const int M_pad = (int)((M + ROW_TILE - 1) / ROW_TILE * ROW_TILE);
-    // Rows and tiles: run after run; the tiles later in a run, which attend to more, first.
-    std::vector<uint32_t> pos(M_pad, TGX_SPARE), slot(M_pad, TGX_SPARE);
-    std::vector<PrefillTile> tiles;
+    plan.M = M;
+    plan.M_pad = (int)((M + ROW_TILE - 1) / ROW_TILE * ROW_TILE);
+    plan.pos.assign(plan.M_pad, TGX_SPARE);
+    plan.slot.assign(plan.M_pad, TGX_SPARE);
+    plan.tiles.clear();
     size_t row = 0;
     for (int r = 0; r < nruns; ++r) {
         const tgx_run& run = runs[r];
         for (uint32_t i = 0; i < run.len; ++i) {
-            pos[row + i] = run.start + i;
-            slot[row + i] = run.slot;
+            plan.pos[row + i] = run.start + i;
+            plan.slot[row + i] = run.slot;
         }
         for (uint32_t t0 = 0; t0 < run.len; t0 += ATTN_ROWS)
-            tiles.push_back(PrefillTile{(uint32_t)(row + t0), run.start + t0, std::min<uint32_t>(ATTN_ROWS, run.len - t0), run.slot});
+            plan.tiles.push_back(PrefillTile{(uint32_t)(row + t0), run.start + t0, std::min<uint32_t>(ATTN_ROWS, run.len - t0), run.slot});
         row += run.len;
     }
-    std::stable_sort(tiles.begin(), tiles.end(), [](const PrefillTile& a, const PrefillTile& b) {
+    std::stable_sort(plan.tiles.begin(), plan.tiles.end(), [](const PrefillTile& a, const PrefillTile& b) {
         return a.pos0 + a.count > b.pos0 + b.count;
     });
-    TGX_TRY(hold_rows(d, M_pad, (int)tiles.size()));
-    PrefillState& p = d->pf;
-    p.M = (int)M;
-    p.M_pad = M_pad;
-    p.ntiles = (int)tiles.size();
+    return TGX_OK;
+}
+
+tgx_status hold_runs(Decoder* d, const tgx_run* runs, int nruns) {
+    for (int r = 0; r < nruns; ++r) TGX_TRY(hold_slot(d, runs[r].slot, runs[r].start + runs[r].len));
+    return TGX_OK;
+}
+
+// The plan's tokens and tiles and the input into the tensors p points at, the padding rows the
+// kernels read before they write cleared (the input's; the attention writes only the runs' rows of
+// its output), then the kernels; on the context's stream, without waiting.
+tgx_status enqueue(Decoder* d, const Plan& plan, const PrefillState& p, const float* x, bool x_on_device) {
+    const size_t h = d->shape.hidden, att = (size_t)d->shape.heads * HEAD_DIM, M = plan.M, pad = plan.M_pad - M;
     hipStream_t st = d->ctx->stream;
     TGX_TRY(sync_slots(d));
-    TGX_HIP(hipMemcpyAsync(p.x, x, M * s.hidden * 4, x_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
-    if ((size_t)M_pad > M) TGX_HIP(hipMemsetAsync(p.x + M * s.hidden, 0, (M_pad - M) * s.hidden * 4, st));
-    TGX_HIP(hipMemcpyAsync(p.tok_pos, pos.data(), M_pad * 4, hipMemcpyHostToDevice, st));
-    TGX_HIP(hipMemcpyAsync(p.tok_slot, slot.data(), M_pad * 4, hipMemcpyHostToDevice, st));
-    TGX_HIP(hipMemcpyAsync(p.tiles, tiles.data(), tiles.size() * sizeof(PrefillTile), hipMemcpyHostToDevice, st));
+    TGX_HIP(hipMemcpyAsync(p.x, x, M * h * 4, x_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+    TGX_HIP(launch_fill_zero(p.x + M * h, pad * h * 4, st));
+    TGX_HIP(launch_fill_zero(p.attended + M * att, pad * att * 2, st));
+    TGX_HIP(hipMemcpyAsync(p.tok_pos, plan.pos.data(), plan.M_pad * 4, hipMemcpyHostToDevice, st));
+    TGX_HIP(hipMemcpyAsync(p.tok_slot, plan.slot.data(), plan.M_pad * 4, hipMemcpyHostToDevice, st));
+    TGX_HIP(hipMemcpyAsync(p.tiles, plan.tiles.data(), plan.tiles.size() * sizeof(PrefillTile), hipMemcpyHostToDevice, st));
     TGX_HIP(hipEventRecord(d->ev_start, st));
-    TGX_TRY(launch(d));
+    TGX_TRY(launch(d, p));
     TGX_HIP(hipEventRecord(d->ev_end, st));
+    return TGX_OK;
+}
+
+size_t whole(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
+// The bytes of a prefill's tensors for `rows` rows and `tiles` tiles, each 256-byte aligned.
+size_t tensor_bytes(const Shape& s, size_t rows, size_t tiles) {
+    const size_t h = s.hidden, att = (size_t)s.heads * HEAD_DIM;
+    return 4 * whole(rows * h * 4) + whole(rows * h * 2) + whole(rows * h / 128 * 4) + 2 * whole(rows * att * 2) +
+           whole(rows * (size_t)s.inner * 2) + 2 * whole(rows * 4) + whole(tiles * sizeof(PrefillTile));
+}
+
+// The tensors laid one after another from `base`.
+void carve(const Shape& s, size_t rows, size_t tiles, unsigned char* base, PrefillState& p) {
+    const size_t h = s.hidden, att = (size_t)s.heads * HEAD_DIM;
+    size_t at = 0;
+    auto take = [&](auto*& ptr, size_t bytes) {
+        ptr = reinterpret_cast<std::remove_reference_t<decltype(ptr)>>(base + at);
+        at += whole(bytes);
+    };
+    take(p.x, rows * h * 4);
+    take(p.h, rows * h * 4);
+    take(p.mid, rows * h * 4);
+    take(p.out, rows * h * 4);
+    take(p.normed, rows * h * 2);
+    take(p.row_sq, rows * h / 128 * 4);
+    take(p.q, rows * att * 2);
+    take(p.attended, rows * att * 2);
+    take(p.mlp, rows * (size_t)s.inner * 2);
+    take(p.tok_pos, rows * 4);
+    take(p.tok_slot, rows * 4);
+    take(p.tiles, tiles * sizeof(PrefillTile));
+}
+
+}  // namespace
+
+size_t prefill_bytes(const Decoder* d) {
+    size_t n = 0;
+    for (const auto& b : d->pf.allocations) n += b.bytes;
+    return n;
+}
+
+tgx_status prefill_device(Decoder* d, const tgx_run* runs, int nruns, const float* x, bool x_on_device) {
+    if (!x) return fail(TGX_E_ARG, "null x");
+    Plan plan;
+    TGX_TRY(make_plan(d, runs, nruns, plan));
+    TGX_TRY(hold_runs(d, runs, nruns));
+    TGX_TRY(hold_rows(d, plan.M_pad, (int)plan.tiles.size()));
+    PrefillState& p = d->pf;
+    p.M = (int)plan.M;
+    p.M_pad = plan.M_pad;
+    p.ntiles = (int)plan.tiles.size();
+    return enqueue(d, plan, p, x, x_on_device);
+}
+
+tgx_status prefill_runs_noalloc(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out) {
+    if (!x || !out) return fail(TGX_E_ARG, "null x or out");
+    Plan plan;
+    TGX_TRY(make_plan(d, runs, nruns, plan));
+    void* base = d->ctx->scratch;
+    if (!base) return fail(TGX_E_HIP, "the device has no prefill scratch");
+    const Shape& s = d->shape;
+    const size_t need = tensor_bytes(s, plan.M_pad, plan.tiles.size());
+    if (need > PREFILL_SCRATCH_BYTES) {
+        size_t most = 0;  // positions a call of one run takes at this shape
+        for (size_t rows = ROW_TILE; tensor_bytes(s, rows, rows / ATTN_ROWS + 1) <= PREFILL_SCRATCH_BYTES; rows += ROW_TILE) most = rows;
+        return fail(TGX_E_SHAPE, std::to_string(plan.M) + " positions take " + std::to_string(need) +
+                                     " bytes of tensors, past the scratch's " + std::to_string(PREFILL_SCRATCH_BYTES) +
+                                     " (up to " + std::to_string(most) + " positions a call at this shape)");
+    }
+    TGX_TRY(hold_runs(d, runs, nruns));
+    PrefillState p;
+    carve(s, plan.M_pad, plan.tiles.size(), (unsigned char*)base, p);
+    p.M = (int)plan.M;
+    p.M_pad = plan.M_pad;
+    p.ntiles = (int)plan.tiles.size();
+    TGX_TRY(enqueue(d, plan, p, x, false));
+    hipStream_t st = d->ctx->stream;
+    TGX_HIP(hipMemcpyAsync(out, p.out, plan.M * s.hidden * 4, hipMemcpyDeviceToHost, st));
+    TGX_HIP(hipStreamSynchronize(st));
     return TGX_OK;
 }
 
@@ -172,7 +274,7 @@ tgx_status prefill_launch(Decoder* d, int times) {
     if (times <= 0) return fail(TGX_E_ARG, "times");
     hipStream_t st = d->ctx->stream;
     TGX_HIP(hipEventRecord(d->ev_start, st));
-    for (int i = 0; i < times; ++i) TGX_TRY(launch(d));
+    for (int i = 0; i < times; ++i) TGX_TRY(launch(d, d->pf));
     TGX_HIP(hipEventRecord(d->ev_end, st));
     TGX_HIP(hipEventRecord(d->ev_done, st));
     d->pending = true;

@@ -16,6 +16,9 @@
 
 #include <math.h>
 
+#include <algorithm>
+#include <mutex>
+
 namespace tgx {
 
 namespace {
@@ -633,6 +636,53 @@ hipError_t allow(const void* kernel, size_t device_lds) {
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// The prefill's scratch for callers that cannot allocate (tgx_prefill_runs_noalloc): one array of
+// PREFILL_SCRATCH_BYTES on each GPU the library runs on, held until the process ends. In host code
+// `scratch` names a host-side stand-in, not the device's array: host code reaches the array only
+// through the address prefill_scratch_address found for the device.
+static __device__ __align__(256) unsigned char scratch[PREFILL_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_lock;
+void* scratch_at[MAX_DEVICES] = {};
+}  // namespace
+
+hipError_t prefill_scratch_address(int device, void** out) {
+    *out = nullptr;
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> hold(scratch_lock);
+    if (!scratch_at[device]) {
+        int current = -1;
+        hipError_t e = hipGetDevice(&current);
+        if (e != hipSuccess) return e;
+        if (current != device) return hipErrorInvalidDevice;  // the caller makes the device current
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        scratch_at[device] = p;
+    }
+    *out = scratch_at[device];
+    return hipSuccess;
+}
+
+// Zeroes `count` 16-byte words at p: a kernel, not hipMemsetAsync, so that a caller may record it
+// into a graph.
+__global__ void __launch_bounds__(256) fill_zero(uint4* __restrict__ p, size_t count) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) p[i] = make_uint4(0, 0, 0, 0);
+}
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
+    if (bytes % 16 || (uintptr_t)p % 16) return hipErrorInvalidValue;
+    const size_t count = bytes / 16;
+    if (count == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 1024);
+    fill_zero<<<blocks, 256, 0, stream>>>((uint4*)p, count);
+    return hipGetLastError();
+}
 
 hipError_t prefill_prepare(size_t device_lds) {
     hipError_t e;

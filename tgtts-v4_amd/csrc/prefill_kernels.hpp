@@ -61,4 +61,13 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
                           const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer = nullptr);
 hipError_t prefill_prepare(size_t device_lds);
 
+// The size of each GPU's prefill scratch (tgx_prefill_runs_noalloc's tensors): 32 MiB, which at
+// the backbone's shape (hidden 1024, inner 4096, 16 heads) holds 1024 positions a call.
+constexpr size_t PREFILL_SCRATCH_BYTES = (size_t)32 << 20;
+// The device address of `device`'s scratch, looked up (hipGetSymbolAddress) on the first call for
+// the device, which must be current then, and kept for the process.
+hipError_t prefill_scratch_address(int device, void** out);
+// Zeroes `bytes` (a multiple of 16, 16-byte aligned) at p with a kernel on `stream`.
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+
 }  // namespace tgx

@@ -108,11 +108,13 @@ tgx_status context_create(int device, Context** out) {
     ctx->lds_bytes = ctx->prop.sharedMemPerBlock;
     e = decode_prepare(ctx->lds_bytes);
     if (e == hipSuccess) e = prefill_prepare(ctx->lds_bytes);
+    // The device is current: the prefill scratch's address on it, kept for the process.
+    if (e == hipSuccess) e = prefill_scratch_address(device, &ctx->scratch);
     if (e != hipSuccess) {
         hipStreamDestroy(ctx->stream);
         delete ctx;
-        return fail(TGX_E_HIP, std::string("allowing ") + std::to_string(ctx->prop.sharedMemPerBlock) +
-                                   " bytes of LDS: " + hipGetErrorString(e));
+        return fail(TGX_E_HIP, std::string("preparing the kernels (") + std::to_string(ctx->prop.sharedMemPerBlock) +
+                                   " bytes of LDS, the prefill scratch): " + hipGetErrorString(e));
     }
     if (std::strncmp(ctx->prop.gcnArchName, "gfx950", 6) != 0) {
         std::string arch = ctx->prop.gcnArchName;

@@ -35,6 +35,7 @@ struct Context {
     hipStream_t stream = nullptr;
     hipDeviceProp_t prop{};
     size_t lds_bytes = 0;  // LDS a workgroup may take
+    void* scratch = nullptr;  // the device's prefill scratch (PREFILL_SCRATCH_BYTES), its device address
 };
 
 // decode::Shape, checked against what the kernels cover.
@@ -159,6 +160,11 @@ tgx_status prefill_runs(Decoder* d, const tgx_run* runs, int nruns, const float*
 // when x_on_device; the output, [rows of the runs in order][hidden] f32, left in d->pf.out.
 tgx_status prefill_device(Decoder* d, const tgx_run* runs, int nruns, const float* x, bool x_on_device);
 tgx_status prefill_launch(Decoder* d, int times);
+// prefill_runs with the tensors in the context's scratch: allocates no device memory; refuses
+// (TGX_E_SHAPE) runs whose tensors pass PREFILL_SCRATCH_BYTES. Calls that overlap on one GPU race.
+tgx_status prefill_runs_noalloc(Decoder* d, const tgx_run* runs, int nruns, const float* x, float* out);
+// Device bytes the prefill's own tensors hold (grown by the longest prefill_runs so far).
+size_t prefill_bytes(const Decoder* d);
 void prefill_release(Decoder* d);
 tgx_status decoder_timings(Decoder* d, int max, tgx_timing* out, int* n);
 tgx_status decoder_read_cache(Decoder* dec, uint32_t slot, uint32_t positions, float* k, float* v);

@@ -137,6 +137,7 @@ EXPORTS = [
     "tgx_prefill_run",
     "tgx_prefill_runs",
     "tgx_prefill_launch",
+    "tgx_prefill_runs_noalloc",
     "tgx_euler_steps",
     "tgx_sampler_create",
     "tgx_sampler_destroy",
@@ -265,6 +266,7 @@ def library() -> ctypes.CDLL:
     lib.tgx_prefill_run.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, P, P]
     lib.tgx_prefill_runs.argtypes = [P, ctypes.POINTER(_Run), ctypes.c_int, P, P]
     lib.tgx_prefill_launch.argtypes = [P, ctypes.c_int]
+    lib.tgx_prefill_runs_noalloc.argtypes = [P, ctypes.POINTER(_Run), ctypes.c_int, P, P]
     FP = ctypes.POINTER(ctypes.c_float)
     lib.tgx_euler_steps.argtypes = [ctypes.c_int, ctypes.c_int, FP, FP, ctypes.POINTER(ctypes.c_int)]
     lib.tgx_sampler_create.argtypes = [P, ctypes.POINTER(_Shape), ctypes.POINTER(_PatchShape), ctypes.POINTER(P)]
@@ -633,6 +635,17 @@ class Decoder:
             arr[i].slot, arr[i].start, arr[i].len = slot, start, n
         out = np.empty_like(x)
         _check(library().tgx_prefill_runs(self._h, arr, len(runs), _ptr(x), _ptr(out)))
+        return out
+
+    def prefill_runs_noalloc(self, runs: Sequence[tuple], x: np.ndarray) -> np.ndarray:
+        """prefill_runs with its tensors in the GPU's fixed scratch array, allocating no device
+        memory (tgx_prefill_runs_noalloc): the same outputs and cache writes."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        arr = (_Run * len(runs))()
+        for i, (slot, start, n) in enumerate(runs):
+            arr[i].slot, arr[i].start, arr[i].len = slot, start, n
+        out = np.empty_like(x)
+        _check(library().tgx_prefill_runs_noalloc(self._h, arr, len(runs), _ptr(x), _ptr(out)))
         return out
 
     def prefill_launch(self, times: int = 1) -> None:
