@@ -87,6 +87,19 @@ __device__ __forceinline__ void lds_landed(uint4 (&v)[N]) {
         v[i] = __builtin_bit_cast(uint4, t);
     }
 }
+// The values lds_read16 gave, usable once a wait for every LDS read before it has passed (an
+// asm s_waitcnt lgkmcnt(0) of the caller's): each passed through an asm the compiler must run
+// after that point, and no wait of its own.
+template <int N>
+__device__ __forceinline__ void lds_arrived(uint4 (&v)[N]) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        u32x4 t = __builtin_bit_cast(u32x4, v[i]);
+        asm volatile("" : "+v"(t));
+        v[i] = __builtin_bit_cast(uint4, t);
+    }
+}
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");

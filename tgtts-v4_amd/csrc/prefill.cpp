@@ -13,7 +13,6 @@ namespace tgx {
 namespace {
 
 constexpr int ROW_TILE = 256;  // the GEMM's rows per workgroup
-constexpr int ATTN_ROWS = 32;  // the attention's positions per workgroup
 
 template <typename T>
 tgx_status prefill_alloc(Decoder* d, T** out, size_t count) {
@@ -146,6 +145,7 @@ tgx_status make_plan(Decoder* d, const tgx_run* runs, int nruns, Plan& plan) {
     plan.pos.assign(plan.M_pad, TGX_SPARE);
     plan.slot.assign(plan.M_pad, TGX_SPARE);
     plan.tiles.clear();
+    const uint32_t tile = (uint32_t)prefill_attention_tile(s.heads / s.kv_heads);  // positions a workgroup
     size_t row = 0;
     for (int r = 0; r < nruns; ++r) {
         const tgx_run& run = runs[r];
@@ -153,8 +153,8 @@ tgx_status make_plan(Decoder* d, const tgx_run* runs, int nruns, Plan& plan) {
             plan.pos[row + i] = run.start + i;
             plan.slot[row + i] = run.slot;
         }
-        for (uint32_t t0 = 0; t0 < run.len; t0 += ATTN_ROWS)
-            plan.tiles.push_back(PrefillTile{(uint32_t)(row + t0), run.start + t0, std::min<uint32_t>(ATTN_ROWS, run.len - t0), run.slot});
+        for (uint32_t t0 = 0; t0 < run.len; t0 += tile)
+            plan.tiles.push_back(PrefillTile{(uint32_t)(row + t0), run.start + t0, std::min<uint32_t>(tile, run.len - t0), run.slot});
         row += run.len;
     }
     std::stable_sort(plan.tiles.begin(), plan.tiles.end(), [](const PrefillTile& a, const PrefillTile& b) {
@@ -249,7 +249,8 @@ tgx_status prefill_runs_noalloc(Decoder* d, const tgx_run* runs, int nruns, cons
     const size_t need = tensor_bytes(s, plan.M_pad, plan.tiles.size());
     if (need > PREFILL_SCRATCH_BYTES) {
         size_t most = 0;  // positions a call of one run takes at this shape
-        for (size_t rows = ROW_TILE; tensor_bytes(s, rows, rows / ATTN_ROWS + 1) <= PREFILL_SCRATCH_BYTES; rows += ROW_TILE) most = rows;
+        const size_t tile = (size_t)prefill_attention_tile(s.heads / s.kv_heads);
+        for (size_t rows = ROW_TILE; tensor_bytes(s, rows, rows / tile + 1) <= PREFILL_SCRATCH_BYTES; rows += ROW_TILE) most = rows;
         return fail(TGX_E_SHAPE, std::to_string(plan.M) + " positions take " + std::to_string(need) +
                                      " bytes of tensors, past the scratch's " + std::to_string(PREFILL_SCRATCH_BYTES) +
                                      " (up to " + std::to_string(most) + " positions a call at this shape)");

@@ -448,7 +448,9 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                 }
                 const int m = m0 + j;
                 if (head < H) {
-                    uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    // q scaled by scale log2(e), the units the attention's softmax takes.
+                    const float qs = log2_scale(a.scale);
+                    uint2 packed = make_uint2(pack_bf16x2(v[0] * qs, v[1] * qs), pack_bf16x2(v[2] * qs, v[3] * qs));
                     *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * HEAD_DIM + d0) = packed;
                     continue;
                 }
@@ -513,33 +515,158 @@ __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* 
 }
 
 // ---------------------------------------------------------------------------------------------
+// The prefill attention's online softmax, with a reference moved lazily. q comes scaled by
+// scale log2(e) (the q/k/v epilogue), and the score MFMA's accumulator starts at -r, so that a
+// block's scores arrive as s - r for the column's reference r, in the units v_exp_f32 (2^x) takes:
+// P = 2^(s - r), in bf16. r moves only when a column's block maximum passes r + LAZY_SHIFT (and
+// on block 0, which every column sees first), the column's o and l then rescaled; otherwise the
+// block costs no subtract and no rescale. P <= 2^LAZY_SHIFT, and o and l stay in f32. A column
+// whose reference stays computes the same bits whether or not others of its wave move theirs
+// (it subtracts 0 and scales by 1), so that a position's result never depends on its neighbours.
+// The values past `vlast` read as zero (as OnlineSoftmax's).
+constexpr float LAZY_SHIFT = 8.0f;
+
+// The largest of three floats in one instruction (fmaxf would quiet each operand first).
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// The value fragments of a block (the A operand of O^T = V^T P, value_index) past `vlast` zeroed:
+// lane 16 g + d % 16 of fragment 2 dt + ks holds in its slot j the position
+// 32 ks + 16 (j / 4) + 4 g + j % 4; word w holds slots 2 w and 2 w + 1.
+__device__ __forceinline__ void zero_values_past(uint4 (&vf)[8], uint32_t p0, uint32_t vlast) {
+    const uint32_t g = (uint32_t)(threadIdx.x % WAVE) / 16;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        uint32_t keep[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t p = p0 + 32 * ks + 16 * (w / 2) + 4 * g + 2 * (w % 2);
+            keep[w] = (p <= vlast ? 0x0000ffffu : 0u) | (p + 1 <= vlast ? 0xffff0000u : 0u);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            uint4& f = vf[dt * 2 + ks];
+            f.x &= keep[0];
+            f.y &= keep[1];
+            f.z &= keep[2];
+            f.w &= keep[3];
+        }
+    }
+}
+
+struct LazySoftmax {
+    f32x4 neg_r = {0.f, 0.f, 0.f, 0.f};  // -r in each slot: the score MFMA's accumulator input
+    f32x4 lsum = {0.f, 0.f, 0.f, 0.f};   // l, the column's sum of P (every slot alike)
+    f32x4 o[4] = {};
+
+    // s: the block's scores less r; vf: its values, zeroed past the last position any column sees.
+    // MASK: keys past the column's position `pos` count for nothing; FIRST: block 0.
+    template <bool MASK, bool FIRST>
+    __device__ __forceinline__ void block(f32x4 (&s)[4], const uint4 (&vf)[8], uint32_t p0, uint32_t pos) {
+        const int lane = threadIdx.x % WAVE;
+        if (MASK) {
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (p0 + pt * 16 + (lane / 16) * 4 + i > pos) s[pt][i] = -INFINITY;
+        }
+        float mx = max3(s[0][0], s[0][1], s[0][2]);
+        mx = max3(mx, s[0][3], s[1][0]);
+        mx = max3(mx, s[1][1], s[1][2]);
+        mx = max3(mx, s[1][3], s[2][0]);
+        mx = max3(mx, s[2][1], s[2][2]);
+        mx = max3(mx, s[2][3], s[3][0]);
+        mx = max3(mx, s[3][1], s[3][2]);
+        mx = fmaxf(mx, s[3][3]);
+        if (FIRST || __builtin_amdgcn_ballot_w64(mx > LAZY_SHIFT) != 0) {
+            // The columns' maxima (each over its four lanes); those past the shift, or all on the
+            // first block, move r to it.
+            float cm = fmaxf(mx, lane_xor16(mx));
+            cm = fmaxf(cm, lane_xor32(cm));
+            const float d = (FIRST || cm > LAZY_SHIFT) ? cm : 0.f;
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) s[pt] -= d;
+            neg_r -= d;
+            if (!FIRST) {
+                const float f = __builtin_amdgcn_exp2f(-d);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[dt] *= f;
+                lsum *= f;
+            }
+        }
+        uint4 pf[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const f32x4 a = s[2 * ks], b = s[2 * ks + 1];
+            pf[ks] = make_uint4(pack_bf16x2(__builtin_amdgcn_exp2f(a[0]), __builtin_amdgcn_exp2f(a[1])),
+                                pack_bf16x2(__builtin_amdgcn_exp2f(a[2]), __builtin_amdgcn_exp2f(a[3])),
+                                pack_bf16x2(__builtin_amdgcn_exp2f(b[0]), __builtin_amdgcn_exp2f(b[1])),
+                                pack_bf16x2(__builtin_amdgcn_exp2f(b[2]), __builtin_amdgcn_exp2f(b[3])));
+        }
+        // Column sums of P (every row of ones^T P is the sum; bf16 1.0 is 0x3f80) and O^T += V^T P,
+        // each accumulator's two products apart, the other four between them.
+        const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            lsum = mfma16(ones, pf[ks], lsum);
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16(vf[dt * 2 + ks], pf[ks], o[dt]);
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------------------------
 // prefill_attention: workgroup (tile, kv): the tile's positions (up to 32, 32 / WAVES to a wave)
 // for the `group` query heads KV head kv serves. Columns of the MFMA are (position, head) pairs,
 // 16 / group positions to a column group, CG column groups to a wave. The slot's blocks from 0 to
 // the tile's last position are staged through LDS in turn; each column keeps its running maximum,
 // sum and output (attention_rows.comp:71-116).
+// A workgroup's tile: ATTN_TILE positions of a run, except for 8 query heads to a KV head, where it
+// takes 16 positions with four waves, so that two workgroups share a CU: their barriers are their
+// own, and one's softmax runs beside the other's products.
 constexpr int ATTN_TILE = 32;
+constexpr int ATTN_TILE_8 = 16;
+// The attention's ring of key-and-value stages: a stage is one block (16 KiB), ATTN_STAGES of them,
+// up to ATTN_STAGES - 2 in flight beyond the two being taken.
+constexpr int ATTN_STAGE = 2 * KV_TILE / 8;  // uint4
+constexpr int ATTN_STAGES = 4;
 
-template <int WAVES, int CG>
-__global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a, const uint16_t* __restrict__ q,
+template <int TILE, int WAVES, int CG>
+__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(2))) prefill_attention(PrefillArgs a, const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ kvpool,
                                                                  uint16_t* __restrict__ attended,
                                                                  const PrefillTile* __restrict__ tiles) {
     constexpr int THREADS = WAVES * WAVE;
-    constexpr int TOK = ATTN_TILE / WAVES;     // positions to a wave
+    constexpr int TOK = TILE / WAVES;          // positions to a wave
     constexpr int per_col = TOK / CG;          // positions to a column group
     constexpr int group = 16 / per_col;
-    constexpr int STAGE = 2 * KV_TILE / 8;     // uint4 of a block's keys then values
-    constexpr int PER_THREAD = STAGE / THREADS;
-    __shared__ uint4 stage[2][STAGE];
+    constexpr int NS = ATTN_STAGES;
+    constexpr int LOADS = ATTN_STAGE / 64 / WAVES;  // 1 KiB loads a wave makes of a stage
+    static_assert(LOADS * 64 * WAVES == ATTN_STAGE, "a stage in whole 1 KiB loads");
+    // The ring of NS stages, each a block's key tile then value tile as they lie in the cache,
+    // then the slot's block ids.
+    extern __shared__ uint4 attn_ring[];
+    uint32_t* block_ids = reinterpret_cast<uint32_t*>(attn_ring + NS * ATTN_STAGE);
     const PrefillTile tile = tiles[blockIdx.x];
     const int kv = blockIdx.y;
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    // The wave's index, uniform: the branches on it below are the whole wave's.
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    const int lane = threadIdx.x % WAVE;
     const int H = a.heads, KV = a.kv_heads;
     const int col = lane % 16;
     const uint32_t last = tile.pos0 + tile.count - 1;
     const int blocks = (int)(last / BLOCK_TOKENS) + 1;
 
+    // The slot's blocks 0 .. blocks - 1 (a block the slot does not hold reads as block 0, never
+    // reached by a position the run holds).
+    for (int i = threadIdx.x; i < blocks; i += THREADS) {
+        const uint32_t blk = a.table[(size_t)tile.slot * a.max_blocks + i];
+        block_ids[i] = blk < (uint32_t)a.nblocks ? blk : 0u;
+    }
     uint4 qf[CG][2];
     uint32_t cpos[CG];
 #pragma unroll
@@ -551,61 +678,97 @@ __global__ void __launch_bounds__(WAVES * WAVE) prefill_attention(PrefillArgs a,
 #pragma unroll
         for (int ds = 0; ds < 2; ++ds) qf[cg][ds] = load16(q + (row * H + head) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
     }
-    OnlineSoftmax sm[CG];
-    const float scale_log2 = log2_scale(a.scale);
+    // The ids and q in place (this wait and barrier are the compiler's own: no load to LDS is in
+    // flight yet).
+    __syncthreads();
+
+    // Block bi into stage bi % NS, straight from the cache into LDS: wave w copies bytes
+    // 1 KiB (LOADS w + j) of the block's 16 KiB, lane l its 16 bytes 16 l. Past the last block the
+    // last is loaded again (never read), so that every wave makes LOADS loads a block and its
+    // count in flight says which stages have landed. The id is read by an LDS read of its own,
+    // which the compiler does not order behind the loads to LDS in flight.
+    auto fetch = [&](int bi) __attribute__((always_inline)) {
+        const uint32_t* at = block_ids + min(bi, blocks - 1);
+        uint32_t id;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(id) : "v"(lds_offset(at)) : "memory");
+        const uint32_t blk = __builtin_amdgcn_readfirstlane(id);
+        const uint16_t* src = kvpool + ((size_t)blk * KV + kv) * 2 * KV_TILE;
+        uint4* dst = attn_ring + (bi % NS) * ATTN_STAGE;
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) load_to_lds(src + (size_t)(w * LOADS + j) * 512 + lane * 8, dst + (w * LOADS + j) * 64);
+    };
+
+    LazySoftmax sm[CG];
     // The wave's first position: blocks wholly at or below it need no mask.
     const uint32_t first = tile.pos0 + w * TOK;
 
-    auto fetch = [&](int bi, uint4 (&r)[PER_THREAD]) {
-        const uint32_t blk = a.table[(size_t)tile.slot * a.max_blocks + bi];
-        const uint16_t* src = kvpool + ((size_t)(blk < (uint32_t)a.nblocks ? blk : 0) * KV + kv) * 2 * KV_TILE;
+    // The ring: block bi's keys are in registers when step bi starts. Its values are read from
+    // LDS while the score MFMAs run; then block bi + 1's stage is waited for (the barrier also says
+    // every wave is done with stage bi - 1, which block bi + NS - 1 takes) and its keys read while
+    // the softmax and the value MFMAs of block bi run.
+    auto read8 = [&](const uint4* src, uint4 (&f)[8]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < PER_THREAD; ++j) r[j] = load16(src + (size_t)(threadIdx.x + j * THREADS) * 8);
+        for (int i = 0; i < 8; ++i) f[i] = lds_read16(src + i * 64 + lane);
     };
-    uint4 reg[PER_THREAD];
-    fetch(0, reg);
 #pragma unroll
-    for (int j = 0; j < PER_THREAD; ++j) stage[0][threadIdx.x + j * THREADS] = reg[j];
-    __syncthreads();
+    for (int bi = 0; bi < NS - 1; ++bi) fetch(bi);
+    wait_vm<LOADS * (NS - 2)>();
+    stage_barrier();
+    uint4 kf[8], vf[8];
+    read8(attn_ring, kf);
+    lds_landed(kf);
     for (int bi = 0; bi < blocks; ++bi) {
-        const int buf = bi % 2;
-        if (bi + 1 < blocks) fetch(bi + 1, reg);
-        uint4 kf[8], vf[8];
+        const uint4* st = attn_ring + (bi % NS) * ATTN_STAGE;
+        read8(st + KV_TILE / 8, vf);
+        // The first halves of every tile's product before any second half: the MFMAs a tile's
+        // second half waits on are done by the time it issues.
+        f32x4 s[CG][4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) kf[i] = stage[buf][i * 64 + lane];
+        for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vf[i] = stage[buf][KV_TILE / 8 + i * 64 + lane];
+            for (int pt = 0; pt < 4; ++pt) s[cg][pt] = mfma16(kf[pt * 2], qf[cg][0], sm[cg].neg_r);
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) s[cg][pt] = mfma16(kf[pt * 2 + 1], qf[cg][1], s[cg][pt]);
+        // Stage bi + 1 landed for every wave: no more than the NS - 3 blocks fetched after it in
+        // flight for this one, then the barrier.
+        wait_vm<LOADS * (NS - 3)>();
+        stage_barrier();
+        fetch(bi + NS - 1);  // its id's LDS read waits for every LDS read before it: vf has landed
+        lds_arrived(vf);
+        const bool more = bi + 1 < blocks;
+        if (more) read8(attn_ring + ((bi + 1) % NS) * ATTN_STAGE, kf);
         const uint32_t p0 = (uint32_t)bi * BLOCK_TOKENS;
         const bool full = p0 + BLOCK_TOKENS - 1 <= first;
+        // Values past the tile's last position read as zero (attention_rows.comp:1-13): every
+        // position up to it was written by this run or before it; the cache may hold anything
+        // past it, NaN included, and 0 NaN is NaN.
+        if (p0 + BLOCK_TOKENS - 1 > last) zero_values_past(vf, p0, last);
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
-            f32x4 s[4];
-#pragma unroll
-            for (int pt = 0; pt < 4; ++pt) {
-                s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(kf[pt * 2 + ds], qf[cg][ds], s[pt]);
+            if (bi == 0) {
+                if (full)
+                    sm[cg].template block<false, true>(s[cg], vf, p0, cpos[cg]);
+                else
+                    sm[cg].template block<true, true>(s[cg], vf, p0, cpos[cg]);
+            } else if (full) {
+                sm[cg].template block<false, false>(s[cg], vf, p0, cpos[cg]);
+            } else {
+                sm[cg].template block<true, false>(s[cg], vf, p0, cpos[cg]);
             }
-            // Values past the tile's last position read as zero (attention_rows.comp:1-13): every
-            // position up to it was written by this run or before it.
-            if (full)
-                sm[cg].template block<false>(s, vf, p0, cpos[cg], last, scale_log2);
-            else
-                sm[cg].template block<true>(s, vf, p0, cpos[cg], last, scale_log2);
         }
-        if (bi + 1 < blocks) {
-#pragma unroll
-            for (int j = 0; j < PER_THREAD; ++j) stage[1 - buf][threadIdx.x + j * THREADS] = reg[j];
-        }
-        __syncthreads();
+        if (more) lds_landed(kf);
     }
+    // No load into this workgroup's LDS may still be in flight when its waves end.
+    wait_vm<0>();
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
         const int tok = w * TOK + cg * per_col + col / group;
         if (tok >= (int)tile.count) continue;
         const int head = kv * group + col % group;
         const size_t row = tile.row0 + tok;
-        const float inv = 1.0f / sm[cg].l;
+        const float inv = 1.0f / sm[cg].lsum[0];
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
             const int d = dt * 16 + (lane / 16) * 4;
@@ -684,6 +847,8 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
     return hipGetLastError();
 }
 
+int prefill_attention_tile(int group) { return group == 8 ? ATTN_TILE_8 : ATTN_TILE; }
+
 hipError_t prefill_prepare(size_t device_lds) {
     hipError_t e;
     if ((e = allow((const void*)prefill_gemm<EPI_QKV, QKV_ROWS, QKV_TM>, device_lds)) != hipSuccess) return e;
@@ -691,6 +856,11 @@ hipError_t prefill_prepare(size_t device_lds) {
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16, O_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4, DOWN_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16, DOWN_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_attention<ATTN_TILE, 2, 1>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_attention<ATTN_TILE, 4, 1>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_attention<ATTN_TILE, 8, 1>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_attention<ATTN_TILE_8, 4, 2>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_attention<ATTN_TILE, 8, 4>, device_lds)) != hipSuccess) return e;
     return allow((const void*)prefill_gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>, device_lds);
 }
 
@@ -699,6 +869,8 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
     const dim3 rows4((a.M_pad + 3) / 4);
     const int group = a.heads / a.kv_heads;
     const int qkv_rows = (a.heads + 2 * a.kv_heads) * HEAD_DIM;
+    // The attention's ring and the slot's block ids.
+    const size_t attn_lds = (size_t)ATTN_STAGES * ATTN_STAGE * sizeof(uint4) + (size_t)a.max_blocks * sizeof(uint32_t);
     // Layer 0's input norm; each later norm's input (the rows times the gain, and their sums of
     // squares) comes from the projection before it, the rows' scales applied by the GEMM after.
     if (nlayers > 0)
@@ -711,11 +883,11 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
                      l == 0 ? nullptr : b.row_sq, nullptr, nullptr, nullptr};
         gemm<EPI_QKV, QKV_ROWS, QKV_TM>("prefill_qkv", a, qkv, stream, timer);
         switch (group) {
-            case 1: dispatch("prefill_attention", prefill_attention<2, 1>, dim3(b.ntiles, a.kv_heads), dim3(2 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 2: dispatch("prefill_attention", prefill_attention<4, 1>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 4: dispatch("prefill_attention", prefill_attention<8, 1>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 8: dispatch("prefill_attention", prefill_attention<8, 2>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 16: dispatch("prefill_attention", prefill_attention<8, 4>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), 0, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 1: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 2, 1>, dim3(b.ntiles, a.kv_heads), dim3(2 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 2: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 4, 1>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 4: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 8, 1>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 8: dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 4, 2>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
+            case 16: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 8, 4>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
             default: return hipErrorInvalidValue;
         }
         if (L.od_rows != 4 && L.od_rows != 16) return hipErrorInvalidValue;

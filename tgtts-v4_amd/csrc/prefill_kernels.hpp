@@ -47,7 +47,7 @@ struct PrefillBuffers {
     float* h;           // residual stream, f32 [M_pad][hidden]
     float* mid;         // after the attention, f32
     uint16_t* normed;   // RMSNorm of the stream, bf16 [M_pad][hidden] in fragment order (act_index)
-    uint16_t* q;        // bf16 [M_pad][heads][64]
+    uint16_t* q;        // bf16 [M_pad][heads][64], times scale log2(e) (the attention softmax's units)
     uint16_t* attended; // bf16 [M_pad][heads 64] in fragment order
     uint16_t* mlp;      // bf16 [M_pad][inner] in fragment order
     float* row_sq;      // a norm's input's sums of squares over each 128 columns, [M_pad][hidden / 128]
@@ -60,6 +60,9 @@ struct PrefillBuffers {
 hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int nlayers, const float* final_norm,
                           const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer = nullptr);
 hipError_t prefill_prepare(size_t device_lds);
+// The positions of a run the attention takes to a workgroup (its PrefillTiles' most) for `group`
+// query heads to a KV head.
+int prefill_attention_tile(int group);
 
 // The size of each GPU's prefill scratch (tgx_prefill_runs_noalloc's tensors): 32 MiB, which at
 // the backbone's shape (hidden 1024, inner 4096, 16 heads) holds 1024 positions a call.
