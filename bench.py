@@ -323,6 +323,16 @@ def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
     }
 
 
+def host_threads() -> int:
+    """The host cores the CPU baseline uses: those the process may run on, at most 16 (the GPU
+    box's share of its host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
 def cpu_baseline(weights, seconds: float):
     """The fp32 CPU path (the oracle in float32, OpenMP over the host's cores) on the same
     24-layer stack at batch 1, decode steps from position 256 of a zero-filled cache."""
@@ -330,8 +340,7 @@ def cpu_baseline(weights, seconds: float):
     from tgx.synth import StackSpec, embeddings
 
     spec = StackSpec(layers=24, dtype="bf16", seed=0)
-    threads = os.cpu_count() or 1
-    oracle.set_threads(threads)
+    oracle.set_threads(host_threads())
     st = oracle.Stack(spec, weights, PROMPT + 512, "f32")
     x = embeddings(7, "bench.cpu", 1, spec.hidden)[0]
     t0 = time.perf_counter()
@@ -350,6 +359,68 @@ def cpu_baseline(weights, seconds: float):
         "sample": f"{n} fp32 decode steps of the 24-layer stack at batch 1, positions {PROMPT + 1}..{PROMPT + n} "
                   f"(keys and values below {PROMPT} zero), {dt:.1f} s on {oracle.threads()} OpenMP threads",
     }
+
+
+def cpu_rows(weights, seconds: float) -> dict:
+    """The other rows of the CPU path beside the GPU's, each on a bounded sample of its workload
+    (the oracle in float32: decode row by row in C with OpenMP, prefill layer by layer with numpy's
+    float32 BLAS; the patch step with its LocDiT in numpy float64): decode steps/s at 16 and 64
+    requests, prefill tok/s of one 2048-position run, patch steps/s at 16 requests."""
+    import oracle
+    import patch_oracle as po
+    from tgx.synth import StackSpec, embeddings, encoder_weights, lm_side_weights, sampler_weights
+
+    spec = StackSpec(layers=24, dtype="bf16", seed=0)
+    oracle.set_threads(host_threads())
+    out = {}
+    st = oracle.Stack(spec, weights, 2048 + 64, "f32")
+    for rows in (16, 64):
+        ctxs = [int(c) for c in np.random.default_rng(rows).integers(64, 1025, rows)]
+        x = embeddings(7, "bench.cpu", rows, spec.hidden)
+        t0, n = time.perf_counter(), 0
+        while n == 0 or time.perf_counter() - t0 < seconds:
+            for r in range(rows):  # a step: every request once, at its own position
+                st.decode(ctxs[r] + n, x[r])
+            n += 1
+        dt = time.perf_counter() - t0
+        out[f"decode_batch{rows}"] = {"value": n / dt, "unit": "steps/s", "tokens_per_s": n * rows / dt,
+                                      "sample": f"{n} steps of {rows} requests (contexts U[64,1024]), {dt:.1f} s"}
+    length = 2048
+    x = embeddings(9, "bench.cpu.prefill", length, spec.hidden)
+    t0 = time.perf_counter()
+    st.prefill_rows(0, x)
+    dt = time.perf_counter() - t0
+    out["prefill"] = {"value": length / dt, "unit": "tok/s",
+                      "sample": f"one {length}-position run (of the 8 x 2048 workload), float32 BLAS, {dt:.1f} s"}
+    # The patch step at 16 requests: the encoder over the patch before, both LMs a position on, the
+    # heads, the sampler's 9 evaluations over both sequences of every request.
+    rows = 16
+    base, res = StackSpec(layers=24, seed=0), StackSpec(layers=8, seed=1)
+    w = lm_side_weights(base, res, 1024, 1024, 256)
+    dw, ew = sampler_weights(StackSpec(layers=4, seed=2), 64), encoder_weights(StackSpec(layers=4, seed=3), 64)
+    lms = [oracle.Stack(s_, {k[len(p_):]: v for k, v in w.items() if k.startswith(p_)}, 256, "f32", rope=(p_ == "base_lm."))
+           for s_, p_ in ((base, "base_lm."), (res, "residual_lm."))]
+    shape = po.StackShape(layers=4)
+    rng = np.random.default_rng(5)
+    cond = rng.standard_normal((rows, 64, 4))
+    noise = rng.standard_normal((rows, 64, 4))
+    sampling = np.array([[1.0, 2.0]] * rows)
+    t0, n = time.perf_counter(), 0
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        emb = po.encode(ew, shape, 64, 4, cond)
+        embed = po.linear(w, "enc_to_lm_proj", emb)
+        base_out = np.stack([lms[0].decode(128 + n, embed[r]) for r in range(rows)])
+        _, lv = po.quantizer(w, base_out, 9)
+        lm_hidden, residual_in, to_dit, _, _ = po.heads_after_levels(w, lv, embed)
+        res_out = np.stack([lms[1].decode(128 + n, residual_in[r]) for r in range(rows)])
+        mu = np.concatenate([to_dit, po.linear(w, "res_to_dit_proj", res_out)], axis=-1).reshape(rows, 2, 1024)
+        _, cond = po.sample(dw, shape, 64, 4, 10, mu, cond, noise, sampling)
+        n += 1
+    dt = time.perf_counter() - t0
+    out["patch_step"] = {"value": n / dt, "unit": "patch steps/s",
+                         "sample": f"{n} patch steps of {rows} requests (encoder, 24 + 8 layers, heads, 4-layer LocDiT "
+                                   f"x 9 evaluations; LocDiT in numpy float64), {dt:.1f} s"}
+    return out
 
 
 COPY_BYTES = 256 << 20
@@ -474,7 +545,7 @@ def main() -> int:
             r.pop("shape")
             for label, k in sorted(r["kernels"].items(), key=lambda kv: -kv[1]["per_step_us"]):
                 log(f"  [{rows:2d}] {label:16s} {k['avg_us']:8.2f} us/launch {k['per_step_us']:8.1f} us/step {k['GB_s'] or 0:8.1f} GB/s")
-            batches[str(rows)] = {k: r[k] for k in ("steps_per_s", "ms_per_step", "hbm_fraction", "kernel_sum_us")}
+            batches[str(rows)] = {k: r[k] for k in ("steps_per_s", "ms_per_step", "hbm_fraction", "kernel_sum_us", "step_bytes_mid")}
             batches[str(rows)]["kernels_us"] = {k: round(v["avg_us"], 3) for k, v in r["kernels"].items()}
             batches[str(rows)]["tokens_per_s"] = r["steps_per_s"] * rows
             batches[str(rows)]["contexts"] = "U[64,1024] seeded, 200 steps"
@@ -527,7 +598,16 @@ def main() -> int:
             "traffic": measured_traffic(label, f"batch {args.batch}"),
             "bytes_per_launch": k["bytes_per_launch"],
             "avg_us": round(k["avg_us"], 3),
+            "of_stream_floor": round(achieved / floor_kernel["GB_s"], 4),
         }
+
+    # The stream-read floor (stream_read.comp, as decode_timing.rs:430-441 reports it): the step's
+    # weight bytes read once by a kernel that does nothing else, at its best of 20 launches; and
+    # one gate/up projection's bytes, the size of the step's largest kernel.
+    floor = ctx.stream_read(shape.weight_bytes(), 20)
+    floor_kernel = ctx.stream_read(kernel_bytes(shape, "gemv_gate_up", args.batch, 0), 50)
+    log(f"stream-read floor: {floor['GB_s']:.0f} GB/s over {floor['bytes']} bytes, "
+        f"{floor_kernel['GB_s']:.0f} GB/s over {floor_kernel['bytes']} bytes ({floor_kernel['best_ms'] * 1e3:.2f} us)")
 
     kernels = head["kernels"]
     by_bytes = max(kernels.items(), key=lambda kv: kv[1]["bytes_per_launch"] * kv[1]["per_step_us"] / kv[1]["avg_us"])
@@ -540,6 +620,9 @@ def main() -> int:
         try:
             cpu = cpu_baseline(weights, args.cpu_seconds)
             log(f"cpu baseline: {cpu['value']:.2f} steps/s on {cpu['cores']} threads")
+            cpu["rows"] = cpu_rows(weights, args.cpu_seconds / 2)
+            for name, r in cpu["rows"].items():
+                log(f"cpu baseline {name}: {r['value']:.3f} {r['unit']} ({r['sample']})")
         except Exception as e:  # the baseline is reported, never required
             log(f"cpu baseline failed: {e}")
 
@@ -567,6 +650,9 @@ def main() -> int:
             "kernels_per_step": 121,
         },
         "hbm_fraction_step": round(head["hbm_fraction"], 4),
+        "stream_read_floor": {"GB_s": round(floor["GB_s"], 1), "bytes": floor["bytes"], "best_ms": round(floor["best_ms"], 4),
+                              "kernel_size_GB_s": round(floor_kernel["GB_s"], 1), "kernel_size_bytes": floor_kernel["bytes"],
+                              "step_at_floor_ms": round(step_bytes(shape, [c + args.steps // 2 for c in headline_contexts]) / (floor["GB_s"] * 1e9) * 1e3, 4)},
         "gpu_ms_per_step": round(head["gpu_ms_per_step"], 4),
         "roofline": roofline,
         "roofline_longest": roofline_longest,

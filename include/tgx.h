@@ -66,6 +66,12 @@ void tgx_context_destroy(tgx_context* ctx);
 /* Context::report. */
 tgx_status tgx_context_report(const tgx_context* ctx, tgx_device_report* out);
 
+/* The stream-read floor (kernels/glsl/stream_read.comp:1-23, as decode_timing.rs:430-441 reports
+ * it): a buffer of `bytes` (rounded down to 32 KiB) read once a launch, 16 bytes a load, `times`
+ * launches each timed by events; the best and the mean milliseconds. The bandwidth the decode
+ * kernels are held to. Allocates the buffer for the call. */
+tgx_status tgx_stream_read(tgx_context* ctx, size_t bytes, int times, float* best_ms, float* mean_ms);
+
 /* ---- the decode step: crates/graph/src/decode.rs ---- */
 
 /* decode::Shape (decode.rs:65-82). `capacity` is the most positions one request (slot) may

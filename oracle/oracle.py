@@ -160,25 +160,25 @@ class Stack:
         float64 matrix products (prefill.rs:137-504 runs the same op order a layer at a time):
         thousands of positions in seconds where position by position takes minutes. The products
         sum in BLAS's order, so it agrees with `prefill` to float64 rounding, not bit for bit
-        (tests/test_oracle.py pins it there). float64 only; writes the caches as `prefill`."""
-        if self.precision != "f64":
-            raise ValueError("prefill_rows runs in float64")
+        (tests/test_oracle.py pins it there). Runs in the stack's precision (float32 for "f32", the
+        CPU baseline's); writes the caches as `prefill`."""
+        dt = self.dt
         s = self.spec
-        x = np.asarray(x, dtype=np.float64)
+        x = np.asarray(x, dtype=dt)
         n = x.shape[0]
         if start < 0 or n <= 0 or start + n > self.capacity:
             raise ValueError(f"oracle prefill of {n} from {start} in {self.capacity}")
         H, KV, d, I = s.heads, s.kv_heads, s.head_dim, s.inner
         group, half, end = H // KV, d // 2, start + n
         pos = np.arange(start, end)
-        co = self.cos[pos].astype(np.float64)[:, None, :]  # [n][1][d/2]
-        si = self.sin[pos].astype(np.float64)[:, None, :]
+        co = self.cos[pos].astype(dt)[:, None, :]  # [n][1][d/2]
+        si = self.sin[pos].astype(dt)[:, None, :]
         rope = self.shape.rope != 0
-        scale = 1.0 / np.sqrt(float(d))
+        scale = dt(1.0 / np.sqrt(float(d)))
         future = np.arange(end)[None, :] > pos[:, None]  # [n][end]: keys past each position
 
         def norm(v, g):
-            return v / np.sqrt(np.mean(v * v, axis=-1, keepdims=True) + s.eps) * g.astype(np.float64)
+            return v / np.sqrt(np.mean(v * v, axis=-1, keepdims=True) + dt(s.eps)) * g.astype(dt)
 
         def rotate(v):  # [n][heads][d]: a' = a cos - c sin, c' = c cos + a sin
             a, c = v[..., :half], v[..., half:]
@@ -186,7 +186,7 @@ class Stack:
 
         hs = x.copy()
         for l in range(s.layers):
-            W = lambda name: self.w[f"layers.{l}.{name}"].astype(np.float64)
+            W = lambda name: self.w[f"layers.{l}.{name}"].astype(dt)
             qkv = norm(hs, self.w[f"layers.{l}.input_layernorm"]) @ W("qkv_proj").T
             q = qkv[:, : H * d].reshape(n, H, d)
             k = qkv[:, H * d : (H + KV) * d].reshape(n, KV, d)
@@ -195,7 +195,7 @@ class Stack:
                 q, k = rotate(q), rotate(k)
             self.k[l, :, start:end] = k.transpose(1, 0, 2)
             self.v[l, :, start:end] = v.transpose(1, 0, 2)
-            att = np.empty((n, H, d))
+            att = np.empty((n, H, d), dtype=dt)
             for h in range(H):
                 keys, values = self.k[l, h // group, :end], self.v[l, h // group, :end]
                 sc = (q[:, h] @ keys.T) * scale
@@ -206,7 +206,7 @@ class Stack:
             hs = hs + att.reshape(n, H * d) @ W("o_proj").T
             gu = norm(hs, self.w[f"layers.{l}.post_attention_layernorm"]) @ W("gate_up_proj").T
             gate, up = gu[:, :I], gu[:, I:]
-            hs = hs + (gate / (1.0 + np.exp(-gate)) * up) @ W("down_proj").T
+            hs = hs + (gate / (dt(1.0) + np.exp(-gate)) * up) @ W("down_proj").T
         return norm(hs, self.norm)
 
 

@@ -280,6 +280,24 @@ def test_the_layer_by_layer_prefill_is_the_position_by_position_one(tiny, rope):
     assert np.max(np.abs(s - want[:55])) > 1e-3 * scale
 
 
+def test_the_layer_by_layer_prefill_in_float32_is_the_float32_path(tiny):
+    """prefill_rows in float32 (the CPU baseline's prefill) against the position-by-position
+    float32 path and the float64 one, to float32 rounding."""
+    import oracle
+    from tgx.synth import embeddings
+
+    spec, w = tiny
+    x = embeddings(6, "x", 40, spec.hidden)
+    want = oracle.Stack(spec, w, 64, "f64").prefill(0, x.astype(np.float64))
+    steps = oracle.Stack(spec, w, 64, "f32").prefill(0, x)
+    rows = oracle.Stack(spec, w, 64, "f32")
+    got = rows.prefill_rows(0, x)
+    assert got.dtype == np.float32 and rows.k.dtype == np.float32
+    scale = np.max(np.abs(want))
+    assert np.max(np.abs(got - steps)) <= 1e-4 * scale
+    assert np.max(np.abs(got - want)) <= 1e-4 * scale
+
+
 def test_a_stack_without_rope_and_its_defects(tiny):
     import oracle
     from tgx.synth import embeddings

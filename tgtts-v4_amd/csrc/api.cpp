@@ -43,6 +43,51 @@ tgx_status tgx_context_report(const tgx_context* ctx, tgx_device_report* out) {
     return TGX_OK;
 }
 
+tgx_status tgx_stream_read(tgx_context* ctx, size_t bytes, int times, float* best_ms, float* mean_ms) {
+    clear_error();
+    if (!ctx || !best_ms || !mean_ms) return fail(TGX_E_ARG, "null context or output");
+    const size_t unit = stream_read_unit();
+    if (bytes < unit || times <= 0) return fail(TGX_E_ARG, "stream read of " + std::to_string(bytes) + " bytes " + std::to_string(times) + " times");
+    bytes -= bytes % unit;
+    Context* c = ctx->ctx;
+    TGX_HIP(hipSetDevice(c->device));
+    void* data = nullptr;
+    uint32_t* out = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    auto done = [&](tgx_status st) {
+        if (data) hipFree(data);
+        if (out) hipFree(out);
+        if (a) hipEventDestroy(a);
+        if (b) hipEventDestroy(b);
+        return st;
+    };
+    auto check = [&](hipError_t e, const char* what) {
+        return e == hipSuccess ? TGX_OK : fail(TGX_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    };
+    tgx_status st = check(hipMalloc(&data, bytes), "hipMalloc");
+    if (st == TGX_OK) st = check(hipMalloc((void**)&out, bytes / unit * 4 * sizeof(uint32_t)), "hipMalloc");
+    if (st == TGX_OK) st = check(hipMemsetAsync(data, 0x5a, bytes, c->stream), "hipMemsetAsync");
+    if (st == TGX_OK) st = check(hipEventCreate(&a), "hipEventCreate");
+    if (st == TGX_OK) st = check(hipEventCreate(&b), "hipEventCreate");
+    if (st == TGX_OK) st = check(launch_stream_read(data, bytes, out, c->stream), "stream_read");  // warm
+    float best = 0.f, total = 0.f;
+    for (int i = 0; i < times && st == TGX_OK; ++i) {
+        st = check(hipEventRecord(a, c->stream), "hipEventRecord");
+        if (st == TGX_OK) st = check(launch_stream_read(data, bytes, out, c->stream), "stream_read");
+        if (st == TGX_OK) st = check(hipEventRecord(b, c->stream), "hipEventRecord");
+        if (st == TGX_OK) st = check(hipEventSynchronize(b), "hipEventSynchronize");
+        float ms = 0.f;
+        if (st == TGX_OK) st = check(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+        total += ms;
+        if (i == 0 || ms < best) best = ms;
+    }
+    if (st == TGX_OK) {
+        *best_ms = best;
+        *mean_ms = total / times;
+    }
+    return done(st);
+}
+
 tgx_status tgx_shape_check(const tgx_shape* shape, const tgx_batch* batch) {
     clear_error();
     Shape s;

@@ -634,6 +634,35 @@ hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const Re
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------
+// stream_read: the bandwidth the decode kernels are held to (kernels/glsl/stream_read.comp:1-23):
+// every thread reads STREAM_LOADS 16-byte pieces a grid's width apart, all issued before any is
+// used, and each wave writes one word of their XOR, so that no read can be left out.
+constexpr int STREAM_THREADS = 256;
+constexpr int STREAM_LOADS = 8;
+
+__global__ void __launch_bounds__(STREAM_THREADS) stream_read(const uint4* __restrict__ data, uint32_t* __restrict__ out) {
+    const size_t stride = (size_t)gridDim.x * STREAM_THREADS;
+    const size_t at = (size_t)blockIdx.x * STREAM_THREADS + threadIdx.x;
+    uint4 v[STREAM_LOADS];
+#pragma unroll
+    for (int i = 0; i < STREAM_LOADS; ++i) v[i] = data[at + i * stride];
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < STREAM_LOADS; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    for (int off = 32; off >= 1; off >>= 1) x ^= (uint32_t)__shfl_xor((int)x, off, WAVE);
+    if (threadIdx.x % WAVE == 0) out[blockIdx.x * (STREAM_THREADS / WAVE) + threadIdx.x / WAVE] = x;
+}
+
+size_t stream_read_unit() { return (size_t)STREAM_THREADS * STREAM_LOADS * sizeof(uint4); }
+
+hipError_t launch_stream_read(const void* data, size_t bytes, uint32_t* out, hipStream_t stream) {
+    if (bytes == 0 || bytes % stream_read_unit()) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(bytes / stream_read_unit());
+    stream_read<<<grid, STREAM_THREADS, 0, stream>>>((const uint4*)data, out);
+    return hipGetLastError();
+}
+
 int decode_tiles(int rows) { return (rows + 15) / 16; }
 
 int decode_residual_rows(int rows) { return rows <= 16 ? 4 : 16; }

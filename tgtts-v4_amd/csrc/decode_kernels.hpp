@@ -90,4 +90,9 @@ hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const Re
 hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out, uint32_t* positions,
                              int advance, hipStream_t stream, DispatchTimer* timer = nullptr);
 
+// The stream-read floor's kernel (kernels/glsl/stream_read.comp): `bytes` (a multiple of
+// stream_read_unit()) read once, one word a wave of their XOR into out (bytes / 4096 words).
+size_t stream_read_unit();
+hipError_t launch_stream_read(const void* data, size_t bytes, uint32_t* out, hipStream_t stream);
+
 }  // namespace tgx

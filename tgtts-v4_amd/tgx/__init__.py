@@ -112,6 +112,7 @@ EXPORTS = [
     "tgx_context_create",
     "tgx_context_destroy",
     "tgx_context_report",
+    "tgx_stream_read",
     "tgx_decoder_create",
     "tgx_decoder_destroy",
     "tgx_decoder_load",
@@ -240,6 +241,7 @@ def library() -> ctypes.CDLL:
     lib.tgx_context_destroy.argtypes = [P]
     lib.tgx_context_destroy.restype = None
     lib.tgx_context_report.argtypes = [P, ctypes.POINTER(_Report)]
+    lib.tgx_stream_read.argtypes = [P, ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
     lib.tgx_decoder_create.argtypes = [P, ctypes.POINTER(_Shape), ctypes.POINTER(_Batch), ctypes.POINTER(P)]
     lib.tgx_decoder_destroy.argtypes = [P]
     lib.tgx_decoder_destroy.restype = None
@@ -471,6 +473,15 @@ class Context:
             "memory_bytes": r.memory_bytes,
             "wavefront": r.wavefront,
         }
+
+    def stream_read(self, nbytes: int, times: int = 10) -> dict:
+        """The stream-read floor (stream_read.comp): `nbytes` read once a launch, the best and mean
+        of `times` launches; GB/s at the best."""
+        best, mean = ctypes.c_float(), ctypes.c_float()
+        _check(library().tgx_stream_read(self._h, nbytes, times, ctypes.byref(best), ctypes.byref(mean)))
+        unit = 256 * 8 * 16
+        read = nbytes - nbytes % unit
+        return {"bytes": read, "best_ms": best.value, "mean_ms": mean.value, "GB_s": read / (best.value * 1e-3) / 1e9}
 
     def close(self) -> None:
         if self._h:
