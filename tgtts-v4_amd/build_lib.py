@@ -34,7 +34,9 @@ HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-Wno-unus
 SOURCES = {
     "decode_kernels.hip": DEVICE_FLAGS,
     "prefill_kernels.hip": DEVICE_FLAGS,
-    "local_kernels.hip": DEVICE_FLAGS,
+    # The ring GEMM's k-block loop unrolls whole (its registers are indexed by k-block), 128
+    # k-blocks for down_proj: past the unroller's default budget for a pragma.
+    "local_kernels.hip": DEVICE_FLAGS + ["-mllvm", "-pragma-unroll-threshold=200000"],
     "heads_kernels.hip": DEVICE_FLAGS,
     "runtime.cpp": HOST_FLAGS,
     "prefill.cpp": HOST_FLAGS,

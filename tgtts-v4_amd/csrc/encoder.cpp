@@ -140,6 +140,7 @@ tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     A(&e->partial, (size_t)LOCAL_MAX_PARTS * Mp * h);
     A(&e->out, Mp * h);
     A(&e->normed, Mp * h);
+    A(&e->row_sq, Mp * (h / LOCAL_SQ_COLS));
     A(&e->q, Mp * att);
     A(&e->k, Mp * KV * HEAD_DIM);
     A(&e->v, Mp * KV * HEAD_DIM);
@@ -208,7 +209,7 @@ hipError_t encoder_enqueue(Encoder* e, const float* patch, float* dst, int* disp
         const Layer& L = e->layers[l];
         layers[l] = LocalLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm};
     }
-    const LocalBuffers b{e->x0, e->x, e->h, e->normed, e->q, e->k, e->v, e->attended, e->mlp, e->partial, e->out,
+    const LocalBuffers b{e->x0, e->x, e->h, e->normed, e->row_sq, e->q, e->k, e->v, e->attended, e->mlp, e->partial, e->out,
                          e->o_parts, e->down_parts};
     if (err == hipSuccess) err = launch_local_stack(a, layers.data(), e->shape.layers, e->final_norm, b, st, nullptr);
     // The learned token's output, the first of each sequence (encoder.rs:113-114).

@@ -4,15 +4,19 @@
 //
 //   local_gemm      C = X W^T over up to a few hundred tokens, bf16 in, f32 accumulate: up to 64
 //                   tokens straight from memory into each wave's registers beside its strips of
-//                   W; more in 64-token tiles held in LDS, read by the waves of a workgroup that
-//                   each stream their own strips of W. The epilogue fused: RoPE at each token's
-//                   place in its sequence (local_qkv_rope.comp), SiLU(gate) up
-//                   (local_gate_up.comp), or the f32 sums of one part of the columns
-//                   (local_partial.comp)
+//                   W (local_gemm_direct); more in 64-token tiles streamed through a ring of LDS
+//                   slots, read by the waves of a workgroup that each stream their own strips of
+//                   W (local_gemm_ring). The epilogue fused: the row's RMSNorm scale with RoPE at
+//                   each token's place in its sequence (local_qkv_rope.comp), the same scale with
+//                   SiLU(gate) up (local_gate_up.comp), the f32 sums of one part of the columns
+//                   (local_partial.comp), or over more than 64 tokens the parts added, the
+//                   residual added and the next norm's input with its sums of squares
+//                   (local_add_norm.comp)
 //   local_attention every token of a sequence attends to every token of it, a wave to a
 //                   sequence and query head, both products on MFMA (local_attention.comp)
-//   local_add_norm  residual + the parts' sums in their order, then RMSNorm (local_add_norm.comp,
-//                   local_norm.comp)
+//   local_add_norm  residual + the parts' sums in their order, then the next norm's input
+//                   (local_add_norm.comp, local_norm.comp): up to 64 tokens, and the first and
+//                   final norms
 //   local_embed     a linear layer over a patch's frames into tokens, and tokens copied beside
 //                   them (local_embed.comp)
 //   dit_euler       out_proj's velocities, CFG-Zero* guidance and the Euler step (dit_euler.comp)
@@ -31,7 +35,7 @@ namespace tgx {
 
 namespace {
 
-enum LocalEpilogue { LEPI_QKV = 0, LEPI_PARTIAL = 1, LEPI_SILU = 2 };
+enum LocalEpilogue { LEPI_QKV = 0, LEPI_PARTIAL = 1, LEPI_SILU = 2, LEPI_ADD = 3 };
 
 struct LocalGemm {
     const uint16_t* w;  // 16-row tiles of [N][K]
@@ -40,6 +44,60 @@ struct LocalGemm {
     float* partial;     // LEPI_PARTIAL: f32 [parts][M_pad][N]
     uint16_t* mlp;      // LEPI_SILU: bf16 [M_pad][N / 2]
     uint16_t *q, *k, *v;
+    // LEPI_QKV, LEPI_SILU: X is an RMSNorm's input times its gain; row m's sums of squares
+    // [M_pad][K / LOCAL_SQ_COLS] give the row's scale, applied to its sums.
+    const float* row_sq;
+    // LEPI_ADD (local_gemm_ring): sum = residual + the parts' sums, and with next_gain, the next
+    // norm's input: normed = sum next_gain in bf16 and sum's sums of squares into sum_sq.
+    const float* residual;
+    float* sum;
+    const float* next_gain;
+    uint16_t* normed;
+    float* sum_sq;
+};
+
+// The sums of squares of a row: one to each LOCAL_SQ_COLS columns (16 at hidden 1024), in
+// column order. Each is four sums of 16 columns added as (a + b) + (c + d), each of those four of
+// 4 columns, added as (a + b) + (c + d) again, each of those 4 squared and added in order from
+// zero by fused multiply-adds: the order local_add_norm's lanes and local_gemm_ring's epilogue
+// both keep, so that a row's scale is the same bits whichever wrote it.
+constexpr int SQ_PARTS = 1024 / LOCAL_SQ_COLS;
+__device__ __forceinline__ float squares4(float a, float b, float c, float d) {
+    float s = 0.f;
+    s = fmaf(a, a, s);
+    s = fmaf(b, b, s);
+    s = fmaf(c, c, s);
+    return fmaf(d, d, s);
+}
+// 1 / rms of a row from its SQ_PARTS sums of squares, added in order.
+__device__ __forceinline__ float row_scale_of(const float4 (&p)[SQ_PARTS / 4], int K, float eps) {
+    float total = 0.f;
+#pragma unroll
+    for (int i = 0; i < SQ_PARTS / 4; ++i) {
+        total += p[i].x;
+        total += p[i].y;
+        total += p[i].z;
+        total += p[i].w;
+    }
+    return 1.0f / sqrtf(total / (float)K + eps);
+}
+// A row's sums of squares, loaded ahead of the GEMM's own loads and pinned there (nothing
+// computed from them moves above the point where they are settled).
+struct RowSq {
+    float4 p[SQ_PARTS / 4];
+    __device__ void load(const float* row_sq, int m) {
+#pragma unroll
+        for (int i = 0; i < SQ_PARTS / 4; ++i) p[i] = *reinterpret_cast<const float4*>(row_sq + (size_t)m * SQ_PARTS + 4 * i);
+    }
+    __device__ void settle() {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int i = 0; i < SQ_PARTS / 4; ++i) {
+            u32x4 t = __builtin_bit_cast(u32x4, p[i]);
+            asm volatile("" : "+v"(t));
+            p[i] = __builtin_bit_cast(float4, t);
+        }
+    }
 };
 
 // A wave's strips of W for work unit u: SW strips in a row, or for the gate/up projection (SW 2)
@@ -57,10 +115,11 @@ __device__ __forceinline__ void local_strips(int u, int N, int (&strip)[SW]) {
 }
 
 // The epilogue of one 16 x 16 block: W rows 16 strip + 4 (lane / 16) + i against token
-// mt + lane % 16. SILU takes the gate's block in `acc` and the up's in `up`.
+// mt + lane % 16, whose row scale is rs (QKV, SILU). SILU takes the gate's block in `acc` and the
+// up's in `up`.
 template <int EPI>
 __device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm& g, int strip, int mt, const f32x4& acc,
-                                            const f32x4& up) {
+                                            const f32x4& up, float rs) {
     const int lane = threadIdx.x % WAVE, quad = lane / 16;
     const int m = mt + lane % 16;
     if (EPI == LEPI_PARTIAL) {
@@ -72,9 +131,12 @@ __device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm&
         const int inner = g.N / 2, n = strip * 16 + quad * 4;
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = acc[i] / (1.0f + __expf(-acc[i])) * up[i];
+        for (int i = 0; i < 4; ++i) {
+            const float gate = acc[i] * rs, u = up[i] * rs;
+            v[i] = gate / (1.0f + __expf(-gate)) * u;
+        }
         *reinterpret_cast<uint2*>(g.mlp + (size_t)m * inner + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-    } else {  // LEPI_QKV: a strip's rows pair as r, r + 8 (lanes l and l ^ 32)
+    } else if (EPI == LEPI_QKV) {  // a strip's rows pair as r, r + 8 (lanes l and l ^ 32)
         const int H = a.heads, KV = a.kv_heads;
         const bool second = quad >= 2;
         const int head = strip / 4, qtr = strip % 4;
@@ -83,7 +145,7 @@ __device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm&
         float own[4], other[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            own[i] = acc[i];
+            own[i] = acc[i] * rs;
             other[i] = lane_xor32(own[i]);
         }
         if (m >= a.M) return;
@@ -112,19 +174,25 @@ __device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm&
 
 template <int EPI, int SW, int TT>
 __device__ __forceinline__ void local_epilogue(const LocalArgs& a, const LocalGemm& g, const int (&strip)[SW], int m0,
-                                               const f32x4 (&acc)[SW][TT]) {
+                                               const f32x4 (&acc)[SW][TT], const float (&rs)[TT]) {
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
         if (EPI == LEPI_SILU) {
-            local_store<EPI>(a, g, strip[0], m0 + 16 * t, acc[0][t], acc[SW - 1][t]);
+            local_store<EPI>(a, g, strip[0], m0 + 16 * t, acc[0][t], acc[SW - 1][t], rs[t]);
         } else {
 #pragma unroll
-            for (int s = 0; s < SW; ++s) local_store<EPI>(a, g, strip[s], m0 + 16 * t, acc[s][t], acc[s][t]);
+            for (int s = 0; s < SW; ++s) local_store<EPI>(a, g, strip[s], m0 + 16 * t, acc[s][t], acc[s][t], rs[t]);
         }
     }
 }
 
-__device__ __forceinline__ uint4 load16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// A 16-byte load from global memory, as such: a pointer passed through an asm (WeightRing's)
+// is no longer known to be global, and a flat load might read LDS, so the compiler would wait for
+// every direct-to-LDS load in flight before issuing it.
+__device__ __forceinline__ uint4 load16(const uint16_t* p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(uint4, *(const __attribute__((address_space(1))) u32x4*)p);
+}
 // The scheduler may move nothing across this: every load above it is in flight before any value
 // is used (left to itself it sinks loads towards their use to save registers).
 __device__ __forceinline__ void all_issued() { __builtin_amdgcn_sched_barrier(0); }
@@ -171,6 +239,10 @@ __global__ void __launch_bounds__(TT * WAVE) local_gemm_direct(LocalArgs a, Loca
     const int kb0 = blockIdx.z * KBP;
     int strip[SW];
     local_strips<EPI, SW>(blockIdx.x, g.N, strip);
+    // The lane's token's sums of squares go first, the GEMM's loads behind them.
+    constexpr bool SCALED = EPI == LEPI_QKV || EPI == LEPI_SILU;
+    RowSq sq;
+    if (SCALED) sq.load(g.row_sq, 16 * t + lane % 16);
     WeightRing<SW, KBP, DEPTH> w;
     w.start(g, strip, kb0, lane);
     const uint16_t* xp = g.x + (size_t)(16 * t + lane % 16) * g.K + kb0 * 32 + (lane / 16) * 8;
@@ -181,6 +253,7 @@ __global__ void __launch_bounds__(TT * WAVE) local_gemm_direct(LocalArgs a, Loca
         xf[d] = load16(xp + d * 32);
     }
     all_issued();
+    if (SCALED) sq.settle();
     f32x4 acc[SW][1];
 #pragma unroll
     for (int s = 0; s < SW; ++s) acc[s][0] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -195,83 +268,169 @@ __global__ void __launch_bounds__(TT * WAVE) local_gemm_direct(LocalArgs a, Loca
         }
         all_issued();  // each k-block's refill stays where it is, DEPTH k-blocks ahead of its use
     }
-    local_epilogue<EPI, SW, 1>(a, g, strip, 16 * t, acc);
+    const float rs[1] = {SCALED ? row_scale_of(sq.p, g.K, a.eps) : 1.f};
+    local_epilogue<EPI, SW, 1>(a, g, strip, 16 * t, acc, rs);
 }
 
-// local_gemm_shared, for more tokens (M_pad a multiple of 64): a workgroup of 4 waves to 64 tokens
-// (4 token tiles) and 4 work units. The token tile goes through LDS in phases of LG_PHASE_KB
-// k-blocks ([4][LG_PHASE_KB][64 lanes] fragments of 16 bytes, 64 KiB, so that two workgroups fit a
-// CU), each landing by direct global-to-LDS loads; each wave streams its own strips of W into
-// registers, DEPTH k-blocks ahead, and reads the tokens' fragments from LDS a k-block ahead.
-// Grid (units / 4, M_pad / 64, parts).
-constexpr int LG_PHASE_KB = 16;
-constexpr int LG_RING = 24;  // k-blocks of W a wave of one strip has in flight
-constexpr size_t LG_SHARED_LDS = (size_t)4 * LG_PHASE_KB * 64 * sizeof(uint4);
+// local_gemm_ring, for more tokens (M_pad a multiple of 64): a workgroup of 4 waves to 64 tokens
+// (4 token tiles) and 4 work units, wave w taking unit 4 blockIdx.x + w against all four tiles.
+// A k-block's loads are a group: each wave's SW fragments of W, into registers (WeightRing), and
+// its token tile's fragment, straight from memory into a ring of RING LDS slots (4 KiB: the four
+// tiles' fragments of one k-block). The groups go out in k-block order RING ahead of their
+// products, so a wave's count of loads in flight says which of its groups have landed, and the
+// barrier after the wait says the same of every wave's; a wave reads a k-block's tiles from LDS
+// while it multiplies the k-block before. No wave ever waits for more than the group it needs
+// next. Each output is P chains of KBP k-blocks, the parts of local_gemm_direct in its order,
+// added in part order as local_add_norm adds them.
+// Grid (units / 4, M_pad / 64).
+constexpr int ring_depth(int sw) { return sw == 1 ? 16 : 12; }
+constexpr size_t ring_lds(int sw) { return (size_t)ring_depth(sw) * 4 * 64 * sizeof(uint4) + (64 + 4 * 64) * sizeof(float); }
 
-template <int EPI, int SW, int KBP>
-__global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2))) local_gemm_shared(LocalArgs a, LocalGemm g) {
-    static_assert(KBP % LG_PHASE_KB == 0, "whole phases");
-    constexpr int XL = LG_PHASE_KB;  // tile loads a wave a phase: 4 LG_PHASE_KB over 4 waves
-    // W's k-blocks in flight: LG_RING fragments of one strip, 8 k-blocks of two (as many as leave
-    // the registers of two workgroups to a CU), and as many as fit beside a phase's tile loads
-    // within the wave's count of loads.
-    constexpr int RING = SW == 1 ? LG_RING : 8;
-    constexpr int ROOM = (63 - XL) / SW < RING ? (63 - XL) / SW : RING;
-    constexpr int DEPTH = ROOM < KBP ? ROOM : KBP;
-    extern __shared__ uint4 xs[];  // [4][LG_PHASE_KB][64]
-    const int wv = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int m0 = blockIdx.y * 64, kb0 = blockIdx.z * KBP;
+// Waits until at most `n` of the wave's loads are in flight, `n` known when the loop is unrolled:
+// the compiler's own wait (wait_vm_seen), so that it knows the loads before those n have landed
+// and puts no wait of its own before their uses.
+template <int N>
+__device__ __forceinline__ void wait_vm_at_most(int n) {
+    if constexpr (N == 0) {
+        wait_vm_seen<0>();
+    } else {
+        if (n >= N)
+            wait_vm_seen<N>();
+        else
+            wait_vm_at_most<N - 1>(n);
+    }
+}
+
+template <int EPI, int SW, int KBP, int P>
+__global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2))) local_gemm_ring(LocalArgs a, LocalGemm g) {
+    constexpr int KB = KBP * P;
+    constexpr int RING = ring_depth(SW);
+    constexpr int GROUP = SW + 1;  // a wave's loads of a k-block
+    constexpr bool SCALED = EPI == LEPI_QKV || EPI == LEPI_SILU;
+    static_assert(KB > RING, "the ring fills before the first product");
+    static_assert(RING * GROUP + SQ_PARTS / 4 < 64, "the loads in flight fit the wave's count");
+    static_assert(EPI != LEPI_ADD || SW == 1, "a workgroup's columns are one span of a sum of squares");
+    extern __shared__ uint4 xs[];  // [RING][4 tiles][64 lanes]
+    float* scales = reinterpret_cast<float*>(xs + RING * 4 * 64);  // [64]: the tokens' row scales
+    float* sq_part = scales + 64;                                   // [4 waves][64 tokens]
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+    const int m0 = blockIdx.y * 64;
     int strip[SW];
     local_strips<EPI, SW>(blockIdx.x * 4 + wv, g.N, strip);
-    WeightRing<SW, KBP, DEPTH> w;
-    w.start(g, strip, kb0, lane);
-    w.fetch(0, DEPTH);
-    f32x4 acc[SW][4];
+    // The tokens' sums of squares (a lane to a token, in every wave, so that each wave's count of
+    // loads is the same) go out before the groups: the wait for the first group covers them.
+    RowSq sq;
+    if (SCALED) sq.load(g.row_sq, m0 + lane);
+    WeightRing<SW, KB, RING> w;
+    w.start(g, strip, 0, lane);
+    const uint16_t* xp = g.x + (size_t)(m0 + 16 * wv + lane % 16) * g.K + (lane / 16) * 8;
+    auto fetch = [&](int kb) __attribute__((always_inline)) {
+        w.fetch(kb, kb + 1);
+        load_to_lds(xp + kb * 32, &xs[((kb % RING) * 4 + wv) * 64]);
+    };
+#pragma unroll
+    for (int kb = 0; kb < RING; ++kb) fetch(kb);
+    all_issued();
+    f32x4 acc[P][SW][4];
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int s = 0; s < SW; ++s)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[p][s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Group 0 landed, every wave's; the scales into LDS, read after the barriers below. The store
+    // is an asm the compiler cannot see: a store it knew of might share bytes with the loads into
+    // the ring, for all it knows, and it would wait for every one of them before the first read.
+    wait_vm_seen<(RING - 1) * GROUP>();
+    if (SCALED) {
+        const float rs = row_scale_of(sq.p, g.K, a.eps);
+        if (wv == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(lds_offset(&scales[lane])), "v"(rs) : "memory");
+    }
+    stage_barrier();
+    uint4 xf[2][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xf[0][t] = lds_read16(&xs[t * 64 + lane]);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        const int b = kb % 2;
+        lds_landed(xf[b]);
+        if (kb + 1 < KB) {
+            // Group kb + 1 landed: the groups after it, up to kb + RING - 1, may be in flight. The
+            // barrier also says every wave has its fragments of k-block kb, whose slot the fetch
+            // below refills.
+            wait_vm_at_most<(RING - 2) * GROUP>(GROUP * (RING - 2 < KB - 2 - kb ? RING - 2 : KB - 2 - kb));
+            stage_barrier();
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xf[1 - b][t] = lds_read16(&xs[(((kb + 1) % RING) * 4 + t) * 64 + lane]);
+        }
+        const int r = kb % RING, p = kb / KBP;
+#pragma unroll
+        for (int s = 0; s < SW; ++s)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[p][s][t] = mfma16(w.wf[r][s], xf[b][t], acc[p][s][t]);
+        if (kb + RING < KB) fetch(kb + RING);  // into the W registers just multiplied
+        all_issued();
+    }
+    // The parts in part order.
+    f32x4 sum[SW][4];
 #pragma unroll
     for (int s = 0; s < SW; ++s)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 4; ++t) {
+            sum[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ph = 0; ph < KBP / LG_PHASE_KB; ++ph) {
-        if (ph > 0) stage_barrier();  // every wave is done with the last phase's tile
-#pragma unroll
-        for (int j = 0; j < XL; ++j) {
-            const int f = wv + 4 * j, t = f / LG_PHASE_KB, kb = ph * LG_PHASE_KB + f % LG_PHASE_KB;
-            load_to_lds(g.x + (size_t)(m0 + 16 * t + lane % 16) * g.K + (kb0 + kb) * 32 + (lane / 16) * 8, &xs[f * 64]);
+            for (int p = 0; p < P; ++p) sum[s][t] += acc[p][s][t];
         }
-        all_issued();
-        // The tile's phase has landed once nothing is in flight: a wait the compiler sees, so that
-        // it knows as much and waits for W's refills no more than their uses need (behind an asm
-        // wait it would wait for every load before the first use of any). The barrier says the
-        // same of every wave's part. The tile is read through asm (lds_read16), whose waits the
-        // kernel keeps itself.
-        wait_vm_seen<0>();
-        stage_barrier();
-        uint4 xf[2][4];
+    if (EPI != LEPI_ADD) {
+        float rs[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) xf[0][t] = lds_read16(&xs[(t * LG_PHASE_KB) * 64 + lane]);
+        for (int t = 0; t < 4; ++t) rs[t] = SCALED ? scales[16 * t + lane % 16] : 1.f;
+        local_epilogue<EPI, SW, 4>(a, g, strip, m0, sum, rs);
+        return;
+    }
+    // LEPI_ADD: the residual added; with next_gain, the next norm's input and each token's sum of
+    // squares over the wave's 16 columns (4 to a lane, then lanes l ^ 16, l ^ 32), the four
+    // waves' added through LDS into the span of the workgroup's 64 columns.
+    const int quad = lane / 16, n = strip[0] * 16 + quad * 4;
+    float4 gn = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (g.next_gain) gn = *reinterpret_cast<const float4*>(g.next_gain + n);
+    float4 r[4];
 #pragma unroll
-        for (int k = 0; k < LG_PHASE_KB; ++k) {
-            const int kb = ph * LG_PHASE_KB + k, r = kb % DEPTH, b = k % 2;
-            lds_landed(xf[b]);
-            if (k + 1 < LG_PHASE_KB) {
+    for (int t = 0; t < 4; ++t) r[t] = *reinterpret_cast<const float4*>(g.residual + (size_t)(m0 + 16 * t + lane % 16) * g.N + n);
 #pragma unroll
-                for (int t = 0; t < 4; ++t) xf[1 - b][t] = lds_read16(&xs[(t * LG_PHASE_KB + k + 1) * 64 + lane]);
-            }
-#pragma unroll
-            for (int s = 0; s < SW; ++s)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) acc[s][t] = mfma16(w.wf[r][s], xf[b][t], acc[s][t]);
-            if (kb + DEPTH < KBP) w.fetch(kb + DEPTH, kb + DEPTH + 1);
-            all_issued();  // each k-block's refill stays where it is, DEPTH k-blocks ahead of its use
+    for (int t = 0; t < 4; ++t) {
+        const int m = m0 + 16 * t + lane % 16;
+        float4 v;
+        v.x = r[t].x + sum[0][t][0];
+        v.y = r[t].y + sum[0][t][1];
+        v.z = r[t].z + sum[0][t][2];
+        v.w = r[t].w + sum[0][t][3];
+        if (m < a.M) {
+            *reinterpret_cast<float4*>(g.sum + (size_t)m * g.N + n) = v;
+            if (g.next_gain)
+                *reinterpret_cast<uint2*>(g.normed + (size_t)m * g.N + n) =
+                    make_uint2(pack_bf16x2(v.x * gn.x, v.y * gn.y), pack_bf16x2(v.z * gn.z, v.w * gn.w));
+        }
+        if (g.next_gain) {
+            float s4 = squares4(v.x, v.y, v.z, v.w);
+            s4 += lane_xor16(s4);
+            s4 += lane_xor32(s4);
+            if (quad == 0) sq_part[wv * 64 + 16 * t + lane] = s4;
         }
     }
-    local_epilogue<EPI, SW, 4>(a, g, strip, m0, acc);
+    if (!g.next_gain) return;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int m = m0 + threadIdx.x;
+        const float s = (sq_part[threadIdx.x] + sq_part[64 + threadIdx.x]) + (sq_part[128 + threadIdx.x] + sq_part[192 + threadIdx.x]);
+        if (m < a.M) g.sum_sq[(size_t)m * SQ_PARTS + blockIdx.x] = s;
+    }
 }
 
-// The GEMM of a projection: `units` work units of SW strips (gate/up: pairs of strips), each output
-// summed over the KBP k-blocks of its part. At most 64 tokens take the direct GEMM, more the
-// shared one.
+// The GEMM of a projection whose epilogue is one of QKV, SILU or PARTIAL: `units` work units of
+// SW strips (gate/up: pairs of strips), each output summed over the KBP k-blocks of its part. At
+// most 64 tokens take the direct GEMM, more the ring (QKV and SILU only: its parts are added in
+// the kernel, LEPI_ADD).
 template <int EPI, int SW, int KBP>
 void local_gemm(const char* label, const LocalArgs& a, const LocalGemm& g, int units, int parts, hipStream_t stream,
                 DispatchTimer* timer) {
@@ -285,14 +444,31 @@ void local_gemm(const char* label, const LocalArgs& a, const LocalGemm& g, int u
         }
         return;
     }
-    const dim3 grid(units / 4, a.M_pad / 64, parts);
-    dispatch(label, local_gemm_shared<EPI, SW, KBP>, grid, dim3(4 * WAVE), LG_SHARED_LDS, stream, timer, a, g);
+    if constexpr (EPI != LEPI_PARTIAL)
+        dispatch(label, local_gemm_ring<EPI, SW, KBP, 1>, dim3(units / 4, a.M_pad / 64), dim3(4 * WAVE), ring_lds(SW), stream,
+                 timer, a, g);
 }
 
-template <int EPI, int SW, int KBP>
-hipError_t local_gemm_lds() {
-    return hipFuncSetAttribute((const void*)local_gemm_shared<EPI, SW, KBP>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)LG_SHARED_LDS);
+// o_proj and down_proj over more than 64 tokens: the ring with the parts added and the residual
+// added in its epilogue (LEPI_ADD), 16 or 32 k-blocks to each of 2 or 4 parts.
+void local_gemm_add(const char* label, const LocalArgs& a, const LocalGemm& g, int kbp, int parts, hipStream_t stream,
+                    DispatchTimer* timer) {
+    const dim3 grid(g.N / 64, a.M_pad / 64), block(4 * WAVE);
+    const size_t lds = ring_lds(1);
+    if (kbp == 16 && parts == 2)
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 16, 2>, grid, block, lds, stream, timer, a, g);
+    else if (kbp == 32 && parts == 2)
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 32, 2>, grid, block, lds, stream, timer, a, g);
+    else if (kbp == 16 && parts == 4)
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 16, 4>, grid, block, lds, stream, timer, a, g);
+    else
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 32, 4>, grid, block, lds, stream, timer, a, g);
+}
+
+template <int EPI, int SW, int KBP, int P>
+hipError_t local_ring_lds() {
+    return hipFuncSetAttribute((const void*)local_gemm_ring<EPI, SW, KBP, P>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)ring_lds(SW));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -361,58 +537,74 @@ __global__ void __launch_bounds__(256) local_attention(LocalArgs a, const uint16
 }
 
 // ---------------------------------------------------------------------------------------------
-// local_add_norm: a wave to a token. sum = residual + the parts' sums in part order (written to
-// `sum` when given), then RMSNorm with gain g: lane l squares its hidden / 64 values in order, the
-// lanes added by a butterfly. FINAL writes the normed row in f32, else in bf16.
+// local_add_norm: a wave to a token, lane l to its columns 16 l .. 16 l + 15 (hidden 1024).
+// v = residual + the parts' sums in part order (written to `sum` when given). FINAL: RMSNorm with
+// gain g in f32 into `out` (lane l squares its values in order, the lanes added by a butterfly).
+// Else the next norm's input for the GEMM that applies the row's scale: normed = v g in bf16, and
+// v's sums of squares over each 64 columns into row_sq, in the order local_gemm_ring's epilogue
+// adds them (squares4 over 4 columns, (a + b) + (c + d) over a lane's 16, then over 4 lanes).
 template <bool FINAL>
 __global__ void __launch_bounds__(256) local_add_norm(LocalArgs a, const float* __restrict__ partial, int parts,
                                                       const float* __restrict__ residual, float* __restrict__ sum,
                                                       const float* __restrict__ gain, uint16_t* __restrict__ normed,
-                                                      float* __restrict__ out) {
+                                                      float* __restrict__ row_sq, float* __restrict__ out) {
     const int m = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (m >= a.M) return;
-    const int K = a.hidden, per = K / WAVE;  // 16 at hidden 1024
-    float v[32];
-    const int base = lane * per;
+    constexpr int K = 1024, PER = K / WAVE;
+    const int base = lane * PER;
+    float v[PER];
 #pragma unroll
-    for (int e = 0; e < 32; e += 4) {
-        if (e >= per) break;
+    for (int e = 0; e < PER; e += 4) {
         float4 r = *reinterpret_cast<const float4*>(residual + (size_t)m * K + base + e);
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int p = 0; p < parts; ++p) {
-            const float4 s = *reinterpret_cast<const float4*>(partial + ((size_t)p * a.M_pad + m) * K + base + e);
-            acc.x += s.x;
-            acc.y += s.y;
-            acc.z += s.z;
-            acc.w += s.w;
+        if (parts > 0) {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int p = 0; p < parts; ++p) {
+                const float4 s = *reinterpret_cast<const float4*>(partial + ((size_t)p * a.M_pad + m) * K + base + e);
+                acc.x += s.x;
+                acc.y += s.y;
+                acc.z += s.z;
+                acc.w += s.w;
+            }
+            r.x += acc.x;
+            r.y += acc.y;
+            r.z += acc.z;
+            r.w += acc.w;
         }
-        v[e] = r.x + acc.x;
-        v[e + 1] = r.y + acc.y;
-        v[e + 2] = r.z + acc.z;
-        v[e + 3] = r.w + acc.w;
-        if (sum) *reinterpret_cast<float4*>(sum + (size_t)m * K + base + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
+        v[e] = r.x;
+        v[e + 1] = r.y;
+        v[e + 2] = r.z;
+        v[e + 3] = r.w;
+        if (sum) *reinterpret_cast<float4*>(sum + (size_t)m * K + base + e) = r;
     }
-    float squares = 0.f;
+    if (FINAL) {
+        float squares = 0.f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-        if (e >= per) break;
-        squares += v[e] * v[e];
+        for (int e = 0; e < PER; ++e) squares += v[e] * v[e];
+        const float scale = 1.0f / sqrtf(wave_sum(squares) / (float)K + a.eps);
+#pragma unroll
+        for (int e = 0; e < PER; e += 4) {
+            float n[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) n[i] = v[e + i] * scale * gain[base + e + i];
+            *reinterpret_cast<float4*>(out + (size_t)m * K + base + e) = make_float4(n[0], n[1], n[2], n[3]);
+        }
+        return;
     }
-    const float scale = 1.0f / sqrtf(wave_sum(squares) / (float)K + a.eps);
 #pragma unroll
-    for (int e = 0; e < 32; e += 8) {
-        if (e >= per) break;
+    for (int e = 0; e < PER; e += 8) {
         float n[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) n[i] = v[e + i] * scale * gain[base + e + i];
-        if (FINAL) {
-            *reinterpret_cast<float4*>(out + (size_t)m * K + base + e) = make_float4(n[0], n[1], n[2], n[3]);
-            *reinterpret_cast<float4*>(out + (size_t)m * K + base + e + 4) = make_float4(n[4], n[5], n[6], n[7]);
-        } else {
-            *reinterpret_cast<uint4*>(normed + (size_t)m * K + base + e) =
-                make_uint4(pack_bf16x2(n[0], n[1]), pack_bf16x2(n[2], n[3]), pack_bf16x2(n[4], n[5]), pack_bf16x2(n[6], n[7]));
-        }
+        for (int i = 0; i < 8; ++i) n[i] = v[e + i] * gain[base + e + i];
+        *reinterpret_cast<uint4*>(normed + (size_t)m * K + base + e) =
+            make_uint4(pack_bf16x2(n[0], n[1]), pack_bf16x2(n[2], n[3]), pack_bf16x2(n[4], n[5]), pack_bf16x2(n[6], n[7]));
     }
+    float q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = squares4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    float s = (q[0] + q[1]) + (q[2] + q[3]);
+    s += __shfl_xor(s, 1, WAVE);
+    s += __shfl_xor(s, 2, WAVE);
+    if (lane % 4 == 0) row_sq[(size_t)m * SQ_PARTS + lane / 4] = s;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -575,43 +767,93 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
     const int H = a.heads, KV = a.kv_heads;
     const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
     const int o_kbp = H * HEAD_DIM / 32 / b.o_parts, down_kbp = a.inner / 32 / b.down_parts;
+    // Over more than 64 tokens o_proj and down_proj add their parts and the residual themselves
+    // (the ring GEMM); up to 64, their parts go out to `partial` for local_add_norm to add.
+    const bool ring = a.M_pad > 64;
     // The first layer's input norm.
     dispatch("local_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0, b.x0,
-             (float*)nullptr, layers[0].input_norm, b.normed, (float*)nullptr);
+             (float*)nullptr, layers[0].input_norm, b.normed, b.row_sq, (float*)nullptr);
     for (int l = 0; l < nlayers; ++l) {
         const LocalLayer& L = layers[l];
+        const bool last = l + 1 == nlayers;
         const float* input = l == 0 ? b.x0 : b.x;
-        LocalGemm qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, b.q, b.k, b.v};
+        LocalGemm qkv{};
+        qkv.w = L.qkv;
+        qkv.x = b.normed;
+        qkv.K = a.hidden;
+        qkv.N = qkv_rows;
+        qkv.q = b.q;
+        qkv.k = b.k;
+        qkv.v = b.v;
+        qkv.row_sq = b.row_sq;
         local_gemm<LEPI_QKV, 1, 32>("local_qkv_rope", a, qkv, qkv_rows / 16, 1, stream, timer);
         dispatch("local_attention", local_attention, dim3(a.M / a.T, H / 4), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
                  (const uint16_t*)b.k, (const uint16_t*)b.v, b.attended);
-        LocalGemm o{L.o, b.attended, H * HEAD_DIM, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
-        if (o_kbp == 16)
-            local_gemm<LEPI_PARTIAL, 1, 16>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
-        else
-            local_gemm<LEPI_PARTIAL, 1, 32>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
-        dispatch("local_o_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial, b.o_parts,
-                 input, b.h, L.post_norm, b.normed, (float*)nullptr);
-        LocalGemm gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, b.mlp, nullptr, nullptr, nullptr};
+        LocalGemm o{};
+        o.w = L.o;
+        o.x = b.attended;
+        o.K = H * HEAD_DIM;
+        o.N = a.hidden;
+        if (ring) {
+            o.residual = input;
+            o.sum = b.h;
+            o.next_gain = L.post_norm;
+            o.normed = b.normed;
+            o.sum_sq = b.row_sq;
+            local_gemm_add("local_o_proj", a, o, o_kbp, b.o_parts, stream, timer);
+        } else {
+            o.partial = b.partial;
+            if (o_kbp == 16)
+                local_gemm<LEPI_PARTIAL, 1, 16>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
+            else
+                local_gemm<LEPI_PARTIAL, 1, 32>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
+            dispatch("local_o_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial, b.o_parts,
+                     input, b.h, L.post_norm, b.normed, b.row_sq, (float*)nullptr);
+        }
+        LocalGemm gu{};
+        gu.w = L.gate_up;
+        gu.x = b.normed;
+        gu.K = a.hidden;
+        gu.N = 2 * a.inner;
+        gu.mlp = b.mlp;
+        gu.row_sq = b.row_sq;
         local_gemm<LEPI_SILU, 2, 32>("local_gate_up", a, gu, a.inner / 16, 1, stream, timer);
-        LocalGemm down{L.down, b.mlp, a.inner, a.hidden, b.partial, nullptr, nullptr, nullptr, nullptr};
+        LocalGemm down{};
+        down.w = L.down;
+        down.x = b.mlp;
+        down.K = a.inner;
+        down.N = a.hidden;
+        if (ring) {
+            down.residual = b.h;
+            down.sum = b.x;
+            down.next_gain = last ? nullptr : layers[l + 1].input_norm;
+            down.normed = b.normed;
+            down.sum_sq = b.row_sq;
+            local_gemm_add("local_down_proj", a, down, down_kbp, b.down_parts, stream, timer);
+            if (last)
+                dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0,
+                         (const float*)b.x, (float*)nullptr, final_norm, (uint16_t*)nullptr, (float*)nullptr, b.out);
+            continue;
+        }
+        down.partial = b.partial;
         if (down_kbp == 16)
             local_gemm<LEPI_PARTIAL, 1, 16>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
         else
             local_gemm<LEPI_PARTIAL, 1, 32>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
-        if (l + 1 < nlayers)
+        if (!last)
             dispatch("local_down_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
-                     b.down_parts, (const float*)b.h, b.x, layers[l + 1].input_norm, b.normed, (float*)nullptr);
+                     b.down_parts, (const float*)b.h, b.x, layers[l + 1].input_norm, b.normed, b.row_sq, (float*)nullptr);
         else
             dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
-                     b.down_parts, (const float*)b.h, b.x, final_norm, (uint16_t*)nullptr, b.out);
+                     b.down_parts, (const float*)b.h, b.x, final_norm, (uint16_t*)nullptr, (float*)nullptr, b.out);
     }
     return hipGetLastError();
 }
 
 bool local_supported(int hidden, int inner, int heads, int kv_heads, int o_parts, int down_parts) {
+    // 2 or 4 parts of 16 or 32 k-blocks of 32 columns (the ring GEMM's instances).
     auto kbp_ok = [](int K, int parts) {
-        return parts >= 1 && parts <= LOCAL_MAX_PARTS && K % (32 * parts) == 0 && (K / 32 / parts == 16 || K / 32 / parts == 32);
+        return (parts == 2 || parts == 4) && K % (32 * parts) == 0 && (K / 32 / parts == 16 || K / 32 / parts == 32);
     };
     return hidden == 1024 && heads % 4 == 0 && kv_heads >= 1 && inner % 64 == 0 && kbp_ok(heads * HEAD_DIM, o_parts) &&
            kbp_ok(inner, down_parts);
@@ -620,10 +862,12 @@ bool local_supported(int hidden, int inner, int heads, int kv_heads, int o_parts
 int local_rows_padded(int M) { return M <= 64 ? (M + 15) / 16 * 16 : (M + 63) / 64 * 64; }
 
 hipError_t local_prepare() {
-    hipError_t e = local_gemm_lds<LEPI_QKV, 1, 32>();
-    if (e == hipSuccess) e = local_gemm_lds<LEPI_SILU, 2, 32>();
-    if (e == hipSuccess) e = local_gemm_lds<LEPI_PARTIAL, 1, 32>();
-    if (e == hipSuccess) e = local_gemm_lds<LEPI_PARTIAL, 1, 16>();
+    hipError_t e = local_ring_lds<LEPI_QKV, 1, 32, 1>();
+    if (e == hipSuccess) e = local_ring_lds<LEPI_SILU, 2, 32, 1>();
+    if (e == hipSuccess) e = local_ring_lds<LEPI_ADD, 1, 16, 2>();
+    if (e == hipSuccess) e = local_ring_lds<LEPI_ADD, 1, 32, 2>();
+    if (e == hipSuccess) e = local_ring_lds<LEPI_ADD, 1, 16, 4>();
+    if (e == hipSuccess) e = local_ring_lds<LEPI_ADD, 1, 32, 4>();
     return e;
 }
 

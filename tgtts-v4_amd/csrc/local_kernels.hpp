@@ -26,6 +26,7 @@ constexpr int LOCAL_MAX_T = 16;        // the longest sequence: local_attention 
 constexpr int LOCAL_MAX_PARTS = 4;
 constexpr int LOCAL_O_PARTS = 2;     // o_proj's columns summed in 2 parts, down_proj's in 4, in part order
 constexpr int LOCAL_DOWN_PARTS = 4;
+constexpr int LOCAL_SQ_COLS = 64;    // the columns of a row that one of its sums of squares spans
 
 struct LocalLayer {
     const uint16_t *qkv, *o, *gate_up, *down;  // 16-row MFMA tiles, q/k/v rows RoPE-paired
@@ -36,7 +37,10 @@ struct LocalLayer {
 struct LocalBuffers {
     const float* x0;     // the embedded tokens, the first layer's residual
     float *x, *h;        // the residual stream after each layer / after each attention
-    uint16_t* normed;    // bf16 [M_pad][hidden]
+    uint16_t* normed;    // bf16 [M_pad][hidden]: an RMSNorm's input times its gain, the rows' scales
+                         // still to apply (the GEMM that reads it applies them)
+    float* row_sq;       // f32 [M_pad][hidden / LOCAL_SQ_COLS]: normed's rows' sums of squares, each
+                         // over LOCAL_SQ_COLS columns
     uint16_t *q, *k, *v; // bf16 [M_pad][heads | kv_heads][64]
     uint16_t* attended;  // bf16 [M_pad][heads 64]
     uint16_t* mlp;       // bf16 [M_pad][inner]
@@ -72,10 +76,10 @@ struct EulerArgs {
     float dt;
 };
 
-// Lets the projections take their token tiles (64 KiB) in LDS; once per process.
+// Lets the ring GEMM take its rings of token tiles (up to 66 KiB) in LDS; once per process.
 hipError_t local_prepare();
 // The stacks the kernels take: hidden 1024, query heads a multiple of 4, and o_proj's and
-// down_proj's parts 16 or 32 k-blocks of 32 columns each.
+// down_proj's columns in 2 or 4 parts of 16 or 32 k-blocks of 32 columns each.
 bool local_supported(int hidden, int inner, int heads, int kv_heads, int o_parts, int down_parts);
 // The rows the token tensors of M tokens take: a multiple of 16 up to 64 tokens, else of 64.
 int local_rows_padded(int M);

@@ -55,7 +55,7 @@ struct Sampler {
     bool times_dirty = true;
     TimeMlp time_mlp, delta_mlp;
     float *cos = nullptr, *sin = nullptr;
-    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr;
+    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr, *row_sq = nullptr;
     uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
     float *mu = nullptr, *cond = nullptr, *noise = nullptr, *state = nullptr, *sampling = nullptr;
     std::map<int, RowProgram> programs;  // recorded on first launch; dropped when the times change
@@ -103,7 +103,7 @@ struct Encoder {
     float* final_norm = nullptr;
     float *in_w = nullptr, *in_b = nullptr, *special = nullptr;  // f32 [hidden][feat], [hidden], [hidden]
     float *cos = nullptr, *sin = nullptr;
-    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr;
+    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr, *row_sq = nullptr;
     uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
     float *patch = nullptr, *embedding = nullptr;  // [rows][feat][frames], [rows][hidden]
     std::map<int, RowProgram> programs;  // patch -> embedding, by rows

@@ -184,6 +184,7 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     A(&smp->partial, (size_t)LOCAL_MAX_PARTS * Mp * h);
     A(&smp->out, Mp * h);
     A(&smp->normed, Mp * h);
+    A(&smp->row_sq, Mp * (h / LOCAL_SQ_COLS));
     A(&smp->q, Mp * att);
     A(&smp->k, Mp * KV * HEAD_DIM);
     A(&smp->v, Mp * KV * HEAD_DIM);
@@ -313,7 +314,7 @@ hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, in
         const Layer& L = s->layers[l];
         layers[l] = LocalLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm};
     }
-    const LocalBuffers b{s->x0, s->x, s->h, s->normed, s->q, s->k, s->v, s->attended, s->mlp, s->partial, s->out,
+    const LocalBuffers b{s->x0, s->x, s->h, s->normed, s->row_sq, s->q, s->k, s->v, s->attended, s->mlp, s->partial, s->out,
                          s->o_parts, s->down_parts};
     const int x_at = COND_AT + F;
     for (size_t i = 0; i < s->step_t.size() && e == hipSuccess; ++i) {
