@@ -135,7 +135,7 @@ __device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm&
             const float gate = acc[i] * rs, u = up[i] * rs;
             v[i] = gate / (1.0f + __expf(-gate)) * u;
         }
-        *reinterpret_cast<uint2*>(g.mlp + (size_t)m * inner + n) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        *reinterpret_cast<uint2*>(g.mlp + act_index(m, n, inner)) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     } else if (EPI == LEPI_QKV) {  // a strip's rows pair as r, r + 8 (lanes l and l ^ 32)
         const int H = a.heads, KV = a.kv_heads;
         const bool second = quad >= 2;
@@ -245,12 +245,12 @@ __global__ void __launch_bounds__(TT * WAVE) local_gemm_direct(LocalArgs a, Loca
     if (SCALED) sq.load(g.row_sq, 16 * t + lane % 16);
     WeightRing<SW, KBP, DEPTH> w;
     w.start(g, strip, kb0, lane);
-    const uint16_t* xp = g.x + (size_t)(16 * t + lane % 16) * g.K + kb0 * 32 + (lane / 16) * 8;
+    const uint16_t* xp = g.x + act_index(16 * t, kb0 * 32, g.K) + lane * 8;  // the tile's fragments, 1 KiB each
     uint4 xf[DEPTH];
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {  // k-block by k-block, so that the first MFMA waits for the first loads only
         w.fetch(d, d + 1);
-        xf[d] = load16(xp + d * 32);
+        xf[d] = load16(xp + d * 512);
     }
     all_issued();
     if (SCALED) sq.settle();
@@ -264,7 +264,7 @@ __global__ void __launch_bounds__(TT * WAVE) local_gemm_direct(LocalArgs a, Loca
         for (int s = 0; s < SW; ++s) acc[s][0] = mfma16(w.wf[r][s], xf[r], acc[s][0]);
         if (kb + DEPTH < KBP) {
             w.fetch(kb + DEPTH, kb + DEPTH + 1);
-            xf[r] = load16(xp + (kb + DEPTH) * 32);
+            xf[r] = load16(xp + (kb + DEPTH) * 512);
         }
         all_issued();  // each k-block's refill stays where it is, DEPTH k-blocks ahead of its use
     }
@@ -323,10 +323,10 @@ __global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2
     if (SCALED) sq.load(g.row_sq, m0 + lane);
     WeightRing<SW, KB, RING> w;
     w.start(g, strip, 0, lane);
-    const uint16_t* xp = g.x + (size_t)(m0 + 16 * wv + lane % 16) * g.K + (lane / 16) * 8;
+    const uint16_t* xp = g.x + act_index(m0 + 16 * wv, 0, g.K) + lane * 8;  // tile wv's fragments, 1 KiB each
     auto fetch = [&](int kb) __attribute__((always_inline)) {
         w.fetch(kb, kb + 1);
-        load_to_lds(xp + kb * 32, &xs[((kb % RING) * 4 + wv) * 64]);
+        load_to_lds(xp + kb * 512, &xs[((kb % RING) * 4 + wv) * 64]);
     };
 #pragma unroll
     for (int kb = 0; kb < RING; ++kb) fetch(kb);
@@ -408,7 +408,7 @@ __global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2
         if (m < a.M) {
             *reinterpret_cast<float4*>(g.sum + (size_t)m * g.N + n) = v;
             if (g.next_gain)
-                *reinterpret_cast<uint2*>(g.normed + (size_t)m * g.N + n) =
+                *reinterpret_cast<uint2*>(g.normed + act_index(m, n, g.N)) =
                     make_uint2(pack_bf16x2(v.x * gn.x, v.y * gn.y), pack_bf16x2(v.z * gn.z, v.w * gn.w));
         }
         if (g.next_gain) {
@@ -529,10 +529,10 @@ __global__ void __launch_bounds__(256) local_attention(LocalArgs a, const uint16
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16(make_uint4(vw[dt][0], vw[dt][1], 0u, 0u), pf, f32x4{0.f, 0.f, 0.f, 0.f});
     if (r >= T) return;
-    uint16_t* out = attended + ((size_t)(first + r) * H + head) * HEAD_DIM;
+    // Into attended in fragment order: dimensions 16 dt + 4 g .. + 3 of the head, 8 bytes.
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
-        *reinterpret_cast<uint2*>(out + 16 * dt + 4 * g) =
+        *reinterpret_cast<uint2*>(attended + act_index(first + r, head * HEAD_DIM + 16 * dt + 4 * g, H * HEAD_DIM)) =
             make_uint2(pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv), pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv));
 }
 
@@ -595,7 +595,7 @@ __global__ void __launch_bounds__(256) local_add_norm(LocalArgs a, const float* 
         float n[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) n[i] = v[e + i] * gain[base + e + i];
-        *reinterpret_cast<uint4*>(normed + (size_t)m * K + base + e) =
+        *reinterpret_cast<uint4*>(normed + act_index(m, base + e, K)) =
             make_uint4(pack_bf16x2(n[0], n[1]), pack_bf16x2(n[2], n[3]), pack_bf16x2(n[4], n[5]), pack_bf16x2(n[6], n[7]));
     }
     float q[4];

@@ -37,13 +37,15 @@ struct LocalLayer {
 struct LocalBuffers {
     const float* x0;     // the embedded tokens, the first layer's residual
     float *x, *h;        // the residual stream after each layer / after each attention
-    uint16_t* normed;    // bf16 [M_pad][hidden]: an RMSNorm's input times its gain, the rows' scales
+    // The GEMMs' inputs are in MFMA fragment order (act_index: each 16 tokens by 32 columns a
+    // contiguous KiB), so that a wave's load of one is one contiguous KiB.
+    uint16_t* normed;    // bf16 [M_pad][hidden], fragment order: an RMSNorm's input times its gain, the rows' scales
                          // still to apply (the GEMM that reads it applies them)
     float* row_sq;       // f32 [M_pad][hidden / LOCAL_SQ_COLS]: normed's rows' sums of squares, each
                          // over LOCAL_SQ_COLS columns
     uint16_t *q, *k, *v; // bf16 [M_pad][heads | kv_heads][64]
-    uint16_t* attended;  // bf16 [M_pad][heads 64]
-    uint16_t* mlp;       // bf16 [M_pad][inner]
+    uint16_t* attended;  // bf16 [M_pad][heads 64], fragment order
+    uint16_t* mlp;       // bf16 [M_pad][inner], fragment order
     float* partial;      // f32 [LOCAL_MAX_PARTS][M_pad][hidden]
     float* out;          // f32 [M_pad][hidden]: the last layer's output after the final norm
     int o_parts, down_parts;
