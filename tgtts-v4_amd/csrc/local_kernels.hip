@@ -272,19 +272,22 @@ __global__ void __launch_bounds__(TT * WAVE) local_gemm_direct(LocalArgs a, Loca
     local_epilogue<EPI, SW, 1>(a, g, strip, 16 * t, acc, rs);
 }
 
-// local_gemm_ring, for more tokens (M_pad a multiple of 64): a workgroup of 4 waves to 64 tokens
-// (4 token tiles) and 4 work units, wave w taking unit 4 blockIdx.x + w against all four tiles.
-// A k-block's loads are a group: each wave's SW fragments of W, into registers (WeightRing), and
-// its token tile's fragment, straight from memory into a ring of RING LDS slots (4 KiB: the four
-// tiles' fragments of one k-block). The groups go out in k-block order RING ahead of their
+// local_gemm_ring, for more tokens (M_pad a multiple of 16 TT): a workgroup of 4 waves to 16 TT
+// tokens (TT token tiles, 4 or 8) and 4 work units, wave w taking unit 4 blockIdx.x + w against
+// every tile. A k-block's loads are a group: each wave's SW fragments of W, into registers
+// (WeightRing), and its TT / 4 token tiles' fragments, straight from memory into a ring of RING
+// LDS slots (TT KiB: the tiles' fragments of one k-block). The groups go out in k-block order RING ahead of their
 // products, so a wave's count of loads in flight says which of its groups have landed, and the
 // barrier after the wait says the same of every wave's; a wave reads a k-block's tiles from LDS
 // while it multiplies the k-block before. No wave ever waits for more than the group it needs
 // next. Each output is P chains of KBP k-blocks, the parts of local_gemm_direct in its order,
 // added in part order as local_add_norm adds them.
-// Grid (units / 4, M_pad / 64).
-constexpr int ring_depth(int sw) { return sw == 1 ? 16 : 12; }
-constexpr size_t ring_lds(int sw) { return (size_t)ring_depth(sw) * 4 * 64 * sizeof(uint4) + (64 + 4 * 64) * sizeof(float); }
+// Grid (units / 4, M_pad / (16 TT)). Eight tiles halve the reads of W a token makes, at the cost of
+// half the workgroups.
+constexpr int ring_depth(int sw, int tt) { return tt == 8 ? 6 : sw == 1 ? 16 : 12; }
+constexpr size_t ring_lds(int sw, int tt) {
+    return (size_t)ring_depth(sw, tt) * tt * 64 * sizeof(uint4) + (16 * tt + 4 * 64) * sizeof(float);
+}
 
 // Waits until at most `n` of the wave's loads are in flight, `n` known when the loop is unrolled:
 // the compiler's own wait (wait_vm_seen), so that it knows the loads before those n have landed
@@ -301,55 +304,62 @@ __device__ __forceinline__ void wait_vm_at_most(int n) {
     }
 }
 
-template <int EPI, int SW, int KBP, int P>
+template <int EPI, int SW, int KBP, int P, int TT>
 __global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2))) local_gemm_ring(LocalArgs a, LocalGemm g) {
     constexpr int KB = KBP * P;
-    constexpr int RING = ring_depth(SW);
-    constexpr int GROUP = SW + 1;  // a wave's loads of a k-block
+    constexpr int RING = ring_depth(SW, TT);
+    constexpr int XL = TT / 4;      // token tiles a wave loads
+    constexpr int GROUP = SW + XL;  // a wave's loads of a k-block
     constexpr bool SCALED = EPI == LEPI_QKV || EPI == LEPI_SILU;
-    static_assert(KB > RING, "the ring fills before the first product");
+    static_assert(TT == 4 || TT == 8, "4 or 8 token tiles");
+    static_assert(EPI != LEPI_ADD || TT == 4, "the sums of squares' reduction takes 64 tokens");
+    static_assert(KB >= RING, "the ring fills before the first product");
     static_assert(RING * GROUP + SQ_PARTS / 4 < 64, "the loads in flight fit the wave's count");
     static_assert(EPI != LEPI_ADD || SW == 1, "a workgroup's columns are one span of a sum of squares");
-    extern __shared__ uint4 xs[];  // [RING][4 tiles][64 lanes]
-    float* scales = reinterpret_cast<float*>(xs + RING * 4 * 64);  // [64]: the tokens' row scales
-    float* sq_part = scales + 64;                                   // [4 waves][64 tokens]
+    extern __shared__ uint4 xs[];  // [RING][TT tiles][64 lanes]
+    float* scales = reinterpret_cast<float*>(xs + RING * TT * 64);  // [16 TT]: the tokens' row scales
+    float* sq_part = scales + 16 * TT;                               // [4 waves][64 tokens]
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
-    const int m0 = blockIdx.y * 64;
+    const int m0 = blockIdx.y * 16 * TT;
     int strip[SW];
     local_strips<EPI, SW>(blockIdx.x * 4 + wv, g.N, strip);
-    // The tokens' sums of squares (a lane to a token, in every wave, so that each wave's count of
-    // loads is the same) go out before the groups: the wait for the first group covers them.
+    // The tokens' sums of squares (a lane to a token, 64 tokens to a wave, in every wave so that
+    // each wave's count of loads is the same) go out before the groups: the wait for the first
+    // group covers them.
     RowSq sq;
-    if (SCALED) sq.load(g.row_sq, m0 + lane);
+    if (SCALED) sq.load(g.row_sq, m0 + 64 * (wv % XL) + lane);
     WeightRing<SW, KB, RING> w;
     w.start(g, strip, 0, lane);
-    const uint16_t* xp = g.x + act_index(m0 + 16 * wv, 0, g.K) + lane * 8;  // tile wv's fragments, 1 KiB each
+    // Tiles wv, wv + 4 ..'s fragments, 1 KiB each.
+    const uint16_t* xp = g.x + act_index(m0 + 16 * wv, 0, g.K) + lane * 8;
+    const size_t tile4 = (size_t)4 * (g.K / 32) * 512;  // four tiles on
     auto fetch = [&](int kb) __attribute__((always_inline)) {
         w.fetch(kb, kb + 1);
-        load_to_lds(xp + kb * 512, &xs[((kb % RING) * 4 + wv) * 64]);
+#pragma unroll
+        for (int j = 0; j < XL; ++j) load_to_lds(xp + j * tile4 + kb * 512, &xs[((kb % RING) * TT + wv + 4 * j) * 64]);
     };
 #pragma unroll
     for (int kb = 0; kb < RING; ++kb) fetch(kb);
     all_issued();
-    f32x4 acc[P][SW][4];
+    f32x4 acc[P][SW][TT];
 #pragma unroll
     for (int p = 0; p < P; ++p)
 #pragma unroll
         for (int s = 0; s < SW; ++s)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[p][s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < TT; ++t) acc[p][s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     // Group 0 landed, every wave's; the scales into LDS, read after the barriers below. The store
     // is an asm the compiler cannot see: a store it knew of might share bytes with the loads into
     // the ring, for all it knows, and it would wait for every one of them before the first read.
     wait_vm_seen<(RING - 1) * GROUP>();
     if (SCALED) {
         const float rs = row_scale_of(sq.p, g.K, a.eps);
-        if (wv == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(lds_offset(&scales[lane])), "v"(rs) : "memory");
+        if (wv < XL) asm volatile("ds_write_b32 %0, %1" ::"v"(lds_offset(&scales[64 * wv + lane])), "v"(rs) : "memory");
     }
     stage_barrier();
-    uint4 xf[2][4];
+    uint4 xf[2][TT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xf[0][t] = lds_read16(&xs[t * 64 + lane]);
+    for (int t = 0; t < TT; ++t) xf[0][t] = lds_read16(&xs[t * 64 + lane]);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
         const int b = kb % 2;
@@ -361,31 +371,31 @@ __global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2
             wait_vm_at_most<(RING - 2) * GROUP>(GROUP * (RING - 2 < KB - 2 - kb ? RING - 2 : KB - 2 - kb));
             stage_barrier();
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xf[1 - b][t] = lds_read16(&xs[(((kb + 1) % RING) * 4 + t) * 64 + lane]);
+            for (int t = 0; t < TT; ++t) xf[1 - b][t] = lds_read16(&xs[(((kb + 1) % RING) * TT + t) * 64 + lane]);
         }
         const int r = kb % RING, p = kb / KBP;
 #pragma unroll
         for (int s = 0; s < SW; ++s)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[p][s][t] = mfma16(w.wf[r][s], xf[b][t], acc[p][s][t]);
+            for (int t = 0; t < TT; ++t) acc[p][s][t] = mfma16(w.wf[r][s], xf[b][t], acc[p][s][t]);
         if (kb + RING < KB) fetch(kb + RING);  // into the W registers just multiplied
         all_issued();
     }
     // The parts in part order.
-    f32x4 sum[SW][4];
+    f32x4 sum[SW][TT];
 #pragma unroll
     for (int s = 0; s < SW; ++s)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < TT; ++t) {
             sum[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int p = 0; p < P; ++p) sum[s][t] += acc[p][s][t];
         }
-    if (EPI != LEPI_ADD) {
-        float rs[4];
+    if constexpr (EPI != LEPI_ADD) {
+        float rs[TT];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) rs[t] = SCALED ? scales[16 * t + lane % 16] : 1.f;
-        local_epilogue<EPI, SW, 4>(a, g, strip, m0, sum, rs);
+        for (int t = 0; t < TT; ++t) rs[t] = SCALED ? scales[16 * t + lane % 16] : 1.f;
+        local_epilogue<EPI, SW, TT>(a, g, strip, m0, sum, rs);
         return;
     }
     // LEPI_ADD: the residual added; with next_gain, the next norm's input and each token's sum of
@@ -444,8 +454,17 @@ void local_gemm(const char* label, const LocalArgs& a, const LocalGemm& g, int u
         }
         return;
     }
+    // Eight token tiles a workgroup for gate/up where the tokens come in 128s (its W, 16 MiB at
+    // the sampler's shape, is the most read); four otherwise.
+    if constexpr (EPI == LEPI_SILU) {
+        if (a.M_pad % 128 == 0) {
+            dispatch(label, local_gemm_ring<EPI, SW, KBP, 1, 8>, dim3(units / 4, a.M_pad / 128), dim3(4 * WAVE), ring_lds(SW, 8),
+                     stream, timer, a, g);
+            return;
+        }
+    }
     if constexpr (EPI != LEPI_PARTIAL)
-        dispatch(label, local_gemm_ring<EPI, SW, KBP, 1>, dim3(units / 4, a.M_pad / 64), dim3(4 * WAVE), ring_lds(SW), stream,
+        dispatch(label, local_gemm_ring<EPI, SW, KBP, 1, 4>, dim3(units / 4, a.M_pad / 64), dim3(4 * WAVE), ring_lds(SW, 4), stream,
                  timer, a, g);
 }
 
@@ -454,21 +473,21 @@ void local_gemm(const char* label, const LocalArgs& a, const LocalGemm& g, int u
 void local_gemm_add(const char* label, const LocalArgs& a, const LocalGemm& g, int kbp, int parts, hipStream_t stream,
                     DispatchTimer* timer) {
     const dim3 grid(g.N / 64, a.M_pad / 64), block(4 * WAVE);
-    const size_t lds = ring_lds(1);
+    const size_t lds = ring_lds(1, 4);
     if (kbp == 16 && parts == 2)
-        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 16, 2>, grid, block, lds, stream, timer, a, g);
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 16, 2, 4>, grid, block, lds, stream, timer, a, g);
     else if (kbp == 32 && parts == 2)
-        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 32, 2>, grid, block, lds, stream, timer, a, g);
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 32, 2, 4>, grid, block, lds, stream, timer, a, g);
     else if (kbp == 16 && parts == 4)
-        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 16, 4>, grid, block, lds, stream, timer, a, g);
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 16, 4, 4>, grid, block, lds, stream, timer, a, g);
     else
-        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 32, 4>, grid, block, lds, stream, timer, a, g);
+        dispatch(label, local_gemm_ring<LEPI_ADD, 1, 32, 4, 4>, grid, block, lds, stream, timer, a, g);
 }
 
-template <int EPI, int SW, int KBP, int P>
+template <int EPI, int SW, int KBP, int P, int TT = 4>
 hipError_t local_ring_lds() {
-    return hipFuncSetAttribute((const void*)local_gemm_ring<EPI, SW, KBP, P>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)ring_lds(SW));
+    return hipFuncSetAttribute((const void*)local_gemm_ring<EPI, SW, KBP, P, TT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)ring_lds(SW, TT));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -864,6 +883,7 @@ int local_rows_padded(int M) { return M <= 64 ? (M + 15) / 16 * 16 : (M + 63) / 
 hipError_t local_prepare() {
     hipError_t e = local_ring_lds<LEPI_QKV, 1, 32, 1>();
     if (e == hipSuccess) e = local_ring_lds<LEPI_SILU, 2, 32, 1>();
+    if (e == hipSuccess) e = local_ring_lds<LEPI_SILU, 2, 32, 1, 8>();
     if (e == hipSuccess) e = local_ring_lds<LEPI_ADD, 1, 16, 2>();
     if (e == hipSuccess) e = local_ring_lds<LEPI_ADD, 1, 32, 2>();
     if (e == hipSuccess) e = local_ring_lds<LEPI_ADD, 1, 16, 4>();
