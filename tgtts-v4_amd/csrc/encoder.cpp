@@ -202,20 +202,21 @@ hipError_t encoder_enqueue(Encoder* e, const float* patch, float* dst, int* disp
     const int C = e->feat, F = e->frames;
     // Token 0 of each row's sequence the learned token, tokens 1 .. F in_proj of its frames
     // (encoder.rs:92-111).
-    EmbedArgs emb{patch, e->in_w, e->in_b, e->special, e->x0, C, F, 1, 0, 1, 0, 1, 1};
+    // The embedding writes every token, and with them the first layer's norm input.
+    EmbedArgs emb{patch, e->in_w, e->in_b, e->special, e->x0, C, F, 1, 0, 1, 0, 1, 1, e->layers[0].input_norm, e->normed, e->row_sq};
     hipError_t err = launch_local_embed(a, emb, e->rows, st, nullptr);
     std::vector<LocalLayer> layers(e->shape.layers);
     for (int l = 0; l < e->shape.layers; ++l) {
         const Layer& L = e->layers[l];
         layers[l] = LocalLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm};
     }
-    const LocalBuffers b{e->x0, e->x, e->h, e->normed, e->row_sq, e->q, e->k, e->v, e->attended, e->mlp, e->partial, e->out,
-                         e->o_parts, e->down_parts};
+    const LocalBuffers b{e->x0, e->x,        e->h,   e->normed,  e->row_sq, e->normed, e->row_sq,   e->q,
+                         e->k,  e->v,        e->attended, e->mlp, e->partial, e->out,  e->o_parts, e->down_parts};
     if (err == hipSuccess) err = launch_local_stack(a, layers.data(), e->shape.layers, e->final_norm, b, st, nullptr);
     // The learned token's output, the first of each sequence (encoder.rs:113-114).
     const size_t row = (size_t)e->shape.hidden * sizeof(float);
     if (err == hipSuccess) err = hipMemcpy2DAsync(dst, row, e->out, (size_t)e->T * row, row, e->rows, hipMemcpyDeviceToDevice, st);
-    if (dispatches) *dispatches = 2 + 7 * e->shape.layers;  // the embedding, the stack
+    if (dispatches) *dispatches = 1 + local_stack_dispatches(a, b, e->shape.layers);  // the embedding, the stack
     return err;
 }
 

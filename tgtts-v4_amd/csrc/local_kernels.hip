@@ -69,6 +69,18 @@ __device__ __forceinline__ float squares4(float a, float b, float c, float d) {
     s = fmaf(c, c, s);
     return fmaf(d, d, s);
 }
+// The sum of squares of a token's LOCAL_SQ_COLS columns held a column to a lane (lane l: column l
+// of the span), in the order above, by the VALU's lane moves: squares4 over lanes 4 i .. 4 i + 3
+// (each quad's values broadcast, quad_perm), (a + b) + (c + d) over those of each 16 lanes (the
+// 16 rotated right 12, 8 and 4 lanes, row_ror: the first lane of a 16 then holds lanes +4, +8,
+// +12), then over the four 16s (lanes l ^ 16, l ^ 32). Every lane of the wave takes part; lane 0
+// has the sum.
+__device__ __forceinline__ float span_squares(float v) {
+    const float s = squares4(dpp_move<0x00>(v), dpp_move<0x55>(v), dpp_move<0xAA>(v), dpp_move<0xFF>(v));
+    const float t = (s + dpp_move<0x12C>(s)) + (dpp_move<0x128>(s) + dpp_move<0x124>(s));
+    const float u = t + lane_xor16(t);
+    return u + lane_xor32(u);
+}
 // 1 / rms of a row from its SQ_PARTS sums of squares, added in order.
 __device__ __forceinline__ float row_scale_of(const float4 (&p)[SQ_PARTS / 4], int K, float eps) {
     float total = 0.f;
@@ -665,13 +677,26 @@ __global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
             for (int f = 0; f < F; ++f) acc[f] += w4[i] * frames[f * C + 4 * v + i];
     }
     const int K = a.hidden;
+    const float g = e.gain ? e.gain[n] : 0.f;
+    // Token m's value v of column n, and with a gain the first norm's input: v g in bf16 and the
+    // sum of squares of the wave's 64 columns (uniform over the wave).
+    auto put = [&](size_t m, float v) {
+        e.x0[m * K + n] = v;
+        if (!e.gain) return;
+        // Columns n, n + 1 (lanes 2 i, 2 i + 1) side by side in fragment order: the even lane
+        // stores both.
+        const float vg = v * g, next = dpp_move<0xB1>(vg);  // quad_perm [1, 0, 3, 2]
+        if (n % 2 == 0) *reinterpret_cast<uint32_t*>(e.normed + act_index((int)m, n, K)) = pack_bf16x2(vg, next);
+        const float sq = span_squares(v);
+        if (threadIdx.x % WAVE == 0) e.row_sq[m * SQ_PARTS + n / LOCAL_SQ_COLS] = sq;
+    };
     for (int s = 0; s < e.seqs; ++s) {
         const size_t seq0 = (size_t)(row * e.seqs + s) * a.T;
 #pragma unroll
-        for (int f = 0; f < F; ++f) e.x0[(seq0 + e.first + f) * K + n] = acc[f];
+        for (int f = 0; f < F; ++f) put(seq0 + e.first + f, acc[f]);
         for (int t = 0; t < e.copies; ++t) {
             const float* src = e.copy_src + ((size_t)(e.shared ? 0 : row * e.copies) + t) * K;
-            e.x0[(seq0 + e.copy_at + t) * K + n] = (e.guided && s > 0) ? 0.f : src[n];
+            put(seq0 + e.copy_at + t, (e.guided && s > 0) ? 0.f : src[n]);
         }
     }
 }
@@ -702,17 +727,31 @@ __global__ void __launch_bounds__(EULER_THREADS) dit_euler(LocalArgs a, EulerArg
     const int tm = lane % 16;
     const bool real = tm < TOKENS;
     const int tmc = real ? tm : 0;
-    const float* src = e.out + ((size_t)(row * 2 + tmc / F) * a.T + e.first + tmc % F) * K + (lane / 16) * 8;
-    float4 lo[EULER_KB], hi[EULER_KB];
+    const size_t token = (size_t)(row * 2 + tmc / F) * a.T + e.first + tmc % F;
+    const float* src = e.x + token * K + (lane / 16) * 8;
+    const float* gain = e.gain + (lane / 16) * 8;
+    RowSq sq;
+    sq.load(e.row_sq, (int)token);
+    float4 lo[EULER_KB], hi[EULER_KB], glo[EULER_KB], ghi[EULER_KB];
     uint4 wf[EULER_KB][EULER_STRIPS];
 #pragma unroll
     for (int j = 0; j < EULER_KB; ++j) {
         const int kb = w * EULER_KB + j;
         lo[j] = *reinterpret_cast<const float4*>(src + kb * 32);
         hi[j] = *reinterpret_cast<const float4*>(src + kb * 32 + 4);
+        glo[j] = *reinterpret_cast<const float4*>(gain + kb * 32);
+        ghi[j] = *reinterpret_cast<const float4*>(gain + kb * 32 + 4);
 #pragma unroll
         for (int s = 0; s < EULER_STRIPS; ++s)
             wf[j][s] = *reinterpret_cast<const uint4*>(e.w + weight_tile_index(min(s, strips - 1), kb, KB, 16) + lane * 8);
+    }
+    // The final norm: x / rms(x) g, its scale from the row's sums of squares.
+    const float scale = row_scale_of(sq.p, K, a.eps);
+    auto normed = [&](float4 v, float4 g4) { return make_float4(v.x * scale * g4.x, v.y * scale * g4.y, v.z * scale * g4.z, v.w * scale * g4.w); };
+#pragma unroll
+    for (int j = 0; j < EULER_KB; ++j) {
+        lo[j] = normed(lo[j], glo[j]);
+        hi[j] = normed(hi[j], ghi[j]);
     }
     f32x4 acc[EULER_STRIPS];
 #pragma unroll
@@ -789,22 +828,23 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
     // Over more than 64 tokens o_proj and down_proj add their parts and the residual themselves
     // (the ring GEMM); up to 64, their parts go out to `partial` for local_add_norm to add.
     const bool ring = a.M_pad > 64;
-    // The first layer's input norm.
-    dispatch("local_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0, b.x0,
-             (float*)nullptr, layers[0].input_norm, b.normed, b.row_sq, (float*)nullptr);
+    // The first layer's input norm, unless the embedding wrote it.
+    if (!b.normed0)
+        dispatch("local_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0, b.x0,
+                 (float*)nullptr, layers[0].input_norm, b.normed, b.row_sq, (float*)nullptr);
     for (int l = 0; l < nlayers; ++l) {
         const LocalLayer& L = layers[l];
         const bool last = l + 1 == nlayers;
         const float* input = l == 0 ? b.x0 : b.x;
         LocalGemm qkv{};
         qkv.w = L.qkv;
-        qkv.x = b.normed;
+        qkv.x = l == 0 && b.normed0 ? b.normed0 : b.normed;
         qkv.K = a.hidden;
         qkv.N = qkv_rows;
         qkv.q = b.q;
         qkv.k = b.k;
         qkv.v = b.v;
-        qkv.row_sq = b.row_sq;
+        qkv.row_sq = l == 0 && b.normed0 ? b.row_sq0 : b.row_sq;
         local_gemm<LEPI_QKV, 1, 32>("local_qkv_rope", a, qkv, qkv_rows / 16, 1, stream, timer);
         dispatch("local_attention", local_attention, dim3(a.M / a.T, H / 4), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
                  (const uint16_t*)b.k, (const uint16_t*)b.v, b.attended);
@@ -842,14 +882,16 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
         down.x = b.mlp;
         down.K = a.inner;
         down.N = a.hidden;
+        // After the last layer, with no `out`, x and its sums of squares for the reader to norm.
+        const float* next_gain = !last ? layers[l + 1].input_norm : b.out ? nullptr : final_norm;
         if (ring) {
             down.residual = b.h;
             down.sum = b.x;
-            down.next_gain = last ? nullptr : layers[l + 1].input_norm;
+            down.next_gain = next_gain;
             down.normed = b.normed;
             down.sum_sq = b.row_sq;
             local_gemm_add("local_down_proj", a, down, down_kbp, b.down_parts, stream, timer);
-            if (last)
+            if (last && b.out)
                 dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0,
                          (const float*)b.x, (float*)nullptr, final_norm, (uint16_t*)nullptr, (float*)nullptr, b.out);
             continue;
@@ -859,14 +901,20 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
             local_gemm<LEPI_PARTIAL, 1, 16>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
         else
             local_gemm<LEPI_PARTIAL, 1, 32>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
-        if (!last)
+        if (next_gain)
             dispatch("local_down_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
-                     b.down_parts, (const float*)b.h, b.x, layers[l + 1].input_norm, b.normed, b.row_sq, (float*)nullptr);
+                     b.down_parts, (const float*)b.h, b.x, next_gain, b.normed, b.row_sq, (float*)nullptr);
         else
             dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
                      b.down_parts, (const float*)b.h, b.x, final_norm, (uint16_t*)nullptr, (float*)nullptr, b.out);
     }
     return hipGetLastError();
+}
+
+int local_stack_dispatches(const LocalArgs& a, const LocalBuffers& b, int nlayers) {
+    const int norms = b.normed0 ? 0 : 1;
+    if (a.M_pad > 64) return norms + 5 * nlayers + (b.out ? 1 : 0);
+    return norms + 7 * nlayers;
 }
 
 bool local_supported(int hidden, int inner, int heads, int kv_heads, int o_parts, int down_parts) {

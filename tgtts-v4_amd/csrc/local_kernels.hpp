@@ -43,11 +43,17 @@ struct LocalBuffers {
                          // still to apply (the GEMM that reads it applies them)
     float* row_sq;       // f32 [M_pad][hidden / LOCAL_SQ_COLS]: normed's rows' sums of squares, each
                          // over LOCAL_SQ_COLS columns
+    // The first layer's normed input and its sums of squares, as the embedding wrote them
+    // (EmbedArgs::gain); null for the stack to norm x0 itself.
+    const uint16_t* normed0;
+    const float* row_sq0;
     uint16_t *q, *k, *v; // bf16 [M_pad][heads | kv_heads][64]
     uint16_t* attended;  // bf16 [M_pad][heads 64], fragment order
     uint16_t* mlp;       // bf16 [M_pad][inner], fragment order
     float* partial;      // f32 [LOCAL_MAX_PARTS][M_pad][hidden]
-    float* out;          // f32 [M_pad][hidden]: the last layer's output after the final norm
+    // f32 [M_pad][hidden]: the last layer's output after the final norm; null to leave the norm
+    // to the stack's reader (x and row_sq then hold its input and sums of squares)
+    float* out;
     int o_parts, down_parts;
 };
 
@@ -56,6 +62,8 @@ struct LocalBuffers {
 // written as tokens `first` .. of each of the row's `seqs` sequences (2 for the sampler's
 // conditional and unconditional ones, 1 for the encoder), and `copies` tokens of `copy_src` at
 // `copy_at` (per row unless `shared`; zero in the second sequence when `guided`).
+// With a gain, each token written is also written as the first layer's norm input: x0 gain in
+// bf16 into `normed` (fragment order) and its sums of squares into `row_sq`.
 struct EmbedArgs {
     const float* src;
     const float* w;
@@ -64,12 +72,18 @@ struct EmbedArgs {
     float* x0;
     int channels, frames, first, copy_at, copies, guided, shared;
     int seqs;
+    const float* gain;  // the first layer's input norm gain, or null
+    uint16_t* normed;
+    float* row_sq;
 };
 
-// One Euler step: velocities out_proj(out[tokens first..]) + b of the conditional and the
-// unconditional sequence, guided as CFG-Zero* guides them, and state -= dt * guided.
+// One Euler step: velocities out_proj(norm(x[tokens first..])) + b of the conditional and the
+// unconditional sequence, guided as CFG-Zero* guides them, and state -= dt * guided. The stack's
+// final norm is taken here, for the tokens read.
 struct EulerArgs {
-    const float* out;   // f32 [M_pad][hidden], the stack's output after the final norm
+    const float* x;       // f32 [M_pad][hidden], the stack's last residual (before its final norm)
+    const float* row_sq;  // x's sums of squares, [M_pad][hidden / LOCAL_SQ_COLS]
+    const float* gain;    // the final norm's gain [hidden]
     const uint16_t* w;  // bf16 [channels][hidden] in 16-row MFMA tiles
     const float* bias;  // [channels]
     const float* sampling;  // [rows][2]: temperature, guidance scale
@@ -87,6 +101,8 @@ bool local_supported(int hidden, int inner, int heads, int kv_heads, int o_parts
 int local_rows_padded(int M);
 hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int nlayers, const float* final_norm,
                               const LocalBuffers& b, hipStream_t stream, DispatchTimer* timer);
+// The dispatches launch_local_stack makes.
+int local_stack_dispatches(const LocalArgs& a, const LocalBuffers& b, int nlayers);
 hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer);
 hipError_t launch_dit_euler(const LocalArgs& a, const EulerArgs& e, int rows, hipStream_t stream, DispatchTimer* timer);
 hipError_t launch_cfm_noise(const float* noise, const float* sampling, float* state, int rows, int len,

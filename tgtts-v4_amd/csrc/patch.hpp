@@ -55,8 +55,8 @@ struct Sampler {
     bool times_dirty = true;
     TimeMlp time_mlp, delta_mlp;
     float *cos = nullptr, *sin = nullptr;
-    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr, *row_sq = nullptr;
-    uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
+    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr, *row_sq = nullptr, *row_sq0 = nullptr;
+    uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr, *normed0 = nullptr;
     float *mu = nullptr, *cond = nullptr, *noise = nullptr, *state = nullptr, *sampling = nullptr;
     std::map<int, RowProgram> programs;  // recorded on first launch; dropped when the times change
     hipGraphExec_t exec = nullptr;  // the current program's
@@ -103,8 +103,8 @@ struct Encoder {
     float* final_norm = nullptr;
     float *in_w = nullptr, *in_b = nullptr, *special = nullptr;  // f32 [hidden][feat], [hidden], [hidden]
     float *cos = nullptr, *sin = nullptr;
-    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr, *row_sq = nullptr;
-    uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr;
+    float *x0 = nullptr, *x = nullptr, *h = nullptr, *partial = nullptr, *out = nullptr, *row_sq = nullptr, *row_sq0 = nullptr;
+    uint16_t *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attended = nullptr, *mlp = nullptr, *normed0 = nullptr;
     float *patch = nullptr, *embedding = nullptr;  // [rows][feat][frames], [rows][hidden]
     std::map<int, RowProgram> programs;  // patch -> embedding, by rows
     hipGraphExec_t exec = nullptr;       // the current program's

@@ -182,9 +182,10 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     A(&smp->x, Mp * h);
     A(&smp->h, Mp * h);
     A(&smp->partial, (size_t)LOCAL_MAX_PARTS * Mp * h);
-    A(&smp->out, Mp * h);
     A(&smp->normed, Mp * h);
     A(&smp->row_sq, Mp * (h / LOCAL_SQ_COLS));
+    A(&smp->normed0, Mp * h);
+    A(&smp->row_sq0, Mp * (h / LOCAL_SQ_COLS));
     A(&smp->q, Mp * att);
     A(&smp->k, Mp * KV * HEAD_DIM);
     A(&smp->v, Mp * KV * HEAD_DIM);
@@ -307,24 +308,28 @@ hipError_t sampler_enqueue(Sampler* s, const float* mu, DispatchTimer* timer, in
     ++n;
     // The condition's tokens: cond_proj of the patch before at COND_AT, mu at 0 (zero in the
     // unconditional sequence), the same in every step (dit.rs:206-211).
-    EmbedArgs cond{s->cond, s->cond_w, s->cond_b, mu, s->x0, C, F, COND_AT, 0, MU_TOKENS, 1, 0, 2};
+    // Each embedding also writes its tokens' first-layer norm input into normed0 / row_sq0.
+    const float* gain0 = s->layers[0].input_norm;
+    EmbedArgs cond{s->cond, s->cond_w, s->cond_b, mu, s->x0, C, F, COND_AT, 0, MU_TOKENS, 1, 0, 2, gain0, s->normed0, s->row_sq0};
     if (e == hipSuccess) e = launch_local_embed(a, cond, rows, st, timer), ++n;
     std::vector<LocalLayer> layers(s->shape.layers);
     for (int l = 0; l < s->shape.layers; ++l) {
         const Layer& L = s->layers[l];
         layers[l] = LocalLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm};
     }
-    const LocalBuffers b{s->x0, s->x, s->h, s->normed, s->row_sq, s->q, s->k, s->v, s->attended, s->mlp, s->partial, s->out,
-                         s->o_parts, s->down_parts};
+    // No `out`: dit_euler takes the final norm of the tokens it reads.
+    const LocalBuffers b{s->x0,       s->x,        s->h, s->normed, s->row_sq,   s->normed0, s->row_sq0, s->q, s->k,
+                         s->v,        s->attended, s->mlp, s->partial, nullptr, s->o_parts, s->down_parts};
     const int x_at = COND_AT + F;
     for (size_t i = 0; i < s->step_t.size() && e == hipSuccess; ++i) {
         // in_proj of the patch so far at x_at, and the step's time token (dit.rs:213-219).
-        EmbedArgs step{s->state, s->in_w, s->in_b, s->time_tokens + i * s->shape.hidden, s->x0, C, F, x_at, TIME_AT, 1, 0, 1, 2};
+        EmbedArgs step{s->state, s->in_w, s->in_b, s->time_tokens + i * s->shape.hidden, s->x0, C, F, x_at, TIME_AT, 1, 0, 1, 2,
+                       gain0, s->normed0, s->row_sq0};
         e = launch_local_embed(a, step, rows, st, timer);
         ++n;
         if (e == hipSuccess) e = launch_local_stack(a, layers.data(), s->shape.layers, s->final_norm, b, st, timer);
-        n += 1 + 7 * s->shape.layers;
-        EulerArgs eu{s->out, s->out_w, s->out_b, s->sampling, s->state, C, F, x_at, s->step_dt[i]};
+        n += local_stack_dispatches(a, b, s->shape.layers);
+        EulerArgs eu{s->x, s->row_sq, s->final_norm, s->out_w, s->out_b, s->sampling, s->state, C, F, x_at, s->step_dt[i]};
         if (e == hipSuccess) e = launch_dit_euler(a, eu, rows, st, timer);
         ++n;
     }
