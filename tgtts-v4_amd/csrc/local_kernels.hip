@@ -644,6 +644,7 @@ __global__ void __launch_bounds__(256) local_add_norm(LocalArgs a, const float* 
 // of the row's sequences; and the copied tokens.
 constexpr int EMBED_MAX = 1024;     // channels x frames a row's patch may hold
 constexpr int EMBED_CHANNELS = 64;  // channels at most (a row of W in 16 float4 loads)
+constexpr int EMBED_COPIES = 2;     // copied tokens at most
 
 // F frames to a patch, a template parameter so that every loop over them unrolls without a
 // branch (a branch around a load makes the compiler wait for it where the paths join).
@@ -657,12 +658,18 @@ __global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
 #pragma unroll
     for (int v = 0; v < EMBED_CHANNELS / 4; ++v)
         wq[v] = *reinterpret_cast<const float4*>(e.w + (size_t)n * C + 4 * min(v, C / 4 - 1));
+    // The copied tokens' values and the gain, loaded beside W.
+    const int K = a.hidden;
+    float cp[EMBED_COPIES];
+#pragma unroll
+    for (int t = 0; t < EMBED_COPIES; ++t)
+        cp[t] = e.copy_src[((size_t)(e.shared ? 0 : row * e.copies) + min(t, e.copies - 1)) * K + n];
+    const float g = e.gain ? e.gain[n] : 0.f;
     for (int i = threadIdx.x; i < C * F; i += 256) {
         const int f = i / C, c = i % C;
         frames[i] = e.src[((size_t)row * C + c) * F + f];
     }
-    __syncthreads();
-    if (blockIdx.x * 256 + threadIdx.x >= a.hidden) return;
+    __syncthreads();  // hidden is a multiple of 256 (the launch checks): every lane has a column
     float acc[F];
     const float b = e.bias[n];
 #pragma unroll
@@ -676,8 +683,6 @@ __global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
 #pragma unroll
             for (int f = 0; f < F; ++f) acc[f] += w4[i] * frames[f * C + 4 * v + i];
     }
-    const int K = a.hidden;
-    const float g = e.gain ? e.gain[n] : 0.f;
     // Token m's value v of column n, and with a gain the first norm's input: v g in bf16 and the
     // sum of squares of the wave's 64 columns (uniform over the wave).
     auto put = [&](size_t m, float v) {
@@ -694,10 +699,9 @@ __global__ void __launch_bounds__(256) local_embed(LocalArgs a, EmbedArgs e) {
         const size_t seq0 = (size_t)(row * e.seqs + s) * a.T;
 #pragma unroll
         for (int f = 0; f < F; ++f) put(seq0 + e.first + f, acc[f]);
-        for (int t = 0; t < e.copies; ++t) {
-            const float* src = e.copy_src + ((size_t)(e.shared ? 0 : row * e.copies) + t) * K;
-            put(seq0 + e.copy_at + t, (e.guided && s > 0) ? 0.f : src[n]);
-        }
+#pragma unroll
+        for (int t = 0; t < EMBED_COPIES; ++t)
+            if (t < e.copies) put(seq0 + e.copy_at + t, (e.guided && s > 0) ? 0.f : cp[t]);
     }
 }
 
@@ -940,6 +944,7 @@ hipError_t local_prepare() {
 }
 
 hipError_t launch_local_embed(const LocalArgs& a, const EmbedArgs& e, int rows, hipStream_t stream, DispatchTimer* timer) {
+    if (e.copies < 1 || e.copies > EMBED_COPIES || a.hidden % 256) return hipErrorInvalidValue;
     const dim3 grid((a.hidden + 255) / 256, rows), block(256);
     switch (e.frames) {
         case 1: dispatch("local_embed", local_embed<1>, grid, block, 0, stream, timer, a, e); break;
