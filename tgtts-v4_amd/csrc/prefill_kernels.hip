@@ -56,7 +56,12 @@ struct GemmTile {
     static_assert((NBUF - 1) * FW < 64, "the loads in flight fit the wave's counter");
 };
 
-enum Epilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2 };
+// EPI_RESIDUAL adds the residual rows to the products in the epilogue; EPI_RESIDUAL_IN starts the
+// accumulators at them (their loads at the start, beside the ring's, where the epilogue would wait
+// for them): for o_proj, whose short K leaves that wait exposed (52 against 61 us a layer at
+// 8 x 2048), not for down_proj, whose long K hides it and which ran 9 us slower so.
+enum Epilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2, EPI_RESIDUAL_IN = 3 };
+__host__ __device__ constexpr bool residual_epilogue(int epi) { return epi == EPI_RESIDUAL || epi == EPI_RESIDUAL_IN; }
 
 constexpr uint32_t TGX_SPARE_POS = 0xffffffffu;
 
@@ -242,11 +247,25 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
         stage_barrier();
     };
 
+    // The accumulators start at zero, or with EPI_RESIDUAL_IN at the residual rows themselves
+    // (rows past M read row M - 1, never stored): their loads go out first, ahead of the ring's,
+    // so that the epilogue waits for no read.
     f32x4 acc[WS][WT];
+    const int quad = lane / 16;
 #pragma unroll
     for (int s = 0; s < WS; ++s)
 #pragma unroll
-        for (int t = 0; t < WT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < WT; ++t) {
+            if constexpr (EPI == EPI_RESIDUAL_IN) {
+                const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
+                const int m = min(m0 + (wm * WT + t) * 16 + lane % 16, a.M - 1);
+                const float4 r = *reinterpret_cast<const float4*>(g.residual + (size_t)m * g.N + n);
+                acc[s][t] = f32x4{r.x, r.y, r.z, r.w};
+            } else {
+                acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    __builtin_amdgcn_sched_barrier(0);  // the residual's loads stay ahead of the ring's
 
     // The wave's fragments of stage st from LDS: fr[t] X tile t, fr[WT + s] W strip s.
     auto read = [&](int st, uint4 (&fr)[WT + WS]) __attribute__((always_inline)) {
@@ -281,7 +300,7 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
     // scales are taken once the first stage has landed (so have they), reaching LDS long before
     // the epilogue, past every barrier of the main loop.
     RowScale<TM> rs;
-    const bool scales = EPI != EPI_RESIDUAL && threadIdx.x < TM;  // whole waves
+    const bool scales = !residual_epilogue(EPI) && threadIdx.x < TM;  // whole waves
     if (scales) rs.load(g, m0);
 #pragma unroll
     for (int p = 0; p < NBUF - 1; ++p) fetch(p);  // K >= 1024: 32 stages at least
@@ -303,11 +322,11 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
 
     // Epilogue: tile (s, t) holds W rows 16 strip + 4 (lane / 16) + i against X row
     // m0 + 16 (WT wm + t) + lane % 16.
-    const int quad = lane / 16;
-    if (EPI == EPI_RESIDUAL) {
-        // With next_gain: each lane's squares of its row's 32 values of the wave's 128 columns,
-        // in strip order, then the 4 lanes of a row added (lanes l ^ 16, l ^ 32). The residual
-        // rows of four strips are loaded at once (rows past M read row M - 1, never stored).
+    if (residual_epilogue(EPI)) {
+        // The residual plus the products (EPI_RESIDUAL_IN: the accumulators hold both). With
+        // next_gain: each lane's squares of its row's 32 values of the wave's 128 columns, in
+        // strip order, then the 4 lanes of a row added (lanes l ^ 16, l ^ 32). EPI_RESIDUAL loads
+        // the residual rows of four strips at once (rows past M read row M - 1, never stored).
         float sq[WT] = {};
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -319,7 +338,8 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
 #pragma unroll
                 for (int t = 0; t < WT; ++t) {
                     const int m = min(m0 + (wm * WT + t) * 16 + lane % 16, a.M - 1);
-                    r[s4][t] = *reinterpret_cast<const float4*>(g.residual + (size_t)m * g.N + n);
+                    r[s4][t] = EPI == EPI_RESIDUAL ? *reinterpret_cast<const float4*>(g.residual + (size_t)m * g.N + n)
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
 #pragma unroll
@@ -330,11 +350,13 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                 for (int t = 0; t < WT; ++t) {
                     const int m = m0 + (wm * WT + t) * 16 + lane % 16;
                     if (m >= a.M) continue;
-                    float4 o;
-                    o.x = r[s4][t].x + acc[s][t][0];
-                    o.y = r[s4][t].y + acc[s][t][1];
-                    o.z = r[s4][t].z + acc[s][t][2];
-                    o.w = r[s4][t].w + acc[s][t][3];
+                    float4 o = make_float4(acc[s][t][0], acc[s][t][1], acc[s][t][2], acc[s][t][3]);
+                    if (EPI == EPI_RESIDUAL) {
+                        o.x = r[s4][t].x + acc[s][t][0];
+                        o.y = r[s4][t].y + acc[s][t][1];
+                        o.z = r[s4][t].z + acc[s][t][2];
+                        o.w = r[s4][t].w + acc[s][t][3];
+                    }
                     *reinterpret_cast<float4*>(g.out + (size_t)m * g.N + n) = o;
                     if (g.next_gain) {
                         *reinterpret_cast<uint2*>(g.out_n + act_index(m, n, g.N)) =
@@ -383,9 +405,13 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
     } else {  // EPI_QKV: rows of a strip pair as r, r + 8 (lanes l and l ^ 32)
         // Each of the tile's 256 rows' position, cache block and RoPE row, staged once in the LDS
         // the main loop is done with: a thread to a row, two round trips to memory in all.
-        float* t_cos = reinterpret_cast<float*>(lds);          // [TM][32]
-        float* t_sin = t_cos + TM * (HEAD_DIM / 2);            // [TM][32]
-        uint32_t* t_pos = reinterpret_cast<uint32_t*>(t_sin + TM * (HEAD_DIM / 2));  // [TM]
+        // A row's 32 values of cos and sin 36 floats apart: the 16 rows a wave's lanes read at once
+        // (and the threads' rows as they store them) then fall on distinct banks, where 32 apart
+        // put every row on the same ones.
+        constexpr int RS = HEAD_DIM / 2 + 4;
+        float* t_cos = reinterpret_cast<float*>(lds);          // [TM][RS]
+        float* t_sin = t_cos + TM * RS;                        // [TM][RS]
+        uint32_t* t_pos = reinterpret_cast<uint32_t*>(t_sin + TM * RS);  // [TM]
         uint32_t* t_blk = t_pos + TM;                           // [TM]
         const float* t_scale = row_scale;
         if (threadIdx.x < TM) {
@@ -400,9 +426,9 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                     if (a.rope) {
 #pragma unroll
                         for (int e = 0; e < HEAD_DIM / 2; e += 4) {
-                            *reinterpret_cast<float4*>(t_cos + j * (HEAD_DIM / 2) + e) =
+                            *reinterpret_cast<float4*>(t_cos + j * RS + e) =
                                 *reinterpret_cast<const float4*>(a.cos + (size_t)p * (HEAD_DIM / 2) + e);
-                            *reinterpret_cast<float4*>(t_sin + j * (HEAD_DIM / 2) + e) =
+                            *reinterpret_cast<float4*>(t_sin + j * RS + e) =
                                 *reinterpret_cast<const float4*>(a.sin + (size_t)p * (HEAD_DIM / 2) + e);
                         }
                     }
@@ -435,8 +461,8 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                 if (pos == TGX_SPARE_POS) continue;
                 float v[4];
                 if (rotate) {
-                    const float4 co = *reinterpret_cast<const float4*>(t_cos + j * (HEAD_DIM / 2) + p0);
-                    const float4 si = *reinterpret_cast<const float4*>(t_sin + j * (HEAD_DIM / 2) + p0);
+                    const float4 co = *reinterpret_cast<const float4*>(t_cos + j * RS + p0);
+                    const float4 si = *reinterpret_cast<const float4*>(t_sin + j * RS + p0);
                     const float c4[4] = {co.x, co.y, co.z, co.w}, s4[4] = {si.x, si.y, si.z, si.w};
                     // As upstream: x cos + rotate_half(x) sin (rope_rows.comp:52-59).
 #pragma unroll
@@ -852,8 +878,8 @@ int prefill_attention_tile(int group) { return group == 8 ? ATTN_TILE_8 : ATTN_T
 hipError_t prefill_prepare(size_t device_lds) {
     hipError_t e;
     if ((e = allow((const void*)prefill_gemm<EPI_QKV, QKV_ROWS, QKV_TM>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4, O_TM>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16, O_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL_IN, 4, O_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL_IN, 16, O_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4, DOWN_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16, DOWN_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_attention<ATTN_TILE, 2, 1>, device_lds)) != hipSuccess) return e;
@@ -894,9 +920,9 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
         GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr,
                    nullptr, L.post_norm, b.normed, b.row_sq};
         if (L.od_rows == 4)
-            gemm<EPI_RESIDUAL, 4, O_TM>("prefill_o", a, o, stream, timer);
+            gemm<EPI_RESIDUAL_IN, 4, O_TM>("prefill_o", a, o, stream, timer);
         else
-            gemm<EPI_RESIDUAL, 16, O_TM>("prefill_o", a, o, stream, timer);
+            gemm<EPI_RESIDUAL_IN, 16, O_TM>("prefill_o", a, o, stream, timer);
         GemmArgs gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, nullptr, b.mlp, nullptr, nullptr,
                     b.row_sq, nullptr, nullptr, nullptr};
         gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>("prefill_gate_up", a, gu, stream, timer);
