@@ -481,10 +481,12 @@ def measured_traffic(label: str, workload: str):
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
-    rec = json.loads(path.read_text()).get(label)
-    if not rec or rec.get("workload") != workload:
-        return None
-    return rec["bytes_per_launch"]
+    data = json.loads(path.read_text())
+    # Batch 1's records at the top, other workloads' under their own key ("batch64").
+    for rec in (data.get(label), data.get(workload.replace(" ", ""), {}).get(label)):
+        if isinstance(rec, dict) and rec.get("workload") == workload:
+            return rec["bytes_per_launch"]
+    return None
 
 
 def main() -> int:
