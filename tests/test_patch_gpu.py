@@ -111,6 +111,24 @@ def test_a_row_samples_the_same_patch_beside_others_as_alone(ctx):
     one.close()
 
 
+def test_repeated_samples_are_the_same_bits(ctx):
+    """The same inputs sampled again and again give the same bits: at 5 rows (128 tokens, the ring
+    GEMM with 4 and 8 token tiles) and 16 rows (384), every workgroup's loads, waits and barriers
+    read what they wait for (a race would show as a sample that differs from the first)."""
+    from tgx.synth import sampler_weights
+
+    spec = _dit_spec()
+    w = sampler_weights(spec, FEAT)
+    for rows in (5, 16):
+        s = _sampler(ctx, rows, spec, w)
+        mu, cond, noise, sampling = _inputs(rows, seed=13)
+        first = s.sample(mu, cond, noise, sampling)
+        for i in range(12):
+            again = s.sample(mu, cond, noise, sampling)
+            assert np.array_equal(first, again), (rows, i)
+        s.close()
+
+
 def test_with_out_proj_reading_nothing_the_patch_is_the_euler_closed_form(ctx):
     import patch_oracle as po
     from tgx.synth import sampler_weights
