@@ -98,8 +98,9 @@ def test_a_row_samples_the_same_patch_beside_others_as_alone(ctx):
     w = sampler_weights(spec, FEAT)
     mu, cond, noise, sampling = _inputs(16, seed=9)
     one = _sampler(ctx, 1, spec, w)
-    # 1 row takes the direct GEMMs, 5 and 16 rows the shared ones with 1 to 4 waves a workgroup.
-    for rows, picks in ((5, (0, 3)), (16, (0, 9, 15))):
+    # 1 row (22 tokens) takes the direct GEMMs; 5 rows (110 tokens, 128 padded) and 16 (352, 384)
+    # the ring GEMMs with 8 token tiles to a gate/up workgroup, 6 rows (132, 192) with 4.
+    for rows, picks in ((5, (0, 3)), (6, (5,)), (16, (0, 9, 15))):
         many = _sampler(ctx, rows, spec, w)
         got = many.sample(mu[:rows], cond[:rows], noise[:rows], sampling[:rows])
         again = many.sample(mu[:rows], cond[:rows], noise[:rows], sampling[:rows])
