@@ -73,6 +73,21 @@ __device__ __forceinline__ uint4 lds_read16(const uint4* p) {
     asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_offset(p)) : "memory");
     return v;
 }
+// Eight fragments STRIDE bytes apart from byte `base` + OFF, the offsets in the instructions' own
+// field (no address adds), in one asm statement.
+template <int OFF, int STRIDE>
+__device__ __forceinline__ void lds_read16_x8(uint32_t base, uint4 (&f)[8]) {
+    static_assert(OFF >= 0 && OFF + 7 * STRIDE < 65536, "ds offsets hold 16 bits");
+    asm volatile(
+        "ds_read_b128 %0, %8 offset:%9\n\tds_read_b128 %1, %8 offset:%10\n\t"
+        "ds_read_b128 %2, %8 offset:%11\n\tds_read_b128 %3, %8 offset:%12\n\t"
+        "ds_read_b128 %4, %8 offset:%13\n\tds_read_b128 %5, %8 offset:%14\n\t"
+        "ds_read_b128 %6, %8 offset:%15\n\tds_read_b128 %7, %8 offset:%16"
+        : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7])
+        : "v"(base), "n"(OFF), "n"(OFF + STRIDE), "n"(OFF + 2 * STRIDE), "n"(OFF + 3 * STRIDE), "n"(OFF + 4 * STRIDE),
+          "n"(OFF + 5 * STRIDE), "n"(OFF + 6 * STRIDE), "n"(OFF + 7 * STRIDE)
+        : "memory");
+}
 __device__ __forceinline__ void wait_lgkm() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // The values lds_read16 gave, usable: the wait, then each value passed through an asm the
 // compiler must run after it, so that nothing reads a register before its load has returned.

@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 namespace tgx {
 
@@ -552,10 +553,26 @@ __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* 
 // The values past `vlast` read as zero (as OnlineSoftmax's).
 constexpr float LAZY_SHIFT = 8.0f;
 
-// The largest of three floats in one instruction (fmaxf would quiet each operand first).
-__device__ __forceinline__ float max3(float a, float b, float c) {
+// The largest of a score tile's 16 floats (a v_max3_f32 chain; fmaxf would quiet each operand
+// first), in one asm statement that starts with 16 wait states. Its inputs come straight from
+// MFMAs, and a VALU read of an MFMA's result needs wait states after the MFMA issues (12 for the
+// bf16 16x16x32 on gfx950): the compiler gives them to its own instructions, but does not look
+// into inline asm.
+__device__ __forceinline__ float peak16(const f32x4 (&s)[4]) {
     float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    asm("s_nop 7\n\ts_nop 7\n\t"
+        "v_max3_f32 %0, %1, %2, %3\n\t"
+        "v_max3_f32 %0, %0, %4, %5\n\t"
+        "v_max3_f32 %0, %0, %6, %7\n\t"
+        "v_max3_f32 %0, %0, %8, %9\n\t"
+        "v_max3_f32 %0, %0, %10, %11\n\t"
+        "v_max3_f32 %0, %0, %12, %13\n\t"
+        "v_max3_f32 %0, %0, %14, %15\n\t"
+        "v_max_f32 %0, %0, %16"
+        : "=&v"(r)
+        : "v"(s[0][0]), "v"(s[0][1]), "v"(s[0][2]), "v"(s[0][3]), "v"(s[1][0]), "v"(s[1][1]), "v"(s[1][2]),
+          "v"(s[1][3]), "v"(s[2][0]), "v"(s[2][1]), "v"(s[2][2]), "v"(s[2][3]), "v"(s[3][0]), "v"(s[3][1]),
+          "v"(s[3][2]), "v"(s[3][3]));
     return r;
 }
 
@@ -588,10 +605,10 @@ struct LazySoftmax {
     f32x4 lsum = {0.f, 0.f, 0.f, 0.f};   // l, the column's sum of P (every slot alike)
     f32x4 o[4] = {};
 
-    // s: the block's scores less r; vf: its values, zeroed past the last position any column sees.
-    // MASK: keys past the column's position `pos` count for nothing; FIRST: block 0.
-    template <bool MASK, bool FIRST>
-    __device__ __forceinline__ void block(f32x4 (&s)[4], const uint4 (&vf)[8], uint32_t p0, uint32_t pos) {
+    // The block's scores less r, s, with the keys past the column's position `pos` at -inf when
+    // MASK; returns the lane's largest.
+    template <bool MASK>
+    __device__ __forceinline__ float peak(f32x4 (&s)[4], uint32_t p0, uint32_t pos) {
         const int lane = threadIdx.x % WAVE;
         if (MASK) {
 #pragma unroll
@@ -600,14 +617,12 @@ struct LazySoftmax {
                 for (int i = 0; i < 4; ++i)
                     if (p0 + pt * 16 + (lane / 16) * 4 + i > pos) s[pt][i] = -INFINITY;
         }
-        float mx = max3(s[0][0], s[0][1], s[0][2]);
-        mx = max3(mx, s[0][3], s[1][0]);
-        mx = max3(mx, s[1][1], s[1][2]);
-        mx = max3(mx, s[1][3], s[2][0]);
-        mx = max3(mx, s[2][1], s[2][2]);
-        mx = max3(mx, s[2][3], s[3][0]);
-        mx = max3(mx, s[3][1], s[3][2]);
-        mx = fmaxf(mx, s[3][3]);
+        return peak16(s);
+    }
+    // The VALU half of a block: s, its scores less r (mx the lane's largest, from peak), into P in
+    // bf16 (pf), the reference moved (and o, l rescaled) where the block asks. FIRST: block 0.
+    template <bool FIRST>
+    __device__ __forceinline__ void probs(f32x4 (&s)[4], float mx, uint4 (&pf)[2]) {
         if (FIRST || __builtin_amdgcn_ballot_w64(mx > LAZY_SHIFT) != 0) {
             // The columns' maxima (each over its four lanes); those past the shift, or all on the
             // first block, move r to it.
@@ -624,7 +639,6 @@ struct LazySoftmax {
                 lsum *= f;
             }
         }
-        uint4 pf[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const f32x4 a = s[2 * ks], b = s[2 * ks + 1];
@@ -633,8 +647,11 @@ struct LazySoftmax {
                                 pack_bf16x2(__builtin_amdgcn_exp2f(b[0]), __builtin_amdgcn_exp2f(b[1])),
                                 pack_bf16x2(__builtin_amdgcn_exp2f(b[2]), __builtin_amdgcn_exp2f(b[3])));
         }
-        // Column sums of P (every row of ones^T P is the sum; bf16 1.0 is 0x3f80) and O^T += V^T P,
-        // each accumulator's two products apart, the other four between them.
+    }
+    // The MFMA half: column sums of P (every row of ones^T P is the sum; bf16 1.0 is 0x3f80) and
+    // O^T += V^T P, each accumulator's two products apart, the other four between them. vf: the
+    // block's values, zeroed past the last position any column sees.
+    __device__ __forceinline__ void accumulate(const uint4 (&pf)[2], const uint4 (&vf)[8]) {
         const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -727,25 +744,32 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     LazySoftmax sm[CG];
     // The wave's first position: blocks wholly at or below it need no mask.
     const uint32_t first = tile.pos0 + w * TOK;
+    // Blocks 0 .. nfull - 1 need no mask: they end at or before the wave's first position and the
+    // tile's last (a wave past the tile's count has a first position past its last).
+    const int nfull = (int)((min(first, last) + 1) / BLOCK_TOKENS);
 
     // The ring: block bi's keys are in registers when step bi starts. Its values are read from
     // LDS while the score MFMAs run; then block bi + 1's stage is waited for (the barrier also says
-    // every wave is done with stage bi - 1, which block bi + NS - 1 takes) and its keys read while
-    // the softmax and the value MFMAs of block bi run.
-    auto read8 = [&](const uint4* src, uint4 (&f)[8]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = lds_read16(src + i * 64 + lane);
-    };
+    // every wave is done with stage bi - 1, which block bi + NS - 1 takes) and, once the softmax has
+    // read every score, its keys read while the exponentials and the value MFMAs of block bi run.
+    // Fragment i of a tile is 1 KiB i on, lane l's 16 bytes 16 l on: its LDS address is the lane's
+    // base plus a constant.
+    constexpr int STAGE_BYTES = ATTN_STAGE * 16;
+    constexpr int VALUES = KV_TILE * 2;  // the value tile's bytes from the stage's start
+    const uint32_t ring0 = lds_offset(attn_ring) + lane * 16;
 #pragma unroll
     for (int bi = 0; bi < NS - 1; ++bi) fetch(bi);
     wait_vm<LOADS * (NS - 2)>();
     stage_barrier();
     uint4 kf[8], vf[8];
-    read8(attn_ring, kf);
+    lds_read16_x8<0, 1024>(ring0, kf);
     lds_landed(kf);
-    for (int bi = 0; bi < blocks; ++bi) {
-        const uint4* st = attn_ring + (bi % NS) * ATTN_STAGE;
-        read8(st + KV_TILE / 8, vf);
+    // Step bi, its softmax half as MASK (keys past a column's position count for nothing, and the
+    // values past the tile's last position read as zero) and FIRST (block 0). Past the last block
+    // the keys of a stage the ring has already waited for are read and never used.
+    auto step = [&](int bi, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value, FIRST = decltype(first_tag)::value;
+        lds_read16_x8<VALUES, 1024>(ring0 + (uint32_t)(bi % NS) * STAGE_BYTES, vf);
         // The first halves of every tile's product before any second half: the MFMAs a tile's
         // second half waits on are done by the time it issues.
         f32x4 s[CG][4];
@@ -763,29 +787,39 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         stage_barrier();
         fetch(bi + NS - 1);  // its id's LDS read waits for every LDS read before it: vf has landed
         lds_arrived(vf);
-        const bool more = bi + 1 < blocks;
-        if (more) read8(attn_ring + ((bi + 1) % NS) * ATTN_STAGE, kf);
         const uint32_t p0 = (uint32_t)bi * BLOCK_TOKENS;
-        const bool full = p0 + BLOCK_TOKENS - 1 <= first;
+        float mx[CG];
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) mx[cg] = sm[cg].template peak<MASK>(s[cg], p0, cpos[cg]);
+        // The keys' reads may take registers the compiler counts free once an MFMA has issued, and
+        // an MFMA reads its accumulator input late in its passes, past the wait states the
+        // compiler would give its own loads (it does not look into asm): the reads come after the
+        // maxima, whose reads of every score wait for every score MFMA to finish.
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) asm volatile("" ::"v"(mx[cg]));
+        lds_read16_x8<0, 1024>(ring0 + (uint32_t)((bi + 1) % NS) * STAGE_BYTES, kf);
         // Values past the tile's last position read as zero (attention_rows.comp:1-13): every
         // position up to it was written by this run or before it; the cache may hold anything
-        // past it, NaN included, and 0 NaN is NaN.
-        if (p0 + BLOCK_TOKENS - 1 > last) zero_values_past(vf, p0, last);
+        // past it, NaN included, and 0 NaN is NaN. A block with no mask ends at or before the
+        // tile's last position.
+        if (MASK && p0 + BLOCK_TOKENS - 1 > last) zero_values_past(vf, p0, last);
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
-            if (bi == 0) {
-                if (full)
-                    sm[cg].template block<false, true>(s[cg], vf, p0, cpos[cg]);
-                else
-                    sm[cg].template block<true, true>(s[cg], vf, p0, cpos[cg]);
-            } else if (full) {
-                sm[cg].template block<false, false>(s[cg], vf, p0, cpos[cg]);
-            } else {
-                sm[cg].template block<true, false>(s[cg], vf, p0, cpos[cg]);
-            }
+            uint4 pf[2];
+            sm[cg].template probs<FIRST>(s[cg], mx[cg], pf);
+            sm[cg].accumulate(pf, vf);
         }
-        if (more) lds_landed(kf);
-    }
+        lds_landed(kf);
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    if (nfull > 0)
+        step(0, no{}, yes{});
+    else
+        step(0, yes{}, yes{});
+    int bi = 1;
+    for (; bi < nfull; ++bi) step(bi, no{}, no{});
+    for (; bi < blocks; ++bi) step(bi, yes{}, no{});
     // No load into this workgroup's LDS may still be in flight when its waves end.
     wait_vm<0>();
 #pragma unroll
