@@ -553,27 +553,18 @@ __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* 
 // The values past `vlast` read as zero (as OnlineSoftmax's).
 constexpr float LAZY_SHIFT = 8.0f;
 
-// The largest of a score tile's 16 floats (a v_max3_f32 chain; fmaxf would quiet each operand
-// first), in one asm statement that starts with 16 wait states. Its inputs come straight from
-// MFMAs, and a VALU read of an MFMA's result needs wait states after the MFMA issues (12 for the
-// bf16 16x16x32 on gfx950): the compiler gives them to its own instructions, but does not look
-// into inline asm.
+// The largest of a score tile's 16 floats, in plain code: the compiler makes it a v_max3_f32 chain
+// (quieting only the first two operands) and gives each read of an MFMA's result the wait states
+// it needs, which it could not do for inline asm.
 __device__ __forceinline__ float peak16(const f32x4 (&s)[4]) {
-    float r;
-    asm("s_nop 7\n\ts_nop 7\n\t"
-        "v_max3_f32 %0, %1, %2, %3\n\t"
-        "v_max3_f32 %0, %0, %4, %5\n\t"
-        "v_max3_f32 %0, %0, %6, %7\n\t"
-        "v_max3_f32 %0, %0, %8, %9\n\t"
-        "v_max3_f32 %0, %0, %10, %11\n\t"
-        "v_max3_f32 %0, %0, %12, %13\n\t"
-        "v_max3_f32 %0, %0, %14, %15\n\t"
-        "v_max_f32 %0, %0, %16"
-        : "=&v"(r)
-        : "v"(s[0][0]), "v"(s[0][1]), "v"(s[0][2]), "v"(s[0][3]), "v"(s[1][0]), "v"(s[1][1]), "v"(s[1][2]),
-          "v"(s[1][3]), "v"(s[2][0]), "v"(s[2][1]), "v"(s[2][2]), "v"(s[2][3]), "v"(s[3][0]), "v"(s[3][1]),
-          "v"(s[3][2]), "v"(s[3][3]));
-    return r;
+    float m = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
+    m = fmaxf(fmaxf(m, s[0][3]), s[1][0]);
+    m = fmaxf(fmaxf(m, s[1][1]), s[1][2]);
+    m = fmaxf(fmaxf(m, s[1][3]), s[2][0]);
+    m = fmaxf(fmaxf(m, s[2][1]), s[2][2]);
+    m = fmaxf(fmaxf(m, s[2][3]), s[3][0]);
+    m = fmaxf(fmaxf(m, s[3][1]), s[3][2]);
+    return fmaxf(m, s[3][3]);
 }
 
 // The value fragments of a block (the A operand of O^T = V^T P, value_index) past `vlast` zeroed:
@@ -619,26 +610,26 @@ struct LazySoftmax {
         }
         return peak16(s);
     }
-    // The VALU half of a block: s, its scores less r (mx the lane's largest, from peak), into P in
-    // bf16 (pf), the reference moved (and o, l rescaled) where the block asks. FIRST: block 0.
+    // The block's columns past the shift (or all on the first block) move r to their maximum (each
+    // column's over its four lanes; mx the lane's largest, from peak), s and o, l rescaled. A
+    // column that stays subtracts 0 and scales by 1: the same bits as no call.
     template <bool FIRST>
-    __device__ __forceinline__ void probs(f32x4 (&s)[4], float mx, uint4 (&pf)[2]) {
-        if (FIRST || __builtin_amdgcn_ballot_w64(mx > LAZY_SHIFT) != 0) {
-            // The columns' maxima (each over its four lanes); those past the shift, or all on the
-            // first block, move r to it.
-            float cm = fmaxf(mx, lane_xor16(mx));
-            cm = fmaxf(cm, lane_xor32(cm));
-            const float d = (FIRST || cm > LAZY_SHIFT) ? cm : 0.f;
+    __device__ __forceinline__ void rescale(f32x4 (&s)[4], float mx) {
+        float cm = fmaxf(mx, lane_xor16(mx));
+        cm = fmaxf(cm, lane_xor32(cm));
+        const float d = (FIRST || cm > LAZY_SHIFT) ? cm : 0.f;
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) s[pt] -= d;
-            neg_r -= d;
-            if (!FIRST) {
-                const float f = __builtin_amdgcn_exp2f(-d);
+        for (int pt = 0; pt < 4; ++pt) s[pt] -= d;
+        neg_r -= d;
+        if (!FIRST) {
+            const float f = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
-                for (int dt = 0; dt < 4; ++dt) o[dt] *= f;
-                lsum *= f;
-            }
+            for (int dt = 0; dt < 4; ++dt) o[dt] *= f;
+            lsum *= f;
         }
+    }
+    // P = 2^s in bf16 (pf): s, the block's scores less r, after any rescale.
+    __device__ __forceinline__ static void probs(const f32x4 (&s)[4], uint4 (&pf)[2]) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const f32x4 a = s[2 * ks], b = s[2 * ks + 1];
@@ -679,7 +670,7 @@ constexpr int ATTN_STAGE = 2 * KV_TILE / 8;  // uint4
 constexpr int ATTN_STAGES = 4;
 
 template <int TILE, int WAVES, int CG>
-__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(2))) prefill_attention(PrefillArgs a, const uint16_t* __restrict__ q,
+__global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(CG >= 4 ? 1 : 2))) prefill_attention(PrefillArgs a, const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ kvpool,
                                                                  uint16_t* __restrict__ attended,
                                                                  const PrefillTile* __restrict__ tiles) {
@@ -803,10 +794,21 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         // past it, NaN included, and 0 NaN is NaN. A block with no mask ends at or before the
         // tile's last position.
         if (MASK && p0 + BLOCK_TOKENS - 1 > last) zero_values_past(vf, p0, last);
+        // One check for the wave's column groups (the rescale is rare past block 0), so that the
+        // exponentials and value MFMAs below are one stretch of code: the compiler runs a group's
+        // exponentials beside the previous group's MFMAs (the SIMD runs a wave's VALU work beside
+        // its own MFMAs, not beside another wave's).
+        float peak_all = mx[0];
+#pragma unroll
+        for (int cg = 1; cg < CG; ++cg) peak_all = fmaxf(peak_all, mx[cg]);
+        if (FIRST || __builtin_amdgcn_ballot_w64(peak_all > LAZY_SHIFT) != 0) {
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) sm[cg].template rescale<FIRST>(s[cg], mx[cg]);
+        }
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
             uint4 pf[2];
-            sm[cg].template probs<FIRST>(s[cg], mx[cg], pf);
+            LazySoftmax::probs(s[cg], pf);
             sm[cg].accumulate(pf, vf);
         }
         lds_landed(kf);
