@@ -382,7 +382,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_gate_up(DecodeArgs a, Layer
             const float sc = scale[t0 + t][c];
             const float gate = reduced<2>(red[t], 0, r, c) * sc;
             const float up = reduced<2>(red[t], 1, r, c) * sc;
-            l.mlp[operand_index(b, s * 16 + r, a.rows)] = (uint16_t)bf16_bits(gate / (1.0f + __expf(-gate)) * up);
+            l.mlp[operand_index(b, s * 16 + r, a.rows)] = (uint16_t)bf16_bits(silu(gate) * up);
         }
     }
 }

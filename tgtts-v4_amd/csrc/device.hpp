@@ -19,6 +19,13 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c)
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// x sigmoid(x) = x / (1 + e^-x), e^-x as 2^(-x log2 e) and the reciprocal by v_rcp_f32 (1 ulp),
+// where a division takes ten instructions (the epilogues that call it sit beside other waves'
+// MFMAs, which the SIMD does not run beside VALU work).
+__device__ __forceinline__ float silu(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 

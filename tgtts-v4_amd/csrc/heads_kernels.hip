@@ -52,7 +52,7 @@ __global__ void __launch_bounds__(256) gemv_linear(LinearArgs a) {
         if (n >= a.N) continue;
         float v = sum[i] + a.bias[n];
         if (a.act == ACT_SILU) {
-            v = v / (1.0f + __expf(-v));
+            v = silu(v);
         } else if (a.act == ACT_LEVELS) {
             // The scalar quantizer (gemv_linear.comp:54-59): tanh rounded to a multiple of 1 / L,
             // ties to even.

@@ -145,7 +145,7 @@ __device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm&
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float gate = acc[i] * rs, u = up[i] * rs;
-            v[i] = gate / (1.0f + __expf(-gate)) * u;
+            v[i] = silu(gate) * u;
         }
         *reinterpret_cast<uint2*>(g.mlp + act_index(m, n, inner)) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     } else if (EPI == LEPI_QKV) {  // a strip's rows pair as r, r + 8 (lanes l and l ^ 32)

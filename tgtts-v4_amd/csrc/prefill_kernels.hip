@@ -397,7 +397,7 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float gate = acc[s][t][i] * rs, up = acc[s + 4][t][i] * rs;
-                    v[i] = gate / (1.0f + __expf(-gate)) * up;
+                    v[i] = silu(gate) * up;
                 }
                 uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                 *reinterpret_cast<uint2*>(g.mlp + act_index(m, n, inner)) = packed;
