@@ -47,14 +47,13 @@ struct GemmTile {
     static constexpr int X_TILES = TM / 16;
     static constexpr int X_STAGE = X_TILES * 64;
     static constexpr int NBUF = TM == 256 ? 4 : 3;
-    // The first half of the waves load W's fragments, the second half X's: FW and FX 1 KiB loads
-    // a wave issues a stage.
-    static constexpr int FW = W_STRIPS / (WAVES / 2);
-    static constexpr int FX = X_TILES / (WAVES / 2);
+    // The 1 KiB loads a wave issues a stage: the stage's W and X fragments over the waves.
+    static constexpr int FB = (W_STRIPS + X_TILES) / WAVES;
+    static_assert(FB * WAVES == W_STRIPS + X_TILES, "the fragments split evenly over the waves");
     static constexpr size_t LDS = (size_t)NBUF * (W_STAGE + X_STAGE) * 16 + TM * sizeof(float);
     static_assert(THREADS >= TM, "the q/k/v epilogue stages a row to a thread");
     static_assert(ROW_TILE_MAX % TM == 0, "M_pad is a multiple of TM");
-    static_assert((NBUF - 1) * FW < 64, "the loads in flight fit the wave's counter");
+    static_assert(NBUF * FB < 64, "the loads in flight fit the wave's counter");
 };
 
 // EPI_RESIDUAL adds the residual rows to the products in the epilogue; EPI_RESIDUAL_IN starts the
@@ -174,7 +173,7 @@ template <int EPI, int WR, int TM>
 __global__ void __launch_bounds__(GemmTile<TM>::THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_gemm(PrefillArgs a, GemmArgs g) {
     using T = GemmTile<TM>;
-    constexpr int NBUF = T::NBUF, X_STAGE = T::X_STAGE, FW = T::FW, FX = T::FX;
+    constexpr int NBUF = T::NBUF, X_STAGE = T::X_STAGE;
     extern __shared__ uint4 lds[];
     uint4* ws = lds;                     // [NBUF][W_STAGE]
     uint4* xs = lds + NBUF * W_STAGE;    // [NBUF][X_STAGE]
@@ -189,62 +188,52 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
     const int stages = kblocks;
     const int m0 = mb * TM;
 
-    // A stage is 16 weight fragments and TM / 16 vector fragments of 1 KiB (the first half of
-    // the waves load W's, FW each, the second half X's, FX each), loaded straight from memory
-    // into LDS: lane l of a load writes bytes 16 l .. 16 l + 15 of the fragment, the MFMA operand
-    // order. A wave issues the same number of loads every stage, so its count in flight says
-    // which stages have landed. Fragment j of stage st is lane's base + off[j] + st * step (a
-    // k-block further along K), the offsets 32-bit (a tensor holds fewer than 2^32 elements).
-    const bool loads_w = w < T::WAVES / 2;
-    constexpr int FMAX = FW > FX ? FW : FX;
-    const uint16_t* base = loads_w ? g.w : g.x;
-    uint32_t off[FMAX];
-    uint32_t step_elems;
-    uint4* dst0;
-    if (loads_w) {
+    // A stage is 16 weight fragments and TM / 16 vector fragments of 1 KiB, loaded straight from
+    // memory into LDS: lane l of a load writes bytes 16 l .. 16 l + 15 of the fragment, the MFMA
+    // operand order. Every wave loads FB of them (slot j of wave w is fragment FB w + j: the W
+    // strips, then the X tiles), the same number every stage, so that its count in flight says
+    // which stages have landed and no wave's loads hold the others at the barrier. Fragment j of
+    // stage st is the lane's base + off[j] + st * fstep[j] (a k-block further along K), the
+    // offsets 32-bit (a tensor holds fewer than 2^32 elements).
+    constexpr int FB = T::FB;
+    const uint16_t* fbase[FB];
+    uint32_t off[FB], fstep[FB];
+    uint4* fdst[FB];
+    int fstride[FB];
 #pragma unroll
-        for (int j = 0; j < FW; ++j) off[j] = (uint32_t)fragment_index<WR>(stage_strip<EPI>(nb, w * FW + j, g.N), 0, kblocks, lane);
-        step_elems = WR * 32;
-        dst0 = ws + w * FW * 64;
-    } else {
-        const int x0 = (w - T::WAVES / 2) * FX;  // the wave's first X tile
-#pragma unroll
-        for (int j = 0; j < FX; ++j) off[j] = (uint32_t)(m0 / 16 + x0 + j) * (uint32_t)kblocks * 512u + (uint32_t)lane * 8u;
-        step_elems = 512;
-        dst0 = xs + x0 * 64;
+    for (int j = 0; j < FB; ++j) {
+        const int f = w * FB + j;
+        if (f < W_STRIPS) {
+            fbase[j] = g.w;
+            off[j] = (uint32_t)fragment_index<WR>(stage_strip<EPI>(nb, f, g.N), 0, kblocks, lane);
+            fstep[j] = WR * 32;
+            fdst[j] = ws + f * 64;
+            fstride[j] = W_STAGE;
+        } else {
+            const int x = f - W_STRIPS;
+            fbase[j] = g.x;
+            off[j] = (uint32_t)(m0 / 16 + x) * (uint32_t)kblocks * 512u + (uint32_t)lane * 8u;
+            fstep[j] = 512;
+            fdst[j] = xs + x * 64;
+            fstride[j] = X_STAGE;
+        }
     }
-    const int stage_stride = loads_w ? W_STAGE : X_STAGE;
-    auto fetch = [&](int st) __attribute__((always_inline)) {
-        uint4* dst = dst0 + (st % NBUF) * stage_stride;
-        const uint32_t along = (uint32_t)st * step_elems;
-        if (loads_w) {
+    // Stage st into buffer buf.
+    auto fetch = [&](int st, int buf) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < FW; ++j) load_to_lds(base + (off[j] + along), dst + j * 64);
-        } else {
-#pragma unroll
-            for (int j = 0; j < FX; ++j) load_to_lds(base + (off[j] + along), dst + j * 64);
-        }
+        for (int j = 0; j < FB; ++j) load_to_lds(fbase[j] + (off[j] + (uint32_t)st * fstep[j]), fdst[j] + buf * fstride[j]);
     };
-    // Waits until stage st has landed for every wave: no more than the stages fetched after it
-    // in flight for this wave, then the barrier, which also says that every wave is done with
-    // stage st - 1, whose buffer the next fetch takes.
-    auto landed = [&](int st) __attribute__((always_inline)) {
-        const int after = min(NBUF - 2, stages - 1 - st);
-        if (loads_w) {
-            if (after >= 2)
-                wait_vm<2 * FW>();
-            else if (after == 1)
-                wait_vm<FW>();
-            else
-                wait_vm<0>();
-        } else {
-            if (after >= 2)
-                wait_vm<2 * FX>();
-            else if (after == 1)
-                wait_vm<FX>();
-            else
-                wait_vm<0>();
-        }
+    // Waits until a stage has landed for every wave: no more than the `after` stages fetched after
+    // it in flight for this wave, then the barrier, which also says that every wave is done with
+    // the step before (and with the buffers it read into registers).
+    auto landed = [&](int after) __attribute__((always_inline)) {
+        static_assert(NBUF <= 3, "up to two stages in flight past the one waited for");
+        if (after >= 2)
+            wait_vm<2 * FB>();
+        else if (after == 1)
+            wait_vm<FB>();
+        else
+            wait_vm<0>();
         stage_barrier();
     };
 
@@ -277,23 +266,49 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
         for (int s = 0; s < WS; ++s) fr[WT + s] = lds_read16(&ws[buf * W_STAGE + (wn * WS + s) * 64 + lane]);
     };
     // Step st: the products of stage st from `cur` (read in the step before) while stage st + 1's
-    // fragments are read into `next`, so that the LDS reads overlap the products. Stage
-    // st + NBUF - 1 is fetched first, into the buffer of stage st - 1, which every wave had read
-    // by the end of step st - 2 (the prologue, for stage 0), before the barrier of step st - 1.
+    // fragments are read into `next`, so that the LDS reads overlap the products. Two ways to keep
+    // the ring fed (what suits q/k/v and gate/up slows o_proj and down_proj, whose X operands are
+    // the larger and whose L2 more stages in flight crowd):
+    //  AHEAD: past the barrier, stage st + NBUF into the buffer of stage st (read into registers
+    //    in the step before, by every wave before this barrier), its loads spread between the
+    //    products: NBUF stages in flight. Past the last stage the last is loaded again into a
+    //    buffer no step reads after, and the last step reads the last stage again (never used):
+    //    every step the same, with no branch.
+    //  otherwise: before the barrier, stage st + NBUF - 1 into the buffer of stage st - 1, which
+    //    every wave had read by the end of step st - 2 (the prologue, for stage 0).
+    constexpr bool AHEAD = !residual_epilogue(EPI);
     auto step = [&](int st, uint4 (&cur)[WT + WS], uint4 (&next)[WT + WS]) __attribute__((always_inline)) {
-        if (st + NBUF - 1 < stages) fetch(st + NBUF - 1);
-        const bool more = st + 1 < stages;
-        if (more) {
-            landed(st + 1);
-            read(st + 1, next);
+        if constexpr (AHEAD) {
+            landed(NBUF - 2);  // stage st + 1
+            read(min(st + 1, stages - 1), next);
+#pragma unroll
+            for (int s = 0; s < WS; ++s)
+#pragma unroll
+                for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(cur[WT + s], cur[t], acc[s][t]);
+            fetch(min(st + NBUF, stages - 1), st % NBUF);
+            // A load after each WS WT / FB products (the few left over after the last load).
+#pragma unroll
+            for (int j = 0; j < FB; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x008, WS * WT / FB, 0);  // MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);             // a load
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            lds_landed(next);
+        } else {
+            if (st + NBUF - 1 < stages) fetch(st + NBUF - 1, (st + NBUF - 1) % NBUF);
+            const bool more = st + 1 < stages;
+            if (more) {
+                landed(min(NBUF - 2, stages - 2 - st));  // stage st + 1
+                read(st + 1, next);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < WS; ++s)
+#pragma unroll
+                for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(cur[WT + s], cur[t], acc[s][t]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) lds_landed(next);
         }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int s = 0; s < WS; ++s)
-#pragma unroll
-            for (int t = 0; t < WT; ++t) acc[s][t] = mfma16(cur[WT + s], cur[t], acc[s][t]);
-        __builtin_amdgcn_sched_barrier(0);
-        if (more) lds_landed(next);
     };
 
     uint4 fa[WT + WS], fb[WT + WS];
@@ -303,9 +318,11 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
     RowScale<TM> rs;
     const bool scales = !residual_epilogue(EPI) && threadIdx.x < TM;  // whole waves
     if (scales) rs.load(g, m0);
+    // K >= 1024: 32 stages at least.
+    constexpr int PRIMED = AHEAD ? NBUF : NBUF - 1;
 #pragma unroll
-    for (int p = 0; p < NBUF - 1; ++p) fetch(p);  // K >= 1024: 32 stages at least
-    landed(0);
+    for (int p = 0; p < PRIMED; ++p) fetch(p, p);
+    landed(PRIMED - 1);  // stage 0
     if (scales) {
         rs.settle();
         row_scale[threadIdx.x] = rs.scale(a, g);
@@ -318,7 +335,9 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
         step(st, fa, fb);
         step(st + 1, fb, fa);
     }
-    // The epilogue below may reuse the LDS: every wave is done with the ring.
+    // No load to the LDS in flight (AHEAD's last ones), every wave done with the ring: the
+    // epilogue below may reuse the LDS.
+    wait_vm<0>();
     stage_barrier();
 
     // Epilogue: tile (s, t) holds W rows 16 strip + 4 (lane / 16) + i against X row
