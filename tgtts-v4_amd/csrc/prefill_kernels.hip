@@ -403,20 +403,25 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
     } else if (EPI == EPI_SILU) {
         const int inner = g.N / 2;
         const float* scale = row_scale;
+        // silu(r g) (r u) for the row's scale r and the products g, u, as g u / ((1 + e) k) with
+        // e = 2^(-r log2(e) g) and k = 1 / r^2: the row's two constants once, then four VALU
+        // instructions and two transcendentals an output.
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
+        for (int t = 0; t < WT; ++t) {
+            const int j = (wm * WT + t) * 16 + lane % 16;
+            const int m = m0 + j;
+            if (m >= a.M) continue;
+            const float rs = scale[j];
+            const float c = -rs * 1.4426950408889634f, k = __builtin_amdgcn_rcpf(rs * rs);
 #pragma unroll
-            for (int t = 0; t < WT; ++t) {
-                const int j = (wm * WT + t) * 16 + lane % 16;
-                const int m = m0 + j;
-                if (m >= a.M) continue;
-                const float rs = scale[j];
+            for (int s = 0; s < 4; ++s) {
+                const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
                 float v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float gate = acc[s][t][i] * rs, up = acc[s + 4][t][i] * rs;
-                    v[i] = silu(gate) * up;
+                    const float gp = acc[s][t][i], up = acc[s + 4][t][i];
+                    const float e = __builtin_amdgcn_exp2f(gp * c);
+                    v[i] = (gp * up) * __builtin_amdgcn_rcpf(__builtin_fmaf(e, k, k));
                 }
                 uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                 *reinterpret_cast<uint2*>(g.mlp + act_index(m, n, inner)) = packed;
