@@ -105,3 +105,31 @@ def test_null_arguments_are_refused_with_a_message():
     lib = tgx.library()
     assert lib.tgx_decoder_step(None, 0, None, None) == 8
     assert b"null" in lib.tgx_last_error()
+
+
+def test_handles_made_from_a_context_close_newest_first():
+    """A patch step (or an engine, or a prompter) uses the encoder, LM side and sampler made
+    before it, which must outlive it (include/tgx.h): the context's close and the exit handler
+    close the handles made from it newest first."""
+    import tgx
+
+    closed = []
+
+    class Handle:
+        def __init__(self, n):
+            self.n = n
+
+        def close(self):
+            closed.append(self.n)
+
+    handles = [Handle(n) for n in range(5)]
+    for h in handles:
+        tgx._opened(h)
+    try:
+        for h in tgx._newest_first(list(tgx._open_decoders)):
+            if h in handles:
+                h.close()
+        assert closed == [4, 3, 2, 1, 0]
+    finally:
+        for h in handles:
+            tgx._open_decoders.discard(h)

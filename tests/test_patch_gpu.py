@@ -413,7 +413,10 @@ def test_a_step_of_fewer_rows_runs_on_the_fewest_program_each_row_as_on_the_larg
     for pick in ([3], [1, 4], [0, 2, 4], [4, 3, 2, 1, 0]):
         patch, stop = step.run_rows([tgx.Row(0, r) for r in pick], cond[pick], noise[pick], sampling[pick])
         for k, r in enumerate(pick):
-            assert np.array_equal(patch[k], full_patch[r]) and np.array_equal(stop[k], full_stop[r]), (pick, r)
+            dp = float(np.abs(patch[k].astype(np.float64) - full_patch[r]).max())
+            ds = float(np.abs(stop[k].astype(np.float64) - full_stop[r]).max())
+            assert np.array_equal(patch[k], full_patch[r]) and np.array_equal(stop[k], full_stop[r]), (
+                f"rows {pick}, row {r}: patch max|d| {dp:.3g}, stop max|d| {ds:.3g}")
     # The components' own entry points take the whole batch again.
     embedding = enc.encode(cond)
     mu, stop = side.step_rows([tgx.Row(0, r) for r in range(rows)], embedding)

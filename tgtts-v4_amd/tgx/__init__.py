@@ -10,6 +10,7 @@ never fall back to anything else.
 from __future__ import annotations
 
 import atexit
+import itertools
 import ctypes
 import os
 import sys
@@ -214,14 +215,26 @@ _lib: Optional[ctypes.CDLL] = None
 
 # Every open handle, closed before the interpreter exits: the HIP runtime tears itself down in the
 # C library's exit handlers, after which no handle may be freed. Decoders, samplers and LM sides
-# (everything made from a context) go before contexts.
+# (everything made from a context) go before contexts, newest first: a patch step or an engine
+# before the encoder, LM side and sampler it uses, which must outlive it.
 _open_decoders: "weakref.WeakSet" = weakref.WeakSet()
 _open_contexts: "weakref.WeakSet" = weakref.WeakSet()
+_open_order = itertools.count()
+
+
+def _opened(handle) -> None:
+    """Registers a handle made from a context, to be closed before it, newest first."""
+    handle._open_seq = next(_open_order)
+    _open_decoders.add(handle)
+
+
+def _newest_first(handles) -> list:
+    return sorted(handles, key=lambda h: getattr(h, "_open_seq", -1), reverse=True)
 
 
 @atexit.register
 def _close_all() -> None:
-    for d in list(_open_decoders):
+    for d in _newest_first(list(_open_decoders)):
         d.close()
     for c in list(_open_contexts):
         c.close()
@@ -485,7 +498,7 @@ class Context:
 
     def close(self) -> None:
         if self._h:
-            for d in list(_open_decoders):
+            for d in _newest_first(list(_open_decoders)):
                 if getattr(d, "ctx", None) is self:
                     d.close()
             library().tgx_context_destroy(self._h)
@@ -512,7 +525,7 @@ class Decoder:
         b = _Batch(batch.rows, batch.slots, batch.block_tokens, batch.blocks)
         self._h = ctypes.c_void_p()
         _check(library().tgx_decoder_create(ctx._h, ctypes.byref(s), ctypes.byref(b), ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
 
     # -- weights --
     def load_checkpoint(self, checkpoint, prefix: str = "") -> None:

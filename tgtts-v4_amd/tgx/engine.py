@@ -13,7 +13,7 @@ from typing import Optional
 
 import numpy as np
 
-from . import Context, Shape, _check, _HeadsShape, _open_decoders, _ptr, _shape_struct, library
+from . import Context, Shape, _check, _HeadsShape, _opened, _ptr, _shape_struct, library
 from .patch import HeadsShape
 
 
@@ -67,7 +67,7 @@ class Engine:
         b, r, e, d = (ctypes.byref(s[0]) for s in structs)
         _check(library().tgx_engine_create(ctx._h, checkpoint._h, b, r, ctypes.byref(hs), e, d, feat_dim, patch_size,
                                            ctypes.byref(st), ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
 
     @classmethod
     def from_config(cls, ctx: Context, config, checkpoint, settings: Settings = Settings(),

@@ -24,7 +24,7 @@ from . import (
     Shape,
     _Batch,
     _HeadsShape,
-    _open_decoders,
+    _opened,
     _PatchShape,
     _ptr,
     _Row,
@@ -83,7 +83,7 @@ class Sampler:
         p = _PatchShape(patch.feat_dim, patch.patch_size, patch.timesteps, patch.rows)
         self._h = ctypes.c_void_p()
         _check(library().tgx_sampler_create(ctx._h, ctypes.byref(s), ctypes.byref(p), ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
 
     def load(self, name: str, values: np.ndarray) -> None:
         a, dtype = _weights(values)
@@ -181,7 +181,7 @@ class LmSide:
         self._h = ctypes.c_void_p()
         _check(library().tgx_lm_side_create(ctx._h, ctypes.byref(b), ctypes.byref(r), ctypes.byref(bt), ctypes.byref(hs),
                                             ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
 
     def load(self, name: str, values: np.ndarray) -> None:
         a, dtype = _weights(values)
@@ -288,7 +288,7 @@ class Encoder:
         p = _PatchShape(patch.feat_dim, patch.patch_size, patch.timesteps, patch.rows)
         self._h = ctypes.c_void_p()
         _check(library().tgx_encoder_create(ctx._h, ctypes.byref(s), ctypes.byref(p), ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
 
     def load(self, name: str, values: np.ndarray) -> None:
         a, dtype = _weights(values)
@@ -339,7 +339,7 @@ class PatchStep:
         self.ctx = side.ctx
         self._h = ctypes.c_void_p()
         _check(library().tgx_patch_step_create(encoder._h, side._h, sampler._h, ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
 
     def run_rows(self, rows: Sequence[Optional[Row]], cond, noise, sampling):
         """PatchStep::run_rows (patch.rs:356-415): up to the step's rows, run on its program of the

@@ -9,7 +9,7 @@ import sys
 from dataclasses import dataclass
 import numpy as np
 
-from . import Context, _check, _open_decoders, _ptr, _Row, library
+from . import Context, _check, _opened, _ptr, _Row, library
 
 
 class _Prompt(ctypes.Structure):
@@ -44,7 +44,7 @@ class PromptCache:
         self.ctx = ctx
         self._h = ctypes.c_void_p()
         _check(library().tgx_prompt_cache_create(ctx._h, budget, ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
 
     def bytes(self) -> int:
         v = ctypes.c_size_t()
@@ -82,7 +82,7 @@ class Prompter:
         self.ctx = step.side.ctx
         self._h = ctypes.c_void_p()
         _check(library().tgx_prompter_create(step._h, max_rows, ctypes.byref(self._h)))
-        _open_decoders.add(self)
+        _opened(self)
         self.hidden = step.side.base_shape.hidden
         self.latent = step.side.heads.latent
 
