@@ -43,8 +43,9 @@ typedef enum {
 /* The last error message of the calling thread ("" when none). */
 const char* tgx_last_error(void);
 
-/* Element types of host arrays handed to tgx_decoder_load. */
-typedef enum { TGX_F32 = 0, TGX_BF16 = 1, TGX_F16 = 2 } tgx_dtype;
+/* Element types of host arrays handed to tgx_decoder_load, and of a kernel's bindings
+ * (ElementType, crates/vulkan/src/element.rs; u32 only for bindings). */
+typedef enum { TGX_F32 = 0, TGX_BF16 = 1, TGX_F16 = 2, TGX_U32 = 3 } tgx_dtype;
 
 /* ---- context: replaces vulkan::Context (crates/vulkan/src/context.rs:237-540) ---- */
 
@@ -524,6 +525,118 @@ tgx_status tgx_engine_take_frames(tgx_engine* e, int slot, float* out, int max, 
 tgx_status tgx_engine_finish(tgx_engine* e, int slot, float* out, int max, int* n);
 /* What the prompt cache keeps (Generator::prompt_cache, generator.rs:364-367). */
 tgx_status tgx_engine_prompt_cache(const tgx_engine* e, size_t* bytes, int* voices);
+
+/* ---- the runtime beneath the models: crates/vulkan's Memory, Kernel and Recording ----
+ *
+ * What the graph crate asks of crates/vulkan (lib.rs:50-60), for callers that compose programs of
+ * their own from the library's kernels: memory in a residence, read and written by the host
+ * between runs; the kernels by name, each with its bindings in order (crates/graph/src/kernels.rs:
+ * 27-63,104-161); and programs, chains of dispatches recorded once (here a HIP graph) and run as
+ * often as needed (crates/vulkan/src/recording.rs:116-760). */
+
+/* Residence (crates/vulkan/src/memory.rs:61-72): HBM for TGX_DEVICE; pinned host memory the
+ * GPU reaches over PCIe for TGX_UPLOAD (the host writes, kernels read) and TGX_READBACK (kernels
+ * write, the host reads). */
+typedef enum { TGX_DEVICE = 0, TGX_UPLOAD = 1, TGX_READBACK = 2 } tgx_residence;
+
+typedef struct tgx_memory tgx_memory;
+
+/* Context::memory_in (context.rs:495-498): `bytes` (> 0) of zeroed memory in `residence`. */
+tgx_status tgx_alloc(tgx_context* ctx, uint64_t bytes, tgx_residence residence, tgx_memory** out);
+/* Frees `mem`; TGX_E_BUSY while a program that binds it exists (a recording owns its buffers,
+ * recording.rs:6-13), and then nothing is freed. */
+tgx_status tgx_free(tgx_memory* mem);
+tgx_status tgx_memory_info(const tgx_memory* mem, uint64_t* bytes, tgx_residence* residence);
+/* Buffer::write_at / read_at: `bytes` at `offset`, copied before the call returns; refuses a
+ * range past the end (TGX_E_SHAPE) and, while a program that binds `mem` runs, TGX_E_BUSY. */
+tgx_status tgx_write(tgx_memory* mem, uint64_t offset, const void* src, uint64_t bytes);
+tgx_status tgx_read(tgx_memory* mem, uint64_t offset, void* dst, uint64_t bytes);
+
+/* How the kernels keep a weight matrix: bf16 MFMA tiles of strips of 16 rows (with q/k/v's rows
+ * ordered so that a strip holds 8 RoPE pairs of one head), or of 4 rows (o_proj and down_proj at
+ * batches of up to 16 rows). */
+typedef enum { TGX_TILES_16 = 0, TGX_TILES_4 = 1, TGX_TILES_QKV = 2 } tgx_tiles;
+/* The bytes a [rows][cols] matrix takes as `tiles` (0 for a shape the tiles cannot hold). */
+uint64_t tgx_tiles_bytes(tgx_tiles tiles, int rows, int cols);
+/* Writes a row-major [rows][cols] matrix of `dtype` at `offset` as `tiles`, rounded to bf16 to
+ * nearest even, as tgx_decoder_load lays out its weights (load_stack's write, decode.rs:740-776). */
+tgx_status tgx_write_tiles(tgx_memory* mem, uint64_t offset, const void* src, tgx_dtype dtype, tgx_tiles tiles,
+                           int rows, int cols);
+/* Shape::rope_tables (decode.rs:143-168): cos and sin [capacity][head_dim / 2] f32. */
+tgx_status tgx_rope_tables(const tgx_shape* shape, float* cos, float* sin);
+
+/* The kernels (kernels.rs KernelInfo): each has a name, bindings in order and constants in order.
+ * The decode step's kernels keep the reference's names but for "attention_decode", which does
+ * attention_split's and attention_combine's work in one; every decode kernel takes the constants
+ * hidden, inner, heads, kv_heads, rows, capacity, slots, max_blocks, blocks, eps (its f32 bits),
+ * rope, then its own. An optional binding may be left out (memory NULL). */
+typedef enum { TGX_READ = 0, TGX_WRITE = 1 } tgx_access;
+typedef struct {
+    char name[24];
+    tgx_access access;
+    tgx_dtype element;
+    int optional;
+} tgx_binding_info;
+int tgx_kernel_count(void);
+/* The kernel called `name` (TGX_E_KERNELS when none is). */
+tgx_status tgx_kernel_find(const char* name, int* kernel);
+tgx_status tgx_kernel_info(int kernel, const char** name, int* bindings, int* constants);
+tgx_status tgx_kernel_binding(int kernel, int i, tgx_binding_info* out);
+tgx_status tgx_kernel_constant(int kernel, int i, const char** name);
+
+/* recording.rs Binding (:31-61): `size` bytes of `memory` from `offset`; size 0 for the rest. */
+typedef struct {
+    tgx_memory* memory;
+    uint64_t offset;
+    uint64_t size;
+} tgx_binding;
+
+/* recording.rs Dispatch (:74-86): a kernel, one binding per binding it declares in order, its
+ * constants in order (f32 ones as their bits), the grid (all 0: the grid the kernel takes for the
+ * constants; otherwise it must be that grid, as check_groups holds, context.rs:46-57), and whether
+ * it waits for every earlier dispatch of the program (`barrier`; without it, it waits only for
+ * those before the last barrier and may run beside the dispatches since). Every binding must hold
+ * the bytes the kernel reaches for the constants (Kernels::check, kernels.rs), else TGX_E_SHAPE. */
+typedef struct {
+    int kernel;
+    const tgx_binding* bindings;
+    int nbindings;
+    const uint32_t* constants;
+    int nconstants;
+    uint32_t groups[3];
+    int barrier;
+} tgx_dispatch;
+
+typedef struct tgx_program tgx_program;
+
+/* Context::record (context.rs:507-518): a program, its dispatches added by
+ * tgx_program_launch, recorded as a HIP graph by tgx_program_end; `timed` as Recording's (each
+ * dispatch launched alone between events of its own, so that tgx_program_timings gives its time). */
+tgx_status tgx_program_begin(tgx_context* ctx, int timed, tgx_program** out);
+/* Adds a dispatch, checked against its kernel's bindings, constants and grid. */
+tgx_status tgx_program_launch(tgx_program* p, const tgx_dispatch* d);
+/* Ends the recording: the program may run from now on and takes no more dispatches. */
+tgx_status tgx_program_end(tgx_program* p);
+/* Recording::start_program / Submission::wait (recording.rs:616-660, 747-753; 60 s at most) /
+ * submit_program (:610-614: both). */
+tgx_status tgx_program_start(tgx_program* p);
+tgx_status tgx_program_wait(tgx_program* p);
+tgx_status tgx_program_run(tgx_program* p);
+/* Recording::timings (recording.rs:663-674): each dispatch's kernel name and GPU time in the last
+ * run of a timed program; *n the dispatches (0 when not timed), of which `max` are written. */
+tgx_status tgx_program_timings(tgx_program* p, int max, tgx_timing* out, int* n);
+/* Recording::elapsed (recording.rs:676-681): the last run's GPU time, from events around it. */
+tgx_status tgx_program_elapsed_ms(tgx_program* p, float* ms);
+tgx_status tgx_program_destroy(tgx_program* p);
+
+/* Recording::copy_in / copy_out (recording.rs:522-597): regions copied from `src` to `dst` on the
+ * context's stream, in order, before the call returns; TGX_E_SHAPE for a region past either end. */
+typedef struct {
+    uint64_t src_offset;
+    uint64_t dst_offset;
+    uint64_t bytes;
+} tgx_region;
+tgx_status tgx_copy_regions(tgx_context* ctx, tgx_memory* dst, tgx_memory* src, const tgx_region* regions, int n);
 
 #ifdef __cplusplus
 }

@@ -14,7 +14,7 @@ ROOT = Path(__file__).resolve().parent.parent
 
 def header_functions():
     text = (ROOT / "include" / "tgx.h").read_text()
-    return sorted(set(re.findall(r"^(?:tgx_status|void|const char\*)\s+(tgx_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:tgx_status|void|const char\*|int|uint64_t)\s+(tgx_\w+)\(", text, re.M)))
 
 
 def test_the_library_exports_every_function_the_header_declares():

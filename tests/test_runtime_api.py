@@ -1,0 +1,78 @@
+"""The runtime beneath the models on the CPU (no device): the kernel table by name with its
+bindings in order (crates/graph/src/kernels.rs:104-161 keeps the same per kernel), the RoPE tables
+as Shape::rope_tables computes them (crates/graph/src/decode.rs:143-168, unit-tested at
+decode.rs:1232-1242), and the weight tiles' refusals."""
+
+import numpy as np
+import pytest
+
+
+def test_the_kernels_keep_the_reference_names_and_binding_order():
+    import tgx.runtime as rt
+
+    table = {k.name: k for k in rt.kernels()}
+    # attention_decode does attention_split's and attention_combine's work in one kernel.
+    assert set(table) == {"gemv_qkv_rope", "attention_decode", "gemv_residual", "gemv_gate_up", "rmsnorm", "stream_read"}
+    names = lambda k: [b.name for b in table[k].bindings]
+    # The reference's bindings keep their relative order (kernels.rs:104-161): x, gain, W, cos,
+    # sin, position -> q, cache; x, W, residual -> out; x, gain -> out; data -> out.
+    qkv = names("gemv_qkv_rope")
+    for a, b in zip(["x", "gain", "w", "cos", "sin", "positions", "q", "kv"], ["gain", "w", "cos", "sin", "positions", "q", "kv", None]):
+        if b is not None:
+            assert qkv.index(a) < qkv.index(b), (a, b)
+    assert names("gemv_residual")[:3] == ["x", "w", "residual"] and names("gemv_residual")[4] == "out"
+    assert names("rmsnorm")[:3] == ["x", "gain", "out"]
+    assert names("stream_read") == ["data", "out"]
+    # What each kernel writes, and only that.
+    writes = {k: [b.name for b in table[k].bindings if b.access == rt.WRITE] for k in table}
+    assert writes == {
+        "gemv_qkv_rope": ["q", "kv"],
+        "attention_decode": ["attended"],
+        "gemv_residual": ["out", "out_n", "out_sq"],
+        "gemv_gate_up": ["mlp"],
+        "rmsnorm": ["out", "positions"],
+        "stream_read": ["out"],
+    }
+    common = ("hidden", "inner", "heads", "kv_heads", "rows", "capacity", "slots", "max_blocks", "blocks", "eps", "rope")
+    for k in ("gemv_qkv_rope", "attention_decode", "gemv_gate_up"):
+        assert table[k].constants == common
+    assert table["gemv_residual"].constants == common + ("K", "N", "strip_rows")
+    assert table["rmsnorm"].constants == common + ("advance",)
+    assert table["stream_read"].constants == ()
+
+
+def test_an_unknown_kernel_is_refused():
+    import tgx
+    import tgx.runtime as rt
+
+    with pytest.raises(tgx.TgxError) as e:
+        rt.kernel("attention_split")
+    assert e.value.kind == "kernels"
+
+
+def test_rope_tables_as_the_reference_unit_tests_them():
+    """decode.rs:1232-1242: identity at t = 0, cos 1 and sin 1 at t = 1 for j = 0; every entry the
+    f32 recipe 1 / theta^(2j / d), t r inv, as the oracle restates it."""
+    import oracle
+    import tgx
+    import tgx.runtime as rt
+
+    shape = tgx.Shape(capacity=96)
+    cos, sin = rt.rope_tables(shape)
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+    # f32's cos(1) and sin(1): the double values rounded once to f32.
+    assert cos[1, 0] == np.float32(np.cos(1.0)) and sin[1, 0] == np.float32(np.sin(1.0))
+    ref_cos, ref_sin = oracle.rope_tables(96, 64)
+    assert np.array_equal(cos, ref_cos) and np.array_equal(sin, ref_sin)
+
+
+def test_weight_tiles_take_whole_strips_and_k_blocks():
+    import tgx.runtime as rt
+
+    assert rt.tiles_bytes(rt.TILES_QKV, 1280, 1024) == 1280 * 1024 * 2
+    assert rt.tiles_bytes(rt.TILES_4, 1024, 4096) == 1024 * 4096 * 2
+    assert rt.tiles_bytes(rt.TILES_16, 8192, 1024) == 8192 * 1024 * 2
+    assert rt.tiles_bytes(rt.TILES_16, 1000, 1024) == 0  # rows in strips of 16
+    assert rt.tiles_bytes(rt.TILES_4, 1024, 1000) == 0  # columns in k-blocks of 32
+    assert rt.tiles_bytes(rt.TILES_QKV, 1040, 1024) == 0  # q/k/v rows a multiple of the head
+    assert rt.tiles_bytes(7, 16, 32) == 0

@@ -48,6 +48,7 @@ SOURCES = {
     "checkpoint.cpp": HOST_FLAGS,
     "prompt.cpp": HOST_FLAGS,
     "engine.cpp": HOST_FLAGS,
+    "runtime_api.cpp": HOST_FLAGS,
 }
 
 

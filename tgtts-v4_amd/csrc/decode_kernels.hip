@@ -570,7 +570,8 @@ __global__ void __launch_bounds__(WAVE) final_rmsnorm(DecodeArgs a, const float*
 }
 
 // ---------------------------------------------------------------------------------------------
-// Launchers.
+// Launchers: each kernel's instance, grid, block and LDS for a shape, shared by the step's
+// launchers below and by the program API, so that a dispatch made either way runs the same code.
 
 namespace {
 
@@ -593,45 +594,89 @@ template <int CH> struct PickResidual4 { static auto get() { return gemv_residua
 template <int CH> struct PickResidual16 { static auto get() { return gemv_residual<CH, 16>; } };
 template <int CH> struct PickFinal { static auto get() { return final_rmsnorm<CH>; } };
 
-hipError_t residual(const char* label, const DecodeArgs& a, const ResidualArgs& r, hipStream_t stream, DispatchTimer* timer) {
-    const dim3 grid(r.N / r.R, decode_tiles(a.rows)), block(GEMV_THREADS);
-    const int chunks = r.K / CHUNK_COLS;
-    if (r.R == 4)
-        dispatch(label, by_chunks<PickResidual4>(chunks), grid, block, 0, stream, timer, a, r);
-    else if (r.R == 16)
-        dispatch(label, by_chunks<PickResidual16>(chunks), grid, block, 0, stream, timer, a, r);
-    else
-        return hipErrorInvalidValue;
-    return hipSuccess;
+// The kernel of `launch` with its arguments `params`, timed by the timer's next events when given.
+hipError_t dispatch_launch(const char* label, const KernelLaunch& k, void** params, hipStream_t stream, DispatchTimer* timer) {
+    if (timer && timer->used < timer->capacity) {
+        const int i = timer->used++;
+        timer->labels[i] = label;
+        return hipExtLaunchKernel(k.func, k.grid, k.block, params, k.lds, stream, timer->start[i], timer->stop[i], 0);
+    }
+    return hipLaunchKernel(k.func, k.grid, k.block, params, k.lds, stream);
 }
 
 }  // namespace
 
-hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o, const ResidualArgs& down,
-                               hipStream_t stream, DispatchTimer* timer) {
-    const int tiles = decode_tiles(a.rows);
-    const int qkv_strips = (a.heads + 2 * a.kv_heads) * HEAD_DIM / QKV_ROWS;
-    const dim3 block(GEMV_THREADS);
-    const int hidden_chunks = a.hidden / CHUNK_COLS;
-    if (l.xn)
-        dispatch("gemv_qkv_rope", by_chunks<PickQkvNormed>(hidden_chunks), dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
+KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed) {
+    const int chunks = a.hidden / CHUNK_COLS;
+    KernelLaunch k;
+    k.func = prenormed ? (const void*)by_chunks<PickQkvNormed>(chunks) : (const void*)by_chunks<PickQkv>(chunks);
+    k.grid = dim3((a.heads + 2 * a.kv_heads) * HEAD_DIM / QKV_ROWS, decode_tiles(a.rows));
+    k.block = dim3(GEMV_THREADS);
+    return k;
+}
+
+KernelLaunch attention_launch(const DecodeArgs& a) {
+    KernelLaunch k;
+    k.func = (const void*)attention_decode;
+    k.grid = dim3(a.kv_heads, a.rows);
+    k.block = dim3(ATTN_THREADS);
+    k.lds = (uint32_t)attention_lds(a);
+    return k;
+}
+
+KernelLaunch residual_launch(const DecodeArgs& a, const ResidualArgs& r) {
+    const int chunks = r.K / CHUNK_COLS;
+    KernelLaunch k;
+    if (r.R == 4)
+        k.func = (const void*)by_chunks<PickResidual4>(chunks);
+    else if (r.R == 16)
+        k.func = (const void*)by_chunks<PickResidual16>(chunks);
     else
-        dispatch("gemv_qkv_rope", by_chunks<PickQkv>(hidden_chunks), dim3(qkv_strips, tiles), block, 0, stream, timer, a, l);
-    dispatch("attention_decode", attention_decode, dim3(a.kv_heads, a.rows), dim3(ATTN_THREADS), attention_lds(a), stream, timer, a, l);
-    hipError_t e = residual("o_proj", a, o, stream, timer);
-    if (e != hipSuccess) return e;
+        return k;
+    k.grid = dim3(r.N / r.R, decode_tiles(a.rows));
+    k.block = dim3(GEMV_THREADS);
+    return k;
+}
+
+KernelLaunch gate_up_launch(const DecodeArgs& a) {
+    const int tiles = decode_tiles(a.rows);
+    const int hidden_chunks = a.hidden / CHUNK_COLS;
     // Past one tile a workgroup takes two or four, reading the strips' weights once for them (for a
     // hidden size of one chunk: more would not fit the registers).
     const int per = hidden_chunks > 1 || tiles == 1 ? 1 : tiles == 2 ? 2 : 4;
-    const dim3 gu_grid(a.inner / 16, (tiles + per - 1) / per);
-    if (per == 1)
-        dispatch("gemv_gate_up", by_chunks<PickGateUp>(hidden_chunks), gu_grid, block, 0, stream, timer, a, l);
-    else if (per == 2)
-        dispatch("gemv_gate_up", gemv_gate_up<1, 2>, gu_grid, block, 0, stream, timer, a, l);
-    else
-        dispatch("gemv_gate_up", gemv_gate_up<1, 4>, gu_grid, block, 0, stream, timer, a, l);
-    if ((e = residual("down_proj", a, down, stream, timer)) != hipSuccess) return e;
-    return hipGetLastError();
+    KernelLaunch k;
+    k.func = per == 1 ? (const void*)by_chunks<PickGateUp>(hidden_chunks)
+             : per == 2 ? (const void*)gemv_gate_up<1, 2>
+                        : (const void*)gemv_gate_up<1, 4>;
+    k.grid = dim3(a.inner / 16, (tiles + per - 1) / per);
+    k.block = dim3(GEMV_THREADS);
+    return k;
+}
+
+KernelLaunch final_norm_launch(const DecodeArgs& a) {
+    KernelLaunch k;
+    k.func = (const void*)by_chunks<PickFinal>(a.hidden / CHUNK_COLS);
+    k.grid = dim3(a.rows);
+    k.block = dim3(WAVE);
+    return k;
+}
+
+hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o, const ResidualArgs& down,
+                               hipStream_t stream, DispatchTimer* timer) {
+    DecodeArgs aa = a;
+    LayerArgs ll = l;
+    ResidualArgs oo = o, dd = down;
+    void* layer_params[] = {&aa, &ll};
+    hipError_t e = dispatch_launch("gemv_qkv_rope", qkv_launch(a, l.xn != nullptr), layer_params, stream, timer);
+    if (e == hipSuccess) e = dispatch_launch("attention_decode", attention_launch(a), layer_params, stream, timer);
+    const KernelLaunch ko = residual_launch(a, o), kd = residual_launch(a, down);
+    if (!ko.func || !kd.func) return hipErrorInvalidValue;
+    void* o_params[] = {&aa, &oo};
+    if (e == hipSuccess) e = dispatch_launch("o_proj", ko, o_params, stream, timer);
+    if (e == hipSuccess) e = dispatch_launch("gemv_gate_up", gate_up_launch(a), layer_params, stream, timer);
+    void* down_params[] = {&aa, &dd};
+    if (e == hipSuccess) e = dispatch_launch("down_proj", kd, down_params, stream, timer);
+    return e != hipSuccess ? e : hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -656,11 +701,19 @@ __global__ void __launch_bounds__(STREAM_THREADS) stream_read(const uint4* __res
 
 size_t stream_read_unit() { return (size_t)STREAM_THREADS * STREAM_LOADS * sizeof(uint4); }
 
+KernelLaunch stream_read_launch(size_t bytes) {
+    KernelLaunch k;
+    k.func = (const void*)stream_read;
+    k.grid = dim3((unsigned)(bytes / stream_read_unit()));
+    k.block = dim3(STREAM_THREADS);
+    return k;
+}
+
 hipError_t launch_stream_read(const void* data, size_t bytes, uint32_t* out, hipStream_t stream) {
     if (bytes == 0 || bytes % stream_read_unit()) return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)(bytes / stream_read_unit());
-    stream_read<<<grid, STREAM_THREADS, 0, stream>>>((const uint4*)data, out);
-    return hipGetLastError();
+    const uint4* d = (const uint4*)data;
+    void* params[] = {&d, &out};
+    return dispatch_launch("stream_read", stream_read_launch(bytes), params, stream, nullptr);
 }
 
 int decode_tiles(int rows) { return (rows + 15) / 16; }
@@ -683,9 +736,10 @@ size_t decode_attention_lds(int heads, int kv_heads) { return (size_t)ATTN_WAVES
 
 hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out, uint32_t* positions,
                              int advance, hipStream_t stream, DispatchTimer* timer) {
-    dispatch("final_norm", by_chunks<PickFinal>(a.hidden / CHUNK_COLS), dim3(a.rows), dim3(WAVE), 0, stream, timer, a, x, gain,
-             out, positions, advance);
-    return hipGetLastError();
+    DecodeArgs aa = a;
+    void* params[] = {&aa, &x, &gain, &out, &positions, &advance};
+    const hipError_t e = dispatch_launch("final_norm", final_norm_launch(a), params, stream, timer);
+    return e != hipSuccess ? e : hipGetLastError();
 }
 
 }  // namespace tgx

@@ -85,6 +85,23 @@ int decode_max_capacity();
 size_t decode_attention_lds(int heads, int kv_heads);
 // Lets the attention take up to `device_lds` bytes of LDS per workgroup.
 hipError_t decode_prepare(size_t device_lds);
+// A dispatch of one of the step's kernels: the kernel instance chosen for the shape, with its grid,
+// block and LDS. The step's launchers and the program API both launch these, so that a kernel
+// dispatched either way is the same code. Each takes (DecodeArgs, LayerArgs) but for
+// gemv_residual (DecodeArgs, ResidualArgs), final_rmsnorm (DecodeArgs, x, gain, out, positions,
+// advance) and stream_read (data, out).
+struct KernelLaunch {
+    const void* func = nullptr;
+    dim3 grid, block;
+    uint32_t lds = 0;
+};
+KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed);
+KernelLaunch attention_launch(const DecodeArgs& a);
+KernelLaunch residual_launch(const DecodeArgs& a, const ResidualArgs& r);  // func null unless r.R is 4 or 16
+KernelLaunch gate_up_launch(const DecodeArgs& a);
+KernelLaunch final_norm_launch(const DecodeArgs& a);
+KernelLaunch stream_read_launch(size_t bytes);
+
 hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o, const ResidualArgs& down,
                                hipStream_t stream, DispatchTimer* timer = nullptr);
 hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out, uint32_t* positions,

@@ -209,6 +209,29 @@ EXPORTS = [
     "tgx_engine_take_frames",
     "tgx_engine_finish",
     "tgx_engine_prompt_cache",
+    "tgx_alloc",
+    "tgx_free",
+    "tgx_memory_info",
+    "tgx_write",
+    "tgx_read",
+    "tgx_tiles_bytes",
+    "tgx_write_tiles",
+    "tgx_rope_tables",
+    "tgx_kernel_count",
+    "tgx_kernel_find",
+    "tgx_kernel_info",
+    "tgx_kernel_binding",
+    "tgx_kernel_constant",
+    "tgx_program_begin",
+    "tgx_program_launch",
+    "tgx_program_end",
+    "tgx_program_start",
+    "tgx_program_wait",
+    "tgx_program_run",
+    "tgx_program_timings",
+    "tgx_program_elapsed_ms",
+    "tgx_program_destroy",
+    "tgx_copy_regions",
 ]
 
 _lib: Optional[ctypes.CDLL] = None
