@@ -71,8 +71,6 @@ def kernel_bytes(shape, label: str, rows: int, kv_positions: int) -> int:
         return qkv * h * 2 + rows * h * 4 + rows * qkv * 2
     if label == "attention_decode":
         return kv_positions * KV * d * 2 * 2 + rows * H * d * 2 * 2
-    if label == "qkv_attention":  # a batch of one row: q/k/v and the attention before its position
-        return qkv * h * 2 + rows * h * 4 + rows * qkv * 2 + kv_positions * KV * d * 2 * 2 + rows * H * (d + 2) * 4
     if label == "o_proj":
         return h * H * d * 2 + rows * H * d * 2 + rows * h * 4 * 2
     if label == "gemv_gate_up":

@@ -11,11 +11,8 @@ def test_the_kernels_keep_the_reference_names_and_binding_order():
     import tgx.runtime as rt
 
     table = {k.name: k for k in rt.kernels()}
-    # attention_decode does attention_split's and attention_combine's work in one kernel; a batch of
-    # one row takes qkv_attention and gemv_residual_fold in place of gemv_qkv_rope, attention_decode
-    # and o_proj's gemv_residual.
-    assert set(table) == {"gemv_qkv_rope", "attention_decode", "gemv_residual", "gemv_gate_up", "rmsnorm", "stream_read",
-                          "qkv_attention", "gemv_residual_fold"}
+    # attention_decode does attention_split's and attention_combine's work in one kernel.
+    assert set(table) == {"gemv_qkv_rope", "attention_decode", "gemv_residual", "gemv_gate_up", "rmsnorm", "stream_read"}
     names = lambda k: [b.name for b in table[k].bindings]
     # The reference's bindings keep their relative order (kernels.rs:104-161): x, gain, W, cos,
     # sin, position -> q, cache; x, W, residual -> out; x, gain -> out; data -> out.
@@ -29,21 +26,17 @@ def test_the_kernels_keep_the_reference_names_and_binding_order():
     # What each kernel writes, and only that.
     writes = {k: [b.name for b in table[k].bindings if b.access == rt.WRITE] for k in table}
     assert writes == {
-        "gemv_qkv_rope": ["q", "kv", "kv_cur"],
+        "gemv_qkv_rope": ["q", "kv"],
         "attention_decode": ["attended"],
-        "qkv_attention": ["q", "kv", "kv_cur", "state"],
-        "gemv_residual_fold": ["out", "out_n", "out_sq"],
         "gemv_residual": ["out", "out_n", "out_sq"],
         "gemv_gate_up": ["mlp"],
         "rmsnorm": ["out", "positions"],
         "stream_read": ["out"],
     }
     common = ("hidden", "inner", "heads", "kv_heads", "rows", "capacity", "slots", "max_blocks", "blocks", "eps", "rope")
-    for k in ("gemv_qkv_rope", "attention_decode", "gemv_gate_up", "qkv_attention"):
+    for k in ("gemv_qkv_rope", "attention_decode", "gemv_gate_up"):
         assert table[k].constants == common
     assert table["gemv_residual"].constants == common + ("K", "N", "strip_rows")
-    assert table["gemv_residual_fold"].constants == common + ("K", "N", "strip_rows")
-    assert names("qkv_attention")[:13] == names("gemv_qkv_rope")
     assert table["rmsnorm"].constants == common + ("advance",)
     assert table["stream_read"].constants == ()
 

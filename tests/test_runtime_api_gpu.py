@@ -72,27 +72,17 @@ class StepProgram:
         self.sq_a, self.sq_b = keep(M(rows * h)), keep(M(rows * h))  # [rows][h / 4] f32
         self.q, self.att = keep(M(rows * H * 64 * 2)), keep(M(rows * H * 64 * 2))
         self.mlp = keep(M(rows * inner * 2))
-        self.kv_cur = keep(M(rows * KV * 2 * 64 * 2))
-        self.state = keep(M(H * 2 * 66 * 4))
         c = [h, inner, H, KV, rows, capacity, slots, max_blocks, blocks, rt.f32_bits(spec.eps), 1]
         self.program = p = rt.Program(ctx, timed=timed)
         for l in range(L):
             first = l == 0
             x_in = self.x if first else self.h_a
-            qkv_in = [self.x if first else None, None if first else self.xn_a, None if first else self.sq_a, self.in_norm[l],
-                      self.qkv[l], self.cos, self.sin, self.positions, self.slots_mem, self.table, self.q, self.kv[l],
-                      self.kv_cur]
-            if rows == 1:
-                # A batch of one row: q/k/v with the attention before the row's position, then
-                # o_proj folding the row's own position in.
-                p.dispatch("qkv_attention", qkv_in + [self.row_table, self.state], c)
-                p.dispatch("gemv_residual_fold", [self.q, self.kv_cur, self.state, self.o[l], x_in, self.post_norm[l], self.h_b,
-                                                  self.xn_b, self.sq_b], c + [H * 64, h, strip_rows])
-            else:
-                p.dispatch("gemv_qkv_rope", qkv_in, c)
-                p.dispatch("attention_decode", [self.q, self.kv[l], self.positions, self.row_table, self.kv_cur, self.att], c)
-                p.dispatch("gemv_residual", [self.att, self.o[l], x_in, self.post_norm[l], self.h_b, self.xn_b, self.sq_b],
-                           c + [H * 64, h, strip_rows])
+            p.dispatch("gemv_qkv_rope", [self.x if first else None, None if first else self.xn_a, None if first else self.sq_a,
+                                         self.in_norm[l], self.qkv[l], self.cos, self.sin, self.positions, self.slots_mem,
+                                         self.table, self.q, self.kv[l]], c)
+            p.dispatch("attention_decode", [self.q, self.kv[l], self.positions, self.row_table, self.att], c)
+            p.dispatch("gemv_residual", [self.att, self.o[l], x_in, self.post_norm[l], self.h_b, self.xn_b, self.sq_b],
+                       c + [H * 64, h, strip_rows])
             p.dispatch("gemv_gate_up", [self.xn_b, self.sq_b, self.gu[l], self.mlp], c)
             last = l == L - 1
             p.dispatch("gemv_residual", [self.mlp, self.down[l], self.h_b, None if last else self.in_norm[l + 1], self.h_a,
@@ -128,21 +118,20 @@ def reference_decoder(ctx, spec, capacity, rows):
     return dec
 
 
-@pytest.mark.parametrize("rows,strip_rows", [(3, 4), (3, 16), (1, 4)])
-def test_a_step_composed_by_kernel_name_is_the_decoders_step_bit_for_bit(ctx, rows, strip_rows):
-    """2 layers, 3 rows in slots 2, 0, 1 (or 1 row, the batch-of-one kernels), 4 steps from
-    position 0: every output bit the decoder's (whose o_proj and down_proj take 4-row strips up to
-    16 rows; 16-row strips give the same bits)."""
+@pytest.mark.parametrize("strip_rows", [4, 16])
+def test_a_step_composed_by_kernel_name_is_the_decoders_step_bit_for_bit(ctx, strip_rows):
+    """2 layers, 3 rows in slots 2, 0, 1, 4 steps from position 0: every output bit the decoder's
+    (whose o_proj and down_proj take 4-row strips at 3 rows; 16-row strips give the same bits)."""
     import tgx
     from tgx.synth import StackSpec, embeddings
 
     spec = StackSpec(layers=2, seed=3)
-    cap = 128
+    cap, rows = 128, 3
     print(f"[runtime api] 2 layers, {rows} rows, strips of {strip_rows}", flush=True)
     prog = StepProgram(ctx, spec, cap, rows, rows, strip_rows=strip_rows)
     dec = reference_decoder(ctx, spec, cap, rows)
     x = embeddings(7, "runtime-api", 4 * rows, spec.hidden).reshape(4, rows, spec.hidden)
-    slots = [2, 0, 1][:rows] if rows == 3 else [0]
+    slots = [2, 0, 1]
     for t in range(4):
         got = prog.step([(t, s) for s in slots], x[t])
         want = dec.step_rows([tgx.Row(t, s) for s in slots], x[t])
@@ -243,7 +232,6 @@ def test_a_recording_refuses_on_the_host_what_the_kernels_could_not_run(ctx):
     kv = rt.Memory(ctx, 2 * KV * 2 * 64 * 64 * 2)
     pos, row_table = rt.Memory(ctx, rows * 4), rt.Memory(ctx, rows * 4)
     att = rt.Memory(ctx, rows * H * 64 * 2)
-    own = rt.Memory(ctx, rows * KV * 2 * 64 * 2)
     p = rt.Program(ctx)
 
     def refused(kind, *args, **kw):
@@ -251,17 +239,16 @@ def test_a_recording_refuses_on_the_host_what_the_kernels_could_not_run(ctx):
             p.dispatch(*args, **kw)
         assert e.value.kind == kind, str(e.value)
 
-    refused("shape", "attention_decode", [q, kv, pos, row_table, own, (att, 0, rows * H * 64 * 2 - 16)], c)
-    refused("shape", "attention_decode", [q, kv, pos, row_table, own], c)
-    refused("shape", "attention_decode", [q, kv, pos, None, own, att], c)
-    refused("shape", "attention_decode", [q, kv, pos, row_table, own, att], c[:-1])
-    refused("shape", "attention_decode", [q, kv, pos, row_table, own, att], c, groups=(2, 1, 1))
-    refused("shape", "attention_decode", [q, (kv, 8, 0), pos, row_table, own, att], c)  # offset not 16-aligned
-    refused("shape", "attention_decode", [q, kv, pos, row_table, own, att], c[:5] + [4096 * 64] + c[6:])  # capacity
-    refused("shape", "attention_decode", [q, kv, pos, row_table, own, att], c[:7] + [0] + c[8:])  # a table too short
+    refused("shape", "attention_decode", [q, kv, pos, row_table, (att, 0, rows * H * 64 * 2 - 16)], c)
+    refused("shape", "attention_decode", [q, kv, pos, row_table], c)
+    refused("shape", "attention_decode", [q, kv, pos, None, att], c)
+    refused("shape", "attention_decode", [q, kv, pos, row_table, att], c[:-1])
+    refused("shape", "attention_decode", [q, kv, pos, row_table, att], c, groups=(2, 1, 1))
+    refused("shape", "attention_decode", [q, (kv, 8, 0), pos, row_table, att], c)  # offset not 16-aligned
+    refused("shape", "attention_decode", [q, kv, pos, row_table, att], c[:5] + [4096 * 64] + c[6:])  # capacity
+    refused("shape", "attention_decode", [q, kv, pos, row_table, att], c[:7] + [0] + c[8:])  # a table too short
     refused("shape", "stream_read", [(q, 0, 1000), att], [])
-    refused("shape", "gemv_residual_fold", [q, own, att, att, att, None, att, None, None], c + [1024, 1024, 4])  # 2 rows
-    p.dispatch("attention_decode", [q, kv, pos, row_table, own, att], c, groups=(KV, rows, 1))
+    p.dispatch("attention_decode", [q, kv, pos, row_table, att], c, groups=(KV, rows, 1))
     with pytest.raises(tgx.TgxError) as e:
         q.close()
     assert e.value.kind == "busy"
@@ -270,11 +257,11 @@ def test_a_recording_refuses_on_the_host_what_the_kernels_could_not_run(ctx):
     assert e.value.kind == "shape"
     p.end()
     with pytest.raises(tgx.TgxError) as e:
-        p.dispatch("attention_decode", [q, kv, pos, row_table, own, att], c)
+        p.dispatch("attention_decode", [q, kv, pos, row_table, att], c)
     assert e.value.kind == "busy"
     # Every row spare: the program runs and writes nothing.
     pos.write(np.full(rows, 0xFFFFFFFF, np.uint32))
     p.run()
     p.close()
-    for m in (q, kv, pos, row_table, own, att):
+    for m in (q, kv, pos, row_table, att):
         m.close()

@@ -249,15 +249,13 @@ __device__ __forceinline__ long block_of(const DecodeArgs& a, uint32_t slot, uin
 // the first), else as the f32 rows. The epilogue's thread (p, c) (pair p, tile row c; the first
 // 128 threads) loads its row's position and slot first of all, and the RoPE factors and cache
 // block that hang on them while the products' operands are on their way.
-// A key or value strip also leaves its row's new key or value in kv_cur, for whichever kernel
-// folds the row's own position into its attention. qkv_strip is the strip's whole work, shared by
-// gemv_qkv_rope and qkv_attention_one (which takes the k and v strips of a batch of one row so).
 template <int CH, bool PRENORMED>
-__device__ __forceinline__ void qkv_strip(const DecodeArgs& a, const LayerArgs& l, int strip_id, int tile) {
+__global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, LayerArgs l) {
     constexpr int R = QKV_ROWS;
     constexpr int EPI = (R / 2) * 16;  // epilogue threads
     __shared__ f32x4 red[GEMV_WAVES * 64];
     __shared__ float sq[GEMV_THREADS], scale[16];
+    const int strip_id = blockIdx.x, tile = blockIdx.y;
     const int strip[1] = {strip_id};
     const int p = threadIdx.x % (R / 2), c = (threadIdx.x / (R / 2)) % 16;
     const int b = tile * 16 + c;
@@ -324,11 +322,8 @@ __device__ __forceinline__ void qkv_strip(const DecodeArgs& a, const LayerArgs& 
         q[i + HEAD_DIM / 2] = (uint16_t)bf16_bits(vc);
         return;
     }
-    const int kv = head < H + KV ? head - H : head - H - KV;
-    uint16_t* own = l.kv_cur + (((size_t)b * KV + kv) * 2 + (head < H + KV ? 0 : 1)) * HEAD_DIM;
-    own[i] = (uint16_t)bf16_bits(va);
-    own[i + HEAD_DIM / 2] = (uint16_t)bf16_bits(vc);
     if (entry >= (uint32_t)a.nblocks) return;  // the slot holds no block there
+    const int kv = head < H + KV ? head - H : head - H - KV;
     uint16_t* tl = l.kv + ((size_t)entry * KV + kv) * 2 * KV_TILE;
     const int pp = (int)(pos % BLOCK_TOKENS);
     if (head < H + KV) {
@@ -338,11 +333,6 @@ __device__ __forceinline__ void qkv_strip(const DecodeArgs& a, const LayerArgs& 
         tl[KV_TILE + value_index(pp, i)] = (uint16_t)bf16_bits(va);
         tl[KV_TILE + value_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
     }
-}
-
-template <int CH, bool PRENORMED>
-__global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, LayerArgs l) {
-    qkv_strip<CH, PRENORMED>(a, l, blockIdx.x, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -442,144 +432,15 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
 }
 
 // ---------------------------------------------------------------------------------------------
-// The attention of a row at position pos over its slot's cache (attention_split.comp:52-111 +
-// attention_combine.comp:29-57): the positions before pos in the cache's 64-position blocks, wave
-// w taking blocks w, w + 8, ... (its turns) with an online softmax, two turns' keys and values in
-// flight at once, the waves joined in order; then the row's own position, its key and value as
-// the q/k/v strips left them in kv_cur, folded in last (own_fold). Per block, S^T = K Q^T (keys as
-// rows, the MFMA's 16 columns the query heads) and O^T += V^T P, P in bf16 straight from the
-// registers S^T left it in.
+// attention_decode: workgroup (kv, b) attends the `group` query heads KV head kv serves of row b
+// over its slot's positions 0..pos; wave w takes blocks w, w + 8, ... (its turns) with an online
+// softmax, two turns' keys and values in flight at once.
+// Per block, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in bf16 straight
+// from the registers S^T left it in.
+// Two memory round trips before the first product: the row's position, the cache blocks of the
+// wave's turns (lane j: block w + 8 j, from the row's copy of its slot's table) and q together,
+// then the first two turns' keys and values.
 
-// A wave's turns over the blocks holding positions 0..pos-1 of one row: the wave takes the blocks
-// of virtual wave vw (vw, vw + 8, ...; `turn_block` lane j: the row's block vw + 8 j) of KV head
-// kv (its cache pool kvl) with an online softmax. fetch0() issues turn 0's loads, run() the rest
-// and takes every turn, leaving each of the first `cols` columns' max and sum in sm_m[slot][c],
-// sm_l[slot][c] and its output in attn_lds[(slot cols + c) 65 + d]. A virtual wave's arithmetic is
-// the same whichever wave of whichever workgroup runs it.
-struct PastTurns {
-    const DecodeArgs& a;
-    const uint16_t* kvl;
-    int kv, vw, blocks;
-    uint32_t last, turn_block;
-    uint4 ka[8], va[8], kb[8], vb[8];
-
-    __device__ PastTurns(const DecodeArgs& a_, const uint16_t* kvl_, int kv_, uint32_t pos, int vw_, uint32_t turn_block_)
-        : a(a_), kvl(kvl_), kv(kv_), vw(vw_), turn_block(turn_block_) {
-        blocks = (int)((pos + BLOCK_TOKENS - 1) / BLOCK_TOKENS);  // 0 at position 0
-        last = pos - 1;                                              // the last position a key is taken from
-    }
-    // Turn j's block, and whether the wave has it (the slot may hold no block there).
-    __device__ uint32_t block_of_turn(int j) const { return (uint32_t)__builtin_amdgcn_readlane((int)turn_block, min(j, WAVE - 1)); }
-    __device__ bool has(int j) const { return vw + ATTN_WAVES * j < blocks && block_of_turn(j) < (uint32_t)a.nblocks; }
-    // Turn j's keys and values. Without the turn (`real` false) the same 1 KiB at the pool's start
-    // is read 16 times over instead, from the caches: the loads are made either way, so that the
-    // waits for them can be counted exactly (a load under a branch makes the compiler wait for
-    // every load before its first use).
-    __device__ void fetch(int j, bool real, uint4 (&k)[8], uint4 (&v)[8]) const {
-        const int lane = threadIdx.x % WAVE;
-        const uint16_t* kt = real ? kvl + ((size_t)block_of_turn(j) * a.kv_heads + kv) * 2 * KV_TILE : kvl;
-        const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) k[i] = load16(kt + i * stride + lane * 8);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + lane * 8);
-    }
-    __device__ void fetch0() { fetch(0, has(0), ka, va); }
-
-    __device__ void run(const uint4 (&qf)[2], int cols, int slot, float* attn_lds, float (*sm_m)[16], float (*sm_l)[16]) {
-        const int lane = threadIdx.x % WAVE, h = lane % 16;
-        OnlineSoftmax sm;
-        const float scale_log2 = log2_scale(a.scale);
-        // S^T = K Q^T for a turn's block, then its softmax step (masked only in the block holding
-        // the last position).
-        auto take = [&](const uint4 (&k)[8], const uint4 (&v)[8], int j) __attribute__((always_inline)) {
-            f32x4 s[4];
-#pragma unroll
-            for (int pt = 0; pt < 4; ++pt) {
-                s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(k[pt * 2 + ds], qf[ds], s[pt]);
-            }
-            const uint32_t p0 = (uint32_t)(vw + ATTN_WAVES * j) * BLOCK_TOKENS;
-            if (p0 + BLOCK_TOKENS - 1 <= last)
-                sm.block<false>(s, v, p0, last, last, scale_log2);
-            else
-                sm.block<true>(s, v, p0, last, last, scale_log2);
-        };
-        // Two buffers: the first two turns straight (every context up to 16 blocks), then the rest
-        // two at a time, each pair's loads issued once the last pair is taken.
-        const bool t0 = has(0), t1 = has(1);
-        fetch(1, t1, kb, vb);
-        if (t0) take(ka, va, 0);
-        if (t1) take(kb, vb, 1);
-        for (int j = 2; t1 && has(j); j += 2) {
-            const bool next = has(j + 1);
-            fetch(j, true, ka, va);
-            fetch(j + 1, next, kb, vb);
-            take(ka, va, j);
-            if (!next) break;
-            take(kb, vb, j + 1);
-        }
-        if (lane < 16) {
-            sm_m[slot][h] = sm.m;
-            sm_l[slot][h] = sm.l;
-        }
-        if (h < cols) {
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) attn_lds[(slot * cols + h) * (HEAD_DIM + 1) + dt * 16 + (lane / 16) * 4 + i] = sm.o[dt][i];
-        }
-    }
-};
-
-// Softmax states joined in order: the max M, the sum L and the output O (not yet divided); M =
-// -inf, L = O = 0 where there is nothing. The eight virtual waves of a row's attention are joined
-// as two halves of four, then the halves (join_pair), in every kernel that joins them.
-struct Joined {
-    float M, L, O;
-};
-// Column c's slots first .. first + count - 1 in dimension d.
-__device__ __forceinline__ Joined join_waves(const float* attn_lds, const float (*sm_m)[16], const float (*sm_l)[16], int cols,
-                                             int c, int d, int first, int count) {
-    Joined r{-INFINITY, 0.f, 0.f};
-    for (int j = first; j < first + count; ++j) r.M = fmaxf(r.M, sm_m[j][c]);
-    for (int j = first; j < first + count; ++j) {
-        const float f = sm_l[j][c] > 0.f ? __builtin_amdgcn_exp2f(sm_m[j][c] - r.M) : 0.f;
-        r.L = fmaf(sm_l[j][c], f, r.L);
-        r.O = fmaf(attn_lds[(j * cols + c) * (HEAD_DIM + 1) + d], f, r.O);
-    }
-    return r;
-}
-// Two states' joint max and sum, and the weights each one's output takes (pair_output).
-struct PairWeights {
-    float M, L, fx, fy;
-};
-__device__ __forceinline__ PairWeights pair_weights(float Mx, float Lx, float My, float Ly) {
-    PairWeights w;
-    w.M = fmaxf(Mx, My);
-    w.fx = Lx > 0.f ? __builtin_amdgcn_exp2f(Mx - w.M) : 0.f;
-    w.fy = Ly > 0.f ? __builtin_amdgcn_exp2f(My - w.M) : 0.f;
-    w.L = fmaf(Lx, w.fx, 0.f);
-    w.L = fmaf(Ly, w.fy, w.L);
-    return w;
-}
-__device__ __forceinline__ float pair_output(float Ox, float Oy, const PairWeights& w) { return fmaf(Oy, w.fy, fmaf(Ox, w.fx, 0.f)); }
-__device__ __forceinline__ Joined join_pair(const Joined& x, const Joined& y) {
-    const PairWeights w = pair_weights(x.M, x.L, y.M, y.L);
-    return Joined{w.M, w.L, pair_output(x.O, y.O, w)};
-}
-constexpr int HALF_WAVES = ATTN_WAVES / 2;
-__device__ __forceinline__ Joined join_eight(const float* attn_lds, const float (*sm_m)[16], const float (*sm_l)[16], int cols, int c,
-                                             int d) {
-    return join_pair(join_waves(attn_lds, sm_m, sm_l, cols, c, d, 0, HALF_WAVES),
-                     join_waves(attn_lds, sm_m, sm_l, cols, c, d, HALF_WAVES, HALF_WAVES));
-}
-
-// attention_decode: workgroup (kv, b) attends the `group` query heads KV head kv serves of row b,
-// wave w running virtual wave w. Two memory round trips before the first product: the row's
-// position, the cache blocks of the wave's turns (from the row's copy of its slot's table), q and
-// the row's own key together, then the first two turns' keys and values.
 __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
     extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
     __shared__ float sm_m[ATTN_WAVES][16];
@@ -592,220 +453,85 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     const uint32_t turn_block =
         a.row_table[(uint32_t)b * (uint32_t)a.max_blocks + (uint32_t)min(w + ATTN_WAVES * lane, a.max_blocks - 1)];
     // Columns past the group read its last head again; nothing reads what they give.
-    uint4 qf[2], kf[2];
-    const uint16_t* own = l.kv_cur + ((size_t)b * KV + kv) * 2 * HEAD_DIM;
+    uint4 qf[2];
 #pragma unroll
-    for (int ds = 0; ds < 2; ++ds) {
-        qf[ds] = load16(l.q + ((size_t)b * H + kv * group + min(h, group - 1)) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
-        kf[ds] = load16(own + ds * 32 + (lane / 16) * 8);
-    }
-    // The row's own value in the one dimension this thread writes (ATTN_THREADS a multiple of 64).
-    const float own_v = bf16_value(own[HEAD_DIM + threadIdx.x % HEAD_DIM]);
+    for (int ds = 0; ds < 2; ++ds) qf[ds] = load16(l.q + ((size_t)b * H + kv * group + min(h, group - 1)) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
     all_issued();
     if (pos >= (uint32_t)a.capacity) return;  // a spare row
-    PastTurns turns(a, l.kv, kv, pos, w, turn_block);
-    turns.fetch0();
-    turns.run(qf, group, w, attn_lds, sm_m, sm_l);
-    const float own_s = own_scores(kf, qf);  // lane c: column c's
+    const int blocks = (int)(pos / BLOCK_TOKENS) + 1;
+
+    // Turn j's block, and whether the wave has it (the slot may hold no block there).
+    auto block_of_turn = [&](int j) { return (uint32_t)__builtin_amdgcn_readlane((int)turn_block, min(j, WAVE - 1)); };
+    auto has = [&](int j) { return w + ATTN_WAVES * j < blocks && block_of_turn(j) < (uint32_t)a.nblocks; };
+    // Turn j's keys and values. Without the turn (`real` false) the same 1 KiB at the pool's start
+    // is read 16 times over instead, from the caches: the loads are made either way, so that the
+    // waits for them can be counted exactly (a load under a branch makes the compiler wait for
+    // every load before its first use).
+    auto fetch = [&](int j, bool real, uint4 (&k)[8], uint4 (&v)[8]) {
+        const uint16_t* kt = real ? l.kv + ((size_t)block_of_turn(j) * KV + kv) * 2 * KV_TILE : l.kv;
+        const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) k[i] = load16(kt + i * stride + lane * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + lane * 8);
+    };
+    OnlineSoftmax sm;
+    const float scale_log2 = log2_scale(a.scale);
+    // S^T = K Q^T for a turn's block, then its softmax step (masked only in the block holding
+    // the position).
+    auto take = [&](const uint4 (&k)[8], const uint4 (&v)[8], int j) __attribute__((always_inline)) {
+        f32x4 s[4];
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+            s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(k[pt * 2 + ds], qf[ds], s[pt]);
+        }
+        const uint32_t p0 = (uint32_t)(w + ATTN_WAVES * j) * BLOCK_TOKENS;
+        if (p0 + BLOCK_TOKENS - 1 <= pos)
+            sm.block<false>(s, v, p0, pos, pos, scale_log2);
+        else
+            sm.block<true>(s, v, p0, pos, pos, scale_log2);
+    };
+    // Two buffers: the first two turns straight (every context up to 16 blocks), then the rest
+    // two at a time, each pair's loads issued once the last pair is taken.
+    uint4 ka[8], va[8], kb[8], vb[8];
+    const bool t0 = has(0), t1 = has(1);
+    fetch(0, t0, ka, va);
+    fetch(1, t1, kb, vb);
+    if (t0) take(ka, va, 0);
+    if (t1) take(kb, vb, 1);
+    for (int j = 2; t1 && has(j); j += 2) {
+        const bool next = has(j + 1);
+        fetch(j, true, ka, va);
+        fetch(j + 1, next, kb, vb);
+        take(ka, va, j);
+        if (!next) break;
+        take(kb, vb, j + 1);
+    }
+    if (lane < 16) {
+        sm_m[w][h] = sm.m;
+        sm_l[w][h] = sm.l;
+    }
+    if (h < group) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) attn_lds[(w * group + h) * (HEAD_DIM + 1) + dt * 16 + (lane / 16) * 4 + i] = sm.o[dt][i];
+    }
     __syncthreads();
+    // The waves joined in order (wave 0 holds block 0, so M is finite).
     for (int idx = threadIdx.x; idx < group * HEAD_DIM; idx += ATTN_THREADS) {
         const int hh = idx / HEAD_DIM, d = idx % HEAD_DIM;
-        const Joined j = join_eight(attn_lds, sm_m, sm_l, group, hh, d);
-        const OwnFold f = own_fold(j.M, j.L, __shfl(own_s, hh, WAVE), log2_scale(a.scale));
-        l.attended[operand_index(b, (kv * group + hh) * HEAD_DIM + d, a.rows)] = (uint16_t)bf16_bits(own_output(j.O, own_v, f));
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
-// qkv_attention_one: q/k/v and the attention of a batch of one row in one kernel. Workgroup
-// 2 h + half (h < heads) takes query head h: its four strips of q (the products, the row's scale
-// and RoPE as gemv_qkv_rope's, bit for bit; both halves make them), then, on its first four waves,
-// virtual waves 4 half .. 4 half + 3 of the head's attention over the positions before the row's
-// (their first turns' keys and values issued beside the weights), joined as attention_decode
-// joins a half, into `state` [heads][2][66] (the output over each dimension, then M, L) for
-// gemv_residual_fold to join the halves and fold the row's own position in. Workgroup
-// 2 heads + j takes strip j of k and v, as gemv_qkv_rope does. No workgroup waits for another.
-template <int CH, bool PRENORMED>
-__global__ void __launch_bounds__(GEMV_THREADS) qkv_attention_one(DecodeArgs a, LayerArgs l) {
-    constexpr int S = HEAD_DIM / QKV_ROWS;  // strips to a head
-    const int H = a.heads, KV = a.kv_heads, group = H / KV;
-    if ((int)blockIdx.x >= 2 * H) {
-        qkv_strip<CH, PRENORMED>(a, l, S * H + ((int)blockIdx.x - 2 * H), 0);
-        return;
-    }
-    __shared__ f32x4 red[GEMV_WAVES * S * 64];
-    __shared__ float sq[GEMV_THREADS], scale[16];
-    __shared__ __align__(16) uint16_t qh[HEAD_DIM];
-    __shared__ float sm_m[HALF_WAVES][16];
-    __shared__ float sm_l[HALF_WAVES][16];
-    __shared__ float attn_lds[HALF_WAVES * (HEAD_DIM + 1)];
-    const int head = blockIdx.x / 2, half = blockIdx.x % 2, kv = head / group;
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const bool attends = w < HALF_WAVES;  // whole waves
-    const int vw = half * HALF_WAVES + min(w, HALF_WAVES - 1);
-    // The epilogue's thread (s4, p) (the first 32): pair p of strip s4, the head's dimensions
-    // i = 8 s4 + p and i + 32.
-    const int s4 = (threadIdx.x / (QKV_ROWS / 2)) % S, p = threadIdx.x % (QKV_ROWS / 2);
-    const int i = s4 * (QKV_ROWS / 2) + p;
-    const uint32_t pos = a.positions[0], slot = a.slots[0];
-    const uint32_t turn_block = a.row_table[(uint32_t)min(vw + ATTN_WAVES * lane, a.max_blocks - 1)];
-    const int strip[S] = {S * head, S * head + 1, S * head + 2, S * head + 3};
-    RowSquares<CH> squares;
-    RawRows<CH> xb;
-    NormedRows<CH> xn;
-    if constexpr (PRENORMED) {
-        squares.load(l.x_sq, 1, 0);
-        xb.load(l.xn, 1, 0);
-    } else {
-        xn.load(l.x, l.input_norm, 1, 0);
-    }
-    Gemv<S, CH> g;
-    g.load(l.qkv, strip);
-    // Every weight load goes out before anything waits for the position or the table.
-    __builtin_amdgcn_sched_barrier(0);
-    const uint32_t pc = min(pos, (uint32_t)a.capacity - 1);
-    const float co = a.cos[pc * (HEAD_DIM / 2) + (uint32_t)i], si = a.sin[pc * (HEAD_DIM / 2) + (uint32_t)i];
-    // The first turn's keys and values on their way beside the weights (the other waves read the
-    // pool's first KiB instead, from the caches).
-    PastTurns turns(a, l.kv, kv, pos < (uint32_t)a.capacity && attends ? pos : 0u, vw, turn_block);
-    turns.fetch0();
-    if (PRENORMED || CH <= 2) all_issued();
-    if constexpr (PRENORMED) {
-        squares.finish(a.eps, scale);
-        g.run(xb.xf);
-        spill<S>(g.acc, red);
-    } else {
-        xn.finish();
-        g.run(xn.xf);
-        spill<S>(g.acc, red, sq, xn.squares);
-        row_scales(sq, a.hidden, a.eps, scale);
-    }
-    if (pos >= (uint32_t)a.capacity || slot >= (uint32_t)a.nslots) return;  // a spare row: nothing to write
-    if (threadIdx.x < S * (QKV_ROWS / 2)) {
-        float va = reduced<S>(red, s4, p, 0) * scale[0];
-        float vc = reduced<S>(red, s4, p + QKV_ROWS / 2, 0) * scale[0];
-        if (a.rope) {
-            const float ra = va * co - vc * si;
-            const float rc = vc * co + va * si;
-            va = ra;
-            vc = rc;
+        float M = -INFINITY;
+        for (int j = 0; j < ATTN_WAVES; ++j) M = fmaxf(M, sm_m[j][hh]);
+        float L = 0.f, O = 0.f;
+        for (int j = 0; j < ATTN_WAVES; ++j) {
+            const float f = sm_l[j][hh] > 0.f ? __builtin_amdgcn_exp2f(sm_m[j][hh] - M) : 0.f;
+            L += sm_l[j][hh] * f;
+            O += attn_lds[(j * group + hh) * (HEAD_DIM + 1) + d] * f;
         }
-        const uint16_t qa = (uint16_t)bf16_bits(va), qc = (uint16_t)bf16_bits(vc);
-        qh[i] = qa;
-        qh[i + HEAD_DIM / 2] = qc;
-        if (half == 0) {
-            l.q[(size_t)head * HEAD_DIM + i] = qa;
-            l.q[(size_t)head * HEAD_DIM + i + HEAD_DIM / 2] = qc;
-        }
-    }
-    __syncthreads();
-    if (attends) {
-        // Every column the head: each gives the bits attention_decode's column for it gives.
-        uint4 qf[2];
-#pragma unroll
-        for (int ds = 0; ds < 2; ++ds) qf[ds] = *reinterpret_cast<const uint4*>(&qh[ds * 32 + (lane / 16) * 8]);
-        turns.run(qf, 1, w, attn_lds, sm_m, sm_l);
-    }
-    __syncthreads();
-    if ((int)threadIdx.x < HEAD_DIM) {
-        const Joined j = join_waves(attn_lds, sm_m, sm_l, 1, 0, threadIdx.x, 0, HALF_WAVES);
-        float* st = l.state + ((size_t)head * 2 + half) * (HEAD_DIM + 2);
-        st[threadIdx.x] = j.O;
-        if (threadIdx.x == 0) {
-            st[HEAD_DIM] = j.M;
-            st[HEAD_DIM + 1] = j.L;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
-// gemv_residual_fold: o_proj for a batch of one row after qkv_attention_one. Its operand, the
-// attention's output, is made first in LDS from the heads' state over the positions before the
-// row's, with the row's own key and value folded in (own_scores, own_fold and own_output:
-// attention_decode's bits), then out = residual + W x as gemv_residual. Wave w < kv_heads takes
-// the own scores of KV head w's query heads.
-template <int CH, int R>
-__global__ void __launch_bounds__(GEMV_THREADS) gemv_residual_fold(DecodeArgs a, ResidualArgs r, LayerArgs l) {
-    constexpr int K = CH * CHUNK_COLS;
-    constexpr int EPI = 16 * (R / SQ_COLS);
-    constexpr int LOADERS = EPI < WAVE ? WAVE : EPI;
-    static_assert(LOADERS % WAVE == 0, "whole waves");
-    __shared__ f32x4 red[GEMV_WAVES * 64];
-    __shared__ __align__(16) uint16_t att[K];
-    __shared__ OwnFold fold[K / HEAD_DIM];
-    __shared__ PairWeights halves[K / HEAD_DIM];
-    const int strip_id = blockIdx.x;
-    const int strip[1] = {strip_id};
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int c = threadIdx.x % 16, q = (threadIdx.x / 16) % (R / SQ_COLS);
-    const int n0 = strip_id * R + q * SQ_COLS;
-    const int H = a.heads, KV = a.kv_heads, group = H / KV;
-    float4 res = make_float4(0.f, 0.f, 0.f, 0.f), gain = res;
-    if (threadIdx.x < LOADERS) {
-        res = load_f4(r.residual + n0);
-        gain = load_f4((r.next_norm ? r.next_norm : r.residual) + n0);
-    }
-    Gemv<1, CH, R> g;
-    g.load(r.w, strip);
-    // Thread t's dimensions 2 (t + 512 j) and the next (one head's): the halves' outputs over the
-    // positions before the row's, and the row's own values there.
-    constexpr int ST = HEAD_DIM + 2;  // a half's state: the output over each dimension, M, L
-    float2 o0[CH], o1[CH];
-    uint32_t vv[CH];
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-        const int k = 2 * ((int)threadIdx.x + j * GEMV_THREADS), hd = k / HEAD_DIM, d = k % HEAD_DIM;
-        const float* st = l.state + (size_t)hd * 2 * ST;
-        o0[j] = *reinterpret_cast<const float2*>(st + d);
-        o1[j] = *reinterpret_cast<const float2*>(st + ST + d);
-        vv[j] = *reinterpret_cast<const uint32_t*>(l.kv_cur + ((size_t)(hd / group) * 2 + 1) * HEAD_DIM + d);
-    }
-    // Wave w (< kv_heads): its query heads' q and the row's own key, and lane c's head's halves'
-    // M and L.
-    const int wk = min(w, KV - 1), hc = wk * group + min(c, group - 1);
-    uint4 qf[2], kf[2];
-#pragma unroll
-    for (int ds = 0; ds < 2; ++ds) {
-        qf[ds] = load16(l.q + (size_t)hc * HEAD_DIM + ds * 32 + (lane / 16) * 8);
-        kf[ds] = load16(l.kv_cur + (size_t)wk * 2 * HEAD_DIM + ds * 32 + (lane / 16) * 8);
-    }
-    const float* sc = l.state + (size_t)hc * 2 * ST;
-    const float M0 = sc[HEAD_DIM], L0 = sc[HEAD_DIM + 1], M1 = sc[ST + HEAD_DIM], L1 = sc[ST + HEAD_DIM + 1];
-    all_issued();
-    const float own_s = own_scores(kf, qf);
-    if (w < KV && lane < group) {
-        const PairWeights pw = pair_weights(M0, L0, M1, L1);
-        fold[w * group + lane] = own_fold(pw.M, pw.L, own_s, log2_scale(a.scale));
-        halves[w * group + lane] = pw;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-        const int k = 2 * ((int)threadIdx.x + j * GEMV_THREADS), hd = k / HEAD_DIM;
-        const PairWeights pw = halves[hd];
-        const OwnFold f = fold[hd];
-        const float lo = own_output(pair_output(o0[j].x, o1[j].x, pw), __uint_as_float(vv[j] << 16), f);
-        const float hi = own_output(pair_output(o0[j].y, o1[j].y, pw), __uint_as_float(vv[j] & 0xffff0000u), f);
-        *reinterpret_cast<uint32_t*>(&att[k]) = pack_bf16x2(lo, hi);
-    }
-    __syncthreads();
-    RawRows<CH> x;
-#pragma unroll
-    for (int i = 0; i < Operand<CH>::KB; ++i) x.xf[i] = *reinterpret_cast<const uint4*>(&att[Operand<CH>::column(i)]);
-    g.run(x.xf);
-    spill<1>(g.acc, red);
-    if (threadIdx.x >= EPI || c >= a.rows) return;
-    const float4 v = make_float4(res.x + reduced<1>(red, 0, q * 4, c), res.y + reduced<1>(red, 0, q * 4 + 1, c),
-                                 res.z + reduced<1>(red, 0, q * 4 + 2, c), res.w + reduced<1>(red, 0, q * 4 + 3, c));
-    *reinterpret_cast<float4*>(r.out + n0) = v;
-    if (r.next_norm) {
-        *reinterpret_cast<uint2*>(r.out_n + operand_index(0, n0, 1)) =
-            make_uint2(pack_bf16x2(v.x * gain.x, v.y * gain.y), pack_bf16x2(v.z * gain.z, v.w * gain.w));
-        float s2 = v.x * v.x;
-        s2 += v.y * v.y;
-        s2 += v.z * v.z;
-        s2 += v.w * v.w;
-        r.out_sq[n0 / SQ_COLS] = s2;
+        l.attended[operand_index(b, (kv * group + hh) * HEAD_DIM + d, a.rows)] = (uint16_t)bf16_bits(O / L);
     }
 }
 
@@ -867,10 +593,6 @@ template <int CH> struct PickGateUp { static auto get() { return gemv_gate_up<CH
 template <int CH> struct PickResidual4 { static auto get() { return gemv_residual<CH, 4>; } };
 template <int CH> struct PickResidual16 { static auto get() { return gemv_residual<CH, 16>; } };
 template <int CH> struct PickFinal { static auto get() { return final_rmsnorm<CH>; } };
-template <int CH> struct PickQkvAttention { static auto get() { return qkv_attention_one<CH, false>; } };
-template <int CH> struct PickQkvAttentionNormed { static auto get() { return qkv_attention_one<CH, true>; } };
-template <int CH> struct PickResidualFold4 { static auto get() { return gemv_residual_fold<CH, 4>; } };
-template <int CH> struct PickResidualFold16 { static auto get() { return gemv_residual_fold<CH, 16>; } };
 
 // The kernel of `launch` with its arguments `params`, timed by the timer's next events when given.
 hipError_t dispatch_launch(const char* label, const KernelLaunch& k, void** params, hipStream_t stream, DispatchTimer* timer) {
@@ -916,29 +638,6 @@ KernelLaunch residual_launch(const DecodeArgs& a, const ResidualArgs& r) {
     return k;
 }
 
-KernelLaunch qkv_attention_launch(const DecodeArgs& a, bool prenormed) {
-    const int chunks = a.hidden / CHUNK_COLS;
-    KernelLaunch k;
-    k.func = prenormed ? (const void*)by_chunks<PickQkvAttentionNormed>(chunks) : (const void*)by_chunks<PickQkvAttention>(chunks);
-    k.grid = dim3(2 * a.heads + 2 * a.kv_heads * (HEAD_DIM / QKV_ROWS));
-    k.block = dim3(GEMV_THREADS);
-    return k;
-}
-
-KernelLaunch residual_fold_launch(const DecodeArgs& a, const ResidualArgs& r) {
-    const int chunks = r.K / CHUNK_COLS;
-    KernelLaunch k;
-    if (r.R == 4)
-        k.func = (const void*)by_chunks<PickResidualFold4>(chunks);
-    else if (r.R == 16)
-        k.func = (const void*)by_chunks<PickResidualFold16>(chunks);
-    else
-        return k;
-    k.grid = dim3(r.N / r.R);
-    k.block = dim3(GEMV_THREADS);
-    return k;
-}
-
 KernelLaunch gate_up_launch(const DecodeArgs& a) {
     const int tiles = decode_tiles(a.rows);
     const int hidden_chunks = a.hidden / CHUNK_COLS;
@@ -968,27 +667,17 @@ hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const Re
     LayerArgs ll = l;
     ResidualArgs oo = o, dd = down;
     void* layer_params[] = {&aa, &ll};
-    void* o_params[] = {&aa, &oo};
-    void* o_fold_params[] = {&aa, &oo, &ll};
-    void* down_params[] = {&aa, &dd};
-    const bool one = a.rows == 1;
-    const KernelLaunch ko = one ? residual_fold_launch(a, o) : residual_launch(a, o), kd = residual_launch(a, down);
+    hipError_t e = dispatch_launch("gemv_qkv_rope", qkv_launch(a, l.xn != nullptr), layer_params, stream, timer);
+    if (e == hipSuccess) e = dispatch_launch("attention_decode", attention_launch(a), layer_params, stream, timer);
+    const KernelLaunch ko = residual_launch(a, o), kd = residual_launch(a, down);
     if (!ko.func || !kd.func) return hipErrorInvalidValue;
-    hipError_t e;
-    if (one) {
-        e = dispatch_launch("qkv_attention", qkv_attention_launch(a, l.xn != nullptr), layer_params, stream, timer);
-        if (e == hipSuccess) e = dispatch_launch("o_proj", ko, o_fold_params, stream, timer);
-    } else {
-        e = dispatch_launch("gemv_qkv_rope", qkv_launch(a, l.xn != nullptr), layer_params, stream, timer);
-        if (e == hipSuccess) e = dispatch_launch("attention_decode", attention_launch(a), layer_params, stream, timer);
-        if (e == hipSuccess) e = dispatch_launch("o_proj", ko, o_params, stream, timer);
-    }
+    void* o_params[] = {&aa, &oo};
+    if (e == hipSuccess) e = dispatch_launch("o_proj", ko, o_params, stream, timer);
     if (e == hipSuccess) e = dispatch_launch("gemv_gate_up", gate_up_launch(a), layer_params, stream, timer);
+    void* down_params[] = {&aa, &dd};
     if (e == hipSuccess) e = dispatch_launch("down_proj", kd, down_params, stream, timer);
     return e != hipSuccess ? e : hipGetLastError();
 }
-
-int decode_layer_dispatches(int rows) { return rows == 1 ? 4 : 5; }
 
 // ---------------------------------------------------------------------------------------------
 // stream_read: the bandwidth the decode kernels are held to (kernels/glsl/stream_read.comp:1-23):

@@ -45,12 +45,6 @@ struct LayerArgs {
     const float* mid_sq;      // [rows][hidden / 4]
     const uint16_t* gate_up;  // tiled bf16 [2 inner][hidden]
     uint16_t* mlp;            // [rows][inner] bf16
-    // Each row's new key and value, [rows][kv_heads][2][64] bf16, which the attention folds in
-    // last; and, for a batch of one row, each head's softmax over the positions before the row's
-    // in two halves ([heads][2][66]: the output over each dimension, then the max and the sum),
-    // which o_proj joins and finishes (qkv_attention_one, gemv_residual_fold).
-    uint16_t* kv_cur;
-    float* state;
 };
 
 // out = residual + W x, W in R-row tiles of [N][K]; with next_norm set, also out next_norm in
@@ -104,17 +98,10 @@ struct KernelLaunch {
 KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed);
 KernelLaunch attention_launch(const DecodeArgs& a);
 KernelLaunch residual_launch(const DecodeArgs& a, const ResidualArgs& r);  // func null unless r.R is 4 or 16
-// A batch of one row: q/k/v and the attention over the positions before the row's in one kernel
-// (DecodeArgs, LayerArgs), then o_proj with the row's own position folded in (DecodeArgs,
-// ResidualArgs, LayerArgs). The same bits as the three kernels above.
-KernelLaunch qkv_attention_launch(const DecodeArgs& a, bool prenormed);
-KernelLaunch residual_fold_launch(const DecodeArgs& a, const ResidualArgs& r);
 KernelLaunch gate_up_launch(const DecodeArgs& a);
 KernelLaunch final_norm_launch(const DecodeArgs& a);
 KernelLaunch stream_read_launch(size_t bytes);
 
-// The dispatches of a layer at `rows` rows: four for a batch of one row, five past it.
-int decode_layer_dispatches(int rows);
 hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const ResidualArgs& o, const ResidualArgs& down,
                                hipStream_t stream, DispatchTimer* timer = nullptr);
 hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out, uint32_t* positions,

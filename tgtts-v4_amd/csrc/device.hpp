@@ -237,43 +237,10 @@ struct OnlineSoftmax {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) o[dt] = mfma16(vf[dt * 2 + ks], pf[ks], o[dt]);
         }
-        // Fused by hand, so that every kernel this is inlined into rounds it alike.
-        l = fmaf(l, rescale, sum[0]);
+        l = l * rescale + sum[0];
         m = m_new;
     }
 };
-
-// A row's own position, folded into a head's softmax over the positions before it (max M in log2
-// units, sum L and unnormalised output O over 0..pos-1; M = -inf, L = O = 0 when there are none):
-// its score s comes from the MFMA chain a block's scores come from (own_scores), P is rounded to
-// bf16 as a block's is. Every kernel that finishes a row's attention takes these, with every
-// multiply-add fused by hand, so that they round alike wherever they run.
-__device__ __forceinline__ float bf16_value(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-
-// The row's own key (kf: every A-operand row that key, dimensions as a key tile's) against the
-// 16 columns' q (qf, as the blocks take it): column c's score in lane c (c < 16), element 0.
-__device__ __forceinline__ float own_scores(const uint4 (&kf)[2], const uint4 (&qf)[2]) {
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ds = 0; ds < 2; ++ds) s = mfma16(kf[ds], qf[ds], s);
-    return s[0];
-}
-
-struct OwnFold {
-    float rescale, p, l;
-};
-
-__device__ __forceinline__ OwnFold own_fold(float M, float L, float s, float scale_log2) {
-    const float m_new = fmaxf(M, s * scale_log2);
-    OwnFold f;
-    f.rescale = __builtin_amdgcn_exp2f(M - m_new);  // 0 when M = -inf
-    f.p = bf16_value((uint16_t)bf16_bits(__builtin_amdgcn_exp2f(fmaf(s, scale_log2, -m_new))));
-    f.l = fmaf(L, f.rescale, f.p);
-    return f;
-}
-
-// The head's output in dimension d from O there and the row's own value v there.
-__device__ __forceinline__ float own_output(float O, float v, const OwnFold& f) { return fmaf(f.p, v, O * f.rescale) / f.l; }
 
 // scale log2(e): scores times this are in the units v_exp_f32 (2^x) takes.
 __host__ __device__ constexpr float log2_scale(float scale) { return scale * 1.4426950408889634f; }

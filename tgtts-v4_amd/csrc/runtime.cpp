@@ -240,8 +240,6 @@ LayerArgs Decoder::layer_args(int l) const {
     la.mid_sq = sq_b;
     la.gate_up = layers[l].gate_up;
     la.mlp = mlp;
-    la.kv_cur = kv_cur;
-    la.state = attn_state;
     return la;
 }
 
@@ -309,7 +307,7 @@ hipError_t enqueue_step(Decoder* d, int advance, DispatchTimer* timer, int* disp
     for (int l = 0; l < d->shape.layers && err == hipSuccess; ++l) {
         // layer 0 reads x_in, which stays as written
         err = launch_decode_layer(a, d->layer_args(l), d->o_args(l), d->down_args(l), s, timer);
-        n += decode_layer_dispatches(d->rows);
+        n += 5;
     }
     const float* x = d->shape.layers > 0 ? d->h_a : d->x_in;
     if (err == hipSuccess) {
@@ -397,8 +395,6 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_TRY(alloc(d, &d->q, (size_t)R * H * HEAD_DIM));
     TGX_TRY(alloc(d, &d->attended, (size_t)R * H * HEAD_DIM));
     TGX_TRY(alloc(d, &d->mlp, (size_t)R * I));
-    TGX_TRY(alloc(d, &d->kv_cur, (size_t)R * KV * 2 * HEAD_DIM));
-    TGX_TRY(alloc(d, &d->attn_state, (size_t)H * 2 * (HEAD_DIM + 2)));
     TGX_TRY(alloc(d, &d->kv, (size_t)s.layers * d->nblocks * KV * 2 * KV_TILE));
     TGX_TRY(alloc(d, &d->positions, (size_t)R));
     TGX_TRY(alloc(d, &d->slot_of_row, (size_t)R));

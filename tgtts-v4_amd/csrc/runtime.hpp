@@ -86,9 +86,6 @@ struct Decoder {
     float *sq_a = nullptr, *sq_b = nullptr;
     int od_rows = 4;  // strip height of o_proj and down_proj (decode_residual_rows)
     uint16_t *q = nullptr, *attended = nullptr, *mlp = nullptr, *kv = nullptr;
-    uint16_t* kv_cur = nullptr;    // [rows][kv_heads][2][64]: each row's new key and value
-    float* attn_state = nullptr;   // [heads][2][66]: a batch of one row's attention before o_proj folds it
-
     uint32_t *positions = nullptr, *slot_of_row = nullptr, *table = nullptr;
     uint32_t* row_table = nullptr;  // [rows][max_blocks]: each row's slot's table row
     float *cos = nullptr, *sin = nullptr;

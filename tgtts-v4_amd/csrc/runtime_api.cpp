@@ -140,8 +140,6 @@ tgx_status holds(const Bound* b, int i, const char* what, uint64_t need) {
 
 uint64_t pool_bytes(const DecodeArgs& a) { return (uint64_t)a.nblocks * a.kv_heads * 2 * KV_TILE * 2; }
 uint64_t qkv_rows(const DecodeArgs& a) { return (uint64_t)(a.heads + 2 * a.kv_heads) * HEAD_DIM; }
-uint64_t kv_cur_bytes(const DecodeArgs& a) { return (uint64_t)a.rows * a.kv_heads * 2 * HEAD_DIM * 2; }
-uint64_t state_bytes(const DecodeArgs& a) { return (uint64_t)a.heads * 2 * (HEAD_DIM + 2) * 4; }
 
 // gemv_qkv_rope (gemv_qkv_rope.comp): x | (xn, x_sq), gain, W, cos, sin, positions, slots, table
 // -> q, cache pool.
@@ -167,7 +165,6 @@ tgx_status build_qkv(const Bound* b, const uint32_t* c, Launch* L) {
     TGX_TRY(holds(b, 9, "table", (uint64_t)a.nslots * a.max_blocks * 4));
     TGX_TRY(holds(b, 10, "q", R * a.heads * HEAD_DIM * 2));
     TGX_TRY(holds(b, 11, "kv", pool_bytes(a)));
-    TGX_TRY(holds(b, 12, "kv_cur", kv_cur_bytes(a)));
     a.positions = (const uint32_t*)b[7].ptr;
     a.slots = (const uint32_t*)b[8].ptr;
     a.table = (const uint32_t*)b[9].ptr;
@@ -181,7 +178,6 @@ tgx_status build_qkv(const Bound* b, const uint32_t* c, Launch* L) {
     l.qkv = (const uint16_t*)b[4].ptr;
     l.q = (uint16_t*)b[10].ptr;
     l.kv = (uint16_t*)b[11].ptr;
-    l.kv_cur = (uint16_t*)b[12].ptr;
     L->a = a;
     L->l = l;
     L->k = qkv_launch(a, prenormed);
@@ -200,15 +196,13 @@ tgx_status build_attention(const Bound* b, const uint32_t* c, Launch* L) {
     TGX_TRY(holds(b, 1, "kv", pool_bytes(a)));
     TGX_TRY(holds(b, 2, "positions", R * 4));
     TGX_TRY(holds(b, 3, "row_table", R * a.max_blocks * 4));
-    TGX_TRY(holds(b, 4, "kv_cur", kv_cur_bytes(a)));
-    TGX_TRY(holds(b, 5, "attended", R * a.heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 4, "attended", R * a.heads * HEAD_DIM * 2));
     a.positions = (const uint32_t*)b[2].ptr;
     a.row_table = (const uint32_t*)b[3].ptr;
     LayerArgs l{};
     l.q = (uint16_t*)b[0].ptr;
     l.kv = (uint16_t*)b[1].ptr;
-    l.kv_cur = (uint16_t*)b[4].ptr;
-    l.attended = (uint16_t*)b[5].ptr;
+    l.attended = (uint16_t*)b[4].ptr;
     L->a = a;
     L->l = l;
     L->k = attention_launch(a);
@@ -256,68 +250,6 @@ tgx_status build_residual(const Bound* b, const uint32_t* c, Launch* L) {
     L->k = residual_launch(a, r);
     L->params[0] = &L->a;
     L->params[1] = &L->r;
-    return TGX_OK;
-}
-
-// qkv_attention (a batch of one row: gemv_qkv_rope's bindings and the row's table row) -> q,
-// cache pool, kv_cur, state.
-tgx_status build_qkv_attention(const Bound* b, const uint32_t* c, Launch* L) {
-    if (c[C_ROWS] != 1) return fail(TGX_E_SHAPE, "qkv_attention takes a batch of one row, not " + std::to_string(c[C_ROWS]));
-    TGX_TRY(build_qkv(b, c, L));
-    const DecodeArgs& a = L->a;
-    TGX_TRY(holds(b, 13, "row_table", (uint64_t)a.max_blocks * 4));
-    TGX_TRY(holds(b, 14, "state", state_bytes(a)));
-    L->a.row_table = (const uint32_t*)b[13].ptr;
-    L->l.state = (float*)b[14].ptr;
-    L->k = qkv_attention_launch(L->a, L->l.xn != nullptr);
-    return TGX_OK;
-}
-
-// gemv_residual_fold (o_proj of a batch of one row after qkv_attention): q, kv_cur, state, W,
-// residual [, next_gain] -> out [, out_n, out_sq]; constants K (heads x 64), N, strip_rows.
-tgx_status build_residual_fold(const Bound* b, const uint32_t* c, Launch* L) {
-    if (c[C_ROWS] != 1) return fail(TGX_E_SHAPE, "gemv_residual_fold takes a batch of one row, not " + std::to_string(c[C_ROWS]));
-    DecodeArgs a;
-    TGX_TRY(decode_args(c, &a));
-    const int K = (int)c[C_COMMON], N = (int)c[C_COMMON + 1], Rs = (int)c[C_COMMON + 2];
-    if (K != a.heads * HEAD_DIM || N <= 0 || N % 16 != 0 || N > (1 << 16) || (Rs != 4 && Rs != 16))
-        return fail(TGX_E_SHAPE, "gemv_residual_fold: K " + std::to_string(K) + " (the heads' " + std::to_string(a.heads * HEAD_DIM) +
-                                     "), N " + std::to_string(N) + " (a multiple of 16), strips of " + std::to_string(Rs) + " rows (4 or 16)");
-    const bool norm = b[5].ptr != nullptr;
-    if (norm != (b[7].ptr != nullptr) || norm != (b[8].ptr != nullptr))
-        return fail(TGX_E_SHAPE, "gemv_residual_fold takes next_gain, out_n and out_sq together or none of them");
-    TGX_TRY(holds(b, 0, "q", (uint64_t)a.heads * HEAD_DIM * 2));
-    TGX_TRY(holds(b, 1, "kv_cur", kv_cur_bytes(a)));
-    TGX_TRY(holds(b, 2, "state", state_bytes(a)));
-    TGX_TRY(holds(b, 3, "w", (uint64_t)N * K * 2));
-    TGX_TRY(holds(b, 4, "residual", (uint64_t)N * 4));
-    TGX_TRY(holds(b, 6, "out", (uint64_t)N * 4));
-    if (norm) {
-        TGX_TRY(holds(b, 5, "next_gain", (uint64_t)N * 4));
-        TGX_TRY(holds(b, 7, "out_n", (uint64_t)N * 2));
-        TGX_TRY(holds(b, 8, "out_sq", (uint64_t)(N / 4) * 4));
-    }
-    LayerArgs l{};
-    l.q = (uint16_t*)b[0].ptr;
-    l.kv_cur = (uint16_t*)b[1].ptr;
-    l.state = (float*)b[2].ptr;
-    ResidualArgs r{};
-    r.w = (const uint16_t*)b[3].ptr;
-    r.residual = (const float*)b[4].ptr;
-    r.next_norm = (const float*)b[5].ptr;
-    r.out = (float*)b[6].ptr;
-    r.out_n = (uint16_t*)b[7].ptr;
-    r.out_sq = (float*)b[8].ptr;
-    r.K = K;
-    r.N = N;
-    r.R = Rs;
-    L->a = a;
-    L->l = l;
-    L->r = r;
-    L->k = residual_fold_launch(a, r);
-    L->params[0] = &L->a;
-    L->params[1] = &L->r;
-    L->params[2] = &L->l;
     return TGX_OK;
 }
 
@@ -403,8 +335,7 @@ const std::vector<KernelDesc>& kernels() {
           {"slots", RD, TGX_U32, false},
           {"table", RD, TGX_U32, false},
           {"q", WR, TGX_BF16, false},
-          {"kv", WR, TGX_BF16, false},
-          {"kv_cur", WR, TGX_BF16, false}},
+          {"kv", WR, TGX_BF16, false}},
          decode_constants(),
          build_qkv},
         {"attention_decode",
@@ -412,40 +343,9 @@ const std::vector<KernelDesc>& kernels() {
           {"kv", RD, TGX_BF16, false},
           {"positions", RD, TGX_U32, false},
           {"row_table", RD, TGX_U32, false},
-          {"kv_cur", RD, TGX_BF16, false},
           {"attended", WR, TGX_BF16, false}},
          decode_constants(),
          build_attention},
-        {"qkv_attention",
-         {{"x", RD, TGX_F32, true},
-          {"xn", RD, TGX_BF16, true},
-          {"x_sq", RD, TGX_F32, true},
-          {"gain", RD, TGX_F32, false},
-          {"w", RD, TGX_BF16, false},
-          {"cos", RD, TGX_F32, false},
-          {"sin", RD, TGX_F32, false},
-          {"positions", RD, TGX_U32, false},
-          {"slots", RD, TGX_U32, false},
-          {"table", RD, TGX_U32, false},
-          {"q", WR, TGX_BF16, false},
-          {"kv", WR, TGX_BF16, false},
-          {"kv_cur", WR, TGX_BF16, false},
-          {"row_table", RD, TGX_U32, false},
-          {"state", WR, TGX_F32, false}},
-         decode_constants(),
-         build_qkv_attention},
-        {"gemv_residual_fold",
-         {{"q", RD, TGX_BF16, false},
-          {"kv_cur", RD, TGX_BF16, false},
-          {"state", RD, TGX_F32, false},
-          {"w", RD, TGX_BF16, false},
-          {"residual", RD, TGX_F32, false},
-          {"next_gain", RD, TGX_F32, true},
-          {"out", WR, TGX_F32, false},
-          {"out_n", WR, TGX_BF16, true},
-          {"out_sq", WR, TGX_F32, true}},
-         decode_constants({"K", "N", "strip_rows"}),
-         build_residual_fold},
         {"gemv_residual",
          {{"x", RD, TGX_BF16, false},
           {"w", RD, TGX_BF16, false},
