@@ -463,17 +463,17 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     // Turn j's block, and whether the wave has it (the slot may hold no block there).
     auto block_of_turn = [&](int j) { return (uint32_t)__builtin_amdgcn_readlane((int)turn_block, min(j, WAVE - 1)); };
     auto has = [&](int j) { return w + ATTN_WAVES * j < blocks && block_of_turn(j) < (uint32_t)a.nblocks; };
-    // Turn j's keys and values. Without the turn (`real` false) the same 1 KiB at the pool's start
-    // is read 16 times over instead, from the caches: the loads are made either way, so that the
-    // waits for them can be counted exactly (a load under a branch makes the compiler wait for
-    // every load before its first use).
+    // Turn j's keys and values. Without the turn (`real` false) every lane reads the pool's first
+    // 16 bytes instead, one cache line an instruction from the caches: the loads are made either
+    // way, so that the waits for them can be counted exactly (a load under a branch makes the
+    // compiler wait for every load before its first use).
     auto fetch = [&](int j, bool real, uint4 (&k)[8], uint4 (&v)[8]) {
         const uint16_t* kt = real ? l.kv + ((size_t)block_of_turn(j) * KV + kv) * 2 * KV_TILE : l.kv;
-        const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0;
+        const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0, at = real ? lane * 8 : 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) k[i] = load16(kt + i * stride + lane * 8);
+        for (int i = 0; i < 8; ++i) k[i] = load16(kt + i * stride + at);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + lane * 8);
+        for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + at);
     };
     OnlineSoftmax sm;
     const float scale_log2 = log2_scale(a.scale);
