@@ -48,7 +48,7 @@ tgx_status record(hipStream_t st, const char* what, F enqueue, hipGraphExec_t* e
     hipError_t e = hipGraphInstantiate(exec, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
     if (e != hipSuccess) return fail(TGX_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
-    return TGX_OK;
+    return upload_graph(*exec, st);
 }
 
 // Waits for `ev` (60 s at most, as Submission::wait, recording.rs:747).

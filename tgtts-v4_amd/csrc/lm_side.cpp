@@ -88,6 +88,7 @@ tgx_status side_record(LmSide* s, int advance, hipGraphExec_t* exec) {
     hipError_t e = hipGraphInstantiate(exec, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
     if (e != hipSuccess) return fail(TGX_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    TGX_TRY(upload_graph(*exec, st));
     s->dispatches = n;
     return TGX_OK;
 }

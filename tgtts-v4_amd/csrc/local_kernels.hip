@@ -350,9 +350,16 @@ __global__ void __launch_bounds__(4 * WAVE) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
         for (int j = 0; j < XL; ++j) load_to_lds(xp + j * tile4 + kb * 512, &xs[((kb % RING) * TT + wv + 4 * j) * 64]);
     };
-#pragma unroll
-    for (int kb = 0; kb < RING; ++kb) fetch(kb);
+    // Each group stays behind the loads before it (the waits below count loads in issue order):
+    // without a scheduling barrier between groups the compiler moves a later group's W loads
+    // ahead of an earlier group's loads into LDS, and a wait that counts whole groups then lets a
+    // wave read a slot whose load is still in flight.
     all_issued();
+#pragma unroll
+    for (int kb = 0; kb < RING; ++kb) {
+        fetch(kb);
+        all_issued();
+    }
     f32x4 acc[P][SW][TT];
 #pragma unroll
     for (int p = 0; p < P; ++p)

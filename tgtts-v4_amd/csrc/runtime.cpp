@@ -88,6 +88,12 @@ void rope_tables(const Shape& s, std::vector<float>& cos, std::vector<float>& si
         }
 }
 
+tgx_status upload_graph(hipGraphExec_t exec, hipStream_t stream) {
+    TGX_HIP(hipGraphUpload(exec, stream));
+    TGX_HIP(hipStreamSynchronize(stream));
+    return TGX_OK;
+}
+
 // ---- context ----
 
 tgx_status context_create(int device, Context** out) {
@@ -334,6 +340,7 @@ tgx_status record(Decoder* d, int advance, hipGraphExec_t* exec) {
     hipError_t e = hipGraphInstantiate(exec, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
     if (e != hipSuccess) return fail(TGX_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    TGX_TRY(upload_graph(*exec, s));
     d->dispatches = dispatches;
     return TGX_OK;
 }

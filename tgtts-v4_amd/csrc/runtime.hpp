@@ -121,6 +121,10 @@ struct Decoder {
     ResidualArgs down_args(int l) const;
 };
 
+// A graph just instantiated: its resources uploaded on `stream` (hipGraphUpload) and the stream
+// drained before its first launch, so that no first launch of a graph overlaps its setup.
+tgx_status upload_graph(hipGraphExec_t exec, hipStream_t stream);
+
 tgx_status context_create(int device, Context** out);
 void context_destroy(Context* ctx);
 

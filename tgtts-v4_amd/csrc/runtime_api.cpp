@@ -665,7 +665,10 @@ tgx_status tgx_program_end(tgx_program* prog) {
     Program* p = prog->p;
     if (p->ended) return TGX_OK;
     if (p->launches.empty()) return fail(TGX_E_SHAPE, "a program of no dispatches");
-    if (!p->timed) TGX_HIP(hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0));
+    if (!p->timed) {
+        TGX_HIP(hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0));
+        TGX_TRY(upload_graph(p->exec, p->ctx->stream));
+    }
     if (p->timed) {
         p->t_start.assign(p->launches.size(), nullptr);
         p->t_stop.assign(p->launches.size(), nullptr);

@@ -377,6 +377,7 @@ tgx_status sampler_record(Sampler* s) {
         s->exec = nullptr;
         return fail(TGX_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
     }
+    TGX_TRY(upload_graph(s->exec, st));
     s->dispatches = n;
     s->exec_dirty = false;
     RowProgram p;
