@@ -320,8 +320,14 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
     if (scales) rs.load(g, m0);
     // K >= 1024: 32 stages at least.
     constexpr int PRIMED = AHEAD ? NBUF : NBUF - 1;
+    // The stages go out in stage order, the row scales' loads ahead of them: landed() counts
+    // loads in issue order.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int p = 0; p < PRIMED; ++p) fetch(p, p);
+    for (int p = 0; p < PRIMED; ++p) {
+        fetch(p, p);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     landed(PRIMED - 1);  // stage 0
     if (scales) {
         rs.settle();
