@@ -324,13 +324,37 @@ def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
 
 
 def host_threads() -> int:
-    """The host cores the CPU baseline uses: those the process may run on, at most 16 (the GPU
-    box's share of its host)."""
+    """The host cores the CPU baseline uses: those the process may run on, at most 16. A one-GPU
+    box is given 16 of its host's CPUs (its OMP_NUM_THREADS is 16), whatever os.cpu_count()
+    reports of the whole host; more threads than that would contend with the GPU's own feeding
+    thread and with each other."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(16, n))
+
+
+def host_info() -> dict:
+    """The host the CPU baseline ran on: its CPU model, the CPUs the OS reports, those this process
+    may run on, and OMP_NUM_THREADS as the box sets it."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": affinity,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "threads_used": host_threads(),
+            "why_16": "a one-GPU box's share of its host is 16 CPUs; threads stop there"}
 
 
 def cpu_baseline(weights, seconds: float):
@@ -355,6 +379,7 @@ def cpu_baseline(weights, seconds: float):
         "value": n / dt,
         "unit": "steps/s",
         "cores": oracle.threads(),
+        "host": host_info(),
         "kind": "port",
         "sample": f"{n} fp32 decode steps of the 24-layer stack at batch 1, positions {PROMPT + 1}..{PROMPT + n} "
                   f"(keys and values below {PROMPT} zero), {dt:.1f} s on {oracle.threads()} OpenMP threads",
@@ -476,17 +501,20 @@ def sampler_profile(rows: int, samples: int) -> int:
 
 def measured_traffic(label: str, workload: str):
     """HBM bytes per launch of `label` measured with rocprofv3's FETCH_SIZE and WRITE_SIZE on the
-    same workload, each scaled by the counter's reading of a copy of known size; None when no
-    measurement of this kernel on this workload is on record."""
+    same workload, each scaled by the counter's reading of a copy of known size, and where that
+    figure comes from (not this run: the record's profile file and the commit it was measured at);
+    (None, None) when no measurement of this kernel on this workload is on record."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
-        return None
+        return None, None
     data = json.loads(path.read_text())
     # Batch 1's records at the top, other workloads' under their own key ("batch64").
     for rec in (data.get(label), data.get(workload.replace(" ", ""), {}).get(label)):
         if isinstance(rec, dict) and rec.get("workload") == workload:
-            return rec["bytes_per_launch"]
-    return None
+            source = {"measured_in_this_run": False, "file": rec.get("source"), "commit": rec.get("commit"),
+                      "counters": "FETCH_SIZE x fetch_scale + WRITE_SIZE x write_scale, KiB a dispatch"}
+            return rec["bytes_per_launch"], source
+    return None, None
 
 
 def main() -> int:
@@ -590,6 +618,7 @@ def main() -> int:
     # algorithmic bytes per step; beside it, the kernel with the most time per step.
     def kernel_roofline(label, k):
         achieved = k["bytes_per_launch"] / (k["avg_us"] * 1e-6) / 1e9
+        traffic, traffic_source = measured_traffic(label, f"batch {args.batch}")
         return {
             "bound": "hbm",
             "kernel": label,
@@ -597,7 +626,8 @@ def main() -> int:
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": round(achieved / (HBM_PEAK / 1e9), 4),
-            "traffic": measured_traffic(label, f"batch {args.batch}"),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "bytes_per_launch": k["bytes_per_launch"],
             "avg_us": round(k["avg_us"], 3),
             "of_stream_floor": round(achieved / floor_kernel["GB_s"], 4),

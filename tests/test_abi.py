@@ -71,6 +71,9 @@ def test_spare_rows_are_placed_past_every_position_and_a_slot_is_taken_once():
         (dict(head_dim=128), dict()),
         (dict(heads=16, kv_heads=3), dict()),
         (dict(heads=32, kv_heads=1), dict()),
+        # 16 query heads to a KV head: the prefill attention's tile would spill, so it is refused
+        (dict(heads=32, kv_heads=2), dict()),
+        (dict(heads=16, kv_heads=1), dict()),
         (dict(capacity=0), dict()),
         (dict(hidden=1000), dict()),
         (dict(inner=5000), dict()),
@@ -97,6 +100,23 @@ def test_the_backbone_shapes_are_taken():
     for rows in (1, 16, 17, 32, 64):
         tgx.check_shape(tgx.Shape(capacity=2048), tgx.Batch(rows=rows, slots=rows))
     tgx.check_shape(tgx.Shape(rope=False, layers=8), tgx.Batch(rows=4, slots=8))
+
+
+@pytest.mark.parametrize("kv_heads", [16, 8, 4, 2])
+def test_groups_of_one_to_eight_query_heads_a_kv_head_are_taken(kv_heads):
+    """16 query heads over 16, 8, 4 or 2 KV heads: groups of 1, 2, 4 and 8, each with its own
+    prefill attention instance and decode attention columns."""
+    import tgx
+
+    tgx.check_shape(tgx.Shape(heads=16, kv_heads=kv_heads), tgx.Batch(rows=4, slots=4))
+
+
+def test_a_group_of_sixteen_is_refused_with_its_reason():
+    import tgx
+
+    with pytest.raises(tgx.TgxError) as e:
+        tgx.check_shape(tgx.Shape(heads=32, kv_heads=2), tgx.Batch(rows=1, slots=1))
+    assert e.value.kind == "shape" and "1, 2, 4 or 8" in str(e.value)
 
 
 def test_null_arguments_are_refused_with_a_message():

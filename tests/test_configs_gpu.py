@@ -12,7 +12,8 @@ the oracle (oracle/) as crates/graph/tests/{decode,prefill}.rs hold the referenc
       outputs and cache against the oracle (prefill.rs:365-377), the other seven bit for bit as
       alone
   C5  the 16-request patch step (24-layer backbone, 8-layer residual LM, 4-layer LocDiT and
-      encoder): two requests stage by stage against the oracle, every request as alone
+      encoder) for 300 steps, rows rotating: two requests' LMs at every step and every stage at
+      four steps against the oracle, all 16 requests bit for bit as run alone over the 300 steps
 
 Tolerance (the north star's, bf16 on the GPU against the oracle): cosine >= 0.999 and
 max|got - ref| / max|ref| <= 1e-2, per position or step.
@@ -248,25 +249,33 @@ def test_c4_8x2048_prefill_then_32_steps(ctx, backbone):
     log(f"C4 runs 1..7 bit for bit as alone, {time.time() - t0:.1f} s in all")
 
 
-def test_c5_16_request_patch_step_stage_by_stage_and_as_alone(ctx, backbone):
-    """C5: the full per-patch step at 16 requests, each LM's cache filled to 64 positions: the
-    4-layer encoder over the patch before, the 24-layer backbone and the 8-layer residual LM with
-    the heads between them, the 4-layer LocDiT's 10 Euler steps with CFG-Zero* (guidance 2.0 over
-    both sequences). Three steps; two requests stage by stage against the oracle, each stage fed
-    the GPU's input to it (levels the quantizer rounds the other way at a tie aside); every request
-    bit for bit as run alone on the patch step's one-row program."""
+def test_c5_16_request_patch_step_300_steps_stage_by_stage_and_each_request_as_alone(ctx, backbone):
+    """C5: the full per-patch step at 16 requests for 300 steps, each LM's cache first filled to 64
+    prompt positions: the 4-layer encoder over the patch before, the 24-layer backbone and the
+    8-layer residual LM with the heads between them, the 4-layer LocDiT's 10 Euler steps with
+    CFG-Zero* (guidance 2.0 over both sequences). Requests move to another row every step (request
+    i in row (i + t) mod 16), as crates/graph/tests/patch.rs:175-211 rotates them.
+
+    Checked: for two requests, the backbone's and the residual LM's outputs at all 300 steps
+    against the oracle (its layer-major restatement over the GPU's inputs to each LM, the
+    positions after the prompt at once) and, at steps 0, 1, 2 and 299, every stage (encoder, heads,
+    quantizer levels but those at a tie, sampler, stop logits within the dot product's bound), each
+    stage fed the GPU's input to it; then every one of the 16 requests run alone on the patch
+    step's one-row program over its whole 300 steps (patch.rs:257-278), each patch and stop logit
+    bit for bit as among the 16 (patch.rs:286-317)."""
     import oracle
     import patch_oracle as po
     import tgx
     from tgx.patch import Encoder, HeadsShape, LmSide, PatchShape, PatchStep, Sampler
     from tgx.synth import StackSpec, embeddings, encoder_weights, lm_side_weights, sampler_weights
 
-    rows, context, feat, frames, levels = 16, 64, 64, 4, 9
+    rows, context, feat, frames, levels, steps = 16, 64, 64, 4, 9, 300
+    staged = (0, 1, 2, steps - 1)
     base_spec, res_spec = StackSpec(layers=24, seed=0), StackSpec(layers=8, seed=1)
     dit_spec, enc_spec = StackSpec(layers=4, seed=2), StackSpec(layers=4, seed=3)
     w = lm_side_weights(base_spec, res_spec, 1024, 1024, 256)
     dw, ew = sampler_weights(dit_spec, feat), encoder_weights(enc_spec, feat)
-    cap = 256
+    cap = 384
     t0 = time.time()
     side = LmSide(ctx, tgx.Shape(layers=24, capacity=cap), tgx.Shape(layers=8, capacity=cap, rope=False),
                   tgx.Batch(rows=rows, slots=rows), HeadsShape(1024, 1024, 256, levels))
@@ -282,57 +291,83 @@ def test_c5_16_request_patch_step_stage_by_stage_and_as_alone(ctx, backbone):
     rng = np.random.default_rng(55)
     sampling = np.array([[1.0, 2.0]] * rows, dtype=np.float32)
     sampling[3] = [0.8, 1.5]
+    sampling[12] = [1.3, 3.0]
     picks = (0, 9)
-    base_ref = {r: oracle.Stack(base_spec, {k[8:]: v for k, v in w.items() if k.startswith("base_lm.")}, cap, "f64")
-                for r in picks}
-    res_ref = {r: oracle.Stack(res_spec, {k[12:]: v for k, v in w.items() if k.startswith("residual_lm.")}, cap, "f64",
-                               rope=False) for r in picks}
-    for r in picks:
-        base_ref[r].prefill_rows(0, prompts[0][r * context : (r + 1) * context])
-        res_ref[r].prefill_rows(0, prompts[1][r * context : (r + 1) * context])
     stack = lambda s: po.StackShape(hidden=s.hidden, inner=s.inner, heads=s.heads, kv_heads=s.kv_heads, layers=s.layers,
                                     eps=s.eps, rope_theta=s.rope_theta)
     cond = rng.standard_normal((rows, feat, frames)).astype(np.float32)
-    record = []
-    for k in range(3):
+    conds, noises, patches, stops = [], [], [], []
+    lm_in = {r: {"embed": [], "base_out": [], "residual_in": [], "residual_out": []} for r in picks}
+    for k in range(steps):
         noise = rng.standard_normal((rows, feat, frames)).astype(np.float32)
-        at = [tgx.Row(context + k, r) for r in range(rows)]
-        patch, stop = step.run_rows(at, cond, noise, sampling)
+        order = [(j - k) % rows for j in range(rows)]  # the request in row j
+        at = [tgx.Row(context + k, i) for i in order]
+        patch_rows, stop_rows = step.run_rows(at, cond[order], noise[order], sampling[order])
+        patch, stop = np.empty_like(patch_rows), np.empty_like(stop_rows)
+        patch[order], stop[order] = patch_rows, stop_rows
+        conds.append(cond.copy())
+        noises.append(noise)
+        patches.append(patch)
+        stops.append(stop)
         t = {n: side.read(n) for n in side.TENSORS}
-        embedding = encoder.encode(cond)
-        record.append((cond.copy(), noise, patch, stop))
+        row_of = {i: j for j, i in enumerate(order)}
         for r in picks:
-            checks = {"encoder": (embedding[r], po.encode(ew, stack(enc_spec), feat, frames, cond[r : r + 1])[0]),
-                      "embed": (t["embed"][r], po.linear(w, "enc_to_lm_proj", embedding[r : r + 1])[0]),
-                      "base_out": (t["base_out"][r], base_ref[r].decode(context + k, t["embed"][r]))}
-            pre, lv = po.quantizer(w, t["base_out"][r : r + 1], levels)
-            tie = t["levels"][r] != lv[0].astype(np.float32)
-            if tie.any():
-                frac = np.abs(np.tanh(np.abs(pre[0][tie])) * levels % 1.0 - 0.5)
-                assert np.all(frac < 0.05) and tie.mean() < 0.05, (k, r, frac)
-            lm_hidden, residual_in, to_dit, stop_hidden, logits = po.heads_after_levels(w, t["levels"][r : r + 1],
-                                                                                         t["embed"][r : r + 1])
-            checks["lm_hidden"] = (t["lm_hidden"][r], lm_hidden[0])
-            checks["residual_in"] = (t["residual_in"][r], residual_in[0])
-            checks["residual_out"] = (t["residual_out"][r], res_ref[r].decode(context + k, t["residual_in"][r]))
-            checks["mu"] = (t["mu"][r], np.concatenate([to_dit[0], po.linear(w, "res_to_dit_proj", t["residual_out"][r : r + 1])[0]]))
-            bound = 2.0**-8 * (np.abs(w["stop_head.weight"]).astype(np.float64) @ np.abs(t["stop_hidden"][r]))
-            assert np.all(np.abs(stop[r] - logits[0]) <= bound + 1e-7), (k, r, stop[r], logits[0])
-            x0, want = po.sample(dw, stack(dit_spec), feat, frames, 10, t["mu"][r].reshape(1, 2, 1024), cond[r : r + 1],
-                                 noise[r : r + 1], sampling[r : r + 1])
-            checks["patch moved"] = (patch[r] - x0[0], want[0] - x0[0])
-            checks["patch"] = (patch[r], want[0])
-            for name, (g, e) in checks.items():
-                d = distance(g, e)
-                assert within(d), f"step {k} request {r} {name}: {d}"
-            log(f"C5 step {k} request {r}: every stage within tolerance, {int(tie.sum())} levels at a tie")
+            for name in lm_in[r]:
+                lm_in[r][name].append(t[name][row_of[r]].copy())
+        if k in staged:
+            embedding = encoder.encode(cond[order])
+            for r in picks:
+                j = row_of[r]
+                checks = {"encoder": (embedding[j], po.encode(ew, stack(enc_spec), feat, frames, cond[r : r + 1])[0]),
+                          "embed": (t["embed"][j], po.linear(w, "enc_to_lm_proj", embedding[j : j + 1])[0])}
+                pre, lv = po.quantizer(w, t["base_out"][j : j + 1], levels)
+                tie = t["levels"][j] != lv[0].astype(np.float32)
+                if tie.any():
+                    frac = np.abs(np.tanh(np.abs(pre[0][tie])) * levels % 1.0 - 0.5)
+                    assert np.all(frac < 0.05) and tie.mean() < 0.05, (k, r, frac)
+                lm_hidden, residual_in, to_dit, stop_hidden, logits = po.heads_after_levels(w, t["levels"][j : j + 1],
+                                                                                             t["embed"][j : j + 1])
+                checks["lm_hidden"] = (t["lm_hidden"][j], lm_hidden[0])
+                checks["residual_in"] = (t["residual_in"][j], residual_in[0])
+                checks["mu"] = (t["mu"][j], np.concatenate([to_dit[0], po.linear(w, "res_to_dit_proj", t["residual_out"][j : j + 1])[0]]))
+                bound = 2.0**-8 * (np.abs(w["stop_head.weight"]).astype(np.float64) @ np.abs(t["stop_hidden"][j]))
+                assert np.all(np.abs(stop[r] - logits[0]) <= bound + 1e-7), (k, r, stop[r], logits[0])
+                x0, want = po.sample(dw, stack(dit_spec), feat, frames, 10, t["mu"][j].reshape(1, 2, 1024), cond[r : r + 1],
+                                     noise[r : r + 1], sampling[r : r + 1])
+                checks["patch moved"] = (patch[r] - x0[0], want[0] - x0[0])
+                checks["patch"] = (patch[r], want[0])
+                for name, (g, e) in checks.items():
+                    d = distance(g, e)
+                    assert within(d), f"step {k} request {r} {name}: {d}"
+                log(f"C5 step {k} request {r} (row {j}): every stage within tolerance, {int(tie.sum())} levels at a tie")
         cond = patch.astype(np.float32)  # the next step samples after this one's patch
-    log(f"C5 three 16-request steps checked, {time.time() - t0:.1f} s")
-    for k, (c, z, patch, stop) in enumerate(record):
-        for r in (0, 5, 15):
-            p1, s1 = step.run_rows([tgx.Row(context + k, r)], c[r : r + 1], z[r : r + 1], sampling[r : r + 1])
-            assert _same_bits(p1[0], patch[r]) and _same_bits(s1[0], stop[r]), f"step {k} request {r} alone"
+        if k % 50 == 49:
+            log(f"C5 {k + 1} 16-request steps, {time.time() - t0:.1f} s")
+    # The two LMs over all 300 steps for the picked requests: the oracle's caches hold the prompt,
+    # then every step's input the GPU gave each LM, the positions after the prompt at once.
+    for r in picks:
+        base_ref = oracle.Stack(base_spec, {k[8:]: v for k, v in w.items() if k.startswith("base_lm.")}, cap, "f64")
+        res_ref = oracle.Stack(res_spec, {k[12:]: v for k, v in w.items() if k.startswith("residual_lm.")}, cap, "f64",
+                               rope=False)
+        base_ref.prefill_rows(0, prompts[0][r * context : (r + 1) * context])
+        res_ref.prefill_rows(0, prompts[1][r * context : (r + 1) * context])
+        for name, ref, inp in (("base_out", base_ref, "embed"), ("residual_out", res_ref, "residual_in")):
+            want = ref.prefill_rows(context, np.stack(lm_in[r][inp]))
+            worst = None
+            for k in range(steps):
+                d = distance(lm_in[r][name][k], want[k])
+                assert within(d), f"request {r} {name} step {k}: {d}"
+                worst = d if worst is None or d["cosine"] < worst["cosine"] else worst
+            log(f"C5 request {r} {name} at all {steps} steps within tolerance, worst {worst}")
+    # Every request alone on the one-row program, its whole run from the prompt on (its slot's
+    # cache past the prompt rewritten step by step as it goes).
+    for r in range(rows):
+        for k in range(steps):
+            p1, s1 = step.run_rows([tgx.Row(context + k, r)], conds[k][r : r + 1], noises[k][r : r + 1], sampling[r : r + 1])
+            assert _same_bits(p1[0], patches[k][r]) and _same_bits(s1[0], stops[k][r]), f"request {r} step {k} alone"
+        if r % 4 == 3:
+            log(f"C5 requests 0..{r} alone bit for bit as among 16 over {steps} steps, {time.time() - t0:.1f} s")
     step.close()
     for o in (side, sampler, encoder):
         o.close()
-    log(f"C5 requests alone bit for bit as among 16, {time.time() - t0:.1f} s in all")
+    log(f"C5 all 16 requests alone bit for bit as among 16, {time.time() - t0:.1f} s in all")

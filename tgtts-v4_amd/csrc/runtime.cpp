@@ -160,8 +160,11 @@ tgx_status check_shape(const tgx_shape* in, Shape* s) {
     if (s->layers < 0 || s->capacity <= 0) return refuse("layers " + std::to_string(s->layers) + ", capacity " + std::to_string(s->capacity));
     if (s->capacity > decode_max_capacity())
         return refuse("capacity " + std::to_string(s->capacity) + " past the attention's " + std::to_string(decode_max_capacity()));
-    if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 16 || 16 % (s->heads / s->kv_heads) != 0)
-        return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) + " KV heads: a group of 1, 2, 4, 8 or 16");
+    // Query heads to a KV head: 1, 2, 4 or 8, each with a prefill attention instance whose
+    // registers hold its tile (16 heads a KV head would spill beside waits that count loads in
+    // issue order, and is refused; the reference takes any group, attention_split.comp:24-27).
+    if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 8 || 8 % (s->heads / s->kv_heads) != 0)
+        return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) + " KV heads: a group of 1, 2, 4 or 8");
     // The projections take K in chunks of 1024 columns, up to 4096 (decode_kernels.hip).
     const int most = decode_max_k();
     for (auto [what, k] : {std::pair<const char*, int>{"hidden", s->hidden}, {"inner", s->inner}, {"heads x head_dim", s->heads * HEAD_DIM}})
