@@ -68,7 +68,13 @@ def test_spare_rows_are_placed_past_every_position_and_a_slot_is_taken_once():
 @pytest.mark.parametrize(
     "change, batch",
     [
-        (dict(head_dim=128), dict()),
+        (dict(head_dim=96), dict()),
+        (dict(head_dim=256), dict()),
+        # hidden past 2048 (VoxCPM2's LMs are 2048 wide), an FFN or heads x head_dim past 6144
+        (dict(hidden=4096), dict()),
+        (dict(hidden=2048, inner=7168, head_dim=128), dict()),
+        (dict(heads=64, kv_heads=8, head_dim=128), dict()),
+        (dict(head_dim=128, capacity=16385), dict()),
         (dict(heads=16, kv_heads=3), dict()),
         (dict(heads=32, kv_heads=1), dict()),
         # 16 query heads to a KV head: the prefill attention's tile would spill, so it is refused
@@ -92,6 +98,20 @@ def test_shapes_the_kernels_cannot_cover_are_refused(change, batch):
     with pytest.raises(tgx.TgxError) as e:
         tgx.check_shape(shape, b)
     assert e.value.kind == "shape"
+
+
+def test_voxcpm2s_own_lm_shapes_are_taken():
+    """VoxCPM2's base and residual LMs (crates/graph/src/decode.rs:919-933,
+    crates/graph/src/lm_side.rs:665-679): hidden 2048, FFN 6144, 16 heads over 2 KV heads of 128
+    dimensions, at the reference's capacity of 1024 and at 4096."""
+    import tgx
+
+    for capacity in (1024, 4096):
+        for rope in (True, False):
+            shape = tgx.Shape(hidden=2048, inner=6144, heads=16, kv_heads=2, head_dim=128, layers=28, capacity=capacity,
+                              rope=rope)
+            for rows in (1, 16, 64):
+                tgx.check_shape(shape, tgx.Batch(rows=rows, slots=rows))
 
 
 def test_the_backbone_shapes_are_taken():

@@ -16,13 +16,20 @@ FEAT, FRAMES, LATENT, LEVELS, VOCAB = 64, 4, 256, 9, 48
 LAYOUT = [True] * 4 + [False] * 6 + [True] * 5
 
 
-def _config():
+# The LMs' width: the backbone's (1024 wide, heads of 64) unless a test asks for VoxCPM2's own
+# (2048 wide, an FFN of 6144, heads of 128; crates/graph/src/lm_side.rs:665-679).
+BACKBONE = dict(hidden=1024, inner=4096, head_dim=64)
+VOXCPM2 = dict(hidden=2048, inner=6144, head_dim=128)
+
+
+def _config(lm_shape=BACKBONE):
     from tgx.config import Config
 
-    lm = {"bos_token_id": 1, "eos_token_id": 2, "hidden_size": 1024, "intermediate_size": 4096,
+    h, d = lm_shape["hidden"], lm_shape["head_dim"]
+    lm = {"bos_token_id": 1, "eos_token_id": 2, "hidden_size": h, "intermediate_size": lm_shape["inner"],
           "max_position_embeddings": 256, "num_attention_heads": 16, "num_hidden_layers": 2, "num_key_value_heads": 2,
-          "rms_norm_eps": 1e-5, "rope_theta": 10000, "kv_channels": 64,
-          "rope_scaling": {"type": "longrope", "long_factor": [1.0] * 32, "short_factor": [1.0] * 32,
+          "rms_norm_eps": 1e-5, "rope_theta": 10000, "kv_channels": d,
+          "rope_scaling": {"type": "longrope", "long_factor": [1.0] * (d // 2), "short_factor": [1.0] * (d // 2),
                            "original_max_position_embeddings": 256},
           "vocab_size": VOCAB, "use_mup": False, "scale_emb": 12, "dim_model_base": 256, "scale_depth": 1.4}
     local = {"hidden_dim": 1024, "ffn_dim": 4096, "num_heads": 16, "num_layers": 1, "kv_channels": 64}
@@ -34,15 +41,12 @@ def _config():
     }))
 
 
-def _checkpoint(tmp_path, stops=False):
+def _checkpoint(tmp_path, stops=False, lm_shape=BACKBONE):
     """A VoxCPM2-named checkpoint; unless `stops`, the stop head's two rows are the same, so that
     its logits tie and it never says to stop (a tie goes on: patch.rs:232-235)."""
-    import torch
-    from safetensors.torch import save_file
-
     from tgx.synth import StackSpec, bf16_round, encoder_weights, lm_side_weights, normal, sampler_weights
 
-    base, residual = StackSpec(layers=2, seed=71), StackSpec(layers=1, seed=72)
+    base, residual = StackSpec(layers=2, seed=71, **lm_shape), StackSpec(layers=1, seed=72, **lm_shape)
     dit, local = StackSpec(layers=1, seed=73), StackSpec(layers=1, seed=74)
     lm_w = lm_side_weights(base, residual, 1024, 1024, LATENT)
     dit_w, enc_w = sampler_weights(dit, FEAT), encoder_weights(local, FEAT)
@@ -56,7 +60,8 @@ def _checkpoint(tmp_path, stops=False):
     e.update({f"feat_encoder.{k}": v for k, v in enc_w.items() if not k.startswith(("layers.", "norm"))})
     if not stops:
         e["stop_head.weight"] = np.stack([e["stop_head.weight"][0]] * 2)
-    e["base_lm.embed_tokens.weight"] = bf16_round(normal(75, "embed_tokens", VOCAB * 1024, np.float32)).reshape(VOCAB, 1024)
+    h = lm_shape["hidden"]
+    e["base_lm.embed_tokens.weight"] = bf16_round(normal(75, "embed_tokens", VOCAB * h, np.float32)).reshape(VOCAB, h)
     path = tmp_path / "model.safetensors"
     _save(path, e)
     return path
@@ -71,10 +76,10 @@ def _prompt(seed):
                   np.array(LAYOUT, dtype=np.uint8)), rng.standard_normal((4 * FRAMES, FEAT)).astype(np.float32)
 
 
-def _engine(ctx, ck, slots=4):
+def _engine(ctx, ck, slots=4, lm_shape=BACKBONE):
     from tgx.engine import Engine, Settings
 
-    return Engine.from_config(ctx, _config(), ck, Settings(slots=slots, capacity=256, max_rows=64, timesteps=10,
+    return Engine.from_config(ctx, _config(lm_shape), ck, Settings(slots=slots, capacity=256, max_rows=64, timesteps=10,
                                                            prompt_cache_bytes=1 << 28))
 
 
@@ -91,13 +96,18 @@ def _generate(engine, steps):
     return out
 
 
-def test_requests_step_together_as_each_does_alone(ctx, tmp_path):
+@pytest.mark.parametrize("lm_shape", [BACKBONE, VOXCPM2], ids=["backbone", "voxcpm2"])
+def test_requests_step_together_as_each_does_alone(ctx, tmp_path, lm_shape):
+    """Two requests started from their prompts and stepped together, then the first again alone
+    in another slot with the same noise: bit for bit. At the backbone's LM width and at VoxCPM2's
+    own (2048 wide, FFN 6144, heads of 128), built from config.json sizes and a checkpoint."""
     from tgx import TgxError
     from tgx.checkpoint import Checkpoint
 
-    ck = Checkpoint(_checkpoint(tmp_path))
+    print(f"[engine] LMs {lm_shape}", flush=True)
+    ck = Checkpoint(_checkpoint(tmp_path, lm_shape=lm_shape))
     (pa, va), (pb, vb) = _prompt(81), _prompt(82)
-    engine = _engine(ctx, ck)
+    engine = _engine(ctx, ck, lm_shape=lm_shape)
     assert engine.slots() == 4
     assert engine.start(0, pa, va, max_patches=3, temperature=1.0, cfg=2.0) == len(pa)
     assert engine.start(2, pb, vb, max_patches=5, temperature=0.8, cfg=1.5) == len(pb)

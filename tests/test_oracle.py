@@ -167,9 +167,10 @@ def test_attention_over_one_position_returns_its_value():
 # ---- the whole stack against an independent float64 model --------------------------------------
 
 
-def torch_stack(spec, weights, x, rope=True, start=0, causal=True):
+def torch_stack(spec, weights, x, rope=True, start=0, causal=True, rope_dim=None):
     """MiniCPM-4 layers over a run of positions from library ops in float64: RMSNorm written out,
-    RoPE by rotate_half, torch's scaled_dot_product_attention (causal, GQA by repeat), SiLU."""
+    RoPE by rotate_half, torch's scaled_dot_product_attention (causal, GQA by repeat), SiLU.
+    rope_dim (a planted defect when not the head width): the width rotate_half pairs within."""
     import torch
     import torch.nn.functional as F
 
@@ -179,18 +180,22 @@ def torch_stack(spec, weights, x, rope=True, start=0, causal=True):
     h = torch.tensor(x, dtype=torch.float64)
     w = {k: torch.tensor(v, dtype=torch.float64) for k, v in weights.items()}
     H, KV, d = spec.heads, spec.kv_heads, spec.head_dim
-    cos, sin = oracle.rope_tables(start + T, d, spec.rope_theta)
+    rd = rope_dim or d
+    cos, sin = oracle.rope_tables(start + T, rd, spec.rope_theta)
     cos = torch.tensor(cos[start:], dtype=torch.float64)
     sin = torch.tensor(sin[start:], dtype=torch.float64)
-    cos = torch.cat([cos, cos], dim=-1)[:, None, :]
-    sin = torch.cat([sin, sin], dim=-1)[:, None, :]
+    cos = torch.cat([cos, cos] * (d // rd), dim=-1)[:, None, :]
+    sin = torch.cat([sin, sin] * (d // rd), dim=-1)[:, None, :]
 
     def norm(v, g):
         return v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + spec.eps) * g
 
     def rotate_half(v):
-        a, b = v[..., : d // 2], v[..., d // 2 :]
-        return torch.cat([-b, a], dim=-1)
+        parts = []
+        for j in range(0, d, rd):
+            a, b = v[..., j : j + rd // 2], v[..., j + rd // 2 : j + rd]
+            parts += [-b, a]
+        return torch.cat(parts, dim=-1)
 
     for l in range(spec.layers):
         n = norm(h, w[f"layers.{l}.input_layernorm"])
@@ -219,6 +224,29 @@ def tiny():
 
     spec = StackSpec(hidden=512, inner=1024, heads=8, kv_heads=2, layers=2, dtype="f32", seed=7)
     return spec, stack_weights(spec)
+
+
+def test_heads_of_128_dimensions_match_the_model_and_a_rope_of_64_fails():
+    """VoxCPM2's LMs take heads of 128 dimensions (crates/graph/src/decode.rs:919-933): decode
+    steps, a prefill and the layer-by-layer prefill at head_dim 128 against the float64 torch
+    model; the model rotating the pairs (i, i + 32) of each 64 dimensions instead of (i, i + 64)
+    must disagree with the oracle."""
+    import oracle
+    from tgx.synth import StackSpec, embeddings, stack_weights
+
+    spec = StackSpec(hidden=1024, inner=1536, heads=8, kv_heads=2, head_dim=128, layers=2, dtype="f32", seed=9)
+    w = stack_weights(spec)
+    x = embeddings(3, "x", 40, spec.hidden).astype(np.float64)
+    want = torch_stack(spec, w, x)
+    st = oracle.Stack(spec, w, 64)
+    out = st.prefill(0, x[:24])
+    steps = np.stack([st.decode(t, x[t]) for t in range(24, 40)])
+    got = np.concatenate([out, steps])
+    assert np.max(np.abs(got - want)) <= 1e-10 * np.max(np.abs(want))
+    rows = oracle.Stack(spec, w, 64).prefill_rows(0, x)
+    assert np.max(np.abs(rows - want)) <= 1e-9 * np.max(np.abs(want))
+    wrong = torch_stack(spec, w, x, rope_dim=64)
+    assert np.max(np.abs(got - wrong)) > 1e-3 * np.max(np.abs(want))
 
 
 def test_decode_steps_match_a_float64_model_of_library_ops(tiny):

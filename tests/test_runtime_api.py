@@ -33,7 +33,8 @@ def test_the_kernels_keep_the_reference_names_and_binding_order():
         "rmsnorm": ["out", "positions"],
         "stream_read": ["out"],
     }
-    common = ("hidden", "inner", "heads", "kv_heads", "rows", "capacity", "slots", "max_blocks", "blocks", "eps", "rope")
+    common = ("hidden", "inner", "heads", "kv_heads", "rows", "capacity", "slots", "max_blocks", "blocks", "eps", "rope",
+              "head_dim")
     for k in ("gemv_qkv_rope", "attention_decode", "gemv_gate_up"):
         assert table[k].constants == common
     assert table["gemv_residual"].constants == common + ("K", "N", "strip_rows")

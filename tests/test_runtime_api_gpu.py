@@ -72,7 +72,7 @@ class StepProgram:
         self.sq_a, self.sq_b = keep(M(rows * h)), keep(M(rows * h))  # [rows][h / 4] f32
         self.q, self.att = keep(M(rows * H * 64 * 2)), keep(M(rows * H * 64 * 2))
         self.mlp = keep(M(rows * inner * 2))
-        c = [h, inner, H, KV, rows, capacity, slots, max_blocks, blocks, rt.f32_bits(spec.eps), 1]
+        c = [h, inner, H, KV, rows, capacity, slots, max_blocks, blocks, rt.f32_bits(spec.eps), 1, 64]
         self.program = p = rt.Program(ctx, timed=timed)
         for l in range(L):
             first = l == 0
@@ -227,7 +227,7 @@ def test_a_recording_refuses_on_the_host_what_the_kernels_could_not_run(ctx):
     import tgx.runtime as rt
 
     h, inner, H, KV, rows, cap = 1024, 4096, 16, 2, 2, 64
-    c = [h, inner, H, KV, rows, cap, 2, 1, 2, rt.f32_bits(1e-5), 1]
+    c = [h, inner, H, KV, rows, cap, 2, 1, 2, rt.f32_bits(1e-5), 1, 64]
     q = rt.Memory(ctx, rows * H * 64 * 2)
     kv = rt.Memory(ctx, 2 * KV * 2 * 64 * 64 * 2)
     pos, row_table = rt.Memory(ctx, rows * 4), rt.Memory(ctx, rows * 4)
@@ -247,6 +247,8 @@ def test_a_recording_refuses_on_the_host_what_the_kernels_could_not_run(ctx):
     refused("shape", "attention_decode", [q, (kv, 8, 0), pos, row_table, att], c)  # offset not 16-aligned
     refused("shape", "attention_decode", [q, kv, pos, row_table, att], c[:5] + [4096 * 64] + c[6:])  # capacity
     refused("shape", "attention_decode", [q, kv, pos, row_table, att], c[:7] + [0] + c[8:])  # a table too short
+    refused("shape", "attention_decode", [q, kv, pos, row_table, att], c[:11] + [96])  # a head width not taken
+    refused("shape", "attention_decode", [q, kv, pos, row_table, att], c[:11] + [128])  # q, kv short for 128
     refused("shape", "stream_read", [(q, 0, 1000), att], [])
     p.dispatch("attention_decode", [q, kv, pos, row_table, att], c, groups=(KV, rows, 1))
     with pytest.raises(tgx.TgxError) as e:

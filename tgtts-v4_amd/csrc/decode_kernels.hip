@@ -37,7 +37,10 @@ constexpr int GEMV_THREADS = GEMV_WAVES * WAVE;
 constexpr int CHUNK_KB = 32;
 constexpr int CHUNK_COLS = CHUNK_KB * 32;
 constexpr int PER_WAVE = CHUNK_KB / GEMV_WAVES;
-constexpr int MAX_CHUNKS = 4;  // K up to 4096; kernels are built for 1 chunk and for up to 4
+constexpr int MAX_CHUNKS = 6;  // K up to 6144 (down_proj's inner); kernels are built for 1 to 6 chunks
+// hidden up to 2048 (VoxCPM2's LMs): the norms, q/k/v and gate/up. Past it layer 0's q/k/v, which
+// reads the f32 rows, would hold more than a wave's registers.
+constexpr int MAX_HIDDEN_CHUNKS = 2;
 // A norm's input carries a sum of squares for each SQ_COLS columns of a row.
 constexpr int SQ_COLS = 4;
 
@@ -244,12 +247,13 @@ __device__ __forceinline__ long block_of(const DecodeArgs& a, uint32_t slot, uin
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
-// gemv_qkv_rope: workgroup (strip, tile): a strip of 16 permuted rows (8 RoPE pairs of a head).
+// gemv_qkv_rope: workgroup (strip, tile): a strip of 16 permuted rows (8 RoPE pairs of a head of
+// D = head_dim dimensions, the pairs (i, i + D / 2)).
 // PRENORMED: the input comes as x input_norm in bf16 with its sums of squares (every layer past
 // the first), else as the f32 rows. The epilogue's thread (p, c) (pair p, tile row c; the first
 // 128 threads) loads its row's position and slot first of all, and the RoPE factors and cache
 // block that hang on them while the products' operands are on their way.
-template <int CH, bool PRENORMED>
+template <int CH, bool PRENORMED, int D>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, LayerArgs l) {
     constexpr int R = QKV_ROWS;
     constexpr int EPI = (R / 2) * 16;  // epilogue threads
@@ -259,7 +263,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
     const int strip[1] = {strip_id};
     const int p = threadIdx.x % (R / 2), c = (threadIdx.x / (R / 2)) % 16;
     const int b = tile * 16 + c;
-    const int per_head = HEAD_DIM / R;  // strips to a head
+    const int per_head = D / R;  // strips to a head
     const int head = strip_id / per_head;
     const int i = (strip_id % per_head) * (R / 2) + p;  // the pair's first dimension in the head
     uint32_t pos = 0, slot = 0;
@@ -284,7 +288,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
     if (threadIdx.x < EPI) {
         // 32-bit indexes (the tables hold far fewer than 2^32 entries)
         const uint32_t pc = min(pos, (uint32_t)a.capacity - 1), sc = min(slot, (uint32_t)a.nslots - 1);
-        const uint32_t at = pc * (HEAD_DIM / 2) + (uint32_t)i;
+        const uint32_t at = pc * (D / 2) + (uint32_t)i;
         co = a.cos[at];
         si = a.sin[at];
         // The product kept apart from the add: fused, they make a 64-bit multiply-add whose unused
@@ -317,21 +321,22 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
         vc = rc;
     }
     if (head < H) {
-        uint16_t* q = l.q + ((size_t)b * H + head) * HEAD_DIM;
+        uint16_t* q = l.q + ((size_t)b * H + head) * D;
         q[i] = (uint16_t)bf16_bits(va);
-        q[i + HEAD_DIM / 2] = (uint16_t)bf16_bits(vc);
+        q[i + D / 2] = (uint16_t)bf16_bits(vc);
         return;
     }
     if (entry >= (uint32_t)a.nblocks) return;  // the slot holds no block there
     const int kv = head < H + KV ? head - H : head - H - KV;
-    uint16_t* tl = l.kv + ((size_t)entry * KV + kv) * 2 * KV_TILE;
+    constexpr int TILE = kv_tile(D);
+    uint16_t* tl = l.kv + ((size_t)entry * KV + kv) * 2 * TILE;
     const int pp = (int)(pos % BLOCK_TOKENS);
     if (head < H + KV) {
-        tl[key_index(pp, i)] = (uint16_t)bf16_bits(va);
-        tl[key_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
+        tl[key_index(pp, i, D)] = (uint16_t)bf16_bits(va);
+        tl[key_index(pp, i + D / 2, D)] = (uint16_t)bf16_bits(vc);
     } else {
-        tl[KV_TILE + value_index(pp, i)] = (uint16_t)bf16_bits(va);
-        tl[KV_TILE + value_index(pp, i + HEAD_DIM / 2)] = (uint16_t)bf16_bits(vc);
+        tl[TILE + value_index(pp, i)] = (uint16_t)bf16_bits(va);
+        tl[TILE + value_index(pp, i + D / 2)] = (uint16_t)bf16_bits(vc);
     }
 }
 
@@ -433,16 +438,24 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
 
 // ---------------------------------------------------------------------------------------------
 // attention_decode: workgroup (kv, b) attends the `group` query heads KV head kv serves of row b
-// over its slot's positions 0..pos; wave w takes blocks w, w + 8, ... (its turns) with an online
-// softmax, two turns' keys and values in flight at once.
-// Per block, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in bf16 straight
+// over its slot's positions 0..pos; wave w takes turns w, w + 8, ... (a turn: TURN positions, a
+// 64-position block at head_dim 64, half a block at 128, so that a turn is 8 key and 8 value
+// fragments either way) with an online softmax, two turns' keys and values in flight at once.
+// Per turn, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in bf16 straight
 // from the registers S^T left it in.
 // Two memory round trips before the first product: the row's position, the cache blocks of the
-// wave's turns (lane j: block w + 8 j, from the row's copy of its slot's table) and q together,
-// then the first two turns' keys and values.
+// wave's turns (lane j: the block of turn w + 8 j, from the row's copy of its slot's table) and q
+// together, then the first two turns' keys and values.
+constexpr int attention_turn(int head_dim) { return head_dim == 64 ? BLOCK_TOKENS : BLOCK_TOKENS / 2; }
 
+template <int D>
 __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
-    extern __shared__ float attn_lds[];  // [waves][group][65] partial outputs
+    constexpr int TURN = attention_turn(D);
+    constexpr int PT = TURN / 16, KS = PT / 2, DT = D / 16, DS = D / 32;
+    constexpr int KF = PT * DS, VF = DT * KS;  // a turn's key and value fragments
+    static_assert(KF == 8 && VF == 8, "a turn is 8 key and 8 value fragments");
+    constexpr int TILE = kv_tile(D);
+    extern __shared__ float attn_lds[];  // [waves][group][D + 1] partial outputs
     __shared__ float sm_m[ATTN_WAVES][16];
     __shared__ float sm_l[ATTN_WAVES][16];
     const int kv = blockIdx.x, b = blockIdx.y;
@@ -450,52 +463,59 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     const int H = a.heads, KV = a.kv_heads, group = H / KV;
     const int h = lane % 16;
     const uint32_t pos = a.positions[b];
-    const uint32_t turn_block =
-        a.row_table[(uint32_t)b * (uint32_t)a.max_blocks + (uint32_t)min(w + ATTN_WAVES * lane, a.max_blocks - 1)];
+    const uint32_t turn_block = a.row_table[(uint32_t)b * (uint32_t)a.max_blocks +
+                                            (uint32_t)min((w + ATTN_WAVES * lane) * TURN / BLOCK_TOKENS, a.max_blocks - 1)];
     // Columns past the group read its last head again; nothing reads what they give.
-    uint4 qf[2];
+    uint4 qf[DS];
 #pragma unroll
-    for (int ds = 0; ds < 2; ++ds) qf[ds] = load16(l.q + ((size_t)b * H + kv * group + min(h, group - 1)) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
+    for (int ds = 0; ds < DS; ++ds) qf[ds] = load16(l.q + ((size_t)b * H + kv * group + min(h, group - 1)) * D + ds * 32 + (lane / 16) * 8);
     all_issued();
     if (pos >= (uint32_t)a.capacity) return;  // a spare row
-    const int blocks = (int)(pos / BLOCK_TOKENS) + 1;
+    const int turns = (int)(pos / TURN) + 1;
 
     // Turn j's block, and whether the wave has it (the slot may hold no block there).
     auto block_of_turn = [&](int j) { return (uint32_t)__builtin_amdgcn_readlane((int)turn_block, min(j, WAVE - 1)); };
-    auto has = [&](int j) { return w + ATTN_WAVES * j < blocks && block_of_turn(j) < (uint32_t)a.nblocks; };
-    // Turn j's keys and values. Without the turn (`real` false) every lane reads the pool's first
-    // 16 bytes instead, one cache line an instruction from the caches: the loads are made either
-    // way, so that the waits for them can be counted exactly (a load under a branch makes the
-    // compiler wait for every load before its first use).
-    auto fetch = [&](int j, bool real, uint4 (&k)[8], uint4 (&v)[8]) {
-        const uint16_t* kt = real ? l.kv + ((size_t)block_of_turn(j) * KV + kv) * 2 * KV_TILE : l.kv;
-        const int stride = real ? 64 * 8 : 0, vt = real ? KV_TILE : 0, at = real ? lane * 8 : 0;
+    auto has = [&](int j) { return w + ATTN_WAVES * j < turns && block_of_turn(j) < (uint32_t)a.nblocks; };
+    // Turn j's keys and values: its positions' key fragments are one run of the block's key tile
+    // (8 of them from fragment 8 half), its value fragments (dt, ks) those of dimensions 16 dt and
+    // positions 32 (half + ks) of the value tile. Without the turn (`real` false) every lane reads
+    // the pool's first 16 bytes instead, one cache line an instruction from the caches: the loads
+    // are made either way, so that the waits for them can be counted exactly (a load under a branch
+    // makes the compiler wait for every load before its first use).
+    auto fetch = [&](int j, bool real, uint4 (&k)[KF], uint4 (&v)[VF]) {
+        const int half = ((w + ATTN_WAVES * j) * TURN % BLOCK_TOKENS) / 32;
+        const uint16_t* kt = real ? l.kv + ((size_t)block_of_turn(j) * KV + kv) * 2 * TILE : l.kv;
+        const int at = real ? lane * 8 : 0;
+        const int k0 = real ? half * KF * 512 : 0, kstride = real ? 512 : 0;
+        const int v0 = real ? TILE + half * 512 : 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) k[i] = load16(kt + i * stride + at);
+        for (int i = 0; i < KF; ++i) k[i] = load16(kt + k0 + i * kstride + at);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = load16(kt + vt + i * stride + at);
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) v[dt * KS + ks] = load16(kt + v0 + (dt * 2 + ks) * kstride + at);
     };
-    OnlineSoftmax sm;
+    OnlineSoftmax<PT, DT> sm;
     const float scale_log2 = log2_scale(a.scale);
-    // S^T = K Q^T for a turn's block, then its softmax step (masked only in the block holding
-    // the position).
-    auto take = [&](const uint4 (&k)[8], const uint4 (&v)[8], int j) __attribute__((always_inline)) {
-        f32x4 s[4];
+    // S^T = K Q^T for a turn's keys, then its softmax step (masked only in the turn holding the
+    // position).
+    auto take = [&](const uint4 (&k)[KF], const uint4 (&v)[VF], int j) __attribute__((always_inline)) {
+        f32x4 s[PT];
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
+        for (int pt = 0; pt < PT; ++pt) {
             s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ds = 0; ds < 2; ++ds) s[pt] = mfma16(k[pt * 2 + ds], qf[ds], s[pt]);
+            for (int ds = 0; ds < DS; ++ds) s[pt] = mfma16(k[pt * DS + ds], qf[ds], s[pt]);
         }
-        const uint32_t p0 = (uint32_t)(w + ATTN_WAVES * j) * BLOCK_TOKENS;
-        if (p0 + BLOCK_TOKENS - 1 <= pos)
-            sm.block<false>(s, v, p0, pos, pos, scale_log2);
+        const uint32_t p0 = (uint32_t)(w + ATTN_WAVES * j) * TURN;
+        if (p0 + TURN - 1 <= pos)
+            sm.template block<false>(s, v, p0, pos, pos, scale_log2);
         else
-            sm.block<true>(s, v, p0, pos, pos, scale_log2);
+            sm.template block<true>(s, v, p0, pos, pos, scale_log2);
     };
-    // Two buffers: the first two turns straight (every context up to 16 blocks), then the rest
+    // Two buffers: the first two turns straight (every context up to 16 turns), then the rest
     // two at a time, each pair's loads issued once the last pair is taken.
-    uint4 ka[8], va[8], kb[8], vb[8];
+    uint4 ka[KF], va[VF], kb[KF], vb[VF];
     const bool t0 = has(0), t1 = has(1);
     fetch(0, t0, ka, va);
     fetch(1, t1, kb, vb);
@@ -515,23 +535,23 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     }
     if (h < group) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) attn_lds[(w * group + h) * (HEAD_DIM + 1) + dt * 16 + (lane / 16) * 4 + i] = sm.o[dt][i];
+            for (int i = 0; i < 4; ++i) attn_lds[(w * group + h) * (D + 1) + dt * 16 + (lane / 16) * 4 + i] = sm.o[dt][i];
     }
     __syncthreads();
-    // The waves joined in order (wave 0 holds block 0, so M is finite).
-    for (int idx = threadIdx.x; idx < group * HEAD_DIM; idx += ATTN_THREADS) {
-        const int hh = idx / HEAD_DIM, d = idx % HEAD_DIM;
+    // The waves joined in order (wave 0 holds turn 0, so M is finite).
+    for (int idx = threadIdx.x; idx < group * D; idx += ATTN_THREADS) {
+        const int hh = idx / D, d = idx % D;
         float M = -INFINITY;
         for (int j = 0; j < ATTN_WAVES; ++j) M = fmaxf(M, sm_m[j][hh]);
         float L = 0.f, O = 0.f;
         for (int j = 0; j < ATTN_WAVES; ++j) {
             const float f = sm_l[j][hh] > 0.f ? __builtin_amdgcn_exp2f(sm_m[j][hh] - M) : 0.f;
             L += sm_l[j][hh] * f;
-            O += attn_lds[(j * group + hh) * (HEAD_DIM + 1) + d] * f;
+            O += attn_lds[(j * group + hh) * (D + 1) + d] * f;
         }
-        l.attended[operand_index(b, (kv * group + hh) * HEAD_DIM + d, a.rows)] = (uint16_t)bf16_bits(O / L);
+        l.attended[operand_index(b, (kv * group + hh) * D + d, a.rows)] = (uint16_t)bf16_bits(O / L);
     }
 }
 
@@ -575,7 +595,7 @@ __global__ void __launch_bounds__(WAVE) final_rmsnorm(DecodeArgs a, const float*
 
 namespace {
 
-size_t attention_lds(const DecodeArgs& a) { return (size_t)ATTN_WAVES * (a.heads / a.kv_heads) * (HEAD_DIM + 1) * 4; }
+size_t attention_lds(const DecodeArgs& a) { return (size_t)ATTN_WAVES * (a.heads / a.kv_heads) * (a.head_dim + 1) * 4; }
 
 // The kernel instantiated for `chunks` chunks of K (1 to MAX_CHUNKS, checked by the shape).
 template <template <int> class Pick>
@@ -584,15 +604,23 @@ auto by_chunks(int chunks) -> decltype(Pick<1>::get()) {
         case 2: return Pick<2>::get();
         case 3: return Pick<3>::get();
         case 4: return Pick<4>::get();
+        case 5: return Pick<5>::get();
+        case 6: return Pick<6>::get();
         default: return Pick<1>::get();
     }
 }
-template <int CH> struct PickQkv { static auto get() { return gemv_qkv_rope<CH, false>; } };
-template <int CH> struct PickQkvNormed { static auto get() { return gemv_qkv_rope<CH, true>; } };
-template <int CH> struct PickGateUp { static auto get() { return gemv_gate_up<CH, 1>; } };
+// Kernels whose K is hidden are built for up to MAX_HIDDEN_CHUNKS chunks (the shape check refuses
+// more); past that the picks name the largest, never launched.
+constexpr int hidden_ch(int ch) { return ch < MAX_HIDDEN_CHUNKS ? ch : MAX_HIDDEN_CHUNKS; }
+template <int D>
+struct Qkv {
+    template <int CH> struct Plain { static auto get() { return gemv_qkv_rope<hidden_ch(CH), false, D>; } };
+    template <int CH> struct Normed { static auto get() { return gemv_qkv_rope<hidden_ch(CH), true, D>; } };
+};
+template <int CH> struct PickGateUp { static auto get() { return gemv_gate_up<hidden_ch(CH), 1>; } };
 template <int CH> struct PickResidual4 { static auto get() { return gemv_residual<CH, 4>; } };
 template <int CH> struct PickResidual16 { static auto get() { return gemv_residual<CH, 16>; } };
-template <int CH> struct PickFinal { static auto get() { return final_rmsnorm<CH>; } };
+template <int CH> struct PickFinal { static auto get() { return final_rmsnorm<hidden_ch(CH)>; } };
 
 // The kernel of `launch` with its arguments `params`, timed by the timer's next events when given.
 hipError_t dispatch_launch(const char* label, const KernelLaunch& k, void** params, hipStream_t stream, DispatchTimer* timer) {
@@ -609,15 +637,18 @@ hipError_t dispatch_launch(const char* label, const KernelLaunch& k, void** para
 KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed) {
     const int chunks = a.hidden / CHUNK_COLS;
     KernelLaunch k;
-    k.func = prenormed ? (const void*)by_chunks<PickQkvNormed>(chunks) : (const void*)by_chunks<PickQkv>(chunks);
-    k.grid = dim3((a.heads + 2 * a.kv_heads) * HEAD_DIM / QKV_ROWS, decode_tiles(a.rows));
+    if (a.head_dim == 128)
+        k.func = prenormed ? (const void*)by_chunks<Qkv<128>::Normed>(chunks) : (const void*)by_chunks<Qkv<128>::Plain>(chunks);
+    else
+        k.func = prenormed ? (const void*)by_chunks<Qkv<64>::Normed>(chunks) : (const void*)by_chunks<Qkv<64>::Plain>(chunks);
+    k.grid = dim3((a.heads + 2 * a.kv_heads) * a.head_dim / QKV_ROWS, decode_tiles(a.rows));
     k.block = dim3(GEMV_THREADS);
     return k;
 }
 
 KernelLaunch attention_launch(const DecodeArgs& a) {
     KernelLaunch k;
-    k.func = (const void*)attention_decode;
+    k.func = a.head_dim == 128 ? (const void*)attention_decode<128> : (const void*)attention_decode<64>;
     k.grid = dim3(a.kv_heads, a.rows);
     k.block = dim3(ATTN_THREADS);
     k.lds = (uint32_t)attention_lds(a);
@@ -722,17 +753,24 @@ int decode_residual_rows(int rows) { return rows <= 16 ? 4 : 16; }
 
 int decode_max_k() { return MAX_CHUNKS * CHUNK_COLS; }
 
-int decode_max_capacity() { return ATTN_WAVES * WAVE * BLOCK_TOKENS; }
+int decode_max_hidden() { return MAX_HIDDEN_CHUNKS * CHUNK_COLS; }
+
+int decode_max_capacity(int head_dim) { return ATTN_WAVES * WAVE * attention_turn(head_dim); }
 
 hipError_t decode_prepare(size_t device_lds) {
-    hipFuncAttributes attr{};
-    hipError_t e = hipFuncGetAttributes(&attr, (const void*)attention_decode);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void*)attention_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)(device_lds - attr.sharedSizeBytes));
+    for (const void* f : {(const void*)attention_decode<64>, (const void*)attention_decode<128>}) {
+        hipFuncAttributes attr{};
+        hipError_t e = hipFuncGetAttributes(&attr, f);
+        if (e != hipSuccess) return e;
+        e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(device_lds - attr.sharedSizeBytes));
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
-size_t decode_attention_lds(int heads, int kv_heads) { return (size_t)ATTN_WAVES * (heads / kv_heads) * (HEAD_DIM + 1) * 4; }
+size_t decode_attention_lds(int heads, int kv_heads, int head_dim) {
+    return (size_t)ATTN_WAVES * (heads / kv_heads) * (head_dim + 1) * 4;
+}
 
 hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* gain, float* out, uint32_t* positions,
                              int advance, hipStream_t stream, DispatchTimer* timer) {

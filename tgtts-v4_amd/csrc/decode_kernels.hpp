@@ -11,6 +11,7 @@ namespace tgx {
 // decode.rs:198-227, plus the paged cache's block table).
 struct DecodeArgs {
     int hidden, inner, heads, kv_heads;
+    int head_dim;    // 64 or 128
     int rows;        // rows of the batch
     int capacity;    // positions a slot may reach
     int nslots;
@@ -22,7 +23,7 @@ struct DecodeArgs {
     const uint32_t* slots;      // [rows]
     const uint32_t* table;      // [nslots][max_blocks], UINT32_MAX where none
     const uint32_t* row_table;  // [rows][max_blocks]: each row's slot's table row (UINT32_MAX for a spare row)
-    const float* cos;           // [capacity][32]
+    const float* cos;           // [capacity][head_dim / 2]
     const float* sin;
 };
 
@@ -38,9 +39,9 @@ struct LayerArgs {
     const float* x_sq;        // [rows][hidden / 4]
     const float* input_norm;  // [hidden] f32
     const uint16_t* qkv;      // tiled bf16, rows permuted (qkv_row_of)
-    uint16_t* q;              // [rows][heads][64] bf16
+    uint16_t* q;              // [rows][heads][head_dim] bf16
     uint16_t* kv;             // the layer's cache pool: [blocks][kv_heads][key tile, value tile]
-    uint16_t* attended;       // [rows][heads 64] bf16
+    uint16_t* attended;       // [rows][heads head_dim] bf16
     const uint16_t* mid_n;    // o_proj's output times post_norm in bf16 [rows][hidden]
     const float* mid_sq;      // [rows][hidden / 4]
     const uint16_t* gate_up;  // tiled bf16 [2 inner][hidden]
@@ -76,13 +77,14 @@ struct DispatchTimer {
     int used = 0, capacity = 0;
 };
 
-// Tiles of 16 rows a batch of `rows` takes, the longest K the projections take, and the LDS the
-// attention takes.
+// Tiles of 16 rows a batch of `rows` takes, the longest K the projections take (the norms' and
+// q/k/v's K, hidden, at most decode_max_hidden()), and the LDS the attention takes.
 int decode_tiles(int rows);
 int decode_max_k();
-// The longest capacity the attention takes: a lane to each block a wave reads.
-int decode_max_capacity();
-size_t decode_attention_lds(int heads, int kv_heads);
+int decode_max_hidden();
+// The longest capacity the attention takes at a head width: a lane to each turn a wave takes.
+int decode_max_capacity(int head_dim);
+size_t decode_attention_lds(int heads, int kv_heads, int head_dim);
 // Lets the attention take up to `device_lds` bytes of LDS per workgroup.
 hipError_t decode_prepare(size_t device_lds);
 // A dispatch of one of the step's kernels: the kernel instance chosen for the shape, with its grid,

@@ -156,34 +156,38 @@ __device__ __forceinline__ float lane_xor32(float v) {
     return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
-// Attention's online softmax over blocks of 64 keys for the 16 columns (query heads or
-// (position, head) pairs) of a wave, from S^T = K Q^T in s[pt] (key 16 pt + 4 (lane / 16) + i,
-// column lane % 16) and the block's value tiles: the running max m, kept in log2 units
-// (scores times scale log2(e)), the running sum l of P and O^T in o (lane 16 g + c: column c,
-// dimensions 16 dt + 4 g .. + 3). P is rounded to bf16 for the product P V and summed as
-// rounded, by an MFMA against ones. MASK: keys past the column's position `pos` count for
-// nothing, and the values past `vlast` (the last position any column of the wave may see) read
-// as zero: P is zero there, but a cache block past the position may hold anything, NaN included
-// (a block handed on from a request that ended not finite), and 0 NaN is NaN. Blocks wholly at
-// or below every column's position need no mask. The first block a column sees holds key
-// 0 <= pos, so m is finite after it.
+// Attention's online softmax over a turn of 16 PT keys (PT 4: a 64-key block at head_dim 64; PT 2:
+// half a block at head_dim 128) for the 16 columns (query heads or (position, head) pairs) of a
+// wave, from S^T = K Q^T in s[pt] (key 16 pt + 4 (lane / 16) + i, column lane % 16) and the turn's
+// value fragments vin[dt KS + ks] (dimensions 16 dt .., positions 32 ks .. of the turn; KS = PT / 2):
+// the running max m, kept in log2 units (scores times scale log2(e)), the running sum l of P and
+// O^T in o (lane 16 g + c: column c, dimensions 16 dt + 4 g .. + 3, DT = head_dim / 16 tiles). P is
+// rounded to bf16 for the product P V and summed as rounded, by an MFMA against ones. MASK: keys
+// past the column's position `pos` count for nothing, and the values past `vlast` (the last
+// position any column of the wave may see) read as zero: P is zero there, but a cache block past
+// the position may hold anything, NaN included (a block handed on from a request that ended not
+// finite), and 0 NaN is NaN. Turns wholly at or below every column's position need no mask. The
+// first turn a column sees holds key 0 <= pos, so m is finite after it.
+template <int PT, int DT>
 struct OnlineSoftmax {
+    static constexpr int KS = PT / 2;
     float m = -INFINITY, l = 0.f;
-    f32x4 o[4] = {};
+    f32x4 o[DT] = {};
 
     template <bool MASK>
-    __device__ __forceinline__ void block(f32x4 (&s)[4], const uint4 (&vin)[8], uint32_t p0, uint32_t pos, uint32_t vlast,
+    __device__ __forceinline__ void block(f32x4 (&s)[PT], const uint4 (&vin)[DT * KS], uint32_t p0, uint32_t pos, uint32_t vlast,
                                           float scale_log2) {
         const int lane = threadIdx.x % WAVE;
-        uint4 vf[8];
+        uint4 vf[DT * KS];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vf[i] = vin[i];
+        for (int i = 0; i < DT * KS; ++i) vf[i] = vin[i];
         if (MASK) {
-            // Lane 16 g + d % 16 of value fragment 2 dt + ks holds in its slot j the position
-            // 32 ks + 16 (j / 4) + 4 g + j % 4 (value_index); word w holds slots 2 w and 2 w + 1.
+            // Lane 16 g + d % 16 of value fragment dt KS + ks holds in its slot j the position
+            // 32 ks + 16 (j / 4) + 4 g + j % 4 of the turn (value_index); word w holds slots 2 w and
+            // 2 w + 1.
             const uint32_t g = (uint32_t)lane / 16;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
+            for (int ks = 0; ks < KS; ++ks) {
                 uint32_t keep[4];
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
@@ -191,8 +195,8 @@ struct OnlineSoftmax {
                     keep[w] = (p <= vlast ? 0x0000ffffu : 0u) | (p + 1 <= vlast ? 0xffff0000u : 0u);
                 }
 #pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    uint4& f = vf[dt * 2 + ks];
+                for (int dt = 0; dt < DT; ++dt) {
+                    uint4& f = vf[dt * KS + ks];
                     f.x &= keep[0];
                     f.y &= keep[1];
                     f.z &= keep[2];
@@ -202,7 +206,7 @@ struct OnlineSoftmax {
         }
         float mx = -INFINITY;
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
+        for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (MASK && p0 + pt * 16 + (lane / 16) * 4 + i > pos) s[pt][i] = -INFINITY;
@@ -212,9 +216,9 @@ struct OnlineSoftmax {
         mx = fmaxf(mx, lane_xor32(mx));
         const float m_new = fmaxf(m, mx * scale_log2);
         const float rescale = __builtin_amdgcn_exp2f(m - m_new);
-        uint4 pf[2];
+        uint4 pf[KS];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
             uint32_t words[4];
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
@@ -230,12 +234,12 @@ struct OnlineSoftmax {
         const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
         f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) sum = mfma16(ones, pf[ks], sum);
+        for (int ks = 0; ks < KS; ++ks) sum = mfma16(ones, pf[ks], sum);
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
+        for (int dt = 0; dt < DT; ++dt) {
             o[dt] *= rescale;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) o[dt] = mfma16(vf[dt * 2 + ks], pf[ks], o[dt]);
+            for (int ks = 0; ks < KS; ++ks) o[dt] = mfma16(vf[dt * KS + ks], pf[ks], o[dt]);
         }
         l = l * rescale + sum[0];
         m = m_new;
@@ -296,17 +300,20 @@ __host__ __device__ constexpr int qkv_row_of(int strip, int r, int head_dim, int
 }
 
 // The paged KV cache: per layer, block and KV head, a key tile and a value tile of 64 positions
-// x 64 dimensions (4096 bf16 each), both in MFMA operand order.
+// x D dimensions (D = head_dim, 64 or 128; 64 D bf16 each), both in MFMA operand order.
 //  keys: A operand of S^T = K Q^T: (p, d) at [p / 16][d / 32][lane = 16 ((d % 32) / 8) + p % 16][d % 8]
+//   (a 16-position tile's D / 32 fragments together, so that 32 positions' keys are one run)
 //  values: A operand of O^T = V^T P: (p, d) at [d / 16][p / 32][lane = 16 g + d % 16][s] where
 //   within the 32 positions pp = p % 32 the slot is g = (pp % 16) / 4, s = pp % 4 + 4 (pp / 16),
 //   the order in which a lane holds P after S^T, so P feeds the second product from registers.
 constexpr int BLOCK_TOKENS = 64;
+// The local stacks' head width (the encoder's and the DiT's), and the narrower of the LMs' two.
 constexpr int HEAD_DIM = 64;
-constexpr int KV_TILE = BLOCK_TOKENS * HEAD_DIM;  // bf16 per key or value tile
+constexpr int KV_TILE = BLOCK_TOKENS * HEAD_DIM;  // bf16 per key or value tile at head_dim 64
+__host__ __device__ constexpr int kv_tile(int head_dim) { return BLOCK_TOKENS * head_dim; }
 
-__host__ __device__ constexpr int key_index(int p, int d) {
-    return (((p / 16) * 2 + d / 32) * 64 + ((d % 32) / 8) * 16 + p % 16) * 8 + d % 8;
+__host__ __device__ constexpr int key_index(int p, int d, int head_dim = HEAD_DIM) {
+    return (((p / 16) * (head_dim / 32) + d / 32) * 64 + ((d % 32) / 8) * 16 + p % 16) * 8 + d % 8;
 }
 __host__ __device__ constexpr int value_index(int p, int d) {
     return (((d / 16) * 2 + p / 32) * 64 + (((p % 32) % 16) / 4) * 16 + d % 16) * 8 + (p % 4) + 4 * ((p % 32) / 16);

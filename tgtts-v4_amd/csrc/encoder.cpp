@@ -95,6 +95,8 @@ tgx_status encoder_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     if (patch->rows < 1) return shape_fail("no rows");
     if (F < 1 || F > 4) return shape_fail(std::to_string(F) + " frames to a patch (1 to 4)");
     if (C < 16 || C % 16 || C > 64) return shape_fail(std::to_string(C) + " channels (16, 32, 48 or 64)");
+    // The local stacks' heads are 64 wide (VoxCPM2's encoder and DiT: 1024 wide over 16 heads).
+    if (s.head_dim != HEAD_DIM) return shape_fail("a local stack of head_dim " + std::to_string(s.head_dim) + " (the kernels take 64)");
     if (T > LOCAL_MAX_T || H % 4) return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads");
     if (s.inner % 256 || !local_supported(s.hidden, s.inner, H, KV, LOCAL_O_PARTS, LOCAL_DOWN_PARTS))
         return shape_fail("a local stack " + std::to_string(s.hidden) + " wide with an FFN " + std::to_string(s.inner) + " wide");

@@ -13,7 +13,7 @@ namespace tgx {
 namespace {
 
 __global__ void __launch_bounds__(256) gemv_linear(LinearArgs a) {
-    __shared__ uint4 xs[LINEAR_MAX_K / 32 * 64];  // [k-block][lane]: 64 KiB at K 2048
+    extern __shared__ uint4 xs[];  // [k-block][lane]: 32 KiB a 1024 columns (128 KiB at K 4096)
     __shared__ f32x4 red[4][WAVE];
     const int strip = blockIdx.x, tile = blockIdx.y;
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -83,8 +83,20 @@ hipError_t launch_select_rows(const uint32_t* flags, const float* a, const float
 }
 
 hipError_t launch_linear(const char* label, const LinearArgs& a, hipStream_t stream, DispatchTimer* timer) {
-    dispatch(label, gemv_linear, dim3((a.N + 15) / 16, (a.rows + 15) / 16), dim3(256), 0, stream, timer, a);
+    const int K = a.K0 + a.K1;
+    if (K <= 0 || K % 32 || K > LINEAR_MAX_K) return hipErrorInvalidValue;
+    dispatch(label, gemv_linear, dim3((a.N + 15) / 16, (a.rows + 15) / 16), dim3(256), (size_t)K / 32 * 64 * sizeof(uint4), stream,
+             timer, a);
     return hipGetLastError();
+}
+
+hipError_t heads_prepare(size_t device_lds) {
+    hipFuncAttributes attr{};
+    hipError_t e = hipFuncGetAttributes(&attr, (const void*)gemv_linear);
+    if (e != hipSuccess) return e;
+    if ((size_t)LINEAR_MAX_K / 32 * 64 * sizeof(uint4) + attr.sharedSizeBytes > device_lds) return hipErrorInvalidValue;
+    return hipFuncSetAttribute((const void*)gemv_linear, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)(device_lds - attr.sharedSizeBytes));
 }
 
 }  // namespace tgx

@@ -22,9 +22,13 @@ struct LinearArgs {
     float levels;
 };
 
-constexpr int LINEAR_MAX_K = 2048;
+// The inputs' columns a linear layer takes (its x0 and x1 together): VoxCPM2's fusion_concat_proj
+// joins two 2048-wide rows. The inputs are staged in LDS, 32 KiB a 1024 columns.
+constexpr int LINEAR_MAX_K = 4096;
 
 hipError_t launch_linear(const char* label, const LinearArgs& a, hipStream_t stream, DispatchTimer* timer);
+// Lets gemv_linear take the LDS of LINEAR_MAX_K columns (of the device's `device_lds` a workgroup).
+hipError_t heads_prepare(size_t device_lds);
 // out[r] = flags[r] ? a[r] : b[r], rows of K f32 values (K a multiple of 4): the quantizer's output at
 // a prompt's audio positions and the base LM's at its text (select_rows.comp).
 hipError_t launch_select_rows(const uint32_t* flags, const float* a, const float* b, float* out, int rows, int K,

@@ -37,7 +37,7 @@ tgx_status hold_rows(Decoder* d, int rows, int tiles) {
     TGX_HIP(hipStreamSynchronize(d->ctx->stream));
     prefill_free(d);
     const Shape& s = d->shape;
-    const size_t h = s.hidden, att = (size_t)s.heads * HEAD_DIM;
+    const size_t h = s.hidden, att = (size_t)s.heads * s.head_dim;
     PrefillState& p = d->pf;
     TGX_TRY(prefill_alloc(d, &p.x, rows * h));
     TGX_TRY(prefill_alloc(d, &p.h, rows * h));
@@ -79,7 +79,8 @@ tgx_status launch(Decoder* d, const PrefillState& p) {
     a.max_blocks = d->max_blocks;
     a.nblocks = d->nblocks;
     a.eps = s.eps;
-    a.scale = 1.0f / std::sqrt((float)HEAD_DIM);
+    a.head_dim = s.head_dim;
+    a.scale = 1.0f / std::sqrt((float)s.head_dim);
     a.rope = s.rope ? 1 : 0;
     a.tok_pos = p.tok_pos;
     a.tok_slot = p.tok_slot;
@@ -90,7 +91,7 @@ tgx_status launch(Decoder* d, const PrefillState& p) {
     for (int l = 0; l < s.layers; ++l) {
         const Layer& L = d->layers[l];
         layers[l] = PrefillLayer{L.qkv, L.o, L.gate_up, L.down, L.input_norm, L.post_norm,
-                                 d->kv + (size_t)l * d->nblocks * s.kv_heads * 2 * KV_TILE, d->od_rows};
+                                 d->kv + (size_t)l * d->nblocks * s.kv_heads * 2 * kv_tile(s.head_dim), d->od_rows};
     }
     PrefillBuffers b{p.x, p.h, p.mid, p.normed, p.q, p.attended, p.mlp, p.row_sq, p.out, p.tiles, p.ntiles};
     if (d->timed) d->timer.used = 0;
@@ -172,7 +173,7 @@ tgx_status hold_runs(Decoder* d, const tgx_run* runs, int nruns) {
 // kernels read before they write cleared (the input's; the attention writes only the runs' rows of
 // its output), then the kernels; on the context's stream, without waiting.
 tgx_status enqueue(Decoder* d, const Plan& plan, const PrefillState& p, const float* x, bool x_on_device) {
-    const size_t h = d->shape.hidden, att = (size_t)d->shape.heads * HEAD_DIM, M = plan.M, pad = plan.M_pad - M;
+    const size_t h = d->shape.hidden, att = (size_t)d->shape.heads * d->shape.head_dim, M = plan.M, pad = plan.M_pad - M;
     hipStream_t st = d->ctx->stream;
     TGX_TRY(sync_slots(d));
     TGX_HIP(hipMemcpyAsync(p.x, x, M * h * 4, x_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
@@ -191,14 +192,14 @@ size_t whole(size_t bytes) { return (bytes + 255) / 256 * 256; }
 
 // The bytes of a prefill's tensors for `rows` rows and `tiles` tiles, each 256-byte aligned.
 size_t tensor_bytes(const Shape& s, size_t rows, size_t tiles) {
-    const size_t h = s.hidden, att = (size_t)s.heads * HEAD_DIM;
+    const size_t h = s.hidden, att = (size_t)s.heads * s.head_dim;
     return 4 * whole(rows * h * 4) + whole(rows * h * 2) + whole(rows * h / 128 * 4) + 2 * whole(rows * att * 2) +
            whole(rows * (size_t)s.inner * 2) + 2 * whole(rows * 4) + whole(tiles * sizeof(PrefillTile));
 }
 
 // The tensors laid one after another from `base`.
 void carve(const Shape& s, size_t rows, size_t tiles, unsigned char* base, PrefillState& p) {
-    const size_t h = s.hidden, att = (size_t)s.heads * HEAD_DIM;
+    const size_t h = s.hidden, att = (size_t)s.heads * s.head_dim;
     size_t at = 0;
     auto take = [&](auto*& ptr, size_t bytes) {
         ptr = reinterpret_cast<std::remove_reference_t<decltype(ptr)>>(base + at);

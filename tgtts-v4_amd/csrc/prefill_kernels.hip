@@ -168,8 +168,8 @@ __device__ __forceinline__ void tile_of(int& nb, int& mb) {
 }
 
 // W in strips of WR rows (o_proj and down_proj: 4 or 16, the rest 16), gathered into 16-row
-// fragments as it lands in LDS.
-template <int EPI, int WR, int TM>
+// fragments as it lands in LDS. D: the head width the q/k/v epilogue rotates and caches by.
+template <int EPI, int WR, int TM, int D = HEAD_DIM>
 __global__ void __launch_bounds__(GemmTile<TM>::THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_gemm(PrefillArgs a, GemmArgs g) {
     using T = GemmTile<TM>;
@@ -439,7 +439,8 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
         // A row's 32 values of cos and sin 36 floats apart: the 16 rows a wave's lanes read at once
         // (and the threads' rows as they store them) then fall on distinct banks, where 32 apart
         // put every row on the same ones.
-        constexpr int RS = HEAD_DIM / 2 + 4;
+        constexpr int RS = D / 2 + 4;
+        static_assert((size_t)TM * (2 * RS + 2) * 4 <= T::LDS, "the rows' RoPE tables fit the ring's LDS");
         float* t_cos = reinterpret_cast<float*>(lds);          // [TM][RS]
         float* t_sin = t_cos + TM * RS;                        // [TM][RS]
         uint32_t* t_pos = reinterpret_cast<uint32_t*>(t_sin + TM * RS);  // [TM]
@@ -456,11 +457,11 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                     blk = a.table[(size_t)sl * a.max_blocks + p / BLOCK_TOKENS];
                     if (a.rope) {
 #pragma unroll
-                        for (int e = 0; e < HEAD_DIM / 2; e += 4) {
+                        for (int e = 0; e < D / 2; e += 4) {
                             *reinterpret_cast<float4*>(t_cos + j * RS + e) =
-                                *reinterpret_cast<const float4*>(a.cos + (size_t)p * (HEAD_DIM / 2) + e);
+                                *reinterpret_cast<const float4*>(a.cos + (size_t)p * (D / 2) + e);
                             *reinterpret_cast<float4*>(t_sin + j * RS + e) =
-                                *reinterpret_cast<const float4*>(a.sin + (size_t)p * (HEAD_DIM / 2) + e);
+                                *reinterpret_cast<const float4*>(a.sin + (size_t)p * (D / 2) + e);
                         }
                     }
                 }
@@ -473,10 +474,10 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const int strip = strip_of<EPI>(nb, wn, s, g.N);
-            const int head = strip / 4, qtr = strip % 4;
+            const int head = strip / (D / 16), qtr = strip % (D / 16);
             const bool second = quad >= 2;  // rows 8..15: the pairs' second halves
             const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
-            const int d0 = p0 + (second ? HEAD_DIM / 2 : 0);
+            const int d0 = p0 + (second ? D / 2 : 0);
             const bool rotate = head < H + KV && a.rope;
 #pragma unroll
             for (int t = 0; t < WT; ++t) {
@@ -508,21 +509,22 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                     // q scaled by scale log2(e), the units the attention's softmax takes.
                     const float qs = log2_scale(a.scale);
                     uint2 packed = make_uint2(pack_bf16x2(v[0] * qs, v[1] * qs), pack_bf16x2(v[2] * qs, v[3] * qs));
-                    *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * HEAD_DIM + d0) = packed;
+                    *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * D + d0) = packed;
                     continue;
                 }
                 const uint32_t blk = t_blk[j];
                 if (blk >= (uint32_t)a.nblocks) continue;
                 const int kv = head < H + KV ? head - H : head - H - KV;
-                uint16_t* tl = g.kv + ((size_t)blk * KV + kv) * 2 * KV_TILE;
+                constexpr int TILE = kv_tile(D);
+                uint16_t* tl = g.kv + ((size_t)blk * KV + kv) * 2 * TILE;
                 const int pp = (int)(pos % BLOCK_TOKENS);
                 if (head < H + KV) {
                     // Four consecutive dimensions of a key sit side by side in its tile.
-                    *reinterpret_cast<uint2*>(tl + key_index(pp, d0)) =
+                    *reinterpret_cast<uint2*>(tl + key_index(pp, d0, D)) =
                         make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) tl[KV_TILE + value_index(pp, d0 + i)] = (uint16_t)bf16_bits(v[i]);
+                    for (int i = 0; i < 4; ++i) tl[TILE + value_index(pp, d0 + i)] = (uint16_t)bf16_bits(v[i]);
                 }
             }
         }
@@ -583,27 +585,25 @@ __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* 
 // The values past `vlast` read as zero (as OnlineSoftmax's).
 constexpr float LAZY_SHIFT = 8.0f;
 
-// The largest of a score tile's 16 floats, in plain code: the compiler makes it a v_max3_f32 chain
-// (quieting only the first two operands) and gives each read of an MFMA's result the wait states
-// it needs, which it could not do for inline asm.
-__device__ __forceinline__ float peak16(const f32x4 (&s)[4]) {
-    float m = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
-    m = fmaxf(fmaxf(m, s[0][3]), s[1][0]);
-    m = fmaxf(fmaxf(m, s[1][1]), s[1][2]);
-    m = fmaxf(fmaxf(m, s[1][3]), s[2][0]);
-    m = fmaxf(fmaxf(m, s[2][1]), s[2][2]);
-    m = fmaxf(fmaxf(m, s[2][3]), s[3][0]);
-    m = fmaxf(fmaxf(m, s[3][1]), s[3][2]);
-    return fmaxf(m, s[3][3]);
+// The largest of a column's scores over PT tiles (16 PT floats), in plain code: the compiler makes it a
+// v_max3_f32 chain (quieting only the first two operands) and gives each read of an MFMA's result
+// the wait states it needs, which it could not do for inline asm.
+template <int PT>
+__device__ __forceinline__ float peak_of(const f32x4 (&s)[PT]) {
+    float m = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+    for (int k = 2; k < 4 * PT; k += 2) m = fmaxf(fmaxf(m, s[k / 4][k % 4]), s[(k + 1) / 4][(k + 1) % 4]);
+    return m;
 }
 
-// The value fragments of a block (the A operand of O^T = V^T P, value_index) past `vlast` zeroed:
-// lane 16 g + d % 16 of fragment 2 dt + ks holds in its slot j the position
-// 32 ks + 16 (j / 4) + 4 g + j % 4; word w holds slots 2 w and 2 w + 1.
-__device__ __forceinline__ void zero_values_past(uint4 (&vf)[8], uint32_t p0, uint32_t vlast) {
+// A chunk's value fragments (the A operand of O^T = V^T P, value_index) past `vlast` zeroed:
+// lane 16 g + d % 16 of fragment dt KS + ks holds in its slot j the position
+// p0 + 32 ks + 16 (j / 4) + 4 g + j % 4; word w holds slots 2 w and 2 w + 1.
+template <int KS, int DT>
+__device__ __forceinline__ void zero_values_past(uint4 (&vf)[DT * KS], uint32_t p0, uint32_t vlast) {
     const uint32_t g = (uint32_t)(threadIdx.x % WAVE) / 16;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
         uint32_t keep[4];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -611,8 +611,8 @@ __device__ __forceinline__ void zero_values_past(uint4 (&vf)[8], uint32_t p0, ui
             keep[w] = (p <= vlast ? 0x0000ffffu : 0u) | (p + 1 <= vlast ? 0xffff0000u : 0u);
         }
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-            uint4& f = vf[dt * 2 + ks];
+        for (int dt = 0; dt < DT; ++dt) {
+            uint4& f = vf[dt * KS + ks];
             f.x &= keep[0];
             f.y &= keep[1];
             f.z &= keep[2];
@@ -621,47 +621,51 @@ __device__ __forceinline__ void zero_values_past(uint4 (&vf)[8], uint32_t p0, ui
     }
 }
 
+// A column's lazy softmax over chunks of 16 PT keys (PT tiles of 16 positions) into DT tiles of
+// 16 output dimensions.
+template <int PT, int DT>
 struct LazySoftmax {
+    static constexpr int KS = PT / 2;    // the chunk's k-blocks of 32 positions
     f32x4 neg_r = {0.f, 0.f, 0.f, 0.f};  // -r in each slot: the score MFMA's accumulator input
     f32x4 lsum = {0.f, 0.f, 0.f, 0.f};   // l, the column's sum of P (every slot alike)
-    f32x4 o[4] = {};
+    f32x4 o[DT] = {};
 
-    // The block's scores less r, s, with the keys past the column's position `pos` at -inf when
+    // The chunk's scores less r, s, with the keys past the column's position `pos` at -inf when
     // MASK; returns the lane's largest.
     template <bool MASK>
-    __device__ __forceinline__ float peak(f32x4 (&s)[4], uint32_t p0, uint32_t pos) {
+    __device__ __forceinline__ float peak(f32x4 (&s)[PT], uint32_t p0, uint32_t pos) {
         const int lane = threadIdx.x % WAVE;
         if (MASK) {
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt)
+            for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     if (p0 + pt * 16 + (lane / 16) * 4 + i > pos) s[pt][i] = -INFINITY;
         }
-        return peak16(s);
+        return peak_of<PT>(s);
     }
-    // The block's columns past the shift (or all on the first block) move r to their maximum (each
+    // The chunk's columns past the shift (or all on the first chunk) move r to their maximum (each
     // column's over its four lanes; mx the lane's largest, from peak), s and o, l rescaled. A
     // column that stays subtracts 0 and scales by 1: the same bits as no call.
     template <bool FIRST>
-    __device__ __forceinline__ void rescale(f32x4 (&s)[4], float mx) {
+    __device__ __forceinline__ void rescale(f32x4 (&s)[PT], float mx) {
         float cm = fmaxf(mx, lane_xor16(mx));
         cm = fmaxf(cm, lane_xor32(cm));
         const float d = (FIRST || cm > LAZY_SHIFT) ? cm : 0.f;
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) s[pt] -= d;
+        for (int pt = 0; pt < PT; ++pt) s[pt] -= d;
         neg_r -= d;
         if (!FIRST) {
             const float f = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[dt] *= f;
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= f;
             lsum *= f;
         }
     }
-    // P = 2^s in bf16 (pf): s, the block's scores less r, after any rescale.
-    __device__ __forceinline__ static void probs(const f32x4 (&s)[4], uint4 (&pf)[2]) {
+    // P = 2^s in bf16 (pf): s, the chunk's scores less r, after any rescale.
+    __device__ __forceinline__ static void probs(const f32x4 (&s)[PT], uint4 (&pf)[KS]) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
             const f32x4 a = s[2 * ks], b = s[2 * ks + 1];
             pf[ks] = make_uint4(pack_bf16x2(__builtin_amdgcn_exp2f(a[0]), __builtin_amdgcn_exp2f(a[1])),
                                 pack_bf16x2(__builtin_amdgcn_exp2f(a[2]), __builtin_amdgcn_exp2f(a[3])),
@@ -670,38 +674,41 @@ struct LazySoftmax {
         }
     }
     // The MFMA half: column sums of P (every row of ones^T P is the sum; bf16 1.0 is 0x3f80) and
-    // O^T += V^T P, each accumulator's two products apart, the other four between them. vf: the
-    // block's values, zeroed past the last position any column sees.
-    __device__ __forceinline__ void accumulate(const uint4 (&pf)[2], const uint4 (&vf)[8]) {
+    // O^T += V^T P, each accumulator's products apart, the others between them. vf: the chunk's
+    // values (fragment dt KS + ks), zeroed past the last position any column sees.
+    __device__ __forceinline__ void accumulate(const uint4 (&pf)[KS], const uint4 (&vf)[DT * KS]) {
         const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
             lsum = mfma16(ones, pf[ks], lsum);
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[dt] = mfma16(vf[dt * 2 + ks], pf[ks], o[dt]);
+            for (int dt = 0; dt < DT; ++dt) o[dt] = mfma16(vf[dt * KS + ks], pf[ks], o[dt]);
         }
     }
 };
 
 // ---------------------------------------------------------------------------------------------
 // prefill_attention: workgroup (tile, kv): the tile's positions (up to 32, 32 / WAVES to a wave)
-// for the `group` query heads KV head kv serves. Columns of the MFMA are (position, head) pairs,
-// 16 / group positions to a column group, CG column groups to a wave. The slot's blocks from 0 to
-// the tile's last position are staged through LDS in turn; each column keeps its running maximum,
-// sum and output (attention_rows.comp:71-116).
+// for the `group` query heads KV head kv serves, heads of D dimensions. Columns of the MFMA are
+// (position, head) pairs, 16 / group positions to a column group, CG column groups to a wave. The
+// slot's positions from 0 to the tile's last are staged through LDS a chunk at a time (CHUNK
+// positions: a 64-position block at D 64, half a block at D 128, so that a chunk's keys and values
+// are 16 KiB either way); each column keeps its running maximum, sum and output
+// (attention_rows.comp:71-116).
 // A workgroup's tile: ATTN_TILE positions of a run, except for 8 query heads to a KV head, where it
-// takes 16 positions with four waves, so that two workgroups share a CU: their barriers are their
-// own, and one's softmax runs beside the other's products. Groups of 1, 2, 4 and 8 have an
+// takes 16 positions with four waves (eight at D 128), so that two workgroups share a CU: their
+// barriers are their own, and one's softmax runs beside the other's products. Groups of 1, 2, 4 and 8 have an
 // instance; 16 (four column groups a wave) would hold more than a wave's registers and spill
 // beside the ring's waits, which count loads in issue order, so the shape check refuses it.
 constexpr int ATTN_TILE = 32;
 constexpr int ATTN_TILE_8 = 16;
-// The attention's ring of key-and-value stages: a stage is one block (16 KiB), ATTN_STAGES of them,
+// The attention's ring of key-and-value stages: a stage is one chunk (16 KiB), ATTN_STAGES of them,
 // up to ATTN_STAGES - 2 in flight beyond the two being taken.
-constexpr int ATTN_STAGE = 2 * KV_TILE / 8;  // uint4
+constexpr int ATTN_STAGE = 2 * KV_TILE / 8;  // uint4: 16 fragments of 1 KiB
 constexpr int ATTN_STAGES = 4;
+constexpr int attention_chunk(int head_dim) { return head_dim == 64 ? BLOCK_TOKENS : BLOCK_TOKENS / 2; }
 
-template <int TILE, int WAVES, int CG>
+template <int TILE, int WAVES, int CG, int D>
 __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_eu(2))) prefill_attention(PrefillArgs a, const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ kvpool,
                                                                  uint16_t* __restrict__ attended,
@@ -711,11 +718,16 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     constexpr int per_col = TOK / CG;          // positions to a column group
     constexpr int group = 16 / per_col;
     static_assert(CG <= 2, "two column groups a wave at most: more spill");
+    constexpr int CHUNK = attention_chunk(D);  // positions a stage holds
+    constexpr int PT = CHUNK / 16, KS = PT / 2, DS = D / 32, DT = D / 16;
+    constexpr int KF = PT * DS, VF = DT * KS;  // a chunk's key and value fragments
+    static_assert(KF == 8 && VF == 8, "a chunk is 8 key and 8 value fragments");
+    constexpr int TILE_ELEMS = kv_tile(D);
     constexpr int NS = ATTN_STAGES;
     constexpr int LOADS = ATTN_STAGE / 64 / WAVES;  // 1 KiB loads a wave makes of a stage
     static_assert(LOADS * 64 * WAVES == ATTN_STAGE, "a stage in whole 1 KiB loads");
-    // The ring of NS stages, each a block's key tile then value tile as they lie in the cache,
-    // then the slot's block ids.
+    // The ring of NS stages, each a chunk's 8 key fragments then its 8 value fragments, then the
+    // slot's block ids.
     extern __shared__ uint4 attn_ring[];
     uint32_t* block_ids = reinterpret_cast<uint32_t*>(attn_ring + NS * ATTN_STAGE);
     const PrefillTile tile = tiles[blockIdx.x];
@@ -727,6 +739,7 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     const int col = lane % 16;
     const uint32_t last = tile.pos0 + tile.count - 1;
     const int blocks = (int)(last / BLOCK_TOKENS) + 1;
+    const int chunks = (int)(last / CHUNK) + 1;
 
     // The slot's blocks 0 .. blocks - 1 (a block the slot does not hold reads as block 0, never
     // reached by a position the run holds).
@@ -734,7 +747,7 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         const uint32_t blk = a.table[(size_t)tile.slot * a.max_blocks + i];
         block_ids[i] = blk < (uint32_t)a.nblocks ? blk : 0u;
     }
-    uint4 qf[CG][2];
+    uint4 qf[CG][DS];
     uint32_t cpos[CG];
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
@@ -743,75 +756,85 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         const size_t row = tile.row0 + (tok < (int)tile.count ? tok : 0);
         cpos[cg] = tile.pos0 + tok;
 #pragma unroll
-        for (int ds = 0; ds < 2; ++ds) qf[cg][ds] = load16(q + (row * H + head) * HEAD_DIM + ds * 32 + (lane / 16) * 8);
+        for (int ds = 0; ds < DS; ++ds) qf[cg][ds] = load16(q + (row * H + head) * D + ds * 32 + (lane / 16) * 8);
     }
     // The ids and q in place (this wait and barrier are the compiler's own: no load to LDS is in
     // flight yet).
     __syncthreads();
 
-    // Block bi into stage bi % NS, straight from the cache into LDS: wave w copies bytes
-    // 1 KiB (LOADS w + j) of the block's 16 KiB, lane l its 16 bytes 16 l. Past the last block the
-    // last is loaded again (never read), so that every wave makes LOADS loads a block and its
-    // count in flight says which stages have landed. The id is read by an LDS read of its own,
-    // which the compiler does not order behind the loads to LDS in flight.
-    auto fetch = [&](int bi) __attribute__((always_inline)) {
-        const uint32_t* at = block_ids + min(bi, blocks - 1);
+    // Chunk ci into stage ci % NS, straight from the cache into LDS: wave w copies the stage's
+    // fragments LOADS w .. LOADS w + LOADS - 1 (of 16: the chunk's keys, a run of its block's key
+    // tile from fragment 8 half, then its values, fragments (dt, half + ks) of the value tile), lane
+    // l its 16 bytes 16 l. Past the last chunk the last is loaded again (never read), so that every
+    // wave makes LOADS loads a chunk and its count in flight says which stages have landed. The
+    // block id is read by an LDS read of its own, which the compiler does not order behind the
+    // loads to LDS in flight.
+    auto fetch = [&](int ci) __attribute__((always_inline)) {
+        const int c = min(ci, chunks - 1);
+        const uint32_t* at = block_ids + c * CHUNK / BLOCK_TOKENS;
         uint32_t id;
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(id) : "v"(lds_offset(at)) : "memory");
         const uint32_t blk = __builtin_amdgcn_readfirstlane(id);
-        const uint16_t* src = kvpool + ((size_t)blk * KV + kv) * 2 * KV_TILE;
-        uint4* dst = attn_ring + (bi % NS) * ATTN_STAGE;
+        const int half = (c * CHUNK % BLOCK_TOKENS) / 32;
+        const uint16_t* src = kvpool + ((size_t)blk * KV + kv) * 2 * TILE_ELEMS;
+        uint4* dst = attn_ring + (ci % NS) * ATTN_STAGE;
 #pragma unroll
-        for (int j = 0; j < LOADS; ++j) load_to_lds(src + (size_t)(w * LOADS + j) * 512 + lane * 8, dst + (w * LOADS + j) * 64);
+        for (int j = 0; j < LOADS; ++j) {
+            const int f = w * LOADS + j;  // the stage's fragment
+            const int from = f < KF ? half * KF + f : TILE_ELEMS / 512 + ((f - KF) / KS) * 2 + half + (f - KF) % KS;
+            load_to_lds(src + (size_t)from * 512 + lane * 8, dst + f * 64);
+        }
     };
 
-    LazySoftmax sm[CG];
-    // The wave's first position: blocks wholly at or below it need no mask.
+    LazySoftmax<PT, DT> sm[CG];
+    // The wave's first position: chunks wholly at or below it need no mask.
     const uint32_t first = tile.pos0 + w * TOK;
-    // Blocks 0 .. nfull - 1 need no mask: they end at or before the wave's first position and the
+    // Chunks 0 .. nfull - 1 need no mask: they end at or before the wave's first position and the
     // tile's last (a wave past the tile's count has a first position past its last).
-    const int nfull = (int)((min(first, last) + 1) / BLOCK_TOKENS);
+    const int nfull = (int)((min(first, last) + 1) / CHUNK);
 
-    // The ring: block bi's keys are in registers when step bi starts. Its values are read from
-    // LDS while the score MFMAs run; then block bi + 1's stage is waited for (the barrier also says
-    // every wave is done with stage bi - 1, which block bi + NS - 1 takes) and, once the softmax has
-    // read every score, its keys read while the exponentials and the value MFMAs of block bi run.
-    // Fragment i of a tile is 1 KiB i on, lane l's 16 bytes 16 l on: its LDS address is the lane's
+    // The ring: chunk ci's keys are in registers when step ci starts. Its values are read from
+    // LDS while the score MFMAs run; then chunk ci + 1's stage is waited for (the barrier also says
+    // every wave is done with stage ci - 1, which chunk ci + NS - 1 takes) and, once the softmax has
+    // read every score, its keys read while the exponentials and the value MFMAs of chunk ci run.
+    // Fragment i of a stage is 1 KiB i on, lane l's 16 bytes 16 l on: its LDS address is the lane's
     // base plus a constant.
     constexpr int STAGE_BYTES = ATTN_STAGE * 16;
-    constexpr int VALUES = KV_TILE * 2;  // the value tile's bytes from the stage's start
+    constexpr int VALUES = KF * 1024;  // the values' bytes from the stage's start
     const uint32_t ring0 = lds_offset(attn_ring) + lane * 16;
 #pragma unroll
-    for (int bi = 0; bi < NS - 1; ++bi) fetch(bi);
+    for (int ci = 0; ci < NS - 1; ++ci) fetch(ci);
     wait_vm<LOADS * (NS - 2)>();
     stage_barrier();
-    uint4 kf[8], vf[8];
+    uint4 kf[KF], vf[VF];
     lds_read16_x8<0, 1024>(ring0, kf);
     lds_landed(kf);
-    // Step bi, its softmax half as MASK (keys past a column's position count for nothing, and the
-    // values past the tile's last position read as zero) and FIRST (block 0). Past the last block
+    // Step ci, its softmax half as MASK (keys past a column's position count for nothing, and the
+    // values past the tile's last position read as zero) and FIRST (chunk 0). Past the last chunk
     // the keys of a stage the ring has already waited for are read and never used.
-    auto step = [&](int bi, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
+    auto step = [&](int ci, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value, FIRST = decltype(first_tag)::value;
-        lds_read16_x8<VALUES, 1024>(ring0 + (uint32_t)(bi % NS) * STAGE_BYTES, vf);
-        // The first halves of every tile's product before any second half: the MFMAs a tile's
-        // second half waits on are done by the time it issues.
-        f32x4 s[CG][4];
+        lds_read16_x8<VALUES, 1024>(ring0 + (uint32_t)(ci % NS) * STAGE_BYTES, vf);
+        // The first k-block of every tile's product before any later one: the MFMAs a tile's
+        // next k-block waits on are done by the time it issues.
+        f32x4 s[CG][PT];
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) s[cg][pt] = mfma16(kf[pt * 2], qf[cg][0], sm[cg].neg_r);
+            for (int pt = 0; pt < PT; ++pt) s[cg][pt] = mfma16(kf[pt * DS], qf[cg][0], sm[cg].neg_r);
 #pragma unroll
-        for (int cg = 0; cg < CG; ++cg)
+        for (int ds = 1; ds < DS; ++ds)
 #pragma unroll
-            for (int pt = 0; pt < 4; ++pt) s[cg][pt] = mfma16(kf[pt * 2 + 1], qf[cg][1], s[cg][pt]);
-        // Stage bi + 1 landed for every wave: no more than the NS - 3 blocks fetched after it in
+            for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) s[cg][pt] = mfma16(kf[pt * DS + ds], qf[cg][ds], s[cg][pt]);
+        // Stage ci + 1 landed for every wave: no more than the NS - 3 chunks fetched after it in
         // flight for this one, then the barrier.
         wait_vm<LOADS * (NS - 3)>();
         stage_barrier();
-        fetch(bi + NS - 1);  // its id's LDS read waits for every LDS read before it: vf has landed
+        fetch(ci + NS - 1);  // its id's LDS read waits for every LDS read before it: vf has landed
         lds_arrived(vf);
-        const uint32_t p0 = (uint32_t)bi * BLOCK_TOKENS;
+        const uint32_t p0 = (uint32_t)ci * CHUNK;
         float mx[CG];
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) mx[cg] = sm[cg].template peak<MASK>(s[cg], p0, cpos[cg]);
@@ -821,13 +844,13 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         // maxima, whose reads of every score wait for every score MFMA to finish.
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) asm volatile("" ::"v"(mx[cg]));
-        lds_read16_x8<0, 1024>(ring0 + (uint32_t)((bi + 1) % NS) * STAGE_BYTES, kf);
+        lds_read16_x8<0, 1024>(ring0 + (uint32_t)((ci + 1) % NS) * STAGE_BYTES, kf);
         // Values past the tile's last position read as zero (attention_rows.comp:1-13): every
         // position up to it was written by this run or before it; the cache may hold anything
-        // past it, NaN included, and 0 NaN is NaN. A block with no mask ends at or before the
+        // past it, NaN included, and 0 NaN is NaN. A chunk with no mask ends at or before the
         // tile's last position.
-        if (MASK && p0 + BLOCK_TOKENS - 1 > last) zero_values_past(vf, p0, last);
-        // One check for the wave's column groups (the rescale is rare past block 0), so that the
+        if (MASK && p0 + CHUNK - 1 > last) zero_values_past<KS, DT>(vf, p0, last);
+        // One check for the wave's column groups (the rescale is rare past chunk 0), so that the
         // exponentials and value MFMAs below are one stretch of code: the compiler runs a group's
         // exponentials beside the previous group's MFMAs (the SIMD runs a wave's VALU work beside
         // its own MFMAs, not beside another wave's).
@@ -840,8 +863,8 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         }
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
-            uint4 pf[2];
-            LazySoftmax::probs(s[cg], pf);
+            uint4 pf[KS];
+            LazySoftmax<PT, DT>::probs(s[cg], pf);
             sm[cg].accumulate(pf, vf);
         }
         lds_landed(kf);
@@ -852,9 +875,9 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         step(0, no{}, yes{});
     else
         step(0, yes{}, yes{});
-    int bi = 1;
-    for (; bi < nfull; ++bi) step(bi, no{}, no{});
-    for (; bi < blocks; ++bi) step(bi, yes{}, no{});
+    int ci = 1;
+    for (; ci < nfull; ++ci) step(ci, no{}, no{});
+    for (; ci < chunks; ++ci) step(ci, yes{}, no{});
     // No load into this workgroup's LDS may still be in flight when its waves end.
     wait_vm<0>();
 #pragma unroll
@@ -865,11 +888,11 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         const size_t row = tile.row0 + tok;
         const float inv = 1.0f / sm[cg].lsum[0];
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
+        for (int dt = 0; dt < DT; ++dt) {
             const int d = dt * 16 + (lane / 16) * 4;
             const f32x4 o = sm[cg].o[dt];
             uint2 packed = make_uint2(pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv));
-            *reinterpret_cast<uint2*>(attended + act_index((int)row, head * HEAD_DIM + d, H * HEAD_DIM)) = packed;
+            *reinterpret_cast<uint2*>(attended + act_index((int)row, head * D + d, H * D)) = packed;
         }
     }
 }
@@ -880,10 +903,33 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
 // beats one 256-row workgroup to a CU for every projection (gate/up by a tenth).
 constexpr int QKV_TM = 128, O_TM = 128, GATE_UP_TM = 128, DOWN_TM = 128;
 
-template <int EPI, int WR, int TM>
+template <int EPI, int WR, int TM, int D = HEAD_DIM>
 void gemm(const char* label, const PrefillArgs& a, const GemmArgs& g, hipStream_t stream, DispatchTimer* timer) {
-    dispatch(label, prefill_gemm<EPI, WR, TM>, dim3(g.N / TN, a.M_pad / TM), dim3(GemmTile<TM>::THREADS), GemmTile<TM>::LDS,
+    dispatch(label, prefill_gemm<EPI, WR, TM, D>, dim3(g.N / TN, a.M_pad / TM), dim3(GemmTile<TM>::THREADS), GemmTile<TM>::LDS,
              stream, timer, a, g);
+}
+
+// The attention's instance for `group` query heads to a KV head and heads of D dimensions.
+template <int D>
+hipError_t attention(const PrefillArgs& a, const PrefillBuffers& b, const uint16_t* kv, size_t lds, hipStream_t stream,
+                     DispatchTimer* timer) {
+    const dim3 grid(b.ntiles, a.kv_heads);
+    const uint16_t* q = b.q;
+    switch (a.heads / a.kv_heads) {
+        case 1: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 2, 1, D>, grid, dim3(2 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles); break;
+        case 2: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 4, 1, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles); break;
+        case 4: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles); break;
+        // 8 heads: at D 64 four waves of two column groups; at D 128 eight waves of one (two
+        // groups' outputs and scores would hold more than a wave's registers).
+        case 8:
+            if constexpr (D == 64)
+                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 4, 2, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles);
+            else
+                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipSuccess;
 }
 
 hipError_t allow(const void* kernel, size_t device_lds) {
@@ -946,23 +992,25 @@ int prefill_attention_tile(int group) { return group == 8 ? ATTN_TILE_8 : ATTN_T
 
 hipError_t prefill_prepare(size_t device_lds) {
     hipError_t e;
-    if ((e = allow((const void*)prefill_gemm<EPI_QKV, QKV_ROWS, QKV_TM>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_QKV, QKV_ROWS, QKV_TM, 64>, device_lds)) != hipSuccess) return e;
+    if ((e = allow((const void*)prefill_gemm<EPI_QKV, QKV_ROWS, QKV_TM, 128>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL_IN, 4, O_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL_IN, 16, O_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 4, DOWN_TM>, device_lds)) != hipSuccess) return e;
     if ((e = allow((const void*)prefill_gemm<EPI_RESIDUAL, 16, DOWN_TM>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_attention<ATTN_TILE, 2, 1>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_attention<ATTN_TILE, 4, 1>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_attention<ATTN_TILE, 8, 1>, device_lds)) != hipSuccess) return e;
-    if ((e = allow((const void*)prefill_attention<ATTN_TILE_8, 4, 2>, device_lds)) != hipSuccess) return e;
+    for (const void* f : {(const void*)prefill_attention<ATTN_TILE, 2, 1, 64>, (const void*)prefill_attention<ATTN_TILE, 4, 1, 64>,
+                          (const void*)prefill_attention<ATTN_TILE, 8, 1, 64>, (const void*)prefill_attention<ATTN_TILE_8, 4, 2, 64>,
+                          (const void*)prefill_attention<ATTN_TILE, 2, 1, 128>, (const void*)prefill_attention<ATTN_TILE, 4, 1, 128>,
+                          (const void*)prefill_attention<ATTN_TILE, 8, 1, 128>, (const void*)prefill_attention<ATTN_TILE_8, 8, 1, 128>})
+        if ((e = allow(f, device_lds)) != hipSuccess) return e;
     return allow((const void*)prefill_gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>, device_lds);
 }
 
 hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int nlayers, const float* final_norm,
                           const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer) {
     const dim3 rows4((a.M_pad + 3) / 4);
-    const int group = a.heads / a.kv_heads;
-    const int qkv_rows = (a.heads + 2 * a.kv_heads) * HEAD_DIM;
+    if (a.head_dim != 64 && a.head_dim != 128) return hipErrorInvalidValue;
+    const int qkv_rows = (a.heads + 2 * a.kv_heads) * a.head_dim;
     // The attention's ring and the slot's block ids.
     const size_t attn_lds = (size_t)ATTN_STAGES * ATTN_STAGE * sizeof(uint4) + (size_t)a.max_blocks * sizeof(uint32_t);
     // Layer 0's input norm; each later norm's input (the rows times the gain, and their sums of
@@ -975,16 +1023,17 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
         const PrefillLayer& L = layers[l];
         GemmArgs qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, nullptr, b.q, L.kv,
                      l == 0 ? nullptr : b.row_sq, nullptr, nullptr, nullptr};
-        gemm<EPI_QKV, QKV_ROWS, QKV_TM>("prefill_qkv", a, qkv, stream, timer);
-        switch (group) {
-            case 1: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 2, 1>, dim3(b.ntiles, a.kv_heads), dim3(2 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 2: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 4, 1>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 4: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 8, 1>, dim3(b.ntiles, a.kv_heads), dim3(8 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            case 8: dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 4, 2>, dim3(b.ntiles, a.kv_heads), dim3(4 * WAVE), attn_lds, stream, timer, a, (const uint16_t*)b.q, (const uint16_t*)L.kv, b.attended, b.tiles); break;
-            default: return hipErrorInvalidValue;
+        hipError_t e;
+        if (a.head_dim == 128) {
+            gemm<EPI_QKV, QKV_ROWS, QKV_TM, 128>("prefill_qkv", a, qkv, stream, timer);
+            e = attention<128>(a, b, L.kv, attn_lds, stream, timer);
+        } else {
+            gemm<EPI_QKV, QKV_ROWS, QKV_TM, 64>("prefill_qkv", a, qkv, stream, timer);
+            e = attention<64>(a, b, L.kv, attn_lds, stream, timer);
         }
+        if (e != hipSuccess) return e;
         if (L.od_rows != 4 && L.od_rows != 16) return hipErrorInvalidValue;
-        GemmArgs o{L.o, b.attended, a.heads * HEAD_DIM, a.hidden, input, b.mid, nullptr, nullptr, nullptr,
+        GemmArgs o{L.o, b.attended, a.heads * a.head_dim, a.hidden, input, b.mid, nullptr, nullptr, nullptr,
                    nullptr, L.post_norm, b.normed, b.row_sq};
         if (L.od_rows == 4)
             gemm<EPI_RESIDUAL_IN, 4, O_TM>("prefill_o", a, o, stream, timer);

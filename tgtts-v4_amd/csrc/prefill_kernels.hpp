@@ -19,6 +19,7 @@ struct PrefillArgs {
     int M;        // rows (positions over every run)
     int M_pad;    // rows the tensors hold, a multiple of 256
     int hidden, inner, heads, kv_heads;
+    int head_dim;  // 64 or 128
     int capacity, nslots, max_blocks, nblocks;
     float eps, scale;
     int rope;
@@ -47,8 +48,8 @@ struct PrefillBuffers {
     float* h;           // residual stream, f32 [M_pad][hidden]
     float* mid;         // after the attention, f32
     uint16_t* normed;   // RMSNorm of the stream, bf16 [M_pad][hidden] in fragment order (act_index)
-    uint16_t* q;        // bf16 [M_pad][heads][64], times scale log2(e) (the attention softmax's units)
-    uint16_t* attended; // bf16 [M_pad][heads 64] in fragment order
+    uint16_t* q;        // bf16 [M_pad][heads][head_dim], times scale log2(e) (the attention softmax's units)
+    uint16_t* attended; // bf16 [M_pad][heads head_dim] in fragment order
     uint16_t* mlp;      // bf16 [M_pad][inner] in fragment order
     float* row_sq;      // a norm's input's sums of squares over each 128 columns, [M_pad][hidden / 128]
     float* out;         // after the final norm, f32 [M_pad][hidden]

@@ -48,7 +48,7 @@ tgx_status check_prompt(const PromptView& pr) {
 bool busy(const Prompter* p) { return p->step->pending || p->step->side->pending || p->step->encoder->pending; }
 
 // A cache block of one layer: every KV head's key tile and value tile of 64 positions.
-size_t block_elems(const Decoder* d) { return (size_t)d->shape.kv_heads * 2 * KV_TILE; }
+size_t block_elems(const Decoder* d) { return (size_t)d->shape.kv_heads * 2 * kv_tile(d->shape.head_dim); }
 uint16_t* kv_block(Decoder* d, int layer, uint32_t block) {
     return d->kv + ((size_t)layer * d->nblocks + block) * block_elems(d);
 }

@@ -4,12 +4,15 @@
 // HIP graph is the MI355X counterpart).
 #include "runtime.hpp"
 
+#include "heads_kernels.hpp"
+
 #include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstring>
 #include <functional>
 #include <thread>
+#include <tuple>
 
 namespace tgx {
 
@@ -114,6 +117,7 @@ tgx_status context_create(int device, Context** out) {
     ctx->lds_bytes = ctx->prop.sharedMemPerBlock;
     e = decode_prepare(ctx->lds_bytes);
     if (e == hipSuccess) e = prefill_prepare(ctx->lds_bytes);
+    if (e == hipSuccess) e = heads_prepare(ctx->lds_bytes);
     // The device is current: the prefill scratch's address on it, kept for the process.
     if (e == hipSuccess) e = prefill_scratch_address(device, &ctx->scratch);
     if (e != hipSuccess) {
@@ -156,18 +160,24 @@ tgx_status check_shape(const tgx_shape* in, Shape* s) {
     s->rope = in->rope != 0;
     s->factors.clear();
     if (in->rope_factors) s->factors.assign(in->rope_factors, in->rope_factors + in->head_dim / 2);
-    if (s->head_dim != HEAD_DIM) return refuse("head_dim " + std::to_string(s->head_dim) + ": the kernels take 64");
+    // Head widths 64 (the backbone's) and 128 (VoxCPM2's LMs, decode.rs:919-933).
+    if (s->head_dim != 64 && s->head_dim != 128)
+        return refuse("head_dim " + std::to_string(s->head_dim) + ": the kernels take 64 or 128");
     if (s->layers < 0 || s->capacity <= 0) return refuse("layers " + std::to_string(s->layers) + ", capacity " + std::to_string(s->capacity));
-    if (s->capacity > decode_max_capacity())
-        return refuse("capacity " + std::to_string(s->capacity) + " past the attention's " + std::to_string(decode_max_capacity()));
+    if (s->capacity > decode_max_capacity(s->head_dim))
+        return refuse("capacity " + std::to_string(s->capacity) + " past the attention's " +
+                      std::to_string(decode_max_capacity(s->head_dim)) + " at head_dim " + std::to_string(s->head_dim));
     // Query heads to a KV head: 1, 2, 4 or 8, each with a prefill attention instance whose
     // registers hold its tile (16 heads a KV head would spill beside waits that count loads in
     // issue order, and is refused; the reference takes any group, attention_split.comp:24-27).
     if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 8 || 8 % (s->heads / s->kv_heads) != 0)
         return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) + " KV heads: a group of 1, 2, 4 or 8");
-    // The projections take K in chunks of 1024 columns, up to 4096 (decode_kernels.hip).
-    const int most = decode_max_k();
-    for (auto [what, k] : {std::pair<const char*, int>{"hidden", s->hidden}, {"inner", s->inner}, {"heads x head_dim", s->heads * HEAD_DIM}})
+    // The projections take K in chunks of 1024 columns: hidden (the norms', q/k/v's and gate/up's
+    // K) up to 2048, inner (down_proj's) and heads x head_dim (o_proj's) up to 6144
+    // (decode_kernels.hip): VoxCPM2's LMs are 2048 wide with an FFN of 6144.
+    for (auto [what, k, most] : {std::tuple<const char*, int, int>{"hidden", s->hidden, decode_max_hidden()},
+                                 {"inner", s->inner, decode_max_k()},
+                                 {"heads x head_dim", s->heads * s->head_dim, decode_max_k()}})
         if (k <= 0 || k % 1024 != 0 || k > most)
             return refuse(std::string(what) + " " + std::to_string(k) + ": a multiple of 1024 up to " + std::to_string(most));
     if (s->inner % 16 != 0 || s->hidden % 16 != 0) return refuse("rows in strips of 16");
@@ -184,7 +194,7 @@ tgx_status check_batch(const Shape& s, const tgx_batch* batch) {
     if (block_tokens != BLOCK_TOKENS)
         return fail(TGX_E_SHAPE, "blocks of " + std::to_string(block_tokens) + " positions: the kernels take 64");
     if (batch->blocks < 0) return fail(TGX_E_SHAPE, "a pool of " + std::to_string(batch->blocks) + " blocks");
-    if (decode_attention_lds(s.heads, s.kv_heads) > 160 * 1024)
+    if (decode_attention_lds(s.heads, s.kv_heads, s.head_dim) > 160 * 1024)
         return fail(TGX_E_SHAPE, "the attention of " + std::to_string(s.heads / s.kv_heads) + " heads to a KV head takes past 160 KiB of LDS");
     return TGX_OK;
 }
@@ -218,6 +228,7 @@ DecodeArgs Decoder::args() const {
     a.inner = shape.inner;
     a.heads = shape.heads;
     a.kv_heads = shape.kv_heads;
+    a.head_dim = shape.head_dim;
     a.rows = rows;
     a.capacity = shape.capacity;
     a.nslots = slots;
@@ -243,7 +254,7 @@ LayerArgs Decoder::layer_args(int l) const {
     la.input_norm = layers[l].input_norm;
     la.qkv = layers[l].qkv;
     la.q = q;
-    la.kv = kv + (size_t)l * nblocks * shape.kv_heads * 2 * KV_TILE;
+    la.kv = kv + (size_t)l * nblocks * shape.kv_heads * 2 * kv_tile(shape.head_dim);
     la.attended = attended;
     la.mid_n = xn_b;
     la.mid_sq = sq_b;
@@ -256,7 +267,7 @@ ResidualArgs Decoder::o_args(int l) const {
     ResidualArgs r{};
     r.w = layers[l].o;
     r.x = attended;
-    r.K = shape.heads * HEAD_DIM;
+    r.K = shape.heads * shape.head_dim;
     r.N = shape.hidden;
     r.R = od_rows;
     r.residual = l == 0 ? x_in : h_a;
@@ -371,7 +382,7 @@ tgx_status use_program(Decoder* d) {
 tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     const Shape& s = d->shape;
     TGX_TRY(check_batch(s, batch));
-    if (decode_attention_lds(s.heads, s.kv_heads) + 4096 > d->ctx->lds_bytes)
+    if (decode_attention_lds(s.heads, s.kv_heads, s.head_dim) + 4096 > d->ctx->lds_bytes)
         return fail(TGX_E_SHAPE, "the attention's LDS is past the device's " + std::to_string(d->ctx->lds_bytes));
     d->rows = batch->rows;
     d->max_rows = batch->rows;
@@ -381,12 +392,12 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     d->max_blocks = (s.capacity + BLOCK_TOKENS - 1) / BLOCK_TOKENS;
     d->nblocks = batch->blocks > 0 ? batch->blocks : d->slots * d->max_blocks;
 
-    const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads;
-    const size_t qkv_rows = (size_t)(H + 2 * KV) * HEAD_DIM;
+    const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads, D = s.head_dim;
+    const size_t qkv_rows = (size_t)(H + 2 * KV) * D;
     d->layers.resize(s.layers);
     for (auto& L : d->layers) {
         TGX_TRY(alloc(d, &L.qkv, qkv_rows * h));
-        TGX_TRY(alloc(d, &L.o, (size_t)h * H * HEAD_DIM));
+        TGX_TRY(alloc(d, &L.o, (size_t)h * H * D));
         TGX_TRY(alloc(d, &L.gate_up, (size_t)2 * I * h));
         TGX_TRY(alloc(d, &L.down, (size_t)h * I));
         TGX_TRY(alloc(d, &L.input_norm, (size_t)h));
@@ -402,16 +413,16 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_TRY(alloc(d, &d->sq_a, (size_t)R * h / 4));
     TGX_TRY(alloc(d, &d->sq_b, (size_t)R * h / 4));
     TGX_TRY(alloc(d, &d->out, (size_t)R * h));
-    TGX_TRY(alloc(d, &d->q, (size_t)R * H * HEAD_DIM));
-    TGX_TRY(alloc(d, &d->attended, (size_t)R * H * HEAD_DIM));
+    TGX_TRY(alloc(d, &d->q, (size_t)R * H * D));
+    TGX_TRY(alloc(d, &d->attended, (size_t)R * H * D));
     TGX_TRY(alloc(d, &d->mlp, (size_t)R * I));
-    TGX_TRY(alloc(d, &d->kv, (size_t)s.layers * d->nblocks * KV * 2 * KV_TILE));
+    TGX_TRY(alloc(d, &d->kv, (size_t)s.layers * d->nblocks * KV * 2 * kv_tile(D)));
     TGX_TRY(alloc(d, &d->positions, (size_t)R));
     TGX_TRY(alloc(d, &d->slot_of_row, (size_t)R));
     TGX_TRY(alloc(d, &d->table, (size_t)d->slots * d->max_blocks));
     TGX_TRY(alloc(d, &d->row_table, (size_t)R * d->max_blocks));
-    TGX_TRY(alloc(d, &d->cos, (size_t)s.capacity * HEAD_DIM / 2));
-    TGX_TRY(alloc(d, &d->sin, (size_t)s.capacity * HEAD_DIM / 2));
+    TGX_TRY(alloc(d, &d->cos, (size_t)s.capacity * D / 2));
+    TGX_TRY(alloc(d, &d->sin, (size_t)s.capacity * D / 2));
     // Norm gains start at one, so that an unloaded stack still runs finite.
     std::vector<float> ones(h, 1.0f);
     for (auto& L : d->layers) {
@@ -595,8 +606,8 @@ std::vector<uint16_t> tile_rows(const std::vector<float>& w, int n, int k, int R
 
 tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, const std::string& what,
                              const void* data, tgx_dtype dtype, size_t count, int o_rows, int down_rows) {
-    const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads;
-    const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
+    const int h = s.hidden, I = s.inner, H = s.heads, KV = s.kv_heads, D = s.head_dim;
+    const int qkv_rows = (H + 2 * KV) * D;
     auto want = [&](size_t expect) -> tgx_status {
         if (count != expect)
             return fail(TGX_E_WEIGHTS, name + ": " + std::to_string(count) + " values, not " + std::to_string(expect));
@@ -614,12 +625,12 @@ tgx_status load_layer_tensor(Layer& L, const Shape& s, const std::string& name, 
     if (what == "qkv_proj") {
         TGX_TRY(want((size_t)qkv_rows * h));
         auto t = tile_rows(as_f32(data, dtype, count), qkv_rows, h, QKV_ROWS,
-                           [](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM, QKV_ROWS); });
+                           [D](int strip, int r) { return qkv_row_of(strip, r, D, QKV_ROWS); });
         return upload(L.qkv, t.data(), t.size() * 2);
     }
     if (what == "o_proj") {
-        TGX_TRY(want((size_t)h * H * HEAD_DIM));
-        auto t = tile_rows(as_f32(data, dtype, count), h, H * HEAD_DIM, o_rows, [o_rows](int strip, int r) { return strip * o_rows + r; });
+        TGX_TRY(want((size_t)h * H * D));
+        auto t = tile_rows(as_f32(data, dtype, count), h, H * D, o_rows, [o_rows](int strip, int r) { return strip * o_rows + r; });
         return upload(L.o, t.data(), t.size() * 2);
     }
     if (what == "gate_up_proj") {
@@ -815,20 +826,20 @@ tgx_status decoder_read_cache(Decoder* d, uint32_t slot, uint32_t positions, flo
     if (slot >= (uint32_t)d->slots || positions > (uint32_t)d->slot_blocks[slot] * BLOCK_TOKENS)
         return fail(TGX_E_SHAPE, "slot " + std::to_string(slot) + " holds fewer than " + std::to_string(positions) + " positions");
     const Shape& s = d->shape;
-    const int KV = s.kv_heads;
-    std::vector<uint16_t> tilebuf(2 * KV_TILE);
+    const int KV = s.kv_heads, D = s.head_dim, TILE = kv_tile(D);
+    std::vector<uint16_t> tilebuf(2 * TILE);
     TGX_HIP(hipStreamSynchronize(d->ctx->stream));
     for (int l = 0; l < s.layers; ++l)
         for (int kv = 0; kv < KV; ++kv)
             for (uint32_t p0 = 0; p0 < positions; p0 += BLOCK_TOKENS) {
                 const uint32_t blk = d->table_host[(size_t)slot * d->max_blocks + p0 / BLOCK_TOKENS];
-                const uint16_t* src = d->kv + (((size_t)l * d->nblocks + blk) * KV + kv) * 2 * KV_TILE;
-                TGX_HIP(hipMemcpy(tilebuf.data(), src, 2 * KV_TILE * 2, hipMemcpyDeviceToHost));
+                const uint16_t* src = d->kv + (((size_t)l * d->nblocks + blk) * KV + kv) * 2 * TILE;
+                TGX_HIP(hipMemcpy(tilebuf.data(), src, 2 * TILE * 2, hipMemcpyDeviceToHost));
                 for (uint32_t p = p0; p < positions && p < p0 + BLOCK_TOKENS; ++p)
-                    for (int dd = 0; dd < HEAD_DIM; ++dd) {
-                        const size_t at = (((size_t)l * KV + kv) * positions + p) * HEAD_DIM + dd;
-                        k[at] = bf16_to_f32(tilebuf[key_index((int)(p - p0), dd)]);
-                        v[at] = bf16_to_f32(tilebuf[KV_TILE + value_index((int)(p - p0), dd)]);
+                    for (int dd = 0; dd < D; ++dd) {
+                        const size_t at = (((size_t)l * KV + kv) * positions + p) * D + dd;
+                        k[at] = bf16_to_f32(tilebuf[key_index((int)(p - p0), dd, D)]);
+                        v[at] = bf16_to_f32(tilebuf[TILE + value_index((int)(p - p0), dd)]);
                     }
             }
     return TGX_OK;

@@ -80,10 +80,10 @@ float as_float(uint32_t bits) {
 
 // The constants every decode kernel takes first, in order.
 constexpr int C_HIDDEN = 0, C_INNER = 1, C_HEADS = 2, C_KV = 3, C_ROWS = 4, C_CAPACITY = 5, C_SLOTS = 6, C_MAX_BLOCKS = 7,
-              C_BLOCKS = 8, C_EPS = 9, C_ROPE = 10, C_COMMON = 11;
+              C_BLOCKS = 8, C_EPS = 9, C_ROPE = 10, C_HEAD_DIM = 11, C_COMMON = 12;
 std::vector<const char*> decode_constants(std::vector<const char*> own = {}) {
     std::vector<const char*> c = {"hidden", "inner", "heads", "kv_heads", "rows", "capacity", "slots", "max_blocks", "blocks",
-                                  "eps", "rope"};
+                                  "eps", "rope", "head_dim"};
     c.insert(c.end(), own.begin(), own.end());
     return c;
 }
@@ -96,7 +96,7 @@ tgx_status decode_args(const uint32_t* c, DecodeArgs* a) {
     in.inner = (int)c[C_INNER];
     in.heads = (int)c[C_HEADS];
     in.kv_heads = (int)c[C_KV];
-    in.head_dim = HEAD_DIM;
+    in.head_dim = (int)c[C_HEAD_DIM];
     in.layers = 1;
     in.capacity = (int)c[C_CAPACITY];
     in.eps = as_float(c[C_EPS]);
@@ -119,13 +119,14 @@ tgx_status decode_args(const uint32_t* c, DecodeArgs* a) {
     a->inner = s.inner;
     a->heads = s.heads;
     a->kv_heads = s.kv_heads;
+    a->head_dim = s.head_dim;
     a->rows = (int)c[C_ROWS];
     a->capacity = s.capacity;
     a->nslots = (int)c[C_SLOTS];
     a->max_blocks = (int)c[C_MAX_BLOCKS];
     a->nblocks = (int)c[C_BLOCKS];
     a->eps = s.eps;
-    a->scale = 1.0f / std::sqrt((float)HEAD_DIM);
+    a->scale = 1.0f / std::sqrt((float)s.head_dim);
     a->rope = (int)c[C_ROPE];
     return TGX_OK;
 }
@@ -138,8 +139,8 @@ tgx_status holds(const Bound* b, int i, const char* what, uint64_t need) {
     return TGX_OK;
 }
 
-uint64_t pool_bytes(const DecodeArgs& a) { return (uint64_t)a.nblocks * a.kv_heads * 2 * KV_TILE * 2; }
-uint64_t qkv_rows(const DecodeArgs& a) { return (uint64_t)(a.heads + 2 * a.kv_heads) * HEAD_DIM; }
+uint64_t pool_bytes(const DecodeArgs& a) { return (uint64_t)a.nblocks * a.kv_heads * 2 * kv_tile(a.head_dim) * 2; }
+uint64_t qkv_rows(const DecodeArgs& a) { return (uint64_t)(a.heads + 2 * a.kv_heads) * a.head_dim; }
 
 // gemv_qkv_rope (gemv_qkv_rope.comp): x | (xn, x_sq), gain, W, cos, sin, positions, slots, table
 // -> q, cache pool.
@@ -158,12 +159,12 @@ tgx_status build_qkv(const Bound* b, const uint32_t* c, Launch* L) {
     }
     TGX_TRY(holds(b, 3, "gain", h * 4));
     TGX_TRY(holds(b, 4, "w", qkv_rows(a) * h * 2));
-    TGX_TRY(holds(b, 5, "cos", (uint64_t)a.capacity * (HEAD_DIM / 2) * 4));
-    TGX_TRY(holds(b, 6, "sin", (uint64_t)a.capacity * (HEAD_DIM / 2) * 4));
+    TGX_TRY(holds(b, 5, "cos", (uint64_t)a.capacity * (a.head_dim / 2) * 4));
+    TGX_TRY(holds(b, 6, "sin", (uint64_t)a.capacity * (a.head_dim / 2) * 4));
     TGX_TRY(holds(b, 7, "positions", R * 4));
     TGX_TRY(holds(b, 8, "slots", R * 4));
     TGX_TRY(holds(b, 9, "table", (uint64_t)a.nslots * a.max_blocks * 4));
-    TGX_TRY(holds(b, 10, "q", R * a.heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 10, "q", R * a.heads * a.head_dim * 2));
     TGX_TRY(holds(b, 11, "kv", pool_bytes(a)));
     a.positions = (const uint32_t*)b[7].ptr;
     a.slots = (const uint32_t*)b[8].ptr;
@@ -192,11 +193,11 @@ tgx_status build_attention(const Bound* b, const uint32_t* c, Launch* L) {
     DecodeArgs a;
     TGX_TRY(decode_args(c, &a));
     const uint64_t R = a.rows;
-    TGX_TRY(holds(b, 0, "q", R * a.heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 0, "q", R * a.heads * a.head_dim * 2));
     TGX_TRY(holds(b, 1, "kv", pool_bytes(a)));
     TGX_TRY(holds(b, 2, "positions", R * 4));
     TGX_TRY(holds(b, 3, "row_table", R * a.max_blocks * 4));
-    TGX_TRY(holds(b, 4, "attended", R * a.heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 4, "attended", R * a.heads * a.head_dim * 2));
     a.positions = (const uint32_t*)b[2].ptr;
     a.row_table = (const uint32_t*)b[3].ptr;
     LayerArgs l{};
@@ -373,10 +374,12 @@ const KernelDesc* kernel_at(int i) { return i >= 0 && i < (int)kernels().size() 
 
 // What the weights' tiles take: strips of 16 (or 4) rows, 32 columns a k-block.
 int tile_height(tgx_tiles t) { return t == TGX_TILES_4 ? 4 : 16; }
+// The head width of q/k/v rows in tiles of `t`: 64 or 128, 0 for rows of no heads.
+int tiles_head_dim(tgx_tiles t) { return t == TGX_TILES_QKV ? 64 : t == TGX_TILES_QKV128 ? 128 : 0; }
 bool tiles_hold(tgx_tiles t, int rows, int cols) {
-    if (t != TGX_TILES_16 && t != TGX_TILES_4 && t != TGX_TILES_QKV) return false;
+    if (t != TGX_TILES_16 && t != TGX_TILES_4 && t != TGX_TILES_QKV && t != TGX_TILES_QKV128) return false;
     if (rows <= 0 || cols <= 0 || rows % tile_height(t) != 0 || cols % 32 != 0) return false;
-    if (t == TGX_TILES_QKV && rows % HEAD_DIM != 0) return false;
+    if (tiles_head_dim(t) && rows % tiles_head_dim(t) != 0) return false;
     return (uint64_t)rows * cols <= (1ull << 31);
 }
 
@@ -503,12 +506,13 @@ tgx_status tgx_write_tiles(tgx_memory* mem, uint64_t offset, const void* src, tg
     if (!tiles_hold(tiles, rows, cols))
         return fail(TGX_E_SHAPE, std::to_string(rows) + " x " + std::to_string(cols) + " in tiles of " +
                                      std::to_string(tile_height(tiles)) + "-row strips and 32-column k-blocks" +
-                                     (tiles == TGX_TILES_QKV ? " (rows a multiple of 64)" : ""));
-    const int R = tile_height(tiles);
+                                     (tiles_head_dim(tiles) ? " (rows a multiple of " + std::to_string(tiles_head_dim(tiles)) + ")"
+                                                            : std::string()));
+    const int R = tile_height(tiles), D = tiles_head_dim(tiles);
     std::vector<uint16_t> t;
-    if (tiles == TGX_TILES_QKV)
+    if (D)
         t = tile_rows(as_f32(src, dtype, (size_t)rows * cols), rows, cols, R,
-                      [](int strip, int r) { return qkv_row_of(strip, r, HEAD_DIM, QKV_ROWS); });
+                      [D](int strip, int r) { return qkv_row_of(strip, r, D, QKV_ROWS); });
     else
         t = tile_rows(as_f32(src, dtype, (size_t)rows * cols), rows, cols, R, [R](int strip, int r) { return strip * R + r; });
     return tgx_write(mem, offset, t.data(), (uint64_t)t.size() * 2);

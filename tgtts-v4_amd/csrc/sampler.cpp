@@ -130,6 +130,8 @@ tgx_status sampler_create(Context* ctx, const tgx_shape* stack, const tgx_patch_
     if (C < 16 || C % 16 || C > 64)
         return shape_fail(std::to_string(C) + " channels of " + std::to_string(F) + " frames (16, 32, 48 or 64)");
     if (s.hidden != 1024) return shape_fail("a stack " + std::to_string(s.hidden) + " wide (the kernels take 1024)");
+    // The local stacks' heads are 64 wide (VoxCPM2's encoder and DiT: 1024 wide over 16 heads).
+    if (s.head_dim != HEAD_DIM) return shape_fail("a local stack of head_dim " + std::to_string(s.head_dim) + " (the kernels take 64)");
     // local_attention: a sequence's tokens as one MFMA tile, its query heads 4 to a workgroup.
     if (T > LOCAL_MAX_T || H % 4)
         return shape_fail(std::to_string(T) + " tokens of " + std::to_string(H) + " heads over " + std::to_string(KV));

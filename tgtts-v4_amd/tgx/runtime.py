@@ -18,7 +18,7 @@ from . import F16, F32, BF16, Shape, TgxError, _check, _opened, _ptr, _shape_str
 U32 = 3
 DEVICE, UPLOAD, READBACK = 0, 1, 2
 READ, WRITE = 0, 1
-TILES_16, TILES_4, TILES_QKV = 0, 1, 2
+TILES_16, TILES_4, TILES_QKV, TILES_QKV128 = 0, 1, 2, 3
 
 _DTYPES = {np.dtype(np.float32): F32, np.dtype(np.float16): F16}
 
@@ -282,5 +282,5 @@ def copy_regions(ctx, dst: Memory, src: Memory, regions: Sequence[tuple]) -> Non
 
 __all__ = [
     "BindingInfo", "KernelInfo", "Memory", "Program", "copy_regions", "f32_bits", "kernel", "kernels", "rope_tables",
-    "tiles_bytes", "DEVICE", "UPLOAD", "READBACK", "READ", "WRITE", "TILES_16", "TILES_4", "TILES_QKV", "U32", "TgxError",
+    "tiles_bytes", "DEVICE", "UPLOAD", "READBACK", "READ", "WRITE", "TILES_16", "TILES_4", "TILES_QKV", "TILES_QKV128", "U32", "TgxError",
 ]
