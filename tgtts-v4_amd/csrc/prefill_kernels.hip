@@ -272,15 +272,16 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
     //  AHEAD: past the barrier, stage st + NBUF into the buffer of stage st (read into registers
     //    in the step before, by every wave before this barrier), its loads spread between the
     //    products: NBUF stages in flight. Past the last stage the last is loaded again into a
-    //    buffer no step reads after, and the last step reads the last stage again (never used):
-    //    every step the same, with no branch.
+    //    buffer no step reads after, and the last step reads the buffer of stage st + 1, which
+    //    holds the last stage loaded again two steps before, landed, and which no load of that
+    //    step writes (never used): every step the same, with no branch.
     //  otherwise: before the barrier, stage st + NBUF - 1 into the buffer of stage st - 1, which
     //    every wave had read by the end of step st - 2 (the prologue, for stage 0).
     constexpr bool AHEAD = !residual_epilogue(EPI);
     auto step = [&](int st, uint4 (&cur)[WT + WS], uint4 (&next)[WT + WS]) __attribute__((always_inline)) {
         if constexpr (AHEAD) {
             landed(NBUF - 2);  // stage st + 1
-            read(min(st + 1, stages - 1), next);
+            read(st + 1, next);  // its buffer: (st + 1) % NBUF
 #pragma unroll
             for (int s = 0; s < WS; ++s)
 #pragma unroll
