@@ -499,6 +499,20 @@ def sampler_profile(rows: int, samples: int) -> int:
     return 0
 
 
+def trace_figure(label: str, workload: str):
+    """The committed kernel trace's average duration of `label` on `workload` (a dispatch-by-dispatch
+    run under rocprofv3, whose interception lengthens a short kernel by ~0.5 us), with the file and
+    commit it comes from; None when none is on record."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    for rec in (data.get(label), data.get(workload.replace(" ", ""), {}).get(label), data.get("prefill_8x2048", {}).get(label)):
+        if isinstance(rec, dict) and rec.get("workload") == workload and rec.get("trace_avg_us"):
+            return {"avg_us": rec["trace_avg_us"], "file": rec.get("trace_file"), "commit": rec.get("commit")}
+    return None
+
+
 def measured_traffic(label: str, workload: str):
     """HBM bytes per launch of `label` measured with rocprofv3's FETCH_SIZE and WRITE_SIZE on the
     same workload, each scaled by the counter's reading of a copy of known size, and where that
@@ -602,7 +616,8 @@ def main() -> int:
             "decode_steps_per_s_after": round(pf["decode_steps_per_s"], 1),
             "roofline": {"bound": "mfma", "kernel": dom[0], "achieved": round(dom[1]["TFLOP_s"], 1),
                          "peak": MFMA_PEAK / 1e12, "unit": "TFLOP/s", "frac": round(dom[1]["TFLOP_s"] * 1e12 / MFMA_PEAK, 4),
-                         "avg_us": round(dom[1]["avg_us"], 2)},
+                         "avg_us": round(dom[1]["avg_us"], 2),
+                         "trace": trace_figure(dom[0], "8 x 2048 prefill")},
             "kernels_us": {k: round(v["avg_us"], 2) for k, v in pf["kernels"].items()},
         }
 
@@ -630,6 +645,7 @@ def main() -> int:
             "traffic_source": traffic_source,
             "bytes_per_launch": k["bytes_per_launch"],
             "avg_us": round(k["avg_us"], 3),
+            "trace": trace_figure(label, f"batch {args.batch}"),
             "of_stream_floor": round(achieved / floor_kernel["GB_s"], 4),
         }
 

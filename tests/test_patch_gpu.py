@@ -425,3 +425,46 @@ def test_a_step_of_fewer_rows_runs_on_the_fewest_program_each_row_as_on_the_larg
     step.close()
     for o in (enc, smp, side):
         o.close()
+
+
+def test_fresh_patch_steps_beside_used_ones_give_a_warm_steps_bits_on_their_first_run(ctx):
+    """The case that once exposed reads of LDS slots before their loads landed (the local ring's
+    waits counting loads in an order the compiler had changed): a patch step made fresh, its
+    encoder, LM side and sampler new beside ones just used and closed, so that its first run meets
+    cold caches. Five fresh sets in turn, 5 rows each: every first run's patches and stop logits,
+    of all 5 rows and of 3 rows alone, bit for bit as a warm step's (the batch-invariance contract,
+    crates/graph/src/decode.rs:8-11, on cold caches); the test stops at the first that differs."""
+    import tgx
+    from tgx.patch import PatchStep
+    from tgx.synth import encoder_weights, sampler_weights
+
+    rows = 5
+    espec, dspec = _encoder_spec(1), _dit_spec(1)
+    ew, dw = encoder_weights(espec, FEAT), sampler_weights(dspec, FEAT)
+    _, _, w = _lm_weights()
+    _, cond, noise, sampling = _inputs(rows, seed=16)
+    at = [tgx.Row(0, r) for r in range(rows)]
+
+    def make():
+        enc, smp, side = _encoder(ctx, rows, espec, ew), _sampler(ctx, rows, dspec, dw), _lm_side(ctx, rows, w)
+        return (enc, smp, side), PatchStep(enc, side, smp)
+
+    def close(parts, step):
+        step.close()
+        for o in parts:
+            o.close()
+
+    parts, step = make()
+    step.run_rows(at, cond, noise, sampling)
+    warm = step.run_rows(at, cond, noise, sampling)
+    close(parts, step)
+    for trial in range(5):
+        parts, step = make()
+        first = step.run_rows(at, cond, noise, sampling)
+        for got, want, what in ((first[0], warm[0], "patches"), (first[1], warm[1], "stop logits")):
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"fresh set {trial}: {what} of its first run"
+        pick = [1, 3, 4]
+        alone = step.run_rows([tgx.Row(0, r) for r in pick], cond[pick], noise[pick], sampling[pick])
+        assert np.array_equal(alone[0].view(np.uint32), warm[0][pick].view(np.uint32)), f"fresh set {trial}: rows {pick}"
+        close(parts, step)
+        print(f"[patch] fresh set {trial}: first run bit for bit as the warm step's", flush=True)
