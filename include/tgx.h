@@ -569,7 +569,15 @@ tgx_status tgx_rope_tables(const tgx_shape* shape, float* cos, float* sin);
  * The decode step's kernels keep the reference's names but for "attention_decode", which does
  * attention_split's and attention_combine's work in one; every decode kernel takes the constants
  * hidden, inner, heads, kv_heads, rows, capacity, slots, max_blocks, blocks, eps (its f32 bits),
- * rope, head_dim (64 or 128), then its own. An optional binding may be left out (memory NULL). */
+ * rope, head_dim (64 or 128), then its own. The prefill's (prefill.rs:32-116: norm_rows,
+ * final_norm_rows, and the GEMMs with the reference's row kernels as epilogues, gemm_rope_rows,
+ * gemm_add_norm_rows, gemm_silu_mul_rows, beside attention_rows) take rows, hidden, inner, heads,
+ * kv_heads, head_dim, capacity, slots, max_blocks, blocks, eps, rope first; the local stacks' and
+ * the sampler's (local/mod.rs:28-113: local_norm, local_qkv_rope, local_attention, local_partial,
+ * local_add_norm, local_final_norm, local_gemm_add_norm, local_gate_up, local_embed, dit_euler)
+ * take tokens, seq_tokens, hidden, inner, heads, kv_heads, eps, rope first; cfm_noise, gemv_linear
+ * (lm_side.rs:28-38, and prompt.rs's linear_rows) and select_rows take their own only. An optional
+ * binding may be left out (memory NULL). */
 typedef enum { TGX_READ = 0, TGX_WRITE = 1 } tgx_access;
 typedef struct {
     char name[24];

@@ -12,7 +12,9 @@ def test_the_kernels_keep_the_reference_names_and_binding_order():
 
     table = {k.name: k for k in rt.kernels()}
     # attention_decode does attention_split's and attention_combine's work in one kernel.
-    assert set(table) == {"gemv_qkv_rope", "attention_decode", "gemv_residual", "gemv_gate_up", "rmsnorm", "stream_read"}
+    decode = {"gemv_qkv_rope", "attention_decode", "gemv_residual", "gemv_gate_up", "rmsnorm", "stream_read"}
+    assert decode <= set(table)
+    table = {k: table[k] for k in decode}
     names = lambda k: [b.name for b in table[k].bindings]
     # The reference's bindings keep their relative order (kernels.rs:104-161): x, gain, W, cos,
     # sin, position -> q, cache; x, W, residual -> out; x, gain -> out; data -> out.
@@ -40,6 +42,59 @@ def test_the_kernels_keep_the_reference_names_and_binding_order():
     assert table["gemv_residual"].constants == common + ("K", "N", "strip_rows")
     assert table["rmsnorm"].constants == common + ("advance",)
     assert table["stream_read"].constants == ()
+
+
+PREFILL = ("rows", "hidden", "inner", "heads", "kv_heads", "head_dim", "capacity", "slots", "max_blocks", "blocks", "eps", "rope")
+LOCAL = ("tokens", "seq_tokens", "hidden", "inner", "heads", "kv_heads", "eps", "rope")
+
+# Each kernel past the decode step's: its bindings in order, what it writes, and its constants.
+# The reference declares prefill.rs:32-81 (norm_rows, add_norm_rows, rope_rows, attention_rows,
+# silu_mul_rows beside its GEMMs), local/mod.rs:28-113 (local_norm .. dit_euler), lm_side.rs:28-38
+# (gemv_linear) and prompt.rs:55-67 (select_rows), reads first and writes after, which these keep.
+# Where a GEMM carries the reference's row kernel as its epilogue the name says both, and the
+# run binding (rows in the reference's run buffer) is a constant here.
+WIDER = {
+    "norm_rows": (["x", "gain", "out"], ["out"], PREFILL),
+    "final_norm_rows": (["x", "gain", "out"], ["out"], PREFILL),
+    "gemm_rope_rows": (["x", "w", "row_sq", "cos", "sin", "positions", "slots", "table", "q", "kv"], ["q", "kv"], PREFILL),
+    "attention_rows": (["q", "kv", "table", "tiles", "attended"], ["attended"], PREFILL + ("tiles",)),
+    "gemm_add_norm_rows": (["x", "w", "residual", "next_gain", "out", "out_n", "out_sq"], ["out", "out_n", "out_sq"],
+                           PREFILL + ("K", "N", "strip_rows", "residual_in")),
+    "gemm_silu_mul_rows": (["x", "w", "row_sq", "mlp"], ["mlp"], PREFILL + ("K", "N")),
+    "local_norm": (["x", "gain", "normed", "row_sq"], ["normed", "row_sq"], LOCAL),
+    "local_qkv_rope": (["x", "w", "row_sq", "cos", "sin", "q", "k", "v"], ["q", "k", "v"], LOCAL),
+    "local_attention": (["q", "k", "v", "attended"], ["attended"], LOCAL),
+    "local_partial": (["x", "w", "partial"], ["partial"], LOCAL + ("K", "N", "parts")),
+    "local_add_norm": (["partial", "residual", "gain", "sum", "normed", "row_sq"], ["sum", "normed", "row_sq"], LOCAL + ("parts",)),
+    "local_final_norm": (["partial", "residual", "gain", "sum", "out"], ["sum", "out"], LOCAL + ("parts",)),
+    "local_gemm_add_norm": (["x", "w", "residual", "next_gain", "sum", "normed", "row_sq"], ["sum", "normed", "row_sq"],
+                            LOCAL + ("K", "N", "parts")),
+    "local_gate_up": (["x", "w", "row_sq", "mlp"], ["mlp"], LOCAL),
+    "local_embed": (["frames", "w", "bias", "tokens", "gain", "x0", "normed", "row_sq"], ["x0", "normed", "row_sq"],
+                    LOCAL + ("patch_rows", "channels", "frames", "first", "copy_at", "copies", "guided", "shared", "seqs")),
+    "cfm_noise": (["noise", "sampling", "state"], ["state"], ("rows", "len")),
+    "dit_euler": (["x", "row_sq", "gain", "w", "bias", "sampling", "state"], ["state"],
+                  LOCAL + ("patch_rows", "channels", "frames", "first", "dt")),
+    "gemv_linear": (["x0", "x1", "w", "bias", "out"], ["out"], ("rows", "K0", "K1", "N", "offset", "stride", "act", "levels")),
+    "select_rows": (["flags", "a", "b", "out"], ["out"], ("rows", "K")),
+}
+
+
+def test_the_prefill_local_stack_dit_and_heads_kernels_are_in_the_table_by_name():
+    import tgx.runtime as rt
+
+    table = {k.name: k for k in rt.kernels()}
+    assert set(table) == set(WIDER) | {"gemv_qkv_rope", "attention_decode", "gemv_residual", "gemv_gate_up", "rmsnorm",
+                                       "stream_read"}
+    for name, (bindings, writes, constants) in WIDER.items():
+        k = table[name]
+        assert [b.name for b in k.bindings] == bindings, name
+        assert [b.name for b in k.bindings if b.access == rt.WRITE] == writes, name
+        # reads first, then writes, as the reference declares them
+        access = [b.access for b in k.bindings]
+        assert access == sorted(access), name
+        assert k.constants == constants, name
+        assert rt.kernel(name).name == name
 
 
 def test_an_unknown_kernel_is_refused():

@@ -35,26 +35,6 @@ namespace tgx {
 
 namespace {
 
-enum LocalEpilogue { LEPI_QKV = 0, LEPI_PARTIAL = 1, LEPI_SILU = 2, LEPI_ADD = 3 };
-
-struct LocalGemm {
-    const uint16_t* w;  // 16-row tiles of [N][K]
-    const uint16_t* x;  // bf16 [M_pad][K]
-    int K, N;
-    float* partial;     // LEPI_PARTIAL: f32 [parts][M_pad][N]
-    uint16_t* mlp;      // LEPI_SILU: bf16 [M_pad][N / 2]
-    uint16_t *q, *k, *v;
-    // LEPI_QKV, LEPI_SILU: X is an RMSNorm's input times its gain; row m's sums of squares
-    // [M_pad][K / LOCAL_SQ_COLS] give the row's scale, applied to its sums.
-    const float* row_sq;
-    // LEPI_ADD (local_gemm_ring): sum = residual + the parts' sums, and with next_gain, the next
-    // norm's input: normed = sum next_gain in bf16 and sum's sums of squares into sum_sq.
-    const float* residual;
-    float* sum;
-    const float* next_gain;
-    uint16_t* normed;
-    float* sum_sq;
-};
 
 // The sums of squares of a row: one to each LOCAL_SQ_COLS columns (16 at hidden 1024), in
 // column order. Each is four sums of 16 columns added as (a + b) + (c + d), each of those four of
@@ -828,22 +808,75 @@ __global__ void __launch_bounds__(256) cfm_noise(const float* __restrict__ noise
 
 }  // namespace
 
+hipError_t launch_local_qkv(const LocalArgs& a, const LocalGemm& g, hipStream_t stream, DispatchTimer* timer) {
+    if (g.K != a.hidden || g.N % 64 || a.M_pad != local_rows_padded(a.M)) return hipErrorInvalidValue;
+    local_gemm<LEPI_QKV, 1, 32>("local_qkv_rope", a, g, g.N / 16, 1, stream, timer);
+    return hipGetLastError();
+}
+
+hipError_t launch_local_attention(const LocalArgs& a, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* attended,
+                                  hipStream_t stream, DispatchTimer* timer) {
+    if (a.T < 1 || a.T > LOCAL_MAX_T || a.M % a.T || a.heads % 4 || a.kv_heads < 1 || a.heads % a.kv_heads) return hipErrorInvalidValue;
+    dispatch("local_attention", local_attention, dim3(a.M / a.T, a.heads / 4), dim3(256), 0, stream, timer, a, q, k, v, attended);
+    return hipGetLastError();
+}
+
+hipError_t launch_local_partial(const LocalArgs& a, const LocalGemm& g, int parts, hipStream_t stream, DispatchTimer* timer) {
+    const int kbp = parts > 0 ? g.K / 32 / parts : 0;
+    if (a.M_pad > 64 || a.M_pad != local_rows_padded(a.M) || parts < 1 || parts > LOCAL_MAX_PARTS || kbp * 32 * parts != g.K ||
+        g.N % 64)
+        return hipErrorInvalidValue;
+    if (kbp == 16)
+        local_gemm<LEPI_PARTIAL, 1, 16>("local_partial", a, g, g.N / 16, parts, stream, timer);
+    else if (kbp == 32)
+        local_gemm<LEPI_PARTIAL, 1, 32>("local_partial", a, g, g.N / 16, parts, stream, timer);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_local_add_norm(const LocalArgs& a, bool final, const float* partial, int parts, const float* residual, float* sum,
+                                 const float* gain, uint16_t* normed, float* row_sq, float* out, hipStream_t stream,
+                                 DispatchTimer* timer) {
+    if (parts < 0 || parts > LOCAL_MAX_PARTS) return hipErrorInvalidValue;
+    const dim3 rows4((a.M + 3) / 4);
+    if (final)
+        dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, partial, parts, residual, sum, gain,
+                 normed, row_sq, out);
+    else
+        dispatch("local_add_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, partial, parts, residual, sum, gain,
+                 normed, row_sq, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_local_add(const LocalArgs& a, const LocalGemm& g, int parts, hipStream_t stream, DispatchTimer* timer) {
+    const int kbp = parts > 0 ? g.K / 32 / parts : 0;
+    if (a.M_pad <= 64 || a.M_pad != local_rows_padded(a.M) || (parts != 2 && parts != 4) || (kbp != 16 && kbp != 32) ||
+        kbp * 32 * parts != g.K || g.N != a.hidden)
+        return hipErrorInvalidValue;
+    local_gemm_add("local_add", a, g, kbp, parts, stream, timer);
+    return hipGetLastError();
+}
+
+hipError_t launch_local_gate_up(const LocalArgs& a, const LocalGemm& g, hipStream_t stream, DispatchTimer* timer) {
+    if (g.K != a.hidden || g.N != 2 * a.inner || a.M_pad != local_rows_padded(a.M)) return hipErrorInvalidValue;
+    local_gemm<LEPI_SILU, 2, 32>("local_gate_up", a, g, a.inner / 16, 1, stream, timer);
+    return hipGetLastError();
+}
+
 hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int nlayers, const float* final_norm,
                               const LocalBuffers& b, hipStream_t stream, DispatchTimer* timer) {
     if (!local_supported(a.hidden, a.inner, a.heads, a.kv_heads, b.o_parts, b.down_parts) || a.M_pad != local_rows_padded(a.M))
         return hipErrorInvalidValue;
-    const dim3 rows4((a.M + 3) / 4);
     const int H = a.heads, KV = a.kv_heads;
     const int qkv_rows = (H + 2 * KV) * HEAD_DIM;
-    const int o_kbp = H * HEAD_DIM / 32 / b.o_parts, down_kbp = a.inner / 32 / b.down_parts;
     // Over more than 64 tokens o_proj and down_proj add their parts and the residual themselves
     // (the ring GEMM); up to 64, their parts go out to `partial` for local_add_norm to add.
     const bool ring = a.M_pad > 64;
+    hipError_t e = hipSuccess;
     // The first layer's input norm, unless the embedding wrote it.
-    if (!b.normed0)
-        dispatch("local_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0, b.x0,
-                 (float*)nullptr, layers[0].input_norm, b.normed, b.row_sq, (float*)nullptr);
-    for (int l = 0; l < nlayers; ++l) {
+    if (!b.normed0) e = launch_local_add_norm(a, false, nullptr, 0, b.x0, nullptr, layers[0].input_norm, b.normed, b.row_sq, nullptr, stream, timer);
+    for (int l = 0; l < nlayers && e == hipSuccess; ++l) {
         const LocalLayer& L = layers[l];
         const bool last = l + 1 == nlayers;
         const float* input = l == 0 ? b.x0 : b.x;
@@ -856,9 +889,8 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
         qkv.k = b.k;
         qkv.v = b.v;
         qkv.row_sq = l == 0 && b.normed0 ? b.row_sq0 : b.row_sq;
-        local_gemm<LEPI_QKV, 1, 32>("local_qkv_rope", a, qkv, qkv_rows / 16, 1, stream, timer);
-        dispatch("local_attention", local_attention, dim3(a.M / a.T, H / 4), dim3(256), 0, stream, timer, a, (const uint16_t*)b.q,
-                 (const uint16_t*)b.k, (const uint16_t*)b.v, b.attended);
+        e = launch_local_qkv(a, qkv, stream, timer);
+        if (e == hipSuccess) e = launch_local_attention(a, b.q, b.k, b.v, b.attended, stream, timer);
         LocalGemm o{};
         o.w = L.o;
         o.x = b.attended;
@@ -870,15 +902,12 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
             o.next_gain = L.post_norm;
             o.normed = b.normed;
             o.sum_sq = b.row_sq;
-            local_gemm_add("local_o_proj", a, o, o_kbp, b.o_parts, stream, timer);
+            if (e == hipSuccess) e = launch_local_add(a, o, b.o_parts, stream, timer);
         } else {
             o.partial = b.partial;
-            if (o_kbp == 16)
-                local_gemm<LEPI_PARTIAL, 1, 16>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
-            else
-                local_gemm<LEPI_PARTIAL, 1, 32>("local_o_proj", a, o, a.hidden / 16, b.o_parts, stream, timer);
-            dispatch("local_o_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial, b.o_parts,
-                     input, b.h, L.post_norm, b.normed, b.row_sq, (float*)nullptr);
+            if (e == hipSuccess) e = launch_local_partial(a, o, b.o_parts, stream, timer);
+            if (e == hipSuccess)
+                e = launch_local_add_norm(a, false, b.partial, b.o_parts, input, b.h, L.post_norm, b.normed, b.row_sq, nullptr, stream, timer);
         }
         LocalGemm gu{};
         gu.w = L.gate_up;
@@ -887,7 +916,7 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
         gu.N = 2 * a.inner;
         gu.mlp = b.mlp;
         gu.row_sq = b.row_sq;
-        local_gemm<LEPI_SILU, 2, 32>("local_gate_up", a, gu, a.inner / 16, 1, stream, timer);
+        if (e == hipSuccess) e = launch_local_gate_up(a, gu, stream, timer);
         LocalGemm down{};
         down.w = L.down;
         down.x = b.mlp;
@@ -901,25 +930,20 @@ hipError_t launch_local_stack(const LocalArgs& a, const LocalLayer* layers, int 
             down.next_gain = next_gain;
             down.normed = b.normed;
             down.sum_sq = b.row_sq;
-            local_gemm_add("local_down_proj", a, down, down_kbp, b.down_parts, stream, timer);
-            if (last && b.out)
-                dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, (const float*)nullptr, 0,
-                         (const float*)b.x, (float*)nullptr, final_norm, (uint16_t*)nullptr, (float*)nullptr, b.out);
+            if (e == hipSuccess) e = launch_local_add(a, down, b.down_parts, stream, timer);
+            if (e == hipSuccess && last && b.out)
+                e = launch_local_add_norm(a, true, nullptr, 0, b.x, nullptr, final_norm, nullptr, nullptr, b.out, stream, timer);
             continue;
         }
         down.partial = b.partial;
-        if (down_kbp == 16)
-            local_gemm<LEPI_PARTIAL, 1, 16>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
-        else
-            local_gemm<LEPI_PARTIAL, 1, 32>("local_down_proj", a, down, a.hidden / 16, b.down_parts, stream, timer);
+        if (e == hipSuccess) e = launch_local_partial(a, down, b.down_parts, stream, timer);
+        if (e != hipSuccess) break;
         if (next_gain)
-            dispatch("local_down_add", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
-                     b.down_parts, (const float*)b.h, b.x, next_gain, b.normed, b.row_sq, (float*)nullptr);
+            e = launch_local_add_norm(a, false, b.partial, b.down_parts, b.h, b.x, next_gain, b.normed, b.row_sq, nullptr, stream, timer);
         else
-            dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, (const float*)b.partial,
-                     b.down_parts, (const float*)b.h, b.x, final_norm, (uint16_t*)nullptr, (float*)nullptr, b.out);
+            e = launch_local_add_norm(a, true, b.partial, b.down_parts, b.h, b.x, final_norm, nullptr, nullptr, b.out, stream, timer);
     }
-    return hipGetLastError();
+    return e;
 }
 
 int local_stack_dispatches(const LocalArgs& a, const LocalBuffers& b, int nlayers) {

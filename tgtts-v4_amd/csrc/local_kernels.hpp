@@ -92,6 +92,45 @@ struct EulerArgs {
     float dt;
 };
 
+// What a local stack's projection writes beside its products (local_gemm_direct, local_gemm_ring):
+// q/k/v with RoPE, the parts of a sum (o_proj and down_proj up to 64 tokens), SiLU(gate) up, or
+// the parts added with the residual and the next norm's input (o_proj and down_proj past 64).
+enum LocalEpilogue { LEPI_QKV = 0, LEPI_PARTIAL = 1, LEPI_SILU = 2, LEPI_ADD = 3 };
+
+// A local projection's operands and its epilogue's tensors.
+struct LocalGemm {
+    const uint16_t* w;  // 16-row tiles of [N][K]
+    const uint16_t* x;  // bf16 [M_pad][K] in fragment order
+    int K, N;
+    float* partial;     // LEPI_PARTIAL: f32 [parts][M_pad][N]
+    uint16_t* mlp;      // LEPI_SILU: bf16 [M_pad][N / 2]
+    uint16_t *q, *k, *v;
+    // LEPI_QKV, LEPI_SILU: X is an RMSNorm's input times its gain; row m's sums of squares
+    // [M_pad][K / LOCAL_SQ_COLS] give the row's scale, applied to its sums.
+    const float* row_sq;
+    // LEPI_ADD (local_gemm_ring): sum = residual + the parts' sums, and with next_gain, the next
+    // norm's input: normed = sum next_gain in bf16 and sum's sums of squares into sum_sq.
+    const float* residual;
+    float* sum;
+    const float* next_gain;
+    uint16_t* normed;
+    float* sum_sq;
+};
+
+// The local stack's kernels one at a time, as launch_local_stack launches them: q/k/v with RoPE
+// (its N the q/k/v rows), the attention within each sequence, o_proj's or down_proj's parts
+// (up to 64 tokens) and their sum with the residual and the next norm's input (or the final norm
+// into `out`), the same fused (past 64 tokens; 2 or 4 parts), and gate/up with SiLU.
+hipError_t launch_local_qkv(const LocalArgs& a, const LocalGemm& g, hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_local_attention(const LocalArgs& a, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* attended,
+                                  hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_local_partial(const LocalArgs& a, const LocalGemm& g, int parts, hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_local_add_norm(const LocalArgs& a, bool final, const float* partial, int parts, const float* residual, float* sum,
+                                 const float* gain, uint16_t* normed, float* row_sq, float* out, hipStream_t stream,
+                                 DispatchTimer* timer);
+hipError_t launch_local_add(const LocalArgs& a, const LocalGemm& g, int parts, hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_local_gate_up(const LocalArgs& a, const LocalGemm& g, hipStream_t stream, DispatchTimer* timer);
+
 // Lets the ring GEMM take its rings of token tiles (up to 66 KiB) in LDS; once per process.
 hipError_t local_prepare();
 // The stacks the kernels take: hidden 1024, query heads a multiple of 4, and o_proj's and

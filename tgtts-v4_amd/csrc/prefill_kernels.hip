@@ -56,37 +56,12 @@ struct GemmTile {
     static_assert(NBUF * FB < 64, "the loads in flight fit the wave's counter");
 };
 
-// EPI_RESIDUAL adds the residual rows to the products in the epilogue; EPI_RESIDUAL_IN starts the
-// accumulators at them (their loads at the start, beside the ring's, where the epilogue would wait
-// for them): for o_proj, whose short K leaves that wait exposed (52 against 61 us a layer at
-// 8 x 2048), not for down_proj, whose long K hides it and which ran 9 us slower so.
-enum Epilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2, EPI_RESIDUAL_IN = 3 };
 __host__ __device__ constexpr bool residual_epilogue(int epi) { return epi == EPI_RESIDUAL || epi == EPI_RESIDUAL_IN; }
 
 constexpr uint32_t TGX_SPARE_POS = 0xffffffffu;
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
-struct GemmArgs {
-    const uint16_t* w;  // tiles of [N][K] in WR-row strips (the kernel's template argument)
-    const uint16_t* x;  // bf16 [M_pad][K] in fragment order (act_index)
-    int K, N;
-    // epilogues
-    const float* residual;  // EPI_RESIDUAL: f32 [M_pad][N]
-    float* out;             // EPI_RESIDUAL: f32 [M_pad][N]
-    uint16_t* mlp;          // EPI_SILU: bf16 [M_pad][N / 2] in fragment order
-    uint16_t* q;            // EPI_QKV
-    uint16_t* kv;           // EPI_QKV: the layer's cache pool
-    // X as an RMSNorm's input times its gain, the rows' scales still to apply (EPI_QKV,
-    // EPI_SILU): row m's sums of squares over each SQ_SPAN columns, [M_pad][K / SQ_SPAN]; null
-    // when X is normed already.
-    const float* row_sq;
-    // EPI_RESIDUAL, when set: out next_gain in bf16 in fragment order into out_n, and out's sums
-    // of squares over each SQ_SPAN columns into out_sq, for the norm that reads out next.
-    const float* next_gain;
-    uint16_t* out_n;
-    float* out_sq;
-};
 
 // The columns a sum of squares spans: a wave's 128 columns of W.
 constexpr int SQ_SPAN = WS * 16;
@@ -732,6 +707,12 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     extern __shared__ uint4 attn_ring[];
     uint32_t* block_ids = reinterpret_cast<uint32_t*>(attn_ring + NS * ATTN_STAGE);
     const PrefillTile tile = tiles[blockIdx.x];
+    // A tile that leaves the tensors (1 to TILE positions, of a slot of the table, inside the
+    // cache's capacity and the M_pad rows) is skipped by the whole workgroup before any barrier:
+    // the host builds valid ones, and a caller's own tiles in device memory cannot be checked there.
+    if (tile.count == 0 || tile.count > (uint32_t)TILE || tile.slot >= (uint32_t)a.nslots || tile.count > (uint32_t)a.capacity ||
+        tile.pos0 > (uint32_t)a.capacity - tile.count || tile.count > (uint32_t)a.M_pad || tile.row0 > (uint32_t)a.M_pad - tile.count)
+        return;
     const int kv = blockIdx.y;
     // The wave's index, uniform: the branches on it below are the whole wave's.
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -912,21 +893,20 @@ void gemm(const char* label, const PrefillArgs& a, const GemmArgs& g, hipStream_
 
 // The attention's instance for `group` query heads to a KV head and heads of D dimensions.
 template <int D>
-hipError_t attention(const PrefillArgs& a, const PrefillBuffers& b, const uint16_t* kv, size_t lds, hipStream_t stream,
-                     DispatchTimer* timer) {
-    const dim3 grid(b.ntiles, a.kv_heads);
-    const uint16_t* q = b.q;
+hipError_t attention(const PrefillArgs& a, const uint16_t* q, const uint16_t* kv, uint16_t* attended, const PrefillTile* tiles,
+                     int ntiles, size_t lds, hipStream_t stream, DispatchTimer* timer) {
+    const dim3 grid(ntiles, a.kv_heads);
     switch (a.heads / a.kv_heads) {
-        case 1: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 2, 1, D>, grid, dim3(2 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles); break;
-        case 2: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 4, 1, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles); break;
-        case 4: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles); break;
+        case 1: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 2, 1, D>, grid, dim3(2 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
+        case 2: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 4, 1, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
+        case 4: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
         // 8 heads: at D 64 four waves of two column groups; at D 128 eight waves of one (two
         // groups' outputs and scores would hold more than a wave's registers).
         case 8:
             if constexpr (D == 64)
-                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 4, 2, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles);
+                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 4, 2, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
             else
-                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, b.attended, b.tiles);
+                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
             break;
         default: return hipErrorInvalidValue;
     }
@@ -1007,54 +987,97 @@ hipError_t prefill_prepare(size_t device_lds) {
     return allow((const void*)prefill_gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>, device_lds);
 }
 
+size_t prefill_attention_lds(int max_blocks) {
+    // The attention's ring and the slot's block ids.
+    return (size_t)ATTN_STAGES * ATTN_STAGE * sizeof(uint4) + (size_t)max_blocks * sizeof(uint32_t);
+}
+
+hipError_t launch_prefill_gemm(const PrefillArgs& a, int epi, int strip_rows, const GemmArgs& g, hipStream_t stream,
+                               DispatchTimer* timer) {
+    if (g.K <= 0 || g.K % 1024 || g.N <= 0 || g.N % TN || a.M_pad % ROW_TILE_MAX) return hipErrorInvalidValue;
+    switch (epi) {
+        case EPI_QKV:
+            if (strip_rows != QKV_ROWS) return hipErrorInvalidValue;
+            if (a.head_dim == 128)
+                gemm<EPI_QKV, QKV_ROWS, QKV_TM, 128>("prefill_qkv", a, g, stream, timer);
+            else if (a.head_dim == 64)
+                gemm<EPI_QKV, QKV_ROWS, QKV_TM, 64>("prefill_qkv", a, g, stream, timer);
+            else
+                return hipErrorInvalidValue;
+            break;
+        case EPI_SILU:
+            if (strip_rows != QKV_ROWS) return hipErrorInvalidValue;
+            gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>("prefill_gate_up", a, g, stream, timer);
+            break;
+        case EPI_RESIDUAL_IN:
+            if (strip_rows == 4)
+                gemm<EPI_RESIDUAL_IN, 4, O_TM>("prefill_o", a, g, stream, timer);
+            else if (strip_rows == 16)
+                gemm<EPI_RESIDUAL_IN, 16, O_TM>("prefill_o", a, g, stream, timer);
+            else
+                return hipErrorInvalidValue;
+            break;
+        case EPI_RESIDUAL:
+            if (strip_rows == 4)
+                gemm<EPI_RESIDUAL, 4, DOWN_TM>("prefill_down", a, g, stream, timer);
+            else if (strip_rows == 16)
+                gemm<EPI_RESIDUAL, 16, DOWN_TM>("prefill_down", a, g, stream, timer);
+            else
+                return hipErrorInvalidValue;
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const PrefillArgs& a, const uint16_t* q, const uint16_t* kv, uint16_t* attended,
+                                    const PrefillTile* tiles, int ntiles, hipStream_t stream, DispatchTimer* timer) {
+    const size_t lds = prefill_attention_lds(a.max_blocks);
+    hipError_t e = a.head_dim == 128 ? attention<128>(a, q, kv, attended, tiles, ntiles, lds, stream, timer)
+                   : a.head_dim == 64 ? attention<64>(a, q, kv, attended, tiles, ntiles, lds, stream, timer)
+                                      : hipErrorInvalidValue;
+    return e != hipSuccess ? e : hipGetLastError();
+}
+
+hipError_t launch_prefill_norm(const PrefillArgs& a, bool final, const float* x, const float* gain, uint16_t* out_bf16,
+                               float* out_f32, hipStream_t stream, DispatchTimer* timer) {
+    const dim3 rows4((a.M_pad + 3) / 4);
+    if (final)
+        dispatch("prefill_final_norm", prefill_norm<true>, rows4, dim3(256), 0, stream, timer, a, x, gain, (uint16_t*)nullptr, out_f32);
+    else
+        dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, x, gain, out_bf16, (float*)nullptr);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int nlayers, const float* final_norm,
                           const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer) {
-    const dim3 rows4((a.M_pad + 3) / 4);
     if (a.head_dim != 64 && a.head_dim != 128) return hipErrorInvalidValue;
     const int qkv_rows = (a.heads + 2 * a.kv_heads) * a.head_dim;
-    // The attention's ring and the slot's block ids.
-    const size_t attn_lds = (size_t)ATTN_STAGES * ATTN_STAGE * sizeof(uint4) + (size_t)a.max_blocks * sizeof(uint32_t);
+    hipError_t e = hipSuccess;
     // Layer 0's input norm; each later norm's input (the rows times the gain, and their sums of
     // squares) comes from the projection before it, the rows' scales applied by the GEMM after.
-    if (nlayers > 0)
-        dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, b.x,
-                 layers[0].input_norm, b.normed, (float*)nullptr);
+    if (nlayers > 0) e = launch_prefill_norm(a, false, b.x, layers[0].input_norm, b.normed, nullptr, stream, timer);
     const float* input = b.x;  // layer 0 reads the run's states, which stay as written
-    for (int l = 0; l < nlayers; ++l) {
+    for (int l = 0; l < nlayers && e == hipSuccess; ++l) {
         const PrefillLayer& L = layers[l];
         GemmArgs qkv{L.qkv, b.normed, a.hidden, qkv_rows, nullptr, nullptr, nullptr, b.q, L.kv,
                      l == 0 ? nullptr : b.row_sq, nullptr, nullptr, nullptr};
-        hipError_t e;
-        if (a.head_dim == 128) {
-            gemm<EPI_QKV, QKV_ROWS, QKV_TM, 128>("prefill_qkv", a, qkv, stream, timer);
-            e = attention<128>(a, b, L.kv, attn_lds, stream, timer);
-        } else {
-            gemm<EPI_QKV, QKV_ROWS, QKV_TM, 64>("prefill_qkv", a, qkv, stream, timer);
-            e = attention<64>(a, b, L.kv, attn_lds, stream, timer);
-        }
-        if (e != hipSuccess) return e;
-        if (L.od_rows != 4 && L.od_rows != 16) return hipErrorInvalidValue;
+        e = launch_prefill_gemm(a, EPI_QKV, QKV_ROWS, qkv, stream, timer);
+        if (e == hipSuccess) e = launch_prefill_attention(a, b.q, L.kv, b.attended, b.tiles, b.ntiles, stream, timer);
         GemmArgs o{L.o, b.attended, a.heads * a.head_dim, a.hidden, input, b.mid, nullptr, nullptr, nullptr,
                    nullptr, L.post_norm, b.normed, b.row_sq};
-        if (L.od_rows == 4)
-            gemm<EPI_RESIDUAL_IN, 4, O_TM>("prefill_o", a, o, stream, timer);
-        else
-            gemm<EPI_RESIDUAL_IN, 16, O_TM>("prefill_o", a, o, stream, timer);
+        if (e == hipSuccess) e = launch_prefill_gemm(a, EPI_RESIDUAL_IN, L.od_rows, o, stream, timer);
         GemmArgs gu{L.gate_up, b.normed, a.hidden, 2 * a.inner, nullptr, nullptr, b.mlp, nullptr, nullptr,
                     b.row_sq, nullptr, nullptr, nullptr};
-        gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>("prefill_gate_up", a, gu, stream, timer);
+        if (e == hipSuccess) e = launch_prefill_gemm(a, EPI_SILU, QKV_ROWS, gu, stream, timer);
         // The last layer's output goes to the final norm, which reads the f32 rows.
         GemmArgs down{L.down, b.mlp, a.inner, a.hidden, b.mid, b.h, nullptr, nullptr, nullptr,
                       nullptr, l + 1 < nlayers ? layers[l + 1].input_norm : nullptr, b.normed, b.row_sq};
-        if (L.od_rows == 4)
-            gemm<EPI_RESIDUAL, 4, DOWN_TM>("prefill_down", a, down, stream, timer);
-        else
-            gemm<EPI_RESIDUAL, 16, DOWN_TM>("prefill_down", a, down, stream, timer);
+        if (e == hipSuccess) e = launch_prefill_gemm(a, EPI_RESIDUAL, L.od_rows, down, stream, timer);
         input = b.h;
     }
-    dispatch("prefill_final_norm", prefill_norm<true>, rows4, dim3(256), 0, stream, timer, a, input, final_norm,
-             (uint16_t*)nullptr, b.out);
-    return hipGetLastError();
+    if (e == hipSuccess) e = launch_prefill_norm(a, true, input, final_norm, nullptr, b.out, stream, timer);
+    return e;
 }
 
 }  // namespace tgx

@@ -57,6 +57,49 @@ struct PrefillBuffers {
     int ntiles;
 };
 
+// The epilogue fused into a prefill GEMM (prefill_gemm in prefill_kernels.hip): q/k/v's RoPE and
+// cache write (rope_rows.comp), the residual add and the next norm's input (add_norm_rows.comp;
+// EPI_RESIDUAL adds the residual rows to the products in the epilogue, EPI_RESIDUAL_IN starts the
+// accumulators at them: for o_proj, whose short K leaves that wait exposed, not for down_proj, whose
+// long K hides it), or SiLU(gate) up (silu_mul_rows.comp).
+enum PrefillEpilogue { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SILU = 2, EPI_RESIDUAL_IN = 3 };
+__host__ __device__ constexpr bool residual_epilogue(int epi) { return epi == EPI_RESIDUAL || epi == EPI_RESIDUAL_IN; }
+
+// A prefill GEMM's operands and its epilogue's tensors.
+struct GemmArgs {
+    const uint16_t* w;  // tiles of [N][K] in strips of 16 rows (o_proj and down_proj: 4 or 16)
+    const uint16_t* x;  // bf16 [M_pad][K] in fragment order (act_index)
+    int K, N;
+    // epilogues
+    const float* residual;  // EPI_RESIDUAL(_IN): f32 [M_pad][N]
+    float* out;             // EPI_RESIDUAL(_IN): f32 [M_pad][N]
+    uint16_t* mlp;          // EPI_SILU: bf16 [M_pad][N / 2] in fragment order
+    uint16_t* q;            // EPI_QKV
+    uint16_t* kv;           // EPI_QKV: the layer's cache pool
+    // X as an RMSNorm's input times its gain, the rows' scales still to apply (EPI_QKV,
+    // EPI_SILU): row m's sums of squares over each 128 columns, [M_pad][K / 128]; null when X is
+    // normed already.
+    const float* row_sq;
+    // EPI_RESIDUAL(_IN), when set: out next_gain in bf16 in fragment order into out_n, and out's
+    // sums of squares over each 128 columns into out_sq, for the norm that reads out next.
+    const float* next_gain;
+    uint16_t* out_n;
+    float* out_sq;
+};
+
+// The prefill's kernels one at a time, as launch_prefill launches them (the instance, grid and LDS
+// the shape picks): a GEMM with its epilogue (strip_rows: W's strip height, 4 or 16 for o_proj and
+// down_proj, 16 otherwise), the causal attention over `ntiles` tiles of a run, and a norm of rows
+// (layer 0's input norm into bf16 in fragment order, or the final norm into f32).
+hipError_t launch_prefill_gemm(const PrefillArgs& a, int epi, int strip_rows, const GemmArgs& g, hipStream_t stream,
+                               DispatchTimer* timer);
+hipError_t launch_prefill_attention(const PrefillArgs& a, const uint16_t* q, const uint16_t* kv, uint16_t* attended,
+                                    const PrefillTile* tiles, int ntiles, hipStream_t stream, DispatchTimer* timer);
+hipError_t launch_prefill_norm(const PrefillArgs& a, bool final, const float* x, const float* gain, uint16_t* out_bf16,
+                               float* out_f32, hipStream_t stream, DispatchTimer* timer);
+// The LDS the attention takes for a slot table of `max_blocks` blocks.
+size_t prefill_attention_lds(int max_blocks);
+
 // Launches the whole prefill of the M rows of b.x (f32) through every layer into b.out.
 hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int nlayers, const float* final_norm,
                           const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer = nullptr);

@@ -5,6 +5,7 @@
 #include "runtime.hpp"
 
 #include "heads_kernels.hpp"
+#include "local_kernels.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -118,6 +119,7 @@ tgx_status context_create(int device, Context** out) {
     e = decode_prepare(ctx->lds_bytes);
     if (e == hipSuccess) e = prefill_prepare(ctx->lds_bytes);
     if (e == hipSuccess) e = heads_prepare(ctx->lds_bytes);
+    if (e == hipSuccess) e = local_prepare();
     // The device is current: the prefill scratch's address on it, kept for the process.
     if (e == hipSuccess) e = prefill_scratch_address(device, &ctx->scratch);
     if (e != hipSuccess) {

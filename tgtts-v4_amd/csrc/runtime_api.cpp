@@ -1,7 +1,10 @@
 // The runtime beneath the models (include/tgx.h, tgx_alloc .. tgx_copy_regions): memory in a
-// residence (crates/vulkan/src/memory.rs), the decode step's kernels by name with their bindings
-// in order (crates/graph/src/kernels.rs:27-161), and programs of dispatches recorded as HIP graphs
-// and run as often as needed (crates/vulkan/src/recording.rs:116-760).
+// residence (crates/vulkan/src/memory.rs), the kernels by name with their bindings in order (the
+// decode step's, crates/graph/src/kernels.rs:27-161; the prefill's, prefill.rs:32-116; the local
+// stacks' and the sampler's, local/mod.rs:28-113; the LM side's and the prompt's, lm_side.rs:28-38
+// and prompt.rs:42-67), and programs of dispatches recorded as HIP graphs and run as often as
+// needed (crates/vulkan/src/recording.rs:116-760). Past the decode step a kernel's launch is the
+// one the models' own launcher makes for the same arguments, captured instead of made.
 //
 // A dispatch is checked on the host before anything is recorded: every binding it must have is
 // there, of its kernel's element size and alignment, and holds every byte the kernel reaches for
@@ -17,6 +20,7 @@
 #include <thread>
 #include <vector>
 
+#include "dispatch.hpp"
 #include "handles.hpp"
 #include "runtime.hpp"
 
@@ -46,7 +50,9 @@ struct Bound {
 };
 
 // A dispatch ready to launch: the kernel, its grid and LDS, and the arguments it takes, kept where
-// `params` points for as long as the program lives.
+// `params` points for as long as the program lives; or, for a kernel whose launch is captured
+// from the models' own launcher (capture_one), each argument's bytes as captured, `captured`
+// pointing at them.
 struct Launch {
     const char* name = nullptr;
     KernelLaunch k;
@@ -59,6 +65,9 @@ struct Launch {
     void* out1 = nullptr;
     int advance = 0;
     void* params[6] = {};
+    std::vector<std::vector<unsigned char>> args;
+    std::vector<void*> captured;
+    void** kernel_params() { return captured.empty() ? params : captured.data(); }
 };
 
 using Builder = tgx_status (*)(const Bound* b, const uint32_t* c, Launch* out);
@@ -88,32 +97,46 @@ std::vector<const char*> decode_constants(std::vector<const char*> own = {}) {
     return c;
 }
 
+// A stack's shape from constants, refused as tgx_decoder_create refuses it.
+tgx_status shape_of(uint32_t hidden, uint32_t inner, uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t capacity,
+                    uint32_t eps, uint32_t rope, Shape* s) {
+    if (rope > 1) return fail(TGX_E_SHAPE, "rope is 0 or 1");
+    if (hidden > (1u << 20) || inner > (1u << 20) || heads > 1024 || kv_heads > 1024 || head_dim > 1024 || capacity > (1u << 24))
+        return fail(TGX_E_SHAPE, "a shape past the kernels' sizes");
+    tgx_shape in{};
+    in.hidden = (int)hidden;
+    in.inner = (int)inner;
+    in.heads = (int)heads;
+    in.kv_heads = (int)kv_heads;
+    in.head_dim = (int)head_dim;
+    in.layers = 1;
+    in.capacity = (int)capacity;
+    in.eps = as_float(eps);
+    in.rope_theta = 10000.f;
+    in.rope = rope != 0;
+    return check_shape(&in, s);
+}
+
+// A placement: `slots` slot tables of `max_blocks` entries each, enough for `capacity` positions,
+// into a pool of `blocks` cache blocks.
+tgx_status check_placement(uint32_t capacity, uint32_t slots, uint32_t max_blocks, uint32_t blocks) {
+    const uint32_t need = (capacity + BLOCK_TOKENS - 1) / BLOCK_TOKENS;
+    if (max_blocks < need || blocks == 0 || slots == 0 || max_blocks > (1u << 20) || blocks > (1u << 24) || slots > (1u << 16))
+        return fail(TGX_E_SHAPE, std::to_string(slots) + " slots of " + std::to_string(max_blocks) + " blocks in a pool of " +
+                                     std::to_string(blocks) + " (a slot's table holds " + std::to_string(need) +
+                                     " blocks at the capacity)");
+    return TGX_OK;
+}
+
 // The shape and placement constants as the kernels take them, refused as tgx_decoder_create
 // refuses a shape and a batch; the placement's tables are bound by the kernels that read them.
 tgx_status decode_args(const uint32_t* c, DecodeArgs* a) {
-    tgx_shape in{};
-    in.hidden = (int)c[C_HIDDEN];
-    in.inner = (int)c[C_INNER];
-    in.heads = (int)c[C_HEADS];
-    in.kv_heads = (int)c[C_KV];
-    in.head_dim = (int)c[C_HEAD_DIM];
-    in.layers = 1;
-    in.capacity = (int)c[C_CAPACITY];
-    in.eps = as_float(c[C_EPS]);
-    in.rope_theta = 10000.f;
-    in.rope = c[C_ROPE] != 0;
     Shape s;
-    TGX_TRY(check_shape(&in, &s));
+    TGX_TRY(shape_of(c[C_HIDDEN], c[C_INNER], c[C_HEADS], c[C_KV], c[C_HEAD_DIM], c[C_CAPACITY], c[C_EPS], c[C_ROPE], &s));
     tgx_batch batch{(int)c[C_ROWS], (int)c[C_SLOTS], BLOCK_TOKENS, (int)c[C_BLOCKS]};
     if ((int)c[C_ROWS] <= 0 || c[C_ROWS] > 64) return fail(TGX_E_SHAPE, "rows " + std::to_string(c[C_ROWS]) + ": 1 to 64");
     TGX_TRY(check_batch(s, &batch));
-    const uint32_t need = (c[C_CAPACITY] + BLOCK_TOKENS - 1) / BLOCK_TOKENS;
-    if (c[C_MAX_BLOCKS] < need || c[C_BLOCKS] == 0 || c[C_SLOTS] == 0 || c[C_MAX_BLOCKS] > (1u << 20) || c[C_BLOCKS] > (1u << 24) ||
-        c[C_SLOTS] > (1u << 16))
-        return fail(TGX_E_SHAPE, std::to_string(c[C_SLOTS]) + " slots of " + std::to_string(c[C_MAX_BLOCKS]) +
-                                     " blocks in a pool of " + std::to_string(c[C_BLOCKS]) + " (a slot's table holds " +
-                                     std::to_string(need) + " blocks at the capacity)");
-    if (c[C_ROPE] > 1) return fail(TGX_E_SHAPE, "rope is 0 or 1");
+    TGX_TRY(check_placement(c[C_CAPACITY], c[C_SLOTS], c[C_MAX_BLOCKS], c[C_BLOCKS]));
     *a = DecodeArgs{};
     a->hidden = s.hidden;
     a->inner = s.inner;
@@ -320,6 +343,619 @@ tgx_status build_stream_read(const Bound* b, const uint32_t*, Launch* L) {
     return TGX_OK;
 }
 
+// The one launch `launcher` makes, captured instead of made (capture_launches): the kernel, grid,
+// LDS and arguments the models' own launch takes for the same arguments.
+template <typename F>
+tgx_status capture_one(const char* who, F&& launcher, Launch* L) {
+    hipError_t e = hipSuccess;
+    std::vector<CapturedLaunch> c = capture_launches([&] { e = launcher(); });
+    if (c.size() != 1) return fail(TGX_E_SHAPE, std::string(who) + ": no instance takes these constants");
+    if (e != hipSuccess) return fail(TGX_E_HIP, std::string(who) + ": " + hipGetErrorString(e));
+    L->k = KernelLaunch{c[0].func, c[0].grid, c[0].block, c[0].lds};
+    L->args = std::move(c[0].args);
+    L->captured.clear();
+    for (auto& a : L->args) L->captured.push_back(a.data());
+    return TGX_OK;
+}
+
+uint64_t round_up(uint64_t v, uint64_t to) { return (v + to - 1) / to * to; }
+
+// ---- the prefill's kernels (prefill.rs:32-81) ----
+
+// The constants every prefill kernel takes first, in order: the run's rows (positions over every
+// run, laid one after another), the stack's shape and the cache's placement. Tensors of rows hold
+// rows_pad of them, rows rounded up to 256 (the GEMM's tile), except where a kernel says.
+constexpr int P_ROWS = 0, P_HIDDEN = 1, P_INNER = 2, P_HEADS = 3, P_KV = 4, P_HEAD_DIM = 5, P_CAPACITY = 6, P_SLOTS = 7,
+              P_MAX_BLOCKS = 8, P_BLOCKS = 9, P_EPS = 10, P_ROPE = 11, P_COMMON = 12;
+constexpr uint32_t PREFILL_MAX_ROWS = 1u << 20;
+std::vector<const char*> prefill_constants(std::vector<const char*> own = {}) {
+    std::vector<const char*> c = {"rows", "hidden", "inner", "heads", "kv_heads", "head_dim", "capacity", "slots", "max_blocks",
+                                  "blocks", "eps", "rope"};
+    c.insert(c.end(), own.begin(), own.end());
+    return c;
+}
+
+tgx_status prefill_args(const uint32_t* c, PrefillArgs* a) {
+    Shape s;
+    TGX_TRY(shape_of(c[P_HIDDEN], c[P_INNER], c[P_HEADS], c[P_KV], c[P_HEAD_DIM], c[P_CAPACITY], c[P_EPS], c[P_ROPE], &s));
+    if (c[P_ROWS] == 0 || c[P_ROWS] > PREFILL_MAX_ROWS)
+        return fail(TGX_E_SHAPE, "rows " + std::to_string(c[P_ROWS]) + ": 1 to " + std::to_string(PREFILL_MAX_ROWS));
+    TGX_TRY(check_placement(c[P_CAPACITY], c[P_SLOTS], c[P_MAX_BLOCKS], c[P_BLOCKS]));
+    *a = PrefillArgs{};
+    a->M = (int)c[P_ROWS];
+    a->M_pad = (int)round_up(c[P_ROWS], 256);
+    a->hidden = s.hidden;
+    a->inner = s.inner;
+    a->heads = s.heads;
+    a->kv_heads = s.kv_heads;
+    a->head_dim = s.head_dim;
+    a->capacity = s.capacity;
+    a->nslots = (int)c[P_SLOTS];
+    a->max_blocks = (int)c[P_MAX_BLOCKS];
+    a->nblocks = (int)c[P_BLOCKS];
+    a->eps = s.eps;
+    a->scale = 1.0f / std::sqrt((float)s.head_dim);
+    a->rope = (int)c[P_ROPE];
+    return TGX_OK;
+}
+
+uint64_t prefill_pool_bytes(const PrefillArgs& a) { return (uint64_t)a.nblocks * a.kv_heads * 2 * kv_tile(a.head_dim) * 2; }
+
+// norm_rows (norm_rows.comp): x, gain -> out. The first layer's input norm: x [rows][hidden] f32
+// into bf16 rows in fragment order (rows_pad of them, zero past rows), as the GEMMs read them.
+tgx_status build_norm_rows(const Bound* b, const uint32_t* c, Launch* L) {
+    PrefillArgs a;
+    TGX_TRY(prefill_args(c, &a));
+    const uint64_t h = a.hidden;
+    TGX_TRY(holds(b, 0, "x", (uint64_t)a.M * h * 4));
+    TGX_TRY(holds(b, 1, "gain", h * 4));
+    TGX_TRY(holds(b, 2, "out", (uint64_t)a.M_pad * h * 2));
+    return capture_one("norm_rows", [&] {
+        return launch_prefill_norm(a, false, (const float*)b[0].ptr, (const float*)b[1].ptr, (uint16_t*)b[2].ptr, nullptr, nullptr, nullptr);
+    }, L);
+}
+
+// final_norm_rows (norm_rows.comp as the last step): x, gain -> out, f32 [rows][hidden] both.
+tgx_status build_final_norm_rows(const Bound* b, const uint32_t* c, Launch* L) {
+    PrefillArgs a;
+    TGX_TRY(prefill_args(c, &a));
+    const uint64_t h = a.hidden;
+    TGX_TRY(holds(b, 0, "x", (uint64_t)a.M * h * 4));
+    TGX_TRY(holds(b, 1, "gain", h * 4));
+    TGX_TRY(holds(b, 2, "out", (uint64_t)a.M * h * 4));
+    return capture_one("final_norm_rows", [&] {
+        return launch_prefill_norm(a, true, (const float*)b[0].ptr, (const float*)b[1].ptr, nullptr, (float*)b[2].ptr, nullptr, nullptr);
+    }, L);
+}
+
+// gemm_rope_rows (the q/k/v GEMM with rope_rows.comp fused): x, W, [row_sq,] cos, sin, positions,
+// slots, table -> q, cache pool. x: bf16 [rows_pad][hidden] in fragment order, an RMSNorm's output,
+// or with row_sq its input times the gain and the rows' sums of squares over each 128 columns
+// ([rows_pad][hidden / 128] f32); W: q/k/v rows in tiles of TGX_TILES_QKV (head_dim 64) or
+// TGX_TILES_QKV128; positions and slots: [rows] u32 (a position past the capacity or a slot past
+// the table's is a spare row: nothing written).
+tgx_status build_gemm_rope_rows(const Bound* b, const uint32_t* c, Launch* L) {
+    PrefillArgs a;
+    TGX_TRY(prefill_args(c, &a));
+    const uint64_t h = a.hidden, D = a.head_dim, Mp = a.M_pad, N = (uint64_t)(a.heads + 2 * a.kv_heads) * D;
+    TGX_TRY(holds(b, 0, "x", Mp * h * 2));
+    TGX_TRY(holds(b, 1, "w", N * h * 2));
+    if (b[2].ptr) TGX_TRY(holds(b, 2, "row_sq", Mp * (h / 128) * 4));
+    TGX_TRY(holds(b, 3, "cos", (uint64_t)a.capacity * (D / 2) * 4));
+    TGX_TRY(holds(b, 4, "sin", (uint64_t)a.capacity * (D / 2) * 4));
+    TGX_TRY(holds(b, 5, "positions", (uint64_t)a.M * 4));
+    TGX_TRY(holds(b, 6, "slots", (uint64_t)a.M * 4));
+    TGX_TRY(holds(b, 7, "table", (uint64_t)a.nslots * a.max_blocks * 4));
+    TGX_TRY(holds(b, 8, "q", Mp * a.heads * D * 2));
+    TGX_TRY(holds(b, 9, "kv", prefill_pool_bytes(a)));
+    a.cos = (const float*)b[3].ptr;
+    a.sin = (const float*)b[4].ptr;
+    a.tok_pos = (const uint32_t*)b[5].ptr;
+    a.tok_slot = (const uint32_t*)b[6].ptr;
+    a.table = (const uint32_t*)b[7].ptr;
+    GemmArgs g{};
+    g.w = (const uint16_t*)b[1].ptr;
+    g.x = (const uint16_t*)b[0].ptr;
+    g.K = a.hidden;
+    g.N = (int)N;
+    g.row_sq = (const float*)b[2].ptr;
+    g.q = (uint16_t*)b[8].ptr;
+    g.kv = (uint16_t*)b[9].ptr;
+    return capture_one("gemm_rope_rows", [&] { return launch_prefill_gemm(a, EPI_QKV, QKV_ROWS, g, nullptr, nullptr); }, L);
+}
+
+// attention_rows (attention_rows.comp): q, cache pool, table, tiles -> attended, constant tiles.
+// Each tile is 4 u32: row0, pos0, count, slot: rows row0 .. row0 + count - 1 are positions
+// pos0 .. of the slot, every position of a run up to its own attending to the slot's cache. A tile
+// holds at most 32 positions (16 at 8 query heads a KV head); one that leaves the tensors is
+// skipped. attended: bf16 [rows_pad][heads head_dim] in fragment order, written at the tiles' rows
+// only (the GEMM after it reads every row: keep the rest zero).
+tgx_status build_attention_rows(const Bound* b, const uint32_t* c, Launch* L) {
+    PrefillArgs a;
+    TGX_TRY(prefill_args(c, &a));
+    const uint32_t ntiles = c[P_COMMON];
+    if (ntiles == 0 || ntiles > PREFILL_MAX_ROWS)
+        return fail(TGX_E_SHAPE, "attention_rows: " + std::to_string(ntiles) + " tiles (1 to " + std::to_string(PREFILL_MAX_ROWS) + ")");
+    const uint64_t Mp = a.M_pad, att = (uint64_t)a.heads * a.head_dim;
+    TGX_TRY(holds(b, 0, "q", Mp * att * 2));
+    TGX_TRY(holds(b, 1, "kv", prefill_pool_bytes(a)));
+    TGX_TRY(holds(b, 2, "table", (uint64_t)a.nslots * a.max_blocks * 4));
+    TGX_TRY(holds(b, 3, "tiles", (uint64_t)ntiles * sizeof(PrefillTile)));
+    TGX_TRY(holds(b, 4, "attended", Mp * att * 2));
+    a.table = (const uint32_t*)b[2].ptr;
+    return capture_one("attention_rows", [&] {
+        return launch_prefill_attention(a, (const uint16_t*)b[0].ptr, (const uint16_t*)b[1].ptr, (uint16_t*)b[4].ptr,
+                                        (const PrefillTile*)b[3].ptr, (int)ntiles, nullptr, nullptr);
+    }, L);
+}
+
+// gemm_add_norm_rows (o_proj or down_proj with add_norm_rows.comp fused): x, W, residual
+// [, next_gain] -> out [, out_n, out_sq]; constants K, N, strip_rows (W's tiles: 4 or 16) and
+// residual_in (1: the accumulators start at the residual, as the prefill does for o_proj; 0: it
+// is added after the products, as for down_proj; the same sums either way). x: bf16
+// [rows_pad][K] in fragment order; residual and out: f32 [rows][N]; with next_gain the next
+// norm's input, out next_gain in bf16 in fragment order ([rows_pad][N]), and out's sums of
+// squares over each 128 columns ([rows][N / 128] f32).
+tgx_status build_gemm_add_norm_rows(const Bound* b, const uint32_t* c, Launch* L) {
+    PrefillArgs a;
+    TGX_TRY(prefill_args(c, &a));
+    const uint32_t K = c[P_COMMON], N = c[P_COMMON + 1], Rs = c[P_COMMON + 2], in = c[P_COMMON + 3];
+    if (K == 0 || K % 1024 || K > (uint32_t)decode_max_k() || N == 0 || N % 256 || N > (1u << 16) || (Rs != 4 && Rs != 16) || in > 1)
+        return fail(TGX_E_SHAPE, "gemm_add_norm_rows: K " + std::to_string(K) + " (a multiple of 1024 up to " +
+                                     std::to_string(decode_max_k()) + "), N " + std::to_string(N) + " (a multiple of 256), strips of " +
+                                     std::to_string(Rs) + " rows (4 or 16), residual_in " + std::to_string(in) + " (0 or 1)");
+    if ((b[3].ptr != nullptr) != (b[5].ptr != nullptr) || (b[3].ptr != nullptr) != (b[6].ptr != nullptr))
+        return fail(TGX_E_SHAPE, "gemm_add_norm_rows takes next_gain, out_n and out_sq together or none of them");
+    const uint64_t M = a.M, Mp = a.M_pad;
+    TGX_TRY(holds(b, 0, "x", Mp * K * 2));
+    TGX_TRY(holds(b, 1, "w", (uint64_t)N * K * 2));
+    TGX_TRY(holds(b, 2, "residual", M * N * 4));
+    TGX_TRY(holds(b, 4, "out", M * N * 4));
+    if (b[3].ptr) {
+        TGX_TRY(holds(b, 3, "next_gain", (uint64_t)N * 4));
+        TGX_TRY(holds(b, 5, "out_n", Mp * N * 2));
+        TGX_TRY(holds(b, 6, "out_sq", M * (N / 128) * 4));
+    }
+    GemmArgs g{};
+    g.w = (const uint16_t*)b[1].ptr;
+    g.x = (const uint16_t*)b[0].ptr;
+    g.K = (int)K;
+    g.N = (int)N;
+    g.residual = (const float*)b[2].ptr;
+    g.out = (float*)b[4].ptr;
+    g.next_gain = (const float*)b[3].ptr;
+    g.out_n = (uint16_t*)b[5].ptr;
+    g.out_sq = (float*)b[6].ptr;
+    const int epi = in ? EPI_RESIDUAL_IN : EPI_RESIDUAL;
+    return capture_one("gemm_add_norm_rows", [&] { return launch_prefill_gemm(a, epi, (int)Rs, g, nullptr, nullptr); }, L);
+}
+
+// gemm_silu_mul_rows (gate/up with silu_mul_rows.comp fused): x, W [, row_sq] -> mlp; constants
+// K, N (gate's rows then up's: N / 2 outputs). x as gemm_rope_rows takes it ([rows_pad][K]); mlp:
+// bf16 [rows_pad][N / 2] in fragment order.
+tgx_status build_gemm_silu_mul_rows(const Bound* b, const uint32_t* c, Launch* L) {
+    PrefillArgs a;
+    TGX_TRY(prefill_args(c, &a));
+    const uint32_t K = c[P_COMMON], N = c[P_COMMON + 1];
+    if (K == 0 || K % 1024 || K > 4096 || N == 0 || N % 256 || N > (1u << 16))
+        return fail(TGX_E_SHAPE, "gemm_silu_mul_rows: K " + std::to_string(K) + " (a multiple of 1024 up to 4096), N " +
+                                     std::to_string(N) + " (a multiple of 256)");
+    const uint64_t Mp = a.M_pad;
+    TGX_TRY(holds(b, 0, "x", Mp * K * 2));
+    TGX_TRY(holds(b, 1, "w", (uint64_t)N * K * 2));
+    if (b[2].ptr) TGX_TRY(holds(b, 2, "row_sq", Mp * (K / 128) * 4));
+    TGX_TRY(holds(b, 3, "mlp", Mp * (N / 2) * 2));
+    GemmArgs g{};
+    g.w = (const uint16_t*)b[1].ptr;
+    g.x = (const uint16_t*)b[0].ptr;
+    g.K = (int)K;
+    g.N = (int)N;
+    g.row_sq = (const float*)b[2].ptr;
+    g.mlp = (uint16_t*)b[3].ptr;
+    return capture_one("gemm_silu_mul_rows", [&] { return launch_prefill_gemm(a, EPI_SILU, QKV_ROWS, g, nullptr, nullptr); }, L);
+}
+
+// ---- the local stacks' and the patch sampler's kernels (local/mod.rs:28-113) ----
+
+// The constants every local-stack kernel takes first: tokens in sequences of seq_tokens (token m
+// at place m % seq_tokens of its sequence) and the stack's shape (head_dim 64, hidden 1024).
+// Tensors of tokens hold tokens_pad of them (tokens rounded up to 16 up to 64 tokens, to 64
+// past that) where a GEMM reads them, `tokens` elsewhere, as each kernel says.
+constexpr int L_TOKENS = 0, L_SEQ = 1, L_HIDDEN = 2, L_INNER = 3, L_HEADS = 4, L_KV = 5, L_EPS = 6, L_ROPE = 7, L_COMMON = 8;
+constexpr uint32_t LOCAL_MAX_TOKENS = 1u << 16;
+std::vector<const char*> local_constants(std::vector<const char*> own = {}) {
+    std::vector<const char*> c = {"tokens", "seq_tokens", "hidden", "inner", "heads", "kv_heads", "eps", "rope"};
+    c.insert(c.end(), own.begin(), own.end());
+    return c;
+}
+
+tgx_status local_args(const uint32_t* c, LocalArgs* a) {
+    const uint32_t M = c[L_TOKENS], T = c[L_SEQ];
+    if (T == 0 || T > (uint32_t)LOCAL_MAX_T || M == 0 || M > LOCAL_MAX_TOKENS || M % T)
+        return fail(TGX_E_SHAPE, std::to_string(M) + " tokens in sequences of " + std::to_string(T) + " (1 to " +
+                                     std::to_string(LOCAL_MAX_T) + " tokens a sequence, whole sequences, " +
+                                     std::to_string(LOCAL_MAX_TOKENS) + " tokens at most)");
+    Shape s;
+    TGX_TRY(shape_of(c[L_HIDDEN], c[L_INNER], c[L_HEADS], c[L_KV], HEAD_DIM, T, c[L_EPS], c[L_ROPE], &s));
+    if (s.hidden != 1024 || s.heads % 4 || s.inner % 64)
+        return fail(TGX_E_SHAPE, "a local stack " + std::to_string(s.hidden) + " wide of " + std::to_string(s.heads) +
+                                     " heads with an FFN " + std::to_string(s.inner) +
+                                     " wide (the kernels take 1024, heads a multiple of 4, an FFN a multiple of 64)");
+    *a = LocalArgs{};
+    a->M = (int)M;
+    a->M_pad = local_rows_padded((int)M);
+    a->T = (int)T;
+    a->hidden = s.hidden;
+    a->inner = s.inner;
+    a->heads = s.heads;
+    a->kv_heads = s.kv_heads;
+    a->eps = s.eps;
+    a->scale = 1.0f / std::sqrt((float)HEAD_DIM);
+    a->rope = s.rope ? 1 : 0;
+    return TGX_OK;
+}
+
+constexpr uint64_t LOCAL_SQ = 1024 / LOCAL_SQ_COLS;  // a token's sums of squares
+
+// local_norm (local_norm.comp): x, gain -> normed, row_sq. The first layer's input norm as the
+// GEMMs after it read it: x [tokens][1024] f32; normed = x gain in bf16, [tokens_pad][1024] in
+// fragment order (written at the tokens' rows); row_sq: each 64 columns' sum of squares of x,
+// [tokens][16] f32 (the GEMM applies the rows' scales).
+tgx_status build_local_norm(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint64_t M = a.M, h = a.hidden;
+    TGX_TRY(holds(b, 0, "x", M * h * 4));
+    TGX_TRY(holds(b, 1, "gain", h * 4));
+    TGX_TRY(holds(b, 2, "normed", (uint64_t)a.M_pad * h * 2));
+    TGX_TRY(holds(b, 3, "row_sq", M * LOCAL_SQ * 4));
+    return capture_one("local_norm", [&] {
+        return launch_local_add_norm(a, false, nullptr, 0, (const float*)b[0].ptr, nullptr, (const float*)b[1].ptr, (uint16_t*)b[2].ptr,
+                                     (float*)b[3].ptr, nullptr, nullptr, nullptr);
+    }, L);
+}
+
+// local_qkv_rope (local_qkv_rope.comp): x, W, row_sq, cos, sin -> q, k, v. x and row_sq as
+// local_norm writes them ([tokens_pad] rows each); W in tiles of TGX_TILES_QKV; cos and sin
+// [seq_tokens][32] (the rotation at each place of a sequence); q [tokens][heads][64], k and v
+// [tokens][kv_heads][64], bf16.
+tgx_status build_local_qkv_rope(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint64_t M = a.M, Mp = a.M_pad, h = a.hidden, N = (uint64_t)(a.heads + 2 * a.kv_heads) * HEAD_DIM;
+    TGX_TRY(holds(b, 0, "x", Mp * h * 2));
+    TGX_TRY(holds(b, 1, "w", N * h * 2));
+    TGX_TRY(holds(b, 2, "row_sq", Mp * LOCAL_SQ * 4));
+    TGX_TRY(holds(b, 3, "cos", (uint64_t)a.T * (HEAD_DIM / 2) * 4));
+    TGX_TRY(holds(b, 4, "sin", (uint64_t)a.T * (HEAD_DIM / 2) * 4));
+    TGX_TRY(holds(b, 5, "q", M * a.heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 6, "k", M * a.kv_heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 7, "v", M * a.kv_heads * HEAD_DIM * 2));
+    a.cos = (const float*)b[3].ptr;
+    a.sin = (const float*)b[4].ptr;
+    LocalGemm g{};
+    g.w = (const uint16_t*)b[1].ptr;
+    g.x = (const uint16_t*)b[0].ptr;
+    g.K = a.hidden;
+    g.N = (int)N;
+    g.row_sq = (const float*)b[2].ptr;
+    g.q = (uint16_t*)b[5].ptr;
+    g.k = (uint16_t*)b[6].ptr;
+    g.v = (uint16_t*)b[7].ptr;
+    return capture_one("local_qkv_rope", [&] { return launch_local_qkv(a, g, nullptr, nullptr); }, L);
+}
+
+// local_attention (local_attention.comp): q, k, v -> attended, every token of a sequence
+// attending to every token of it; attended bf16 [tokens_pad][heads 64] in fragment order, written
+// at the tokens' rows.
+tgx_status build_local_attention(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint64_t M = a.M;
+    TGX_TRY(holds(b, 0, "q", M * a.heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 1, "k", M * a.kv_heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 2, "v", M * a.kv_heads * HEAD_DIM * 2));
+    TGX_TRY(holds(b, 3, "attended", (uint64_t)a.M_pad * a.heads * HEAD_DIM * 2));
+    return capture_one("local_attention", [&] {
+        return launch_local_attention(a, (const uint16_t*)b[0].ptr, (const uint16_t*)b[1].ptr, (const uint16_t*)b[2].ptr,
+                                      (uint16_t*)b[3].ptr, nullptr, nullptr);
+    }, L);
+}
+
+// local_partial (local_partial.comp): x, W -> partial; constants K, N, parts. Up to 64 tokens:
+// the products over each of `parts` equal spans of K (16 or 32 k-blocks of 32 columns each),
+// f32 [parts][tokens_pad][N]; x bf16 [tokens_pad][K] in fragment order.
+tgx_status build_local_partial(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint32_t K = c[L_COMMON], N = c[L_COMMON + 1], parts = c[L_COMMON + 2];
+    if (K == 0 || K > 8192 || N == 0 || N > 8192 || parts == 0 || parts > (uint32_t)LOCAL_MAX_PARTS)
+        return fail(TGX_E_SHAPE, "local_partial: K " + std::to_string(K) + ", N " + std::to_string(N) + " in " + std::to_string(parts) +
+                                     " parts");
+    const uint64_t Mp = a.M_pad;
+    TGX_TRY(holds(b, 0, "x", Mp * K * 2));
+    TGX_TRY(holds(b, 1, "w", (uint64_t)N * K * 2));
+    TGX_TRY(holds(b, 2, "partial", parts * Mp * N * 4));
+    LocalGemm g{};
+    g.w = (const uint16_t*)b[1].ptr;
+    g.x = (const uint16_t*)b[0].ptr;
+    g.K = (int)K;
+    g.N = (int)N;
+    g.partial = (float*)b[2].ptr;
+    return capture_one("local_partial", [&] { return launch_local_partial(a, g, (int)parts, nullptr, nullptr); }, L);
+}
+
+// The add-norm kernels' checks: `parts` of partial ([parts][tokens_pad][1024] f32, bound when
+// parts > 0), the residual [tokens][1024] f32 and the gain.
+tgx_status add_norm_inputs(const Bound* b, const LocalArgs& a, uint32_t parts, const char* who) {
+    if (parts > (uint32_t)LOCAL_MAX_PARTS || (parts > 0) != (b[0].ptr != nullptr))
+        return fail(TGX_E_SHAPE, std::string(who) + ": " + std::to_string(parts) + " parts (0 to " + std::to_string(LOCAL_MAX_PARTS) +
+                                     ", partial bound when more than 0)");
+    const uint64_t M = a.M, h = a.hidden;
+    if (parts) TGX_TRY(holds(b, 0, "partial", parts * (uint64_t)a.M_pad * h * 4));
+    TGX_TRY(holds(b, 1, "residual", M * h * 4));
+    TGX_TRY(holds(b, 2, "gain", h * 4));
+    if (b[3].ptr) TGX_TRY(holds(b, 3, "sum", M * h * 4));
+    return TGX_OK;
+}
+
+// local_add_norm (local_add_norm.comp): [partial,] residual, gain -> [sum,] normed, row_sq;
+// constant parts. sum = residual + the parts' sums in part order; then the next norm's input as
+// local_norm writes it.
+tgx_status build_local_add_norm(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint32_t parts = c[L_COMMON];
+    TGX_TRY(add_norm_inputs(b, a, parts, "local_add_norm"));
+    TGX_TRY(holds(b, 4, "normed", (uint64_t)a.M_pad * a.hidden * 2));
+    TGX_TRY(holds(b, 5, "row_sq", (uint64_t)a.M * LOCAL_SQ * 4));
+    return capture_one("local_add_norm", [&] {
+        return launch_local_add_norm(a, false, (const float*)b[0].ptr, (int)parts, (const float*)b[1].ptr, (float*)b[3].ptr,
+                                     (const float*)b[2].ptr, (uint16_t*)b[4].ptr, (float*)b[5].ptr, nullptr, nullptr, nullptr);
+    }, L);
+}
+
+// local_final_norm (local_norm.comp as a stack's last step): [partial,] residual, gain ->
+// [sum,] out; constant parts. out = RMSNorm(residual + the parts' sums) gain, f32 [tokens][1024].
+tgx_status build_local_final_norm(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint32_t parts = c[L_COMMON];
+    TGX_TRY(add_norm_inputs(b, a, parts, "local_final_norm"));
+    TGX_TRY(holds(b, 4, "out", (uint64_t)a.M * a.hidden * 4));
+    return capture_one("local_final_norm", [&] {
+        return launch_local_add_norm(a, true, (const float*)b[0].ptr, (int)parts, (const float*)b[1].ptr, (float*)b[3].ptr,
+                                     (const float*)b[2].ptr, nullptr, nullptr, (float*)b[4].ptr, nullptr, nullptr);
+    }, L);
+}
+
+// local_gemm_add_norm (local_partial.comp and local_add_norm.comp fused, past 64 tokens): x, W,
+// residual [, next_gain] -> sum [, normed, row_sq]; constants K, N (1024), parts (2 or 4 spans of
+// 16 or 32 k-blocks, added in part order as local_add_norm adds them). residual: f32
+// [tokens_pad][1024]; sum [tokens][1024]; with next_gain the next norm's input as local_norm
+// writes it.
+tgx_status build_local_gemm_add_norm(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint32_t K = c[L_COMMON], N = c[L_COMMON + 1], parts = c[L_COMMON + 2];
+    if (K == 0 || K > 8192 || N != (uint32_t)a.hidden || parts == 0 || parts > (uint32_t)LOCAL_MAX_PARTS)
+        return fail(TGX_E_SHAPE, "local_gemm_add_norm: K " + std::to_string(K) + ", N " + std::to_string(N) + " (the hidden width) in " +
+                                     std::to_string(parts) + " parts");
+    if ((b[3].ptr != nullptr) != (b[5].ptr != nullptr) || (b[3].ptr != nullptr) != (b[6].ptr != nullptr))
+        return fail(TGX_E_SHAPE, "local_gemm_add_norm takes next_gain, normed and row_sq together or none of them");
+    const uint64_t M = a.M, Mp = a.M_pad;
+    TGX_TRY(holds(b, 0, "x", Mp * K * 2));
+    TGX_TRY(holds(b, 1, "w", (uint64_t)N * K * 2));
+    TGX_TRY(holds(b, 2, "residual", Mp * N * 4));
+    TGX_TRY(holds(b, 4, "sum", M * N * 4));
+    if (b[3].ptr) {
+        TGX_TRY(holds(b, 3, "next_gain", (uint64_t)N * 4));
+        TGX_TRY(holds(b, 5, "normed", Mp * N * 2));
+        TGX_TRY(holds(b, 6, "row_sq", M * LOCAL_SQ * 4));
+    }
+    LocalGemm g{};
+    g.w = (const uint16_t*)b[1].ptr;
+    g.x = (const uint16_t*)b[0].ptr;
+    g.K = (int)K;
+    g.N = (int)N;
+    g.residual = (const float*)b[2].ptr;
+    g.next_gain = (const float*)b[3].ptr;
+    g.sum = (float*)b[4].ptr;
+    g.normed = (uint16_t*)b[5].ptr;
+    g.sum_sq = (float*)b[6].ptr;
+    return capture_one("local_gemm_add_norm", [&] { return launch_local_add(a, g, (int)parts, nullptr, nullptr); }, L);
+}
+
+// local_gate_up (local_gate_up.comp): x, W, row_sq -> mlp. x and row_sq as local_norm writes them
+// ([tokens_pad] rows each); W: the gate's rows then the up's, 2 inner x 1024 in tiles of
+// TGX_TILES_16; mlp = SiLU(gate) up, bf16 [tokens_pad][inner] in fragment order.
+tgx_status build_local_gate_up(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint64_t Mp = a.M_pad, h = a.hidden;
+    TGX_TRY(holds(b, 0, "x", Mp * h * 2));
+    TGX_TRY(holds(b, 1, "w", 2 * (uint64_t)a.inner * h * 2));
+    TGX_TRY(holds(b, 2, "row_sq", Mp * LOCAL_SQ * 4));
+    TGX_TRY(holds(b, 3, "mlp", Mp * a.inner * 2));
+    LocalGemm g{};
+    g.w = (const uint16_t*)b[1].ptr;
+    g.x = (const uint16_t*)b[0].ptr;
+    g.K = a.hidden;
+    g.N = 2 * a.inner;
+    g.row_sq = (const float*)b[2].ptr;
+    g.mlp = (uint16_t*)b[3].ptr;
+    return capture_one("local_gate_up", [&] { return launch_local_gate_up(a, g, nullptr, nullptr); }, L);
+}
+
+// local_embed (local_embed.comp): frames, W, bias, tokens [, gain] -> x0 [, normed, row_sq];
+// constants past the stack's: patch_rows, channels, frames, first, copy_at, copies, guided,
+// shared, seqs. Each patch row's frames [channels][frames] f32 through the linear layer (W f32
+// [1024][channels], bias [1024]) into tokens first .. first + frames - 1 of each of its `seqs`
+// sequences, and `copies` tokens of `tokens` ([patch_rows][copies][1024] f32, or [copies][1024]
+// when shared) at copy_at .. (zero in the second sequence when guided); with gain, each token
+// written is also the first layer's norm input as local_norm writes it. x0: f32 [tokens][1024].
+tgx_status build_local_embed(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint32_t* o = c + L_COMMON;
+    const uint32_t rows = o[0], C = o[1], F = o[2], first = o[3], copy_at = o[4], copies = o[5], guided = o[6], shared = o[7],
+                   seqs = o[8];
+    const uint64_t T = a.T;
+    if (rows == 0 || seqs == 0 || seqs > 2 || (uint64_t)rows * seqs * T > (uint64_t)a.M || C == 0 || C % 4 || C > 64 || F == 0 ||
+        F > 4 || C * F > 1024 || first + F > T || copies == 0 || copies > 2 || copy_at + copies > T || guided > 1 || shared > 1)
+        return fail(TGX_E_SHAPE, "local_embed: " + std::to_string(rows) + " patch rows of " + std::to_string(seqs) +
+                                     " sequences, frames of " + std::to_string(C) + " channels x " + std::to_string(F) +
+                                     " at token " + std::to_string(first) + ", " + std::to_string(copies) + " tokens copied at " +
+                                     std::to_string(copy_at) + " (channels a multiple of 4 up to 64, 1 to 4 frames, 1 or 2 "
+                                     "sequences and copies, within a sequence of " + std::to_string(T) + " and the tokens)");
+    if ((b[4].ptr != nullptr) != (b[6].ptr != nullptr) || (b[4].ptr != nullptr) != (b[7].ptr != nullptr))
+        return fail(TGX_E_SHAPE, "local_embed takes gain, normed and row_sq together or none of them");
+    const uint64_t h = a.hidden;
+    TGX_TRY(holds(b, 0, "frames", (uint64_t)rows * C * F * 4));
+    TGX_TRY(holds(b, 1, "w", h * C * 4));
+    TGX_TRY(holds(b, 2, "bias", h * 4));
+    TGX_TRY(holds(b, 3, "tokens", (uint64_t)(shared ? 1 : rows) * copies * h * 4));
+    TGX_TRY(holds(b, 5, "x0", (uint64_t)a.M * h * 4));
+    if (b[4].ptr) {
+        TGX_TRY(holds(b, 4, "gain", h * 4));
+        TGX_TRY(holds(b, 6, "normed", (uint64_t)a.M_pad * h * 2));
+        TGX_TRY(holds(b, 7, "row_sq", (uint64_t)a.M * LOCAL_SQ * 4));
+    }
+    EmbedArgs e{};
+    e.src = (const float*)b[0].ptr;
+    e.w = (const float*)b[1].ptr;
+    e.bias = (const float*)b[2].ptr;
+    e.copy_src = (const float*)b[3].ptr;
+    e.x0 = (float*)b[5].ptr;
+    e.channels = (int)C;
+    e.frames = (int)F;
+    e.first = (int)first;
+    e.copy_at = (int)copy_at;
+    e.copies = (int)copies;
+    e.guided = (int)guided;
+    e.shared = (int)shared;
+    e.seqs = (int)seqs;
+    e.gain = (const float*)b[4].ptr;
+    e.normed = (uint16_t*)b[6].ptr;
+    e.row_sq = (float*)b[7].ptr;
+    return capture_one("local_embed", [&] { return launch_local_embed(a, e, (int)rows, nullptr, nullptr); }, L);
+}
+
+// cfm_noise (cfm_noise.comp): noise, sampling -> state; constants rows, len. state[r][i] =
+// sampling[r][0] (the row's temperature) noise[r][i], f32 [rows][len].
+tgx_status build_cfm_noise(const Bound* b, const uint32_t* c, Launch* L) {
+    const uint32_t rows = c[0], len = c[1];
+    if (rows == 0 || len == 0 || (uint64_t)rows * len > (1u << 30))
+        return fail(TGX_E_SHAPE, "cfm_noise: " + std::to_string(rows) + " rows of " + std::to_string(len));
+    const uint64_t n = (uint64_t)rows * len;
+    TGX_TRY(holds(b, 0, "noise", n * 4));
+    TGX_TRY(holds(b, 1, "sampling", (uint64_t)rows * 2 * 4));
+    TGX_TRY(holds(b, 2, "state", n * 4));
+    return capture_one("cfm_noise", [&] {
+        return launch_cfm_noise((const float*)b[0].ptr, (const float*)b[1].ptr, (float*)b[2].ptr, (int)rows, (int)len, nullptr, nullptr);
+    }, L);
+}
+
+// dit_euler (dit_euler.comp): x, row_sq, gain, W, bias, sampling -> state (read and written);
+// constants past the stack's: patch_rows, channels, frames, first, dt (f32 bits). The stack's
+// last residual x [tokens][1024] and its sums of squares [tokens][16], normed with the final
+// gain; out_proj (W [channels][1024] in tiles of TGX_TILES_16, bias [channels]) over tokens
+// first .. first + frames - 1 of each patch row's two sequences (the conditional, then the
+// unconditional); CFG-Zero* with the row's guidance scale (sampling [rows][2]: temperature,
+// scale), and state [rows][channels][frames] -= dt guided.
+tgx_status build_dit_euler(const Bound* b, const uint32_t* c, Launch* L) {
+    LocalArgs a;
+    TGX_TRY(local_args(c, &a));
+    const uint32_t* o = c + L_COMMON;
+    const uint32_t rows = o[0], C = o[1], F = o[2], first = o[3];
+    const float dt = as_float(o[4]);
+    if (rows == 0 || (uint64_t)rows * 2 * a.T > (uint64_t)a.M || C == 0 || C % 16 || C > 64 || F == 0 || F > 4 || C * F > 512 ||
+        first + F > (uint32_t)a.T || !std::isfinite(dt))
+        return fail(TGX_E_SHAPE, "dit_euler: " + std::to_string(rows) + " patch rows, frames of " + std::to_string(C) + " channels x " +
+                                     std::to_string(F) + " at token " + std::to_string(first) +
+                                     " (channels a multiple of 16 up to 64, 1 to 4 frames, two sequences a row within the tokens, "
+                                     "a finite dt)");
+    const uint64_t M = a.M, h = a.hidden;
+    TGX_TRY(holds(b, 0, "x", M * h * 4));
+    TGX_TRY(holds(b, 1, "row_sq", M * LOCAL_SQ * 4));
+    TGX_TRY(holds(b, 2, "gain", h * 4));
+    TGX_TRY(holds(b, 3, "w", (uint64_t)C * h * 2));
+    TGX_TRY(holds(b, 4, "bias", (uint64_t)C * 4));
+    TGX_TRY(holds(b, 5, "sampling", (uint64_t)rows * 2 * 4));
+    TGX_TRY(holds(b, 6, "state", (uint64_t)rows * C * F * 4));
+    EulerArgs e{};
+    e.x = (const float*)b[0].ptr;
+    e.row_sq = (const float*)b[1].ptr;
+    e.gain = (const float*)b[2].ptr;
+    e.w = (const uint16_t*)b[3].ptr;
+    e.bias = (const float*)b[4].ptr;
+    e.sampling = (const float*)b[5].ptr;
+    e.state = (float*)b[6].ptr;
+    e.channels = (int)C;
+    e.frames = (int)F;
+    e.first = (int)first;
+    e.dt = dt;
+    return capture_one("dit_euler", [&] { return launch_dit_euler(a, e, (int)rows, nullptr, nullptr); }, L);
+}
+
+// ---- the layers between VoxCPM2's LMs (lm_side.rs:28-38) ----
+
+// gemv_linear (gemv_linear.comp): x0 [, x1], W, bias -> out; constants rows, K0, K1, N, offset,
+// stride, act (0 none, 1 SiLU, 2 the scalar quantizer's levels), levels (f32 bits). out[r][offset
+// + n] = act(W [x0[r]; x1[r]] + bias)[n]: x0 [rows][K0] and x1 [rows][K1] f32 (K1 0 without x1,
+// K0 + K1 up to 4096, each a multiple of 32), W in tiles of TGX_TILES_16 of N rows rounded up to
+// 16 (rows past N zero), out rows `stride` floats apart.
+tgx_status build_gemv_linear(const Bound* b, const uint32_t* c, Launch* L) {
+    const uint32_t rows = c[0], K0 = c[1], K1 = c[2], N = c[3], offset = c[4], stride = c[5], act = c[6];
+    const float levels = as_float(c[7]);
+    if (rows == 0 || rows > (1u << 16) || K0 == 0 || K0 % 32 || K1 % 32 || K0 + K1 > (uint32_t)LINEAR_MAX_K || N == 0 ||
+        N > (1u << 16) || (uint64_t)offset + N > stride || stride > (1u << 20) || act > 2 || (K1 > 0) != (b[1].ptr != nullptr) ||
+        (act == ACT_LEVELS && !(levels > 0.f && std::isfinite(levels))))
+        return fail(TGX_E_SHAPE, "gemv_linear: " + std::to_string(rows) + " rows of " + std::to_string(K0) + " + " + std::to_string(K1) +
+                                     " columns into " + std::to_string(N) + " at " + std::to_string(offset) + " of rows " +
+                                     std::to_string(stride) + " apart, act " + std::to_string(act) +
+                                     " (columns multiples of 32 up to " + std::to_string(LINEAR_MAX_K) +
+                                     " in all, x1 bound when K1 > 0, levels positive)");
+    const uint64_t K = K0 + K1;
+    TGX_TRY(holds(b, 0, "x0", (uint64_t)rows * K0 * 4));
+    if (K1) TGX_TRY(holds(b, 1, "x1", (uint64_t)rows * K1 * 4));
+    TGX_TRY(holds(b, 2, "w", round_up(N, 16) * K * 2));
+    TGX_TRY(holds(b, 3, "bias", (uint64_t)N * 4));
+    TGX_TRY(holds(b, 4, "out", ((uint64_t)(rows - 1) * stride + offset + N) * 4));
+    LinearArgs l{};
+    l.w = (const uint16_t*)b[2].ptr;
+    l.bias = (const float*)b[3].ptr;
+    l.x0 = (const float*)b[0].ptr;
+    l.x1 = (const float*)b[1].ptr;
+    l.out = (float*)b[4].ptr;
+    l.K0 = (int)K0;
+    l.K1 = (int)K1;
+    l.N = (int)N;
+    l.rows = (int)rows;
+    l.offset = (int)offset;
+    l.stride = (int)stride;
+    l.act = (int)act;
+    l.levels = levels;
+    return capture_one("gemv_linear", [&] { return launch_linear("gemv_linear", l, nullptr, nullptr); }, L);
+}
+
+// select_rows (select_rows.comp): flags, a, b -> out; constants rows, K. out[r] = flags[r] ? a[r]
+// : b[r], rows of K f32 values (K a multiple of 4).
+tgx_status build_select_rows(const Bound* b, const uint32_t* c, Launch* L) {
+    const uint32_t rows = c[0], K = c[1];
+    if (rows == 0 || K == 0 || K % 4 || (uint64_t)rows * K > (1u << 30))
+        return fail(TGX_E_SHAPE, "select_rows: " + std::to_string(rows) + " rows of " + std::to_string(K) + " (a multiple of 4)");
+    const uint64_t n = (uint64_t)rows * K * 4;
+    TGX_TRY(holds(b, 0, "flags", (uint64_t)rows * 4));
+    TGX_TRY(holds(b, 1, "a", n));
+    TGX_TRY(holds(b, 2, "b", n));
+    TGX_TRY(holds(b, 3, "out", n));
+    return capture_one("select_rows", [&] {
+        return launch_select_rows((const uint32_t*)b[0].ptr, (const float*)b[1].ptr, (const float*)b[2].ptr, (float*)b[3].ptr, (int)rows,
+                                  (int)K, nullptr, nullptr);
+    }, L);
+}
+
 constexpr tgx_access RD = TGX_READ, WR = TGX_WRITE;
 
 const std::vector<KernelDesc>& kernels() {
@@ -366,6 +1002,136 @@ const std::vector<KernelDesc>& kernels() {
          decode_constants({"advance"}),
          build_rmsnorm},
         {"stream_read", {{"data", RD, TGX_U32, false}, {"out", WR, TGX_U32, false}}, {}, build_stream_read},
+        // The prefill's (prefill.rs:32-81): the GEMMs carry rope_rows, add_norm_rows and
+        // silu_mul_rows as their epilogues.
+        {"norm_rows", {{"x", RD, TGX_F32, false}, {"gain", RD, TGX_F32, false}, {"out", WR, TGX_BF16, false}}, prefill_constants(),
+         build_norm_rows},
+        {"final_norm_rows", {{"x", RD, TGX_F32, false}, {"gain", RD, TGX_F32, false}, {"out", WR, TGX_F32, false}},
+         prefill_constants(), build_final_norm_rows},
+        {"gemm_rope_rows",
+         {{"x", RD, TGX_BF16, false},
+          {"w", RD, TGX_BF16, false},
+          {"row_sq", RD, TGX_F32, true},
+          {"cos", RD, TGX_F32, false},
+          {"sin", RD, TGX_F32, false},
+          {"positions", RD, TGX_U32, false},
+          {"slots", RD, TGX_U32, false},
+          {"table", RD, TGX_U32, false},
+          {"q", WR, TGX_BF16, false},
+          {"kv", WR, TGX_BF16, false}},
+         prefill_constants(),
+         build_gemm_rope_rows},
+        {"attention_rows",
+         {{"q", RD, TGX_BF16, false},
+          {"kv", RD, TGX_BF16, false},
+          {"table", RD, TGX_U32, false},
+          {"tiles", RD, TGX_U32, false},
+          {"attended", WR, TGX_BF16, false}},
+         prefill_constants({"tiles"}),
+         build_attention_rows},
+        {"gemm_add_norm_rows",
+         {{"x", RD, TGX_BF16, false},
+          {"w", RD, TGX_BF16, false},
+          {"residual", RD, TGX_F32, false},
+          {"next_gain", RD, TGX_F32, true},
+          {"out", WR, TGX_F32, false},
+          {"out_n", WR, TGX_BF16, true},
+          {"out_sq", WR, TGX_F32, true}},
+         prefill_constants({"K", "N", "strip_rows", "residual_in"}),
+         build_gemm_add_norm_rows},
+        {"gemm_silu_mul_rows",
+         {{"x", RD, TGX_BF16, false}, {"w", RD, TGX_BF16, false}, {"row_sq", RD, TGX_F32, true}, {"mlp", WR, TGX_BF16, false}},
+         prefill_constants({"K", "N"}),
+         build_gemm_silu_mul_rows},
+        // The local stacks' and the sampler's (local/mod.rs:28-113).
+        {"local_norm",
+         {{"x", RD, TGX_F32, false}, {"gain", RD, TGX_F32, false}, {"normed", WR, TGX_BF16, false}, {"row_sq", WR, TGX_F32, false}},
+         local_constants(),
+         build_local_norm},
+        {"local_qkv_rope",
+         {{"x", RD, TGX_BF16, false},
+          {"w", RD, TGX_BF16, false},
+          {"row_sq", RD, TGX_F32, false},
+          {"cos", RD, TGX_F32, false},
+          {"sin", RD, TGX_F32, false},
+          {"q", WR, TGX_BF16, false},
+          {"k", WR, TGX_BF16, false},
+          {"v", WR, TGX_BF16, false}},
+         local_constants(),
+         build_local_qkv_rope},
+        {"local_attention",
+         {{"q", RD, TGX_BF16, false}, {"k", RD, TGX_BF16, false}, {"v", RD, TGX_BF16, false}, {"attended", WR, TGX_BF16, false}},
+         local_constants(),
+         build_local_attention},
+        {"local_partial", {{"x", RD, TGX_BF16, false}, {"w", RD, TGX_BF16, false}, {"partial", WR, TGX_F32, false}},
+         local_constants({"K", "N", "parts"}), build_local_partial},
+        {"local_add_norm",
+         {{"partial", RD, TGX_F32, true},
+          {"residual", RD, TGX_F32, false},
+          {"gain", RD, TGX_F32, false},
+          {"sum", WR, TGX_F32, true},
+          {"normed", WR, TGX_BF16, false},
+          {"row_sq", WR, TGX_F32, false}},
+         local_constants({"parts"}),
+         build_local_add_norm},
+        {"local_final_norm",
+         {{"partial", RD, TGX_F32, true},
+          {"residual", RD, TGX_F32, false},
+          {"gain", RD, TGX_F32, false},
+          {"sum", WR, TGX_F32, true},
+          {"out", WR, TGX_F32, false}},
+         local_constants({"parts"}),
+         build_local_final_norm},
+        {"local_gemm_add_norm",
+         {{"x", RD, TGX_BF16, false},
+          {"w", RD, TGX_BF16, false},
+          {"residual", RD, TGX_F32, false},
+          {"next_gain", RD, TGX_F32, true},
+          {"sum", WR, TGX_F32, false},
+          {"normed", WR, TGX_BF16, true},
+          {"row_sq", WR, TGX_F32, true}},
+         local_constants({"K", "N", "parts"}),
+         build_local_gemm_add_norm},
+        {"local_gate_up",
+         {{"x", RD, TGX_BF16, false}, {"w", RD, TGX_BF16, false}, {"row_sq", RD, TGX_F32, false}, {"mlp", WR, TGX_BF16, false}},
+         local_constants(),
+         build_local_gate_up},
+        {"local_embed",
+         {{"frames", RD, TGX_F32, false},
+          {"w", RD, TGX_F32, false},
+          {"bias", RD, TGX_F32, false},
+          {"tokens", RD, TGX_F32, false},
+          {"gain", RD, TGX_F32, true},
+          {"x0", WR, TGX_F32, false},
+          {"normed", WR, TGX_BF16, true},
+          {"row_sq", WR, TGX_F32, true}},
+         local_constants({"patch_rows", "channels", "frames", "first", "copy_at", "copies", "guided", "shared", "seqs"}),
+         build_local_embed},
+        {"cfm_noise", {{"noise", RD, TGX_F32, false}, {"sampling", RD, TGX_F32, false}, {"state", WR, TGX_F32, false}}, {"rows", "len"},
+         build_cfm_noise},
+        {"dit_euler",
+         {{"x", RD, TGX_F32, false},
+          {"row_sq", RD, TGX_F32, false},
+          {"gain", RD, TGX_F32, false},
+          {"w", RD, TGX_BF16, false},
+          {"bias", RD, TGX_F32, false},
+          {"sampling", RD, TGX_F32, false},
+          {"state", WR, TGX_F32, false}},
+         local_constants({"patch_rows", "channels", "frames", "first", "dt"}),
+         build_dit_euler},
+        // The layers between VoxCPM2's LMs (lm_side.rs:28-38) and the prompt's row select (prompt.rs:55-60).
+        {"gemv_linear",
+         {{"x0", RD, TGX_F32, false},
+          {"x1", RD, TGX_F32, true},
+          {"w", RD, TGX_BF16, false},
+          {"bias", RD, TGX_F32, false},
+          {"out", WR, TGX_F32, false}},
+         {"rows", "K0", "K1", "N", "offset", "stride", "act", "levels"},
+         build_gemv_linear},
+        {"select_rows",
+         {{"flags", RD, TGX_U32, false}, {"a", RD, TGX_F32, false}, {"b", RD, TGX_F32, false}, {"out", WR, TGX_F32, false}},
+         {"rows", "K"},
+         build_select_rows},
     };
     return table;
 }
@@ -649,7 +1415,7 @@ tgx_status tgx_program_launch(tgx_program* prog, const tgx_dispatch* d) {
     np.gridDim = L->k.grid;
     np.blockDim = L->k.block;
     np.sharedMemBytes = L->k.lds;
-    np.kernelParams = L->params;
+    np.kernelParams = L->kernel_params();
     np.extra = nullptr;
     hipGraphNode_t node = nullptr;
     TGX_HIP(hipGraphAddKernelNode(&node, p->graph, p->after.data(), p->after.size(), &np));
@@ -696,9 +1462,8 @@ tgx_status tgx_program_start(tgx_program* prog) {
     if (p->timed) {
         // Dispatch by dispatch in order, each between events of its own.
         for (size_t i = 0; i < p->launches.size(); ++i) {
-            const Launch& L = *p->launches[i];
-            TGX_HIP(hipExtLaunchKernel(L.k.func, L.k.grid, L.k.block, const_cast<void**>(L.params), L.k.lds, s, p->t_start[i],
-                                       p->t_stop[i], 0));
+            Launch& L = *p->launches[i];
+            TGX_HIP(hipExtLaunchKernel(L.k.func, L.k.grid, L.k.block, L.kernel_params(), L.k.lds, s, p->t_start[i], p->t_stop[i], 0));
         }
         p->timings_valid = true;
     } else {
