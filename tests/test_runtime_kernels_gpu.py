@@ -201,6 +201,36 @@ def test_a_prefill_composed_by_kernel_name_is_tgx_prefill_runs_bit_for_bit(ctx, 
     stack.close()
 
 
+def test_a_long_prefill_composed_by_kernel_name_is_tgx_prefill_runs_bit_for_bit(ctx):
+    """2 runs of 6700 positions (13,400 rows, 13,568 padded; the GEMMs past one round of
+    workgroups, the attention's tiles reaching 105 cache blocks): every output bit and every
+    cache bit as tgx_prefill_runs gives them."""
+    import tgx
+    from tgx.synth import StackSpec, embeddings, stack_weights
+
+    spec = StackSpec(layers=2, seed=19)
+    cap, slots, n = 6784, 2, 6700
+    print("[prefill by name] 2 x 6700 positions", flush=True)
+    stack = PrefillStack(ctx, spec, cap, slots, 4)
+    shape = tgx.Shape(hidden=spec.hidden, inner=spec.inner, heads=spec.heads, kv_heads=spec.kv_heads, head_dim=spec.head_dim,
+                      layers=spec.layers, capacity=cap, eps=spec.eps, rope_theta=spec.rope_theta)
+    dec = tgx.Decoder(ctx, shape, tgx.Batch(rows=2, slots=slots))
+    dec.load_all(stack_weights(spec))
+    x = embeddings(11, "long-prefill-by-name", 2 * n, spec.hidden)
+    runs = [(0, 0, n), (1, 0, n)]
+    got = stack.run(runs, x)
+    want = dec.prefill_runs(runs, x)
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for s in range(slots):
+        gk, gv = stack.read_cache(s, n)
+        wk, wv = dec.read_cache(s, n)
+        assert np.array_equal(gk.view(np.uint32), wk.view(np.uint32)), f"keys of slot {s}"
+        assert np.array_equal(gv.view(np.uint32), wv.view(np.uint32)), f"values of slot {s}"
+    dec.close()
+    stack.close()
+
+
 FEAT, FRAMES = 64, 4
 MU_TOKENS, TIME_AT, COND_AT = 2, 2, 3  # a sequence: mu, mu, time, cond frames, x frames
 
