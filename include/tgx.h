@@ -66,6 +66,24 @@ tgx_status tgx_context_create(int device, tgx_context** out);
 void tgx_context_destroy(tgx_context* ctx);
 /* Context::report. */
 tgx_status tgx_context_report(const tgx_context* ctx, tgx_device_report* out);
+/* Context::set_fence_spin (crates/vulkan/src/context.rs:467-474, its wait Inner::wait_for,
+ * :116-133): every wait for the context's work (tgx_decoder_wait, tgx_program_wait and the
+ * sampler's, LM side's, encoder's and patch step's) polls for up to `ns` nanoseconds before it
+ * sleeps between polls, 20 µs apart, 60 s at most in all; 0, the default, sleeps at once. */
+tgx_status tgx_context_set_fence_spin(tgx_context* ctx, uint64_t ns);
+/* Calibration (context.rs:73-88): the GPU's clock read `ticks` while the host's CLOCK_MONOTONIC
+ * read `monotonic_ns`, give or take `deviation_ns`; `period_ns` nanoseconds a tick. */
+typedef struct {
+    uint64_t ticks;
+    uint64_t monotonic_ns;
+    uint64_t deviation_ns;
+    float period_ns;
+} tgx_calibration;
+/* Context::calibrate (context.rs:445-465): the GPU's constant-rate wall clock
+ * (hipDeviceAttributeWallClockRate) read by a one-wave kernel between two readings of the host's
+ * clock, once the context's stream is idle: monotonic_ns their midpoint, deviation_ns half their
+ * distance (a launch and a wait, tens of µs). */
+tgx_status tgx_context_calibrate(tgx_context* ctx, tgx_calibration* out);
 
 /* The stream-read floor (kernels/glsl/stream_read.comp:1-23, as decode_timing.rs:430-441 reports
  * it): a buffer of `bytes` (rounded down to 32 KiB) read once a launch, 16 bytes a load, `times`
@@ -635,6 +653,16 @@ tgx_status tgx_program_run(tgx_program* p);
 tgx_status tgx_program_timings(tgx_program* p, int max, tgx_timing* out, int* n);
 /* Recording::elapsed (recording.rs:676-681): the last run's GPU time, from events around it. */
 tgx_status tgx_program_elapsed_ms(tgx_program* p, float* ms);
+/* Recording::ends (recording.rs:681-686): the GPU clock's ticks (tgx_calibration's clock) when
+ * the last run started and when it ended, which a calibration places on the host's clock:
+ * the run's events taken from an anchor the start re-takes at most once a second (the clock read
+ * by a one-wave kernel, an event after it), so within that kernel's few µs. TGX_E_BUSY before a
+ * run has finished. */
+tgx_status tgx_program_ends(tgx_program* p, uint64_t ends[2]);
+/* Recording::replace_program (recording.rs:219-244): waits for the program, then drops its
+ * dispatches and the memories they bound; it takes dispatches again (tgx_program_launch, then
+ * tgx_program_end), timed or not, in their place. */
+tgx_status tgx_program_reset(tgx_program* p, int timed);
 tgx_status tgx_program_destroy(tgx_program* p);
 
 /* Recording::copy_in / copy_out (recording.rs:522-597): regions copied from `src` to `dst` on the

@@ -267,3 +267,110 @@ def test_a_recording_refuses_on_the_host_what_the_kernels_could_not_run(ctx):
     p.close()
     for m in (q, kv, pos, row_table, att):
         m.close()
+
+
+def test_a_calibration_places_a_programs_ends_on_the_hosts_clock(ctx):
+    """Context::calibrate and Recording::ends (the reference's crates/vulkan/tests/recording.rs:
+    346-372): two calibrations 50 ms apart measure the same time on both clocks; a run's ends are
+    in order, apart by its elapsed time, and placed on the host's clock they fall between the
+    host's readings before its start and after its wait."""
+    import time
+
+    import tgx.runtime as rt
+
+    a = ctx.calibrate()
+    time.sleep(0.05)
+    b = ctx.calibrate()
+    period = a["period_ns"]
+    assert period > 0 and b["period_ns"] == period
+    host = b["monotonic_ns"] - a["monotonic_ns"]
+    gpu = (b["ticks"] - a["ticks"]) * period
+    assert abs(gpu - host) <= a["deviation_ns"] + b["deviation_ns"] + 0.001 * host + 20_000, (gpu, host, a, b)
+    data = np.random.default_rng(6).integers(0, 2**32, 16 << 20, dtype=np.uint32)  # 64 MiB
+    m, o = rt.Memory(ctx, data.nbytes), rt.Memory(ctx, 8192 * 4)  # a word a wave: 2048 workgroups of 4
+    m.write(data)
+    p = rt.Program(ctx)
+    p.dispatch("stream_read", [m, o], [])
+    p.end()
+    with pytest.raises(Exception):
+        p.ends()  # no run yet
+    p.run()
+    cal = ctx.calibrate()
+    before = time.monotonic_ns()
+    p.start()
+    p.wait()
+    after = time.monotonic_ns()
+    e0, e1 = p.ends()
+    assert e1 > e0
+    ms = p.elapsed_ms()
+    assert abs((e1 - e0) * period * 1e-6 - ms) <= 0.01 + 0.01 * ms, (e0, e1, ms)
+    on_host = lambda t: cal["monotonic_ns"] + (t - cal["ticks"]) * period
+    slack = cal["deviation_ns"] + 50_000
+    assert before - slack <= on_host(e0) <= on_host(e1) <= after + slack, (before, on_host(e0), on_host(e1), after)
+    p.close()
+    m.close()
+    o.close()
+
+
+def test_a_reset_program_takes_new_dispatches_and_lets_its_old_memory_go(ctx):
+    """Recording::replace_program (recording.rs:219-244; the reference's recording.rs:260-280 test):
+    a program re-recorded in place runs its new dispatches, timed when asked, and the memory only
+    its old dispatches bound may be freed."""
+    import tgx
+    import tgx.runtime as rt
+
+    rng = np.random.default_rng(7)
+    a = rng.integers(0, 2**32, 16384, dtype=np.uint32)
+    b = rng.integers(0, 2**32, 32768, dtype=np.uint32)
+    ma, mb = rt.Memory(ctx, a.nbytes), rt.Memory(ctx, b.nbytes)
+    ma.write(a)
+    mb.write(b)
+    oa, ob = rt.Memory(ctx, 8 * 4), rt.Memory(ctx, 16 * 4)
+    p = rt.Program(ctx)
+    p.dispatch("stream_read", [ma, oa], [])
+    p.end()
+    p.run()
+    assert np.array_equal(oa.read(np.uint32, 8), stream_words(a))
+    with pytest.raises(tgx.TgxError) as e:
+        ma.close()
+    assert e.value.kind == "busy"
+    p.reset(timed=True)
+    ma.close()
+    p.dispatch("stream_read", [mb, ob], [])
+    p.end()
+    p.run()
+    assert np.array_equal(ob.read(np.uint32, 16), stream_words(b))
+    assert [n for n, _ in p.timings()] == ["stream_read"]
+    p.close()
+    for m in (mb, oa, ob):
+        m.close()
+
+
+def test_a_fence_spin_changes_how_waits_poll_and_not_what_they_give(ctx):
+    """Context::set_fence_spin (context.rs:467-474): waits that poll for 2 ms before sleeping give
+    the same words as waits that sleep at once, for programs and for a decoder's steps."""
+    import tgx
+    import tgx.runtime as rt
+    from tgx.synth import StackSpec, embeddings
+
+    data = np.random.default_rng(8).integers(0, 2**32, 16384, dtype=np.uint32)
+    m, o = rt.Memory(ctx, data.nbytes), rt.Memory(ctx, 8 * 4)
+    m.write(data)
+    p = rt.Program(ctx)
+    p.dispatch("stream_read", [m, o], [])
+    p.end()
+    spec = StackSpec(layers=2, seed=5)
+    x = embeddings(9, "fence-spin", 2, spec.hidden)
+    outs = []
+    for spin in (2_000_000, 0):
+        ctx.set_fence_spin(spin)
+        p.run()
+        dec = reference_decoder(ctx, spec, 64, 1)
+        outs.append((o.read(np.uint32, 8), dec.step(0, x[0]), dec.step(1, x[1])))
+        dec.close()
+    for got, want in zip(outs[0], outs[1]):
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(outs[1][0], stream_words(data))
+    p.close()
+    m.close()
+    o.close()

@@ -740,6 +740,17 @@ KernelLaunch stream_read_launch(size_t bytes) {
     return k;
 }
 
+namespace {
+__global__ void __launch_bounds__(WAVE) read_clock(uint64_t* out) {
+    if (threadIdx.x == 0) *out = wall_clock64();
+}
+}  // namespace
+
+hipError_t launch_read_clock(uint64_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL(read_clock, dim3(1), dim3(WAVE), 0, stream, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_stream_read(const void* data, size_t bytes, uint32_t* out, hipStream_t stream) {
     if (bytes == 0 || bytes % stream_read_unit()) return hipErrorInvalidValue;
     const uint4* d = (const uint4*)data;

@@ -113,5 +113,8 @@ hipError_t launch_final_norm(const DecodeArgs& a, const float* x, const float* g
 // stream_read_unit()) read once, one word a wave of their XOR into out (bytes / 4096 words).
 size_t stream_read_unit();
 hipError_t launch_stream_read(const void* data, size_t bytes, uint32_t* out, hipStream_t stream);
+// One wave reads the GPU's constant-rate wall clock (hipDeviceAttributeWallClockRate ticks a
+// second) into *out, on `stream`.
+hipError_t launch_read_clock(uint64_t* out, hipStream_t stream);
 
 }  // namespace tgx

@@ -51,18 +51,6 @@ tgx_status record(hipStream_t st, const char* what, F enqueue, hipGraphExec_t* e
     return upload_graph(*exec, st);
 }
 
-// Waits for `ev` (60 s at most, as Submission::wait, recording.rs:747).
-tgx_status wait_event(hipEvent_t ev, const char* what) {
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(60);
-    while (true) {
-        hipError_t q = hipEventQuery(ev);
-        if (q == hipSuccess) return TGX_OK;
-        if (q != hipErrorNotReady) return fail(TGX_E_HIP, std::string(what) + ": " + hipGetErrorString(q));
-        if (std::chrono::steady_clock::now() > deadline) return fail(TGX_E_TIMEOUT, std::string(what) + " took over 60 s");
-        std::this_thread::sleep_for(std::chrono::microseconds(20));
-    }
-}
-
 }  // namespace
 
 LocalArgs Encoder::args() const {
@@ -238,7 +226,7 @@ tgx_status encoder_encode(Encoder* e, const float* patch, float* out) {
     TGX_HIP(hipEventRecord(e->ev_start, st));
     TGX_HIP(hipGraphLaunch(e->exec, st));
     TGX_HIP(hipEventRecord(e->ev_end, st));
-    TGX_TRY(wait_event(e->ev_end, "the encoding"));
+    TGX_TRY(wait_event(e->ctx, e->ev_end, "the encoding"));
     const size_t n = (size_t)e->rows * e->shape.hidden;
     TGX_HIP(hipMemcpy(out, e->embedding, n * 4, hipMemcpyDeviceToHost));
     for (size_t i = 0; i < n; ++i)
@@ -391,7 +379,7 @@ tgx_status patch_step_launch(PatchStep* p, int times, int advance) {
 tgx_status patch_step_wait(PatchStep* p) {
     if (!p) return fail(TGX_E_ARG, "null patch step");
     if (!p->pending) return TGX_OK;
-    tgx_status r = wait_event(p->ev_end, "the patch step");
+    tgx_status r = wait_event(p->side->ctx, p->ev_end, "the patch step");
     if (r != TGX_E_TIMEOUT) p->pending = false;
     return r;
 }

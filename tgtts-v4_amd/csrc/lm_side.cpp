@@ -320,19 +320,9 @@ tgx_status lm_side_launch(LmSide* s, int times, int advance) {
 tgx_status lm_side_wait(LmSide* s) {
     if (!s) return fail(TGX_E_ARG, "null LM side");
     if (!s->pending) return TGX_OK;
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(60);
-    while (true) {
-        hipError_t q = hipEventQuery(s->ev_end);
-        if (q == hipSuccess) break;
-        if (q != hipErrorNotReady) {
-            s->pending = false;
-            return fail(TGX_E_HIP, std::string("the LM side: ") + hipGetErrorString(q));
-        }
-        if (std::chrono::steady_clock::now() > deadline) return fail(TGX_E_TIMEOUT, "the LM side took over 60 s");
-        std::this_thread::sleep_for(std::chrono::microseconds(20));
-    }
-    s->pending = false;
-    return TGX_OK;
+    const tgx_status r = wait_event(s->ctx, s->ev_end, "the LM side");
+    if (r != TGX_E_TIMEOUT) s->pending = false;
+    return r;
 }
 
 tgx_status lm_side_read(LmSide* s, const char* tensor, float* out, size_t count) {

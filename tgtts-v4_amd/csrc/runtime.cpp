@@ -116,6 +116,9 @@ tgx_status context_create(int device, Context** out) {
         return fail(TGX_E_HIP, std::string("context: ") + hipGetErrorString(e));
     }
     ctx->lds_bytes = ctx->prop.sharedMemPerBlock;
+    int clock_khz = 0;
+    if (hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device) == hipSuccess && clock_khz > 0)
+        ctx->tick_ns = 1e6 / (double)clock_khz;
     e = decode_prepare(ctx->lds_bytes);
     if (e == hipSuccess) e = prefill_prepare(ctx->lds_bytes);
     if (e == hipSuccess) e = heads_prepare(ctx->lds_bytes);
@@ -142,7 +145,21 @@ void context_destroy(Context* ctx) {
     if (!ctx) return;
     hipSetDevice(ctx->device);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
+    if (ctx->clock_host) hipHostFree(ctx->clock_host);
     delete ctx;
+}
+
+tgx_status wait_event(const Context* ctx, hipEvent_t ev, const char* what) {
+    const auto begin = std::chrono::steady_clock::now();
+    const auto spin = std::chrono::nanoseconds(ctx ? ctx->fence_spin_ns.load(std::memory_order_relaxed) : 0);
+    while (true) {
+        const hipError_t q = hipEventQuery(ev);
+        if (q == hipSuccess) return TGX_OK;
+        if (q != hipErrorNotReady) return fail(TGX_E_HIP, std::string(what) + ": " + hipGetErrorString(q));
+        const auto waited = std::chrono::steady_clock::now() - begin;
+        if (waited > std::chrono::seconds(60)) return fail(TGX_E_TIMEOUT, std::string(what) + " did not finish in 60 s");
+        if (waited >= spin) std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
 }
 
 // ---- shapes ----
@@ -750,21 +767,9 @@ tgx_status decoder_start(Decoder* d) {
 tgx_status decoder_wait(Decoder* d) {
     if (!d) return fail(TGX_E_ARG, "null decoder");
     if (!d->pending) return TGX_OK;
-    // Spin, then sleep, for at most 60 s (crates/vulkan/src/context.rs:24,120-136).
-    const auto begin = std::chrono::steady_clock::now();
-    for (int i = 0;; ++i) {
-        hipError_t e = hipEventQuery(d->ev_done);
-        if (e == hipSuccess) break;
-        if (e != hipErrorNotReady) {
-            d->pending = false;
-            return fail(TGX_E_HIP, std::string("waiting for the step: ") + hipGetErrorString(e));
-        }
-        if (std::chrono::steady_clock::now() - begin > std::chrono::seconds(60))
-            return fail(TGX_E_TIMEOUT, "the step did not finish in 60 s");
-        if (i > 1000) std::this_thread::sleep_for(std::chrono::microseconds(50));
-    }
-    d->pending = false;
-    return TGX_OK;
+    const tgx_status r = wait_event(d->ctx, d->ev_done, "the step");
+    if (r != TGX_E_TIMEOUT) d->pending = false;
+    return r;
 }
 
 tgx_status decoder_output(Decoder* d, float* out) {

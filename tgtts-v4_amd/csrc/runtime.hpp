@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <functional>
 #include <string>
 #include <map>
@@ -36,7 +37,18 @@ struct Context {
     hipDeviceProp_t prop{};
     size_t lds_bytes = 0;  // LDS a workgroup may take
     void* scratch = nullptr;  // the device's prefill scratch (PREFILL_SCRATCH_BYTES), its device address
+    // How long a wait for the context's work polls before it sleeps between polls, in ns
+    // (tgx_context_set_fence_spin; 0 sleeps at once).
+    std::atomic<uint64_t> fence_spin_ns{0};
+    double tick_ns = 10.0;            // a tick of the GPU's wall clock (read_clock), in ns
+    uint64_t* clock_host = nullptr;   // pinned host word read_clock writes for tgx_context_calibrate
 };
+
+// Waits for `ev`, recorded on the context's stream: polls it without pause for the context's
+// fence spin, then every 20 µs, for 60 s at most (Inner::wait_for, crates/vulkan/src/context.rs:
+// 116-133, and its FENCE_TIMEOUT_NS). TGX_E_HIP for an error the event reports, TGX_E_TIMEOUT
+// past 60 s, each naming `what`.
+tgx_status wait_event(const Context* ctx, hipEvent_t ev, const char* what);
 
 // decode::Shape, checked against what the kernels cover.
 struct Shape {

@@ -15,6 +15,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <ctime>
 #include <memory>
 #include <string>
 #include <thread>
@@ -1163,7 +1164,36 @@ struct Program {
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
     std::vector<hipEvent_t> t_start, t_stop;
     bool timings_valid = false;
+    bool ran = false;  // the last run has finished
+    // The GPU clock's ticks at `origin`, an event recorded right after a one-wave kernel read the
+    // clock into clock_host (re-taken by a start at most once a second): the run's events become
+    // ticks from it (tgx_program_ends).
+    hipEvent_t origin = nullptr;
+    uint64_t* clock_host = nullptr;
+    std::chrono::steady_clock::time_point origin_at{};
+    bool origin_set = false;
 };
+
+// Drops what the program recorded: its launches, graph, timing events and the bindings it holds.
+static void release_program(Program* p) {
+    for (tgx_memory* m : p->memories) --m->programs;
+    p->memories.clear();
+    p->launches.clear();
+    p->nodes.clear();
+    p->frontier.clear();
+    p->after.clear();
+    if (p->exec) hipGraphExecDestroy(p->exec);
+    if (p->graph) hipGraphDestroy(p->graph);
+    p->exec = nullptr;
+    p->graph = nullptr;
+    for (hipEvent_t e : p->t_start) if (e) hipEventDestroy(e);
+    for (hipEvent_t e : p->t_stop) if (e) hipEventDestroy(e);
+    p->t_start.clear();
+    p->t_stop.clear();
+    p->timings_valid = false;
+    p->ran = false;
+    p->ended = false;
+}
 
 }  // namespace tgx
 
@@ -1350,8 +1380,12 @@ tgx_status tgx_program_begin(tgx_context* ctx, int timed, tgx_program** out) {
     hipError_t e = hipGraphCreate(&p->graph, 0);
     if (e == hipSuccess) e = hipEventCreate(&p->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&p->ev_end);
+    if (e == hipSuccess) e = hipEventCreate(&p->origin);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&p->clock_host, sizeof(uint64_t), hipHostMallocDefault);
     if (e != hipSuccess) {
         if (p->ev_start) hipEventDestroy(p->ev_start);
+        if (p->ev_end) hipEventDestroy(p->ev_end);
+        if (p->origin) hipEventDestroy(p->origin);
         if (p->graph) hipGraphDestroy(p->graph);
         delete p;
         return fail(TGX_E_HIP, std::string("starting a program: ") + hipGetErrorString(e));
@@ -1458,7 +1492,17 @@ tgx_status tgx_program_start(tgx_program* prog) {
     if (!p->ended) return fail(TGX_E_BUSY, "the program is still recording: tgx_program_end first");
     if (p->pending) return fail(TGX_E_BUSY, "the program runs");
     hipStream_t s = p->ctx->stream;
+    const auto now = std::chrono::steady_clock::now();
+    if (!p->origin_set || now - p->origin_at > std::chrono::seconds(1)) {
+        // The clock's reading for tgx_program_ends, anchored close to the run (an event's time
+        // relative to another is a float of milliseconds).
+        TGX_HIP(launch_read_clock(p->clock_host, s));
+        TGX_HIP(hipEventRecord(p->origin, s));
+        p->origin_at = now;
+        p->origin_set = true;
+    }
     TGX_HIP(hipEventRecord(p->ev_start, s));
+    p->ran = false;
     if (p->timed) {
         // Dispatch by dispatch in order, each between events of its own.
         for (size_t i = 0; i < p->launches.size(); ++i) {
@@ -1480,23 +1524,12 @@ tgx_status tgx_program_wait(tgx_program* prog) {
     if (!prog) return fail(TGX_E_ARG, "null program");
     Program* p = prog->p;
     if (!p->pending) return TGX_OK;
-    // Spin, then sleep, for at most 60 s (crates/vulkan/src/context.rs:24,120-136).
-    const auto begin = std::chrono::steady_clock::now();
-    for (int i = 0;; ++i) {
-        hipError_t e = hipEventQuery(p->ev_end);
-        if (e == hipSuccess) break;
-        if (e != hipErrorNotReady) {
-            for (tgx_memory* m : p->memories) --m->running;
-            p->pending = false;
-            return fail(TGX_E_HIP, std::string("waiting for the program: ") + hipGetErrorString(e));
-        }
-        if (std::chrono::steady_clock::now() - begin > std::chrono::seconds(60))
-            return fail(TGX_E_TIMEOUT, "the program did not finish in 60 s");
-        if (i > 1000) std::this_thread::sleep_for(std::chrono::microseconds(50));
-    }
+    const tgx_status r = wait_event(p->ctx, p->ev_end, "the program");
+    if (r == TGX_E_TIMEOUT) return r;  // still running: it stays pending
     for (tgx_memory* m : p->memories) --m->running;
     p->pending = false;
-    return TGX_OK;
+    if (r == TGX_OK) p->ran = true;
+    return r;
 }
 
 tgx_status tgx_program_run(tgx_program* prog) {
@@ -1536,16 +1569,67 @@ tgx_status tgx_program_destroy(tgx_program* prog) {
     // A program's drop waits for it (recording.rs:730-760).
     tgx_status st = tgx_program_wait(prog);
     if (st == TGX_E_TIMEOUT) return st;  // still running: nothing it uses may go
-    for (tgx_memory* m : p->memories) --m->programs;
-    if (p->exec) hipGraphExecDestroy(p->exec);
-    if (p->graph) hipGraphDestroy(p->graph);
-    for (hipEvent_t e : p->t_start) if (e) hipEventDestroy(e);
-    for (hipEvent_t e : p->t_stop) if (e) hipEventDestroy(e);
+    release_program(p);
     hipEventDestroy(p->ev_start);
     hipEventDestroy(p->ev_end);
+    hipEventDestroy(p->origin);
+    hipHostFree(p->clock_host);
     delete p;
     delete prog;
     return st;
+}
+
+tgx_status tgx_program_ends(tgx_program* prog, uint64_t ends[2]) {
+    clear_error();
+    if (!prog || !ends) return fail(TGX_E_ARG, "null program or ends");
+    Program* p = prog->p;
+    if (p->pending || !p->ran) return fail(TGX_E_BUSY, "the ends of a program not run to the end");
+    float ms[2] = {0.f, 0.f};
+    TGX_HIP(hipEventElapsedTime(&ms[0], p->origin, p->ev_start));
+    TGX_HIP(hipEventElapsedTime(&ms[1], p->origin, p->ev_end));
+    for (int i = 0; i < 2; ++i) ends[i] = *p->clock_host + (uint64_t)std::llround((double)ms[i] * 1e6 / p->ctx->tick_ns);
+    return TGX_OK;
+}
+
+tgx_status tgx_program_reset(tgx_program* prog, int timed) {
+    clear_error();
+    if (!prog) return fail(TGX_E_ARG, "null program");
+    Program* p = prog->p;
+    TGX_TRY(tgx_program_wait(prog));
+    release_program(p);
+    p->timed = timed != 0;
+    TGX_HIP(hipGraphCreate(&p->graph, 0));
+    return TGX_OK;
+}
+
+tgx_status tgx_context_set_fence_spin(tgx_context* ctx, uint64_t ns) {
+    clear_error();
+    if (!ctx) return fail(TGX_E_ARG, "null context");
+    ctx->ctx->fence_spin_ns.store(ns, std::memory_order_relaxed);
+    return TGX_OK;
+}
+
+tgx_status tgx_context_calibrate(tgx_context* ctx, tgx_calibration* out) {
+    clear_error();
+    if (!ctx || !out) return fail(TGX_E_ARG, "null context or out");
+    Context* c = ctx->ctx;
+    if (!c->clock_host) TGX_HIP(hipHostMalloc((void**)&c->clock_host, sizeof(uint64_t), hipHostMallocDefault));
+    hipStream_t s = c->stream;
+    TGX_HIP(hipStreamSynchronize(s));  // nothing queued ahead of the reading
+    auto monotonic = [] {
+        timespec t{};
+        clock_gettime(CLOCK_MONOTONIC, &t);
+        return (uint64_t)t.tv_sec * 1000000000ull + (uint64_t)t.tv_nsec;
+    };
+    const uint64_t before = monotonic();
+    TGX_HIP(launch_read_clock(c->clock_host, s));
+    TGX_HIP(hipStreamSynchronize(s));
+    const uint64_t after = monotonic();
+    out->ticks = *c->clock_host;
+    out->monotonic_ns = before + (after - before) / 2;
+    out->deviation_ns = (after - before + 1) / 2;
+    out->period_ns = (float)c->tick_ns;
+    return TGX_OK;
 }
 
 tgx_status tgx_copy_regions(tgx_context* ctx, tgx_memory* dst, tgx_memory* src, const tgx_region* regions, int n) {

@@ -441,19 +441,9 @@ tgx_status sampler_launch(Sampler* s, int times) {
 tgx_status sampler_wait(Sampler* s) {
     if (!s) return fail(TGX_E_ARG, "null sampler");
     if (!s->pending) return TGX_OK;
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::seconds(60);
-    while (true) {
-        hipError_t q = hipEventQuery(s->ev_end);
-        if (q == hipSuccess) break;
-        if (q != hipErrorNotReady) {
-            s->pending = false;
-            return fail(TGX_E_HIP, std::string("the sample: ") + hipGetErrorString(q));
-        }
-        if (std::chrono::steady_clock::now() > deadline) return fail(TGX_E_TIMEOUT, "the sample took over 60 s");
-        std::this_thread::sleep_for(std::chrono::microseconds(20));
-    }
-    s->pending = false;
-    return TGX_OK;
+    const tgx_status r = wait_event(s->ctx, s->ev_end, "the sample");
+    if (r != TGX_E_TIMEOUT) s->pending = false;
+    return r;
 }
 
 tgx_status sampler_read(Sampler* s, float* patch) {

@@ -96,6 +96,11 @@ class _Timing(ctypes.Structure):
     _fields_ = [("label", ctypes.c_char * 32), ("ms", ctypes.c_float)]
 
 
+class _Calibration(ctypes.Structure):
+    _fields_ = [("ticks", ctypes.c_uint64), ("monotonic_ns", ctypes.c_uint64), ("deviation_ns", ctypes.c_uint64),
+                ("period_ns", ctypes.c_float)]
+
+
 class _Report(ctypes.Structure):
     _fields_ = [
         ("name", ctypes.c_char * 64),
@@ -277,6 +282,8 @@ def library() -> ctypes.CDLL:
     lib.tgx_context_destroy.argtypes = [P]
     lib.tgx_context_destroy.restype = None
     lib.tgx_context_report.argtypes = [P, ctypes.POINTER(_Report)]
+    lib.tgx_context_set_fence_spin.argtypes = [P, ctypes.c_uint64]
+    lib.tgx_context_calibrate.argtypes = [P, ctypes.POINTER(_Calibration)]
     lib.tgx_stream_read.argtypes = [P, ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
     lib.tgx_decoder_create.argtypes = [P, ctypes.POINTER(_Shape), ctypes.POINTER(_Batch), ctypes.POINTER(P)]
     lib.tgx_decoder_destroy.argtypes = [P]
@@ -509,6 +516,18 @@ class Context:
             "memory_bytes": r.memory_bytes,
             "wavefront": r.wavefront,
         }
+
+    def set_fence_spin(self, ns: int) -> None:
+        """Context::set_fence_spin: every wait for this context's work polls for up to `ns`
+        nanoseconds before it sleeps between polls (0, the default, sleeps at once)."""
+        _check(library().tgx_context_set_fence_spin(self._h, int(ns)))
+
+    def calibrate(self) -> dict:
+        """Context::calibrate: the GPU clock's `ticks` read while CLOCK_MONOTONIC read
+        `monotonic_ns` (give or take `deviation_ns`), `period_ns` nanoseconds a tick."""
+        c = _Calibration()
+        _check(library().tgx_context_calibrate(self._h, ctypes.byref(c)))
+        return {"ticks": c.ticks, "monotonic_ns": c.monotonic_ns, "deviation_ns": c.deviation_ns, "period_ns": c.period_ns}
 
     def stream_read(self, nbytes: int, times: int = 10) -> dict:
         """The stream-read floor (stream_read.comp): `nbytes` read once a launch, the best and mean

@@ -85,6 +85,8 @@ def _lib() -> ctypes.CDLL:
     lib.tgx_program_timings.argtypes = [P, ctypes.c_int, ctypes.POINTER(_Timing), ctypes.POINTER(ctypes.c_int)]
     lib.tgx_program_elapsed_ms.argtypes = [P, ctypes.POINTER(ctypes.c_float)]
     lib.tgx_program_destroy.argtypes = [P]
+    lib.tgx_program_ends.argtypes = [P, ctypes.POINTER(U64)]
+    lib.tgx_program_reset.argtypes = [P, ctypes.c_int]
     lib.tgx_copy_regions.argtypes = [P, P, P, ctypes.POINTER(_Region), ctypes.c_int]
     _ready = True
     return lib
@@ -259,6 +261,16 @@ class Program:
         v = ctypes.c_float()
         _check(_lib().tgx_program_elapsed_ms(self._h, ctypes.byref(v)))
         return v.value
+
+    def ends(self) -> tuple:
+        """Recording::ends: the GPU clock's ticks when the last run started and ended."""
+        e = (ctypes.c_uint64 * 2)()
+        _check(_lib().tgx_program_ends(self._h, e))
+        return int(e[0]), int(e[1])
+
+    def reset(self, timed: bool = False) -> None:
+        """Recording::replace_program: drop the dispatches; new ones follow, then `end`."""
+        _check(_lib().tgx_program_reset(self._h, 1 if timed else 0))
 
     def close(self) -> None:
         if self._h:
