@@ -635,6 +635,10 @@ typedef struct {
 
 typedef struct tgx_program tgx_program;
 
+/* Context::dispatch (context.rs:517-540): one dispatch run alone and waited for, its bindings
+ * checked as a program's are; *ms (when not NULL) its GPU time between events on either side. */
+tgx_status tgx_context_dispatch(tgx_context* ctx, const tgx_dispatch* d, float* ms);
+
 /* Context::record (context.rs:507-518): a program, its dispatches added by
  * tgx_program_launch, recorded as a HIP graph by tgx_program_end; `timed` as Recording's (each
  * dispatch launched alone between events of its own, so that tgx_program_timings gives its time). */

@@ -374,3 +374,22 @@ def test_a_fence_spin_changes_how_waits_poll_and_not_what_they_give(ctx):
     p.close()
     m.close()
     o.close()
+
+
+def test_a_single_dispatch_runs_alone_and_is_timed(ctx):
+    """Context::dispatch (context.rs:517-540, as the reference's kernel tests run one kernel): the
+    stream-read words as a program gives them, a GPU time, and a refusal with its message."""
+    import tgx
+    import tgx.runtime as rt
+
+    data = np.random.default_rng(9).integers(0, 2**32, 32768, dtype=np.uint32)
+    m, o = rt.Memory(ctx, data.nbytes), rt.Memory(ctx, 16 * 4)
+    m.write(data)
+    ms = rt.dispatch(ctx, "stream_read", [m, o], [])
+    assert ms > 0
+    assert np.array_equal(o.read(np.uint32, 16), stream_words(data))
+    with pytest.raises(tgx.TgxError) as e:
+        rt.dispatch(ctx, "stream_read", [(m, 0, 1000), o], [])
+    assert e.value.kind == "shape" and "stream_read" in str(e.value)
+    m.close()  # the dispatch's program is gone: nothing binds the memory
+    o.close()

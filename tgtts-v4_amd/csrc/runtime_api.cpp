@@ -1602,6 +1602,25 @@ tgx_status tgx_program_reset(tgx_program* prog, int timed) {
     return TGX_OK;
 }
 
+tgx_status tgx_context_dispatch(tgx_context* ctx, const tgx_dispatch* d, float* ms) {
+    clear_error();
+    if (!ctx || !d) return fail(TGX_E_ARG, "null context or dispatch");
+    tgx_program* prog = nullptr;
+    TGX_TRY(tgx_program_begin(ctx, 1, &prog));
+    tgx_status st = tgx_program_launch(prog, d);
+    if (st == TGX_OK) st = tgx_program_end(prog);
+    if (st == TGX_OK) st = tgx_program_run(prog);
+    tgx_timing t{};
+    int n = 0;
+    if (st == TGX_OK) st = tgx_program_timings(prog, 1, &t, &n);
+    const std::string why = last_error();
+    const tgx_status gone = tgx_program_destroy(prog);
+    if (st != TGX_OK) return fail(st, why);
+    if (gone != TGX_OK) return gone;
+    if (ms) *ms = t.ms;
+    return TGX_OK;
+}
+
 tgx_status tgx_context_set_fence_spin(tgx_context* ctx, uint64_t ns) {
     clear_error();
     if (!ctx) return fail(TGX_E_ARG, "null context");

@@ -86,6 +86,7 @@ def _lib() -> ctypes.CDLL:
     lib.tgx_program_elapsed_ms.argtypes = [P, ctypes.POINTER(ctypes.c_float)]
     lib.tgx_program_destroy.argtypes = [P]
     lib.tgx_program_ends.argtypes = [P, ctypes.POINTER(U64)]
+    lib.tgx_context_dispatch.argtypes = [P, ctypes.POINTER(_Dispatch), ctypes.POINTER(ctypes.c_float)]
     lib.tgx_program_reset.argtypes = [P, ctypes.c_int]
     lib.tgx_copy_regions.argtypes = [P, P, P, ctypes.POINTER(_Region), ctypes.c_int]
     _ready = True
@@ -286,6 +287,18 @@ class Program:
             pass
 
 
+def dispatch(ctx, kernel_name: str, bindings: Sequence, constants: Sequence[int], groups: tuple = (0, 0, 0)) -> float:
+    """Context::dispatch: one dispatch run alone and waited for; its GPU time in ms."""
+    k = ctypes.c_int()
+    _check(_lib().tgx_kernel_find(kernel_name.encode(), ctypes.byref(k)))
+    b = _bindings(bindings)
+    c = (ctypes.c_uint32 * max(1, len(constants)))(*[int(v) & 0xFFFFFFFF for v in constants])
+    d = _Dispatch(k.value, b, len(bindings), c, len(constants), (ctypes.c_uint32 * 3)(*groups), 1)
+    ms = ctypes.c_float()
+    _check(_lib().tgx_context_dispatch(ctx._h, ctypes.byref(d), ctypes.byref(ms)))
+    return ms.value
+
+
 def copy_regions(ctx, dst: Memory, src: Memory, regions: Sequence[tuple]) -> None:
     """Recording::copy_in / copy_out (recording.rs:522-597): (src_offset, dst_offset, bytes) each."""
     arr = (_Region * max(1, len(regions)))(*[_Region(*r) for r in regions])
@@ -294,5 +307,5 @@ def copy_regions(ctx, dst: Memory, src: Memory, regions: Sequence[tuple]) -> Non
 
 __all__ = [
     "BindingInfo", "KernelInfo", "Memory", "Program", "copy_regions", "f32_bits", "kernel", "kernels", "rope_tables",
-    "tiles_bytes", "DEVICE", "UPLOAD", "READBACK", "READ", "WRITE", "TILES_16", "TILES_4", "TILES_QKV", "TILES_QKV128", "U32", "TgxError",
+    "tiles_bytes", "dispatch", "DEVICE", "UPLOAD", "READBACK", "READ", "WRITE", "TILES_16", "TILES_4", "TILES_QKV", "TILES_QKV128", "U32", "TgxError",
 ]
