@@ -391,3 +391,47 @@ def test_a_dit_evaluation_composed_by_kernel_name_is_tgx_sampler_sample_bit_for_
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     composed.close()
     sampler.close()
+
+
+def test_the_wider_kernels_refuse_on_the_host_what_they_could_not_run(ctx):
+    """Each kernel past the decode step checks its constants and every binding's bytes before
+    anything is recorded (Kernels::check, crates/graph/src/kernels.rs), as the decode kernels do."""
+    import tgx
+    import tgx.runtime as rt
+
+    big = rt.Memory(ctx, 64 << 20)
+    small = rt.Memory(ctx, 1024)  # short of a 1024-wide gain, or a 2 x 8 block table's 64 bytes and more
+    tiny = rt.Memory(ctx, 16)
+    p = rt.Program(ctx)
+
+    def refused(name, bindings, constants):
+        with pytest.raises(tgx.TgxError) as e:
+            p.dispatch(name, bindings, constants)
+        assert e.value.kind == "shape", (name, str(e.value))
+
+    eps = rt.f32_bits(1e-5)
+    pre = [256, 1024, 4096, 16, 2, 64, 512, 2, 8, 16, eps, 1]  # rows .. rope
+    refused("norm_rows", [big, small, big], pre)  # gain short of 1024 floats
+    refused("norm_rows", [big, big, big], [0] + pre[1:])  # no rows
+    refused("attention_rows", [big, big, big, big, big], pre + [0])  # no tiles
+    refused("attention_rows", [big, big, big, big, big], pre[:5] + [96] + pre[6:] + [4])  # a head width not taken
+    refused("gemm_add_norm_rows", [big, big, big, None, big, None, None], pre + [1000, 1024, 4, 1])  # K
+    refused("gemm_add_norm_rows", [big, big, big, big, big, None, None], pre + [1024, 1024, 4, 1])  # next norm in part
+    refused("gemm_silu_mul_rows", [big, big, None, big], pre + [1024, 300])  # N
+    refused("gemm_rope_rows", [big, big, None, big, big, big, big, tiny, big, big], pre)  # table short of 2 x 8 entries
+    loc = [22, 11, 1024, 4096, 16, 2, eps, 1]  # tokens .. rope
+    refused("local_norm", [big, big, big, big], [23] + loc[1:])  # tokens not whole sequences
+    refused("local_norm", [big, big, big, big], loc[:2] + [2048] + loc[3:])  # a stack 2048 wide
+    refused("local_partial", [big, big, big], loc + [1024, 1024, 5])  # parts
+    refused("local_add_norm", [None, big, big, None, big, big], loc + [2])  # parts without partial
+    refused("local_embed", [big, big, big, big, None, big, None, None], loc + [1, 64, 5, 7, 2, 1, 0, 0, 2])  # frames
+    refused("local_embed", [big, big, big, big, big, big, None, None], loc + [1, 64, 4, 7, 2, 1, 0, 0, 2])  # gain alone
+    refused("dit_euler", [big, big, big, big, big, big, big], loc + [1, 20, 4, 7, rt.f32_bits(0.1)])  # channels
+    refused("dit_euler", [big, big, big, big, big, big, big], loc + [1, 64, 4, 7, rt.f32_bits(float("nan"))])  # dt
+    refused("cfm_noise", [big, big, big], [0, 256])
+    refused("gemv_linear", [big, None, big, big, big], [4, 1024, 1024, 256, 0, 256, 0, 0])  # K1 without x1
+    refused("gemv_linear", [big, None, big, big, big], [4, 1024, 0, 256, 16, 256, 0, 0])  # out rows too narrow
+    refused("select_rows", [big, big, big, big], [4, 6])  # K not a multiple of 4
+    p.close()
+    for m in (big, small, tiny):
+        m.close()
