@@ -76,9 +76,9 @@ def test_spare_rows_are_placed_past_every_position_and_a_slot_is_taken_once():
         (dict(heads=64, kv_heads=8, head_dim=128), dict()),
         (dict(head_dim=128, capacity=16385), dict()),
         (dict(heads=16, kv_heads=3), dict()),
+        # 32 query heads to a KV head: past the decode attention's 16 columns
         (dict(heads=32, kv_heads=1), dict()),
-        # 16 query heads to a KV head: the prefill attention's tile would spill, so it is refused
-        (dict(heads=32, kv_heads=2), dict()),
+        # a group of 16 whose q/k/v rows (18 heads of 64) are not a multiple of the prefill's 256
         (dict(heads=16, kv_heads=1), dict()),
         (dict(capacity=0), dict()),
         (dict(hidden=1000), dict()),
@@ -122,21 +122,24 @@ def test_the_backbone_shapes_are_taken():
     tgx.check_shape(tgx.Shape(rope=False, layers=8), tgx.Batch(rows=4, slots=8))
 
 
-@pytest.mark.parametrize("kv_heads", [16, 8, 4, 2])
-def test_groups_of_one_to_eight_query_heads_a_kv_head_are_taken(kv_heads):
-    """16 query heads over 16, 8, 4 or 2 KV heads: groups of 1, 2, 4 and 8, each with its own
-    prefill attention instance and decode attention columns."""
+@pytest.mark.parametrize("heads,kv_heads", [(16, 16), (16, 8), (16, 4), (16, 2), (32, 2)])
+def test_groups_of_one_to_sixteen_query_heads_a_kv_head_are_taken(heads, kv_heads):
+    """Groups of 1, 2, 4, 8 and 16 query heads to a KV head, each with its own prefill attention
+    instance and decode attention columns."""
     import tgx
 
-    tgx.check_shape(tgx.Shape(heads=16, kv_heads=kv_heads), tgx.Batch(rows=4, slots=4))
+    tgx.check_shape(tgx.Shape(heads=heads, kv_heads=kv_heads), tgx.Batch(rows=4, slots=4))
 
 
-def test_a_group_of_sixteen_is_refused_with_its_reason():
+def test_groups_of_one_to_sixteen_are_taken_and_thirty_two_refused_with_its_reason():
     import tgx
 
+    for heads, kv, head_dim in ((16, 16, 64), (16, 8, 64), (16, 4, 64), (16, 2, 64), (32, 2, 64), (16, 1, 128), (16, 2, 128),
+                                (32, 2, 128), (48, 3, 128)):
+        tgx.check_shape(tgx.Shape(heads=heads, kv_heads=kv, head_dim=head_dim), tgx.Batch(rows=1, slots=1))
     with pytest.raises(tgx.TgxError) as e:
-        tgx.check_shape(tgx.Shape(heads=32, kv_heads=2), tgx.Batch(rows=1, slots=1))
-    assert e.value.kind == "shape" and "1, 2, 4 or 8" in str(e.value)
+        tgx.check_shape(tgx.Shape(heads=32, kv_heads=1), tgx.Batch(rows=1, slots=1))
+    assert e.value.kind == "shape" and "1, 2, 4, 8 or 16" in str(e.value)
 
 
 def test_null_arguments_are_refused_with_a_message():

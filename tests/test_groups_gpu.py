@@ -1,6 +1,7 @@
 """Every group of query heads to a KV head the shape check takes, on the GPU against the oracle:
-16 query heads over 16, 8 and 4 KV heads (groups 1, 2 and 4; the backbone's 16 over 2, a group of
-8, is every other test's shape). The reference's attention takes any group
+16 query heads over 16, 8 and 4 KV heads (groups 1, 2 and 4), and 32 over 2 (a group of 16; its
+q/k/v rows a multiple of the prefill GEMM's 256) and at head_dim 128 16 over 1 (the backbone's 16
+over 2, a group of 8, is every other test's shape). The reference's attention takes any group
 (kernels/glsl/attention_split.comp:24-27); here each group has its own prefill attention
 instance and the decode attention's columns past the group read its last head again.
 
@@ -19,15 +20,15 @@ from test_decode_gpu import inputs, make_decoder, oracle_stack
 pytestmark = pytest.mark.gpu
 
 
-def group_spec(kv_heads):
+def group_spec(kv_heads, head_dim=64, heads=16):
     from tgx.synth import StackSpec
 
-    return StackSpec(layers=2, heads=16, kv_heads=kv_heads, dtype="bf16", seed=kv_heads)
+    return StackSpec(layers=2, heads=heads, kv_heads=kv_heads, head_dim=head_dim, dtype="bf16", seed=heads + kv_heads + head_dim)
 
 
-@pytest.mark.parametrize("kv_heads", [16, 8, 4])
-def test_prefill_and_decode_at_each_group_match_the_oracle_and_rows_are_as_alone(ctx, kv_heads):
-    spec = group_spec(kv_heads)
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(16, 16, 64), (16, 8, 64), (16, 4, 64), (32, 2, 64), (16, 1, 128)])
+def test_prefill_and_decode_at_each_group_match_the_oracle_and_rows_are_as_alone(ctx, heads, kv_heads, head_dim):
+    spec = group_spec(kv_heads, head_dim, heads)
     print(f"group {spec.heads // kv_heads}: {spec.heads} heads over {kv_heads} KV heads, 2 layers", flush=True)
     cap = 256
     lengths = (130, 45)

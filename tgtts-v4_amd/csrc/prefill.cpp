@@ -146,7 +146,7 @@ tgx_status make_plan(Decoder* d, const tgx_run* runs, int nruns, Plan& plan) {
     plan.pos.assign(plan.M_pad, TGX_SPARE);
     plan.slot.assign(plan.M_pad, TGX_SPARE);
     plan.tiles.clear();
-    const uint32_t tile = (uint32_t)prefill_attention_tile(s.heads / s.kv_heads);  // positions a workgroup
+    const uint32_t tile = (uint32_t)prefill_attention_tile(s.heads / s.kv_heads, s.head_dim);  // positions a workgroup
     size_t row = 0;
     for (int r = 0; r < nruns; ++r) {
         const tgx_run& run = runs[r];
@@ -250,7 +250,7 @@ tgx_status prefill_runs_noalloc(Decoder* d, const tgx_run* runs, int nruns, cons
     const size_t need = tensor_bytes(s, plan.M_pad, plan.tiles.size());
     if (need > PREFILL_SCRATCH_BYTES) {
         size_t most = 0;  // positions a call of one run takes at this shape
-        const size_t tile = (size_t)prefill_attention_tile(s.heads / s.kv_heads);
+        const size_t tile = (size_t)prefill_attention_tile(s.heads / s.kv_heads, s.head_dim);
         for (size_t rows = ROW_TILE; tensor_bytes(s, rows, rows / tile + 1) <= PREFILL_SCRATCH_BYTES; rows += ROW_TILE) most = rows;
         return fail(TGX_E_SHAPE, std::to_string(plan.M) + " positions take " + std::to_string(need) +
                                      " bytes of tensors, past the scratch's " + std::to_string(PREFILL_SCRATCH_BYTES) +

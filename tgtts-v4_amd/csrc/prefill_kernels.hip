@@ -673,11 +673,18 @@ struct LazySoftmax {
 // (attention_rows.comp:71-116).
 // A workgroup's tile: ATTN_TILE positions of a run, except for 8 query heads to a KV head, where it
 // takes 16 positions with four waves (eight at D 128), so that two workgroups share a CU: their
-// barriers are their own, and one's softmax runs beside the other's products. Groups of 1, 2, 4 and 8 have an
-// instance; 16 (four column groups a wave) would hold more than a wave's registers and spill
-// beside the ring's waits, which count loads in issue order, so the shape check refuses it.
+// barriers are their own, and one's softmax runs beside the other's products. At 16 query heads to
+// a KV head a column group is one position's 16 heads: eight waves of two column groups take 16
+// positions at D 64, and eight of one take 8 at D 128 (four column groups a wave, 32 positions,
+// would hold more than a wave's registers and spill beside the ring's waits, which count loads in
+// issue order). Groups of 1, 2, 4, 8 and 16 have an instance each.
 constexpr int ATTN_TILE = 32;
 constexpr int ATTN_TILE_8 = 16;
+constexpr int ATTN_TILE_16 = 16, ATTN_TILE_16_D128 = 8;
+// The positions a workgroup takes for `group` query heads to a KV head and heads of `head_dim`.
+__host__ __device__ constexpr int attention_tile(int group, int head_dim) {
+    return group == 16 ? (head_dim == 128 ? ATTN_TILE_16_D128 : ATTN_TILE_16) : group == 8 ? ATTN_TILE_8 : ATTN_TILE;
+}
 // The attention's ring of key-and-value stages: a stage is one chunk (16 KiB), ATTN_STAGES of them,
 // up to ATTN_STAGES - 2 in flight beyond the two being taken.
 constexpr int ATTN_STAGE = 2 * KV_TILE / 8;  // uint4: 16 fragments of 1 KiB
@@ -908,6 +915,13 @@ hipError_t attention(const PrefillArgs& a, const uint16_t* q, const uint16_t* kv
             else
                 dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
             break;
+        // 16 heads: a position to a column group, eight waves of two at D 64, of one at D 128.
+        case 16:
+            if constexpr (D == 64)
+                dispatch("prefill_attention", prefill_attention<ATTN_TILE_16, 8, 2, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
+            else
+                dispatch("prefill_attention", prefill_attention<ATTN_TILE_16_D128, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipSuccess;
@@ -969,7 +983,7 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
     return hipGetLastError();
 }
 
-int prefill_attention_tile(int group) { return group == 8 ? ATTN_TILE_8 : ATTN_TILE; }
+int prefill_attention_tile(int group, int head_dim) { return attention_tile(group, head_dim); }
 
 hipError_t prefill_prepare(size_t device_lds) {
     hipError_t e;
@@ -982,7 +996,8 @@ hipError_t prefill_prepare(size_t device_lds) {
     for (const void* f : {(const void*)prefill_attention<ATTN_TILE, 2, 1, 64>, (const void*)prefill_attention<ATTN_TILE, 4, 1, 64>,
                           (const void*)prefill_attention<ATTN_TILE, 8, 1, 64>, (const void*)prefill_attention<ATTN_TILE_8, 4, 2, 64>,
                           (const void*)prefill_attention<ATTN_TILE, 2, 1, 128>, (const void*)prefill_attention<ATTN_TILE, 4, 1, 128>,
-                          (const void*)prefill_attention<ATTN_TILE, 8, 1, 128>, (const void*)prefill_attention<ATTN_TILE_8, 8, 1, 128>})
+                          (const void*)prefill_attention<ATTN_TILE, 8, 1, 128>, (const void*)prefill_attention<ATTN_TILE_8, 8, 1, 128>,
+                          (const void*)prefill_attention<ATTN_TILE_16, 8, 2, 64>, (const void*)prefill_attention<ATTN_TILE_16_D128, 8, 1, 128>})
         if ((e = allow(f, device_lds)) != hipSuccess) return e;
     return allow((const void*)prefill_gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>, device_lds);
 }

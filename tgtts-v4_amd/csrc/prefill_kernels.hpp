@@ -105,8 +105,8 @@ hipError_t launch_prefill(const PrefillArgs& a, const PrefillLayer* layers, int 
                           const PrefillBuffers& b, hipStream_t stream, DispatchTimer* timer = nullptr);
 hipError_t prefill_prepare(size_t device_lds);
 // The positions of a run the attention takes to a workgroup (its PrefillTiles' most) for `group`
-// query heads to a KV head.
-int prefill_attention_tile(int group);
+// query heads to a KV head and heads of `head_dim`.
+int prefill_attention_tile(int group, int head_dim);
 
 // The size of each GPU's prefill scratch (tgx_prefill_runs_noalloc's tensors): 32 MiB, which at
 // the backbone's shape (hidden 1024, inner 4096, 16 heads) holds 1024 positions a call.

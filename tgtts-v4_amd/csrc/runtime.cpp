@@ -186,11 +186,16 @@ tgx_status check_shape(const tgx_shape* in, Shape* s) {
     if (s->capacity > decode_max_capacity(s->head_dim))
         return refuse("capacity " + std::to_string(s->capacity) + " past the attention's " +
                       std::to_string(decode_max_capacity(s->head_dim)) + " at head_dim " + std::to_string(s->head_dim));
-    // Query heads to a KV head: 1, 2, 4 or 8, each with a prefill attention instance whose
-    // registers hold its tile (16 heads a KV head would spill beside waits that count loads in
-    // issue order, and is refused; the reference takes any group, attention_split.comp:24-27).
-    if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 8 || 8 % (s->heads / s->kv_heads) != 0)
-        return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) + " KV heads: a group of 1, 2, 4 or 8");
+    // Query heads to a KV head: 1, 2, 4, 8 or 16, each with a prefill attention instance whose
+    // registers hold its tile (the reference takes any group, attention_split.comp:24-27; the
+    // decode attention's 16 columns take up to 16 heads).
+    if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 16 || 16 % (s->heads / s->kv_heads) != 0)
+        return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) +
+                      " KV heads: a group of 1, 2, 4, 8 or 16");
+    // The prefill GEMM takes q/k/v's rows in tiles of 256.
+    if ((s->heads + 2 * s->kv_heads) * s->head_dim % 256 != 0)
+        return refuse(std::to_string(s->heads) + " + 2 x " + std::to_string(s->kv_heads) + " heads of " + std::to_string(s->head_dim) +
+                      ": q/k/v's rows are not a multiple of 256");
     // The projections take K in chunks of 1024 columns: hidden (the norms', q/k/v's and gate/up's
     // K) up to 2048, inner (down_proj's) and heads x head_dim (o_proj's) up to 6144
     // (decode_kernels.hip): VoxCPM2's LMs are 2048 wide with an FFN of 6144.

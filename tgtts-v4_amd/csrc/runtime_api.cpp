@@ -468,8 +468,8 @@ tgx_status build_gemm_rope_rows(const Bound* b, const uint32_t* c, Launch* L) {
 // attention_rows (attention_rows.comp): q, cache pool, table, tiles -> attended, constant tiles.
 // Each tile is 4 u32: row0, pos0, count, slot: rows row0 .. row0 + count - 1 are positions
 // pos0 .. of the slot, every position of a run up to its own attending to the slot's cache. A tile
-// holds at most 32 positions (16 at 8 query heads a KV head); one that leaves the tensors is
-// skipped. attended: bf16 [rows_pad][heads head_dim] in fragment order, written at the tiles' rows
+// holds at most 32 positions (16 at 8 or 16 query heads a KV head, 8 at 16 of 128 dimensions); one
+// that leaves the tensors is skipped. attended: bf16 [rows_pad][heads head_dim] in fragment order, written at the tiles' rows
 // only (the GEMM after it reads every row: keep the rest zero).
 tgx_status build_attention_rows(const Bound* b, const uint32_t* c, Launch* L) {
     PrefillArgs a;
