@@ -324,10 +324,10 @@ def run_tts(ctx, rows: int, steps: int, warmup: int, context: int = 128):
 
 
 def host_threads() -> int:
-    """The host cores the CPU baseline uses: those the process may run on, at most 16. A one-GPU
-    box is given 16 of its host's CPUs (its OMP_NUM_THREADS is 16), whatever os.cpu_count()
-    reports of the whole host; more threads than that would contend with the GPU's own feeding
-    thread and with each other."""
+    """The host cores the CPU baseline uses: those the process may run on, at most 16. A job on
+    one GPU of an 8-GPU host has 16 of the host's CPUs to itself (OMP_NUM_THREADS 16), whatever
+    os.cpu_count() reports of the whole host; more threads than that would contend with the GPU's
+    own feeding thread and with each other."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -337,7 +337,7 @@ def host_threads() -> int:
 
 def host_info() -> dict:
     """The host the CPU baseline ran on: its CPU model, the CPUs the OS reports, those this process
-    may run on, and OMP_NUM_THREADS as the box sets it."""
+    may run on, and OMP_NUM_THREADS as the environment sets it."""
     model = None
     try:
         with open("/proc/cpuinfo") as f:
@@ -354,7 +354,7 @@ def host_info() -> dict:
     return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": affinity,
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
             "threads_used": host_threads(),
-            "why_16": "a one-GPU box's share of its host is 16 CPUs; threads stop there"}
+            "why_16": "a one-GPU job's share of an 8-GPU host is 16 CPUs; threads stop there"}
 
 
 def cpu_baseline(weights, seconds: float):

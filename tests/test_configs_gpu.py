@@ -15,7 +15,7 @@ the oracle (oracle/) as crates/graph/tests/{decode,prefill}.rs hold the referenc
       encoder) for 300 steps, rows rotating: two requests' LMs at every step and every stage at
       four steps against the oracle, all 16 requests bit for bit as run alone over the 300 steps
 
-Tolerance (the north star's, bf16 on the GPU against the oracle): cosine >= 0.999 and
+Tolerance (bf16 on the GPU against the fp32 oracle): cosine >= 0.999 and
 max|got - ref| / max|ref| <= 1e-2, per position or step.
 """
 
