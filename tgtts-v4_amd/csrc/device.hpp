@@ -20,8 +20,7 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c)
 }
 
 // x sigmoid(x) = x / (1 + e^-x), e^-x as 2^(-x log2 e) and the reciprocal by v_rcp_f32 (1 ulp),
-// where a division takes ten instructions (the epilogues that call it sit beside other waves'
-// MFMAs, which the SIMD does not run beside VALU work).
+// where a division takes ten instructions (an epilogue costs what its VALU instructions take).
 __device__ __forceinline__ float silu(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }

@@ -841,8 +841,8 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
         if (MASK && p0 + CHUNK - 1 > last) zero_values_past<KS, DT>(vf, p0, last);
         // One check for the wave's column groups (the rescale is rare past chunk 0), so that the
         // exponentials and value MFMAs below are one stretch of code: the compiler runs a group's
-        // exponentials beside the previous group's MFMAs (the SIMD runs a wave's VALU work beside
-        // its own MFMAs, not beside another wave's).
+        // exponentials beside the previous group's MFMAs (a wave's VALU work runs beside its own
+        // MFMAs when they do not depend on it).
         float peak_all = mx[0];
 #pragma unroll
         for (int cg = 1; cg < CG; ++cg) peak_all = fmaxf(peak_all, mx[cg]);
