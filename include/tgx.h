@@ -571,8 +571,9 @@ tgx_status tgx_write(tgx_memory* mem, uint64_t offset, const void* src, uint64_t
 tgx_status tgx_read(tgx_memory* mem, uint64_t offset, void* dst, uint64_t bytes);
 
 /* How the kernels keep a weight matrix: bf16 MFMA tiles of strips of 16 rows (with q/k/v's rows
- * ordered so that a strip holds 8 RoPE pairs of one head: heads of 64 dimensions, TGX_TILES_QKV,
- * or of 128, TGX_TILES_QKV128), or of 4 rows (o_proj and down_proj at batches of up to 16 rows). */
+ * ordered so that a strip holds 8 RoPE pairs of one head, each pair's two rows side by side: heads
+ * of 64 dimensions, TGX_TILES_QKV, or of 128, TGX_TILES_QKV128), or of 4 rows (o_proj and
+ * down_proj at batches of up to 16 rows). */
 typedef enum { TGX_TILES_16 = 0, TGX_TILES_4 = 1, TGX_TILES_QKV = 2, TGX_TILES_QKV128 = 3 } tgx_tiles;
 /* The bytes a [rows][cols] matrix takes as `tiles` (0 for a shape the tiles cannot hold). */
 uint64_t tgx_tiles_bytes(tgx_tiles tiles, int rows, int cols);

@@ -311,8 +311,8 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
 
     const int H = a.heads, KV = a.kv_heads;
     if (threadIdx.x >= EPI || b >= a.rows || pos >= (uint32_t)a.capacity || slot >= (uint32_t)a.nslots) return;
-    float va = reduced<1>(red, 0, p, c) * scale[c];
-    float vc = reduced<1>(red, 0, p + R / 2, c) * scale[c];
+    float va = reduced<1>(red, 0, 2 * p, c) * scale[c];      // strip rows 2 p, 2 p + 1: the pair (qkv_row_of)
+    float vc = reduced<1>(red, 0, 2 * p + 1, c) * scale[c];
     if (head < H + KV && a.rope) {
         // As upstream: x cos + rotate_half(x) sin (gemv_qkv_rope.comp:88-94).
         const float ra = va * co - vc * si;

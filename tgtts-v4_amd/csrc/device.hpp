@@ -155,6 +155,16 @@ __device__ __forceinline__ float lane_xor32(float v) {
     return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// A lane's two packed words of a RoPE pair's halves (lo: dimensions e, e + 1; hi: e + D / 2,
+// e + 1 + D / 2) as 8 bytes of four consecutive dimensions, from a trade with lane l ^ 16, which
+// holds e + 2 and e + 3 (v_permlane16_swap: the odd rows of 16 lanes of lo trade with the even
+// rows of hi): an even row's lanes get lo and the partner's lo, an odd row's the partner's hi and
+// hi. Every lane and its partner run it together (the same row: both spare or neither).
+__device__ __forceinline__ uint2 quad_halves(uint32_t lo, uint32_t hi) {
+    const auto r = __builtin_amdgcn_permlane16_swap(lo, hi, false, false);
+    return make_uint2(r[0], r[1]);
+}
+
 // Attention's online softmax over a turn of 16 PT keys (PT 4: a 64-key block at head_dim 64; PT 2:
 // half a block at head_dim 128) for the 16 columns (query heads or (position, head) pairs) of a
 // wave, from S^T = K Q^T in s[pt] (key 16 pt + 4 (lane / 16) + i, column lane % 16) and the turn's
@@ -291,11 +301,11 @@ __host__ __device__ constexpr size_t fragment_index(int S, int kb, int kblocks, 
 }
 
 // The q/k/v projection's rows are permuted so that each strip of R holds R/2 of a head's RoPE
-// pairs: strip rows 0..R/2-1 are the head's rows p0 .. p0 + R/2 - 1 and rows R/2..R-1 those
-// head_dim/2 further (head_dim 64: 64 / R strips to a head). Row r of strip s is original row:
+// pairs side by side: strip rows 2 k and 2 k + 1 are the head's rows p0 + k and p0 + k + head_dim/2
+// (p0 = (s % (head_dim / R)) R/2; head_dim / R strips to a head), so that the four rows an MFMA
+// lane holds of a strip are two whole pairs. Row r of strip s is original row:
 __host__ __device__ constexpr int qkv_row_of(int strip, int r, int head_dim, int R) {
-    return (strip / (head_dim / R)) * head_dim + (strip % (head_dim / R)) * (R / 2) +
-           (r < R / 2 ? r : head_dim / 2 + r - R / 2);
+    return (strip / (head_dim / R)) * head_dim + (strip % (head_dim / R)) * (R / 2) + r / 2 + (r % 2) * (head_dim / 2);
 }
 
 // The paged KV cache: per layer, block and KV head, a key tile and a value tile of 64 positions

@@ -128,33 +128,37 @@ __device__ __forceinline__ void local_store(const LocalArgs& a, const LocalGemm&
             v[i] = silu(gate) * u;
         }
         *reinterpret_cast<uint2*>(g.mlp + act_index(m, n, inner)) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-    } else if (EPI == LEPI_QKV) {  // a strip's rows pair as r, r + 8 (lanes l and l ^ 32)
+    } else if (EPI == LEPI_QKV) {  // a lane's four rows of a strip are two RoPE pairs (qkv_row_of)
         const int H = a.heads, KV = a.kv_heads;
-        const bool second = quad >= 2;
         const int head = strip / 4, qtr = strip % 4;
-        const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
-        const int d0 = p0 + (second ? HEAD_DIM / 2 : 0);
-        float own[4], other[4];
+        // Rows 4 quad .. 4 quad + 3 of the strip: the pairs of dimensions (e, e + 32) and
+        // (e + 1, e + 33), each first half then second; lanes l and l ^ 16 (the same token) trade
+        // halves for the stores: the even quad stores dimensions e .. e + 3, the odd one
+        // e + 30 .. e + 33.
+        const int e = qtr * 8 + quad * 2;
+        const int d0 = (quad & 1) ? e - 2 + HEAD_DIM / 2 : e;
+        float lo[2], hi[2];  // dimensions e + k and e + k + 32
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            own[i] = acc[i] * rs;
-            other[i] = lane_xor32(own[i]);
+        for (int k = 0; k < 2; ++k) {
+            lo[k] = acc[2 * k] * rs;
+            hi[k] = acc[2 * k + 1] * rs;
         }
-        if (m >= a.M) return;
-        float v[4];
         if (head < H + KV && a.rope) {
             const int place = m % a.T;
-            const float4 co = *reinterpret_cast<const float4*>(a.cos + place * (HEAD_DIM / 2) + p0);
-            const float4 si = *reinterpret_cast<const float4*>(a.sin + place * (HEAD_DIM / 2) + p0);
-            const float c4[4] = {co.x, co.y, co.z, co.w}, s4[4] = {si.x, si.y, si.z, si.w};
-            // As upstream: x cos + rotate_half(x) sin (local_qkv_rope.comp:71-76).
+            const float2 co = *reinterpret_cast<const float2*>(a.cos + place * (HEAD_DIM / 2) + e);
+            const float2 si = *reinterpret_cast<const float2*>(a.sin + place * (HEAD_DIM / 2) + e);
+            // As upstream: x cos + rotate_half(x) sin (local_qkv_rope.comp:71-76), a pair
+            // (x1, x2) to (x1 cos - x2 sin, x2 cos + x1 sin).
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = second ? own[i] * c4[i] + other[i] * s4[i] : own[i] * c4[i] - other[i] * s4[i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = own[i];
+            for (int k = 0; k < 2; ++k) {
+                const float cs = k ? co.y : co.x, sn = k ? si.y : si.x;
+                const float x1 = lo[k], x2 = hi[k];
+                lo[k] = __builtin_fmaf(x1, cs, -(x2 * sn));
+                hi[k] = __builtin_fmaf(x2, cs, x1 * sn);
+            }
         }
-        const uint2 packed = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        const uint2 packed = quad_halves(pack_bf16x2(lo[0], lo[1]), pack_bf16x2(hi[0], hi[1]));
+        if (m >= a.M) return;
         if (head < H)
             *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * HEAD_DIM + d0) = packed;
         else if (head < H + KV)

@@ -409,12 +409,12 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                 *reinterpret_cast<uint2*>(g.mlp + act_index(m, n, inner)) = packed;
             }
         }
-    } else {  // EPI_QKV: rows of a strip pair as r, r + 8 (lanes l and l ^ 32)
+    } else {  // EPI_QKV: a lane's four rows of a strip are two RoPE pairs (qkv_row_of)
         // Each of the tile's 256 rows' position, cache block and RoPE row, staged once in the LDS
         // the main loop is done with: a thread to a row, two round trips to memory in all.
-        // A row's 32 values of cos and sin 36 floats apart: the 16 rows a wave's lanes read at once
-        // (and the threads' rows as they store them) then fall on distinct banks, where 32 apart
-        // put every row on the same ones.
+        // A row's 32 values of cos and sin 36 floats apart, so that the 16 rows a wave's lanes read
+        // at once (and the threads' rows as they store them) do not all fall on the same banks, as
+        // 32 apart would put them.
         constexpr int RS = D / 2 + 4;
         static_assert((size_t)TM * (2 * RS + 2) * 4 <= T::LDS, "the rows' RoPE tables fit the ring's LDS");
         float* t_cos = reinterpret_cast<float*>(lds);          // [TM][RS]
@@ -451,41 +451,44 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
         for (int s = 0; s < 8; ++s) {
             const int strip = strip_of<EPI>(nb, wn, s, g.N);
             const int head = strip / (D / 16), qtr = strip % (D / 16);
-            const bool second = quad >= 2;  // rows 8..15: the pairs' second halves
-            const int p0 = qtr * 8 + (quad % 2) * 4;  // the first of this lane's 4 pairs
-            const int d0 = p0 + (second ? D / 2 : 0);
+            // Rows 4 quad .. 4 quad + 3 of the strip: the pairs of dimensions (e, e + D / 2) and
+            // (e + 1, e + 1 + D / 2), each first half then second. For the stores the lanes l and
+            // l ^ 16 (quads 2 h and 2 h + 1, the same row) trade halves: the even quad stores
+            // dimensions e .. e + 3 and the odd one e - 2 + D / 2 .. e + 1 + D / 2, 8 bytes each.
+            const int e = qtr * 8 + quad * 2;
+            const int d0 = (quad & 1) ? e - 2 + D / 2 : e;
             const bool rotate = head < H + KV && a.rope;
 #pragma unroll
             for (int t = 0; t < WT; ++t) {
                 const int j = (wm * WT + t) * 16 + lane % 16;  // the row within the tile
-                const float rs = t_scale[j];
-                float own[4], other[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    own[i] = acc[s][t][i] * rs;
-                    other[i] = lane_xor32(own[i]);
-                }
                 const uint32_t pos = t_pos[j];
                 if (pos == TGX_SPARE_POS) continue;
-                float v[4];
+                const float rs = t_scale[j];
+                float lo[2], hi[2];  // dimensions e + k and e + k + D / 2
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    lo[k] = acc[s][t][2 * k] * rs;
+                    hi[k] = acc[s][t][2 * k + 1] * rs;
+                }
                 if (rotate) {
-                    const float4 co = *reinterpret_cast<const float4*>(t_cos + j * RS + p0);
-                    const float4 si = *reinterpret_cast<const float4*>(t_sin + j * RS + p0);
-                    const float c4[4] = {co.x, co.y, co.z, co.w}, s4[4] = {si.x, si.y, si.z, si.w};
-                    // As upstream: x cos + rotate_half(x) sin (rope_rows.comp:52-59).
+                    const float2 co = *reinterpret_cast<const float2*>(t_cos + j * RS + e);
+                    const float2 si = *reinterpret_cast<const float2*>(t_sin + j * RS + e);
+                    // As upstream: x cos + rotate_half(x) sin (rope_rows.comp:52-59), a pair
+                    // (x1, x2) to (x1 cos - x2 sin, x2 cos + x1 sin).
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        v[i] = second ? own[i] * c4[i] + other[i] * s4[i] : own[i] * c4[i] - other[i] * s4[i];
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) v[i] = own[i];
+                    for (int k = 0; k < 2; ++k) {
+                        const float cs = k ? co.y : co.x, sn = k ? si.y : si.x;
+                        const float x1 = lo[k], x2 = hi[k];
+                        lo[k] = __builtin_fmaf(x1, cs, -(x2 * sn));
+                        hi[k] = __builtin_fmaf(x2, cs, x1 * sn);
+                    }
                 }
                 const int m = m0 + j;
                 if (head < H) {
                     // q scaled by scale log2(e), the units the attention's softmax takes.
                     const float qs = log2_scale(a.scale);
-                    uint2 packed = make_uint2(pack_bf16x2(v[0] * qs, v[1] * qs), pack_bf16x2(v[2] * qs, v[3] * qs));
-                    *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * D + d0) = packed;
+                    const auto w4 = quad_halves(pack_bf16x2(lo[0] * qs, lo[1] * qs), pack_bf16x2(hi[0] * qs, hi[1] * qs));
+                    *reinterpret_cast<uint2*>(g.q + ((size_t)m * H + head) * D + d0) = w4;
                     continue;
                 }
                 const uint32_t blk = t_blk[j];
@@ -495,12 +498,14 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                 uint16_t* tl = g.kv + ((size_t)blk * KV + kv) * 2 * TILE;
                 const int pp = (int)(pos % BLOCK_TOKENS);
                 if (head < H + KV) {
-                    // Four consecutive dimensions of a key sit side by side in its tile.
-                    *reinterpret_cast<uint2*>(tl + key_index(pp, d0, D)) =
-                        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    // Four consecutive dimensions of a key sit side by side in its tile (d0 % 4 == 0).
+                    *reinterpret_cast<uint2*>(tl + key_index(pp, d0, D)) = quad_halves(pack_bf16x2(lo[0], lo[1]), pack_bf16x2(hi[0], hi[1]));
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) tl[TILE + value_index(pp, d0 + i)] = (uint16_t)bf16_bits(v[i]);
+                    for (int k = 0; k < 2; ++k) {
+                        tl[TILE + value_index(pp, e + k)] = (uint16_t)bf16_bits(lo[k]);
+                        tl[TILE + value_index(pp, e + k + D / 2)] = (uint16_t)bf16_bits(hi[k]);
+                    }
                 }
             }
         }
