@@ -165,6 +165,16 @@ __device__ __forceinline__ uint2 quad_halves(uint32_t lo, uint32_t hi) {
     return make_uint2(r[0], r[1]);
 }
 
+// Two blocks' 8-byte pieces as one 16-byte piece a lane: lane l of an even row of 16 lanes holds
+// columns c .. c + 3 of blocks a and b (two packed words each) and lane l ^ 16 columns c + 4 ..
+// c + 7; after two v_permlane16_swap trades the even row's lane holds block a's c .. c + 7 and the
+// odd row's block b's. Every lane and its partner run it together.
+__device__ __forceinline__ uint4 pair_blocks(const uint32_t (&a)[2], const uint32_t (&b)[2]) {
+    const auto r0 = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto r1 = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    return make_uint4(r0[0], r1[0], r0[1], r1[1]);
+}
+
 // Attention's online softmax over a turn of 16 PT keys (PT 4: a 64-key block at head_dim 64; PT 2:
 // half a block at head_dim 128) for the 16 columns (query heads or (position, head) pairs) of a
 // wave, from S^T = K Q^T in s[pt] (key 16 pt + 4 (lane / 16) + i, column lane % 16) and the turn's

@@ -344,29 +344,39 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
+            // The next norm's bf16 operand two strips at a time: lanes l and l ^ 16 (the same row)
+            // trade so that each stores 8 columns of one strip, 16 bytes (pair_blocks).
 #pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4) {
-                const int s = 4 * half + s4;
-                const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
+            for (int t = 0; t < WT; ++t) {
+                const int m = m0 + (wm * WT + t) * 16 + lane % 16;
+                if (m >= a.M) continue;
 #pragma unroll
-                for (int t = 0; t < WT; ++t) {
-                    const int m = m0 + (wm * WT + t) * 16 + lane % 16;
-                    if (m >= a.M) continue;
-                    float4 o = make_float4(acc[s][t][0], acc[s][t][1], acc[s][t][2], acc[s][t][3]);
-                    if (EPI == EPI_RESIDUAL) {
-                        o.x = r[s4][t].x + acc[s][t][0];
-                        o.y = r[s4][t].y + acc[s][t][1];
-                        o.z = r[s4][t].z + acc[s][t][2];
-                        o.w = r[s4][t].w + acc[s][t][3];
+                for (int s2 = 0; s2 < 4; s2 += 2) {
+                    uint32_t normed[2][2];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int s4 = s2 + h, s = 4 * half + s4;
+                        const int n = strip_of<EPI>(nb, wn, s, g.N) * 16 + quad * 4;
+                        float4 o = make_float4(acc[s][t][0], acc[s][t][1], acc[s][t][2], acc[s][t][3]);
+                        if (EPI == EPI_RESIDUAL) {
+                            o.x = r[s4][t].x + acc[s][t][0];
+                            o.y = r[s4][t].y + acc[s][t][1];
+                            o.z = r[s4][t].z + acc[s][t][2];
+                            o.w = r[s4][t].w + acc[s][t][3];
+                        }
+                        *reinterpret_cast<float4*>(g.out + (size_t)m * g.N + n) = o;
+                        normed[h][0] = pack_bf16x2(o.x * gn[s4].x, o.y * gn[s4].y);
+                        normed[h][1] = pack_bf16x2(o.z * gn[s4].z, o.w * gn[s4].w);
+                        if (g.next_gain) {
+                            sq[t] += o.x * o.x;
+                            sq[t] += o.y * o.y;
+                            sq[t] += o.z * o.z;
+                            sq[t] += o.w * o.w;
+                        }
                     }
-                    *reinterpret_cast<float4*>(g.out + (size_t)m * g.N + n) = o;
                     if (g.next_gain) {
-                        *reinterpret_cast<uint2*>(g.out_n + act_index(m, n, g.N)) =
-                            make_uint2(pack_bf16x2(o.x * gn[s4].x, o.y * gn[s4].y), pack_bf16x2(o.z * gn[s4].z, o.w * gn[s4].w));
-                        sq[t] += o.x * o.x;
-                        sq[t] += o.y * o.y;
-                        sq[t] += o.z * o.z;
-                        sq[t] += o.w * o.w;
+                        const int n = strip_of<EPI>(nb, wn, 4 * half + s2 + (quad & 1), g.N) * 16 + (quad & 2) * 4;
+                        *reinterpret_cast<uint4*>(g.out_n + act_index(m, n, g.N)) = pair_blocks(normed[0], normed[1]);
                     }
                 }
             }
