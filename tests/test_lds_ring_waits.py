@@ -180,7 +180,8 @@ def prefill_attention_case(symbol):
     mem[TILES] = b"".join(struct.pack("<4I", *t) for t in tiles)
     a = prefill_args(L, 3 * tile, 256, hidden, inner, heads, kv, d, 1024, max_blocks, max_blocks)
     explicit = [a, struct.pack("<Q", Q), struct.pack("<Q", KV), struct.pack("<Q", ATT), struct.pack("<Q", TILES)]
-    runs = replay(k, explicit, (len(tiles), kv, 1), waves * 64, mem, [(i, kv - 1, 0) for i in range(len(tiles))])
+    # Workgroup kv t + h takes tile t for KV head h: each tile for the last head.
+    runs = replay(k, explicit, (len(tiles) * kv, 1, 1), waves * 64, mem, [(i * kv + kv - 1, 0, 0) for i in range(len(tiles))])
     check(runs, f"prefill_attention<{tile}, {waves}, {cg}, {d}> (group {group})")
 
 

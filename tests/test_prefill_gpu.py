@@ -63,6 +63,25 @@ def test_runs_of_any_length_continue_each_other(ctx, lengths):
         assert within(distance(dec.step(t, x[t]), ref.decode(t, x[t])))
 
 
+@pytest.mark.parametrize("lengths", [(192,), (191, 1), (17, 175)])
+def test_runs_that_end_at_the_capacity_match_the_oracle(ctx, lengths):
+    """Runs ending at the cache's last position (capacity 192: three 64-position blocks, the last
+    run's tiles ending on it), against the oracle, outputs and the whole cache."""
+    spec = tiny_spec(layers=2)
+    cap = 192
+    dec = make_decoder(ctx, spec, cap)
+    ref = oracle_stack(spec, cap)
+    x = inputs(spec, cap)
+    print(f"[prefill] runs {lengths} to the capacity {cap}", flush=True)
+    start = 0
+    for n in lengths:
+        check_rows(dec.prefill(start, x[start : start + n]), ref.prefill(start, x[start : start + n]), f"run from {start}")
+        start += n
+    k, v = dec.read_cache(0, cap)
+    assert within(distance(k, ref.k[:, :, :cap])) and within(distance(v, ref.v[:, :, :cap]))
+    dec.close()
+
+
 def test_several_runs_at_once_are_bit_for_bit_as_alone(ctx):
     spec = tiny_spec(layers=2)
     cap = 512

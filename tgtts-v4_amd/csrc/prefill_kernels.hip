@@ -728,14 +728,16 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     // slot's block ids.
     extern __shared__ uint4 attn_ring[];
     uint32_t* block_ids = reinterpret_cast<uint32_t*>(attn_ring + NS * ATTN_STAGE);
-    const PrefillTile tile = tiles[blockIdx.x];
+    // Workgroup KV t + kv takes tile t for KV head kv: a tile's heads are dispatched together, in
+    // the tiles' order (the longest first), so that the last workgroups to start are short ones.
+    const int kv = (int)(blockIdx.x % (uint32_t)a.kv_heads);
+    const PrefillTile tile = tiles[blockIdx.x / (uint32_t)a.kv_heads];
     // A tile that leaves the tensors (1 to TILE positions, of a slot of the table, inside the
     // cache's capacity and the M_pad rows) is skipped by the whole workgroup before any barrier:
     // the host builds valid ones, and a caller's own tiles in device memory cannot be checked there.
     if (tile.count == 0 || tile.count > (uint32_t)TILE || tile.slot >= (uint32_t)a.nslots || tile.count > (uint32_t)a.capacity ||
         tile.pos0 > (uint32_t)a.capacity - tile.count || tile.count > (uint32_t)a.M_pad || tile.row0 > (uint32_t)a.M_pad - tile.count)
         return;
-    const int kv = blockIdx.y;
     // The wave's index, uniform: the branches on it below are the whole wave's.
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     const int lane = threadIdx.x % WAVE;
@@ -917,7 +919,7 @@ void gemm(const char* label, const PrefillArgs& a, const GemmArgs& g, hipStream_
 template <int D>
 hipError_t attention(const PrefillArgs& a, const uint16_t* q, const uint16_t* kv, uint16_t* attended, const PrefillTile* tiles,
                      int ntiles, size_t lds, hipStream_t stream, DispatchTimer* timer) {
-    const dim3 grid(ntiles, a.kv_heads);
+    const dim3 grid((uint32_t)ntiles * (uint32_t)a.kv_heads);
     switch (a.heads / a.kv_heads) {
         case 1: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 2, 1, D>, grid, dim3(2 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
         case 2: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 4, 1, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
