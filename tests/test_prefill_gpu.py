@@ -98,6 +98,33 @@ def test_several_runs_at_once_are_bit_for_bit_as_alone(ctx):
         row += n
 
 
+def test_a_run_in_a_decoder_of_16_row_strips_is_bit_for_bit_as_in_one_of_4_row_strips(ctx):
+    """A decoder of more than 16 rows keeps o_proj and down_proj in 16-row strips, one of 16 or
+    fewer in 4-row strips: the same runs prefilled in each (together in the 20-row one, alone in
+    1-row ones) give the same bits, outputs and the steps after them."""
+    import tgx
+
+    spec = tiny_spec(layers=2)
+    cap = 512
+    lengths = [300, 45, 129]
+    x = inputs(spec, sum(lengths) + 1)
+    wide = make_decoder(ctx, spec, cap, rows=20, slots=20)
+    print(f"[prefill] runs {lengths} in a 20-row decoder against 1-row ones", flush=True)
+    together = wide.prefill_runs([(5, 0, 300), (0, 0, 45), (19, 0, 129)], x[: sum(lengths)])
+    row = 0
+    for slot, n in zip((5, 0, 19), lengths):
+        alone_dec = make_decoder(ctx, spec, cap)
+        alone = alone_dec.prefill(0, x[row : row + n])
+        assert np.array_equal(together[row : row + n].view(np.uint32), alone.view(np.uint32)), f"run of {n}"
+        # The step after the run reads the cache the prefill wrote.
+        a = alone_dec.step(n, x[-1])
+        b = wide.step_rows([tgx.Row(position=n, slot=slot)] + [None] * 19, np.repeat(x[-1:], 20, axis=0))[0]
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step after the run of {n}"
+        alone_dec.close()
+        row += n
+    wide.close()
+
+
 def test_a_long_run_in_slots_past_the_first(ctx):
     """Two runs of 600 positions in slots 1 and 2 of a 2-layer stack, against the oracle."""
     spec = tiny_spec(layers=2)

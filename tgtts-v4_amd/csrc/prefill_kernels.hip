@@ -523,35 +523,45 @@ prefill_gemm(PrefillArgs a, GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// prefill_norm: a wave to a row: lane l sums the squares of its K/64 elements in order, the lanes
-// added by a butterfly (norm.glsl:12-29); rows past M are written zero.
-template <bool FINAL>
+// prefill_norm: a wave to a row: lane l sums the squares of its PL = K/64 elements in order, the
+// lanes added by a butterfly (norm.glsl:12-29); rows past M are written zero. A lane issues all of
+// its row's and gain's loads before it uses any.
+template <bool FINAL, int PL>
 __global__ void __launch_bounds__(256) prefill_norm(PrefillArgs a, const float* __restrict__ x, const float* __restrict__ gain,
                                                     uint16_t* __restrict__ out_bf16, float* __restrict__ out_f32) {
     const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (row >= a.M_pad) return;
-    const int K = a.hidden, per_lane = K / WAVE;
+    constexpr int K = PL * WAVE, per_lane = PL;
     if (row >= a.M) {
         if (!FINAL)
+#pragma unroll
             for (int e = 0; e < per_lane; e += 8)
                 *reinterpret_cast<uint4*>(out_bf16 + act_index(row, lane * per_lane + e, K)) = make_uint4(0, 0, 0, 0);
         return;
     }
     const float* r = x + (size_t)row * K + lane * per_lane;
+    float4 xv[PL / 4], gv[PL / 4];
+#pragma unroll
+    for (int i = 0; i < PL / 4; ++i) xv[i] = *reinterpret_cast<const float4*>(r + 4 * i);
+#pragma unroll
+    for (int i = 0; i < PL / 4; ++i) gv[i] = *reinterpret_cast<const float4*>(gain + lane * per_lane + 4 * i);
+    // The sum starts at a zero the compiler cannot see (it would fold 0 + x0 x0 to a product and
+    // fuse the next term the other way round): every term is an FMA onto the sum, in order.
     float squares = 0.f;
-    for (int e = 0; e < per_lane; e += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(r + e);
+    asm volatile("" : "+v"(squares));
+#pragma unroll
+    for (int i = 0; i < PL / 4; ++i) {
+        const float4 v = xv[i];
         squares += v.x * v.x;
         squares += v.y * v.y;
         squares += v.z * v.z;
         squares += v.w * v.w;
     }
     const float scale = 1.0f / sqrtf(wave_sum(squares) / (float)K + a.eps);
+#pragma unroll
     for (int e = 0; e < per_lane; e += 8) {
-        const float4 v0 = *reinterpret_cast<const float4*>(r + e);
-        const float4 v1 = *reinterpret_cast<const float4*>(r + e + 4);
-        const float4 g0 = *reinterpret_cast<const float4*>(gain + lane * per_lane + e);
-        const float4 g1 = *reinterpret_cast<const float4*>(gain + lane * per_lane + e + 4);
+        const float4 v0 = xv[e / 4], v1 = xv[e / 4 + 1];
+        const float4 g0 = gv[e / 4], g1 = gv[e / 4 + 1];
         const float n[8] = {v0.x * scale * g0.x, v0.y * scale * g0.y, v0.z * scale * g0.z, v0.w * scale * g0.w,
                             v1.x * scale * g1.x, v1.y * scale * g1.y, v1.z * scale * g1.z, v1.w * scale * g1.w};
         if (FINAL) {
@@ -1074,10 +1084,15 @@ hipError_t launch_prefill_attention(const PrefillArgs& a, const uint16_t* q, con
 hipError_t launch_prefill_norm(const PrefillArgs& a, bool final, const float* x, const float* gain, uint16_t* out_bf16,
                                float* out_f32, hipStream_t stream, DispatchTimer* timer) {
     const dim3 rows4((a.M_pad + 3) / 4);
+    // hidden is 1024 or 2048 (the shape check's).
+    if (a.hidden != 1024 && a.hidden != 2048) return hipErrorInvalidValue;
+    const bool wide = a.hidden == 2048;
     if (final)
-        dispatch("prefill_final_norm", prefill_norm<true>, rows4, dim3(256), 0, stream, timer, a, x, gain, (uint16_t*)nullptr, out_f32);
+        dispatch("prefill_final_norm", wide ? prefill_norm<true, 32> : prefill_norm<true, 16>, rows4, dim3(256), 0, stream, timer, a, x,
+                 gain, (uint16_t*)nullptr, out_f32);
     else
-        dispatch("prefill_norm", prefill_norm<false>, rows4, dim3(256), 0, stream, timer, a, x, gain, out_bf16, (float*)nullptr);
+        dispatch("prefill_norm", wide ? prefill_norm<false, 32> : prefill_norm<false, 16>, rows4, dim3(256), 0, stream, timer, a, x, gain,
+                 out_bf16, (float*)nullptr);
     return hipGetLastError();
 }
 
