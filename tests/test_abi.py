@@ -122,10 +122,10 @@ def test_the_backbone_shapes_are_taken():
     tgx.check_shape(tgx.Shape(rope=False, layers=8), tgx.Batch(rows=4, slots=8))
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(16, 16), (16, 8), (16, 4), (16, 2), (32, 2)])
+@pytest.mark.parametrize("heads,kv_heads", [(16, 16), (16, 8), (16, 4), (16, 2), (32, 2), (48, 16), (80, 16), (48, 8), (80, 8), (48, 4)])
 def test_groups_of_one_to_sixteen_query_heads_a_kv_head_are_taken(heads, kv_heads):
-    """Groups of 1, 2, 4, 8 and 16 query heads to a KV head, each with its own prefill attention
-    instance and decode attention columns."""
+    """Groups of 1 to 16 query heads to a KV head (here 1, 2, 4, 8, 16 and 3, 5, 6, 10, 12), each
+    with a prefill attention instance and decode attention columns."""
     import tgx
 
     tgx.check_shape(tgx.Shape(heads=heads, kv_heads=kv_heads), tgx.Batch(rows=4, slots=4))
@@ -135,11 +135,12 @@ def test_groups_of_one_to_sixteen_are_taken_and_thirty_two_refused_with_its_reas
     import tgx
 
     for heads, kv, head_dim in ((16, 16, 64), (16, 8, 64), (16, 4, 64), (16, 2, 64), (32, 2, 64), (16, 1, 128), (16, 2, 128),
-                                (32, 2, 128), (48, 3, 128)):
+                                (32, 2, 128), (48, 3, 128), (24, 8, 128), (40, 8, 128), (48, 16, 64)):
         tgx.check_shape(tgx.Shape(heads=heads, kv_heads=kv, head_dim=head_dim), tgx.Batch(rows=1, slots=1))
-    with pytest.raises(tgx.TgxError) as e:
-        tgx.check_shape(tgx.Shape(heads=32, kv_heads=1), tgx.Batch(rows=1, slots=1))
-    assert e.value.kind == "shape" and "1, 2, 4, 8 or 16" in str(e.value)
+    for heads, kv in ((32, 1), (34, 2), (16, 3)):
+        with pytest.raises(tgx.TgxError) as e:
+            tgx.check_shape(tgx.Shape(heads=heads, kv_heads=kv), tgx.Batch(rows=1, slots=1))
+        assert e.value.kind == "shape" and "a whole group of 1 to 16" in str(e.value)
 
 
 def test_null_arguments_are_refused_with_a_message():

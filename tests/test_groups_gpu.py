@@ -1,9 +1,12 @@
-"""Every group of query heads to a KV head the shape check takes, on the GPU against the oracle:
-16 query heads over 16, 8 and 4 KV heads (groups 1, 2 and 4), and 32 over 2 (a group of 16; its
+"""Groups of query heads to a KV head the shape check takes, on the GPU against the oracle: 16
+query heads over 16, 8 and 4 KV heads (groups 1, 2 and 4), and 32 over 2 (a group of 16; its
 q/k/v rows a multiple of the prefill GEMM's 256) and at head_dim 128 16 over 1 (the backbone's 16
-over 2, a group of 8, is every other test's shape). The reference's attention takes any group
-(kernels/glsl/attention_split.comp:24-27); here each group has its own prefill attention
-instance and the decode attention's columns past the group read its last head again.
+over 2, a group of 8, is every other test's shape); groups that do not divide 16, whose prefill
+column groups leave columns spare: 3 (48 over 16), 5 (80 over 16), 6 (48 over 8) and 12 (48 over
+4) at head_dim 64, 3 and 5 at 128 (24 and 40 over 8). The reference's attention takes any group
+(kernels/glsl/attention_split.comp:24-27); here a prefill attention instance takes the groups
+whose column groups hold the same number of positions, and the decode attention's columns past
+the group read its last head again.
 
 For each group, a 2-layer stack: two prefill runs at once in two slots (ragged lengths, a tile
 of positions left part-filled), then decode steps of both rows, per position against the fp64
@@ -26,7 +29,11 @@ def group_spec(kv_heads, head_dim=64, heads=16):
     return StackSpec(layers=2, heads=heads, kv_heads=kv_heads, head_dim=head_dim, dtype="bf16", seed=heads + kv_heads + head_dim)
 
 
-@pytest.mark.parametrize("heads,kv_heads,head_dim", [(16, 16, 64), (16, 8, 64), (16, 4, 64), (32, 2, 64), (16, 1, 128)])
+@pytest.mark.parametrize(
+    "heads,kv_heads,head_dim",
+    [(16, 16, 64), (16, 8, 64), (16, 4, 64), (32, 2, 64), (16, 1, 128), (48, 16, 64), (80, 16, 64), (48, 8, 64), (48, 4, 64),
+     (24, 8, 128), (40, 8, 128)],
+)
 def test_prefill_and_decode_at_each_group_match_the_oracle_and_rows_are_as_alone(ctx, heads, kv_heads, head_dim):
     spec = group_spec(kv_heads, head_dim, heads)
     print(f"group {spec.heads // kv_heads}: {spec.heads} heads over {kv_heads} KV heads, 2 layers", flush=True)

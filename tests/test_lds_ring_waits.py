@@ -160,7 +160,7 @@ def prefill_gemm_case(symbol):
 
 def test_prefill_attention_reads_no_chunk_before_it_lands():
     symbols = instances(assembly("prefill_kernels.hip"), "prefill_attention")
-    assert len(symbols) == 10, symbols  # groups 1, 2, 4, 8, 16 at head widths 64 and 128
+    assert len(symbols) == 14, symbols  # column groups of 16, 8, 5, 4, 3, 2, 1 positions at head widths 64 and 128
     for symbol in symbols:
         prefill_attention_case(symbol)
 

@@ -696,19 +696,26 @@ struct LazySoftmax {
 // positions: a 64-position block at D 64, half a block at D 128, so that a chunk's keys and values
 // are 16 KiB either way); each column keeps its running maximum, sum and output
 // (attention_rows.comp:71-116).
-// A workgroup's tile: ATTN_TILE positions of a run, except for 8 query heads to a KV head, where it
-// takes 16 positions with four waves (eight at D 128), so that two workgroups share a CU: their
-// barriers are their own, and one's softmax runs beside the other's products. At 16 query heads to
-// a KV head a column group is one position's 16 heads: eight waves of two column groups take 16
-// positions at D 64, and eight of one take 8 at D 128 (four column groups a wave, 32 positions,
-// would hold more than a wave's registers and spill beside the ring's waits, which count loads in
-// issue order). Groups of 1, 2, 4, 8 and 16 have an instance each.
+// A workgroup's tile, by the positions a column group holds (per_col = 16 / group, any group of 1
+// to 16): ATTN_TILE positions at groups 1, 2 and 4 (a column group of 16, 8, 4 positions; one a
+// wave); at group 3 (5 positions) ATTN_TILE_3 and at 5 (3 positions) ATTN_TILE_5, four waves of two
+// column groups at D 64 and eight of one at D 128; at groups 6 to 8 (2 positions) 16 positions with
+// four waves of two (eight of one at D 128), so that two workgroups share a CU: their barriers are
+// their own, and one's softmax runs beside the other's products; at groups 9 to 16 a column group is
+// one position's heads: eight waves of two column groups take 16 positions at D 64, and eight of one
+// take 8 at D 128 (four column groups a wave, 32 positions, would hold more than a wave's registers
+// and spill beside the ring's waits, which count loads in issue order).
 constexpr int ATTN_TILE = 32;
+constexpr int ATTN_TILE_3 = 40, ATTN_TILE_5 = 24;
 constexpr int ATTN_TILE_8 = 16;
 constexpr int ATTN_TILE_16 = 16, ATTN_TILE_16_D128 = 8;
 // The positions a workgroup takes for `group` query heads to a KV head and heads of `head_dim`.
 __host__ __device__ constexpr int attention_tile(int group, int head_dim) {
-    return group == 16 ? (head_dim == 128 ? ATTN_TILE_16_D128 : ATTN_TILE_16) : group == 8 ? ATTN_TILE_8 : ATTN_TILE;
+    return group > 8   ? (head_dim == 128 ? ATTN_TILE_16_D128 : ATTN_TILE_16)
+           : group > 5 ? ATTN_TILE_8
+           : group == 5 ? ATTN_TILE_5
+           : group == 3 ? ATTN_TILE_3
+                        : ATTN_TILE;
 }
 // The attention's ring of key-and-value stages: a stage is one chunk (16 KiB), ATTN_STAGES of them,
 // up to ATTN_STAGES - 2 in flight beyond the two being taken.
@@ -724,7 +731,10 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     constexpr int THREADS = WAVES * WAVE;
     constexpr int TOK = TILE / WAVES;          // positions to a wave
     constexpr int per_col = TOK / CG;          // positions to a column group
-    constexpr int group = 16 / per_col;
+    // The query heads a KV head serves (16 / per_col of them, or fewer: a column group's columns
+    // past per_col group repeat its last real one, computed alike and never stored).
+    const int group = a.heads / a.kv_heads;
+    const int used = per_col * group;
     static_assert(CG <= 2, "two column groups a wave at most: more spill");
     constexpr int CHUNK = attention_chunk(D);  // positions a stage holds
     constexpr int PT = CHUNK / 16, KS = PT / 2, DS = D / 32, DT = D / 16;
@@ -765,10 +775,11 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     }
     uint4 qf[CG][DS];
     uint32_t cpos[CG];
+    const int colr = min(col, used - 1);  // the real column this one computes
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
-        const int tok = w * TOK + cg * per_col + col / group;  // within the tile
-        const int head = kv * group + col % group;
+        const int tok = w * TOK + cg * per_col + colr / group;  // within the tile
+        const int head = kv * group + colr % group;
         const size_t row = tile.row0 + (tok < (int)tile.count ? tok : 0);
         cpos[cg] = tile.pos0 + tok;
 #pragma unroll
@@ -898,9 +909,9 @@ __global__ void __launch_bounds__(WAVES * WAVE) __attribute__((amdgpu_waves_per_
     wait_vm<0>();
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
-        const int tok = w * TOK + cg * per_col + col / group;
-        if (tok >= (int)tile.count) continue;
-        const int head = kv * group + col % group;
+        const int tok = w * TOK + cg * per_col + colr / group;
+        if (col >= used || tok >= (int)tile.count) continue;
+        const int head = kv * group + colr % group;
         const size_t row = tile.row0 + tok;
         const float inv = 1.0f / sm[cg].lsum[0];
 #pragma unroll
@@ -930,27 +941,35 @@ template <int D>
 hipError_t attention(const PrefillArgs& a, const uint16_t* q, const uint16_t* kv, uint16_t* attended, const PrefillTile* tiles,
                      int ntiles, size_t lds, hipStream_t stream, DispatchTimer* timer) {
     const dim3 grid((uint32_t)ntiles * (uint32_t)a.kv_heads);
-    switch (a.heads / a.kv_heads) {
-        case 1: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 2, 1, D>, grid, dim3(2 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
-        case 2: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 4, 1, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
-        case 4: dispatch("prefill_attention", prefill_attention<ATTN_TILE, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles); break;
-        // 8 heads: at D 64 four waves of two column groups; at D 128 eight waves of one (two
-        // groups' outputs and scores would hold more than a wave's registers).
-        case 8:
-            if constexpr (D == 64)
-                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 4, 2, D>, grid, dim3(4 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
-            else
-                dispatch("prefill_attention", prefill_attention<ATTN_TILE_8, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
-            break;
-        // 16 heads: a position to a column group, eight waves of two at D 64, of one at D 128.
-        case 16:
-            if constexpr (D == 64)
-                dispatch("prefill_attention", prefill_attention<ATTN_TILE_16, 8, 2, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
-            else
-                dispatch("prefill_attention", prefill_attention<ATTN_TILE_16_D128, 8, 1, D>, grid, dim3(8 * WAVE), lds, stream, timer, a, q, kv, attended, tiles);
-            break;
-        default: return hipErrorInvalidValue;
+    if (a.kv_heads <= 0 || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
+    const int group = a.heads / a.kv_heads;
+#define TGX_ATTENTION(TILE_, WAVES_, CG_) \
+    dispatch("prefill_attention", prefill_attention<TILE_, WAVES_, CG_, D>, grid, dim3(WAVES_ * WAVE), lds, stream, timer, a, q, kv, attended, tiles)
+    // At D 128 a wave holds one column group: two groups' outputs and scores would hold more than
+    // its registers.
+    if (group == 1)
+        TGX_ATTENTION(ATTN_TILE, 2, 1);
+    else if (group == 2)
+        TGX_ATTENTION(ATTN_TILE, 4, 1);
+    else if (group == 3) {
+        if constexpr (D == 64) TGX_ATTENTION(ATTN_TILE_3, 4, 2);
+        else TGX_ATTENTION(ATTN_TILE_3, 8, 1);
+    } else if (group == 4)
+        TGX_ATTENTION(ATTN_TILE, 8, 1);
+    else if (group == 5) {
+        if constexpr (D == 64) TGX_ATTENTION(ATTN_TILE_5, 4, 2);
+        else TGX_ATTENTION(ATTN_TILE_5, 8, 1);
+    } else if (group <= 8) {
+        if constexpr (D == 64) TGX_ATTENTION(ATTN_TILE_8, 4, 2);
+        else TGX_ATTENTION(ATTN_TILE_8, 8, 1);
+    } else if (group <= 16) {
+        // A position to a column group, eight waves of two at D 64, of one at D 128.
+        if constexpr (D == 64) TGX_ATTENTION(ATTN_TILE_16, 8, 2);
+        else TGX_ATTENTION(ATTN_TILE_16_D128, 8, 1);
+    } else {
+        return hipErrorInvalidValue;
     }
+#undef TGX_ATTENTION
     return hipSuccess;
 }
 
@@ -1024,7 +1043,9 @@ hipError_t prefill_prepare(size_t device_lds) {
                           (const void*)prefill_attention<ATTN_TILE, 8, 1, 64>, (const void*)prefill_attention<ATTN_TILE_8, 4, 2, 64>,
                           (const void*)prefill_attention<ATTN_TILE, 2, 1, 128>, (const void*)prefill_attention<ATTN_TILE, 4, 1, 128>,
                           (const void*)prefill_attention<ATTN_TILE, 8, 1, 128>, (const void*)prefill_attention<ATTN_TILE_8, 8, 1, 128>,
-                          (const void*)prefill_attention<ATTN_TILE_16, 8, 2, 64>, (const void*)prefill_attention<ATTN_TILE_16_D128, 8, 1, 128>})
+                          (const void*)prefill_attention<ATTN_TILE_16, 8, 2, 64>, (const void*)prefill_attention<ATTN_TILE_16_D128, 8, 1, 128>,
+                          (const void*)prefill_attention<ATTN_TILE_3, 4, 2, 64>, (const void*)prefill_attention<ATTN_TILE_3, 8, 1, 128>,
+                          (const void*)prefill_attention<ATTN_TILE_5, 4, 2, 64>, (const void*)prefill_attention<ATTN_TILE_5, 8, 1, 128>})
         if ((e = allow(f, device_lds)) != hipSuccess) return e;
     return allow((const void*)prefill_gemm<EPI_SILU, QKV_ROWS, GATE_UP_TM>, device_lds);
 }

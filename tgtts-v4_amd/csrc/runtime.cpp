@@ -186,12 +186,12 @@ tgx_status check_shape(const tgx_shape* in, Shape* s) {
     if (s->capacity > decode_max_capacity(s->head_dim))
         return refuse("capacity " + std::to_string(s->capacity) + " past the attention's " +
                       std::to_string(decode_max_capacity(s->head_dim)) + " at head_dim " + std::to_string(s->head_dim));
-    // Query heads to a KV head: 1, 2, 4, 8 or 16, each with a prefill attention instance whose
-    // registers hold its tile (the reference takes any group, attention_split.comp:24-27; the
-    // decode attention's 16 columns take up to 16 heads).
-    if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 16 || 16 % (s->heads / s->kv_heads) != 0)
+    // Query heads to a KV head: any group of 1 to 16 (the reference takes any group,
+    // attention_split.comp:24-27): the decode attention's 16 MFMA columns hold up to 16 heads, and
+    // a prefill attention column group 16 / group positions of them.
+    if (s->kv_heads <= 0 || s->heads % s->kv_heads != 0 || s->heads / s->kv_heads > 16)
         return refuse(std::to_string(s->heads) + " heads over " + std::to_string(s->kv_heads) +
-                      " KV heads: a group of 1, 2, 4, 8 or 16");
+                      " KV heads: a whole group of 1 to 16 query heads a KV head");
     // The prefill GEMM takes q/k/v's rows in tiles of 256.
     if ((s->heads + 2 * s->kv_heads) * s->head_dim % 256 != 0)
         return refuse(std::to_string(s->heads) + " + 2 x " + std::to_string(s->kv_heads) + " heads of " + std::to_string(s->head_dim) +
