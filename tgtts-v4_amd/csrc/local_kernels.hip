@@ -565,7 +565,9 @@ __global__ void __launch_bounds__(256) local_attention(LocalArgs a, const uint16
 // Else the next norm's input for the GEMM that applies the row's scale: normed = v g in bf16, and
 // v's sums of squares over each 64 columns into row_sq, in the order local_gemm_ring's epilogue
 // adds them (squares4 over 4 columns, (a + b) + (c + d) over a lane's 16, then over 4 lanes).
-template <bool FINAL>
+// PARTS (= parts, 0 to LOCAL_MAX_PARTS) is a template argument so that a lane's loads of every part
+// are issued together, not one round trip a part.
+template <bool FINAL, int PARTS>
 __global__ void __launch_bounds__(256) local_add_norm(LocalArgs a, const float* __restrict__ partial, int parts,
                                                       const float* __restrict__ residual, float* __restrict__ sum,
                                                       const float* __restrict__ gain, uint16_t* __restrict__ normed,
@@ -578,9 +580,10 @@ __global__ void __launch_bounds__(256) local_add_norm(LocalArgs a, const float* 
 #pragma unroll
     for (int e = 0; e < PER; e += 4) {
         float4 r = *reinterpret_cast<const float4*>(residual + (size_t)m * K + base + e);
-        if (parts > 0) {
+        if (PARTS > 0) {
             float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int p = 0; p < parts; ++p) {
+#pragma unroll
+            for (int p = 0; p < PARTS; ++p) {
                 const float4 s = *reinterpret_cast<const float4*>(partial + ((size_t)p * a.M_pad + m) * K + base + e);
                 acc.x += s.x;
                 acc.y += s.y;
@@ -842,14 +845,20 @@ hipError_t launch_local_partial(const LocalArgs& a, const LocalGemm& g, int part
 hipError_t launch_local_add_norm(const LocalArgs& a, bool final, const float* partial, int parts, const float* residual, float* sum,
                                  const float* gain, uint16_t* normed, float* row_sq, float* out, hipStream_t stream,
                                  DispatchTimer* timer) {
+    static_assert(LOCAL_MAX_PARTS == 4, "an instance for each count of parts");
     if (parts < 0 || parts > LOCAL_MAX_PARTS) return hipErrorInvalidValue;
     const dim3 rows4((a.M + 3) / 4);
+    using Kernel = decltype(&local_add_norm<true, 0>);
+    static constexpr Kernel finals[] = {local_add_norm<true, 0>, local_add_norm<true, 1>, local_add_norm<true, 2>,
+                                        local_add_norm<true, 3>, local_add_norm<true, 4>};
+    static constexpr Kernel adds[] = {local_add_norm<false, 0>, local_add_norm<false, 1>, local_add_norm<false, 2>,
+                                      local_add_norm<false, 3>, local_add_norm<false, 4>};
     if (final)
-        dispatch("local_final_norm", local_add_norm<true>, rows4, dim3(256), 0, stream, timer, a, partial, parts, residual, sum, gain,
-                 normed, row_sq, out);
+        dispatch("local_final_norm", finals[parts], rows4, dim3(256), 0, stream, timer, a, partial, parts, residual, sum, gain, normed,
+                 row_sq, out);
     else
-        dispatch("local_add_norm", local_add_norm<false>, rows4, dim3(256), 0, stream, timer, a, partial, parts, residual, sum, gain,
-                 normed, row_sq, out);
+        dispatch("local_add_norm", adds[parts], rows4, dim3(256), 0, stream, timer, a, partial, parts, residual, sum, gain, normed,
+                 row_sq, out);
     return hipGetLastError();
 }
 
