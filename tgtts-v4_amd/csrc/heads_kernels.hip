@@ -19,6 +19,7 @@ __global__ void __launch_bounds__(256) gemv_linear(LinearArgs a) {
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int K = a.K0 + a.K1, kblocks = K / 32;
     // Fragment (kb, lane): batch row 16 tile + lane % 16, k = 32 kb + 8 (lane / 16) .. + 7.
+#pragma unroll 8
     for (int i = threadIdx.x; i < kblocks * 64; i += 256) {
         const int kb = i / 64, l = i % 64;
         const int b = tile * 16 + l % 16;
@@ -33,10 +34,19 @@ __global__ void __launch_bounds__(256) gemv_linear(LinearArgs a) {
         xs[i] = v;
     }
     __syncthreads();
+    // Wave w's chain over k-blocks w, w + 4, ... in order, eight k-blocks' weights loaded at once.
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = w; kb < kblocks; kb += 4) {
-        const uint4 af = *reinterpret_cast<const uint4*>(a.w + weight_tile_index(strip, kb, kblocks, 16) + lane * 8);
-        acc = mfma16(af, xs[kb * 64 + lane], acc);
+    constexpr int AHEAD = 8;
+    for (int kb0 = w; kb0 < kblocks; kb0 += 4 * AHEAD) {
+        uint4 af[AHEAD];
+#pragma unroll
+        for (int j = 0; j < AHEAD; ++j) {
+            const int kb = min(kb0 + 4 * j, kblocks - 1);  // past the last, the last again (not used)
+            af[j] = *reinterpret_cast<const uint4*>(a.w + weight_tile_index(strip, kb, kblocks, 16) + lane * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < AHEAD; ++j)
+            if (kb0 + 4 * j < kblocks) acc = mfma16(af[j], xs[(kb0 + 4 * j) * 64 + lane], acc);
     }
     red[w][lane] = acc;
     __syncthreads();
