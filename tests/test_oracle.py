@@ -167,10 +167,11 @@ def test_attention_over_one_position_returns_its_value():
 # ---- the whole stack against an independent float64 model --------------------------------------
 
 
-def torch_stack(spec, weights, x, rope=True, start=0, causal=True, rope_dim=None):
+def torch_stack(spec, weights, x, rope=True, start=0, causal=True, rope_dim=None, gqa_tiled=False):
     """MiniCPM-4 layers over a run of positions from library ops in float64: RMSNorm written out,
     RoPE by rotate_half, torch's scaled_dot_product_attention (causal, GQA by repeat), SiLU.
-    rope_dim (a planted defect when not the head width): the width rotate_half pairs within."""
+    rope_dim (a planted defect when not the head width): the width rotate_half pairs within.
+    gqa_tiled (a planted defect): query head h reads KV head h % kv_heads, not h // group."""
     import torch
     import torch.nn.functional as F
 
@@ -206,8 +207,11 @@ def torch_stack(spec, weights, x, rope=True, start=0, causal=True, rope_dim=None
         if rope:
             q = q * cos + rotate_half(q) * sin
             k = k * cos + rotate_half(k) * sin
-        k = k.repeat_interleave(H // KV, dim=1)
-        v = v.repeat_interleave(H // KV, dim=1)
+        if gqa_tiled:
+            k, v = k.repeat(1, H // KV, 1), v.repeat(1, H // KV, 1)
+        else:
+            k = k.repeat_interleave(H // KV, dim=1)
+            v = v.repeat_interleave(H // KV, dim=1)
         att = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), is_causal=causal)
         att = att.transpose(0, 1).reshape(T, H * d)
         h = h + att @ w[f"layers.{l}.o_proj"].T
@@ -246,6 +250,25 @@ def test_heads_of_128_dimensions_match_the_model_and_a_rope_of_64_fails():
     rows = oracle.Stack(spec, w, 64).prefill_rows(0, x)
     assert np.max(np.abs(rows - want)) <= 1e-9 * np.max(np.abs(want))
     wrong = torch_stack(spec, w, x, rope_dim=64)
+    assert np.max(np.abs(got - wrong)) > 1e-3 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(6, 2), (10, 2), (12, 2), (24, 2)])
+def test_groups_that_do_not_divide_16_match_the_model_and_the_wrong_kv_head_fails(heads, kv_heads):
+    """Groups of 3, 5, 6 and 12 query heads a KV head (the kernels take any group up to 16): a
+    prefill and decode steps against the float64 torch model (GQA by repeat_interleave: head h reads
+    KV head h // group); the model reading KV head h % kv_heads instead must disagree."""
+    import oracle
+    from tgx.synth import StackSpec, embeddings, stack_weights
+
+    spec = StackSpec(hidden=384, inner=768, heads=heads, kv_heads=kv_heads, layers=2, dtype="f32", seed=heads)
+    w = stack_weights(spec)
+    x = embeddings(4, "x", 30, spec.hidden).astype(np.float64)
+    want = torch_stack(spec, w, x)
+    st = oracle.Stack(spec, w, 32)
+    got = np.concatenate([st.prefill(0, x[:20]), np.stack([st.decode(t, x[t]) for t in range(20, 30)])])
+    assert np.max(np.abs(got - want)) <= 1e-10 * np.max(np.abs(want))
+    wrong = torch_stack(spec, w, x, gqa_tiled=True)
     assert np.max(np.abs(got - wrong)) > 1e-3 * np.max(np.abs(want))
 
 
