@@ -577,6 +577,12 @@ tgx_status tgx_read(tgx_memory* mem, uint64_t offset, void* dst, uint64_t bytes)
 typedef enum { TGX_TILES_16 = 0, TGX_TILES_4 = 1, TGX_TILES_QKV = 2, TGX_TILES_QKV128 = 3 } tgx_tiles;
 /* The bytes a [rows][cols] matrix takes as `tiles` (0 for a shape the tiles cannot hold). */
 uint64_t tgx_tiles_bytes(tgx_tiles tiles, int rows, int cols);
+/* The most positions an attention_rows tile may hold for heads over kv_heads of head_dim (0 for a
+ * shape the kernels do not take): 32, 40 at 3 heads a KV head, 24 at 5, 16 at 6 to 16, 8 at 9 to
+ * 16 of 128 dimensions. The kernel skips a tile of more (it cannot refuse what device memory
+ * holds), so a caller sizes its tiles by this. No counterpart in the reference, whose attention
+ * kernel takes a fixed number of positions a workgroup (attention_rows.comp). */
+int tgx_attention_tile(int heads, int kv_heads, int head_dim);
 /* Writes a row-major [rows][cols] matrix of `dtype` at `offset` as `tiles`, rounded to bf16 to
  * nearest even, as tgx_decoder_load lays out its weights (load_stack's write, decode.rs:740-776). */
 tgx_status tgx_write_tiles(tgx_memory* mem, uint64_t offset, const void* src, tgx_dtype dtype, tgx_tiles tiles,

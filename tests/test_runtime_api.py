@@ -132,3 +132,16 @@ def test_weight_tiles_take_whole_strips_and_k_blocks():
     assert rt.tiles_bytes(rt.TILES_4, 1024, 1000) == 0  # columns in k-blocks of 32
     assert rt.tiles_bytes(rt.TILES_QKV, 1040, 1024) == 0  # q/k/v rows a multiple of the head
     assert rt.tiles_bytes(7, 16, 32) == 0
+
+
+def test_attention_tiles_take_the_positions_of_the_groups_instance():
+    """tgx_attention_tile: the positions a prefill attention tile may hold, by the group's instance
+    (16 / group positions to a column group), and 0 for a shape the kernels do not take."""
+    import tgx.runtime as rt
+
+    for (heads, kv, d), want in {(16, 16, 64): 32, (16, 8, 64): 32, (48, 16, 64): 40, (16, 4, 64): 32, (80, 16, 64): 24,
+                                 (48, 8, 64): 16, (16, 2, 64): 16, (16, 2, 128): 16, (48, 4, 64): 16, (48, 4, 128): 8,
+                                 (32, 2, 64): 16, (32, 2, 128): 8, (24, 8, 128): 40}.items():
+        assert rt.attention_tile(heads, kv, d) == want, (heads, kv, d)
+    for heads, kv, d in ((32, 1, 64), (16, 3, 64), (16, 2, 96), (16, 0, 64)):
+        assert rt.attention_tile(heads, kv, d) == 0, (heads, kv, d)

@@ -77,7 +77,7 @@ class PrefillStack:
         self.table_host = np.arange(self.blocks, dtype=np.uint32).reshape(slots, self.max_blocks)
         self.table = M(self.table_host.nbytes)
         self.table.write(self.table_host)
-        self.tile = {8: 16, 16: 16 if D == 64 else 8}.get(H // KV, 32)  # positions an attention tile takes
+        self.tile = rt.attention_tile(H, KV, D)  # positions an attention tile takes
 
     def alloc(self, nbytes):
         import tgx.runtime as rt

@@ -1294,6 +1294,11 @@ uint64_t tgx_tiles_bytes(tgx_tiles tiles, int rows, int cols) {
     return tiles_hold(tiles, rows, cols) ? (uint64_t)rows * cols * 2 : 0;
 }
 
+int tgx_attention_tile(int heads, int kv_heads, int head_dim) {
+    if (kv_heads <= 0 || heads <= 0 || heads % kv_heads != 0 || heads / kv_heads > 16 || (head_dim != 64 && head_dim != 128)) return 0;
+    return prefill_attention_tile(heads / kv_heads, head_dim);
+}
+
 tgx_status tgx_write_tiles(tgx_memory* mem, uint64_t offset, const void* src, tgx_dtype dtype, tgx_tiles tiles, int rows,
                            int cols) {
     clear_error();

@@ -67,6 +67,8 @@ def _lib() -> ctypes.CDLL:
     lib.tgx_read.argtypes = [P, U64, P, U64]
     lib.tgx_tiles_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.tgx_tiles_bytes.restype = U64
+    lib.tgx_attention_tile.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    lib.tgx_attention_tile.restype = ctypes.c_int
     lib.tgx_write_tiles.argtypes = [P, U64, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.tgx_rope_tables.argtypes = [P, P, P]
     lib.tgx_kernel_count.argtypes = []
@@ -140,6 +142,11 @@ def kernel(name: str) -> KernelInfo:
 
 def tiles_bytes(tiles: int, rows: int, cols: int) -> int:
     return int(_lib().tgx_tiles_bytes(tiles, rows, cols))
+
+
+def attention_tile(heads: int, kv_heads: int, head_dim: int) -> int:
+    """The most positions an attention_rows tile may hold for the shape (0: not taken)."""
+    return int(_lib().tgx_attention_tile(heads, kv_heads, head_dim))
 
 
 def rope_tables(shape: Shape) -> tuple:
@@ -307,5 +314,5 @@ def copy_regions(ctx, dst: Memory, src: Memory, regions: Sequence[tuple]) -> Non
 
 __all__ = [
     "BindingInfo", "KernelInfo", "Memory", "Program", "copy_regions", "f32_bits", "kernel", "kernels", "rope_tables",
-    "tiles_bytes", "dispatch", "DEVICE", "UPLOAD", "READBACK", "READ", "WRITE", "TILES_16", "TILES_4", "TILES_QKV", "TILES_QKV128", "U32", "TgxError",
+    "tiles_bytes", "attention_tile", "dispatch", "DEVICE", "UPLOAD", "READBACK", "READ", "WRITE", "TILES_16", "TILES_4", "TILES_QKV", "TILES_QKV128", "U32", "TgxError",
 ]
