@@ -164,10 +164,9 @@ def test_batch_of_64_rows_is_as_alone(ctx):
 
 
 def test_long_contexts_match_the_oracle_and_each_row_is_as_alone(ctx):
-    """Past 512 positions each of the attention's waves takes more than one 64-position block
-    (its turns, two at a time): a row at 1100 positions (18 blocks, three turns) matches the
-    oracle step by step, and each row of a batch of long and short contexts is bit for bit as it
-    is alone."""
+    """Past 256 positions each of the attention's waves takes more than one 32-position turn (two
+    at a time): a row at 1100 positions (35 turns, five for some waves) matches the oracle step by
+    step, and each row of a batch of long and short contexts is bit for bit as it is alone."""
     import tgx
 
     spec = tiny_spec(layers=1)
@@ -196,6 +195,33 @@ def test_long_contexts_match_the_oracle_and_each_row_is_as_alone(ctx):
             got = alone.step(L + k, xs[r][L + k])
             assert np.array_equal(got.view(np.uint32), together[k][r].view(np.uint32)), f"row {r} ({L} positions), step {k}"
         alone.close()
+
+
+def test_a_row_past_16384_positions_steps_as_the_prefill_computes_and_as_alone(ctx):
+    """Past 16384 positions a wave of the attention has more than 64 turns, their cache blocks in a
+    second register: a row at 20000 positions steps as a prefill of one more position computes its
+    last output (the prefill's own kernels, checked against the oracle elsewhere; the oracle would
+    take minutes over 20000 positions), and beside a short row bit for bit as alone."""
+    import tgx
+
+    spec = tiny_spec(layers=1, dtype="bf16")
+    cap, n = 20480, 20000
+    x = inputs(spec, n + 2)
+    print(f"[decode] a row at {n} positions of {cap}", flush=True)
+    whole = make_decoder(ctx, spec, cap)
+    want = whole.prefill_runs([(0, 0, n + 1)], x[: n + 1])[n]
+    whole.close()
+    dec = make_decoder(ctx, spec, cap)
+    dec.prefill_runs([(0, 0, n)], x[:n])
+    got = dec.step(n, x[n])
+    d = distance(got, want)
+    assert within(d), f"step at {n}: {d}"
+    two = make_decoder(ctx, spec, cap, rows=2)
+    two.prefill_runs([(0, 0, n), (1, 0, 40)], np.concatenate([x[:n], x[:40]]))
+    both = two.step_rows([tgx.Row(n, 0), tgx.Row(40, 1)], np.stack([x[n], x[40]]))
+    assert np.array_equal(both[0].view(np.uint32), got.view(np.uint32))
+    two.close()
+    dec.close()
 
 
 def test_launched_steps_move_the_rows_on_as_single_steps_do(ctx):

@@ -438,22 +438,27 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
 
 // ---------------------------------------------------------------------------------------------
 // attention_decode: workgroup (kv, b) attends the `group` query heads KV head kv serves of row b
-// over its slot's positions 0..pos; wave w takes turns w, w + 8, ... (a turn: TURN positions, a
-// 64-position block at head_dim 64, half a block at 128, so that a turn is 8 key and 8 value
-// fragments either way) with an online softmax, two turns' keys and values in flight at once.
-// Per turn, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in bf16 straight
-// from the registers S^T left it in.
+// over its slot's positions 0..pos; wave w takes turns w, w + 8, ... (a turn: TURN = 32 positions,
+// half a cache block, D / 16 key and D / 16 value fragments; at 256 positions all eight waves have
+// one, where whole-block turns left four idle) with an online softmax, two turns' keys and values
+// in flight at once. Per turn, S^T = K Q^T (keys as rows, heads as columns) and O^T += V^T P, P in
+// bf16 straight from the registers S^T left it in.
 // Two memory round trips before the first product: the row's position, the cache blocks of the
-// wave's turns (lane j: the block of turn w + 8 j, from the row's copy of its slot's table) and q
-// together, then the first two turns' keys and values.
-constexpr int attention_turn(int head_dim) { return head_dim == 64 ? BLOCK_TOKENS : BLOCK_TOKENS / 2; }
+// wave's turns (lane j of register r: the block of turn w + 8 (j + 64 r), from the row's copy of
+// its slot's table) and q together, then the first two turns' keys and values.
+constexpr int attention_turn(int head_dim) { return BLOCK_TOKENS / 2; }
+// The positions a row may reach: 32768 at head_dim 64, 16384 at 128 (the block ids of a wave's
+// turns in two registers and one).
+constexpr int attention_capacity(int head_dim) { return head_dim == 64 ? 32768 : 16384; }
 
 template <int D>
 __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, LayerArgs l) {
     constexpr int TURN = attention_turn(D);
     constexpr int PT = TURN / 16, KS = PT / 2, DT = D / 16, DS = D / 32;
     constexpr int KF = PT * DS, VF = DT * KS;  // a turn's key and value fragments
-    static_assert(KF == 8 && VF == 8, "a turn is 8 key and 8 value fragments");
+    static_assert(KF == D / 16 && VF == D / 16, "a turn is D / 16 key and D / 16 value fragments");
+    constexpr int BREGS = attention_capacity(D) / (ATTN_WAVES * WAVE * TURN);  // block-id registers
+    static_assert(BREGS == 1 || BREGS == 2, "one or two registers of a wave's turns' blocks");
     constexpr int TILE = kv_tile(D);
     extern __shared__ float attn_lds[];  // [waves][group][D + 1] partial outputs
     __shared__ float sm_m[ATTN_WAVES][16];
@@ -463,8 +468,11 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     const int H = a.heads, KV = a.kv_heads, group = H / KV;
     const int h = lane % 16;
     const uint32_t pos = a.positions[b];
-    const uint32_t turn_block = a.row_table[(uint32_t)b * (uint32_t)a.max_blocks +
-                                            (uint32_t)min((w + ATTN_WAVES * lane) * TURN / BLOCK_TOKENS, a.max_blocks - 1)];
+    uint32_t turn_block[BREGS];
+#pragma unroll
+    for (int r = 0; r < BREGS; ++r)
+        turn_block[r] = a.row_table[(uint32_t)b * (uint32_t)a.max_blocks +
+                                    (uint32_t)min((w + ATTN_WAVES * (lane + WAVE * r)) * TURN / BLOCK_TOKENS, a.max_blocks - 1)];
     // Columns past the group read its last head again; nothing reads what they give.
     uint4 qf[DS];
 #pragma unroll
@@ -474,7 +482,13 @@ __global__ void __launch_bounds__(ATTN_THREADS) attention_decode(DecodeArgs a, L
     const int turns = (int)(pos / TURN) + 1;
 
     // Turn j's block, and whether the wave has it (the slot may hold no block there).
-    auto block_of_turn = [&](int j) { return (uint32_t)__builtin_amdgcn_readlane((int)turn_block, min(j, WAVE - 1)); };
+    auto block_of_turn = [&](int j) {
+        if constexpr (BREGS == 1)
+            return (uint32_t)__builtin_amdgcn_readlane((int)turn_block[0], min(j, WAVE - 1));
+        else
+            return (uint32_t)(j < WAVE ? __builtin_amdgcn_readlane((int)turn_block[0], j)
+                                       : __builtin_amdgcn_readlane((int)turn_block[1], min(j - WAVE, WAVE - 1)));
+    };
     auto has = [&](int j) { return w + ATTN_WAVES * j < turns && block_of_turn(j) < (uint32_t)a.nblocks; };
     // Turn j's keys and values: its positions' key fragments are one run of the block's key tile
     // (8 of them from fragment 8 half), its value fragments (dt, ks) those of dimensions 16 dt and
@@ -766,7 +780,7 @@ int decode_max_k() { return MAX_CHUNKS * CHUNK_COLS; }
 
 int decode_max_hidden() { return MAX_HIDDEN_CHUNKS * CHUNK_COLS; }
 
-int decode_max_capacity(int head_dim) { return ATTN_WAVES * WAVE * attention_turn(head_dim); }
+int decode_max_capacity(int head_dim) { return attention_capacity(head_dim); }
 
 hipError_t decode_prepare(size_t device_lds) {
     for (const void* f : {(const void*)attention_decode<64>, (const void*)attention_decode<128>}) {
