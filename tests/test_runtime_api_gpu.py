@@ -79,11 +79,12 @@ class StepProgram:
             x_in = self.x if first else self.h_a
             p.dispatch("gemv_qkv_rope", [self.x if first else None, None if first else self.xn_a, None if first else self.sq_a,
                                          self.in_norm[l], self.qkv[l], self.cos, self.sin, self.positions, self.slots_mem,
-                                         self.table, self.q, self.kv[l]], c)
+                                         self.table, self.q, self.kv[l]], c + [strip_rows])
             p.dispatch("attention_decode", [self.q, self.kv[l], self.positions, self.row_table, self.att], c)
             p.dispatch("gemv_residual", [self.att, self.o[l], x_in, self.post_norm[l], self.h_b, self.xn_b, self.sq_b],
                        c + [H * 64, h, strip_rows])
-            p.dispatch("gemv_gate_up", [self.xn_b, self.sq_b, self.gu[l], self.mlp], c)
+            # The squares gemv_residual leaves span its strips' rows.
+            p.dispatch("gemv_gate_up", [self.xn_b, self.sq_b, self.gu[l], self.mlp], c + [strip_rows])
             last = l == L - 1
             p.dispatch("gemv_residual", [self.mlp, self.down[l], self.h_b, None if last else self.in_norm[l + 1], self.h_a,
                                          None if last else self.xn_a, None if last else self.sq_a], c + [inner, h, strip_rows])

@@ -41,8 +41,10 @@ constexpr int MAX_CHUNKS = 6;  // K up to 6144 (down_proj's inner); kernels are 
 // hidden up to 2048 (VoxCPM2's LMs): the norms, q/k/v and gate/up. Past it layer 0's q/k/v, which
 // reads the f32 rows, would hold more than a wave's registers.
 constexpr int MAX_HIDDEN_CHUNKS = 2;
-// A norm's input carries a sum of squares for each SQ_COLS columns of a row.
+// A norm's input carries a sum of squares for each SQ_COLS columns of a row, or for each
+// SQ_WIDE_COLS where the projection that wrote it took strips of that many rows.
 constexpr int SQ_COLS = 4;
+constexpr int SQ_WIDE_COLS = 16;
 
 // Attention: a workgroup of eight waves to each (row, KV head).
 constexpr int ATTN_WAVES = 8;
@@ -132,14 +134,16 @@ struct NormedRows : Operand<CH> {
     }
 };
 
-// The tile's rows' scales 1 / sqrt(sum / K + eps) from their sums of squares over each SQ_COLS
-// columns, sq [B][K / SQ_COLS] (K = CH 1024: 256 CH sums a row): wave w takes tile rows
-// RPW w .. RPW w + RPW - 1, lane l sums 4 l .. 4 l + 3 of each 256 in order, and the lanes'
-// totals are added in a fixed order (wave_sum). The same arithmetic for a row whatever the batch.
-template <int CH>
+// The tile's rows' scales 1 / sqrt(sum / K + eps) from their sums of squares, sq [B][K / cols]
+// (K = CH 1024; cols = SQ_COLS, or SQ_WIDE_COLS when WIDE): wave w takes tile rows
+// RPW w .. RPW w + RPW - 1; lane l of chunk c takes its columns c 1024 + 16 l .. + 15, four
+// 4-column sums added in column order or the one 16-column sum the strip made so; the chunks'
+// are added in chunk order and the lanes' totals in a fixed order (wave_sum). The same arithmetic
+// for a row whatever the batch and whichever width its sums span.
+template <int CH, bool WIDE>
 struct RowSquares {
     static constexpr int RPW = 16 / GEMV_WAVES;  // rows to a wave
-    float4 part[RPW][CH];
+    float4 part[RPW][CH];                        // four 4-column sums, or (WIDE) a 16-column sum in .x
 
     __device__ void load(const float* __restrict__ sq, int B, int tile) {
         const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -147,7 +151,12 @@ struct RowSquares {
         for (int h = 0; h < RPW; ++h) {
             const int b = min(tile * 16 + RPW * w + h, B - 1);
 #pragma unroll
-            for (int c = 0; c < CH; ++c) part[h][c] = load_f4(sq + (size_t)b * (CH * 256) + c * 256 + lane * 4);
+            for (int c = 0; c < CH; ++c) {
+                if constexpr (WIDE)
+                    part[h][c].x = sq[(size_t)b * (CH * 64) + c * 64 + lane];
+                else
+                    part[h][c] = load_f4(sq + (size_t)b * (CH * 256) + c * 256 + lane * 4);
+            }
         }
     }
     // scale[RPW w + h], behind the caller's next barrier.
@@ -158,10 +167,13 @@ struct RowSquares {
             float t = 0.f;
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
-                t += part[h][c].x;
-                t += part[h][c].y;
-                t += part[h][c].z;
-                t += part[h][c].w;
+                float u = part[h][c].x;
+                if constexpr (!WIDE) {
+                    u += part[h][c].y;
+                    u += part[h][c].z;
+                    u += part[h][c].w;
+                }
+                t = c == 0 ? u : t + u;
             }
             const float total = wave_sum(t);
             if (lane == 0) scale[RPW * w + h] = 1.0f / sqrtf(total / (float)(CH * CHUNK_COLS) + eps);
@@ -253,7 +265,7 @@ __device__ __forceinline__ long block_of(const DecodeArgs& a, uint32_t slot, uin
 // the first), else as the f32 rows. The epilogue's thread (p, c) (pair p, tile row c; the first
 // 128 threads) loads its row's position and slot first of all, and the RoPE factors and cache
 // block that hang on them while the products' operands are on their way.
-template <int CH, bool PRENORMED, int D>
+template <int CH, bool PRENORMED, int D, bool WIDE = false>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, LayerArgs l) {
     constexpr int R = QKV_ROWS;
     constexpr int EPI = (R / 2) * 16;  // epilogue threads
@@ -271,7 +283,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
         pos = a.positions[min(b, a.rows - 1)];
         slot = a.slots[min(b, a.rows - 1)];
     }
-    RowSquares<CH> squares;
+    RowSquares<CH, WIDE> squares;
     RawRows<CH> xb;
     NormedRows<CH> xn;
     if constexpr (PRENORMED) {
@@ -346,7 +358,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_qkv_rope(DecodeArgs a, Laye
 // sums of squares. The strips' weights are read once for the TT tiles, and each tile's products
 // are the same chains as with one tile to a workgroup; the tiles' partial sums go through LDS two
 // at a time.
-template <int CH, int TT>
+template <int CH, int TT, bool WIDE = false>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_gate_up(DecodeArgs a, LayerArgs l) {
     constexpr int TS = TT < 2 ? TT : 2;  // tiles reduced at once
     __shared__ f32x4 red[TS][GEMV_WAVES * 2 * 64];
@@ -354,7 +366,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_gate_up(DecodeArgs a, Layer
     const int s = blockIdx.x, tile0 = blockIdx.y * TT;
     const int strip[2] = {s, s + a.inner / 16};
     const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    RowSquares<CH> squares[TT];
+    RowSquares<CH, WIDE> squares[TT];
     RawRows<CH> x[TT];
     Gemv<2, CH> g;
 #pragma unroll
@@ -395,8 +407,10 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_gate_up(DecodeArgs a, Layer
 // ---------------------------------------------------------------------------------------------
 // gemv_residual: out = residual + W x, workgroup (strip, tile): a strip of R rows over the whole
 // of K. The epilogue's thread (c, q) (tile row c, rows 4 q .. 4 q + 3 of the strip; the first
-// 4 R threads) loads its residual and next-norm gains first of all, and with
-// next_norm set also writes out next_norm in bf16 and the 4 rows' sum of squares, in row order.
+// 4 R threads) loads its residual and next-norm gains first of all, and with next_norm set also
+// writes out next_norm in bf16 and the sum of squares of the strip's R columns of row c: its 4 in
+// order, and at R = 16 the four threads' sums added in column order (the order a 4-column reader
+// adds them in).
 template <int CH, int R>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, ResidualArgs r) {
     constexpr int EPI = 16 * (R / SQ_COLS);
@@ -420,19 +434,29 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
     all_issued();
     g.run(x.xf);
     spill<1>(g.acc, red);
-    if (threadIdx.x >= EPI || b >= a.rows) return;
+    if (threadIdx.x >= EPI) return;  // whole waves stay (EPI is 16 or 64): the shuffles below read every lane
     const float4 v = make_float4(res.x + reduced<1>(red, 0, q * 4, c), res.y + reduced<1>(red, 0, q * 4 + 1, c),
                                  res.z + reduced<1>(red, 0, q * 4 + 2, c), res.w + reduced<1>(red, 0, q * 4 + 3, c));
+    float s2 = v.x * v.x;
+    s2 += v.y * v.y;
+    s2 += v.z * v.z;
+    s2 += v.w * v.w;
+    if constexpr (R == SQ_WIDE_COLS) {
+        // Lanes c, c + 16, c + 32 and c + 48 hold row c's sums of the strip's columns 0-3, 4-7,
+        // 8-11 and 12-15.
+        static_assert(EPI == WAVE, "the strip's four sums of a row in one wave");
+        const float s4 = __shfl_down(s2, 16), s8 = __shfl_down(s2, 32), s12 = __shfl_down(s2, 48);
+        s2 += s4;
+        s2 += s8;
+        s2 += s12;
+    }
+    if (b >= a.rows) return;
     const size_t at = (size_t)b * r.N + n0;
     *reinterpret_cast<float4*>(r.out + at) = v;
     if (r.next_norm) {
         *reinterpret_cast<uint2*>(r.out_n + operand_index(b, n0, a.rows)) =
             make_uint2(pack_bf16x2(v.x * gain.x, v.y * gain.y), pack_bf16x2(v.z * gain.z, v.w * gain.w));
-        float s2 = v.x * v.x;
-        s2 += v.y * v.y;
-        s2 += v.z * v.z;
-        s2 += v.w * v.w;
-        r.out_sq[(size_t)b * (r.N / SQ_COLS) + n0 / SQ_COLS] = s2;
+        if (q == 0) r.out_sq[(size_t)b * (r.N / R) + strip_id] = s2;
     }
 }
 
@@ -630,8 +654,10 @@ template <int D>
 struct Qkv {
     template <int CH> struct Plain { static auto get() { return gemv_qkv_rope<hidden_ch(CH), false, D>; } };
     template <int CH> struct Normed { static auto get() { return gemv_qkv_rope<hidden_ch(CH), true, D>; } };
+    template <int CH> struct NormedWide { static auto get() { return gemv_qkv_rope<hidden_ch(CH), true, D, true>; } };
 };
 template <int CH> struct PickGateUp { static auto get() { return gemv_gate_up<hidden_ch(CH), 1>; } };
+template <int CH> struct PickGateUpWide { static auto get() { return gemv_gate_up<hidden_ch(CH), 1, true>; } };
 template <int CH> struct PickResidual4 { static auto get() { return gemv_residual<CH, 4>; } };
 template <int CH> struct PickResidual16 { static auto get() { return gemv_residual<CH, 16>; } };
 template <int CH> struct PickFinal { static auto get() { return final_rmsnorm<hidden_ch(CH)>; } };
@@ -648,13 +674,17 @@ hipError_t dispatch_launch(const char* label, const KernelLaunch& k, void** para
 
 }  // namespace
 
-KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed) {
+KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed, bool wide) {
     const int chunks = a.hidden / CHUNK_COLS;
     KernelLaunch k;
     if (a.head_dim == 128)
-        k.func = prenormed ? (const void*)by_chunks<Qkv<128>::Normed>(chunks) : (const void*)by_chunks<Qkv<128>::Plain>(chunks);
+        k.func = !prenormed ? (const void*)by_chunks<Qkv<128>::Plain>(chunks)
+                 : wide     ? (const void*)by_chunks<Qkv<128>::NormedWide>(chunks)
+                            : (const void*)by_chunks<Qkv<128>::Normed>(chunks);
     else
-        k.func = prenormed ? (const void*)by_chunks<Qkv<64>::Normed>(chunks) : (const void*)by_chunks<Qkv<64>::Plain>(chunks);
+        k.func = !prenormed ? (const void*)by_chunks<Qkv<64>::Plain>(chunks)
+                 : wide     ? (const void*)by_chunks<Qkv<64>::NormedWide>(chunks)
+                            : (const void*)by_chunks<Qkv<64>::Normed>(chunks);
     k.grid = dim3((a.heads + 2 * a.kv_heads) * a.head_dim / QKV_ROWS, decode_tiles(a.rows));
     k.block = dim3(GEMV_THREADS);
     return k;
@@ -683,16 +713,21 @@ KernelLaunch residual_launch(const DecodeArgs& a, const ResidualArgs& r) {
     return k;
 }
 
-KernelLaunch gate_up_launch(const DecodeArgs& a) {
+KernelLaunch gate_up_launch(const DecodeArgs& a, bool wide) {
     const int tiles = decode_tiles(a.rows);
     const int hidden_chunks = a.hidden / CHUNK_COLS;
     // Past one tile a workgroup takes two or four, reading the strips' weights once for them (for a
     // hidden size of one chunk: more would not fit the registers).
     const int per = hidden_chunks > 1 || tiles == 1 ? 1 : tiles == 2 ? 2 : 4;
     KernelLaunch k;
-    k.func = per == 1 ? (const void*)by_chunks<PickGateUp>(hidden_chunks)
-             : per == 2 ? (const void*)gemv_gate_up<1, 2>
-                        : (const void*)gemv_gate_up<1, 4>;
+    if (wide)
+        k.func = per == 1 ? (const void*)by_chunks<PickGateUpWide>(hidden_chunks)
+                 : per == 2 ? (const void*)gemv_gate_up<1, 2, true>
+                            : (const void*)gemv_gate_up<1, 4, true>;
+    else
+        k.func = per == 1 ? (const void*)by_chunks<PickGateUp>(hidden_chunks)
+                 : per == 2 ? (const void*)gemv_gate_up<1, 2>
+                            : (const void*)gemv_gate_up<1, 4>;
     k.grid = dim3(a.inner / 16, (tiles + per - 1) / per);
     k.block = dim3(GEMV_THREADS);
     return k;
@@ -712,13 +747,15 @@ hipError_t launch_decode_layer(const DecodeArgs& a, const LayerArgs& l, const Re
     LayerArgs ll = l;
     ResidualArgs oo = o, dd = down;
     void* layer_params[] = {&aa, &ll};
-    hipError_t e = dispatch_launch("gemv_qkv_rope", qkv_launch(a, l.xn != nullptr), layer_params, stream, timer);
+    // The squares o_proj and down_proj leave span their strips' rows: 16 columns at 16-row strips.
+    const bool wide = o.R == SQ_WIDE_COLS;
+    hipError_t e = dispatch_launch("gemv_qkv_rope", qkv_launch(a, l.xn != nullptr, wide), layer_params, stream, timer);
     if (e == hipSuccess) e = dispatch_launch("attention_decode", attention_launch(a), layer_params, stream, timer);
     const KernelLaunch ko = residual_launch(a, o), kd = residual_launch(a, down);
     if (!ko.func || !kd.func) return hipErrorInvalidValue;
     void* o_params[] = {&aa, &oo};
     if (e == hipSuccess) e = dispatch_launch("o_proj", ko, o_params, stream, timer);
-    if (e == hipSuccess) e = dispatch_launch("gemv_gate_up", gate_up_launch(a), layer_params, stream, timer);
+    if (e == hipSuccess) e = dispatch_launch("gemv_gate_up", gate_up_launch(a, wide), layer_params, stream, timer);
     void* down_params[] = {&aa, &dd};
     if (e == hipSuccess) e = dispatch_launch("down_proj", kd, down_params, stream, timer);
     return e != hipSuccess ? e : hipGetLastError();

@@ -28,28 +28,30 @@ struct DecodeArgs {
 };
 
 // One layer's tensors. A norm's input comes as the f32 rows and, past layer 0, also as the rows
-// times the norm's gain in bf16 with their sums of squares over each 4 columns, which the
-// projection that wrote the rows left (ResidualArgs::next_norm): the consumer then reads 2 bytes a
-// column and adds the row's sums in a fixed order.
+// times the norm's gain in bf16 with their sums of squares over each 4 columns (each 16 where the
+// projection that wrote the rows took 16-row strips), which that projection left
+// (ResidualArgs::next_norm): the consumer then reads 2 bytes a column and adds the row's sums in a
+// fixed order, the same whichever width they span.
 struct LayerArgs {
     const float* x;           // layer input [rows][hidden] f32
     // The projections' bf16 operands (xn, attended, mid_n, mlp) are kept in operand order: k-block
     // by k-block, [K / 32][rows][32].
     const uint16_t* xn;       // x input_norm in bf16 [rows][hidden], or null: taken from x
-    const float* x_sq;        // [rows][hidden / 4]
+    const float* x_sq;        // [rows][hidden / 4], or [rows][hidden / 16] (wide)
     const float* input_norm;  // [hidden] f32
     const uint16_t* qkv;      // tiled bf16, rows permuted (qkv_row_of)
     uint16_t* q;              // [rows][heads][head_dim] bf16
     uint16_t* kv;             // the layer's cache pool: [blocks][kv_heads][key tile, value tile]
     uint16_t* attended;       // [rows][heads head_dim] bf16
     const uint16_t* mid_n;    // o_proj's output times post_norm in bf16 [rows][hidden]
-    const float* mid_sq;      // [rows][hidden / 4]
+    const float* mid_sq;      // [rows][hidden / 4], or [rows][hidden / 16] (wide)
     const uint16_t* gate_up;  // tiled bf16 [2 inner][hidden]
     uint16_t* mlp;            // [rows][inner] bf16
 };
 
 // out = residual + W x, W in R-row tiles of [N][K]; with next_norm set, also out next_norm in
-// bf16 and out's sums of squares over each 4 columns, for the norm that reads out next.
+// bf16 and out's sums of squares over each R columns (a workgroup's strip), for the norm that
+// reads out next.
 struct ResidualArgs {
     const uint16_t* w;
     const uint16_t* x;  // [rows][K] bf16 in operand order
@@ -59,7 +61,7 @@ struct ResidualArgs {
     float* out;             // [rows][N]
     const float* next_norm; // [N], or null
     uint16_t* out_n;        // [rows][N] in operand order
-    float* out_sq;          // [rows][N / 4]
+    float* out_sq;          // [rows][N / R]
 };
 
 // The strip height of o_proj and down_proj for a batch of `rows`: 4 while the batch is one
@@ -97,10 +99,11 @@ struct KernelLaunch {
     dim3 grid, block;
     uint32_t lds = 0;
 };
-KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed);
+// wide: x_sq holds a sum of squares for each 16 columns (written by 16-row strips), else each 4.
+KernelLaunch qkv_launch(const DecodeArgs& a, bool prenormed, bool wide);
 KernelLaunch attention_launch(const DecodeArgs& a);
 KernelLaunch residual_launch(const DecodeArgs& a, const ResidualArgs& r);  // func null unless r.R is 4 or 16
-KernelLaunch gate_up_launch(const DecodeArgs& a);
+KernelLaunch gate_up_launch(const DecodeArgs& a, bool wide);
 KernelLaunch final_norm_launch(const DecodeArgs& a);
 KernelLaunch stream_read_launch(size_t bytes);
 

@@ -166,18 +166,29 @@ tgx_status holds(const Bound* b, int i, const char* what, uint64_t need) {
 uint64_t pool_bytes(const DecodeArgs& a) { return (uint64_t)a.nblocks * a.kv_heads * 2 * kv_tile(a.head_dim) * 2; }
 uint64_t qkv_rows(const DecodeArgs& a) { return (uint64_t)(a.heads + 2 * a.kv_heads) * a.head_dim; }
 
+// The columns one of a norm's input's sums of squares spans, as gemv_residual's strip_rows made
+// them: 4 or 16.
+tgx_status sq_cols_of(uint32_t v, const char* who, uint32_t* cols) {
+    if (v != 4 && v != 16) return fail(TGX_E_SHAPE, std::string(who) + ": sq_cols " + std::to_string(v) + " (4 or 16)");
+    *cols = v;
+    return TGX_OK;
+}
+
 // gemv_qkv_rope (gemv_qkv_rope.comp): x | (xn, x_sq), gain, W, cos, sin, positions, slots, table
-// -> q, cache pool.
+// -> q, cache pool; constant sq_cols (the columns each of x_sq's sums spans: 4, or 16 where
+// gemv_residual took 16-row strips).
 tgx_status build_qkv(const Bound* b, const uint32_t* c, Launch* L) {
     DecodeArgs a;
     TGX_TRY(decode_args(c, &a));
+    uint32_t cols;
+    TGX_TRY(sq_cols_of(c[C_COMMON], "gemv_qkv_rope", &cols));
     const uint64_t R = a.rows, h = a.hidden;
     const bool prenormed = b[1].ptr != nullptr;
     if (prenormed == (b[0].ptr != nullptr) || prenormed != (b[2].ptr != nullptr))
         return fail(TGX_E_SHAPE, "gemv_qkv_rope takes x, or xn with x_sq");
     if (prenormed) {
         TGX_TRY(holds(b, 1, "xn", R * h * 2));
-        TGX_TRY(holds(b, 2, "x_sq", R * (h / 4) * 4));
+        TGX_TRY(holds(b, 2, "x_sq", R * (h / cols) * 4));
     } else {
         TGX_TRY(holds(b, 0, "x", R * h * 4));
     }
@@ -205,7 +216,7 @@ tgx_status build_qkv(const Bound* b, const uint32_t* c, Launch* L) {
     l.kv = (uint16_t*)b[11].ptr;
     L->a = a;
     L->l = l;
-    L->k = qkv_launch(a, prenormed);
+    L->k = qkv_launch(a, prenormed, cols == 16);
     L->params[0] = &L->a;
     L->params[1] = &L->l;
     return TGX_OK;
@@ -237,7 +248,8 @@ tgx_status build_attention(const Bound* b, const uint32_t* c, Launch* L) {
 }
 
 // gemv_residual (gemv_residual.comp): x, W, residual [, next_gain] -> out [, out_n, out_sq];
-// constants K, N, strip_rows (4 or 16: W's tiles) past the common ones.
+// constants K, N, strip_rows (4 or 16: W's tiles, and the columns each of out_sq's sums of squares
+// spans) past the common ones.
 tgx_status build_residual(const Bound* b, const uint32_t* c, Launch* L) {
     DecodeArgs a;
     TGX_TRY(decode_args(c, &a));
@@ -257,7 +269,7 @@ tgx_status build_residual(const Bound* b, const uint32_t* c, Launch* L) {
     if (norm) {
         TGX_TRY(holds(b, 3, "next_gain", (uint64_t)N * 4));
         TGX_TRY(holds(b, 5, "out_n", R * N * 2));
-        TGX_TRY(holds(b, 6, "out_sq", R * (N / 4) * 4));
+        TGX_TRY(holds(b, 6, "out_sq", R * (N / Rs) * 4));
     }
     ResidualArgs r{};
     r.x = (const uint16_t*)b[0].ptr;
@@ -278,13 +290,15 @@ tgx_status build_residual(const Bound* b, const uint32_t* c, Launch* L) {
     return TGX_OK;
 }
 
-// gemv_gate_up (gemv_gate_up.comp): mid_n, mid_sq, W -> mlp.
+// gemv_gate_up (gemv_gate_up.comp): mid_n, mid_sq, W -> mlp; constant sq_cols (as gemv_qkv_rope's).
 tgx_status build_gate_up(const Bound* b, const uint32_t* c, Launch* L) {
     DecodeArgs a;
     TGX_TRY(decode_args(c, &a));
+    uint32_t cols;
+    TGX_TRY(sq_cols_of(c[C_COMMON], "gemv_gate_up", &cols));
     const uint64_t R = a.rows, h = a.hidden;
     TGX_TRY(holds(b, 0, "mid_n", R * h * 2));
-    TGX_TRY(holds(b, 1, "mid_sq", R * (h / 4) * 4));
+    TGX_TRY(holds(b, 1, "mid_sq", R * (h / cols) * 4));
     TGX_TRY(holds(b, 2, "w", 2 * (uint64_t)a.inner * h * 2));
     TGX_TRY(holds(b, 3, "mlp", R * a.inner * 2));
     LayerArgs l{};
@@ -294,7 +308,7 @@ tgx_status build_gate_up(const Bound* b, const uint32_t* c, Launch* L) {
     l.mlp = (uint16_t*)b[3].ptr;
     L->a = a;
     L->l = l;
-    L->k = gate_up_launch(a);
+    L->k = gate_up_launch(a, cols == 16);
     L->params[0] = &L->a;
     L->params[1] = &L->l;
     return TGX_OK;
@@ -974,7 +988,7 @@ const std::vector<KernelDesc>& kernels() {
           {"table", RD, TGX_U32, false},
           {"q", WR, TGX_BF16, false},
           {"kv", WR, TGX_BF16, false}},
-         decode_constants(),
+         decode_constants({"sq_cols"}),
          build_qkv},
         {"attention_decode",
          {{"q", RD, TGX_BF16, false},
@@ -996,7 +1010,7 @@ const std::vector<KernelDesc>& kernels() {
          build_residual},
         {"gemv_gate_up",
          {{"mid_n", RD, TGX_BF16, false}, {"mid_sq", RD, TGX_F32, false}, {"w", RD, TGX_BF16, false}, {"mlp", WR, TGX_BF16, false}},
-         decode_constants(),
+         decode_constants({"sq_cols"}),
          build_gate_up},
         {"rmsnorm",
          {{"x", RD, TGX_F32, false}, {"gain", RD, TGX_F32, false}, {"out", WR, TGX_F32, false}, {"positions", WR, TGX_U32, true}},
