@@ -470,7 +470,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_residual(DecodeArgs a, Resi
 // Two memory round trips before the first product: the row's position, the cache blocks of the
 // wave's turns (lane j of register r: the block of turn w + 8 (j + 64 r), from the row's copy of
 // its slot's table) and q together, then the first two turns' keys and values.
-constexpr int attention_turn(int head_dim) { return BLOCK_TOKENS / 2; }
+constexpr int attention_turn(int /* head_dim: either width */) { return BLOCK_TOKENS / 2; }
 // The positions a row may reach: 32768 at head_dim 64, 16384 at 128 (the block ids of a wave's
 // turns in two registers and one).
 constexpr int attention_capacity(int head_dim) { return head_dim == 64 ? 32768 : 16384; }
