@@ -136,6 +136,25 @@ def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int,
         for label, ms in dec.timings():
             per.setdefault(label, []).append(ms)
     dec.set_timed(EAGER)
+    # Through the boundary with host arrays, as a caller of tgx_decoder_step_rows steps: each
+    # step's inputs copied in, the step's graph launched and waited for, its outputs copied out,
+    # from the same positions (inside the reserved blocks). Beside `value`, never it.
+    # The wait sleeps between polls unless the context spins first (tgx_context_set_fence_spin, as
+    # decode_timing.rs:505-511 sweeps it): both, the spin at 1 ms.
+    host = None
+    if not EAGER:
+        n_host = min(100, steps // 2)
+        host = {"steps": n_host}
+        for spin_us in (0, 1000):
+            ctx.set_fence_spin(spin_us * 1000)
+            t0 = time.perf_counter()
+            for k in range(n_host):
+                dec.step_rows([tgx.Row(m.position + k, m.slot) for m in mid], x)
+            host_wall = time.perf_counter() - t0
+            key = "" if spin_us == 0 else f"_spin_{spin_us}us"
+            host["steps_per_s" + key] = n_host / host_wall
+            host["ms_per_step" + key] = host_wall * 1e3 / n_host
+        ctx.set_fence_spin(0)
     dec.close()
     positions_mid = [c + steps // 2 for c in contexts]
     bytes_mid = step_bytes(shape, positions_mid)
@@ -162,6 +181,7 @@ def run_decode(ctx, weights, rows: int, contexts: list, steps: int, warmup: int,
         "hbm_fraction": bytes_mid / (ms_per_step * 1e-3) / HBM_PEAK,
         "kernels": kernels,
         "kernel_sum_us": sum(k["per_step_us"] for k in kernels.values()),
+        "host_boundary": host,
         "shape": shape,
     }
 
@@ -576,6 +596,9 @@ def main() -> int:
     shape = head.pop("shape")
     log(f"batch {args.batch}: {head['steps_per_s']:.1f} steps/s, {head['ms_per_step']*1e3:.1f} us/step, "
         f"kernels sum {head['kernel_sum_us']:.1f} us")
+    if head["host_boundary"]:
+        log(f"batch {args.batch} through host arrays: {head['host_boundary']['steps_per_s']:.1f} steps/s, "
+            f"{head['host_boundary']['steps_per_s_spin_1000us']:.1f} with the wait spinning")
     for label, k in sorted(head["kernels"].items(), key=lambda kv: -kv[1]["per_step_us"]):
         log(f"  {label:16s} {k['avg_us']:8.2f} us/launch {k['per_step_us']:8.1f} us/step {k['GB_s'] or 0:8.1f} GB/s")
 
@@ -589,12 +612,14 @@ def main() -> int:
             r.pop("shape")
             for label, k in sorted(r["kernels"].items(), key=lambda kv: -kv[1]["per_step_us"]):
                 log(f"  [{rows:2d}] {label:16s} {k['avg_us']:8.2f} us/launch {k['per_step_us']:8.1f} us/step {k['GB_s'] or 0:8.1f} GB/s")
-            batches[str(rows)] = {k: r[k] for k in ("steps_per_s", "ms_per_step", "hbm_fraction", "kernel_sum_us", "step_bytes_mid")}
+            batches[str(rows)] = {k: r[k] for k in ("steps_per_s", "ms_per_step", "hbm_fraction", "kernel_sum_us", "step_bytes_mid", "host_boundary")}
             batches[str(rows)]["kernels_us"] = {k: round(v["avg_us"], 3) for k, v in r["kernels"].items()}
             batches[str(rows)]["tokens_per_s"] = r["steps_per_s"] * rows
             batches[str(rows)]["contexts"] = "U[64,1024] seeded, 200 steps"
             log(f"batch {rows}: {r['steps_per_s']:.1f} steps/s ({r['steps_per_s']*rows:.0f} tok/s), "
-                f"{r['hbm_fraction']*100:.1f}% of HBM peak on algorithmic bytes")
+                f"{r['hbm_fraction']*100:.1f}% of HBM peak on algorithmic bytes"
+                + (f"; through host arrays {r['host_boundary']['steps_per_s']:.1f} steps/s, "
+                   f"{r['host_boundary']['steps_per_s_spin_1000us']:.1f} spinning" if r["host_boundary"] else ""))
 
     prefill = None
     if not args.no_prefill:
@@ -702,6 +727,8 @@ def main() -> int:
                               "kernel_size_GB_s": round(floor_kernel["GB_s"], 1), "kernel_size_bytes": floor_kernel["bytes"],
                               "step_at_floor_ms": round(step_bytes(shape, [c + args.steps // 2 for c in headline_contexts]) / (floor["GB_s"] * 1e9) * 1e3, 4)},
         "gpu_ms_per_step": round(head["gpu_ms_per_step"], 4),
+        # Steps through tgx_decoder_step_rows with host arrays (PCIe copies and a wait each step).
+        "host_boundary": head["host_boundary"],
         "roofline": roofline,
         "roofline_longest": roofline_longest,
         "cpu_baseline": cpu,

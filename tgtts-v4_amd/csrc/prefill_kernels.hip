@@ -1029,6 +1029,47 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Copies `count` 16-byte words from device memory to pinned host memory the device maps, by the
+// compute queue's own stores: a copy engine's transfer queued behind a kernel starts only on a
+// signal between the queues, which at 256 KiB took longer than the copy itself.
+__global__ void __launch_bounds__(256) copy_words(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t count) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t stream) {
+    if (bytes % 16 || (uintptr_t)src % 16 || (uintptr_t)dst % 16) return hipErrorInvalidValue;
+    const size_t count = bytes / 16;
+    if (count == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 256);
+    copy_words<<<blocks, 256, 0, stream>>>((const uint4*)src, (uint4*)dst, count);
+    return hipGetLastError();
+}
+
+// Copies the segments' 4-byte words in one launch (host staging the device maps, read over the
+// bus, into device memory): the step's inputs reach the device on the compute queue, ahead of the
+// step, with no signal between queues.
+__global__ void __launch_bounds__(256) copy_segments(CopySegments c) {
+    const uint32_t total = c.end[c.n - 1];
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+        int k = 0;
+        while (i >= c.end[k]) ++k;
+        const uint32_t j = i - (k ? c.end[k - 1] : 0u);
+        c.dst[k][j] = c.src[k][j];
+    }
+}
+
+hipError_t launch_copy_segments(const CopySegments& c, hipStream_t stream) {
+    if (c.n <= 0) return hipSuccess;
+    if (c.n > COPY_SEGMENTS) return hipErrorInvalidValue;
+    for (int k = 0; k < c.n; ++k)
+        if ((k ? c.end[k - 1] : 0u) > c.end[k]) return hipErrorInvalidValue;
+    const uint32_t total = c.end[c.n - 1];
+    if (total == 0) return hipSuccess;
+    const unsigned blocks = std::min<unsigned>((total + 255) / 256, 256);
+    copy_segments<<<blocks, 256, 0, stream>>>(c);
+    return hipGetLastError();
+}
+
 int prefill_attention_tile(int group, int head_dim) { return attention_tile(group, head_dim); }
 
 hipError_t prefill_prepare(size_t device_lds) {

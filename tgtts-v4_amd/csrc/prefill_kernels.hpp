@@ -116,5 +116,19 @@ constexpr size_t PREFILL_SCRATCH_BYTES = (size_t)32 << 20;
 hipError_t prefill_scratch_address(int device, void** out);
 // Zeroes `bytes` (a multiple of 16, 16-byte aligned) at p with a kernel on `stream`.
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+// `bytes` (a multiple of 16) from device memory at src to host memory the device maps at dst (a
+// pinned allocation's device address), by a kernel on `stream`.
+hipError_t launch_copy_words(const void* src, void* dst, size_t bytes, hipStream_t stream);
+// Up to COPY_SEGMENTS copies of 4-byte words in one kernel: segment k copies words
+// end[k - 1] .. end[k] - 1 of the whole (end[-1] = 0) from src[k] (memory the device reads: a
+// pinned host allocation's device address, or device memory) to dst[k].
+constexpr int COPY_SEGMENTS = 8;
+struct CopySegments {
+    const uint32_t* src[COPY_SEGMENTS];
+    uint32_t* dst[COPY_SEGMENTS];
+    uint32_t end[COPY_SEGMENTS];
+    int n;
+};
+hipError_t launch_copy_segments(const CopySegments& c, hipStream_t stream);
 
 }  // namespace tgx

@@ -459,18 +459,25 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_HIP(hipMemcpy(d->cos, cos.data(), cos.size() * 4, hipMemcpyHostToDevice));
     TGX_HIP(hipMemcpy(d->sin, sin.data(), sin.size() * 4, hipMemcpyHostToDevice));
 
-    TGX_HIP(hipHostMalloc((void**)&d->x_host, (size_t)R * h * 4, hipHostMallocDefault));
-    TGX_HIP(hipHostMalloc((void**)&d->out_host, (size_t)R * h * 4, hipHostMallocDefault));
-    TGX_HIP(hipHostMalloc((void**)&d->placement_host, (size_t)2 * R * 4, hipHostMallocDefault));
-    TGX_HIP(hipHostMalloc((void**)&d->table_host, (size_t)d->slots * d->max_blocks * 4, hipHostMallocDefault));
-    TGX_HIP(hipHostMalloc((void**)&d->row_table_host, (size_t)R * d->max_blocks * 4, hipHostMallocDefault));
+    TGX_HIP(hipHostMalloc((void**)&d->x_host, (size_t)R * h * 4, hipHostMallocCoherent));
+    TGX_HIP(hipHostGetDevicePointer((void**)&d->x_mapped, d->x_host, 0));
+    // The step's output is stored into it by a kernel (launch_copy_words), through its device
+    // address: coherent, so that the stores reach host memory past the GPU's caches.
+    TGX_HIP(hipHostMalloc((void**)&d->out_host, (size_t)R * h * 4, hipHostMallocCoherent));
+    TGX_HIP(hipHostGetDevicePointer((void**)&d->out_mapped, d->out_host, 0));
+    TGX_HIP(hipHostMalloc((void**)&d->placement_stage, (size_t)2 * R * 4, hipHostMallocCoherent));
+    TGX_HIP(hipHostMalloc((void**)&d->table_stage, (size_t)d->slots * d->max_blocks * 4, hipHostMallocCoherent));
+    TGX_HIP(hipHostMalloc((void**)&d->row_table_host, (size_t)R * d->max_blocks * 4, hipHostMallocCoherent));
+    TGX_HIP(hipHostGetDevicePointer((void**)&d->placement_mapped, d->placement_stage, 0));
+    TGX_HIP(hipHostGetDevicePointer((void**)&d->table_mapped, d->table_stage, 0));
+    TGX_HIP(hipHostGetDevicePointer((void**)&d->row_table_mapped, d->row_table_host, 0));
     std::memset(d->x_host, 0, (size_t)R * h * 4);
     std::memset(d->out_host, 0, (size_t)R * h * 4);
-    for (int i = 0; i < 2 * R; ++i) d->placement_host[i] = TGX_SPARE;
-    for (size_t i = 0; i < (size_t)d->slots * d->max_blocks; ++i) d->table_host[i] = TGX_SPARE;
-    TGX_HIP(hipMemcpy(d->positions, d->placement_host, R * 4, hipMemcpyHostToDevice));
-    TGX_HIP(hipMemcpy(d->slot_of_row, d->placement_host + R, R * 4, hipMemcpyHostToDevice));
-    TGX_HIP(hipMemcpy(d->table, d->table_host, (size_t)d->slots * d->max_blocks * 4, hipMemcpyHostToDevice));
+    d->placement_host.assign(2 * (size_t)R, TGX_SPARE);
+    d->table_host.assign((size_t)d->slots * d->max_blocks, TGX_SPARE);
+    TGX_HIP(hipMemcpy(d->positions, d->placement_host.data(), R * 4, hipMemcpyHostToDevice));
+    TGX_HIP(hipMemcpy(d->slot_of_row, d->placement_host.data() + R, R * 4, hipMemcpyHostToDevice));
+    TGX_HIP(hipMemcpy(d->table, d->table_host.data(), (size_t)d->slots * d->max_blocks * 4, hipMemcpyHostToDevice));
     d->table_dirty = false;
     d->rows_dirty = true;
     d->slot_blocks.assign(d->slots, 0);
@@ -492,6 +499,7 @@ tgx_status create_inner(Decoder* d, const tgx_batch* batch) {
     TGX_HIP(hipEventCreate(&d->ev_start));
     TGX_HIP(hipEventCreate(&d->ev_end));
     TGX_HIP(hipEventCreateWithFlags(&d->ev_done, hipEventDisableTiming));
+    TGX_HIP(hipEventCreateWithFlags(&d->ev_staged, hipEventDisableTiming));
     TGX_HIP(hipDeviceSynchronize());
     return use_program(d);
 }
@@ -537,22 +545,78 @@ void moved_on(Decoder* d, int times) {
         if (d->placement_host[b] != TGX_SPARE) d->placement_host[b] += (uint32_t)times;
 }
 
-tgx_status sync_slots(Decoder* d) {
-    if (!d->table_dirty && !d->rows_dirty) return TGX_OK;
-    hipStream_t s = d->ctx->stream;
+namespace {
+
+// Before the host fills any pinned staging buffer: the copies queued from them before have run.
+tgx_status staging_wait(Decoder* d) {
+    if (d->staged) {
+        TGX_HIP(hipEventSynchronize(d->ev_staged));
+        d->staged = false;
+    }
+    return TGX_OK;
+}
+
+// The staged copies launched (one kernel on the context's stream), the event after them.
+tgx_status staging_queued(Decoder* d) {
+    const hipError_t e = launch_copy_segments(d->copies, d->ctx->stream);
+    d->copies.n = 0;
+    if (e != hipSuccess) return fail(TGX_E_HIP, std::string("copying the step's inputs: ") + hipGetErrorString(e));
+    TGX_HIP(hipEventRecord(d->ev_staged, d->ctx->stream));
+    d->staged = true;
+    return TGX_OK;
+}
+
+// A copy of `bytes` (whole 4-byte words) from a staging buffer's device address to device memory,
+// staged for the next staging_queued (the ones before launched first when the list is full).
+tgx_status stage_copy(Decoder* d, const void* mapped, void* dst, size_t bytes) {
+    CopySegments& c = d->copies;
+    if (c.n == COPY_SEGMENTS) {
+        const hipError_t e = launch_copy_segments(c, d->ctx->stream);
+        c.n = 0;
+        if (e != hipSuccess) return fail(TGX_E_HIP, std::string("copying the step's inputs: ") + hipGetErrorString(e));
+    }
+    const uint32_t before = c.n ? c.end[c.n - 1] : 0u;
+    c.src[c.n] = static_cast<const uint32_t*>(mapped);
+    c.dst[c.n] = static_cast<uint32_t*>(dst);
+    c.end[c.n] = before + (uint32_t)(bytes / 4);
+    c.n += 1;
+    return TGX_OK;
+}
+
+// The block table (when it changed) and the rows' copies of their slots' rows of it, staged and
+// queued for the device; the caller has waited for the staging (staging_wait).
+tgx_status queue_slots(Decoder* d) {
     const size_t mb = (size_t)d->max_blocks;
-    if (d->table_dirty) TGX_HIP(hipMemcpyAsync(d->table, d->table_host, d->slots * mb * 4, hipMemcpyHostToDevice, s));
+    if (d->table_dirty) {
+        std::memcpy(d->table_stage, d->table_host.data(), d->slots * mb * 4);
+        TGX_TRY(stage_copy(d, d->table_mapped, d->table, d->slots * mb * 4));
+    }
     for (int b = 0; b < d->rows; ++b) {
         const uint32_t slot = d->placement_host[d->rows + b];
         for (size_t i = 0; i < mb; ++i)
             d->row_table_host[b * mb + i] = slot < (uint32_t)d->slots ? d->table_host[slot * mb + i] : TGX_SPARE;
     }
-    TGX_HIP(hipMemcpyAsync(d->row_table, d->row_table_host, d->rows * mb * 4, hipMemcpyHostToDevice, s));
-    // The pinned buffers may not change until the copies have gone.
-    TGX_HIP(hipStreamSynchronize(s));
+    TGX_TRY(stage_copy(d, d->row_table_mapped, d->row_table, d->rows * mb * 4));
     d->table_dirty = false;
     d->rows_dirty = false;
     return TGX_OK;
+}
+
+// The placement's words staged and queued for the device (the caller has waited for the staging).
+tgx_status queue_placement(Decoder* d) {
+    const size_t R = (size_t)d->rows;
+    std::memcpy(d->placement_stage, d->placement_host.data(), 2 * R * 4);
+    TGX_TRY(stage_copy(d, d->placement_mapped, d->positions, R * 4));
+    return stage_copy(d, d->placement_mapped + R, d->slot_of_row, R * 4);
+}
+
+}  // namespace
+
+tgx_status sync_slots(Decoder* d) {
+    if (!d->table_dirty && !d->rows_dirty) return TGX_OK;
+    TGX_TRY(staging_wait(d));
+    TGX_TRY(queue_slots(d));
+    return staging_queued(d);
 }
 
 tgx_status decoder_create(Context* ctx, const tgx_shape* shape, const tgx_batch* batch, Decoder** out) {
@@ -592,8 +656,9 @@ void decoder_destroy(Decoder* d) {
     for (auto& b : d->allocations) hipFree(b.ptr);
     if (d->x_host) hipHostFree(d->x_host);
     if (d->out_host) hipHostFree(d->out_host);
-    if (d->placement_host) hipHostFree(d->placement_host);
-    if (d->table_host) hipHostFree(d->table_host);
+    if (d->ev_staged) hipEventDestroy(d->ev_staged);
+    if (d->placement_stage) hipHostFree(d->placement_stage);
+    if (d->table_stage) hipHostFree(d->table_stage);
     if (d->row_table_host) hipHostFree(d->row_table_host);
     delete d;
 }
@@ -691,7 +756,11 @@ tgx_status decoder_load(Decoder* d, const char* name, const void* data, tgx_dtyp
     return load_layer_tensor(d->layers[l], s, n, what, data, dtype, count, d->od_rows, d->od_rows);
 }
 
-tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {
+namespace {
+
+// The rows placed (checked, their slots' blocks held) and their placement and block tables
+// queued for the device; the caller waits for the staging before and marks it after.
+tgx_status place_rows(Decoder* d, const tgx_row* rows, int nrows) {
     if (!d || !rows) return fail(TGX_E_ARG, "null decoder or rows");
     if (d->pending) return fail(TGX_E_BUSY, "a step is under way");
     if (nrows != d->rows)
@@ -703,15 +772,21 @@ tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {
         if (r.position == TGX_SPARE) continue;
         TGX_TRY(hold_slot(d, r.slot, r.position + 1));
     }
-    std::memcpy(d->placement_host, words.data(), words.size() * 4);
+    std::copy(words.begin(), words.end(), d->placement_host.begin());
     d->rows_dirty = true;
-    hipStream_t s = d->ctx->stream;
-    TGX_TRY(sync_slots(d));
-    TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
-    TGX_HIP(hipMemcpyAsync(d->slot_of_row, d->placement_host + nrows, (size_t)nrows * 4, hipMemcpyHostToDevice, s));
-    // The pinned buffer may not change until the copies have gone.
-    TGX_HIP(hipStreamSynchronize(s));
-    return TGX_OK;
+    TGX_TRY(queue_slots(d));
+    return queue_placement(d);
+}
+
+}  // namespace
+
+tgx_status decoder_place(Decoder* d, const tgx_row* rows, int nrows) {
+    if (!d) return fail(TGX_E_ARG, "null decoder");
+    TGX_TRY(staging_wait(d));
+    const tgx_status st = place_rows(d, rows, nrows);
+    // Whatever was queued before a refusal is marked too.
+    TGX_TRY(staging_queued(d));
+    return st;
 }
 
 tgx_status decoder_use_rows(Decoder* d, int rows) {
@@ -728,23 +803,26 @@ tgx_status decoder_use_rows(Decoder* d, int rows) {
         return st;
     }
     // Every row spare until placed again.
-    for (int i = 0; i < 2 * rows; ++i) d->placement_host[i] = TGX_SPARE;
+    std::fill(d->placement_host.begin(), d->placement_host.begin() + 2 * rows, TGX_SPARE);
     d->rows_dirty = true;
-    hipStream_t s = d->ctx->stream;
-    TGX_HIP(hipMemcpyAsync(d->positions, d->placement_host, (size_t)rows * 4, hipMemcpyHostToDevice, s));
-    TGX_HIP(hipMemcpyAsync(d->slot_of_row, d->placement_host + rows, (size_t)rows * 4, hipMemcpyHostToDevice, s));
-    TGX_HIP(hipStreamSynchronize(s));
-    return TGX_OK;
+    TGX_TRY(staging_wait(d));
+    TGX_TRY(queue_placement(d));
+    return staging_queued(d);
 }
 
 tgx_status decoder_set_rows(Decoder* d, const tgx_row* rows, int nrows, const float* x) {
     if (!d || !rows || !x) return fail(TGX_E_ARG, "null decoder, rows or x");
-    TGX_TRY(decoder_place(d, rows, nrows));
-    std::memcpy(d->x_host, x, (size_t)nrows * d->shape.hidden * 4);
-    hipStream_t s = d->ctx->stream;
-    TGX_HIP(hipMemcpyAsync(d->x_in, d->x_host, (size_t)nrows * d->shape.hidden * 4, hipMemcpyHostToDevice, s));
-    TGX_HIP(hipStreamSynchronize(s));
-    return TGX_OK;
+    // One wait for the staging, then the placement, the tables and x queued behind one mark: the
+    // step's own launch and wait follow them on the stream, so a step through host arrays makes
+    // one round trip to the device.
+    TGX_TRY(staging_wait(d));
+    tgx_status st = place_rows(d, rows, nrows);
+    if (st == TGX_OK) {
+        std::memcpy(d->x_host, x, (size_t)nrows * d->shape.hidden * 4);
+        st = stage_copy(d, d->x_mapped, d->x_in, (size_t)nrows * d->shape.hidden * 4);
+    }
+    TGX_TRY(staging_queued(d));
+    return st;
 }
 
 tgx_status decoder_start(Decoder* d) {
@@ -763,7 +841,7 @@ tgx_status decoder_start(Decoder* d) {
         TGX_HIP(hipGraphLaunch(d->step_exec, s));
     }
     TGX_HIP(hipEventRecord(d->ev_end, s));
-    TGX_HIP(hipMemcpyAsync(d->out_host, d->out, (size_t)d->rows * d->shape.hidden * 4, hipMemcpyDeviceToHost, s));
+    TGX_HIP(launch_copy_words(d->out, d->out_mapped, (size_t)d->rows * d->shape.hidden * 4, s));
     TGX_HIP(hipEventRecord(d->ev_done, s));
     d->pending = true;
     return TGX_OK;

@@ -101,10 +101,19 @@ struct Decoder {
     uint32_t *positions = nullptr, *slot_of_row = nullptr, *table = nullptr;
     uint32_t* row_table = nullptr;  // [rows][max_blocks]: each row's slot's table row
     float *cos = nullptr, *sin = nullptr;
-    // host mirrors, in pinned memory
-    float *x_host = nullptr, *out_host = nullptr;
-    uint32_t *placement_host = nullptr;  // [positions..., slots...]
-    uint32_t *table_host = nullptr, *row_table_host = nullptr;
+    // host mirrors of the placement ([positions..., slots...]) and of the slots' block tables
+    std::vector<uint32_t> placement_host, table_host;
+    // Pinned staging (coherent: the device reads it past its caches) that copies to the device
+    // read from, through each buffer's device address (*_mapped): each is filled just before its
+    // copy is staged in `copies`, once the copies queued from the staging before have run
+    // (staging_wait); staging_queued launches them, one kernel, and the event follows it on the
+    // stream. out_host takes the step's output, which a kernel stores through out_mapped.
+    float *x_host = nullptr, *out_host = nullptr, *x_mapped = nullptr, *out_mapped = nullptr;
+    uint32_t *placement_stage = nullptr, *table_stage = nullptr, *row_table_host = nullptr;
+    uint32_t *placement_mapped = nullptr, *table_mapped = nullptr, *row_table_mapped = nullptr;
+    CopySegments copies{};
+    hipEvent_t ev_staged = nullptr;
+    bool staged = false;
     bool table_dirty = true, rows_dirty = true;
     std::vector<int> slot_blocks;     // blocks each slot holds
     std::vector<uint32_t> free_list;  // blocks nobody holds
@@ -161,8 +170,9 @@ tgx_status decoder_output(Decoder* dec, float* out);
 tgx_status decoder_release_slot(Decoder* dec, uint32_t slot);
 tgx_status decoder_reserve(Decoder* dec, uint32_t slot, uint32_t positions);
 tgx_status decoder_launch(Decoder* dec, int times, int advance);
-// Hands `slot` the blocks for positions 0..positions-1; copies the block table, and the rows'
-// copies of their slots' rows of it, to the device when they changed.
+// Hands `slot` the blocks for positions 0..positions-1 (in the host's table); sync_slots queues
+// copies of the block table, and of the rows' copies of their slots' rows of it, to the device
+// on the context's stream when they changed, without waiting for them.
 tgx_status hold_slot(Decoder* d, uint32_t slot, uint32_t positions);
 tgx_status sync_slots(Decoder* d);
 // Before `times` steps (each placed row moved on a position a step with `advance`): holds every
