@@ -385,3 +385,37 @@ def test_launched_steps_past_the_reserved_blocks_hold_them_and_match_single_step
     a.wait()
     a.close()
     b.close()
+
+
+def test_rows_set_again_before_a_step_run_as_last_set(ctx):
+    """The host's staging for a step's inputs (placement, block tables, x) is refilled only once
+    the copies queued from it have run: rows and inputs set, a slot's blocks reserved, and rows set
+    again with other inputs and positions before the step run the last ones, bit for bit as a
+    decoder that only ever saw them; steps through host arrays one after another, each with new
+    inputs, as single steps on a fresh decoder."""
+    import tgx
+
+    spec = tiny_spec(layers=2)
+    cap = 256
+    prompt = inputs(spec, 70, name="prompt")
+    x = inputs(spec, 12)
+    a = make_decoder(ctx, spec, cap, rows=2, slots=2)
+    b = make_decoder(ctx, spec, cap, rows=2, slots=2)
+    for d in (a, b):
+        d.prefill_runs([(0, 0, 40), (1, 0, 30)], prompt)
+    rows = [tgx.Row(40, 0), tgx.Row(30, 1)]
+    a.set_rows([tgx.Row(30, 1), tgx.Row(40, 0)], x[2:4])  # replaced before any step
+    a.reserve(0, 200)
+    a.set_rows(rows, x[0:2])
+    a.start()
+    a.wait()
+    got = a.output()
+    want = b.step_rows(rows, x[0:2])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for t in range(1, 5):
+        rows_t = [tgx.Row(40 + t, 0), tgx.Row(30 + t, 1)]
+        got = a.step_rows(rows_t, x[2 * t : 2 * t + 2])
+        want = b.step_rows(rows_t, x[2 * t : 2 * t + 2])
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"step {t}"
+    a.close()
+    b.close()
