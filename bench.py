@@ -228,6 +228,14 @@ def run_prefill(ctx, weights, count: int, length: int, times: int, decode_steps:
     dec.wait()
     wall = (time.perf_counter() - t0) / times
     gpu = dec.elapsed_ms() / times * 1e-3
+    # Through the boundary with host arrays (tgx_prefill_runs: the inputs copied in from pageable
+    # host memory, the outputs copied back), beside the resident rate, never it.
+    host_ms = None
+    if not EAGER:
+        t0 = time.perf_counter()
+        for _ in range(2):
+            dec.prefill_runs(runs, x)
+        host_ms = (time.perf_counter() - t0) / 2 * 1e3
     dec.set_timed(True)
     dec.prefill_launch(1)
     dec.wait()
@@ -262,6 +270,8 @@ def run_prefill(ctx, weights, count: int, length: int, times: int, decode_steps:
         "kernels": kernels,
         "finite": finite,
         "decode_steps_per_s": decode_steps / dwall,
+        "host_ms": host_ms,
+        "rows": rows,
     }
 
 
@@ -628,7 +638,8 @@ def main() -> int:
             log(f"  [prefill] {label:18s} {k['avg_us']:10.1f} us x {k['launches']:3d}"
                 + (f"  {k['TFLOP_s']:8.1f} TFLOP/s" if k["TFLOP_s"] else ""))
         log(f"prefill 8 x 2048: {pf['tokens_per_s']:.0f} tok/s, {pf['ms']:.2f} ms, "
-            f"{pf['mfma_fraction'] * 100:.1f}% of bf16 MFMA peak; then {pf['decode_steps_per_s']:.0f} steps/s at batch 8")
+            f"{pf['mfma_fraction'] * 100:.1f}% of bf16 MFMA peak; then {pf['decode_steps_per_s']:.0f} steps/s at batch 8"
+            + (f"; through host arrays {pf['host_ms']:.2f} ms" if pf["host_ms"] else ""))
         gemms = {k: v for k, v in pf["kernels"].items() if v["TFLOP_s"]}
         dom = max(gemms.items(), key=lambda kv: kv[1]["avg_us"] * kv[1]["launches"])
         prefill = {
@@ -639,6 +650,9 @@ def main() -> int:
             "mfma_fraction": round(pf["mfma_fraction"], 4),
             "finite": pf["finite"],
             "decode_steps_per_s_after": round(pf["decode_steps_per_s"], 1),
+            # tgx_prefill_runs with the inputs and outputs in (pageable) host memory.
+            "host_boundary": None if pf["host_ms"] is None else
+                {"ms": round(pf["host_ms"], 3), "tokens_per_s": round(pf["rows"] / (pf["host_ms"] * 1e-3), 1)},
             "roofline": {"bound": "mfma", "kernel": dom[0], "achieved": round(dom[1]["TFLOP_s"], 1),
                          "peak": MFMA_PEAK / 1e12, "unit": "TFLOP/s", "frac": round(dom[1]["TFLOP_s"] * 1e12 / MFMA_PEAK, 4),
                          "avg_us": round(dom[1]["avg_us"], 2),
